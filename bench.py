@@ -1,0 +1,169 @@
+#!/usr/bin/env python3
+"""Dual-AR decode benchmark: audio frames/s of the Slow+Fast AR loop, batch 1.
+
+Default workload ("full"): S2-Pro-shaped random-init model (36 Slow layers,
+d=2560, 32 q / 8 kv heads, head_dim 128, FFN 9728, vocab 155776; 4 Fast
+layers, 10 codebooks x 4096), f16 weights N(0, 0.02) seed 1, a 256-token
+uniform-random prompt, greedy, KV cache 768.  One step = one frame (one
+Slow-AR decode step + the Fast-AR's 9 codebook passes + sampling); the timed
+window runs from after prefill to the last frame's codes (HIP events inside
+the library).  Prints one JSON line.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "fish-s2pro_amd"), ROOT]
+
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (shape, prompt, frames, max_seq, temperature, top_p, top_k)
+    "full": ("full", 256, 512, 768, 0.0, 1.0, 0),
+    "full_q8": ("full_q8", 256, 512, 768, 0.7, 0.9, 0),
+    "full_q4": ("full_q4", 256, 1024, 1280, 0.0, 1.0, 0),
+    "tiny": ("tiny", 32, 16, 64, 0.0, 1.0, 0),
+}
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def frame_bytes(spec, shape, avg_t, kv_bytes=4):
+    """Algorithmic HBM bytes of one frame: Slow weights once, Fast weights for
+    9 passes (positions 0 and 1 share one pass), the candidate head rows,
+    embeddings, norms and KV reads/writes at the stored KV dtype."""
+    b_w = {1: 2.0, 8: 34 / 32, 2: 18 / 32}[spec["linear_type"]]
+    d, L, Lf = spec["dim"], spec["slow_layers"], spec["fast_layers"]
+    ncb, C = spec["num_codebooks"], spec["codebook_size"]
+    kv = spec["kv_heads"] * spec["head_dim"]
+    slow = L * shape.linear_params_per_slow_layer() * b_w
+    slow += L * (2 * d + 2 * spec["head_dim"]) * 2 + 2 * d + (ncb + 1) * d * 2
+    slow += (C + 1) * d * 2  # semantic rows + im_end of the tied head
+    slow += avg_t * L * 2 * kv * kv_bytes + L * 2 * kv * kv_bytes
+    fast_pass = Lf * shape.linear_params_per_fast_layer() * b_w + d * C * b_w + Lf * 2 * d * 2 + 2 * d + d * 2
+    fkv = spec["fast_kv_heads"] * spec["fast_head_dim"]
+    fast = (ncb - 1) * fast_pass + Lf * 2 * fkv * kv_bytes * (ncb * (ncb + 1) // 2 + ncb)
+    return slow + fast
+
+
+def cpu_baseline(path, shape, threads, prompt_len, frames):
+    """The oracle in faithful mode (per-step Slow layer reload + f32 expansion,
+    Fast-AR prefix recompute, row-parallel f32 linears) on a bounded sample."""
+    from oracle import oracle as O
+    from s2hip import synth
+
+    m = O.OracleModel(path, prompt_len + frames + 1, shape.im_end_id,
+                      flags=O.FAITHFUL_SLOW_RELOAD | O.FAITHFUL_FAST_RECOMPUTE, threads=threads)
+    prompt = synth.synthetic_prompt(shape, prompt_len, seed=shape.seed)
+    r = m.generate_codes(prompt, frames, 0.0, 1.0, 0, 1 << 30, 0)
+    m.close()
+    return r["n_frames"] / r["decode_seconds"], r
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="frames in the timed run (default: workload's)")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed warm-up generations")
+    ap.add_argument("--workload", default="full", choices=sorted(WORKLOADS))
+    ap.add_argument("--model-dir", default=os.environ.get("S2HIP_MODEL_DIR", "/tmp/s2hip_models"))
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-baseline", type=int, default=1)
+    ap.add_argument("--cpu-frames", type=int, default=2)
+    ap.add_argument("--cpu-prompt", type=int, default=4)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the dual-AR loop is a single-GPU "
+              "batch-1 path in this build", file=sys.stderr)
+        sys.exit(2)
+
+    from s2hip import Engine, synth
+
+    shape_name, prompt_len, frames, max_seq, temp, top_p, top_k = WORKLOADS[args.workload]
+    if args.steps:
+        frames = args.steps
+        max_seq = max(max_seq, prompt_len + frames)
+    shape = synth.SHAPES[shape_name]
+    t0 = time.time()
+    path = synth.ensure_gguf(shape, args.model_dir, threads=min(16, os.cpu_count() or 1))
+    log(f"model {path} ready in {time.time() - t0:.1f}s")
+    t0 = time.time()
+    eng = Engine(path, max_seq, shape.im_end_id, use_graph=not args.no_graph)
+    spec = eng.spec
+    log(f"engine loaded in {time.time() - t0:.1f}s ({spec['weight_bytes'] / 1e9:.2f} GB in HBM)")
+    prompt = synth.synthetic_prompt(shape, prompt_len, seed=shape.seed)
+    kw = dict(temperature=temp, top_p=top_p, top_k=top_k, min_tokens_before_end=1 << 30, rng_state=shape.seed)
+    for i in range(args.warmup):
+        r = eng.generate_codes(prompt, frames, **kw)
+        log(f"warmup {i}: {r['n_frames']} frames, prefill {r['prefill_ms']:.1f} ms, decode {r['decode_ms']:.1f} ms")
+    r = eng.generate_codes(prompt, frames, **kw)
+    n = r["n_frames"]
+    dec_s = r["decode_ms"] / 1e3
+    fps = n / dec_s
+    log(f"timed: {n} frames in {dec_s * 1e3:.1f} ms -> {fps:.1f} frames/s (prefill {r['prefill_ms']:.1f} ms)")
+
+    avg_t = prompt_len + n / 2.0
+    fb = frame_bytes(spec, shape, avg_t)
+    kern = "slow_w13"
+    us, kb = eng.time_kernel(kern, reps=5)
+    achieved = kb / (us * 1e-6) / 1e9
+    log(f"{kern}: {us:.2f} us/launch, {kb / 1e6:.2f} MB -> {achieved:.0f} GB/s")
+    other = {}
+    for k in ("slow_wqkv", "slow_wo", "slow_w2", "slow_head"):
+        ku, kbb = eng.time_kernel(k, reps=5)
+        other[k] = {"us": round(ku, 3), "GBs": round(kbb / (ku * 1e-6) / 1e9, 1)}
+    eng.close()
+
+    cpu = None
+    if args.cpu_baseline:
+        threads = min(16, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
+        log(f"cpu baseline: oracle faithful mode, {threads} threads, prompt {args.cpu_prompt}, "
+            f"{args.cpu_frames} frames")
+        t0 = time.time()
+        cfps, cr = cpu_baseline(path, shape, threads, args.cpu_prompt, args.cpu_frames)
+        log(f"cpu baseline {cfps:.4f} frames/s ({time.time() - t0:.1f}s wall)")
+        cpu = {"value": round(cfps, 5), "unit": "frames/s", "cores": threads, "kind": "port",
+               "sample": f"{shape_name} model, {args.cpu_prompt}-token prompt, {cr['n_frames']} greedy frames "
+                         f"after prefill; faithful mode (Slow layers re-read + expanded to f32 every step, "
+                         f"Fast-AR prefix recompute)"}
+
+    out = {
+        "metric": "audio frames/sec (Slow+Fast AR) batch-1 f16; % of HBM roofline",
+        "value": round(fps, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec_s * 1e3 / max(1, n), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {1: "f16", 8: "q8_0", 2: "q4_0"}[spec["linear_type"]] + " weights, f32 accumulate",
+        "data": "synthetic (random-init N(0,0.02) weights, uniform random prompt ids)",
+        "config": {"workload": f"{args.workload}: {spec['slow_layers']}+{spec['fast_layers']} layers d={spec['dim']}, "
+                               f"{prompt_len}-token prompt, {n} frames, KV {max_seq}",
+                   "prompt_tokens": prompt_len, "frames": n, "kv_cache": max_seq, "sampler":
+                       {"temperature": temp, "top_p": top_p, "top_k": top_k}, "parallelism": "single GPU"},
+        "codes_per_s": round(fps * spec["num_codebooks"], 1),
+        "prefill_ms": round(r["prefill_ms"], 2),
+        "frame_bytes": round(fb),
+        "frame_roofline_frac": round(fb * fps / (HBM_PEAK_GBS * 1e9), 4),
+        "roofline": {"bound": "hbm", "kernel": f"gemv {kern} (fused RMSNorm + w1/w3 + SwiGLU)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": round(kb), "avg_us": round(us, 3)},
+        "kernels": other,
+        "cpu_baseline": cpu,
+        "graph_used": r["graph_used"],
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

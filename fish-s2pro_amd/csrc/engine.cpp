@@ -1,0 +1,1317 @@
+// engine.cpp -- s2hip engine: HBM-resident dual-AR state behind the C ABI.
+//
+// One engine = one loaded transformer GGUF on one device:
+//   * every tensor uploaded once in its GGUF layout (F16 / Q8_0 / Q4_0 rows),
+//     RMSNorm gains expanded to f32;
+//   * Slow-AR KV cache f32 [layer][kv_head][max_seq][head_dim];
+//   * Fast-AR KV cache f32 [layer][kv_head][num_codebooks + 1][head_dim],
+//     filled incrementally (9 weight passes per frame instead of the
+//     reference's prefix recompute, crates/fish_s2_infer/src/fast_ar.rs:417-424);
+//   * a DevState block (positions, frame counter, RNG state, frame codes) so
+//     one captured HIP graph replays every frame with no host round trip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "gguf.h"
+#include "kernels.h"
+#include "s2hip.h"
+
+namespace s2 {
+namespace {
+
+struct HipFailure : std::runtime_error {
+  explicit HipFailure(const std::string& m) : std::runtime_error(m) {}
+};
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw HipFailure(std::string(what) + ": " + hipGetErrorString(e));
+}
+#define HIPC(expr) hip_check((expr), #expr)
+
+[[noreturn]] void fail(const std::string& m) { throw std::runtime_error(m); }
+
+constexpr uint32_t PREFILL_COLS = 4;
+constexpr uint32_t FRAME_BATCH = 16;
+constexpr size_t WEIGHT_PAD = 256;  // trailing bytes so block loads never leave a buffer
+
+float f16_to_f32(uint16_t h) {
+  const uint32_t sign = uint32_t(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t bits;
+  if (e == 0) {
+    const float v = std::ldexp(float(m), -24);
+    return sign ? -v : v;
+  }
+  bits = e == 0x1f ? (sign | 0x7f800000u | (m << 13)) : (sign | ((e + 112u) << 23) | (m << 13));
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+struct DevLin {
+  uint8_t* w = nullptr;
+  uint32_t type = 0;
+  uint32_t in = 0, out = 0;
+  size_t row_bytes = 0;
+  uint64_t bytes = 0;
+};
+
+struct SlowLayer {
+  float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  DevLin wqkv, wo, w1, w2, w3;
+};
+
+struct FastLayer {
+  float *attn_norm = nullptr, *ffn_norm = nullptr;
+  DevLin wqkv, wo, w1, w2, w3;
+};
+
+std::string lname(const char* pre, uint32_t l, const char* suf) {
+  return std::string(pre) + "." + std::to_string(l) + "." + suf;
+}
+
+}  // namespace
+
+class Engine {
+ public:
+  explicit Engine(const s2hip_config& cfg);
+  ~Engine();
+
+  s2hip_spec spec{};
+  int device = 0;
+
+  void select() { HIPC(hipSetDevice(device)); }
+  void reset();
+  void eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out);
+  void fast_logits(const float* hidden, const uint32_t* prefix, size_t plen, float* logits);
+  void fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampler& smp, uint64_t* rng, uint32_t* codes);
+  void generate(const int32_t* prompt, size_t cols, const s2hip_gen_params& p, uint64_t* rng, int32_t* codes,
+                uint32_t* n_frames, s2hip_gen_stats* stats);
+  uint32_t n_past_host = 0;
+
+  // op level
+  void op_linear(const void* w, uint32_t type, size_t in, size_t out, const float* x, size_t ncol, float* y);
+  void op_rms_norm(const float* x, const float* w, size_t n, size_t ncol, float eps, float* y);
+  void op_dequant(const void* w, uint32_t type, size_t in, size_t rows, float* out);
+  void op_qk_rope(const float* qkv, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t pos, float base,
+                  const float* qn, const float* kn, float eps, float* q, float* k, float* v);
+  void op_attention(const float* q, const float* k, const float* v, uint32_t H, uint32_t Hkv, uint32_t hd,
+                    uint32_t T, float scale, float* out);
+  void op_swiglu(const float* g, const float* u, size_t n, int fast, float* out);
+  void op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
+                 uint32_t* tok);
+  void time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes);
+
+ private:
+  template <class T>
+  T* dalloc(size_t count, size_t pad = 0) {
+    void* p = nullptr;
+    HIPC(hipMalloc(&p, count * sizeof(T) + pad));
+    allocs_.push_back(p);
+    return static_cast<T*>(p);
+  }
+  void upload(void* dst, const void* src, size_t bytes);
+  DevLin load_lin(const GgufFile& g, const std::string& name, uint64_t in, uint64_t out);
+  float* load_norm(const GgufFile& g, const std::string& name, uint64_t n);
+  uint16_t* load_f16_table(const GgufFile& g, const std::string& name, uint64_t dim, uint64_t min_rows,
+                           uint64_t* rows_out);
+  void build_rope(float2* dst, uint32_t positions, uint32_t hd, float base);
+
+  void gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
+            const float* norm, float eps, float* y, uint32_t ldy, const uint32_t* row_map, uint32_t out_rows,
+            const uint32_t* done);
+  void enqueue_slow_layers(uint32_t ncol, const uint32_t* done);
+  void enqueue_head(uint32_t col, bool full, const uint32_t* done);
+  void enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* done);
+  void enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done);
+  void enqueue_frame(const SamplerCfg& cfg);
+  void enqueue_prefill(const int32_t* prompt_dev, size_t n_tok);
+  void ensure_prompt(size_t n_int);
+  void ensure_codes(size_t n_int);
+  void check_state_err();
+
+  hipStream_t stream_ = nullptr;
+  std::vector<void*> allocs_;
+  uint8_t* staging_[2] = {nullptr, nullptr};
+  hipEvent_t staging_ev_[2] = {nullptr, nullptr};
+  static constexpr size_t STAGING = 64u << 20;
+  uint32_t im_end_ = 0;
+  uint32_t flags_ = 0;
+
+  // weights
+  uint16_t *emb_ = nullptr, *cb_emb_ = nullptr, *fast_emb_ = nullptr;
+  uint64_t cb_rows_ = 0;
+  float *norm_ = nullptr, *fast_norm_ = nullptr;
+  DevLin head_full_, fast_out_;
+  std::vector<SlowLayer> slow_;
+  std::vector<FastLayer> fast_;
+  uint32_t* head_rows_ = nullptr;
+  uint32_t n_cand_ = 0;
+
+  // activations
+  float *h_ = nullptr, *qkv_ = nullptr, *q_ = nullptr, *att_ = nullptr, *part_ = nullptr, *act_ = nullptr;
+  float *hn_ = nullptr, *logits_c_ = nullptr, *logits_full_ = nullptr;
+  float *kc_ = nullptr, *vc_ = nullptr;
+  float2 *rope_slow_ = nullptr, *rope_fast_ = nullptr;
+  uint32_t attn_chunk_ = 64, attn_chunks_ = 1;
+  float *fh_ = nullptr, *fqkv_ = nullptr, *fq_ = nullptr, *fatt_ = nullptr, *fpart_ = nullptr, *fact_ = nullptr;
+  float *flogits_ = nullptr, *fkc_ = nullptr, *fvc_ = nullptr;
+  uint32_t fctx_ = 11;
+
+  DevState* st_ = nullptr;
+  DevState* st_host_ = nullptr;  // pinned
+  uint32_t* done_host_ = nullptr;  // pinned [2]
+  int32_t* codes_dev_ = nullptr;
+  size_t codes_cap_ = 0;
+  int32_t* prompt_dev_ = nullptr;
+  size_t prompt_cap_ = 0;
+
+  hipGraphExec_t graph_exec_ = nullptr;
+  hipGraph_t graph_ = nullptr;
+  SamplerCfg graph_cfg_{};
+  int32_t* graph_codes_ = nullptr;
+};
+
+Engine::Engine(const s2hip_config& cfg) {
+  if (!cfg.gguf_path) fail("gguf_path is NULL");
+  if (cfg.max_seq_len == 0) fail("max_seq_len must be non-zero");
+  device = cfg.device;
+  flags_ = cfg.flags;
+  im_end_ = cfg.im_end_id;
+  int ndev = 0;
+  HIPC(hipGetDeviceCount(&ndev));
+  if (device < 0 || device >= ndev) fail("HIP device " + std::to_string(device) + " not present");
+  select();
+  HIPC(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  for (int i = 0; i < 2; ++i) {
+    HIPC(hipHostMalloc(reinterpret_cast<void**>(&staging_[i]), STAGING, hipHostMallocDefault));
+    HIPC(hipEventCreateWithFlags(&staging_ev_[i], hipEventDisableTiming));
+  }
+
+  GgufFile g;
+  g.open(cfg.gguf_path);
+  // DualArGraphSpec::from_gguf (crates/fish_s2_infer/src/registry.rs:45-214), shape-generic.
+  if (g.str("general.architecture") != "fish-speech")
+    fail("expected fish-speech transformer GGUF, got " + g.str("general.architecture"));
+  s2hip_spec& s = spec;
+  s.slow_layers = g.u32("fish-speech.block_count");
+  s.dim = g.u32("fish-speech.embedding_length");
+  s.ffn = g.u32("fish-speech.feed_forward_length");
+  s.heads = g.u32("fish-speech.attention.head_count");
+  s.kv_heads = g.u32("fish-speech.attention.head_count_kv");
+  s.rope_base = g.f32("fish-speech.rope.freq_base");
+  s.eps = g.f32("fish-speech.attention.layer_norm_rms_epsilon");
+  s.slow_qk_norm = g.flag("fish_speech.attention_qk_norm") ? 1u : 0u;
+  s.head_dim = s.slow_qk_norm ? uint32_t(g.tensor("layers.0.attention.q_norm.weight").elements())
+                              : s.dim / std::max(1u, s.heads);
+  s.fast_layers = g.u32("fish_speech.fast_block_count");
+  const uint32_t fast_dim = g.u32("fish_speech.fast_embedding_length");
+  s.fast_ffn = g.u32("fish_speech.fast_feed_forward_length");
+  s.fast_heads = g.u32("fish_speech.fast_head_count");
+  s.fast_kv_heads = g.u32("fish_speech.fast_head_count_kv");
+  s.fast_head_dim = g.u32("fish_speech.fast_head_dim");
+  s.fast_rope_base = g.f32("fish_speech.fast_rope_freq_base");
+  s.fast_eps = g.f32("fish_speech.fast_layer_norm_rms_eps");
+  s.codebook_size = g.u32("fish_speech.codebook_size");
+  s.num_codebooks = g.u32("fish_speech.num_codebooks");
+  s.semantic_begin = g.u32("fish_speech.semantic_begin_id");
+  s.semantic_end = g.u32("fish_speech.semantic_end_id");
+  s.scale_codebook_embeddings = g.flag("fish_speech.scale_codebook_embeddings") ? 1u : 0u;
+  if (g.flag("fish_speech.fast_project_in")) fail("fast_project_in is not implemented");  // fast_ar.rs:366-370
+  if (fast_dim != s.dim) fail("fast embedding_length must equal the slow embedding_length");
+  if (s.kv_heads == 0 || s.heads % s.kv_heads) fail("invalid GQA head split");
+  if (s.fast_kv_heads == 0 || s.fast_heads % s.fast_kv_heads) fail("invalid fast GQA head split");
+  if (s.head_dim == 0 || s.head_dim % 4 || s.head_dim > 256 || s.fast_head_dim == 0 || s.fast_head_dim % 4 ||
+      s.fast_head_dim > 256)
+    fail("head_dim must be a non-zero multiple of 4 and at most 256");
+  if (s.num_codebooks == 0 || s.num_codebooks > 16) fail("num_codebooks must be in 1..16");
+  if (s.semantic_end < s.semantic_begin) fail("invalid semantic id range");
+  if (s.dim % 8) fail("embedding_length must be a multiple of 8");
+  s.max_seq_len = cfg.max_seq_len;
+
+  uint64_t vocab_rows = 0;
+  emb_ = load_f16_table(g, "embeddings.weight", s.dim, 1, &vocab_rows);
+  s.vocab = uint32_t(vocab_rows);
+  if (s.semantic_end >= s.vocab) fail("semantic ids exceed the vocabulary");
+  cb_emb_ = load_f16_table(g, "codebook_embeddings.weight", s.dim, uint64_t(s.num_codebooks) * s.codebook_size,
+                           &cb_rows_);
+  uint64_t fast_rows = 0;
+  fast_emb_ = load_f16_table(g, "fast_embeddings.weight", s.dim, s.codebook_size, &fast_rows);
+  norm_ = load_norm(g, "norm.weight", s.dim);
+  fast_norm_ = load_norm(g, "fast_norm.weight", s.dim);
+  fast_out_ = load_lin(g, "fast_output.weight", s.dim, s.codebook_size);
+  head_full_.w = reinterpret_cast<uint8_t*>(emb_);
+  head_full_.type = W_F16;
+  head_full_.in = s.dim;
+  head_full_.out = s.vocab;
+  head_full_.row_bytes = size_t(s.dim) * 2;
+  head_full_.bytes = uint64_t(s.vocab) * s.dim * 2;
+
+  const uint64_t q = uint64_t(s.heads) * s.head_dim, kv = uint64_t(s.kv_heads) * s.head_dim;
+  slow_.resize(s.slow_layers);
+  for (uint32_t l = 0; l < s.slow_layers; ++l) {
+    SlowLayer& L = slow_[l];
+    L.attn_norm = load_norm(g, lname("layers", l, "attention_norm.weight"), s.dim);
+    L.ffn_norm = load_norm(g, lname("layers", l, "ffn_norm.weight"), s.dim);
+    if (s.slow_qk_norm) {
+      L.q_norm = load_norm(g, lname("layers", l, "attention.q_norm.weight"), s.head_dim);
+      L.k_norm = load_norm(g, lname("layers", l, "attention.k_norm.weight"), s.head_dim);
+    }
+    L.wqkv = load_lin(g, lname("layers", l, "attention.wqkv.weight"), s.dim, q + 2 * kv);
+    L.wo = load_lin(g, lname("layers", l, "attention.wo.weight"), q, s.dim);
+    L.w1 = load_lin(g, lname("layers", l, "feed_forward.w1.weight"), s.dim, s.ffn);
+    L.w2 = load_lin(g, lname("layers", l, "feed_forward.w2.weight"), s.ffn, s.dim);
+    L.w3 = load_lin(g, lname("layers", l, "feed_forward.w3.weight"), s.dim, s.ffn);
+  }
+  s.linear_type = s.slow_layers ? slow_[0].wqkv.type : uint32_t(W_F16);
+  const uint64_t fq = uint64_t(s.fast_heads) * s.fast_head_dim, fkv = uint64_t(s.fast_kv_heads) * s.fast_head_dim;
+  fast_.resize(s.fast_layers);
+  for (uint32_t l = 0; l < s.fast_layers; ++l) {
+    FastLayer& L = fast_[l];
+    L.attn_norm = load_norm(g, lname("fast_layers", l, "attention_norm.weight"), s.dim);
+    L.ffn_norm = load_norm(g, lname("fast_layers", l, "ffn_norm.weight"), s.dim);
+    L.wqkv = load_lin(g, lname("fast_layers", l, "attention.wqkv.weight"), s.dim, fq + 2 * fkv);
+    L.wo = load_lin(g, lname("fast_layers", l, "attention.wo.weight"), fq, s.dim);
+    L.w1 = load_lin(g, lname("fast_layers", l, "feed_forward.w1.weight"), s.dim, s.fast_ffn);
+    L.w2 = load_lin(g, lname("fast_layers", l, "feed_forward.w2.weight"), s.fast_ffn, s.dim);
+    L.w3 = load_lin(g, lname("fast_layers", l, "feed_forward.w3.weight"), s.dim, s.fast_ffn);
+  }
+  HIPC(hipStreamSynchronize(stream_));
+  for (int i = 0; i < 2; ++i) {
+    HIPC(hipHostFree(staging_[i]));
+    staging_[i] = nullptr;
+  }
+
+  // candidate rows of the output head: semantic ids + im_end, ascending
+  std::vector<uint32_t> rows;
+  for (uint32_t id = s.semantic_begin; id <= s.semantic_end; ++id) rows.push_back(id);
+  if (im_end_ < s.vocab && (im_end_ < s.semantic_begin || im_end_ > s.semantic_end)) rows.push_back(im_end_);
+  std::sort(rows.begin(), rows.end());
+  n_cand_ = uint32_t(rows.size());
+  if (n_cand_ > 8191) fail("too many sampling candidates");
+  head_rows_ = dalloc<uint32_t>(rows.size());
+  HIPC(hipMemcpy(head_rows_, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
+
+  // activations
+  const uint32_t NC = PREFILL_COLS;
+  const uint64_t qkv_w = q + 2 * kv;
+  attn_chunk_ = 64u * ((s.max_seq_len + 64u * 16u - 1u) / (64u * 16u));
+  attn_chunks_ = (s.max_seq_len + attn_chunk_ - 1) / attn_chunk_;
+  h_ = dalloc<float>(size_t(NC) * s.dim);
+  qkv_ = dalloc<float>(size_t(NC) * qkv_w);
+  q_ = dalloc<float>(size_t(NC) * q);
+  att_ = dalloc<float>(size_t(NC) * q);
+  part_ = dalloc<float>(size_t(NC) * s.heads * attn_chunks_ * (s.head_dim + 2));
+  act_ = dalloc<float>(size_t(NC) * s.ffn);
+  hn_ = dalloc<float>(s.dim);
+  logits_c_ = dalloc<float>(n_cand_);
+  logits_full_ = dalloc<float>(s.vocab);
+  const size_t kv_elems = size_t(s.slow_layers) * kv * s.max_seq_len;
+  kc_ = dalloc<float>(kv_elems);
+  vc_ = dalloc<float>(kv_elems);
+  HIPC(hipMemset(kc_, 0, kv_elems * 4));
+  HIPC(hipMemset(vc_, 0, kv_elems * 4));
+  fctx_ = s.num_codebooks + 1;
+  rope_slow_ = dalloc<float2>(size_t(s.max_seq_len) * (s.head_dim / 2));
+  rope_fast_ = dalloc<float2>(size_t(fctx_) * (s.fast_head_dim / 2));
+  build_rope(rope_slow_, s.max_seq_len, s.head_dim, s.rope_base);
+  build_rope(rope_fast_, fctx_, s.fast_head_dim, s.fast_rope_base);
+  fh_ = dalloc<float>(2 * size_t(s.dim));
+  fqkv_ = dalloc<float>(2 * (fq + 2 * fkv));
+  fq_ = dalloc<float>(2 * fq);
+  fatt_ = dalloc<float>(2 * fq);
+  fpart_ = dalloc<float>(2 * size_t(s.fast_heads) * 1 * (s.fast_head_dim + 2));
+  fact_ = dalloc<float>(2 * size_t(s.fast_ffn));
+  flogits_ = dalloc<float>(s.codebook_size);
+  fkc_ = dalloc<float>(size_t(s.fast_layers) * fkv * fctx_);
+  fvc_ = dalloc<float>(size_t(s.fast_layers) * fkv * fctx_);
+  HIPC(hipMemset(fkc_, 0, size_t(s.fast_layers) * fkv * fctx_ * 4));
+  HIPC(hipMemset(fvc_, 0, size_t(s.fast_layers) * fkv * fctx_ * 4));
+  st_ = dalloc<DevState>(1);
+  HIPC(hipMemset(st_, 0, sizeof(DevState)));
+  HIPC(hipHostMalloc(reinterpret_cast<void**>(&st_host_), sizeof(DevState), hipHostMallocDefault));
+  HIPC(hipHostMalloc(reinterpret_cast<void**>(&done_host_), 2 * sizeof(uint32_t), hipHostMallocDefault));
+  s.weight_bytes = 0;
+  for (auto& L : slow_) s.weight_bytes += L.wqkv.bytes + L.wo.bytes + L.w1.bytes + L.w2.bytes + L.w3.bytes;
+  for (auto& L : fast_) s.weight_bytes += L.wqkv.bytes + L.wo.bytes + L.w1.bytes + L.w2.bytes + L.w3.bytes;
+  s.weight_bytes += head_full_.bytes + cb_rows_ * s.dim * 2 + fast_rows * s.dim * 2 + fast_out_.bytes;
+  HIPC(hipDeviceSynchronize());
+}
+
+Engine::~Engine() {
+  if (device >= 0) (void)hipSetDevice(device);
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
+  if (graph_) (void)hipGraphDestroy(graph_);
+  for (void* p : allocs_) (void)hipFree(p);
+  for (int i = 0; i < 2; ++i) {
+    if (staging_[i]) (void)hipHostFree(staging_[i]);
+    if (staging_ev_[i]) (void)hipEventDestroy(staging_ev_[i]);
+  }
+  if (st_host_) (void)hipHostFree(st_host_);
+  if (done_host_) (void)hipHostFree(done_host_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+// Chunked pinned double-buffered upload from the mapped file.
+void Engine::upload(void* dst, const void* src, size_t bytes) {
+  static int slot = 0;
+  const uint8_t* s8 = static_cast<const uint8_t*>(src);
+  uint8_t* d8 = static_cast<uint8_t*>(dst);
+  for (size_t off = 0; off < bytes; off += STAGING) {
+    const size_t n = std::min(STAGING, bytes - off);
+    HIPC(hipEventSynchronize(staging_ev_[slot]));
+    memcpy(staging_[slot], s8 + off, n);
+    HIPC(hipMemcpyAsync(d8 + off, staging_[slot], n, hipMemcpyHostToDevice, stream_));
+    HIPC(hipEventRecord(staging_ev_[slot], stream_));
+    slot ^= 1;
+  }
+}
+
+DevLin Engine::load_lin(const GgufFile& g, const std::string& name, uint64_t in, uint64_t out) {
+  const GgufTensor& t = g.tensor(name);
+  if (t.dims.size() != 2 || t.dims[0] != in || t.dims[1] != out)
+    fail(name + " dimensions mismatch: expected [" + std::to_string(in) + ", " + std::to_string(out) + "]");
+  if (t.type != W_F16 && t.type != W_Q8_0 && t.type != W_Q4_0)
+    fail(name + ": unsupported linear weight type " + std::to_string(t.type));
+  DevLin L;
+  L.type = t.type;
+  L.in = uint32_t(in);
+  L.out = uint32_t(out);
+  L.row_bytes = size_t(ggml_row_bytes(t.type, in));
+  L.bytes = t.bytes;
+  L.w = dalloc<uint8_t>(t.bytes, WEIGHT_PAD);
+  HIPC(hipMemsetAsync(L.w + t.bytes, 0, WEIGHT_PAD, stream_));
+  upload(L.w, t.data, t.bytes);
+  return L;
+}
+
+float* Engine::load_norm(const GgufFile& g, const std::string& name, uint64_t n) {
+  const GgufTensor& t = g.tensor(name);
+  if (t.elements() != n) fail(name + ": expected " + std::to_string(n) + " elements");
+  std::vector<float> v(n);
+  if (t.type == 1) {
+    for (uint64_t i = 0; i < n; ++i) {
+      uint16_t b;
+      memcpy(&b, t.data + 2 * i, 2);
+      v[i] = f16_to_f32(b);
+    }
+  } else if (t.type == 0) {
+    memcpy(v.data(), t.data, n * 4);
+  } else {
+    fail(name + ": norm weights must be F16 or F32");
+  }
+  float* d = dalloc<float>(n);
+  HIPC(hipMemcpy(d, v.data(), n * 4, hipMemcpyHostToDevice));
+  return d;
+}
+
+uint16_t* Engine::load_f16_table(const GgufFile& g, const std::string& name, uint64_t dim, uint64_t min_rows,
+                                 uint64_t* rows_out) {
+  const GgufTensor& t = g.tensor(name);
+  if (t.dims.size() != 2 || t.dims[0] != dim || t.type != 1 || t.dims[1] < min_rows)
+    fail(name + ": expected an F16 [" + std::to_string(dim) + ", >=" + std::to_string(min_rows) + "] table");
+  *rows_out = t.dims[1];
+  uint16_t* d = dalloc<uint16_t>(t.bytes / 2, WEIGHT_PAD);
+  upload(d, t.data, t.bytes);
+  return d;
+}
+
+// apply_rope_normal's angles (crates/fish_s2_infer/src/attention.rs:195-203),
+// evaluated once on the host with the same libm calls in f32.
+void Engine::build_rope(float2* dst, uint32_t positions, uint32_t hd, float base) {
+  std::vector<float2> t(size_t(positions) * (hd / 2));
+  for (uint32_t pos = 0; pos < positions; ++pos) {
+    for (uint32_t pair = 0; pair < hd; pair += 2) {
+      const float theta = float(pos) / powf(base, float(pair) / float(hd));
+      t[size_t(pos) * (hd / 2) + pair / 2] = make_float2(cosf(theta), sinf(theta));
+    }
+  }
+  HIPC(hipMemcpy(dst, t.data(), t.size() * sizeof(float2), hipMemcpyHostToDevice));
+}
+
+void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
+                  const float* norm, float eps, float* y, uint32_t ldy, const uint32_t* row_map, uint32_t out_rows,
+                  const uint32_t* done) {
+  uint32_t c = 0;
+  while (c < ncol) {
+    uint32_t w = 8;
+    while (w > 1 && (w > ncol - c || size_t(w) * L.in * 4 > 150 * 1024)) w >>= 1;
+    GemvArgs a{};
+    a.w = L.w;
+    a.w3 = L3 ? L3->w : nullptr;
+    a.row_bytes = L.row_bytes;
+    a.row_map = row_map;
+    a.in = L.in;
+    a.out = out_rows;
+    a.x = x + size_t(c) * ldx;
+    a.ldx = ldx;
+    a.norm = norm;
+    a.eps = eps;
+    a.y = y + size_t(c) * ldy;
+    a.ldy = ldy;
+    a.done = done;
+    HIPC(launch_gemv(L.type, epi, int(w), a, stream_));
+    c += w;
+  }
+}
+
+void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
+  const s2hip_spec& s = spec;
+  const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim, qkv_w = q + 2 * kv;
+  for (uint32_t l = 0; l < s.slow_layers; ++l) {
+    const SlowLayer& L = slow_[l];
+    gemv(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, nullptr, L.wqkv.out, done);
+    QkvPostArgs pa{};
+    pa.qkv = qkv_;
+    pa.q_out = q_;
+    pa.k_cache = kc_ + size_t(l) * kv * s.max_seq_len;
+    pa.v_cache = vc_ + size_t(l) * kv * s.max_seq_len;
+    pa.q_norm = L.q_norm;
+    pa.k_norm = L.k_norm;
+    pa.rope = rope_slow_;
+    pa.pos_ptr = &st_->n_past;
+    pa.pos_offset = 0;
+    pa.H = s.heads;
+    pa.Hkv = s.kv_heads;
+    pa.hd = s.head_dim;
+    pa.max_seq = s.max_seq_len;
+    pa.ncol = ncol;
+    pa.eps = s.eps;
+    pa.done = done;
+    pa.err = &st_->err;
+    HIPC(launch_qkv_post(pa, stream_));
+    AttnArgs aa{};
+    aa.q = q_;
+    aa.k_cache = pa.k_cache;
+    aa.v_cache = pa.v_cache;
+    aa.part = part_;
+    aa.out = att_;
+    aa.pos_ptr = &st_->n_past;
+    aa.pos_offset = 0;
+    aa.H = s.heads;
+    aa.Hkv = s.kv_heads;
+    aa.hd = s.head_dim;
+    aa.max_seq = s.max_seq_len;
+    aa.ncol = ncol;
+    aa.chunk = attn_chunk_;
+    aa.max_chunks = attn_chunks_;
+    aa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
+    aa.done = done;
+    HIPC(launch_attention(aa, stream_));
+    gemv(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, nullptr, L.wo.out, done);
+    gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, nullptr, L.w1.out, done);
+    gemv(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, nullptr, L.w2.out, done);
+  }
+  HIPC(launch_add_position(st_, ncol, stream_));
+}
+
+// SlowArOutputHeadF16Weights::forward_logits (slow_ar.rs:943-955): post-norm
+// hidden -> tied embedding rows.  Generation only needs the candidate rows
+// (semantic ids + im_end); every other id is masked to -inf before sampling.
+void Engine::enqueue_head(uint32_t col, bool full, const uint32_t* done) {
+  const s2hip_spec& s = spec;
+  HIPC(launch_rms_norm(h_ + size_t(col) * s.dim, norm_, hn_, s.dim, 1, s.eps, done, stream_));
+  gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, head_rows_, n_cand_, done);
+  if (full)
+    gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_full_, s.vocab, nullptr, s.vocab, done);
+}
+
+void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* done) {
+  const s2hip_spec& s = spec;
+  const uint32_t fq = s.fast_heads * s.fast_head_dim, fkv = s.fast_kv_heads * s.fast_head_dim;
+  const uint32_t w = fq + 2 * fkv;
+  for (uint32_t l = 0; l < s.fast_layers; ++l) {
+    const FastLayer& L = fast_[l];
+    gemv(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, nullptr, L.wqkv.out, done);
+    QkvPostArgs pa{};
+    pa.qkv = fqkv_;
+    pa.q_out = fq_;
+    pa.k_cache = fkc_ + size_t(l) * fkv * fctx_;
+    pa.v_cache = fvc_ + size_t(l) * fkv * fctx_;
+    pa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
+    pa.k_norm = nullptr;
+    pa.rope = rope_fast_;
+    pa.pos_ptr = nullptr;
+    pa.pos_offset = p0;
+    pa.H = s.fast_heads;
+    pa.Hkv = s.fast_kv_heads;
+    pa.hd = s.fast_head_dim;
+    pa.max_seq = fctx_;
+    pa.ncol = ncol;
+    pa.eps = s.fast_eps;
+    pa.done = done;
+    pa.err = &st_->err;
+    HIPC(launch_qkv_post(pa, stream_));
+    AttnArgs aa{};
+    aa.q = fq_;
+    aa.k_cache = pa.k_cache;
+    aa.v_cache = pa.v_cache;
+    aa.part = fpart_;
+    aa.out = fatt_;
+    aa.pos_ptr = nullptr;
+    aa.pos_offset = p0;
+    aa.H = s.fast_heads;
+    aa.Hkv = s.fast_kv_heads;
+    aa.hd = s.fast_head_dim;
+    aa.max_seq = fctx_;
+    aa.ncol = ncol;
+    aa.chunk = 64;
+    aa.max_chunks = 1;
+    aa.scale = 1.0f / std::sqrt(float(s.fast_head_dim));  // fast_ar.rs:60-62
+    aa.done = done;
+    HIPC(launch_attention(aa, stream_));
+    gemv(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, nullptr, L.wo.out, done);
+    gemv(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, nullptr,
+         L.w1.out, done);
+    gemv(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, nullptr, L.w2.out, done);
+  }
+}
+
+// generate_codebooks_for_semantic (fast_ar.rs:440-470), incremental: sub-step 1
+// runs positions 0 (slow hidden) and 1 (fast_emb[code0]) together, each later
+// sub-step appends one position.  The sampler writes the next input row.
+void Engine::enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done) {
+  const s2hip_spec& s = spec;
+  HIPC(launch_fast_begin(st_, hn_, fast_emb_, fh_, s.dim, s.codebook_size, s.semantic_begin, s.semantic_end,
+                         stream_));
+  uint32_t ncol = 2, p0 = 0;
+  for (uint32_t cb = 1; cb < s.num_codebooks; ++cb) {
+    enqueue_fast_layers(ncol, p0, done);
+    gemv(fast_out_, nullptr, EPI_STORE, 1, fh_ + size_t(ncol - 1) * s.dim, s.dim, fast_norm_, s.fast_eps, flogits_,
+         s.codebook_size, nullptr, s.codebook_size, done);
+    SampleArgs sa{};
+    sa.logits = flogits_;
+    sa.n = s.codebook_size;
+    sa.vocab = s.codebook_size;
+    sa.cfg = cfg;
+    sa.st = st_;
+    sa.cb_index = cb;
+    sa.fast_emb = fast_emb_;
+    sa.next_input = (cb + 1 < s.num_codebooks) ? fh_ : nullptr;
+    sa.dim = s.dim;
+    HIPC(launch_sample_fast(sa, stream_));
+    p0 += ncol;
+    ncol = 1;
+  }
+}
+
+// One generate_codes loop iteration (generate.rs:165-211): Fast-AR codebooks
+// for the current main token, Slow-AR step on [main, codes...], next sample.
+void Engine::enqueue_frame(const SamplerCfg& cfg) {
+  const s2hip_spec& s = spec;
+  const uint32_t* done = &st_->done;
+  enqueue_fast_frame(cfg, done);
+  EmbedArgs ea{};
+  ea.tokens = nullptr;
+  ea.state = st_;
+  ea.emb = emb_;
+  ea.cb_emb = cb_emb_;
+  ea.h = h_;
+  ea.n = 1;
+  ea.dim = s.dim;
+  ea.vocab = s.vocab;
+  ea.cb_rows = uint32_t(cb_rows_);
+  ea.num_codebooks = s.num_codebooks;
+  ea.codebook_size = s.codebook_size;
+  ea.sem_begin = s.semantic_begin;
+  ea.sem_end = s.semantic_end;
+  ea.sem_scale = 1.0f / std::sqrt(float(s.num_codebooks + 1));
+  ea.scale_enabled = s.scale_codebook_embeddings;
+  ea.done = done;
+  ea.err = &st_->err;
+  HIPC(launch_embed(ea, stream_));
+  enqueue_slow_layers(1, done);
+  enqueue_head(0, false, done);
+  SampleArgs sa{};
+  sa.logits = logits_c_;
+  sa.ids = head_rows_;
+  sa.n = n_cand_;
+  sa.vocab = s.vocab;
+  sa.cfg = cfg;
+  sa.st = st_;
+  sa.im_end = im_end_;
+  sa.after_step = 1;
+  sa.codes_out = codes_dev_;
+  sa.num_codebooks = s.num_codebooks;
+  HIPC(launch_sample_slow(sa, stream_));
+}
+
+void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  size_t t = 0;
+  uint32_t last_cols = 1;
+  while (t < n_tok) {
+    const uint32_t nc = uint32_t(std::min<size_t>(PREFILL_COLS, n_tok - t));
+    EmbedArgs ea{};
+    ea.tokens = prompt_dev + t * cdim;
+    ea.emb = emb_;
+    ea.cb_emb = cb_emb_;
+    ea.h = h_;
+    ea.n = nc;
+    ea.dim = s.dim;
+    ea.vocab = s.vocab;
+    ea.cb_rows = uint32_t(cb_rows_);
+    ea.num_codebooks = s.num_codebooks;
+    ea.codebook_size = s.codebook_size;
+    ea.sem_begin = s.semantic_begin;
+    ea.sem_end = s.semantic_end;
+    ea.sem_scale = 1.0f / std::sqrt(float(cdim));
+    ea.scale_enabled = s.scale_codebook_embeddings;
+    ea.err = &st_->err;
+    HIPC(launch_embed(ea, stream_));
+    enqueue_slow_layers(nc, nullptr);
+    t += nc;
+    last_cols = nc;
+  }
+  (void)last_cols;
+}
+
+void Engine::ensure_prompt(size_t n_int) {
+  if (n_int <= prompt_cap_) return;
+  if (prompt_dev_) {
+    HIPC(hipStreamSynchronize(stream_));
+    HIPC(hipFree(prompt_dev_));
+    allocs_.erase(std::find(allocs_.begin(), allocs_.end(), static_cast<void*>(prompt_dev_)));
+  }
+  prompt_cap_ = std::max<size_t>(n_int, 4096);
+  prompt_dev_ = dalloc<int32_t>(prompt_cap_);
+}
+
+void Engine::ensure_codes(size_t n_int) {
+  if (n_int <= codes_cap_ && codes_dev_) return;
+  if (codes_dev_) {
+    HIPC(hipStreamSynchronize(stream_));
+    HIPC(hipFree(codes_dev_));
+    allocs_.erase(std::find(allocs_.begin(), allocs_.end(), static_cast<void*>(codes_dev_)));
+  }
+  codes_cap_ = std::max<size_t>(n_int, 16 * 1024);
+  codes_dev_ = dalloc<int32_t>(codes_cap_);
+}
+
+void Engine::check_state_err() {
+  if (st_host_->err & ERR_TOKEN_RANGE) fail("token id out of range");
+  if (st_host_->err & ERR_KV_OVERFLOW) fail("KV cache overflow");
+  if (st_host_->err & ERR_SAMPLER) fail("sampler failure");
+}
+
+void Engine::reset() {
+  select();
+  HIPC(hipStreamSynchronize(stream_));
+  HIPC(hipMemsetAsync(st_, 0, sizeof(DevState), stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  n_past_host = 0;
+}
+
+void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out) {
+  select();
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  if (n_tok == 0) fail("expected at least one token");
+  if (n_past_host + n_tok > s.max_seq_len)
+    fail("KV cache overflow: n_past=" + std::to_string(n_past_host) + " n_tokens=" + std::to_string(n_tok) +
+         " max_seq_len=" + std::to_string(s.max_seq_len));
+  for (size_t t = 0; t < n_tok; ++t) {
+    const int32_t id = flat[t * cdim];
+    if (id < 0) fail("semantic token id must be non-negative, got " + std::to_string(id));
+    if (uint32_t(id) >= s.vocab) fail("embedding index " + std::to_string(id) + " out of range");
+    if (uint32_t(id) >= s.semantic_begin && uint32_t(id) <= s.semantic_end)
+      for (uint32_t cb = 0; cb < s.num_codebooks; ++cb)
+        if (flat[t * cdim + 1 + cb] < 0 ||
+            uint64_t(flat[t * cdim + 1 + cb]) + uint64_t(cb) * s.codebook_size >= cb_rows_)
+          fail("codebook token out of range");
+  }
+  ensure_prompt(n_tok * cdim);
+  HIPC(hipMemcpyAsync(prompt_dev_, flat, n_tok * cdim * 4, hipMemcpyHostToDevice, stream_));
+  // done = 0, err = 0 (eval never runs under a finished frame loop)
+  HIPC(hipMemsetAsync(&st_->done, 0, sizeof(uint32_t), stream_));
+  HIPC(hipMemsetAsync(&st_->err, 0, sizeof(uint32_t), stream_));
+  enqueue_prefill(prompt_dev_, n_tok);
+  const uint32_t last_col = uint32_t((n_tok - 1) % PREFILL_COLS);
+  enqueue_head(last_col, logits_out != nullptr, nullptr);
+  HIPC(hipMemcpyAsync(hidden_out, hn_, s.dim * 4, hipMemcpyDeviceToHost, stream_));
+  if (logits_out) HIPC(hipMemcpyAsync(logits_out, logits_full_, size_t(s.vocab) * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  check_state_err();
+  n_past_host += uint32_t(n_tok);
+}
+
+void Engine::fast_logits(const float* hidden, const uint32_t* prefix, size_t plen, float* logits) {
+  select();
+  const s2hip_spec& s = spec;
+  if (plen >= s.num_codebooks) fail("fast prefix too long: " + std::to_string(plen) + " codes");
+  std::vector<uint16_t> row(s.dim);
+  std::vector<float> rowf(s.dim);
+  HIPC(hipMemcpyAsync(fh_, hidden, s.dim * 4, hipMemcpyHostToDevice, stream_));
+  enqueue_fast_layers(1, 0, nullptr);
+  for (size_t j = 0; j < plen; ++j) {
+    if (prefix[j] >= s.codebook_size) fail("fast prefix code out of range");
+    HIPC(hipMemcpyAsync(row.data(), fast_emb_ + size_t(prefix[j]) * s.dim, s.dim * 2, hipMemcpyDeviceToHost,
+                        stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    for (uint32_t i = 0; i < s.dim; ++i) rowf[i] = f16_to_f32(row[i]);
+    HIPC(hipMemcpyAsync(fh_, rowf.data(), s.dim * 4, hipMemcpyHostToDevice, stream_));
+    enqueue_fast_layers(1, uint32_t(j + 1), nullptr);
+  }
+  gemv(fast_out_, nullptr, EPI_STORE, 1, fh_, s.dim, fast_norm_, s.fast_eps, flogits_, s.codebook_size, nullptr,
+       s.codebook_size, nullptr);
+  HIPC(hipMemcpyAsync(logits, flogits_, s.codebook_size * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampler& smp, uint64_t* rng,
+                            uint32_t* codes) {
+  select();
+  const s2hip_spec& s = spec;
+  if (sem >= s.codebook_size) fail("semantic_code " + std::to_string(sem) + " >= codebook_size");
+  DevState init{};
+  init.main_token = s.semantic_begin + sem;
+  init.rng = *rng;
+  HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  init.n_past = st_host_->n_past;  // keep the Slow-AR position
+  *st_host_ = init;
+  HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(hn_, hidden, s.dim * 4, hipMemcpyHostToDevice, stream_));
+  enqueue_fast_frame(SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, nullptr);
+  HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  check_state_err();
+  for (uint32_t cb = 0; cb < s.num_codebooks; ++cb) codes[cb] = st_host_->codes_frame[cb];
+  *rng = st_host_->rng;
+}
+
+// generate_codes (crates/fish_s2_infer/src/generate.rs:117-221)
+void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params& p, uint64_t* rng, int32_t* codes,
+                      uint32_t* n_frames, s2hip_gen_stats* stats) {
+  select();
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  if (cols == 0) fail("expected at least one token");
+  if (cols > s.max_seq_len)
+    fail("KV cache overflow: n_past=0 n_tokens=" + std::to_string(cols) + " max_seq_len=" + std::to_string(s.max_seq_len));
+  for (size_t t = 0; t < cols; ++t) {
+    const int32_t id = prompt[t * cdim];
+    if (id < 0 || uint32_t(id) >= s.vocab) fail("prompt token id out of range: " + std::to_string(id));
+    if (uint32_t(id) >= s.semantic_begin && uint32_t(id) <= s.semantic_end)
+      for (uint32_t cb = 0; cb < s.num_codebooks; ++cb)
+        if (prompt[t * cdim + 1 + cb] < 0 ||
+            uint64_t(prompt[t * cdim + 1 + cb]) + uint64_t(cb) * s.codebook_size >= cb_rows_)
+          fail("prompt codebook token out of range");
+  }
+  const SamplerCfg cfg{p.temperature, p.top_p, p.top_k};
+  const size_t ncodes = size_t(s.num_codebooks) * p.max_new_tokens;
+  ensure_codes(ncodes);
+  ensure_prompt(cols * cdim);
+  HIPC(hipStreamSynchronize(stream_));
+  // SlowArState::reset + sampler state
+  DevState init{};
+  init.rng = *rng;
+  init.prompt_cols = uint32_t(cols);
+  init.max_new = p.max_new_tokens;
+  init.min_tokens_before_end = p.min_tokens_before_end;
+  *st_host_ = init;
+  HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemsetAsync(codes_dev_, 0, ncodes * 4 + 4, stream_));
+  HIPC(hipMemcpyAsync(prompt_dev_, prompt, cols * cdim * 4, hipMemcpyHostToDevice, stream_));
+  hipEvent_t ev[3];
+  for (auto& e : ev) HIPC(hipEventCreate(&e));
+  HIPC(hipEventRecord(ev[0], stream_));
+  enqueue_prefill(prompt_dev_, cols);
+  enqueue_head(uint32_t((cols - 1) % PREFILL_COLS), false, nullptr);
+  SampleArgs sa{};
+  sa.logits = logits_c_;
+  sa.ids = head_rows_;
+  sa.n = n_cand_;
+  sa.vocab = s.vocab;
+  sa.cfg = cfg;
+  sa.st = st_;
+  sa.im_end = im_end_;
+  sa.after_step = 0;
+  sa.num_codebooks = s.num_codebooks;
+  HIPC(launch_sample_slow(sa, stream_));
+  HIPC(hipEventRecord(ev[1], stream_));
+
+  const uint32_t max_frames = std::min<uint32_t>(p.max_new_tokens, s.max_seq_len - uint32_t(cols));
+  bool use_graph = !(flags_ & S2HIP_FLAG_NO_GRAPH);
+  uint32_t launched = 0;
+  if (max_frames > 0) {
+    enqueue_frame(cfg);  // frame 0 eagerly (also configures every kernel)
+    launched = 1;
+  }
+  if (use_graph && launched < max_frames) {
+    const bool stale = !graph_exec_ || graph_codes_ != codes_dev_ || graph_cfg_.temperature != cfg.temperature ||
+                       graph_cfg_.top_p != cfg.top_p || graph_cfg_.top_k != cfg.top_k;
+    if (stale) {
+      if (graph_exec_) {
+        HIPC(hipGraphExecDestroy(graph_exec_));
+        graph_exec_ = nullptr;
+      }
+      if (graph_) {
+        HIPC(hipGraphDestroy(graph_));
+        graph_ = nullptr;
+      }
+      HIPC(hipStreamBeginCapture(stream_, hipStreamCaptureModeRelaxed));
+      try {
+        enqueue_frame(cfg);
+      } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      HIPC(hipStreamEndCapture(stream_, &graph_));
+      HIPC(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
+      graph_cfg_ = cfg;
+      graph_codes_ = codes_dev_;
+    }
+  }
+  // Frames in batches; the done flag of batch i is read while batch i+1 runs.
+  int pending = -1;
+  hipEvent_t flag_ev[2];
+  for (auto& e : flag_ev) HIPC(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+  int slot = 0;
+  bool finished = false;
+  while (launched < max_frames && !finished) {
+    const uint32_t n = std::min(FRAME_BATCH, max_frames - launched);
+    for (uint32_t i = 0; i < n; ++i) {
+      if (use_graph)
+        HIPC(hipGraphLaunch(graph_exec_, stream_));
+      else
+        enqueue_frame(cfg);
+    }
+    launched += n;
+    HIPC(hipMemcpyAsync(&done_host_[slot], &st_->done, 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipEventRecord(flag_ev[slot], stream_));
+    if (pending >= 0) {
+      HIPC(hipEventSynchronize(flag_ev[pending]));
+      if (done_host_[pending]) finished = true;
+    }
+    pending = slot;
+    slot ^= 1;
+  }
+  HIPC(hipEventRecord(ev[2], stream_));
+  HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  for (auto& e : flag_ev) (void)hipEventDestroy(e);
+  float ms_prefill = 0.0f, ms_decode = 0.0f;
+  HIPC(hipEventElapsedTime(&ms_prefill, ev[0], ev[1]));
+  HIPC(hipEventElapsedTime(&ms_decode, ev[1], ev[2]));
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  check_state_err();
+  const uint32_t nf = st_host_->step_index;
+  std::vector<int32_t> full(ncodes);
+  if (ncodes) HIPC(hipMemcpy(full.data(), codes_dev_, ncodes * 4, hipMemcpyDeviceToHost));
+  // compact_codes (generate.rs:346-390): codebook-major [num_codebooks][n_frames]
+  for (uint32_t cb = 0; cb < s.num_codebooks; ++cb)
+    for (uint32_t t = 0; t < nf; ++t) codes[size_t(cb) * nf + t] = full[size_t(cb) * p.max_new_tokens + t];
+  *n_frames = nf;
+  *rng = st_host_->rng;
+  n_past_host = st_host_->n_past;
+  if (stats) {
+    stats->prefill_ms = ms_prefill;
+    stats->decode_ms = ms_decode;
+    stats->n_frames = nf;
+    stats->graph_used = use_graph ? 1u : 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// op level
+// ---------------------------------------------------------------------------
+namespace {
+struct TmpBuf {
+  void* p = nullptr;
+  TmpBuf(size_t bytes) { hip_check(hipMalloc(&p, bytes + WEIGHT_PAD), "hipMalloc"); }
+  ~TmpBuf() { (void)hipFree(p); }
+  template <class T>
+  T* as() { return static_cast<T*>(p); }
+};
+}  // namespace
+
+void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, const float* x, size_t ncol, float* y) {
+  select();
+  if (type != W_F16 && type != W_Q8_0 && type != W_Q4_0) fail("unsupported weight type");
+  if (in == 0 || out == 0 || ncol == 0) fail("empty linear");
+  const size_t rb = size_t(ggml_row_bytes(type, in));
+  TmpBuf dw(rb * out), dx(in * ncol * 4), dy(out * ncol * 4);
+  HIPC(hipMemsetAsync(dw.as<uint8_t>() + rb * out, 0, WEIGHT_PAD, stream_));
+  HIPC(hipMemcpyAsync(dw.p, w, rb * out, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(dx.p, x, in * ncol * 4, hipMemcpyHostToDevice, stream_));
+  DevLin L;
+  L.w = dw.as<uint8_t>();
+  L.type = type;
+  L.in = uint32_t(in);
+  L.out = uint32_t(out);
+  L.row_bytes = rb;
+  gemv(L, nullptr, EPI_STORE, uint32_t(ncol), dx.as<float>(), uint32_t(in), nullptr, 0.0f, dy.as<float>(),
+       uint32_t(out), nullptr, uint32_t(out), nullptr);
+  HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_rms_norm(const float* x, const float* w, size_t n, size_t ncol, float eps, float* y) {
+  select();
+  if (n == 0) fail("rms_norm input is empty");
+  TmpBuf dx(n * ncol * 4), dw(n * 4), dy(n * ncol * 4);
+  HIPC(hipMemcpyAsync(dx.p, x, n * ncol * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(dw.p, w, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(launch_rms_norm(dx.as<float>(), dw.as<float>(), dy.as<float>(), uint32_t(n), uint32_t(ncol), eps, nullptr,
+                       stream_));
+  HIPC(hipMemcpyAsync(y, dy.p, n * ncol * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_dequant(const void* w, uint32_t type, size_t in, size_t rows, float* out) {
+  select();
+  if (type != W_F16 && type != W_Q8_0 && type != W_Q4_0) fail("unsupported weight type");
+  const size_t rb = size_t(ggml_row_bytes(type, in));
+  TmpBuf dw(rb * rows), dy(in * rows * 4);
+  HIPC(hipMemsetAsync(dw.as<uint8_t>() + rb * rows, 0, WEIGHT_PAD, stream_));
+  HIPC(hipMemcpyAsync(dw.p, w, rb * rows, hipMemcpyHostToDevice, stream_));
+  HIPC(launch_dequant_rows(type, dw.as<uint8_t>(), rb, uint32_t(rows), uint32_t(in), dy.as<float>(), stream_));
+  HIPC(hipMemcpyAsync(out, dy.p, in * rows * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_qk_rope(const float* qkv, uint32_t H, uint32_t Hkv, uint32_t hd, uint32_t pos, float base,
+                        const float* qn, const float* kn, float eps, float* q, float* k, float* v) {
+  select();
+  if (Hkv == 0 || H % Hkv || hd == 0 || hd % 2 || hd > 256) fail("invalid attention shape");
+  const size_t width = size_t(H + 2 * Hkv) * hd;
+  TmpBuf dqkv(width * 4), dq(size_t(H) * hd * 4), dk(size_t(Hkv) * hd * 4), dv(size_t(Hkv) * hd * 4),
+      dqn(hd * 4), dkn(hd * 4), drope(size_t(pos + 1) * (hd / 2) * sizeof(float2));
+  HIPC(hipMemcpyAsync(dqkv.p, qkv, width * 4, hipMemcpyHostToDevice, stream_));
+  if (qn) HIPC(hipMemcpyAsync(dqn.p, qn, hd * 4, hipMemcpyHostToDevice, stream_));
+  if (kn) HIPC(hipMemcpyAsync(dkn.p, kn, hd * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  build_rope(drope.as<float2>(), pos + 1, hd, base);
+  QkvPostArgs pa{};
+  pa.qkv = dqkv.as<float>();
+  pa.q_out = dq.as<float>();
+  pa.k_cache = dk.as<float>();  // max_seq = 1: the cache row is the output
+  pa.v_cache = dv.as<float>();
+  pa.q_norm = qn ? dqn.as<float>() : nullptr;
+  pa.k_norm = kn ? dkn.as<float>() : nullptr;
+  pa.rope = drope.as<float2>() + size_t(pos) * (hd / 2);
+  pa.pos_ptr = nullptr;
+  pa.pos_offset = 0;
+  pa.H = H;
+  pa.Hkv = Hkv;
+  pa.hd = hd;
+  pa.max_seq = 1;
+  pa.ncol = 1;
+  pa.eps = eps;
+  HIPC(launch_qkv_post(pa, stream_));
+  HIPC(hipMemcpyAsync(q, dq.p, size_t(H) * hd * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(k, dk.p, size_t(Hkv) * hd * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(v, dv.p, size_t(Hkv) * hd * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_attention(const float* q, const float* k, const float* v, uint32_t H, uint32_t Hkv, uint32_t hd,
+                          uint32_t T, float scale, float* out) {
+  select();
+  if (Hkv == 0 || H % Hkv) fail("invalid GQA split");
+  if (hd == 0 || T == 0 || hd % 4 || hd > 256) fail("invalid attention dims");
+  // reference layout [token][kv_head][hd] -> cache layout [kv_head][token][hd]
+  std::vector<float> kc(size_t(Hkv) * T * hd), vc(kc.size());
+  for (uint32_t t = 0; t < T; ++t)
+    for (uint32_t g = 0; g < Hkv; ++g)
+      for (uint32_t d = 0; d < hd; ++d) {
+        kc[(size_t(g) * T + t) * hd + d] = k[(size_t(t) * Hkv + g) * hd + d];
+        vc[(size_t(g) * T + t) * hd + d] = v[(size_t(t) * Hkv + g) * hd + d];
+      }
+  const uint32_t chunk = 64, nch = (T + chunk - 1) / chunk;
+  TmpBuf dq(size_t(H) * hd * 4), dk(kc.size() * 4), dv(vc.size() * 4), dpart(size_t(H) * nch * (hd + 2) * 4),
+      dout(size_t(H) * hd * 4);
+  HIPC(hipMemcpyAsync(dq.p, q, size_t(H) * hd * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(dk.p, kc.data(), kc.size() * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(dv.p, vc.data(), vc.size() * 4, hipMemcpyHostToDevice, stream_));
+  AttnArgs aa{};
+  aa.q = dq.as<float>();
+  aa.k_cache = dk.as<float>();
+  aa.v_cache = dv.as<float>();
+  aa.part = dpart.as<float>();
+  aa.out = dout.as<float>();
+  aa.pos_ptr = nullptr;
+  aa.pos_offset = T - 1;
+  aa.H = H;
+  aa.Hkv = Hkv;
+  aa.hd = hd;
+  aa.max_seq = T;
+  aa.ncol = 1;
+  aa.chunk = chunk;
+  aa.max_chunks = nch;
+  aa.scale = scale;
+  HIPC(launch_attention(aa, stream_));
+  HIPC(hipMemcpyAsync(out, dout.p, size_t(H) * hd * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_swiglu(const float* g, const float* u, size_t n, int fast, float* out) {
+  select();
+  if (n == 0) return;
+  TmpBuf dg(n * 4), du(n * 4), dy(n * 4);
+  HIPC(hipMemcpyAsync(dg.p, g, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(du.p, u, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(launch_swiglu(dg.as<float>(), du.as<float>(), dy.as<float>(), uint32_t(n), fast, stream_));
+  HIPC(hipMemcpyAsync(out, dy.p, n * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
+                       uint32_t* tok) {
+  select();
+  if (n == 0) {
+    *tok = 0;
+    return;
+  }
+  if (n > 8191) fail("sample_token supports at most 8191 logits on the device");
+  TmpBuf dl(n * 4), dr(8), dt(4), de(4);
+  HIPC(hipMemcpyAsync(dl.p, logits, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(dr.p, rng, 8, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemsetAsync(de.p, 0, 4, stream_));
+  HIPC(launch_sample_plain(dl.as<float>(), uint32_t(n), SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, always,
+                           dr.as<uint64_t>(), dt.as<uint32_t>(), de.as<uint32_t>(), stream_));
+  uint32_t e = 0;
+  HIPC(hipMemcpyAsync(rng, dr.p, 8, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(tok, dt.p, 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(&e, de.p, 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  if (e) fail("sampler failure");
+}
+
+void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes) {
+  select();
+  const s2hip_spec& s = spec;
+  if (reps == 0) reps = 1;
+  const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim;
+  HIPC(hipMemsetAsync(h_, 0, size_t(PREFILL_COLS) * s.dim * 4, stream_));
+  HIPC(hipMemsetAsync(att_, 0, size_t(PREFILL_COLS) * q * 4, stream_));
+  HIPC(hipMemsetAsync(act_, 0, size_t(PREFILL_COLS) * s.ffn * 4, stream_));
+  auto pass = [&](uint32_t l) {
+    const SlowLayer& L = slow_[l];
+    if (name == "slow_w13")
+      gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, 1, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, nullptr, L.w1.out, nullptr);
+    else if (name == "slow_wqkv")
+      gemv(L.wqkv, nullptr, EPI_STORE, 1, h_, s.dim, L.attn_norm, s.eps, qkv_, q + 2 * kv, nullptr, L.wqkv.out,
+           nullptr);
+    else if (name == "slow_wo")
+      gemv(L.wo, nullptr, EPI_STORE, 1, att_, q, nullptr, 0.0f, act_, s.dim, nullptr, L.wo.out, nullptr);
+    else if (name == "slow_w2")
+      gemv(L.w2, nullptr, EPI_STORE, 1, act_, s.ffn, nullptr, 0.0f, qkv_, s.dim, nullptr, L.w2.out, nullptr);
+    else if (name == "slow_head")
+      gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, head_rows_, n_cand_,
+           nullptr);
+    else
+      fail("unknown kernel name " + name);
+  };
+  double b = 0;
+  const SlowLayer& L0 = slow_[0];
+  if (name == "slow_w13") b = double(L0.w1.bytes + L0.w3.bytes) + 4.0 * (s.dim + s.ffn + s.dim);
+  else if (name == "slow_wqkv") b = double(L0.wqkv.bytes) + 4.0 * (s.dim + s.dim + q + 2 * kv);
+  else if (name == "slow_wo") b = double(L0.wo.bytes) + 4.0 * (q + s.dim);
+  else if (name == "slow_w2") b = double(L0.w2.bytes) + 4.0 * (s.ffn + s.dim);
+  else if (name == "slow_head") b = double(n_cand_) * s.dim * 2 + 4.0 * (s.dim + n_cand_);
+  const uint32_t layers = name == "slow_head" ? 1u : s.slow_layers;
+  for (uint32_t l = 0; l < layers; ++l) pass(l);  // warm-up
+  hipEvent_t e0, e1;
+  HIPC(hipEventCreate(&e0));
+  HIPC(hipEventCreate(&e1));
+  HIPC(hipEventRecord(e0, stream_));
+  for (uint32_t r = 0; r < reps; ++r)
+    for (uint32_t l = 0; l < layers; ++l) pass(l);
+  HIPC(hipEventRecord(e1, stream_));
+  HIPC(hipEventSynchronize(e1));
+  float ms = 0.0f;
+  HIPC(hipEventElapsedTime(&ms, e0, e1));
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  *avg_us = double(ms) * 1000.0 / double(reps * layers);
+  *bytes = b;
+}
+
+}  // namespace s2
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+struct s2hip_engine {
+  std::unique_ptr<s2::Engine> e;
+};
+
+namespace {
+void set_err(char* err, size_t cap, const char* msg) {
+  if (err && cap) snprintf(err, cap, "%s", msg);
+}
+
+template <class F>
+int32_t guarded(char* err, size_t cap, F&& f) {
+  try {
+    f();
+    return 1;
+  } catch (const std::exception& ex) {
+    set_err(err, cap, ex.what());
+    return 0;
+  } catch (...) {
+    set_err(err, cap, "unknown error");
+    return 0;
+  }
+}
+}  // namespace
+
+extern "C" {
+
+const char* s2hip_version(void) { return "s2hip 0.1.0 (gfx950)"; }
+
+s2hip_engine* s2hip_create(const s2hip_config* cfg, char* err, size_t err_cap) {
+  if (!cfg) {
+    set_err(err, err_cap, "config is NULL");
+    return nullptr;
+  }
+  s2hip_engine* h = nullptr;
+  guarded(err, err_cap, [&] {
+    std::unique_ptr<s2hip_engine> tmp(new s2hip_engine());
+    tmp->e.reset(new s2::Engine(*cfg));
+    h = tmp.release();
+  });
+  return h;
+}
+
+void s2hip_destroy(s2hip_engine* engine) { delete engine; }
+
+int32_t s2hip_get_spec(const s2hip_engine* engine, s2hip_spec* out) {
+  if (!engine || !out) return 0;
+  *out = engine->e->spec;
+  return 1;
+}
+
+int32_t s2hip_reset(s2hip_engine* engine, char* err, size_t err_cap) {
+  if (!engine) return 0;
+  return guarded(err, err_cap, [&] { engine->e->reset(); });
+}
+
+uint32_t s2hip_n_past(const s2hip_engine* engine) { return engine ? engine->e->n_past_host : 0u; }
+
+int32_t s2hip_eval(s2hip_engine* engine, const int32_t* flat, size_t n_tokens, float* hidden_out, float* logits_out,
+                   char* err, size_t err_cap) {
+  if (!engine || !flat || !hidden_out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->eval(flat, n_tokens, hidden_out, logits_out); });
+}
+
+int32_t s2hip_fast_logits(s2hip_engine* engine, const float* hidden, const uint32_t* prefix, size_t plen,
+                          float* logits, char* err, size_t err_cap) {
+  if (!engine || !hidden || !logits || (plen && !prefix)) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->fast_logits(hidden, prefix, plen, logits); });
+}
+
+int32_t s2hip_fast_codebooks(s2hip_engine* engine, const float* hidden, uint32_t sem, const s2hip_sampler* smp,
+                             uint64_t* rng, uint32_t* codes, char* err, size_t err_cap) {
+  if (!engine || !hidden || !smp || !rng || !codes) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->fast_codebooks(hidden, sem, *smp, rng, codes); });
+}
+
+int32_t s2hip_generate_codes(s2hip_engine* engine, const int32_t* prompt, size_t cols, const s2hip_gen_params* p,
+                             uint64_t* rng, int32_t* codes, uint32_t* n_frames, s2hip_gen_stats* stats, char* err,
+                             size_t err_cap) {
+  if (!engine || !prompt || !p || !rng || !codes || !n_frames) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->generate(prompt, cols, *p, rng, codes, n_frames, stats); });
+}
+
+int32_t s2hip_op_linear(s2hip_engine* engine, const void* w, uint32_t type, size_t in, size_t out, const float* x,
+                        size_t ncol, float* y, char* err, size_t err_cap) {
+  if (!engine || !w || !x || !y) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_linear(w, type, in, out, x, ncol, y); });
+}
+
+int32_t s2hip_op_rms_norm(s2hip_engine* engine, const float* x, const float* w, size_t n, size_t ncol, float eps,
+                          float* y, char* err, size_t err_cap) {
+  if (!engine || !x || !w || !y) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_rms_norm(x, w, n, ncol, eps, y); });
+}
+
+int32_t s2hip_op_dequant_rows(s2hip_engine* engine, const void* w, uint32_t type, size_t in, size_t rows, float* out,
+                              char* err, size_t err_cap) {
+  if (!engine || !w || !out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_dequant(w, type, in, rows, out); });
+}
+
+int32_t s2hip_op_qk_rope(s2hip_engine* engine, const float* qkv, uint32_t H, uint32_t Hkv, uint32_t hd,
+                         uint32_t pos, float base, const float* qn, const float* kn, float eps, float* q, float* k,
+                         float* v, char* err, size_t err_cap) {
+  if (!engine || !qkv || !q || !k || !v) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_qk_rope(qkv, H, Hkv, hd, pos, base, qn, kn, eps, q, k, v); });
+}
+
+int32_t s2hip_op_attention(s2hip_engine* engine, const float* q, const float* k, const float* v, uint32_t H,
+                           uint32_t Hkv, uint32_t hd, uint32_t T, float scale, float* out, char* err, size_t err_cap) {
+  if (!engine || !q || !k || !v || !out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_attention(q, k, v, H, Hkv, hd, T, scale, out); });
+}
+
+int32_t s2hip_op_swiglu(s2hip_engine* engine, const float* g, const float* u, size_t n, int32_t fast, float* out,
+                        char* err, size_t err_cap) {
+  if (!engine || !g || !u || !out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_swiglu(g, u, n, fast, out); });
+}
+
+int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, const s2hip_sampler* smp,
+                        int64_t always, uint64_t* rng, uint32_t* tok, char* err, size_t err_cap) {
+  if (!engine || !logits || !smp || !rng || !tok) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_sample(logits, n, *smp, always, rng, tok); });
+}
+
+int32_t s2hip_time_kernel(s2hip_engine* engine, const char* kernel, uint32_t reps, double* avg_us, double* bytes,
+                          char* err, size_t err_cap) {
+  if (!engine || !kernel || !avg_us || !bytes) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->time_kernel(kernel, reps, avg_us, bytes); });
+}
+
+}  // extern "C"

@@ -1,0 +1,160 @@
+// kernels.h -- launch interface of the s2hip device kernels (gfx950, wave64).
+//
+// All activations are f32.  Weights stay in their GGUF block layout:
+// row-major [out][in] with `in` contiguous; F16 rows, or GGML Q8_0 / Q4_0
+// blocks of 32 elements along `in`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace s2 {
+
+enum WeightType : uint32_t { W_F16 = 1, W_Q4_0 = 2, W_Q8_0 = 8 };
+
+enum Epilogue : int {
+  EPI_STORE = 0,        // y[c][o] = acc
+  EPI_RESID = 1,        // y[c][o] = y[c][o] + acc (residual add in place)
+  EPI_SWIGLU_SLOW = 2,  // y[c][o] = g * (1 / (1 + e^-g)) * u
+  EPI_SWIGLU_FAST = 3,  // y[c][o] = g / (1 + e^-g) * u
+};
+
+// Per-sequence device state read by graph-replayed kernels.
+struct DevState {
+  uint32_t n_past;      // Slow-AR positions already in the KV cache
+  uint32_t step_index;  // frames generated
+  uint32_t done;        // set once im_end is sampled or max_new frames exist
+  uint32_t main_token;  // last sampled Slow-AR token
+  uint32_t err;         // error bits (ERR_*)
+  uint32_t prompt_cols;
+  uint32_t max_new;
+  uint32_t min_tokens_before_end;
+  uint64_t rng;         // SeededRng state
+  uint32_t codes_frame[16];  // codebook ids of the frame being built
+};
+
+enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u };
+
+struct GemvArgs {
+  const uint8_t* w;      // weight rows
+  const uint8_t* w3;     // second matrix for SwiGLU epilogues (same shape)
+  size_t row_bytes;
+  const uint32_t* row_map;  // optional: logical row -> weight row
+  uint32_t in, out;      // `out` logical rows
+  const float* x;        // [ncol][ldx]
+  uint32_t ldx;
+  const float* norm;     // optional RMSNorm gain [in] applied to x first
+  float eps;
+  float* y;              // [ncol][ldy]
+  uint32_t ldy;
+  const uint32_t* done;  // optional early-exit flag
+};
+
+struct SamplerCfg {
+  float temperature;
+  float top_p;
+  int32_t top_k;
+};
+
+// GEMV over `ncol` input columns (1, 2, 4 or 8).
+hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s);
+
+// Per-column RMSNorm: y[c] = (x[c] * scale_c) * w.
+hipError_t launch_rms_norm(const float* x, const float* w, float* y, uint32_t n, uint32_t ncol, float eps,
+                           const uint32_t* done, hipStream_t s);
+
+// QK-norm (optional) + NORMAL RoPE + KV append for `ncol` consecutive positions
+// starting at *pos_ptr + pos_offset.  qkv: [ncol][(H + 2 Hkv) hd].
+struct QkvPostArgs {
+  const float* qkv;
+  float* q_out;            // [ncol][H hd]
+  float* k_cache;          // [Hkv][max_seq][hd] for this layer
+  float* v_cache;
+  const float* q_norm;     // nullable
+  const float* k_norm;     // nullable
+  const float2* rope;      // [max_pos][hd/2] (cos, sin)
+  const uint32_t* pos_ptr; // nullable: base position = *pos_ptr + pos_offset
+  uint32_t pos_offset;
+  uint32_t H, Hkv, hd, max_seq, ncol;
+  float eps;
+  const uint32_t* done;
+  uint32_t* err;
+};
+hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
+
+// Split-T GQA decode attention for `ncol` query positions; column c sees
+// T_c = *pos_ptr + pos_offset + c + 1 cache positions.
+struct AttnArgs {
+  const float* q;          // [ncol][H hd]
+  const float* k_cache;    // [Hkv][max_seq][hd]
+  const float* v_cache;
+  float* part;             // [ncol][H][max_chunks][hd + 2]
+  float* out;              // [ncol][H hd]
+  const uint32_t* pos_ptr;
+  uint32_t pos_offset;
+  uint32_t H, Hkv, hd, max_seq, ncol;
+  uint32_t chunk;          // positions per work-group (multiple of 64)
+  uint32_t max_chunks;
+  float scale;
+  const uint32_t* done;
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+// Slow-AR token embedding (time-major flat ids [n][cdim]).
+struct EmbedArgs {
+  const int32_t* tokens;       // nullable: use the device step input built from state
+  const DevState* state;       // used when tokens == nullptr
+  const uint16_t* emb;         // [vocab][dim] f16
+  const uint16_t* cb_emb;      // [cb_rows][dim] f16
+  float* h;                    // [n][dim]
+  uint32_t n, dim, vocab, cb_rows, num_codebooks, codebook_size, sem_begin, sem_end;
+  float sem_scale;             // 1/sqrt(num_codebooks+1) or 1
+  uint32_t scale_enabled;
+  const uint32_t* done;
+  uint32_t* err;
+};
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
+
+// Fast-AR frame start: codes_frame[0] = semantic code of main_token,
+// fh[0] = slow hidden, fh[1] = fast_emb[code0].
+hipError_t launch_fast_begin(DevState* st, const float* slow_hidden, const uint16_t* fast_emb, float* fh,
+                             uint32_t dim, uint32_t codebook_size, uint32_t sem_begin, uint32_t sem_end,
+                             hipStream_t s);
+
+// Sampling.  Slow mode: logits over candidate rows `ids` (ascending vocab ids),
+// full vocab `vocab`; applies the semantic mask / im_end rule and updates the
+// frame state.  Fast mode: logits over codebook ids, writes codes_frame[cb] and
+// the next Fast-AR input row.
+struct SampleArgs {
+  const float* logits;
+  const uint32_t* ids;       // nullable: id = index
+  uint32_t n;                // candidates
+  uint32_t vocab;            // full vocabulary size
+  SamplerCfg cfg;
+  DevState* st;
+  // slow mode
+  uint32_t im_end;
+  uint32_t after_step;       // 1: a Slow step just ran (advance frame counters)
+  int32_t* codes_out;        // [num_codebooks][max_new] codebook-major (nullable)
+  uint32_t num_codebooks;
+  // fast mode
+  uint32_t cb_index;         // codebook being sampled (1..num_codebooks-1)
+  const uint16_t* fast_emb;  // next-input gather (nullable)
+  float* next_input;
+  uint32_t dim;
+  uint32_t* token_out;       // optional copy of the sampled id
+};
+hipError_t launch_sample_slow(const SampleArgs& a, hipStream_t s);
+hipError_t launch_sample_fast(const SampleArgs& a, hipStream_t s);
+// Plain sample_token over `n` logits (ids = index) with optional always-include id.
+hipError_t launch_sample_plain(const float* logits, uint32_t n, SamplerCfg cfg, int64_t always_include,
+                               uint64_t* rng, uint32_t* token_out, uint32_t* err, hipStream_t s);
+
+// Expand GGML rows to f32 (bit-exact dequantisation).
+hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_bytes, uint32_t rows, uint32_t in,
+                               float* out, hipStream_t s);
+
+hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n, int fast, hipStream_t s);
+hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s);
+
+}  // namespace s2

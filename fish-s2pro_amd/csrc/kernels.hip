@@ -1,0 +1,1003 @@
+// kernels.hip -- s2hip device kernels for gfx950 (CDNA4, wave64).
+//
+// Decode is HBM bound: every kernel here streams its operand once with
+// coalesced 16-byte loads per lane and keeps activations in f32.  Weights are
+// read in their GGUF block layout (F16 rows, GGML Q8_0 / Q4_0 blocks) and
+// dequantised in registers.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "kernels.h"
+
+namespace s2 {
+namespace {
+
+constexpr int WAVE = 64;
+constexpr int GEMV_THREADS = 256;
+constexpr int GEMV_WAVES = GEMV_THREADS / WAVE;
+constexpr int SAMPLE_THREADS = 1024;
+constexpr uint32_t SAMPLE_MAX = 8192;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = WAVE / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = WAVE / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
+  return v;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
+
+// Correctly rounded (in all but vanishingly rare double-rounding cases) expf:
+// exp evaluated in double, rounded once to float.
+__device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
+
+// ---------------------------------------------------------------------------
+// Weight decode: 8 consecutive elements [e, e+8) of one row.
+// ---------------------------------------------------------------------------
+template <uint32_t WT>
+__device__ __forceinline__ void load_w8(const uint8_t* row, uint32_t e, float w[8]);
+
+template <>
+__device__ __forceinline__ void load_w8<W_F16>(const uint8_t* row, uint32_t e, float w[8]) {
+  const half8 v = *reinterpret_cast<const half8*>(row + size_t(e) * 2);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) w[i] = static_cast<float>(v[i]);
+}
+
+// Q8_0 block (34 B): f16 d, int8 q[32].  Lane part p = (e/8)%4 covers q[8p, 8p+8).
+// The 8 quant bytes start at an address that is 0 or 2 mod 4: read the
+// enclosing aligned 12-byte window and funnel-shift.  Allocations carry
+// trailing padding so the window never leaves the buffer.
+template <>
+__device__ __forceinline__ void load_w8<W_Q8_0>(const uint8_t* row, uint32_t e, float w[8]) {
+  const uint32_t b = e >> 5, p = (e >> 3) & 3u;
+  const uint8_t* blk = row + size_t(b) * 34;
+  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
+  const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2 + p * 8);
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  const uint32_t sh = uint32_t(a & 3u);
+  const uint32_t w0 = base[0], w1 = base[1], w2 = base[2];
+  const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+  const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = static_cast<float>(static_cast<int8_t>((lo >> (8 * i)) & 0xffu)) * d;
+    w[4 + i] = static_cast<float>(static_cast<int8_t>((hi >> (8 * i)) & 0xffu)) * d;
+  }
+}
+
+// Q4_0 block (18 B): f16 d, u8 qs[16]; element j<16 is the low nibble of
+// qs[j], element 16+j the high nibble.  Part p reads qs[8(p&1), +8) and takes
+// low nibbles for p<2, high nibbles for p>=2; x = (nibble - 8) * d.
+template <>
+__device__ __forceinline__ void load_w8<W_Q4_0>(const uint8_t* row, uint32_t e, float w[8]) {
+  const uint32_t b = e >> 5, p = (e >> 3) & 3u;
+  const uint8_t* blk = row + size_t(b) * 18;
+  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
+  const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2 + (p & 1u) * 8);
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+  const uint32_t sh = uint32_t(a & 3u);
+  const uint32_t w0 = base[0], w1 = base[1], w2 = base[2];
+  const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+  const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+  const uint32_t nshift = (p >= 2) ? 4u : 0u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    w[i] = static_cast<float>(int((lo >> (8 * i + nshift)) & 0xfu) - 8) * d;
+    w[4 + i] = static_cast<float>(int((hi >> (8 * i + nshift)) & 0xfu) - 8) * d;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GEMV: y[c][o] (+)= sum_i x[c][i] * W[o][i]
+//   block = 4 waves, each wave owns R consecutive output rows; lanes stride
+//   the row 8 elements (16 B of f16) at a time.  x (optionally RMS-normalised)
+//   is staged once per block in LDS.
+// ---------------------------------------------------------------------------
+template <uint32_t WT, int NCOL, int R, int EPI>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
+  if (a.done && *a.done) return;
+  extern __shared__ float xs[];  // [NCOL][in]
+  __shared__ float red[GEMV_WAVES][NCOL];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+  const uint32_t in = a.in;
+
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) {
+    const float* xc = a.x + size_t(c) * a.ldx;
+    float ss = 0.0f;
+    for (uint32_t i = tid; i < in; i += GEMV_THREADS) {
+      const float v = xc[i];
+      xs[c * in + i] = v;
+      ss += v * v;
+    }
+    if (a.norm) {
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave][c] = ss;
+    }
+  }
+  if (a.norm) {
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float tot = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+      const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(in)), a.eps)));
+      for (uint32_t i = tid; i < in; i += GEMV_THREADS)
+        xs[c * in + i] = __fmul_rn(__fmul_rn(xs[c * in + i], scale), a.norm[i]);
+    }
+  }
+  __syncthreads();
+
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  const uint32_t row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
+  const uint8_t* rp[R];
+  const uint8_t* rp3[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t lr = row0 + r;
+    if (lr >= a.out) lr = 0;  // clamp; result discarded
+    const uint32_t wr = a.row_map ? a.row_map[lr] : lr;
+    rp[r] = a.w + size_t(wr) * a.row_bytes;
+    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  }
+  float acc[R][NCOL];
+  float acc3[R][NCOL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      acc[r][c] = 0.0f;
+      acc3[r][c] = 0.0f;
+    }
+
+#pragma unroll 2
+  for (uint32_t base = 0; base < in; base += WAVE * 8) {
+    const uint32_t e = base + lane * 8;
+    if (e < in) {
+      float w[R][8];
+      float w3[DUAL ? R : 1][8];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        load_w8<WT>(rp[r], e, w[r]);
+        if constexpr (DUAL) load_w8<WT>(rp3[r], e, w3[r]);
+      }
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) {
+        const float4 xa = *reinterpret_cast<const float4*>(&xs[c * in + e]);
+        const float4 xb = *reinterpret_cast<const float4*>(&xs[c * in + e + 4]);
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc[r][c] = fmaf(w[r][k], xv[k], acc[r][c]);
+          if constexpr (DUAL) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc3[r][c] = fmaf(w3[r][k], xv[k], acc3[r][c]);
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float g = wave_sum(acc[r][c]);
+      float u = 0.0f;
+      if constexpr (DUAL) u = wave_sum(acc3[r][c]);
+      const uint32_t lr = row0 + r;
+      if (lane == 0 && lr < a.out) {
+        float* dst = a.y + size_t(c) * a.ldy + lr;
+        if constexpr (EPI == EPI_STORE) {
+          *dst = g;
+        } else if constexpr (EPI == EPI_RESID) {
+          *dst = __fadd_rn(*dst, g);
+        } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+          *dst = __fmul_rn(__fmul_rn(g, sig), u);
+        } else {
+          *dst = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        }
+      }
+    }
+  }
+}
+
+template <uint32_t WT, int NCOL, int R, int EPI>
+hipError_t gemv_launch_one(const GemvArgs& a, hipStream_t s) {
+  const size_t lds = size_t(NCOL) * a.in * sizeof(float);
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemv_kernel<WT, NCOL, R, EPI>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 1024);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const uint32_t rows_per_block = GEMV_WAVES * R;
+  const dim3 grid((a.out + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL((gemv_kernel<WT, NCOL, R, EPI>), grid, dim3(GEMV_THREADS), lds, s, a);
+  return hipGetLastError();
+}
+
+template <uint32_t WT, int NCOL, int EPI>
+hipError_t gemv_pick_r(const GemvArgs& a, hipStream_t s) {
+  if (NCOL == 1 && a.out > 4096) return gemv_launch_one<WT, NCOL, 2, EPI>(a, s);
+  return gemv_launch_one<WT, NCOL, 1, EPI>(a, s);
+}
+
+template <uint32_t WT, int EPI>
+hipError_t gemv_pick_ncol(int ncol, const GemvArgs& a, hipStream_t s) {
+  switch (ncol) {
+    case 1: return gemv_pick_r<WT, 1, EPI>(a, s);
+    case 2: return gemv_pick_r<WT, 2, EPI>(a, s);
+    case 4: return gemv_pick_r<WT, 4, EPI>(a, s);
+    case 8: return gemv_pick_r<WT, 8, EPI>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <uint32_t WT>
+hipError_t gemv_pick_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: return gemv_pick_ncol<WT, EPI_STORE>(ncol, a, s);
+    case EPI_RESID: return gemv_pick_ncol<WT, EPI_RESID>(ncol, a, s);
+    case EPI_SWIGLU_SLOW: return gemv_pick_ncol<WT, EPI_SWIGLU_SLOW>(ncol, a, s);
+    case EPI_SWIGLU_FAST: return gemv_pick_ncol<WT, EPI_SWIGLU_FAST>(ncol, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm over `ncol` vectors (one block per column).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const float* w, float* y, uint32_t n,
+                                                       float eps, const uint32_t* done) {
+  if (done && *done) return;
+  __shared__ float red[4];
+  const uint32_t c = blockIdx.x;
+  const float* xc = x + size_t(c) * n;
+  float ss = 0.0f;
+  for (uint32_t i = threadIdx.x; i < n; i += 256) ss += xc[i] * xc[i];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(n)), eps)));
+  for (uint32_t i = threadIdx.x; i < n; i += 256) y[size_t(c) * n + i] = __fmul_rn(__fmul_rn(xc[i], scale), w[i]);
+}
+
+// ---------------------------------------------------------------------------
+// QK-norm + RoPE + KV append.  One wave per head; grid (H + 2 Hkv, ncol).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
+  if (a.done && *a.done) return;
+  const uint32_t hi = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
+  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
+  if (pos >= a.max_seq) {
+    if (lane == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
+    return;
+  }
+  const uint32_t hd = a.hd, width = (a.H + 2 * a.Hkv) * hd;
+  const float* src = a.qkv + size_t(col) * width + size_t(hi) * hd;
+  float* dst;
+  const float* norm;
+  if (hi < a.H) {
+    dst = a.q_out + size_t(col) * a.H * hd + size_t(hi) * hd;
+    norm = a.q_norm;
+  } else if (hi < a.H + a.Hkv) {
+    dst = a.k_cache + (size_t(hi - a.H) * a.max_seq + pos) * hd;
+    norm = a.k_norm;
+  } else {
+    float* vd = a.v_cache + (size_t(hi - a.H - a.Hkv) * a.max_seq + pos) * hd;
+    for (uint32_t i = lane; i < hd; i += 64) vd[i] = src[i];
+    return;
+  }
+  float scale = 1.0f;
+  if (norm) {
+    float ss = 0.0f;
+    for (uint32_t i = lane; i < hd; i += 64) ss += src[i] * src[i];
+    ss = wave_sum(ss);
+    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(hd)), a.eps)));
+  }
+  const float2* rope = a.rope + size_t(pos) * (hd / 2);
+  for (uint32_t p = lane; p < hd / 2; p += 64) {
+    float x0 = src[2 * p], x1 = src[2 * p + 1];
+    if (norm) {
+      x0 = __fmul_rn(__fmul_rn(x0, scale), norm[2 * p]);
+      x1 = __fmul_rn(__fmul_rn(x1, scale), norm[2 * p + 1]);
+    }
+    const float cs = rope[p].x, sn = rope[p].y;
+    dst[2 * p] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
+    dst[2 * p + 1] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split-T decode attention.  grid (max_chunks, Hkv, ncol); 4 waves per block,
+// wave w serves q heads g*rep + w, + 4, ...  Scores: one lane per cache
+// position; PV: one lane per head-dim element.  Writes per-chunk (m, l, o).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  if (a.done && *a.done) return;
+  const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
+  const uint32_t T = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col + 1;
+  const uint32_t t0 = chunk * a.chunk;
+  if (t0 >= T || T > a.max_seq) return;  // uniform across the block
+  const uint32_t t1 = min(T, t0 + a.chunk);
+  const uint32_t hd = a.hd, rep = a.H / a.Hkv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float qs[GEMV_WAVES][256];
+  __shared__ float ps[GEMV_WAVES][64];
+  const float* kbase = a.k_cache + size_t(g) * a.max_seq * hd;
+  const float* vbase = a.v_cache + size_t(g) * a.max_seq * hd;
+  const uint32_t rounds = (rep + GEMV_WAVES - 1) / GEMV_WAVES;
+  for (uint32_t it = 0; it < rounds; ++it) {  // same trip count for every wave
+    const uint32_t h_local = wave + GEMV_WAVES * it;
+    const bool active = h_local < rep;
+    const uint32_t h = g * rep + (active ? h_local : 0u);
+    const float* q = a.q + size_t(col) * a.H * hd + size_t(h) * hd;
+    for (uint32_t i = lane; i < hd; i += 64) qs[wave][i] = q[i];
+    __syncthreads();
+    float m = -INFINITY, l = 0.0f;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // hd <= 256
+    for (uint32_t tb = t0; tb < t1; tb += 64) {
+      const uint32_t t = tb + lane;
+      float sc = -INFINITY;
+      if (t < t1) {
+        const float4* kr = reinterpret_cast<const float4*>(kbase + size_t(t) * hd);
+        float dsum = 0.0f;
+        for (uint32_t i = 0; i < hd / 4; ++i) {
+          const float4 kv = kr[i];
+          dsum = fmaf(qs[wave][4 * i], kv.x, dsum);
+          dsum = fmaf(qs[wave][4 * i + 1], kv.y, dsum);
+          dsum = fmaf(qs[wave][4 * i + 2], kv.z, dsum);
+          dsum = fmaf(qs[wave][4 * i + 3], kv.w, dsum);
+        }
+        sc = dsum * a.scale;
+      }
+      const float mb = wave_max(sc);
+      const float mn = fmaxf(m, mb);
+      const float p = (t < t1) ? expf(sc - mn) : 0.0f;
+      const float corr = (m == -INFINITY) ? 0.0f : expf(m - mn);
+      l = l * corr + wave_sum(p);
+      ps[wave][lane] = p;
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] *= corr;
+      const uint32_t nt = min(64u, t1 - tb);
+      for (uint32_t tt = 0; tt < nt; ++tt) {
+        const float pv = ps[wave][tt];
+        const float* vr = vbase + size_t(tb + tt) * hd;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t dd = lane + 64 * j;
+          if (dd < hd) o[j] = fmaf(pv, vr[dd], o[j]);
+        }
+      }
+      __syncthreads();
+      m = mn;
+    }
+    if (active) {
+      float* part = a.part + ((size_t(col) * a.H + h) * a.max_chunks + chunk) * (hd + 2);
+      if (lane == 0) {
+        part[0] = m;
+        part[1] = l;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t dd = lane + 64 * j;
+        if (dd < hd) part[2 + dd] = o[j];
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  if (a.done && *a.done) return;
+  const uint32_t h = blockIdx.x, col = blockIdx.y;
+  const uint32_t T = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col + 1;
+  if (T > a.max_seq) return;
+  const uint32_t nch = (T + a.chunk - 1) / a.chunk;
+  const uint32_t hd = a.hd;
+  const float* part = a.part + (size_t(col) * a.H + h) * a.max_chunks * (hd + 2);
+  float M = -INFINITY;
+  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, part[c * (hd + 2)]);
+  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
+    float L = 0.0f, o = 0.0f;
+    for (uint32_t c = 0; c < nch; ++c) {
+      const float* pc = part + c * (hd + 2);
+      const float f = expf(pc[0] - M);
+      L = fmaf(pc[1], f, L);
+      o = fmaf(pc[2 + d], f, o);
+    }
+    a.out[size_t(col) * a.H * hd + size_t(h) * hd + d] = o / L;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Slow-AR embedding (time-major ids) -- one block per token.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
+  if (a.done && *a.done) return;
+  const uint32_t t = blockIdx.x;
+  const uint32_t cdim = a.num_codebooks + 1;
+  int32_t tok[17];
+  if (a.tokens) {
+    for (uint32_t i = 0; i < cdim && i < 17; ++i) tok[i] = a.tokens[size_t(t) * cdim + i];
+  } else {
+    // build_step_input: [main, cb0..cb(n-1)] when main is semantic, else [main, 0..]
+    const uint32_t main = a.state->main_token;
+    const bool sem = main >= a.sem_begin && main <= a.sem_end;
+    tok[0] = int32_t(main);
+    for (uint32_t i = 0; i < a.num_codebooks && i < 16; ++i) tok[1 + i] = sem ? int32_t(a.state->codes_frame[i]) : 0;
+  }
+  uint32_t id = uint32_t(tok[0]);
+  if (tok[0] < 0 || id >= a.vocab) {
+    if (threadIdx.x == 0 && a.err) atomicOr(a.err, ERR_TOKEN_RANGE);
+    id = 0;
+  }
+  const bool sem = id >= a.sem_begin && id <= a.sem_end;
+  uint32_t rows[16];
+  if (sem) {
+    for (uint32_t cb = 0; cb < a.num_codebooks && cb < 16; ++cb) {
+      uint32_t r = uint32_t(tok[1 + cb]) + cb * a.codebook_size;
+      if (tok[1 + cb] < 0 || r >= a.cb_rows) {
+        if (threadIdx.x == 0 && a.err) atomicOr(a.err, ERR_TOKEN_RANGE);
+        r = 0;
+      }
+      rows[cb] = r;
+    }
+  }
+  const float sc = (a.scale_enabled && sem) ? a.sem_scale : 1.0f;
+  float* h = a.h + size_t(t) * a.dim;
+  for (uint32_t i = threadIdx.x; i < a.dim; i += 256) {
+    float v = half_bits_to_float(a.emb[size_t(id) * a.dim + i]);
+    if (sem) {
+      float cs = 0.0f;
+      for (uint32_t cb = 0; cb < a.num_codebooks && cb < 16; ++cb)
+        cs = __fadd_rn(cs, half_bits_to_float(a.cb_emb[size_t(rows[cb]) * a.dim + i]));
+      v = __fadd_rn(v, cs);
+    }
+    if (a.scale_enabled) v = __fmul_rn(v, sc);
+    h[i] = v;
+  }
+}
+
+__device__ __forceinline__ uint32_t sem_to_code(uint32_t tok, uint32_t sem_begin, uint32_t sem_end,
+                                                uint32_t codebook_size) {
+  if (tok < sem_begin || tok > sem_end) return 0;
+  const uint32_t c = tok - sem_begin;
+  return c >= codebook_size ? codebook_size - 1 : c;
+}
+
+__global__ __launch_bounds__(256) void fast_begin_kernel(DevState* st, const float* slow_hidden,
+                                                         const uint16_t* fast_emb, float* fh, uint32_t dim,
+                                                         uint32_t codebook_size, uint32_t sem_begin,
+                                                         uint32_t sem_end) {
+  if (st->done) return;
+  const uint32_t code = sem_to_code(st->main_token, sem_begin, sem_end, codebook_size);
+  if (blockIdx.x == 0 && threadIdx.x == 0) st->codes_frame[0] = code;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256) {
+    fh[i] = slow_hidden[i];
+    fh[dim + i] = half_bits_to_float(fast_emb[size_t(code) * dim + i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sampler: exact restatement of sample_token (top-k -> force-include ->
+// temperature softmax -> top-p -> renormalise -> discrete draw) on one block.
+// Candidates are given in ascending vocabulary-id order; every id outside
+// the candidate set (or masked) has logit -inf.  Sequential f32 sums are
+// done by one thread in the reference's order.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t encode_key(float v, uint32_t id) {
+  if (v == 0.0f) v = 0.0f;  // -0 == +0 for the sort
+  const uint32_t bits = __float_as_uint(v);
+  const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
+  return (uint64_t(~ord) << 32) | id;  // ascending key == descending value, then ascending id
+}
+
+__device__ __forceinline__ float decode_key(uint64_t k) {
+  const uint32_t ord = ~uint32_t(k >> 32);
+  const uint32_t bits = (ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord;
+  return __uint_as_float(bits);
+}
+
+struct SampleShared {
+  uint64_t keys[SAMPLE_MAX];
+  float probs[SAMPLE_MAX + 1];
+  float redf[SAMPLE_THREADS / WAVE];
+  uint32_t redu[SAMPLE_THREADS / WAVE];
+  float bcast_f;
+  uint32_t bcast_u[4];
+};
+
+__device__ __forceinline__ double lcg_next_unit(uint64_t* s) {
+  *s = *s * 6364136223846793005ull + 1ull;
+  const uint64_t mant = (*s >> 11) & ((1ull << 53) - 1ull);
+  return double(mant) / double(1ull << 53);
+}
+
+// j-th id (ascending) of [0, vocab) minus the ids of the n_fin sorted keys.
+__device__ uint32_t masked_id(const uint64_t* keys, uint32_t n_fin, uint32_t j, uint32_t vocab) {
+  uint32_t lo = 0, hi = vocab ? vocab - 1 : 0;
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    uint32_t le = 0;
+    for (uint32_t i = 0; i < n_fin; ++i) le += (uint32_t(keys[i]) <= mid) ? 1u : 0u;
+    const uint32_t masked_le = mid + 1 - le;
+    if (masked_le >= j + 1) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
+__device__ uint32_t sample_core(SampleShared& sh, const float* logits, const uint32_t* ids, uint32_t n,
+                                uint32_t vocab, SamplerCfg cfg, int64_t masked, int64_t force, uint64_t* rng,
+                                uint32_t* err) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr uint32_t NW = SAMPLE_THREADS / WAVE;
+  // pass 1: max and finite count
+  float mx = -INFINITY;
+  uint32_t nfin = 0;
+  for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
+    const uint32_t id = ids ? ids[i] : i;
+    const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
+    if (v > -INFINITY) {
+      mx = fmaxf(mx, v);
+      ++nfin;
+    }
+  }
+  mx = wave_max(mx);
+  float nf = wave_sum(float(nfin));
+  if (lane == 0) {
+    sh.redf[wave] = mx;
+    sh.redu[wave] = uint32_t(nf);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float m = -INFINITY;
+    uint32_t c = 0;
+    for (uint32_t w = 0; w < NW; ++w) {
+      m = fmaxf(m, sh.redf[w]);
+      c += sh.redu[w];
+    }
+    sh.bcast_f = m;
+    sh.bcast_u[0] = c;
+  }
+  __syncthreads();
+  const float M = sh.bcast_f;
+  const uint32_t n_fin = sh.bcast_u[0];
+  __syncthreads();
+
+  if (n_fin == 0) {  // every candidate masked: the reference returns the first id of a -inf list
+    uint32_t tok = 0;
+    if (tid == 0) {
+      (void)lcg_next_unit(rng);
+      tok = 0;
+    }
+    return tok;
+  }
+
+  // greedy fast path: T <= 0 and a unique value within 1e-6 of the max
+  if (!(cfg.temperature > 0.0f)) {
+    uint32_t cnt = 0, arg = 0xffffffffu;
+    for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
+      const uint32_t id = ids ? ids[i] : i;
+      const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
+      if (v > -INFINITY && fabsf(v - M) < 1e-6f) {
+        ++cnt;
+        arg = min(arg, id);
+      }
+    }
+    cnt = uint32_t(wave_sum(float(cnt)));
+    for (int off = 32; off >= 1; off >>= 1) arg = min(arg, uint32_t(__shfl_xor(int(arg), off, 64)));
+    if (lane == 0) {
+      sh.redu[wave] = cnt;
+      sh.keys[wave] = arg;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t c = 0, a = 0xffffffffu;
+      for (uint32_t w = 0; w < NW; ++w) {
+        c += sh.redu[w];
+        a = min(a, uint32_t(sh.keys[w]));
+      }
+      sh.bcast_u[1] = c;
+      sh.bcast_u[2] = a;
+    }
+    __syncthreads();
+    if (sh.bcast_u[1] == 1) {
+      const uint32_t tok = sh.bcast_u[2];
+      if (tid == 0) (void)lcg_next_unit(rng);
+      __syncthreads();
+      return tok;
+    }
+    __syncthreads();
+  }
+
+  // general path: sort finite candidates by (value desc, id asc)
+  if (n > SAMPLE_MAX) {
+    if (tid == 0 && err) atomicOr(err, ERR_SAMPLER);
+    return 0;
+  }
+  uint32_t P = 1;
+  while (P < n_fin) P <<= 1;
+  // compact finite keys: write all, non-finite become +inf keys (sorted last)
+  for (uint32_t i = tid; i < P; i += SAMPLE_THREADS) sh.keys[i] = ~0ull;
+  __syncthreads();
+  if (tid == 0) sh.bcast_u[3] = 0;
+  __syncthreads();
+  for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
+    const uint32_t id = ids ? ids[i] : i;
+    const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
+    if (v > -INFINITY) {
+      const uint32_t slot = atomicAdd(&sh.bcast_u[3], 1u);
+      sh.keys[slot] = encode_key(v, id);
+    }
+  }
+  __syncthreads();
+  for (uint32_t k = 2; k <= P; k <<= 1) {
+    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+      for (uint32_t i = tid; i < P; i += SAMPLE_THREADS) {
+        const uint32_t ixj = i ^ j;
+        if (ixj > i) {
+          const uint64_t a = sh.keys[i], b = sh.keys[ixj];
+          const bool up = (i & k) == 0;
+          if ((a > b) == up) {
+            sh.keys[i] = b;
+            sh.keys[ixj] = a;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  // item list: sorted finite (first min(k, n_fin)), then masked ids (if k > n_fin),
+  // or the appended always-include item.
+  const uint32_t k_lim = cfg.top_k > 0 ? min(uint32_t(cfg.top_k), vocab) : vocab;
+  const uint32_t n_top = min(k_lim, n_fin);
+  // force-include: present within the first k?  (thread 0 decides)
+  if (tid == 0) {
+    uint32_t force_pos = 0xffffffffu, appended = 0;
+    if (force >= 0 && uint64_t(force) < vocab) {
+      uint32_t rank = 0xffffffffu;
+      for (uint32_t i = 0; i < n_fin; ++i)
+        if (uint32_t(sh.keys[i]) == uint32_t(force)) {
+          rank = i;
+          break;
+        }
+      if (rank != 0xffffffffu) {
+        if (rank < n_top) {
+          force_pos = rank;
+        } else if (decode_key(sh.keys[rank]) > -1e30f) {
+          appended = 1;
+          force_pos = n_top;
+          sh.keys[SAMPLE_MAX - 1] = sh.keys[rank];  // stash the appended item
+        }
+      }
+    }
+    sh.bcast_u[1] = force_pos;
+    sh.bcast_u[2] = appended;
+  }
+  __syncthreads();
+  const uint32_t force_pos = sh.bcast_u[1];
+  const uint32_t appended = sh.bcast_u[2];
+  const uint32_t n_items = appended ? n_top + 1 : k_lim;  // masked tail when k_lim > n_fin
+  const uint32_t n_valued = appended ? n_top + 1 : n_top;  // items with a finite logit
+  const float vmax = decode_key(sh.keys[0]);
+  // softmax numerators in parallel (elementwise), sums sequential
+  for (uint32_t i = tid; i < n_valued; i += SAMPLE_THREADS) {
+    const uint64_t key = (appended && i == n_top) ? sh.keys[SAMPLE_MAX - 1] : sh.keys[i];
+    const float v = decode_key(key);
+    float p;
+    if (cfg.temperature > 0.0f)
+      p = expf_cr(__fdiv_rn(__fsub_rn(v, vmax), cfg.temperature));
+    else
+      p = fabsf(__fsub_rn(v, vmax)) < 1e-6f ? 1.0f : 0.0f;
+    sh.probs[i] = p;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < n_valued; ++i) sum = __fadd_rn(sum, sh.probs[i]);
+    sh.bcast_f = sum;
+  }
+  __syncthreads();
+  const float sum = sh.bcast_f;
+  if (sum > 0.0f)
+    for (uint32_t i = tid; i < n_valued; i += SAMPLE_THREADS) sh.probs[i] = __fdiv_rn(sh.probs[i], sum);
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t p_idx = 0;
+    float cs = 0.0f;
+    bool reached = false;
+    while (p_idx < n_valued) {
+      cs = __fadd_rn(cs, sh.probs[p_idx]);
+      p_idx += 1;
+      if (cs >= cfg.top_p) {
+        reached = true;
+        break;
+      }
+    }
+    if (!reached) p_idx = n_items;  // zero-probability tail never reaches top_p either
+    if (p_idx == 0) p_idx = 1;
+    if (force_pos != 0xffffffffu && force_pos >= p_idx) p_idx = force_pos + 1;
+    sh.bcast_u[1] = p_idx;
+    float sp = 0.0f;
+    for (uint32_t i = 0; i < min(p_idx, n_valued); ++i) sp = __fadd_rn(sp, sh.probs[i]);
+    sh.bcast_f = sp;
+  }
+  __syncthreads();
+  const uint32_t p_idx = sh.bcast_u[1];
+  const float sum_p = sh.bcast_f;
+  const uint32_t n_pv = min(p_idx, n_valued);
+  if (sum_p > 0.0f)
+    for (uint32_t i = tid; i < n_pv; i += SAMPLE_THREADS) sh.probs[i] = __fdiv_rn(sh.probs[i], sum_p);
+  __syncthreads();
+  if (tid == 0) {
+    const double draw = lcg_next_unit(rng);
+    const float target = fminf(fmaxf(float(draw), 0.0f), 1.0f - 1e-7f);
+    float cs = 0.0f;
+    uint32_t choice = p_idx - 1;
+    for (uint32_t i = 0; i < p_idx; ++i) {
+      cs = __fadd_rn(cs, i < n_valued ? sh.probs[i] : 0.0f);
+      if (target < cs) {
+        choice = i;
+        break;
+      }
+    }
+    uint32_t tok;
+    if (choice < n_top)
+      tok = uint32_t(sh.keys[choice]);
+    else if (appended)
+      tok = uint32_t(sh.keys[SAMPLE_MAX - 1]);
+    else
+      tok = masked_id(sh.keys, n_fin, choice - n_fin, vocab);
+    sh.bcast_u[0] = tok;
+  }
+  __syncthreads();
+  return sh.bcast_u[0];
+}
+
+__global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs a) {
+  extern __shared__ uint8_t smem_raw[];
+  SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
+  DevState* st = a.st;
+  if (st->done) return;
+  __shared__ uint32_t gen;
+  if (threadIdx.x == 0) {
+    if (a.after_step) {
+      if (a.codes_out) {
+        for (uint32_t cb = 0; cb < a.num_codebooks; ++cb)
+          a.codes_out[size_t(cb) * st->max_new + st->step_index] = int32_t(st->codes_frame[cb]);
+      }
+      st->step_index += 1;
+      const uint32_t past = st->n_past >= st->prompt_cols ? st->n_past - st->prompt_cols : 0u;
+      gen = past + st->step_index;
+    } else {
+      gen = 0;
+    }
+  }
+  __syncthreads();
+  const bool block = gen < st->min_tokens_before_end;
+  const int64_t masked = block ? int64_t(a.im_end) : -1;
+  const int64_t force = block ? -1 : int64_t(a.im_end);
+  uint64_t rng_local = st->rng;
+  const uint32_t tok = sample_core(sh, a.logits, a.ids, a.n, a.vocab, a.cfg, masked, force, &rng_local, &st->err);
+  if (threadIdx.x == 0) {
+    st->rng = rng_local;
+    st->main_token = tok;
+    if (a.token_out) *a.token_out = tok;
+    if (tok == a.im_end || st->step_index >= st->max_new) st->done = 1;
+  }
+}
+
+__global__ __launch_bounds__(SAMPLE_THREADS) void sample_fast_kernel(SampleArgs a) {
+  extern __shared__ uint8_t smem_raw[];
+  SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
+  DevState* st = a.st;
+  if (st->done) return;
+  uint64_t rng_local = st->rng;
+  const uint32_t tok = sample_core(sh, a.logits, nullptr, a.n, a.vocab, a.cfg, -1, -1, &rng_local, &st->err);
+  __shared__ uint32_t tok_s;
+  if (threadIdx.x == 0) {
+    st->rng = rng_local;
+    uint32_t t = tok;
+    if (t >= a.n) {
+      atomicOr(&st->err, ERR_SAMPLER);
+      t = 0;
+    }
+    st->codes_frame[a.cb_index] = t;
+    if (a.token_out) *a.token_out = t;
+    tok_s = t;
+  }
+  __syncthreads();
+  if (a.next_input) {
+    const uint32_t t = tok_s;
+    for (uint32_t i = threadIdx.x; i < a.dim; i += SAMPLE_THREADS)
+      a.next_input[i] = half_bits_to_float(a.fast_emb[size_t(t) * a.dim + i]);
+  }
+}
+
+__global__ __launch_bounds__(SAMPLE_THREADS) void sample_plain_kernel(const float* logits, uint32_t n, SamplerCfg cfg,
+                                                                      int64_t always_include, uint64_t* rng,
+                                                                      uint32_t* token_out, uint32_t* err) {
+  extern __shared__ uint8_t smem_raw[];
+  SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
+  uint64_t r = *rng;
+  const uint32_t tok = sample_core(sh, logits, nullptr, n, n, cfg, -1, always_include, &r, err);
+  if (threadIdx.x == 0) {
+    *rng = r;
+    *token_out = tok;
+  }
+}
+
+template <uint32_t WT>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* w, size_t row_bytes, uint32_t in, float* out) {
+  const uint32_t r = blockIdx.x;
+  const uint8_t* row = w + size_t(r) * row_bytes;
+  for (uint32_t e = threadIdx.x * 8; e < in; e += 256 * 8) {
+    float v[8];
+    load_w8<WT>(row, e, v);
+    for (int i = 0; i < 8; ++i) out[size_t(r) * in + e + i] = v[i];
+  }
+}
+
+__global__ void swiglu_kernel(const float* g, const float* u, float* out, uint32_t n, int fast) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gv = g[i];
+  if (fast)
+    out[i] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), u[i]);
+  else
+    out[i] = __fmul_rn(__fmul_rn(gv, __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gv)))), u[i]);
+}
+
+__global__ void add_position_kernel(DevState* st, uint32_t n) {
+  if (st->done) return;
+  if (threadIdx.x == 0) st->n_past += n;
+}
+
+template <class K>
+hipError_t set_max_lds(K kernel) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             int(sizeof(SampleShared)));
+}
+
+}  // namespace
+
+hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
+  if (size_t(ncol) * a.in * sizeof(float) > 150 * 1024) return hipErrorInvalidValue;
+  switch (wtype) {
+    case W_F16:
+      if (a.in % 8) return hipErrorInvalidValue;
+      return gemv_pick_epi<W_F16>(epi, ncol, a, s);
+    case W_Q8_0:
+      if (a.in % 32) return hipErrorInvalidValue;
+      return gemv_pick_epi<W_Q8_0>(epi, ncol, a, s);
+    case W_Q4_0:
+      if (a.in % 32) return hipErrorInvalidValue;
+      return gemv_pick_epi<W_Q4_0>(epi, ncol, a, s);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_rms_norm(const float* x, const float* w, float* y, uint32_t n, uint32_t ncol, float eps,
+                           const uint32_t* done, hipStream_t s) {
+  hipLaunchKernelGGL(rms_norm_kernel, dim3(ncol), dim3(256), 0, s, x, w, y, n, eps, done);
+  return hipGetLastError();
+}
+
+hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
+  if (a.hd % 2 || a.hd > 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(qkv_post_kernel, dim3(a.H + 2 * a.Hkv, a.ncol), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+  if (a.hd % 4 || a.hd > 256 || a.chunk % 64 || a.H % a.Hkv) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(attn_partial_kernel, dim3(a.max_chunks, a.Hkv, a.ncol), dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3(a.H, a.ncol), dim3(128), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
+  if (a.num_codebooks > 16) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(embed_kernel, dim3(a.n), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fast_begin(DevState* st, const float* slow_hidden, const uint16_t* fast_emb, float* fh,
+                             uint32_t dim, uint32_t codebook_size, uint32_t sem_begin, uint32_t sem_end,
+                             hipStream_t s) {
+  hipLaunchKernelGGL(fast_begin_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, st, slow_hidden, fast_emb, fh,
+                     dim, codebook_size, sem_begin, sem_end);
+  return hipGetLastError();
+}
+
+hipError_t launch_sample_slow(const SampleArgs& a, hipStream_t s) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = set_max_lds(sample_slow_kernel);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  if (a.n > SAMPLE_MAX - 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sample_slow_kernel, dim3(1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sample_fast(const SampleArgs& a, hipStream_t s) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = set_max_lds(sample_fast_kernel);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  if (a.n > SAMPLE_MAX - 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sample_fast_kernel, dim3(1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sample_plain(const float* logits, uint32_t n, SamplerCfg cfg, int64_t always_include,
+                               uint64_t* rng, uint32_t* token_out, uint32_t* err, hipStream_t s) {
+  static bool configured = false;
+  if (!configured) {
+    hipError_t e = set_max_lds(sample_plain_kernel);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  if (n > SAMPLE_MAX - 1 || n == 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(sample_plain_kernel, dim3(1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, logits, n, cfg,
+                     always_include, rng, token_out, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_bytes, uint32_t rows, uint32_t in,
+                               float* out, hipStream_t s) {
+  switch (wtype) {
+    case W_F16:
+      if (in % 8) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(dequant_kernel<W_F16>, dim3(rows), dim3(256), 0, s, w, row_bytes, in, out);
+      break;
+    case W_Q8_0:
+      if (in % 32) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(dequant_kernel<W_Q8_0>, dim3(rows), dim3(256), 0, s, w, row_bytes, in, out);
+      break;
+    case W_Q4_0:
+      if (in % 32) return hipErrorInvalidValue;
+      hipLaunchKernelGGL(dequant_kernel<W_Q4_0>, dim3(rows), dim3(256), 0, s, w, row_bytes, in, out);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n, int fast, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256), dim3(256), 0, s, g, u, out, n, fast);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s) {
+  hipLaunchKernelGGL(add_position_kernel, dim3(1), dim3(64), 0, s, st, n);
+  return hipGetLastError();
+}
+
+}  // namespace s2

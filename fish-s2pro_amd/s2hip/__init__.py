@@ -1,0 +1,9 @@
+"""s2hip -- MI355X-native dual-AR (Slow-AR + Fast-AR) token loop.
+
+The compute path is libs2hip.so (HIP kernels for gfx950 behind the C ABI in
+include/s2hip.h); this package is its host-side binding plus the seeded
+synthetic-model writer.
+"""
+
+from .engine import Engine, S2HipError, version  # noqa: F401
+from . import synth  # noqa: F401

@@ -1,0 +1,176 @@
+/*
+ * s2hip.h -- C ABI of the MI355X (gfx950) dual-AR token loop.
+ *
+ * Drop-in for the Slow-AR / Fast-AR code generation of stevenke1981/fish-s2pro's
+ * rust-pure backend (crates/fish_s2_infer).  The ABI follows the reference's
+ * own native-engine convention (crates/fish_s2_infer/ffi/s2_engine_ffi.h:10-37):
+ * an opaque handle from *_create (NULL on failure), int32_t returns with
+ * 1 = success / 0 = failure, and the failure text copied (truncated,
+ * NUL-terminated) into a caller-provided err buffer of err_cap bytes.
+ * No HIP, torch or device types cross this boundary: inputs are caller-owned
+ * host pointers and outputs go to caller-provided host buffers.
+ *
+ * Threading: a handle is not thread-safe; the caller serialises calls on one
+ * handle, as the reference serialises InferenceEngine behind a Mutex
+ * (crates/fish_s2_infer/src/server.rs:57, engine.rs:159).  Each handle owns
+ * one HIP stream on its device.
+ */
+#ifndef S2HIP_H
+#define S2HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define S2HIP_ABI_VERSION 1
+
+/* GGML tensor type ids (crates/fish_s2_core/src/gguf.rs:178-200). */
+#define S2HIP_GGML_F32 0u
+#define S2HIP_GGML_F16 1u
+#define S2HIP_GGML_Q4_0 2u
+#define S2HIP_GGML_Q8_0 8u
+
+/* s2hip_config.flags */
+#define S2HIP_FLAG_NO_GRAPH 1u /* launch every frame kernel directly instead of replaying a HIP graph */
+
+typedef struct s2hip_engine s2hip_engine;
+
+typedef struct {
+  const char* gguf_path;  /* transformer GGUF: F16, Q8_0 or Q4_0 linear weights */
+  uint32_t max_seq_len;   /* Slow-AR KV capacity (positions) */
+  uint32_t im_end_id;     /* tokenizer <|im_end|> id (tokenizer.rs:36-62) */
+  int32_t device;         /* HIP device ordinal */
+  uint32_t flags;         /* S2HIP_FLAG_* */
+} s2hip_config;
+
+/* Model shape read from GGUF metadata (registry.rs:45-214), shape-generic. */
+typedef struct {
+  uint32_t slow_layers, fast_layers;
+  uint32_t dim, ffn, heads, kv_heads, head_dim;
+  uint32_t fast_ffn, fast_heads, fast_kv_heads, fast_head_dim;
+  uint32_t vocab, codebook_size, num_codebooks;
+  uint32_t semantic_begin, semantic_end;
+  uint32_t slow_qk_norm, scale_codebook_embeddings;
+  uint32_t linear_type; /* GGML type of the linear weights */
+  uint32_t max_seq_len;
+  float rope_base, fast_rope_base, eps, fast_eps;
+  uint64_t weight_bytes; /* bytes resident in HBM for all tensors */
+} s2hip_spec;
+
+/* SamplerParams (crates/fish_s2_infer/src/sampling.rs:12-27). */
+typedef struct {
+  float temperature;
+  float top_p;
+  int32_t top_k;
+} s2hip_sampler;
+
+/* GenerateParams (crates/fish_s2_infer/src/generate.rs:13-32). */
+typedef struct {
+  uint32_t max_new_tokens;
+  float temperature;
+  float top_p;
+  int32_t top_k;
+  uint32_t min_tokens_before_end;
+} s2hip_gen_params;
+
+/* Timing of one s2hip_generate_codes call (HIP events on the engine stream). */
+typedef struct {
+  double prefill_ms; /* prompt prefill + first semantic sample */
+  double decode_ms;  /* all frames: Fast-AR codebooks + Slow-AR step + sampling */
+  uint32_t n_frames;
+  uint32_t graph_used;
+} s2hip_gen_stats;
+
+const char* s2hip_version(void);
+
+/* SlowArState::open (crates/fish_s2_infer/src/slow_ar.rs:387-412) +
+ * FastArWeights::from_gguf (fast_ar.rs:202-224): parse the GGUF once and
+ * upload every tensor to HBM in its native block layout; allocate the
+ * device KV cache for max_seq_len positions. */
+s2hip_engine* s2hip_create(const s2hip_config* cfg, char* err, size_t err_cap);
+void s2hip_destroy(s2hip_engine* engine);
+int32_t s2hip_get_spec(const s2hip_engine* engine, s2hip_spec* out);
+
+/* SlowArState::reset (slow_ar.rs:434-438). */
+int32_t s2hip_reset(s2hip_engine* engine, char* err, size_t err_cap);
+/* SlowArState::n_past (slow_ar.rs:418-420). */
+uint32_t s2hip_n_past(const s2hip_engine* engine);
+
+/* SlowArState::prefill / step / eval (slow_ar.rs:440-527): flat_tokens is
+ * time-major [n_tokens][num_codebooks + 1].  hidden_out receives the
+ * post-final-norm hidden of the last token [dim]; logits_out (nullable)
+ * receives the full-vocabulary logits [vocab]. */
+int32_t s2hip_eval(s2hip_engine* engine, const int32_t* flat_tokens, size_t n_tokens, float* hidden_out,
+                   float* logits_out, char* err, size_t err_cap);
+
+/* forward_codebook_prefix (crates/fish_s2_infer/src/fast_ar.rs:360-437):
+ * logits_out [codebook_size]. */
+int32_t s2hip_fast_logits(s2hip_engine* engine, const float* slow_hidden, const uint32_t* prefix_codes,
+                          size_t prefix_len, float* logits_out, char* err, size_t err_cap);
+
+/* generate_codebooks_for_semantic (fast_ar.rs:440-470): codes_out
+ * [num_codebooks]; rng_state is the SeededRng state (sampling.rs:34-52),
+ * updated in place. */
+int32_t s2hip_fast_codebooks(s2hip_engine* engine, const float* slow_hidden, uint32_t semantic_code,
+                             const s2hip_sampler* sampler, uint64_t* rng_state, uint32_t* codes_out, char* err,
+                             size_t err_cap);
+
+/* generate_codes (crates/fish_s2_infer/src/generate.rs:117-221): prompt_flat is
+ * time-major [prompt_cols][num_codebooks + 1] (prompt.rs:77-103).  codes_out
+ * holds num_codebooks * max_new_tokens entries and receives the compacted
+ * codebook-major codes [num_codebooks][n_frames] (generate.rs:346-390).
+ * stats is nullable. */
+int32_t s2hip_generate_codes(s2hip_engine* engine, const int32_t* prompt_flat, size_t prompt_cols,
+                             const s2hip_gen_params* params, uint64_t* rng_state, int32_t* codes_out,
+                             uint32_t* n_frames_out, s2hip_gen_stats* stats, char* err, size_t err_cap);
+
+/* ---- op level: the MatmulBackend seam (crates/fish_s2_infer/src/backend.rs:5-39)
+ * and the other per-op functions, run on the engine's device with host
+ * inputs/outputs.  Used by parity dumps and tests. */
+
+/* MatmulBackend::linear (backend.rs:8-14) generalised to GGML row types:
+ * y[c][o] = sum_i x[c][i] * W[o][i] for n_cols input columns.  weight holds
+ * out_dim GGML rows of in_dim elements (F16 / Q8_0 / Q4_0). */
+int32_t s2hip_op_linear(s2hip_engine* engine, const void* weight, uint32_t ggml_type, size_t in_dim,
+                        size_t out_dim, const float* x, size_t n_cols, float* y, char* err, size_t err_cap);
+/* MatmulBackend::rms_norm (backend.rs:16-18) over n_cols vectors. */
+int32_t s2hip_op_rms_norm(s2hip_engine* engine, const float* x, const float* weight, size_t n, size_t n_cols,
+                          float eps, float* y, char* err, size_t err_cap);
+/* Q-block / f16 dequantisation of `rows` GGML rows to f32 (bit-exact). */
+int32_t s2hip_op_dequant_rows(s2hip_engine* engine, const void* weight, uint32_t ggml_type, size_t in_dim,
+                              size_t rows, float* out, char* err, size_t err_cap);
+/* Slow-AR prepare step: QK-norm (if q_norm/k_norm non-NULL) + apply_rope_normal
+ * (attention.rs:172-206) at `position`, on one token's qkv row
+ * [(heads + 2 kv_heads) head_dim]; outputs q [heads*hd], k and v [kv_heads*hd]. */
+int32_t s2hip_op_qk_rope(s2hip_engine* engine, const float* qkv, uint32_t heads, uint32_t kv_heads,
+                         uint32_t head_dim, uint32_t position, float rope_base, const float* q_norm,
+                         const float* k_norm, float eps, float* q_out, float* k_out, float* v_out, char* err,
+                         size_t err_cap);
+/* MatmulBackend::gqa_decode_attention (backend.rs:30-38): keys/values
+ * [token_count][kv_heads][head_dim]. */
+int32_t s2hip_op_attention(s2hip_engine* engine, const float* q, const float* keys, const float* values,
+                           uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t token_count,
+                           float attn_scale, float* out, char* err, size_t err_cap);
+/* swiglu_split: Slow (slow_ar.rs:1215-1232) when fast == 0, Fast (fast_ar.rs:472-485) otherwise. */
+int32_t s2hip_op_swiglu(s2hip_engine* engine, const float* gate, const float* up, size_t n, int32_t fast,
+                        float* out, char* err, size_t err_cap);
+/* sample_token (sampling.rs:120-241); always_include < 0 means None. */
+int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, const s2hip_sampler* sampler,
+                        int64_t always_include, uint64_t* rng_state, uint32_t* token_out, char* err,
+                        size_t err_cap);
+
+/* Measurement: average device time of one launch of a named decode kernel,
+ * timed with HIP events on the engine stream over `reps` passes across every
+ * layer (so no pass re-reads weights from cache).  kernel: "slow_w13",
+ * "slow_wqkv", "slow_wo", "slow_w2", "slow_head".  bytes_per_launch receives
+ * the algorithmic HBM bytes of one launch (weights + input + output). */
+int32_t s2hip_time_kernel(s2hip_engine* engine, const char* kernel, uint32_t reps, double* avg_us,
+                          double* bytes_per_launch, char* err, size_t err_cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

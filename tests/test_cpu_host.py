@@ -1,0 +1,92 @@
+"""CPU-only checks: golden fixtures, the synthetic GGUF writer, and that the
+C-ABI library loads and exports every symbol include/s2hip.h declares (no
+compute call is made: there is no GPU here)."""
+
+import ctypes
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from s2hip import _lib, _paths, synth
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+GOLD = json.load(open(os.path.join(HERE, "golden", "tiny_greedy_codes.json")))
+
+
+def _sha(path):
+    return hashlib.sha256(open(path, "rb").read()).hexdigest()
+
+
+def test_synthetic_writer_is_deterministic(tiny_gguf, tiny_q8_gguf, tiny_q4_gguf):
+    assert _sha(tiny_gguf) == GOLD["gguf_sha256"]["tiny_f16"]
+    assert _sha(tiny_q8_gguf) == GOLD["gguf_sha256"]["tiny_q8_0"]
+    assert _sha(tiny_q4_gguf) == GOLD["gguf_sha256"]["tiny_q4_0"]
+
+
+def test_oracle_reproduces_golden_codes(tiny_gguf):
+    m = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    r = m.generate_codes(np.array(GOLD["prompt_flat"], np.int32), GOLD["max_new_tokens"], 0.0, 1.0, 0,
+                         GOLD["min_tokens_before_end"], GOLD["rng_seed"])
+    assert r["codes"].tolist() == GOLD["codes"] and r["rng_state"] == GOLD["rng_state"]
+
+
+def test_synthetic_weights_statistics(tiny_gguf):
+    import gguf_util
+
+    t = gguf_util.read_tensors(tiny_gguf)
+    emb = t["embeddings.weight"]
+    assert emb.shape == (8192, 512) and emb.dtype == np.float16
+    assert abs(float(emb.astype(np.float64).std()) - 0.02) < 2e-4
+    assert abs(float(emb.astype(np.float64).mean())) < 2e-4
+    assert (t["norm.weight"] == 1).all() and (t["layers.0.attention.q_norm.weight"] == 1).all()
+    w = t["layers.3.feed_forward.w2.weight"]
+    assert w.shape == (512, 1536) and abs(float(w.astype(np.float64).std()) - 0.02) < 4e-4
+
+
+@pytest.mark.parametrize("gtype", [synth.GGML_Q8_0, synth.GGML_Q4_0])
+def test_quantizer_error_bound(gtype):
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        x = (rng.standard_normal(32) * 0.02).astype(np.float32)
+        blk = synth.quantize_block(gtype, x)
+        y = O.dequant_row(blk, gtype, 32)
+        amax = np.abs(x).max()
+        if gtype == synth.GGML_Q8_0:
+            step = amax / 127.0  # rounding to nearest + f16 rounding of d (rel 2^-11) on |q| <= 127
+            bound = 0.5 * step + 127 * step * 2.0 ** -10
+        else:
+            step = amax / 8.0  # the clamp at 15 costs one step on the side opposite the max
+            bound = 1.0 * step + 8 * step * 2.0 ** -10
+        assert np.max(np.abs(x - y)) <= bound
+
+
+def test_f16_writer_matches_numpy():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.standard_normal(5000) * 0.02, rng.standard_normal(500) * 1e-6]).astype(np.float32)
+    got = np.array([synth._load().s2synth_f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, x.astype(np.float16).view(np.uint16))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    declared = _lib.declared_functions()
+    assert len(declared) >= 17
+    missing = [f for f in declared if not hasattr(L, f)]
+    assert not missing
+    assert L.s2hip_version().decode().startswith("s2hip")
+
+
+def test_library_has_gfx950_code_object():
+    # the fat binary embedded in the library names its offload target
+    assert b"amdgcn-amd-amdhsa--gfx950" in open(_paths.hip_library(), "rb").read()
+
+
+def test_create_rejects_bad_config_without_gpu():
+    L = _lib.load()
+    err = ctypes.create_string_buffer(256)
+    assert not L.s2hip_create(None, err, len(err))
+    assert b"NULL" in err.value

@@ -1,0 +1,160 @@
+"""Dual-AR loop parity on the tiny shape: HIP engine vs the CPU oracle.
+
+Greedy and seeded-sampler code ids must be bit-exact; hidden states and
+logits within the f16-path tolerance (1e-2 relative; actual ~1e-5).
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import make_prompt
+from oracle import oracle as O
+from s2hip import synth
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _engine(path, max_seq=64, im_end=None, graph=True):
+    from s2hip import Engine
+
+    return Engine(path, max_seq, synth.TINY.im_end_id if im_end is None else im_end, use_graph=graph)
+
+
+def _oracle(path, max_seq=64, im_end=None):
+    return O.OracleModel(path, max_seq, synth.TINY.im_end_id if im_end is None else im_end)
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(1e-30, float(np.max(np.abs(b)))))
+
+
+def test_eval_prefill_and_steps_match_oracle(tiny_gguf):
+    prompt = make_prompt(synth.TINY, 32, seed=0)
+    e, o = _engine(tiny_gguf), _oracle(tiny_gguf)
+    hg, lg = e.eval(prompt)
+    ho, lo = o.eval(prompt)
+    assert _rel(hg, ho) < 1e-4 and _rel(lg, lo) < 1e-4
+    for t in range(3):
+        tok = np.zeros(11, np.int32)
+        tok[0] = synth.TINY.semantic_begin + 5 * t
+        tok[1:] = np.arange(10) * 3 + t
+        hg, lg = e.step(tok)
+        ho, lo = o.eval(tok)
+        assert _rel(hg, ho) < 1e-4 and _rel(lg, lo) < 1e-4
+    assert e.n_past == o.n_past == 35
+    e.reset()
+    o.reset()
+    assert e.n_past == 0
+    hg, _ = e.eval(prompt[:11 * 5])
+    ho, _ = o.eval(prompt[:11 * 5])
+    assert _rel(hg, ho) < 1e-4
+
+
+def test_fast_logits_match_oracle(tiny_gguf):
+    e, o = _engine(tiny_gguf), _oracle(tiny_gguf)
+    h, _ = o.eval(make_prompt(synth.TINY, 8, seed=1))
+    for plen in range(0, 10):
+        prefix = (np.arange(plen) * 97 + 13) % synth.TINY.codebook_size
+        assert _rel(e.fast_logits(h, prefix), o.fast_logits(h, prefix)) < 1e-4
+
+
+@pytest.mark.parametrize("T,top_p,top_k,seed", [(0.0, 1.0, 0, 0), (0.7, 0.9, 0, 3), (0.7, 0.7, 30, 9)])
+def test_fast_codebooks_match_oracle(tiny_gguf, T, top_p, top_k, seed):
+    e, o = _engine(tiny_gguf), _oracle(tiny_gguf)
+    h, _ = o.eval(make_prompt(synth.TINY, 8, seed=2))
+    for sem in (0, 17, 1023):
+        cg, sg = e.fast_codebooks(h, sem, T, top_p, top_k, seed)
+        co, so = o.fast_codebooks(h, sem, T, top_p, top_k, seed)
+        assert np.array_equal(cg, co) and sg == so
+
+
+def test_greedy_codes_bit_exact_and_golden(tiny_gguf):
+    gold = json.load(open(os.path.join(HERE, "golden", "tiny_greedy_codes.json")))
+    prompt = np.array(gold["prompt_flat"], np.int32)
+    e = _engine(tiny_gguf)
+    r = e.generate_codes(prompt, gold["max_new_tokens"], 0.0, 1.0, 0, gold["min_tokens_before_end"],
+                         gold["rng_seed"])
+    assert r["n_frames"] == gold["n_frames"]
+    assert r["codes"].tolist() == gold["codes"]
+    o = _oracle(tiny_gguf)
+    ro = o.generate_codes(prompt, gold["max_new_tokens"], 0.0, 1.0, 0, gold["min_tokens_before_end"],
+                          gold["rng_seed"])
+    assert np.array_equal(r["codes"], ro["codes"]) and r["rng_state"] == ro["rng_state"]
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_sampled_codes_bit_exact(tiny_gguf, graph):
+    prompt = make_prompt(synth.TINY, 32, seed=11)
+    e, o = _engine(tiny_gguf, graph=graph), _oracle(tiny_gguf)
+    kw = dict(temperature=0.7, top_p=0.9, top_k=0, min_tokens_before_end=40, rng_state=1)
+    r = e.generate_codes(prompt, 20, **kw)
+    ro = o.generate_codes(prompt, 20, **kw)
+    assert r["n_frames"] == ro["n_frames"] == 20
+    assert np.array_equal(r["codes"], ro["codes"]) and r["rng_state"] == ro["rng_state"]
+    assert r["graph_used"] == graph
+
+
+def test_repeated_generate_is_deterministic(tiny_gguf):
+    prompt = make_prompt(synth.TINY, 16, seed=12)
+    e = _engine(tiny_gguf)
+    a = e.generate_codes(prompt, 12, min_tokens_before_end=100)
+    b = e.generate_codes(prompt, 12, min_tokens_before_end=100)
+    c = e.generate_codes(prompt, 5, min_tokens_before_end=100)
+    assert np.array_equal(a["codes"], b["codes"])
+    assert np.array_equal(a["codes"][:, :5], c["codes"])
+
+
+def test_im_end_stops_generation_like_oracle(tiny_gguf):
+    prompt = make_prompt(synth.TINY, 16, seed=13)
+    o = _oracle(tiny_gguf)
+    ref = o.generate_codes(prompt, 12, min_tokens_before_end=0)
+    # make the main token of frame 6 the end token: both sides must stop there
+    stop_id = synth.TINY.semantic_begin + int(ref["codes"][0, 6])
+    e2, o2 = _engine(tiny_gguf, im_end=stop_id), _oracle(tiny_gguf, im_end=stop_id)
+    for mtbe in (0, 4):
+        rg = e2.generate_codes(prompt, 12, min_tokens_before_end=mtbe)
+        ro = o2.generate_codes(prompt, 12, min_tokens_before_end=mtbe)
+        assert rg["n_frames"] == ro["n_frames"] < 12
+        assert np.array_equal(rg["codes"], ro["codes"]) and rg["rng_state"] == ro["rng_state"]
+
+
+@pytest.mark.parametrize("which", ["q8", "q4"])
+def test_quantized_codes_bit_exact(request, which):
+    path = request.getfixturevalue(f"tiny_{which}_gguf")
+    prompt = make_prompt(synth.TINY, 24, seed=14)
+    e, o = _engine(path), _oracle(path)
+    hg, lg = e.eval(prompt)
+    ho, lo = o.eval(prompt)
+    assert _rel(hg, ho) < 2e-2 and _rel(lg, lo) < 2e-2
+    for kw in (dict(), dict(temperature=0.7, top_p=0.9, rng_state=5)):
+        rg = e.generate_codes(prompt, 16, min_tokens_before_end=100, **kw)
+        ro = o.generate_codes(prompt, 16, min_tokens_before_end=100, **kw)
+        assert np.array_equal(rg["codes"], ro["codes"]) and rg["rng_state"] == ro["rng_state"]
+
+
+def test_errors_match_reference_behaviour(tiny_gguf):
+    from s2hip import S2HipError
+
+    e = _engine(tiny_gguf, max_seq=40)
+    prompt = make_prompt(synth.TINY, 32, seed=15)
+    with pytest.raises(S2HipError, match="KV cache overflow"):
+        e.eval(make_prompt(synth.TINY, 41, seed=15))
+    with pytest.raises(S2HipError, match="KV cache overflow"):
+        e.generate_codes(prompt, 16, min_tokens_before_end=100)
+    bad = prompt.copy()
+    bad[0] = synth.TINY.vocab + 5
+    with pytest.raises(S2HipError, match="out of range"):
+        e.generate_codes(bad, 4)
+    with pytest.raises(S2HipError, match="step token width"):
+        e.step(np.zeros(5, np.int32))
+    with pytest.raises(S2HipError):
+        _engine("/nonexistent.gguf")
+    # the engine still works after the errors
+    e.reset()
+    r = e.generate_codes(prompt[:11 * 8], 4, min_tokens_before_end=100)
+    assert r["n_frames"] == 4

@@ -1,0 +1,132 @@
+"""Per-op parity of the HIP kernels against the CPU oracle (through the C ABI).
+
+Tolerances are the north-star bars: 1e-2 relative for f16-weight paths and
+2e-2 for quantised ones (the kernels accumulate in f32, so actual errors are
+~1e-6); dequantisation and sampling must be bit-exact.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from s2hip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def eng(tiny_gguf):
+    from s2hip import Engine
+
+    e = Engine(tiny_gguf, 64, synth.TINY.im_end_id)
+    yield e
+    e.close()
+
+
+def _rows(gtype, wf):
+    if gtype == 1:
+        return wf.astype(np.float16).view(np.uint8).ravel()
+    return np.frombuffer(b"".join(synth.quantize_block(gtype, b) for b in wf.reshape(-1, 32)), np.uint8)
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(1e-30, float(np.max(np.abs(b)))))
+
+
+@pytest.mark.parametrize("gtype", [1, 8, 2])
+def test_dequant_bit_exact(eng, gtype):
+    rng = np.random.default_rng(10 + gtype)
+    in_dim, rows = 2560, 24
+    wf = (rng.standard_normal((rows, in_dim)) * 0.02).astype(np.float32)
+    raw = _rows(gtype, wf)
+    got = eng.dequant_rows(raw, gtype, in_dim, rows)
+    want = O.dequant_row(raw.tobytes(), gtype, in_dim * rows).reshape(rows, in_dim)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("gtype,tol", [(1, 1e-2), (8, 2e-2), (2, 2e-2)])
+@pytest.mark.parametrize("in_dim,out_dim,ncol", [(512, 768, 1), (2560, 6144, 1), (9728, 2560, 1),
+                                                 (4096, 2560, 2), (2560, 9728, 4), (1536, 100, 3)])
+def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
+    rng = np.random.default_rng(in_dim + out_dim + ncol)
+    wf = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
+    raw = _rows(gtype, wf)
+    x = rng.standard_normal((ncol, in_dim)).astype(np.float32)
+    got = eng.linear(raw, gtype, in_dim, out_dim, x)
+    for c in range(ncol):
+        want = O.linear(x[c], raw, gtype, in_dim, out_dim)
+        assert _rel(got[c], want) < min(tol, 1e-4), c
+
+
+def test_rms_norm_matches_oracle(eng):
+    rng = np.random.default_rng(20)
+    x = rng.standard_normal((3, 2560)).astype(np.float32) * 3
+    w = rng.standard_normal(2560).astype(np.float32)
+    got = eng.rms_norm(x, w, 1e-6)
+    for c in range(3):
+        np.testing.assert_allclose(got[c], O.rms_norm(x[c], w, 1e-6), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("hd,H,Hkv,qk", [(128, 32, 8, True), (64, 8, 2, True), (128, 32, 8, False)])
+@pytest.mark.parametrize("pos", [0, 1, 255, 767])
+def test_qk_norm_rope_matches_oracle(eng, hd, H, Hkv, qk, pos):
+    rng = np.random.default_rng(hd + pos)
+    qkv = rng.standard_normal((H + 2 * Hkv) * hd).astype(np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if qk else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if qk else None
+    q, k, v = eng.qk_rope(qkv, H, Hkv, hd, pos, 1.0e6, qn, kn, 1e-6)
+    q_raw, k_raw, v_raw = qkv[:H * hd], qkv[H * hd:(H + Hkv) * hd], qkv[(H + Hkv) * hd:]
+    if qk:
+        q_raw = O.rms_norm_heads(q_raw, qn, hd, 1e-6)
+        k_raw = O.rms_norm_heads(k_raw, kn, hd, 1e-6)
+    np.testing.assert_allclose(q, O.rope_normal(q_raw, hd, pos, 1.0e6), rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(k, O.rope_normal(k_raw, hd, pos, 1.0e6), rtol=1e-5, atol=1e-5)
+    assert np.array_equal(v, v_raw)
+
+
+@pytest.mark.parametrize("H,Hkv,hd,T", [(32, 8, 128, 1), (32, 8, 128, 200), (32, 8, 128, 768), (8, 2, 64, 37),
+                                        (32, 8, 128, 10)])
+def test_attention_matches_oracle(eng, H, Hkv, hd, T):
+    rng = np.random.default_rng(T + hd)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    k = rng.standard_normal(T * Hkv * hd).astype(np.float32)
+    v = rng.standard_normal(T * Hkv * hd).astype(np.float32)
+    sc = 1 / math.sqrt(hd)
+    got = eng.attention(q, k, v, H, Hkv, hd, T, sc)
+    want = O.gqa_attention(q, k, v, H, Hkv, hd, T, sc)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("fast", [False, True])
+def test_swiglu_matches_oracle(eng, fast):
+    rng = np.random.default_rng(30)
+    g = (rng.standard_normal(9728) * 4).astype(np.float32)
+    u = rng.standard_normal(9728).astype(np.float32)
+    np.testing.assert_allclose(eng.swiglu(g, u, fast), O.swiglu(g, u, fast), rtol=1e-6, atol=1e-6)
+
+
+SAMPLER_CASES = [
+    (0.0, 1.0, 0), (0.0, 0.9, 0), (0.0, 1.0, 30), (0.7, 0.9, 0), (0.7, 0.7, 30), (1.0, 1.0, 0),
+    (0.3, 0.5, 5), (0.7, 1.0, 4096), (1.5, 0.95, 1),
+]
+
+
+@pytest.mark.parametrize("T,top_p,top_k", SAMPLER_CASES)
+@pytest.mark.parametrize("n", [4096, 1024, 4097, 37])
+def test_sampler_bit_exact(eng, T, top_p, top_k, n):
+    rng = np.random.default_rng(n * 7 + int(T * 10) + top_k)
+    st_o = st_g = 12345 + n
+    for trial in range(12):
+        logits = rng.standard_normal(n).astype(np.float32)
+        if trial % 4 == 1:
+            logits[rng.integers(0, n, 3)] = logits.max()  # exact ties at the max
+        if trial % 4 == 2:
+            logits[rng.integers(0, n, n // 3)] = -np.inf  # masked entries
+        if trial % 4 == 3:
+            logits = np.round(logits * 4) / 4  # many equal values
+        always = int(rng.integers(0, n)) if trial % 3 == 0 else None
+        to, st_o = O.sample_token(logits, T, top_p, top_k, always, st_o)
+        tg, st_g = eng.sample(logits, T, top_p, top_k, always, st_g)
+        assert (tg, st_g) == (to, st_o), (trial, tg, to)

@@ -1,0 +1,345 @@
+"""Pins the CPU oracle (oracle/s2_oracle.cpp) before it is trusted as the checker.
+
+Sources of truth, in order:
+* the reference's own known-answer tests (values copied from its #[test]s);
+* closed forms / textbook routines (IEEE half via numpy, sequential f32 sums
+  via np.add.accumulate, float64 softmax attention, the LCG in Python ints);
+* invariants the reference itself asserts (decode == prefill, Fast-AR
+  recompute == incremental).
+"""
+
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+import gguf_util
+from conftest import make_prompt
+from s2hip import synth
+
+
+# ---------------------------------------------------------------- f16 ----
+def test_f16_decode_kat():
+    # crates/fish_s2_infer/src/tensor.rs:339-345
+    assert [O.f16_to_f32(b) for b in (0x3C00, 0xC000, 0x3800, 0x4400)] == [1.0, -2.0, 0.5, 4.0]
+
+
+def test_f16_round_kat():
+    # tensor.rs:356-364
+    for v in (1.0, -2.0, 0.5):
+        assert O.f16_to_f32(O.f32_to_f16(v)) == v
+    assert O.f32_to_f16(float("inf")) == 0x7C00
+    assert O.f32_to_f16(float("-inf")) == 0xFC00
+    assert O.f32_to_f16(float("nan")) & 0x7C00 == 0x7C00
+
+
+def test_f16_decode_exhaustive_matches_ieee():
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([O.f16_to_f32(int(b)) for b in bits], np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+
+
+def test_f16_round_matches_numpy_rne():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 0.02,
+        (rng.standard_normal(5000) * 1e-6).astype(np.float32),  # f16 subnormals
+        rng.uniform(-70000, 70000, 5000).astype(np.float32),    # overflow region
+        np.array([65504, 65519.99, 65520, 2.0 ** -25, 2.0 ** -24, 1.5 * 2.0 ** -24], np.float32),
+    ])
+    want = x.astype(np.float16).view(np.uint16)
+    got = np.array([O.f32_to_f16(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, want)
+
+
+# --------------------------------------------------------- Q blocks ------
+def _q8_block(d, q):
+    return np.frombuffer(np.float16(d).tobytes(), np.uint8).tobytes() + np.asarray(q, np.int8).tobytes()
+
+
+def _q4_block(d, nib):
+    nib = np.asarray(nib, np.uint8)
+    qs = (nib[:16] | (nib[16:] << 4)).astype(np.uint8)
+    return np.frombuffer(np.float16(d).tobytes(), np.uint8).tobytes() + qs.tobytes()
+
+
+def test_q8_0_dequant_closed_form():
+    rng = np.random.default_rng(1)
+    raw, want = b"", []
+    for _ in range(8):
+        d = np.float16(rng.uniform(-0.01, 0.01))
+        q = rng.integers(-128, 128, 32)
+        raw += _q8_block(d, q)
+        want.append(np.float32(d) * q.astype(np.float32))
+    got = O.dequant_row(raw, 8, 256)
+    assert np.array_equal(got, np.concatenate(want).astype(np.float32))
+
+
+def test_q4_0_dequant_closed_form():
+    rng = np.random.default_rng(2)
+    raw, want = b"", []
+    for _ in range(8):
+        d = np.float16(rng.uniform(-0.01, 0.01))
+        nib = rng.integers(0, 16, 32)
+        raw += _q4_block(d, nib)
+        want.append(np.float32(d) * (nib.astype(np.float32) - 8.0))
+    got = O.dequant_row(raw, 2, 256)
+    assert np.array_equal(got, np.concatenate(want).astype(np.float32))
+
+
+# ------------------------------------------------------------- ops -------
+def test_rms_norm_kat():
+    # tensor.rs:366-371
+    out = O.rms_norm([1.0, 2.0, 3.0, 4.0], [1.0, 0.5, 2.0, -1.0], 1e-6)
+    s = np.float32(1.0) / np.sqrt(np.float32(7.5) + np.float32(1e-6))
+    np.testing.assert_allclose(out, [s, s, 6 * s, -4 * s], atol=1e-6)
+
+
+def test_rms_norm_sequential_order():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(2560).astype(np.float32)
+    w = rng.standard_normal(2560).astype(np.float32)
+    ss = np.add.accumulate(x * x, dtype=np.float32)[-1]
+    scale = np.float32(1.0) / np.sqrt(ss / np.float32(2560) + np.float32(1e-6))
+    assert np.array_equal(O.rms_norm(x, w, 1e-6), (x * scale) * w)
+
+
+def test_linear_kat_f32_and_f16():
+    # backend.rs:208-215 and tensor.rs:373-391 ([out][in] layout)
+    w = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    assert np.array_equal(O.linear([2.0, -1.0], w.view(np.uint8), 0, 2, 3), [0.0, 2.0, 4.0])
+    assert np.array_equal(O.linear([2.0, -1.0], w.astype(np.float16).view(np.uint8), 1, 2, 3), [0.0, 2.0, 4.0])
+
+
+@pytest.mark.parametrize("gtype", [1, 8, 2])
+def test_linear_is_sequential_dot_over_dequantised_rows(gtype):
+    rng = np.random.default_rng(4)
+    in_dim, out_dim = 512, 48
+    wf = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
+    if gtype == 1:
+        raw = wf.astype(np.float16).view(np.uint8).ravel()
+    else:
+        raw = np.frombuffer(b"".join(synth.quantize_block(gtype, blk) for blk in wf.reshape(-1, 32)), np.uint8)
+    rows = O.dequant_row(raw.tobytes(), gtype, in_dim * out_dim).reshape(out_dim, in_dim)
+    x = rng.standard_normal(in_dim).astype(np.float32)
+    want = np.array([np.add.accumulate(x * r, dtype=np.float32)[-1] for r in rows], np.float32)
+    assert np.array_equal(O.linear(x, raw, gtype, in_dim, out_dim), want)
+
+
+def test_rope_kat():
+    # crates/fish_s2_infer/src/attention.rs:337-343
+    out = O.rope_normal([1.0, 0.0, 0.0, 1.0], 4, 1, 10000.0)
+    np.testing.assert_allclose(out, [math.cos(1), math.sin(1), -math.sin(0.01), math.cos(0.01)], atol=1e-5)
+
+
+def test_rope_closed_form_float64():
+    rng = np.random.default_rng(5)
+    hd, pos, base = 128, 37, 1.0e6
+    v = rng.standard_normal(4 * hd).astype(np.float32)
+    got = O.rope_normal(v, hd, pos, base)
+    x = v.astype(np.float64).reshape(4, hd // 2, 2)
+    th = pos / base ** (np.arange(0, hd, 2) / hd)
+    want = np.stack([x[..., 0] * np.cos(th) - x[..., 1] * np.sin(th),
+                     x[..., 0] * np.sin(th) + x[..., 1] * np.cos(th)], -1).ravel()
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+
+
+def test_gqa_attention_kat():
+    # attention.rs:362-406
+    q = [1.0, 0.0, 0.0, 1.0, 1.0, 0.0, 0.0, 1.0]
+    k = [1.0, 0.0, 0.0, 1.0, 0.0, 1.0, 1.0, 0.0]
+    v = [10.0, 0.0, 0.0, 10.0, 20.0, 0.0, 0.0, 20.0]
+    out = O.gqa_attention(q, k, v, 4, 2, 2, 2, 1.0)
+    ph = math.e / (math.e + 1)
+    pl = 1 - ph
+    np.testing.assert_allclose(out, [10 * ph + 20 * pl, 0, 10 * pl + 20 * ph, 0, 0, 10 * pl + 20 * ph, 0,
+                                     10 * ph + 20 * pl], atol=1e-5)
+
+
+def test_cached_attention_kat():
+    # attention.rs:408-428
+    out = O.gqa_attention([1.0, 0.0, 0.0, 1.0], [1.0, 0.0, 0.0, 1.0], [2.0, 0.0, 4.0, 0.0], 2, 1, 2, 2, 1.0)
+    ph = math.e / (math.e + 1)
+    pl = 1 - ph
+    np.testing.assert_allclose(out, [2 * ph + 4 * pl, 0, 2 * pl + 4 * ph, 0], atol=1e-5)
+
+
+def test_attention_matches_float64_softmax():
+    rng = np.random.default_rng(6)
+    H, Hkv, hd, T = 8, 2, 64, 37
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    k = rng.standard_normal(T * Hkv * hd).astype(np.float32)
+    v = rng.standard_normal(T * Hkv * hd).astype(np.float32)
+    got = O.gqa_attention(q, k, v, H, Hkv, hd, T, 1 / math.sqrt(hd))
+    q64, k64, v64 = q.reshape(H, hd), k.reshape(T, Hkv, hd), v.reshape(T, Hkv, hd)
+    want = []
+    for h in range(H):
+        g = h // (H // Hkv)
+        s = k64[:, g, :].astype(np.float64) @ q64[h] / math.sqrt(hd)
+        p = np.exp(s - s.max())
+        want.append((p / p.sum()) @ v64[:, g, :])
+    np.testing.assert_allclose(got, np.concatenate(want), atol=1e-5)
+
+
+def test_swiglu_kat_and_closed_form():
+    # slow_ar.rs:1518-1521
+    np.testing.assert_allclose(O.swiglu([0.0, 1.0], [2.0, 3.0]), [0.0, 3.0 / (1.0 + math.exp(-1.0))], atol=1e-6)
+    rng = np.random.default_rng(7)
+    g = rng.standard_normal(1000).astype(np.float32) * 4
+    u = rng.standard_normal(1000).astype(np.float32)
+    want = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64))) * u
+    np.testing.assert_allclose(O.swiglu(g, u), want, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(O.swiglu(g, u, fast=True), want, rtol=1e-6, atol=1e-6)
+
+
+# --------------------------------------------------------- sampling ------
+def test_lcg_closed_form():
+    # SeededRng (sampling.rs:34-52) in Python integers
+    s = 42
+    st = 42
+    for _ in range(100):
+        s = (s * 6364136223846793005 + 1) % (1 << 64)
+        want = ((s >> 11) & ((1 << 53) - 1)) / float(1 << 53)
+        got, st = O.next_unit(st)
+        assert got == want and st == s
+
+
+def test_sampler_kats():
+    # sampling.rs:276-328
+    assert O.sample_token([0.1, 5.0, 3.0, 2.0], 0.0, 1.0, 0, rng_state=1)[0] == 1
+    assert O.sample_token([10.0, 9.0, 8.0, 0.0], 0.0, 1.0, 2, rng_state=99)[0] <= 1
+    ninf = float("-inf")
+    assert O.sample_token([ninf] * 4 + [5.0], 0.0, 1.0, 1, always_include=4, rng_state=1)[0] == 4
+    a = O.sample_token([1.0, 3.0, 2.0, 0.5, 4.0], 0.8, 0.9, 3, rng_state=42)
+    b = O.sample_token([1.0, 3.0, 2.0, 0.5, 4.0], 0.8, 0.9, 3, rng_state=42)
+    assert a == b
+
+
+def test_greedy_tie_uses_the_draw():
+    # T=0 gives every value within 1e-6 of the max probability 1, so two
+    # tied maxima are chosen by the draw: u < 0.5 -> first (lower id).
+    for seed in range(20):
+        u, _ = O.next_unit(seed)
+        tok, st = O.sample_token([1.0, 5.0, 5.0, 2.0], 0.0, 1.0, 0, rng_state=seed)
+        assert tok == (1 if u < 0.5 else 2)
+        assert st == O.next_unit(seed)[1]
+
+
+def test_sampler_frequencies_follow_softmax():
+    logits = np.array([2.0, 1.0, 0.5, -1.0, 0.0], np.float32)
+    T = 0.7
+    p = np.exp((logits - logits.max()) / T)
+    p /= p.sum()
+    st = 7
+    counts = np.zeros(5)
+    n = 20000
+    for _ in range(n):
+        tok, st = O.sample_token(logits, T, 1.0, 0, rng_state=st)
+        counts[tok] += 1
+    np.testing.assert_allclose(counts / n, p, atol=0.015)
+
+
+def test_top_p_truncates_the_tail():
+    logits = np.array([3.0, 2.0, 1.0, 0.0, -1.0], np.float32)
+    st = 11
+    seen = set()
+    for _ in range(2000):
+        tok, st = O.sample_token(logits, 1.0, 0.5, 0, rng_state=st)
+        seen.add(tok)
+    # softmax(3,2,1,0,-1) = .636 .234 ..: top-p 0.5 keeps only the first item
+    assert seen == {0}
+
+
+def test_compact_and_transpose_kats():
+    # generate.rs:410-415, prompt.rs:289-303
+    assert O.compact_codes([10, 11, 0, 20, 21, 0], 2, 3, 2).tolist() == [10, 11, 20, 21]
+    assert O.transpose_to_time_major([10, 20, 1, 2, 3, 4], 3, 2).tolist() == [10, 1, 3, 20, 2, 4]
+
+
+# ----------------------------------------------------- model level -------
+TOY_WQKV = [[1, 0, 0, 0], [0, 0, 0, 0], [0, 0, 0, 0], [1, 0, 0, 0], [1, 0, 0, 0], [0, 0, 0, 0], [3, 0, 0, 0],
+            [0, 0, 0, 0]]
+TOY_WO = [[1, 0, 0, 0], [0, 0, 2, 0], [0, 0, 0, 0], [0, 0, 0, 0]]
+
+
+@pytest.fixture(scope="module")
+def toy_gguf(tmp_path_factory):
+    p = str(tmp_path_factory.mktemp("toy") / "toy.gguf")
+    gguf_util.toy_dual_ar(p, TOY_WQKV, TOY_WO, [0.5, 1, 1, 1], [1 / math.sqrt(2)] * 2)
+    return p
+
+
+def test_toy_layer_decode_kat(toy_gguf):
+    # slow_ar.rs:1283-1349: token [1,0,0,0] -> layer hidden [4,6,0,0]; the FFN
+    # is zero, and eval returns the final-RMSNorm'd hidden (eps 0, gains 1).
+    m = O.OracleModel(toy_gguf, 4, im_end_id=3)
+    hidden, logits = m.eval([0, 0])
+    np.testing.assert_allclose(hidden, np.array([4, 6, 0, 0]) / math.sqrt(13.0), atol=1e-6)
+    np.testing.assert_allclose(logits, [hidden[0], hidden[0] + hidden[1], 0, 0], atol=1e-6)
+
+
+def test_toy_decode_equals_prefill(toy_gguf):
+    # slow_ar.rs:1455-1493: a two-token prefill equals two single-token steps
+    a = O.OracleModel(toy_gguf, 4, im_end_id=3)
+    h_pre, l_pre = a.eval([0, 0, 1, 0])
+    b = O.OracleModel(toy_gguf, 4, im_end_id=3)
+    b.eval([0, 0])
+    h_dec, l_dec = b.eval([1, 0])
+    assert np.array_equal(h_pre, h_dec) and np.array_equal(l_pre, l_dec)
+    assert a.n_past == b.n_past == 2
+
+
+def test_kv_overflow_and_bad_token_errors(toy_gguf):
+    m = O.OracleModel(toy_gguf, 2, im_end_id=3)
+    with pytest.raises(RuntimeError, match="KV cache overflow"):
+        m.eval([0, 0, 1, 0, 0, 0])
+    with pytest.raises(RuntimeError, match="out of range"):
+        m.eval([9, 0])
+
+
+def test_tiny_fast_incremental_equals_recompute(tiny_gguf):
+    # Fast-AR without KV cache (fast_ar.rs:417-424) vs. the incremental form
+    prompt = make_prompt(synth.TINY, 8, seed=3)
+    inc = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    rec = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id, flags=O.FAITHFUL_FAST_RECOMPUTE)
+    h, _ = inc.eval(prompt)
+    for T, top_p, seed in ((0.0, 1.0, 0), (0.7, 0.9, 5)):
+        ci, si = inc.fast_codebooks(h, 17, T, top_p, 0, seed)
+        cr, sr = rec.fast_codebooks(h, 17, T, top_p, 0, seed)
+        assert np.array_equal(ci, cr) and si == sr
+
+
+def test_tiny_faithful_modes_give_identical_codes(tiny_gguf):
+    prompt = make_prompt(synth.TINY, 12, seed=4)
+    fast = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    faithful = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id,
+                             flags=O.FAITHFUL_FAST_RECOMPUTE | O.FAITHFUL_SLOW_RELOAD)
+    a = fast.generate_codes(prompt, 6, min_tokens_before_end=100)
+    b = faithful.generate_codes(prompt, 6, min_tokens_before_end=100)
+    assert np.array_equal(a["codes"], b["codes"]) and a["rng_state"] == b["rng_state"]
+    assert a["n_frames"] == 6
+
+
+def test_tiny_prefill_chunking_is_exact(tiny_gguf):
+    # one 10-token prefill == 10 single-token evals (the decode path)
+    prompt = make_prompt(synth.TINY, 10, seed=6)
+    a = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    ha, la = a.eval(prompt)
+    b = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    for t in range(10):
+        hb, lb = b.eval(prompt[t * 11:(t + 1) * 11])
+    assert np.array_equal(ha, hb) and np.array_equal(la, lb)
+
+
+def test_im_end_blocking_yields_exact_frame_count(tiny_gguf):
+    prompt = make_prompt(synth.TINY, 8, seed=9)
+    m = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    r = m.generate_codes(prompt, 5, min_tokens_before_end=10)
+    assert r["n_frames"] == 5 and r["codes"].shape == (10, 5)
+    # codebook 0 is the semantic code of each frame's main token
+    assert (r["codes"] >= 0).all() and (r["codes"] < synth.TINY.codebook_size).all()
