@@ -91,6 +91,7 @@ def main():
         max_seq = max(max_seq, prompt_len + frames)
     shape = synth.SHAPES[shape_name]
     t0 = time.time()
+    os.environ.setdefault("S2SYNTH_PROGRESS", "1")
     path = synth.ensure_gguf(shape, args.model_dir, threads=min(16, os.cpu_count() or 1))
     log(f"model {path} ready in {time.time() - t0:.1f}s")
     t0 = time.time()

@@ -161,7 +161,8 @@ class Engine {
   float *hn_ = nullptr, *logits_c_ = nullptr, *logits_full_ = nullptr;
   float *kc_ = nullptr, *vc_ = nullptr;
   float2 *rope_slow_ = nullptr, *rope_fast_ = nullptr;
-  uint32_t attn_chunk_ = 64, attn_chunks_ = 1;
+  uint32_t attn_chunks_ = 1;
+  uint32_t* counters_ = nullptr;
   float *fh_ = nullptr, *fqkv_ = nullptr, *fq_ = nullptr, *fatt_ = nullptr, *fpart_ = nullptr, *fact_ = nullptr;
   float *flogits_ = nullptr, *fkc_ = nullptr, *fvc_ = nullptr;
   uint32_t fctx_ = 11;
@@ -229,9 +230,10 @@ Engine::Engine(const s2hip_config& cfg) {
   if (fast_dim != s.dim) fail("fast embedding_length must equal the slow embedding_length");
   if (s.kv_heads == 0 || s.heads % s.kv_heads) fail("invalid GQA head split");
   if (s.fast_kv_heads == 0 || s.fast_heads % s.fast_kv_heads) fail("invalid fast GQA head split");
-  if (s.head_dim == 0 || s.head_dim % 4 || s.head_dim > 256 || s.fast_head_dim == 0 || s.fast_head_dim % 4 ||
-      s.fast_head_dim > 256)
-    fail("head_dim must be a non-zero multiple of 4 and at most 256");
+  if ((s.head_dim != 64 && s.head_dim != 128) || (s.fast_head_dim != 64 && s.fast_head_dim != 128))
+    fail("head_dim must be 64 or 128");
+  if (s.heads / s.kv_heads > 4 || s.fast_heads / s.fast_kv_heads > 4)
+    fail("at most 4 query heads per kv head are supported");
   if (s.num_codebooks == 0 || s.num_codebooks > 16) fail("num_codebooks must be in 1..16");
   if (s.semantic_end < s.semantic_begin) fail("invalid semantic id range");
   if (s.dim % 8) fail("embedding_length must be a multiple of 8");
@@ -303,13 +305,14 @@ Engine::Engine(const s2hip_config& cfg) {
   // activations
   const uint32_t NC = PREFILL_COLS;
   const uint64_t qkv_w = q + 2 * kv;
-  attn_chunk_ = 64u * ((s.max_seq_len + 64u * 16u - 1u) / (64u * 16u));
-  attn_chunks_ = (s.max_seq_len + attn_chunk_ - 1) / attn_chunk_;
+  attn_chunks_ = (s.max_seq_len + 63) / 64;
   h_ = dalloc<float>(size_t(NC) * s.dim);
   qkv_ = dalloc<float>(size_t(NC) * qkv_w);
   q_ = dalloc<float>(size_t(NC) * q);
   att_ = dalloc<float>(size_t(NC) * q);
   part_ = dalloc<float>(size_t(NC) * s.heads * attn_chunks_ * (s.head_dim + 2));
+  counters_ = dalloc<uint32_t>(size_t(NC) * std::max(s.kv_heads, s.fast_kv_heads));
+  HIPC(hipMemset(counters_, 0, size_t(NC) * std::max(s.kv_heads, s.fast_kv_heads) * 4));
   act_ = dalloc<float>(size_t(NC) * s.ffn);
   hn_ = dalloc<float>(s.dim);
   logits_c_ = dalloc<float>(n_cand_);
@@ -328,7 +331,7 @@ Engine::Engine(const s2hip_config& cfg) {
   fqkv_ = dalloc<float>(2 * (fq + 2 * fkv));
   fq_ = dalloc<float>(2 * fq);
   fatt_ = dalloc<float>(2 * fq);
-  fpart_ = dalloc<float>(2 * size_t(s.fast_heads) * 1 * (s.fast_head_dim + 2));
+  fpart_ = dalloc<float>(2 * size_t(s.fast_heads) * ((fctx_ + 63) / 64) * (s.fast_head_dim + 2));
   fact_ = dalloc<float>(2 * size_t(s.fast_ffn));
   flogits_ = dalloc<float>(s.codebook_size);
   fkc_ = dalloc<float>(size_t(s.fast_layers) * fkv * fctx_);
@@ -470,30 +473,16 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
   for (uint32_t l = 0; l < s.slow_layers; ++l) {
     const SlowLayer& L = slow_[l];
     gemv(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, nullptr, L.wqkv.out, done);
-    QkvPostArgs pa{};
-    pa.qkv = qkv_;
-    pa.q_out = q_;
-    pa.k_cache = kc_ + size_t(l) * kv * s.max_seq_len;
-    pa.v_cache = vc_ + size_t(l) * kv * s.max_seq_len;
-    pa.q_norm = L.q_norm;
-    pa.k_norm = L.k_norm;
-    pa.rope = rope_slow_;
-    pa.pos_ptr = &st_->n_past;
-    pa.pos_offset = 0;
-    pa.H = s.heads;
-    pa.Hkv = s.kv_heads;
-    pa.hd = s.head_dim;
-    pa.max_seq = s.max_seq_len;
-    pa.ncol = ncol;
-    pa.eps = s.eps;
-    pa.done = done;
-    pa.err = &st_->err;
-    HIPC(launch_qkv_post(pa, stream_));
     AttnArgs aa{};
-    aa.q = q_;
-    aa.k_cache = pa.k_cache;
-    aa.v_cache = pa.v_cache;
+    aa.qkv = qkv_;
+    aa.q_norm = L.q_norm;
+    aa.k_norm = L.k_norm;
+    aa.eps = s.eps;
+    aa.rope = rope_slow_;
+    aa.k_cache = kc_ + size_t(l) * kv * s.max_seq_len;
+    aa.v_cache = vc_ + size_t(l) * kv * s.max_seq_len;
     aa.part = part_;
+    aa.counters = counters_;
     aa.out = att_;
     aa.pos_ptr = &st_->n_past;
     aa.pos_offset = 0;
@@ -502,10 +491,10 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
     aa.hd = s.head_dim;
     aa.max_seq = s.max_seq_len;
     aa.ncol = ncol;
-    aa.chunk = attn_chunk_;
     aa.max_chunks = attn_chunks_;
     aa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
     aa.done = done;
+    aa.err = &st_->err;
     HIPC(launch_attention(aa, stream_));
     gemv(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, nullptr, L.wo.out, done);
     gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, nullptr, L.w1.out, done);
@@ -532,30 +521,16 @@ void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* don
   for (uint32_t l = 0; l < s.fast_layers; ++l) {
     const FastLayer& L = fast_[l];
     gemv(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, nullptr, L.wqkv.out, done);
-    QkvPostArgs pa{};
-    pa.qkv = fqkv_;
-    pa.q_out = fq_;
-    pa.k_cache = fkc_ + size_t(l) * fkv * fctx_;
-    pa.v_cache = fvc_ + size_t(l) * fkv * fctx_;
-    pa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
-    pa.k_norm = nullptr;
-    pa.rope = rope_fast_;
-    pa.pos_ptr = nullptr;
-    pa.pos_offset = p0;
-    pa.H = s.fast_heads;
-    pa.Hkv = s.fast_kv_heads;
-    pa.hd = s.fast_head_dim;
-    pa.max_seq = fctx_;
-    pa.ncol = ncol;
-    pa.eps = s.fast_eps;
-    pa.done = done;
-    pa.err = &st_->err;
-    HIPC(launch_qkv_post(pa, stream_));
     AttnArgs aa{};
-    aa.q = fq_;
-    aa.k_cache = pa.k_cache;
-    aa.v_cache = pa.v_cache;
+    aa.qkv = fqkv_;
+    aa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
+    aa.k_norm = nullptr;
+    aa.eps = s.fast_eps;
+    aa.rope = rope_fast_;
+    aa.k_cache = fkc_ + size_t(l) * fkv * fctx_;
+    aa.v_cache = fvc_ + size_t(l) * fkv * fctx_;
     aa.part = fpart_;
+    aa.counters = counters_;
     aa.out = fatt_;
     aa.pos_ptr = nullptr;
     aa.pos_offset = p0;
@@ -564,10 +539,10 @@ void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* don
     aa.hd = s.fast_head_dim;
     aa.max_seq = fctx_;
     aa.ncol = ncol;
-    aa.chunk = 64;
-    aa.max_chunks = 1;
+    aa.max_chunks = (fctx_ + 63) / 64;
     aa.scale = 1.0f / std::sqrt(float(s.fast_head_dim));  // fast_ar.rs:60-62
     aa.done = done;
+    aa.err = &st_->err;
     HIPC(launch_attention(aa, stream_));
     gemv(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, nullptr, L.wo.out, done);
     gemv(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, nullptr,
@@ -822,7 +797,7 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
   init.min_tokens_before_end = p.min_tokens_before_end;
   *st_host_ = init;
   HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
-  HIPC(hipMemsetAsync(codes_dev_, 0, ncodes * 4 + 4, stream_));
+  if (ncodes) HIPC(hipMemsetAsync(codes_dev_, 0, ncodes * 4, stream_));
   HIPC(hipMemcpyAsync(prompt_dev_, prompt, cols * cdim * 4, hipMemcpyHostToDevice, stream_));
   hipEvent_t ev[3];
   for (auto& e : ev) HIPC(hipEventCreate(&e));
@@ -842,7 +817,10 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
   HIPC(launch_sample_slow(sa, stream_));
   HIPC(hipEventRecord(ev[1], stream_));
 
-  const uint32_t max_frames = std::min<uint32_t>(p.max_new_tokens, s.max_seq_len - uint32_t(cols));
+  // No cap at the KV capacity: a frame that would write past max_seq_len sets
+  // ERR_KV_OVERFLOW on the device and the call fails, as SlowArState::eval does
+  // (slow_ar.rs:469-474).
+  const uint32_t max_frames = p.max_new_tokens;
   bool use_graph = !(flags_ & S2HIP_FLAG_NO_GRAPH);
   uint32_t launched = 0;
   if (max_frames > 0) {
@@ -1019,11 +997,15 @@ void Engine::op_qk_rope(const float* qkv, uint32_t H, uint32_t Hkv, uint32_t hd,
   HIPC(hipStreamSynchronize(stream_));
 }
 
+// gqa_decode_attention through the fused decode kernel: the last token's
+// k/v and the query travel in a qkv row (no QK-norm, identity rotation),
+// earlier tokens come from the cache.
 void Engine::op_attention(const float* q, const float* k, const float* v, uint32_t H, uint32_t Hkv, uint32_t hd,
                           uint32_t T, float scale, float* out) {
   select();
   if (Hkv == 0 || H % Hkv) fail("invalid GQA split");
-  if (hd == 0 || T == 0 || hd % 4 || hd > 256) fail("invalid attention dims");
+  if (T == 0) fail("invalid attention dims");
+  if ((hd != 64 && hd != 128) || H / Hkv > 4) fail("attention shape not supported on the device");
   // reference layout [token][kv_head][hd] -> cache layout [kv_head][token][hd]
   std::vector<float> kc(size_t(Hkv) * T * hd), vc(kc.size());
   for (uint32_t t = 0; t < T; ++t)
@@ -1032,17 +1014,28 @@ void Engine::op_attention(const float* q, const float* k, const float* v, uint32
         kc[(size_t(g) * T + t) * hd + d] = k[(size_t(t) * Hkv + g) * hd + d];
         vc[(size_t(g) * T + t) * hd + d] = v[(size_t(t) * Hkv + g) * hd + d];
       }
-  const uint32_t chunk = 64, nch = (T + chunk - 1) / chunk;
-  TmpBuf dq(size_t(H) * hd * 4), dk(kc.size() * 4), dv(vc.size() * 4), dpart(size_t(H) * nch * (hd + 2) * 4),
-      dout(size_t(H) * hd * 4);
-  HIPC(hipMemcpyAsync(dq.p, q, size_t(H) * hd * 4, hipMemcpyHostToDevice, stream_));
+  const size_t width = size_t(H + 2 * Hkv) * hd;
+  std::vector<float> row(width);
+  memcpy(row.data(), q, size_t(H) * hd * 4);
+  memcpy(row.data() + size_t(H) * hd, k + size_t(T - 1) * Hkv * hd, size_t(Hkv) * hd * 4);
+  memcpy(row.data() + size_t(H + Hkv) * hd, v + size_t(T - 1) * Hkv * hd, size_t(Hkv) * hd * 4);
+  std::vector<float2> rope(size_t(T) * (hd / 2), make_float2(1.0f, 0.0f));
+  const uint32_t nch = (T + 63) / 64;
+  TmpBuf drow(width * 4), dk(kc.size() * 4), dv(vc.size() * 4), dpart(size_t(Hkv) * nch * (H / Hkv) * (hd + 2) * 4),
+      dout(size_t(H) * hd * 4), drope(rope.size() * sizeof(float2)), dctr(size_t(Hkv) * 4);
+  HIPC(hipMemcpyAsync(drow.p, row.data(), width * 4, hipMemcpyHostToDevice, stream_));
   HIPC(hipMemcpyAsync(dk.p, kc.data(), kc.size() * 4, hipMemcpyHostToDevice, stream_));
   HIPC(hipMemcpyAsync(dv.p, vc.data(), vc.size() * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(drope.p, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemsetAsync(dctr.p, 0, size_t(Hkv) * 4, stream_));
   AttnArgs aa{};
-  aa.q = dq.as<float>();
+  aa.qkv = drow.as<float>();
+  aa.eps = 0.0f;
+  aa.rope = drope.as<float2>();
   aa.k_cache = dk.as<float>();
   aa.v_cache = dv.as<float>();
   aa.part = dpart.as<float>();
+  aa.counters = dctr.as<uint32_t>();
   aa.out = dout.as<float>();
   aa.pos_ptr = nullptr;
   aa.pos_offset = T - 1;
@@ -1051,7 +1044,6 @@ void Engine::op_attention(const float* q, const float* k, const float* v, uint32
   aa.hd = hd;
   aa.max_seq = T;
   aa.ncol = 1;
-  aa.chunk = chunk;
   aa.max_chunks = nch;
   aa.scale = scale;
   HIPC(launch_attention(aa, stream_));

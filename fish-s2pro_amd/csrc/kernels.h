@@ -82,21 +82,29 @@ struct QkvPostArgs {
 };
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 
-// Split-T GQA decode attention for `ncol` query positions; column c sees
-// T_c = *pos_ptr + pos_offset + c + 1 cache positions.
+// Fused decode attention for `ncol` consecutive query positions starting at
+// *pos_ptr + pos_offset: QK-norm (optional) + RoPE of q and of the new k,
+// KV append at the position, split-T GQA attention over positions
+// [0, pos] and the cross-chunk combine.  qkv: [ncol][(H + 2 Hkv) hd] raw
+// wqkv output.  hd must be 64 or 128 and H / Hkv <= 4.
 struct AttnArgs {
-  const float* q;          // [ncol][H hd]
-  const float* k_cache;    // [Hkv][max_seq][hd]
-  const float* v_cache;
-  float* part;             // [ncol][H][max_chunks][hd + 2]
+  const float* qkv;
+  const float* q_norm;     // nullable
+  const float* k_norm;     // nullable
+  float eps;
+  const float2* rope;      // [max_pos][hd/2] (cos, sin)
+  float* k_cache;          // [Hkv][max_seq][hd] for this layer
+  float* v_cache;
+  float* part;             // [ncol][Hkv][max_chunks][rep][hd + 2]
+  uint32_t* counters;      // [ncol][Hkv], zero between launches
   float* out;              // [ncol][H hd]
-  const uint32_t* pos_ptr;
+  const uint32_t* pos_ptr; // nullable
   uint32_t pos_offset;
   uint32_t H, Hkv, hd, max_seq, ncol;
-  uint32_t chunk;          // positions per work-group (multiple of 64)
-  uint32_t max_chunks;
+  uint32_t max_chunks;     // ceil(max_seq / 64)
   float scale;
   const uint32_t* done;
+  uint32_t* err;
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 

@@ -43,84 +43,135 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
 __device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
 
 // ---------------------------------------------------------------------------
-// Weight decode: 8 consecutive elements [e, e+8) of one row.
+// Raw weight payload for 8 consecutive elements, loaded first and decoded
+// later so a wave can keep many independent 16-byte loads in flight.
 // ---------------------------------------------------------------------------
 template <uint32_t WT>
-__device__ __forceinline__ void load_w8(const uint8_t* row, uint32_t e, float w[8]);
-
+struct Raw8 {
+  uint32_t d, w0, w1, w2;  // Q8_0 / Q4_0: d bits | shift << 16 | part << 20; aligned 12-byte window
+};
 template <>
-__device__ __forceinline__ void load_w8<W_F16>(const uint8_t* row, uint32_t e, float w[8]) {
-  const half8 v = *reinterpret_cast<const half8*>(row + size_t(e) * 2);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) w[i] = static_cast<float>(v[i]);
+struct Raw8<W_F16> {
+  half8 v;
+};
+
+template <uint32_t WT>
+__device__ __forceinline__ Raw8<WT> load_raw(const uint8_t* row, uint32_t e) {
+  Raw8<WT> r;
+  if constexpr (WT == W_F16) {
+    r.v = *reinterpret_cast<const half8*>(row + size_t(e) * 2);
+  } else {
+    constexpr uint32_t BB = (WT == W_Q8_0) ? 34u : 18u;
+    const uint32_t b = e >> 5, p = (e >> 3) & 3u;
+    const uint8_t* blk = row + size_t(b) * BB;
+    const uint32_t qoff = (WT == W_Q8_0) ? 2 + p * 8 : 2 + (p & 1u) * 8;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(blk + qoff);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
+    r.d = uint32_t(*reinterpret_cast<const uint16_t*>(blk)) | (uint32_t(a & 3u) << 16) | (p << 20);
+    r.w0 = base[0];
+    r.w1 = base[1];
+    r.w2 = base[2];
+  }
+  return r;
 }
 
-// Q8_0 block (34 B): f16 d, int8 q[32].  Lane part p = (e/8)%4 covers q[8p, 8p+8).
-// The 8 quant bytes start at an address that is 0 or 2 mod 4: read the
-// enclosing aligned 12-byte window and funnel-shift.  Allocations carry
-// trailing padding so the window never leaves the buffer.
-template <>
-__device__ __forceinline__ void load_w8<W_Q8_0>(const uint8_t* row, uint32_t e, float w[8]) {
-  const uint32_t b = e >> 5, p = (e >> 3) & 3u;
-  const uint8_t* blk = row + size_t(b) * 34;
-  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
-  const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2 + p * 8);
-  const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-  const uint32_t sh = uint32_t(a & 3u);
-  const uint32_t w0 = base[0], w1 = base[1], w2 = base[2];
-  const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
-  const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+template <uint32_t WT>
+__device__ __forceinline__ void decode8(const Raw8<WT>& r, float w[8]) {
+  if constexpr (WT == W_F16) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[i] = static_cast<float>(static_cast<int8_t>((lo >> (8 * i)) & 0xffu)) * d;
-    w[4 + i] = static_cast<float>(static_cast<int8_t>((hi >> (8 * i)) & 0xffu)) * d;
+    for (int i = 0; i < 8; ++i) w[i] = static_cast<float>(r.v[i]);
+  } else {
+    const float d = half_bits_to_float(uint16_t(r.d & 0xffffu));
+    const uint32_t sh = (r.d >> 16) & 3u, p = (r.d >> 20) & 3u;
+    const uint32_t lo = __builtin_amdgcn_alignbyte(r.w1, r.w0, sh);
+    const uint32_t hi = __builtin_amdgcn_alignbyte(r.w2, r.w1, sh);
+    if constexpr (WT == W_Q8_0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w[i] = static_cast<float>(static_cast<int8_t>((lo >> (8 * i)) & 0xffu)) * d;
+        w[4 + i] = static_cast<float>(static_cast<int8_t>((hi >> (8 * i)) & 0xffu)) * d;
+      }
+    } else {
+      const uint32_t ns = (p >= 2) ? 4u : 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w[i] = static_cast<float>(int((lo >> (8 * i + ns)) & 0xfu) - 8) * d;
+        w[4 + i] = static_cast<float>(int((hi >> (8 * i + ns)) & 0xfu) - 8) * d;
+      }
+    }
   }
 }
 
-// Q4_0 block (18 B): f16 d, u8 qs[16]; element j<16 is the low nibble of
-// qs[j], element 16+j the high nibble.  Part p reads qs[8(p&1), +8) and takes
-// low nibbles for p<2, high nibbles for p>=2; x = (nibble - 8) * d.
-template <>
-__device__ __forceinline__ void load_w8<W_Q4_0>(const uint8_t* row, uint32_t e, float w[8]) {
-  const uint32_t b = e >> 5, p = (e >> 3) & 3u;
-  const uint8_t* blk = row + size_t(b) * 18;
-  const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
-  const uintptr_t a = reinterpret_cast<uintptr_t>(blk + 2 + (p & 1u) * 8);
-  const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-  const uint32_t sh = uint32_t(a & 3u);
-  const uint32_t w0 = base[0], w1 = base[1], w2 = base[2];
-  const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
-  const uint32_t hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
-  const uint32_t nshift = (p >= 2) ? 4u : 0u;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    w[i] = static_cast<float>(int((lo >> (8 * i + nshift)) & 0xfu) - 8) * d;
-    w[4 + i] = static_cast<float>(int((hi >> (8 * i + nshift)) & 0xfu) - 8) * d;
-  }
+template <uint32_t WT>
+__device__ __forceinline__ void load_w8(const uint8_t* row, uint32_t e, float w[8]) {
+  decode8<WT>(load_raw<WT>(row, e), w);
 }
 
 // ---------------------------------------------------------------------------
 // GEMV: y[c][o] (+)= sum_i x[c][i] * W[o][i]
-//   block = 4 waves, each wave owns R consecutive output rows; lanes stride
-//   the row 8 elements (16 B of f16) at a time.  x (optionally RMS-normalised)
-//   is staged once per block in LDS.
+//   block = 4 waves; each wave owns R consecutive output rows and each lane
+//   handles 8 consecutive elements per 512-element step.  The first batch of
+//   PF steps of weight loads is issued before x is staged (and optionally
+//   RMS-normalised) in LDS, so the x prologue hides under HBM latency.
 // ---------------------------------------------------------------------------
 template <uint32_t WT, int NCOL, int R, int EPI>
 __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
   if (a.done && *a.done) return;
   extern __shared__ float xs[];  // [NCOL][in]
   __shared__ float red[GEMV_WAVES][NCOL];
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr int PF = 16 / (R * (DUAL ? 2 : 1) * (NCOL > 2 ? 2 : 1));
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
   const uint32_t in = a.in;
+  const uint32_t kit = (in + WAVE * 8 - 1) / (WAVE * 8);
 
+  const uint32_t row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
+  const uint8_t* rp[R];
+  const uint8_t* rp3[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t lr = row0 + r;
+    if (lr >= a.out) lr = 0;  // clamp; result discarded
+    const uint32_t wr = a.row_map ? a.row_map[lr] : lr;
+    rp[r] = a.w + size_t(wr) * a.row_bytes;
+    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  }
+
+  Raw8<WT> wb[R][PF];
+  Raw8<WT> wb3[DUAL ? R : 1][PF];
+  auto load_batch = [&](uint32_t it0) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+      const uint32_t e = (it0 + j) * (WAVE * 8) + lane * 8;
+      if (it0 + j < kit && e < in) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          wb[r][j] = load_raw<WT>(rp[r], e);
+          if constexpr (DUAL) wb3[r][j] = load_raw<WT>(rp3[r], e);
+        }
+      }
+    }
+  };
+  load_batch(0);
+
+  // stage x (16-byte loads), with the RMSNorm sum of squares on the way
+  const bool vec = (in % 4 == 0) && (a.ldx % 4 == 0);
 #pragma unroll
   for (int c = 0; c < NCOL; ++c) {
     const float* xc = a.x + size_t(c) * a.ldx;
     float ss = 0.0f;
-    for (uint32_t i = tid; i < in; i += GEMV_THREADS) {
-      const float v = xc[i];
-      xs[c * in + i] = v;
-      ss += v * v;
+    if (vec) {
+      for (uint32_t i = tid * 4; i < in; i += GEMV_THREADS * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(xc + i);
+        *reinterpret_cast<float4*>(&xs[c * in + i]) = v;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+    } else {
+      for (uint32_t i = tid; i < in; i += GEMV_THREADS) {
+        const float v = xc[i];
+        xs[c * in + i] = v;
+        ss += v * v;
+      }
     }
     if (a.norm) {
       ss = wave_sum(ss);
@@ -139,18 +190,6 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
   }
   __syncthreads();
 
-  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
-  const uint32_t row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
-  const uint8_t* rp[R];
-  const uint8_t* rp3[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    uint32_t lr = row0 + r;
-    if (lr >= a.out) lr = 0;  // clamp; result discarded
-    const uint32_t wr = a.row_map ? a.row_map[lr] : lr;
-    rp[r] = a.w + size_t(wr) * a.row_bytes;
-    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
-  }
   float acc[R][NCOL];
   float acc3[R][NCOL];
 #pragma unroll
@@ -161,29 +200,32 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
       acc3[r][c] = 0.0f;
     }
 
-#pragma unroll 2
-  for (uint32_t base = 0; base < in; base += WAVE * 8) {
-    const uint32_t e = base + lane * 8;
-    if (e < in) {
-      float w[R][8];
-      float w3[DUAL ? R : 1][8];
+  for (uint32_t it0 = 0; it0 < kit; it0 += PF) {
+    if (it0 > 0) load_batch(it0);
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        load_w8<WT>(rp[r], e, w[r]);
-        if constexpr (DUAL) load_w8<WT>(rp3[r], e, w3[r]);
-      }
-#pragma unroll
-      for (int c = 0; c < NCOL; ++c) {
-        const float4 xa = *reinterpret_cast<const float4*>(&xs[c * in + e]);
-        const float4 xb = *reinterpret_cast<const float4*>(&xs[c * in + e + 4]);
-        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    for (int j = 0; j < PF; ++j) {
+      const uint32_t e = (it0 + j) * (WAVE * 8) + lane * 8;
+      if (it0 + j < kit && e < in) {
+        float w[R][8];
+        float w3[DUAL ? R : 1][8];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
+          decode8<WT>(wb[r][j], w[r]);
+          if constexpr (DUAL) decode8<WT>(wb3[r][j], w3[r]);
+        }
 #pragma unroll
-          for (int k = 0; k < 8; ++k) acc[r][c] = fmaf(w[r][k], xv[k], acc[r][c]);
-          if constexpr (DUAL) {
+        for (int c = 0; c < NCOL; ++c) {
+          const float4 xa = *reinterpret_cast<const float4*>(&xs[c * in + e]);
+          const float4 xb = *reinterpret_cast<const float4*>(&xs[c * in + e + 4]);
+          const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-            for (int k = 0; k < 8; ++k) acc3[r][c] = fmaf(w3[r][k], xv[k], acc3[r][c]);
+          for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[r][c] = fmaf(w[r][k], xv[k], acc[r][c]);
+            if constexpr (DUAL) {
+#pragma unroll
+              for (int k = 0; k < 8; ++k) acc3[r][c] = fmaf(w3[r][k], xv[k], acc3[r][c]);
+            }
           }
         }
       }
@@ -233,7 +275,8 @@ hipError_t gemv_launch_one(const GemvArgs& a, hipStream_t s) {
 
 template <uint32_t WT, int NCOL, int EPI>
 hipError_t gemv_pick_r(const GemvArgs& a, hipStream_t s) {
-  if (NCOL == 1 && a.out > 4096) return gemv_launch_one<WT, NCOL, 2, EPI>(a, s);
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  if (NCOL == 1 && !DUAL && a.out > 4096) return gemv_launch_one<WT, NCOL, 2, EPI>(a, s);
   return gemv_launch_one<WT, NCOL, 1, EPI>(a, s);
 }
 
@@ -260,6 +303,179 @@ hipError_t gemv_pick_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode GEMV (1-2 input columns): every weight load of a wave's R rows is
+// issued up front (predicated on the runtime step count, at most KMAX
+// 512-element steps per row), x and the RMSNorm gain are read through the
+// L1 cache, and the only block-level synchronisation is the RMSNorm scale.
+// ---------------------------------------------------------------------------
+template <uint32_t WT, int NCOL, int R, int EPI, int KMAX>
+__global__ __launch_bounds__(GEMV_THREADS) void gemv_direct_kernel(GemvArgs a) {
+  if (a.done && *a.done) return;
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  __shared__ float red[GEMV_WAVES][NCOL];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+  const uint32_t in = a.in;
+  const uint32_t kit = in / (WAVE * 8);  // host guarantees in % 512 == 0
+  const uint32_t row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
+
+  const uint8_t* rp[R];
+  const uint8_t* rp3[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t lr = row0 + r;
+    if (lr >= a.out) lr = 0;  // clamp; result discarded
+    const uint32_t wr = a.row_map ? a.row_map[lr] : lr;
+    rp[r] = a.w + size_t(wr) * a.row_bytes;
+    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  }
+  Raw8<WT> wb[R][KMAX];
+  Raw8<WT> wb3[DUAL ? R : 1][KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    if (k < kit) {
+      const uint32_t e = k * (WAVE * 8) + lane * 8;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        wb[r][k] = load_raw<WT>(rp[r], e);
+        if constexpr (DUAL) wb3[r][k] = load_raw<WT>(rp3[r], e);
+      }
+    }
+  }
+
+  float scale[NCOL];
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) scale[c] = 1.0f;
+  if (a.norm) {
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float* xc = a.x + size_t(c) * a.ldx;
+      float ss = 0.0f;
+      for (uint32_t i = tid * 4; i < in; i += GEMV_THREADS * 4) {
+        const float4 v = *reinterpret_cast<const float4*>(xc + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave][c] = ss;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float tot = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
+      scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(in)), a.eps)));
+    }
+  }
+
+  float acc[R][NCOL];
+  float acc3[R][NCOL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      acc[r][c] = 0.0f;
+      acc3[r][c] = 0.0f;
+    }
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    if (k < kit) {
+      const uint32_t e = k * (WAVE * 8) + lane * 8;
+      float w[R][8];
+      float w3[DUAL ? R : 1][8];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        decode8<WT>(wb[r][k], w[r]);
+        if constexpr (DUAL) decode8<WT>(wb3[r][k], w3[r]);
+      }
+      float g[8];
+      if (a.norm) {
+        const float4 ga = *reinterpret_cast<const float4*>(a.norm + e);
+        const float4 gb = *reinterpret_cast<const float4*>(a.norm + e + 4);
+        g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w;
+        g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
+      }
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) {
+        const float* xc = a.x + size_t(c) * a.ldx + e;
+        const float4 xa = *reinterpret_cast<const float4*>(xc);
+        const float4 xb = *reinterpret_cast<const float4*>(xc + 4);
+        float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        if (a.norm) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) xv[i] = __fmul_rn(__fmul_rn(xv[i], scale[c]), g[i]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[r][c] = fmaf(w[r][i], xv[i], acc[r][c]);
+          if constexpr (DUAL) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc3[r][c] = fmaf(w3[r][i], xv[i], acc3[r][c]);
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float gsum = wave_sum(acc[r][c]);
+      float u = 0.0f;
+      if constexpr (DUAL) u = wave_sum(acc3[r][c]);
+      const uint32_t lr = row0 + r;
+      if (lane == 0 && lr < a.out) {
+        float* dst = a.y + size_t(c) * a.ldy + lr;
+        if constexpr (EPI == EPI_STORE) {
+          *dst = gsum;
+        } else if constexpr (EPI == EPI_RESID) {
+          *dst = __fadd_rn(*dst, gsum);
+        } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+          *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
+        } else {
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+        }
+      }
+    }
+  }
+}
+
+template <uint32_t WT, int NCOL, int R, int EPI, int KMAX>
+hipError_t gemv_direct_launch(const GemvArgs& a, hipStream_t s) {
+  const uint32_t rows_per_block = GEMV_WAVES * R;
+  const dim3 grid((a.out + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL((gemv_direct_kernel<WT, NCOL, R, EPI, KMAX>), grid, dim3(GEMV_THREADS), 0, s, a);
+  return hipGetLastError();
+}
+
+template <uint32_t WT, int NCOL, int EPI>
+hipError_t gemv_direct_pick(const GemvArgs& a, hipStream_t s) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  if (a.in <= 8 * 512) {
+    if (!DUAL && NCOL == 1 && a.out > 4096) return gemv_direct_launch<WT, NCOL, 2, EPI, 8>(a, s);
+    return gemv_direct_launch<WT, NCOL, 1, EPI, 8>(a, s);
+  }
+  return gemv_direct_launch<WT, NCOL, 1, EPI, 20>(a, s);
+}
+
+template <uint32_t WT, int EPI>
+hipError_t gemv_direct_ncol(int ncol, const GemvArgs& a, hipStream_t s) {
+  if (ncol == 1) return gemv_direct_pick<WT, 1, EPI>(a, s);
+  return gemv_direct_pick<WT, 2, EPI>(a, s);
+}
+
+template <uint32_t WT>
+hipError_t gemv_direct_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: return gemv_direct_ncol<WT, EPI_STORE>(ncol, a, s);
+    case EPI_RESID: return gemv_direct_ncol<WT, EPI_RESID>(ncol, a, s);
+    case EPI_SWIGLU_SLOW: return gemv_direct_ncol<WT, EPI_SWIGLU_SLOW>(ncol, a, s);
+    case EPI_SWIGLU_FAST: return gemv_direct_ncol<WT, EPI_SWIGLU_FAST>(ncol, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // RMSNorm over `ncol` vectors (one block per column).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const float* w, float* y, uint32_t n,
@@ -279,8 +495,32 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const flo
 }
 
 // ---------------------------------------------------------------------------
-// QK-norm + RoPE + KV append.  One wave per head; grid (H + 2 Hkv, ncol).
+// Per-head QK-norm (optional) + NORMAL RoPE for one wave: pairs (2p, 2p+1)
+// rotated by the host-built (cos, sin) row of the position.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ void head_norm_rope(const float* src, const float* norm, float eps,
+                                               const float2* rope_row, uint32_t hd, uint32_t lane, float* dst) {
+  float scale = 1.0f;
+  if (norm) {
+    float ss = 0.0f;
+    for (uint32_t i = lane; i < hd; i += 64) ss += src[i] * src[i];
+    ss = wave_sum(ss);
+    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(hd)), eps)));
+  }
+  for (uint32_t p = lane; p < hd / 2; p += 64) {
+    float x0 = src[2 * p], x1 = src[2 * p + 1];
+    if (norm) {
+      x0 = __fmul_rn(__fmul_rn(x0, scale), norm[2 * p]);
+      x1 = __fmul_rn(__fmul_rn(x1, scale), norm[2 * p + 1]);
+    }
+    const float cs = rope_row[p].x, sn = rope_row[p].y;
+    dst[2 * p] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
+    dst[2 * p + 1] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+  }
+}
+
+// QK-norm + RoPE + KV append as a standalone step (one wave per head; grid
+// (H + 2 Hkv, ncol)); the decode path fuses the same math into attention.
 __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
   if (a.done && *a.done) return;
   const uint32_t hi = blockIdx.x, col = blockIdx.y, lane = threadIdx.x;
@@ -291,138 +531,170 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
   }
   const uint32_t hd = a.hd, width = (a.H + 2 * a.Hkv) * hd;
   const float* src = a.qkv + size_t(col) * width + size_t(hi) * hd;
-  float* dst;
-  const float* norm;
+  const float2* rope_row = a.rope + size_t(pos) * (hd / 2);
   if (hi < a.H) {
-    dst = a.q_out + size_t(col) * a.H * hd + size_t(hi) * hd;
-    norm = a.q_norm;
+    head_norm_rope(src, a.q_norm, a.eps, rope_row, hd, lane, a.q_out + size_t(col) * a.H * hd + size_t(hi) * hd);
   } else if (hi < a.H + a.Hkv) {
-    dst = a.k_cache + (size_t(hi - a.H) * a.max_seq + pos) * hd;
-    norm = a.k_norm;
+    head_norm_rope(src, a.k_norm, a.eps, rope_row, hd, lane, a.k_cache + (size_t(hi - a.H) * a.max_seq + pos) * hd);
   } else {
     float* vd = a.v_cache + (size_t(hi - a.H - a.Hkv) * a.max_seq + pos) * hd;
     for (uint32_t i = lane; i < hd; i += 64) vd[i] = src[i];
-    return;
-  }
-  float scale = 1.0f;
-  if (norm) {
-    float ss = 0.0f;
-    for (uint32_t i = lane; i < hd; i += 64) ss += src[i] * src[i];
-    ss = wave_sum(ss);
-    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(hd)), a.eps)));
-  }
-  const float2* rope = a.rope + size_t(pos) * (hd / 2);
-  for (uint32_t p = lane; p < hd / 2; p += 64) {
-    float x0 = src[2 * p], x1 = src[2 * p + 1];
-    if (norm) {
-      x0 = __fmul_rn(__fmul_rn(x0, scale), norm[2 * p]);
-      x1 = __fmul_rn(__fmul_rn(x1, scale), norm[2 * p + 1]);
-    }
-    const float cs = rope[p].x, sn = rope[p].y;
-    dst[2 * p] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-    dst[2 * p + 1] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
   }
 }
 
 // ---------------------------------------------------------------------------
-// Split-T decode attention.  grid (max_chunks, Hkv, ncol); 4 waves per block,
-// wave w serves q heads g*rep + w, + 4, ...  Scores: one lane per cache
-// position; PV: one lane per head-dim element.  Writes per-chunk (m, l, o).
+// Fused decode attention for one layer: QK-norm + RoPE of the new position,
+// KV append, split-T GQA attention and the cross-chunk combine.
+//   grid (max_chunks, Hkv, ncol), 256 threads; block (c, g, col) owns cache
+//   positions [64c, 64c + 64) of kv head g for query column col, wave w serves
+//   q head g*rep + w.  K/V tiles are staged in LDS with coalesced loads; the
+//   last block to finish a (col, g) pair (device-scope counter) merges the
+//   per-chunk (max, sum, o) partials and resets the counter for the next launch.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+template <int HD>
+__global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a) {
+  constexpr int CH = 64;
+  constexpr int KS = HD + 1;  // padded K row: lane-per-position reads hit distinct banks
+  __shared__ float kt[CH * KS];
+  __shared__ float vt[CH * HD];
+  __shared__ float qs[GEMV_WAVES][HD];
+  __shared__ float ps[GEMV_WAVES][CH];
+  __shared__ float knew[4][HD], vnew[4][HD];  // positions of this launch's columns
+  __shared__ uint32_t last_flag;
   if (a.done && *a.done) return;
   const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
-  const uint32_t T = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col + 1;
-  const uint32_t t0 = chunk * a.chunk;
-  if (t0 >= T || T > a.max_seq) return;  // uniform across the block
-  const uint32_t t1 = min(T, t0 + a.chunk);
-  const uint32_t hd = a.hd, rep = a.H / a.Hkv;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  __shared__ float qs[GEMV_WAVES][256];
-  __shared__ float ps[GEMV_WAVES][64];
-  const float* kbase = a.k_cache + size_t(g) * a.max_seq * hd;
-  const float* vbase = a.v_cache + size_t(g) * a.max_seq * hd;
-  const uint32_t rounds = (rep + GEMV_WAVES - 1) / GEMV_WAVES;
-  for (uint32_t it = 0; it < rounds; ++it) {  // same trip count for every wave
-    const uint32_t h_local = wave + GEMV_WAVES * it;
-    const bool active = h_local < rep;
-    const uint32_t h = g * rep + (active ? h_local : 0u);
-    const float* q = a.q + size_t(col) * a.H * hd + size_t(h) * hd;
-    for (uint32_t i = lane; i < hd; i += 64) qs[wave][i] = q[i];
-    __syncthreads();
-    float m = -INFINITY, l = 0.0f;
-    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // hd <= 256
-    for (uint32_t tb = t0; tb < t1; tb += 64) {
-      const uint32_t t = tb + lane;
-      float sc = -INFINITY;
-      if (t < t1) {
-        const float4* kr = reinterpret_cast<const float4*>(kbase + size_t(t) * hd);
-        float dsum = 0.0f;
-        for (uint32_t i = 0; i < hd / 4; ++i) {
-          const float4 kv = kr[i];
-          dsum = fmaf(qs[wave][4 * i], kv.x, dsum);
-          dsum = fmaf(qs[wave][4 * i + 1], kv.y, dsum);
-          dsum = fmaf(qs[wave][4 * i + 2], kv.z, dsum);
-          dsum = fmaf(qs[wave][4 * i + 3], kv.w, dsum);
-        }
-        sc = dsum * a.scale;
-      }
-      const float mb = wave_max(sc);
-      const float mn = fmaxf(m, mb);
-      const float p = (t < t1) ? expf(sc - mn) : 0.0f;
-      const float corr = (m == -INFINITY) ? 0.0f : expf(m - mn);
-      l = l * corr + wave_sum(p);
-      ps[wave][lane] = p;
-      __syncthreads();
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] *= corr;
-      const uint32_t nt = min(64u, t1 - tb);
-      for (uint32_t tt = 0; tt < nt; ++tt) {
-        const float pv = ps[wave][tt];
-        const float* vr = vbase + size_t(tb + tt) * hd;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t dd = lane + 64 * j;
-          if (dd < hd) o[j] = fmaf(pv, vr[dd], o[j]);
-        }
-      }
-      __syncthreads();
-      m = mn;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
+  if (pos >= a.max_seq) {
+    if (tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
+    return;
+  }
+  const uint32_t T = pos + 1;
+  const uint32_t nch = (T + CH - 1) / CH;
+  if (chunk >= nch) return;
+  const uint32_t t0 = chunk * CH, t1 = min(T, t0 + CH), nt = t1 - t0;
+  const uint32_t rep = a.H / a.Hkv;
+  const float* row = a.qkv + size_t(col) * (a.H + 2 * a.Hkv) * HD;
+  const float2* rope_row = a.rope + size_t(pos) * (HD / 2);
+  float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
+  float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
+  // Positions [base, pos] belong to this launch's columns: their K/V come
+  // from the qkv rows (another block may still be writing them to the cache).
+  const uint32_t base = pos - col;
+  const uint32_t lo = max(t0, base);
+
+  if (wave < rep) head_norm_rope(row + size_t(g * rep + wave) * HD, a.q_norm, a.eps, rope_row, HD, lane, qs[wave]);
+  for (uint32_t tt = lo + wave; tt < t1; tt += GEMV_WAVES) {
+    const float* r2 = a.qkv + size_t(tt - base) * (a.H + 2 * a.Hkv) * HD;
+    head_norm_rope(r2 + size_t(a.H + g) * HD, a.k_norm, a.eps, a.rope + size_t(tt) * (HD / 2), HD, lane,
+                   knew[tt - lo]);
+    const float* vs = r2 + size_t(a.H + a.Hkv + g) * HD;
+    for (uint32_t i = lane; i < HD; i += 64) vnew[tt - lo][i] = vs[i];
+  }
+  // K/V tiles of the cached positions
+  for (uint32_t idx = tid; idx < CH * HD / 4; idx += 256) {
+    const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
+    const uint32_t tt = t0 + t;
+    float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+    if (tt < lo) {
+      k4 = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
+      v4 = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
     }
-    if (active) {
-      float* part = a.part + ((size_t(col) * a.H + h) * a.max_chunks + chunk) * (hd + 2);
+    kt[t * KS + d] = k4.x;
+    kt[t * KS + d + 1] = k4.y;
+    kt[t * KS + d + 2] = k4.z;
+    kt[t * KS + d + 3] = k4.w;
+    *reinterpret_cast<float4*>(&vt[t * HD + d]) = v4;
+  }
+  __syncthreads();
+  for (uint32_t tt = lo; tt < t1; ++tt) {
+    const uint32_t tn = tt - t0;
+    for (uint32_t i = tid; i < HD; i += 256) {
+      kt[tn * KS + i] = knew[tt - lo][i];
+      vt[tn * HD + i] = vnew[tt - lo][i];
+      if (tt == pos) {  // SlowArKvCache::write_token for this column's position
+        kc[size_t(pos) * HD + i] = knew[tt - lo][i];
+        vc[size_t(pos) * HD + i] = vnew[tt - lo][i];
+      }
+    }
+  }
+  __syncthreads();
+
+  float m = -INFINITY, l = 0.0f;
+  if (wave < rep) {
+    float s = -INFINITY;
+    if (lane < nt) {
+      float dsum = 0.0f;
+#pragma unroll 16
+      for (int d = 0; d < HD; ++d) dsum = fmaf(qs[wave][d], kt[lane * KS + d], dsum);
+      s = dsum * a.scale;
+    }
+    m = wave_max(s);
+    const float p = (lane < nt) ? expf(s - m) : 0.0f;
+    l = wave_sum(p);
+    ps[wave][lane] = p;
+  }
+  __syncthreads();
+  const uint32_t h = g * rep + wave;
+  float o[HD / 64];
+  if (wave < rep) {
+#pragma unroll
+    for (int j = 0; j < HD / 64; ++j) o[j] = 0.0f;
+    for (uint32_t t = 0; t < nt; ++t) {
+      const float pv = ps[wave][t];
+#pragma unroll
+      for (int j = 0; j < HD / 64; ++j) o[j] = fmaf(pv, vt[t * HD + lane + 64 * j], o[j]);
+    }
+    if (nch == 1) {
+      float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
+      const float inv = 1.0f / l;
+#pragma unroll
+      for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = o[j] * inv;
+    } else {
+      float* part = a.part + (((size_t(col) * a.Hkv + g) * a.max_chunks + chunk) * rep + wave) * (HD + 2);
       if (lane == 0) {
         part[0] = m;
         part[1] = l;
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t dd = lane + 64 * j;
-        if (dd < hd) part[2 + dd] = o[j];
-      }
+      for (int j = 0; j < HD / 64; ++j) part[2 + lane + 64 * j] = o[j];
     }
   }
-}
-
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-  if (a.done && *a.done) return;
-  const uint32_t h = blockIdx.x, col = blockIdx.y;
-  const uint32_t T = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col + 1;
-  if (T > a.max_seq) return;
-  const uint32_t nch = (T + a.chunk - 1) / a.chunk;
-  const uint32_t hd = a.hd;
-  const float* part = a.part + (size_t(col) * a.H + h) * a.max_chunks * (hd + 2);
-  float M = -INFINITY;
-  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, part[c * (hd + 2)]);
-  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-    float L = 0.0f, o = 0.0f;
+  if (nch == 1) return;
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* ctr = a.counters + size_t(col) * a.Hkv + g;
+    const uint32_t old = atomicAdd(ctr, 1u);
+    last_flag = (old == nch - 1) ? 1u : 0u;
+    if (last_flag) atomicExch(ctr, 0u);
+  }
+  __syncthreads();
+  if (!last_flag) return;
+  __threadfence();
+  if (wave < rep) {
+    const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks) * rep * (HD + 2);
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < nch; ++c)
+      M = fmaxf(M, __hip_atomic_load(pbase + (size_t(c) * rep + wave) * (HD + 2), __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT));
+    float L = 0.0f, acc[HD / 64];
+#pragma unroll
+    for (int j = 0; j < HD / 64; ++j) acc[j] = 0.0f;
     for (uint32_t c = 0; c < nch; ++c) {
-      const float* pc = part + c * (hd + 2);
-      const float f = expf(pc[0] - M);
-      L = fmaf(pc[1], f, L);
-      o = fmaf(pc[2 + d], f, o);
+      const float* pc = pbase + (size_t(c) * rep + wave) * (HD + 2);
+      const float mc = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float lc = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float f = expf(mc - M);
+      L = fmaf(lc, f, L);
+#pragma unroll
+      for (int j = 0; j < HD / 64; ++j)
+        acc[j] = fmaf(__hip_atomic_load(pc + 2 + lane + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, acc[j]);
     }
-    a.out[size_t(col) * a.H * hd + size_t(h) * hd + d] = o / L;
+    float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
+    const float inv = 1.0f / L;
+#pragma unroll
+    for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = acc[j] * inv;
   }
 }
 
@@ -880,19 +1152,21 @@ hipError_t set_max_lds(K kernel) {
 }  // namespace
 
 hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
+  if (wtype != W_F16 && wtype != W_Q8_0 && wtype != W_Q4_0) return hipErrorInvalidValue;
+  if (a.in % (wtype == W_F16 ? 8 : 32)) return hipErrorInvalidValue;
+  const bool direct = ncol <= 2 && a.in % 512 == 0 && a.in <= 20 * 512 && a.ldx % 4 == 0;
+  if (direct) {
+    switch (wtype) {
+      case W_F16: return gemv_direct_epi<W_F16>(epi, ncol, a, s);
+      case W_Q8_0: return gemv_direct_epi<W_Q8_0>(epi, ncol, a, s);
+      default: return gemv_direct_epi<W_Q4_0>(epi, ncol, a, s);
+    }
+  }
   if (size_t(ncol) * a.in * sizeof(float) > 150 * 1024) return hipErrorInvalidValue;
   switch (wtype) {
-    case W_F16:
-      if (a.in % 8) return hipErrorInvalidValue;
-      return gemv_pick_epi<W_F16>(epi, ncol, a, s);
-    case W_Q8_0:
-      if (a.in % 32) return hipErrorInvalidValue;
-      return gemv_pick_epi<W_Q8_0>(epi, ncol, a, s);
-    case W_Q4_0:
-      if (a.in % 32) return hipErrorInvalidValue;
-      return gemv_pick_epi<W_Q4_0>(epi, ncol, a, s);
-    default:
-      return hipErrorInvalidValue;
+    case W_F16: return gemv_pick_epi<W_F16>(epi, ncol, a, s);
+    case W_Q8_0: return gemv_pick_epi<W_Q8_0>(epi, ncol, a, s);
+    default: return gemv_pick_epi<W_Q4_0>(epi, ncol, a, s);
   }
 }
 
@@ -909,11 +1183,13 @@ hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  if (a.hd % 4 || a.hd > 256 || a.chunk % 64 || a.H % a.Hkv) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(a.max_chunks, a.Hkv, a.ncol), dim3(256), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3(a.H, a.ncol), dim3(128), 0, s, a);
+  if (a.H % a.Hkv || a.H / a.Hkv > 4 || !a.counters || a.ncol > 4) return hipErrorInvalidValue;
+  const dim3 grid(a.max_chunks, a.Hkv, a.ncol);
+  switch (a.hd) {
+    case 64: hipLaunchKernelGGL(attn_fused_kernel<64>, grid, dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL(attn_fused_kernel<128>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 #include <string>
@@ -317,6 +318,8 @@ void write_gguf(const char* path, const s2synth_config& c, unsigned threads) {
   const double stdv = c.init_std;
   const unsigned nt = threads ? threads : std::max(1u, std::thread::hardware_concurrency());
   std::vector<uint8_t> buf;
+  const bool progress = getenv("S2SYNTH_PROGRESS") != nullptr;
+  uint64_t reported = 0;
   for (size_t ti = 0; ti < ts.size(); ++ti) {
     const Tensor& t = ts[ti];
     const uint64_t tkey = splitmix64(c.seed ^ splitmix64(0x5EED0000ull + ti));
@@ -334,6 +337,10 @@ void write_gguf(const char* path, const s2synth_config& c, unsigned threads) {
     if (w.pos() != data_start + t.offset) fail("internal offset mismatch for %s", t.name.c_str());
     w.bytes(buf.data(), buf.size());
     w.pad(32);
+    if (progress && (w.pos() >> 30) != reported) {
+      reported = w.pos() >> 30;
+      fprintf(stderr, "[s2synth] %s: %.2f GB written\n", path, double(w.pos()) / 1e9);
+    }
   }
   w.close();
 }
