@@ -39,7 +39,7 @@ void hip_check(hipError_t e, const char* what) {
 [[noreturn]] void fail(const std::string& m) { throw std::runtime_error(m); }
 
 constexpr uint32_t PREFILL_COLS = 4;
-constexpr uint32_t FRAME_BATCH = 16;
+constexpr uint32_t FRAME_BATCH = 4;
 constexpr size_t WEIGHT_PAD = 256;  // trailing bytes so block loads never leave a buffer
 
 float f16_to_f32(uint16_t h) {
@@ -126,7 +126,7 @@ class Engine {
   void build_rope(float2* dst, uint32_t positions, uint32_t hd, float base);
 
   void gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
-            const float* norm, float eps, float* y, uint32_t ldy, const uint32_t* row_map, uint32_t out_rows,
+            const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row, uint32_t out_rows,
             const uint32_t* done);
   void enqueue_slow_layers(uint32_t ncol, const uint32_t* done);
   void enqueue_head(uint32_t col, bool full, const uint32_t* done);
@@ -153,7 +153,8 @@ class Engine {
   DevLin head_full_, fast_out_;
   std::vector<SlowLayer> slow_;
   std::vector<FastLayer> fast_;
-  uint32_t* head_rows_ = nullptr;
+  uint32_t* head_rows_ = nullptr;  // vocabulary id of each candidate logit
+  uint32_t head_extra_ = NO_ROW;
   uint32_t n_cand_ = 0;
 
   // activations
@@ -293,10 +294,14 @@ Engine::Engine(const s2hip_config& cfg) {
   }
 
   // candidate rows of the output head: semantic ids + im_end, ascending
+  // (semantic ids, then im_end when it lies outside them: the sampler orders
+  // candidates by value and id, not by position)
   std::vector<uint32_t> rows;
   for (uint32_t id = s.semantic_begin; id <= s.semantic_end; ++id) rows.push_back(id);
-  if (im_end_ < s.vocab && (im_end_ < s.semantic_begin || im_end_ > s.semantic_end)) rows.push_back(im_end_);
-  std::sort(rows.begin(), rows.end());
+  if (im_end_ < s.vocab && (im_end_ < s.semantic_begin || im_end_ > s.semantic_end)) {
+    rows.push_back(im_end_);
+    head_extra_ = im_end_;
+  }
   n_cand_ = uint32_t(rows.size());
   if (n_cand_ > 8191) fail("too many sampling candidates");
   head_rows_ = dalloc<uint32_t>(rows.size());
@@ -442,7 +447,7 @@ void Engine::build_rope(float2* dst, uint32_t positions, uint32_t hd, float base
 }
 
 void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
-                  const float* norm, float eps, float* y, uint32_t ldy, const uint32_t* row_map, uint32_t out_rows,
+                  const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row, uint32_t out_rows,
                   const uint32_t* done) {
   uint32_t c = 0;
   while (c < ncol) {
@@ -452,7 +457,8 @@ void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, con
     a.w = L.w;
     a.w3 = L3 ? L3->w : nullptr;
     a.row_bytes = L.row_bytes;
-    a.row_map = row_map;
+    a.row_base = row_base;
+    a.extra_row = extra_row;
     a.in = L.in;
     a.out = out_rows;
     a.x = x + size_t(c) * ldx;
@@ -472,7 +478,7 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
   const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim, qkv_w = q + 2 * kv;
   for (uint32_t l = 0; l < s.slow_layers; ++l) {
     const SlowLayer& L = slow_[l];
-    gemv(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, nullptr, L.wqkv.out, done);
+    gemv(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, 0, NO_ROW, L.wqkv.out, done);
     AttnArgs aa{};
     aa.qkv = qkv_;
     aa.q_norm = L.q_norm;
@@ -496,9 +502,9 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
     aa.done = done;
     aa.err = &st_->err;
     HIPC(launch_attention(aa, stream_));
-    gemv(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, nullptr, L.wo.out, done);
-    gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, nullptr, L.w1.out, done);
-    gemv(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, nullptr, L.w2.out, done);
+    gemv(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.wo.out, done);
+    gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, done);
+    gemv(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.w2.out, done);
   }
   HIPC(launch_add_position(st_, ncol, stream_));
 }
@@ -509,9 +515,10 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
 void Engine::enqueue_head(uint32_t col, bool full, const uint32_t* done) {
   const s2hip_spec& s = spec;
   HIPC(launch_rms_norm(h_ + size_t(col) * s.dim, norm_, hn_, s.dim, 1, s.eps, done, stream_));
-  gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, head_rows_, n_cand_, done);
+  gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, s.semantic_begin, head_extra_,
+       n_cand_, done);
   if (full)
-    gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_full_, s.vocab, nullptr, s.vocab, done);
+    gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_full_, s.vocab, 0, NO_ROW, s.vocab, done);
 }
 
 void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* done) {
@@ -520,7 +527,7 @@ void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* don
   const uint32_t w = fq + 2 * fkv;
   for (uint32_t l = 0; l < s.fast_layers; ++l) {
     const FastLayer& L = fast_[l];
-    gemv(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, nullptr, L.wqkv.out, done);
+    gemv(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out, done);
     AttnArgs aa{};
     aa.qkv = fqkv_;
     aa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
@@ -544,10 +551,10 @@ void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* don
     aa.done = done;
     aa.err = &st_->err;
     HIPC(launch_attention(aa, stream_));
-    gemv(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, nullptr, L.wo.out, done);
-    gemv(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, nullptr,
+    gemv(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
+    gemv(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
          L.w1.out, done);
-    gemv(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, nullptr, L.w2.out, done);
+    gemv(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.w2.out, done);
   }
 }
 
@@ -562,7 +569,7 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done) {
   for (uint32_t cb = 1; cb < s.num_codebooks; ++cb) {
     enqueue_fast_layers(ncol, p0, done);
     gemv(fast_out_, nullptr, EPI_STORE, 1, fh_ + size_t(ncol - 1) * s.dim, s.dim, fast_norm_, s.fast_eps, flogits_,
-         s.codebook_size, nullptr, s.codebook_size, done);
+         s.codebook_size, 0, NO_ROW, s.codebook_size, done);
     SampleArgs sa{};
     sa.logits = flogits_;
     sa.n = s.codebook_size;
@@ -738,7 +745,7 @@ void Engine::fast_logits(const float* hidden, const uint32_t* prefix, size_t ple
     HIPC(hipMemcpyAsync(fh_, rowf.data(), s.dim * 4, hipMemcpyHostToDevice, stream_));
     enqueue_fast_layers(1, uint32_t(j + 1), nullptr);
   }
-  gemv(fast_out_, nullptr, EPI_STORE, 1, fh_, s.dim, fast_norm_, s.fast_eps, flogits_, s.codebook_size, nullptr,
+  gemv(fast_out_, nullptr, EPI_STORE, 1, fh_, s.dim, fast_norm_, s.fast_eps, flogits_, s.codebook_size, 0, NO_ROW,
        s.codebook_size, nullptr);
   HIPC(hipMemcpyAsync(logits, flogits_, s.codebook_size * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
@@ -933,7 +940,7 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
   L.out = uint32_t(out);
   L.row_bytes = rb;
   gemv(L, nullptr, EPI_STORE, uint32_t(ncol), dx.as<float>(), uint32_t(in), nullptr, 0.0f, dy.as<float>(),
-       uint32_t(out), nullptr, uint32_t(out), nullptr);
+       uint32_t(out), 0, NO_ROW, uint32_t(out), nullptr);
   HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
 }
@@ -1095,16 +1102,17 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   auto pass = [&](uint32_t l) {
     const SlowLayer& L = slow_[l];
     if (name == "slow_w13")
-      gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, 1, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, nullptr, L.w1.out, nullptr);
+      gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, 1, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, nullptr);
     else if (name == "slow_wqkv")
-      gemv(L.wqkv, nullptr, EPI_STORE, 1, h_, s.dim, L.attn_norm, s.eps, qkv_, q + 2 * kv, nullptr, L.wqkv.out,
+      gemv(L.wqkv, nullptr, EPI_STORE, 1, h_, s.dim, L.attn_norm, s.eps, qkv_, q + 2 * kv, 0, NO_ROW, L.wqkv.out,
            nullptr);
     else if (name == "slow_wo")
-      gemv(L.wo, nullptr, EPI_STORE, 1, att_, q, nullptr, 0.0f, act_, s.dim, nullptr, L.wo.out, nullptr);
+      gemv(L.wo, nullptr, EPI_STORE, 1, att_, q, nullptr, 0.0f, act_, s.dim, 0, NO_ROW, L.wo.out, nullptr);
     else if (name == "slow_w2")
-      gemv(L.w2, nullptr, EPI_STORE, 1, act_, s.ffn, nullptr, 0.0f, qkv_, s.dim, nullptr, L.w2.out, nullptr);
+      gemv(L.w2, nullptr, EPI_STORE, 1, act_, s.ffn, nullptr, 0.0f, qkv_, s.dim, 0, NO_ROW, L.w2.out, nullptr);
     else if (name == "slow_head")
-      gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, head_rows_, n_cand_,
+      gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, s.semantic_begin, head_extra_,
+           n_cand_,
            nullptr);
     else
       fail("unknown kernel name " + name);

@@ -34,12 +34,16 @@ struct DevState {
 };
 
 enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u };
+constexpr uint32_t NO_ROW = 0xffffffffu;
 
 struct GemvArgs {
   const uint8_t* w;      // weight rows
   const uint8_t* w3;     // second matrix for SwiGLU epilogues (same shape)
   size_t row_bytes;
-  const uint32_t* row_map;  // optional: logical row -> weight row
+  // logical row r < out maps to weight row row_base + r, except that when
+  // extra_row != NO_ROW the last logical row (out - 1) maps to extra_row
+  uint32_t row_base;
+  uint32_t extra_row;
   uint32_t in, out;      // `out` logical rows
   const float* x;        // [ncol][ldx]
   uint32_t ldx;

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     uint32_t lr = row0 + r;
     if (lr >= a.out) lr = 0;  // clamp; result discarded
-    const uint32_t wr = a.row_map ? a.row_map[lr] : lr;
+    const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
     rp[r] = a.w + size_t(wr) * a.row_bytes;
     rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
   }
@@ -308,15 +308,38 @@ hipError_t gemv_pick_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
 // 512-element steps per row), x and the RMSNorm gain are read through the
 // L1 cache, and the only block-level synchronisation is the RMSNorm scale.
 // ---------------------------------------------------------------------------
-template <uint32_t WT, int NCOL, int R, int EPI, int KMAX>
-__global__ __launch_bounds__(GEMV_THREADS) void gemv_direct_kernel(GemvArgs a) {
+template <uint32_t WT, int NCOL, int R, int EPI, int KMAX, int WPB, bool XREG>
+__global__ __launch_bounds__(64 * WPB) void gemv_direct_kernel(GemvArgs a) {
   if (a.done && *a.done) return;
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
-  __shared__ float red[GEMV_WAVES][NCOL];
+  // XREG: x (and the norm gain) held in registers, loaded before the weights
+  constexpr int XK = XREG ? KMAX : 1;
+  __shared__ float red[WPB][NCOL];
   const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
   const uint32_t in = a.in;
   const uint32_t kit = in / (WAVE * 8);  // host guarantees in % 512 == 0
-  const uint32_t row0 = (blockIdx.x * GEMV_WAVES + wave) * R;
+  const uint32_t row0 = (blockIdx.x * WPB + wave) * R;
+
+  float4 xr[NCOL][XK][2];
+  float4 gr[XK][2];
+  if constexpr (XREG) {
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k < kit) {
+        const uint32_t e = k * (WAVE * 8) + lane * 8;
+#pragma unroll
+        for (int c = 0; c < NCOL; ++c) {
+          const float* xc = a.x + size_t(c) * a.ldx + e;
+          xr[c][k][0] = *reinterpret_cast<const float4*>(xc);
+          xr[c][k][1] = *reinterpret_cast<const float4*>(xc + 4);
+        }
+        if (a.norm) {
+          gr[k][0] = *reinterpret_cast<const float4*>(a.norm + e);
+          gr[k][1] = *reinterpret_cast<const float4*>(a.norm + e + 4);
+        }
+      }
+    }
+  }
 
   const uint8_t* rp[R];
   const uint8_t* rp3[R];
@@ -324,7 +347,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_direct_kernel(GemvArgs a) {
   for (int r = 0; r < R; ++r) {
     uint32_t lr = row0 + r;
     if (lr >= a.out) lr = 0;  // clamp; result discarded
-    const uint32_t wr = a.row_map ? a.row_map[lr] : lr;
+    const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
     rp[r] = a.w + size_t(wr) * a.row_bytes;
     rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
   }
@@ -346,22 +369,42 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_direct_kernel(GemvArgs a) {
 #pragma unroll
   for (int c = 0; c < NCOL; ++c) scale[c] = 1.0f;
   if (a.norm) {
+    if constexpr (XREG) {
+      // every lane holds in/64 elements of each column: a wave sum covers x
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-      const float* xc = a.x + size_t(c) * a.ldx;
-      float ss = 0.0f;
-      for (uint32_t i = tid * 4; i < in; i += GEMV_THREADS * 4) {
-        const float4 v = *reinterpret_cast<const float4*>(xc + i);
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      for (int c = 0; c < NCOL; ++c) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+          if (k < kit) {
+            const float4 u = xr[c][k][0], v = xr[c][k][1];
+            ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+          }
+        }
+        ss = wave_sum(ss);
+        scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(in)), a.eps)));
       }
-      ss = wave_sum(ss);
-      if (lane == 0) red[wave][c] = ss;
-    }
-    __syncthreads();
+    } else {
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-      const float tot = (red[0][c] + red[1][c]) + (red[2][c] + red[3][c]);
-      scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(in)), a.eps)));
+      for (int c = 0; c < NCOL; ++c) {
+        const float* xc = a.x + size_t(c) * a.ldx;
+        float ss = 0.0f;
+        for (uint32_t i = tid * 4; i < in; i += 64 * WPB * 4) {
+          const float4 v = *reinterpret_cast<const float4*>(xc + i);
+          ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave][c] = ss;
+      }
+      if constexpr (WPB > 1) __syncthreads();
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) {
+        float tot = red[0][c];
+#pragma unroll
+        for (int w = 1; w < WPB; ++w) tot += red[w][c];
+        scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(in)), a.eps)));
+      }
     }
   }
 
@@ -385,20 +428,30 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_direct_kernel(GemvArgs a) {
         decode8<WT>(wb[r][k], w[r]);
         if constexpr (DUAL) decode8<WT>(wb3[r][k], w3[r]);
       }
-      float g[8];
+      float4 ga, gb;
       if (a.norm) {
-        const float4 ga = *reinterpret_cast<const float4*>(a.norm + e);
-        const float4 gb = *reinterpret_cast<const float4*>(a.norm + e + 4);
-        g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w;
-        g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
+        if constexpr (XREG) {
+          ga = gr[k][0];
+          gb = gr[k][1];
+        } else {
+          ga = *reinterpret_cast<const float4*>(a.norm + e);
+          gb = *reinterpret_cast<const float4*>(a.norm + e + 4);
+        }
       }
 #pragma unroll
       for (int c = 0; c < NCOL; ++c) {
-        const float* xc = a.x + size_t(c) * a.ldx + e;
-        const float4 xa = *reinterpret_cast<const float4*>(xc);
-        const float4 xb = *reinterpret_cast<const float4*>(xc + 4);
+        float4 xa, xb;
+        if constexpr (XREG) {
+          xa = xr[c][k][0];
+          xb = xr[c][k][1];
+        } else {
+          const float* xc = a.x + size_t(c) * a.ldx + e;
+          xa = *reinterpret_cast<const float4*>(xc);
+          xb = *reinterpret_cast<const float4*>(xc + 4);
+        }
         float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
         if (a.norm) {
+          const float g[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
 #pragma unroll
           for (int i = 0; i < 8; ++i) xv[i] = __fmul_rn(__fmul_rn(xv[i], scale[c]), g[i]);
         }
@@ -440,11 +493,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_direct_kernel(GemvArgs a) {
   }
 }
 
-template <uint32_t WT, int NCOL, int R, int EPI, int KMAX>
+template <uint32_t WT, int NCOL, int R, int EPI, int KMAX, int WPB = 4, bool XREG = false>
 hipError_t gemv_direct_launch(const GemvArgs& a, hipStream_t s) {
-  const uint32_t rows_per_block = GEMV_WAVES * R;
+  const uint32_t rows_per_block = WPB * R;
   const dim3 grid((a.out + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL((gemv_direct_kernel<WT, NCOL, R, EPI, KMAX>), grid, dim3(GEMV_THREADS), 0, s, a);
+  hipLaunchKernelGGL((gemv_direct_kernel<WT, NCOL, R, EPI, KMAX, WPB, XREG>), grid, dim3(64 * WPB), 0, s, a);
   return hipGetLastError();
 }
 
@@ -474,6 +527,358 @@ hipError_t gemv_direct_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) 
     default: return hipErrorInvalidValue;
   }
 }
+
+// ---------------------------------------------------------------------------
+// Decode GEMV with a compile-time row length (KIT 512-element steps): no
+// predication, every weight load of the wave's R rows issued at once.  The
+// RMSNorm x loads go out before the weights (loads complete in order), so
+// each wave has its norm scale by the time its weights land, with no block
+// barrier.  The early-exit flag is read after the loads are in flight.
+// ---------------------------------------------------------------------------
+template <uint32_t WT, int NCOL, int R, int EPI, int KIT, int WPB, bool NORM>
+__global__ __launch_bounds__(64 * WPB) void gemv_k_kernel(GemvArgs a) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+  constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
+  constexpr int XK = NORM ? KIT : 1;
+  const uint32_t row0 = (blockIdx.x * WPB + wave) * R;
+  (void)tid;
+
+  // 1. x loads of the normalised GEMVs (kept in registers for the FMA loop)
+  float4 xr[NCOL][XK][2];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c)
+#pragma unroll
+      for (int k = 0; k < KIT; ++k) {
+        const float* xc = a.x + size_t(c) * a.ldx + k * 512 + lane * 8;
+        xr[c][k][0] = *reinterpret_cast<const float4*>(xc);
+        xr[c][k][1] = *reinterpret_cast<const float4*>(xc + 4);
+      }
+  }
+  // 2. weight loads: all of the wave's rows at once
+  const uint8_t* rp[R];
+  const uint8_t* rp3[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t lr = row0 + r;
+    if (lr >= a.out) lr = 0;  // clamp; result discarded
+    const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
+    rp[r] = a.w + size_t(wr) * a.row_bytes;
+    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  }
+  Raw8<WT> wb[R][KIT];
+  Raw8<WT> wb3[DUAL ? R : 1][KIT];
+#pragma unroll
+  for (int k = 0; k < KIT; ++k) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      wb[r][k] = load_raw<WT>(rp[r], k * 512 + lane * 8);
+      if constexpr (DUAL) wb3[r][k] = load_raw<WT>(rp3[r], k * 512 + lane * 8);
+    }
+  }
+  // read after the weight loads are issued: the scalar wait then overlaps them
+  const uint32_t done = a.done ? __builtin_nontemporal_load(a.done) : 0u;
+  // 3. RMSNorm scale: each lane holds in/64 elements, a wave sum covers x
+  float scale[NCOL];
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) {
+    scale[c] = 1.0f;
+    if constexpr (NORM) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KIT; ++k) {
+        const float4 u = xr[c][k][0], v = xr[c][k][1];
+        ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      ss = wave_sum(ss);
+      scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(IN)), a.eps)));
+    }
+  }
+  if (done) return;
+
+  float acc[R][NCOL];
+  float acc3[R][NCOL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      acc[r][c] = 0.0f;
+      acc3[r][c] = 0.0f;
+    }
+#pragma unroll
+  for (int k = 0; k < KIT; ++k) {
+    const uint32_t e = k * 512 + lane * 8;
+    float w[R][8];
+    float w3[DUAL ? R : 1][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      decode8<WT>(wb[r][k], w[r]);
+      if constexpr (DUAL) decode8<WT>(wb3[r][k], w3[r]);
+    }
+    float g[8];
+    if constexpr (NORM) {
+      const float4 ga = *reinterpret_cast<const float4*>(a.norm + e);
+      const float4 gb = *reinterpret_cast<const float4*>(a.norm + e + 4);
+      g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w;
+      g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
+    }
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      float4 xa, xb;
+      if constexpr (NORM) {
+        xa = xr[c][k][0];
+        xb = xr[c][k][1];
+      } else {
+        const float* xc = a.x + size_t(c) * a.ldx + e;
+        xa = *reinterpret_cast<const float4*>(xc);
+        xb = *reinterpret_cast<const float4*>(xc + 4);
+      }
+      float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+      if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = __fmul_rn(__fmul_rn(xv[i], scale[c]), g[i]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[r][c] = fmaf(w[r][i], xv[i], acc[r][c]);
+        if constexpr (DUAL) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc3[r][c] = fmaf(w3[r][i], xv[i], acc3[r][c]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float gsum = wave_sum(acc[r][c]);
+      float u = 0.0f;
+      if constexpr (DUAL) u = wave_sum(acc3[r][c]);
+      const uint32_t lr = row0 + r;
+      if (lane == 0 && lr < a.out) {
+        float* dst = a.y + size_t(c) * a.ldy + lr;
+        if constexpr (EPI == EPI_STORE) {
+          *dst = gsum;
+        } else if constexpr (EPI == EPI_RESID) {
+          *dst = __fadd_rn(*dst, gsum);
+        } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+          *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
+        } else {
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+        }
+      }
+    }
+  }
+}
+
+template <uint32_t WT, int NCOL, int R, int EPI, int KIT, int WPB>
+hipError_t gemv_k_launch(const GemvArgs& a, hipStream_t s) {
+  const uint32_t rows_per_block = WPB * R;
+  const dim3 grid((a.out + rows_per_block - 1) / rows_per_block);
+  if (a.norm)
+    hipLaunchKernelGGL((gemv_k_kernel<WT, NCOL, R, EPI, KIT, WPB, true>), grid, dim3(64 * WPB), 0, s, a);
+  else
+    hipLaunchKernelGGL((gemv_k_kernel<WT, NCOL, R, EPI, KIT, WPB, false>), grid, dim3(64 * WPB), 0, s, a);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Decode GEMV, LDS variant: x (and the RMSNorm gain) are loaded first, staged
+// in LDS and shared by the block's waves; the weight loads are issued before
+// the barrier so it overlaps their HBM latency.  Each wave derives the norm
+// scale from the staged x.
+// ---------------------------------------------------------------------------
+template <uint32_t WT, int NCOL, int R, int EPI, int KIT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemv_l_kernel(GemvArgs a) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
+  constexpr int NT = 64 * WPB;
+  __shared__ float xs[NCOL][IN];
+  __shared__ float gs[IN];
+  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+  const uint32_t row0 = (blockIdx.x * WPB + wave) * R;
+  // 1. x / gain loads (16 B per thread per step)
+  constexpr int XS = (IN / 4 + NT - 1) / NT;
+  float4 xv4[NCOL][XS];
+  float4 gv4[XS];
+#pragma unroll
+  for (int j = 0; j < XS; ++j) {
+    const uint32_t i = (j * NT + tid) * 4;
+    if (i < IN) {
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) xv4[c][j] = *reinterpret_cast<const float4*>(a.x + size_t(c) * a.ldx + i);
+      if (a.norm) gv4[j] = *reinterpret_cast<const float4*>(a.norm + i);
+    }
+  }
+  // 2. weight loads
+  const uint8_t* rp[R];
+  const uint8_t* rp3[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    uint32_t lr = row0 + r;
+    if (lr >= a.out) lr = 0;
+    const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
+    rp[r] = a.w + size_t(wr) * a.row_bytes;
+    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  }
+  Raw8<WT> wb[R][KIT];
+  Raw8<WT> wb3[DUAL ? R : 1][KIT];
+#pragma unroll
+  for (int k = 0; k < KIT; ++k) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      wb[r][k] = load_raw<WT>(rp[r], k * 512 + lane * 8);
+      if constexpr (DUAL) wb3[r][k] = load_raw<WT>(rp3[r], k * 512 + lane * 8);
+    }
+  }
+  const uint32_t done = a.done ? __builtin_nontemporal_load(a.done) : 0u;
+  // 3. stage (waits only for the x / gain loads)
+#pragma unroll
+  for (int j = 0; j < XS; ++j) {
+    const uint32_t i = (j * NT + tid) * 4;
+    if (i < IN) {
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) *reinterpret_cast<float4*>(&xs[c][i]) = xv4[c][j];
+      if (a.norm) *reinterpret_cast<float4*>(&gs[i]) = gv4[j];
+    }
+  }
+  __syncthreads();
+  if (done) return;
+  float scale[NCOL];
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) {
+    scale[c] = 1.0f;
+    if (a.norm) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int k = 0; k < KIT; ++k) {
+        const float4 u = *reinterpret_cast<const float4*>(&xs[c][k * 512 + lane * 8]);
+        const float4 v = *reinterpret_cast<const float4*>(&xs[c][k * 512 + lane * 8 + 4]);
+        ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+      }
+      ss = wave_sum(ss);
+      scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(IN)), a.eps)));
+    }
+  }
+  float acc[R][NCOL];
+  float acc3[R][NCOL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      acc[r][c] = 0.0f;
+      acc3[r][c] = 0.0f;
+    }
+#pragma unroll
+  for (int k = 0; k < KIT; ++k) {
+    const uint32_t e = k * 512 + lane * 8;
+    float w[R][8];
+    float w3[DUAL ? R : 1][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      decode8<WT>(wb[r][k], w[r]);
+      if constexpr (DUAL) decode8<WT>(wb3[r][k], w3[r]);
+    }
+    float g[8];
+    if (a.norm) {
+      const float4 ga = *reinterpret_cast<const float4*>(&gs[e]);
+      const float4 gb = *reinterpret_cast<const float4*>(&gs[e + 4]);
+      g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w;
+      g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
+    }
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float4 xa = *reinterpret_cast<const float4*>(&xs[c][e]);
+      const float4 xb = *reinterpret_cast<const float4*>(&xs[c][e + 4]);
+      float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+      if (a.norm) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = __fmul_rn(__fmul_rn(xv[i], scale[c]), g[i]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[r][c] = fmaf(w[r][i], xv[i], acc[r][c]);
+        if constexpr (DUAL) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc3[r][c] = fmaf(w3[r][i], xv[i], acc3[r][c]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      const float gsum = wave_sum(acc[r][c]);
+      float u = 0.0f;
+      if constexpr (DUAL) u = wave_sum(acc3[r][c]);
+      const uint32_t lr = row0 + r;
+      if (lane == 0 && lr < a.out) {
+        float* dst = a.y + size_t(c) * a.ldy + lr;
+        if constexpr (EPI == EPI_STORE) {
+          *dst = gsum;
+        } else if constexpr (EPI == EPI_RESID) {
+          *dst = __fadd_rn(*dst, gsum);
+        } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+          *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
+        } else {
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+        }
+      }
+    }
+  }
+}
+
+template <uint32_t WT, int NCOL, int R, int EPI, int KIT, int WPB>
+hipError_t gemv_l_launch(const GemvArgs& a, hipStream_t s) {
+  const uint32_t rows_per_block = WPB * R;
+  const dim3 grid((a.out + rows_per_block - 1) / rows_per_block);
+  hipLaunchKernelGGL((gemv_l_kernel<WT, NCOL, R, EPI, KIT, WPB>), grid, dim3(64 * WPB), 0, s, a);
+  return hipGetLastError();
+}
+
+// Row shapes of the S2-Pro family: 512 / 1536 (tiny), 2560, 4096, 9728.
+// Returns hipErrorNotSupported for other row lengths.
+template <uint32_t WT, int NCOL, int EPI>
+hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr int RS = DUAL ? 1 : 2;  // rows per wave for short rows
+  switch (a.in) {
+    case 512: return gemv_k_launch<WT, NCOL, RS, EPI, 1, 4>(a, s);
+    case 1536: return gemv_k_launch<WT, NCOL, RS, EPI, 3, 4>(a, s);
+    case 2560: return gemv_k_launch<WT, NCOL, RS, EPI, 5, 4>(a, s);
+    case 4096: return gemv_k_launch<WT, NCOL, 1, EPI, 8, 2>(a, s);
+    case 9728: return gemv_k_launch<WT, NCOL, 1, EPI, 19, 1>(a, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+template <uint32_t WT, int EPI>
+hipError_t gemv_k_ncol(int ncol, const GemvArgs& a, hipStream_t s) {
+  if (ncol == 1) return gemv_k_pick<WT, 1, EPI>(a, s);
+  return gemv_k_pick<WT, 2, EPI>(a, s);
+}
+
+template <uint32_t WT>
+hipError_t gemv_k_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: return gemv_k_ncol<WT, EPI_STORE>(ncol, a, s);
+    case EPI_RESID: return gemv_k_ncol<WT, EPI_RESID>(ncol, a, s);
+    case EPI_SWIGLU_SLOW: return gemv_k_ncol<WT, EPI_SWIGLU_SLOW>(ncol, a, s);
+    case EPI_SWIGLU_FAST: return gemv_k_ncol<WT, EPI_SWIGLU_FAST>(ncol, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool gemv_k_supported(uint32_t in) { return in == 512 || in == 1536 || in == 2560 || in == 4096 || in == 9728; }
 
 // ---------------------------------------------------------------------------
 // RMSNorm over `ncol` vectors (one block per column).
@@ -676,20 +1081,19 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a) {
     const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks) * rep * (HD + 2);
     float M = -INFINITY;
     for (uint32_t c = 0; c < nch; ++c)
-      M = fmaxf(M, __hip_atomic_load(pbase + (size_t(c) * rep + wave) * (HD + 2), __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT));
+      M = fmaxf(M, pbase[(size_t(c) * rep + wave) * (HD + 2)]);
     float L = 0.0f, acc[HD / 64];
 #pragma unroll
     for (int j = 0; j < HD / 64; ++j) acc[j] = 0.0f;
     for (uint32_t c = 0; c < nch; ++c) {
       const float* pc = pbase + (size_t(c) * rep + wave) * (HD + 2);
-      const float mc = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const float lc = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const float mc = pc[0];
+      const float lc = pc[1];
       const float f = expf(mc - M);
       L = fmaf(lc, f, L);
 #pragma unroll
       for (int j = 0; j < HD / 64; ++j)
-        acc[j] = fmaf(__hip_atomic_load(pc + 2 + lane + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, acc[j]);
+        acc[j] = fmaf(pc[2 + lane + 64 * j], f, acc[j]);
     }
     float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
     const float inv = 1.0f / L;
@@ -1154,6 +1558,13 @@ hipError_t set_max_lds(K kernel) {
 hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
   if (wtype != W_F16 && wtype != W_Q8_0 && wtype != W_Q4_0) return hipErrorInvalidValue;
   if (a.in % (wtype == W_F16 ? 8 : 32)) return hipErrorInvalidValue;
+  if (ncol <= 2 && a.ldx % 4 == 0 && gemv_k_supported(a.in)) {
+    switch (wtype) {
+      case W_F16: return gemv_k_epi<W_F16>(epi, ncol, a, s);
+      case W_Q8_0: return gemv_k_epi<W_Q8_0>(epi, ncol, a, s);
+      default: return gemv_k_epi<W_Q4_0>(epi, ncol, a, s);
+    }
+  }
   const bool direct = ncol <= 2 && a.in % 512 == 0 && a.in <= 20 * 512 && a.ldx % 4 == 0;
   if (direct) {
     switch (wtype) {
