@@ -116,9 +116,12 @@ def main():
     achieved = kb / (us * 1e-6) / 1e9
     log(f"{kern}: {us:.2f} us/launch, {kb / 1e6:.2f} MB -> {achieved:.0f} GB/s")
     other = {}
-    for k in ("slow_wqkv", "slow_wo", "slow_w2", "slow_head"):
+    for k in ("slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn", "fast_head",
+              "sample_fast", "sample_slow", "fast_frame", "empty"):
         ku, kbb = eng.time_kernel(k, reps=5)
-        other[k] = {"us": round(ku, 3), "GBs": round(kbb / (ku * 1e-6) / 1e9, 1)}
+        other[k] = {"us": round(ku, 3)}
+        if kbb:
+            other[k]["GBs"] = round(kbb / (ku * 1e-6) / 1e9, 1)
     eng.close()
 
     cpu = None

@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <stdexcept>
@@ -163,6 +164,7 @@ class Engine {
   float *kc_ = nullptr, *vc_ = nullptr;
   float2 *rope_slow_ = nullptr, *rope_fast_ = nullptr;
   uint32_t attn_chunks_ = 1;
+  uint32_t attn_mode_ = ATTN_SPLIT;
   uint32_t* counters_ = nullptr;
   float *fh_ = nullptr, *fqkv_ = nullptr, *fq_ = nullptr, *fatt_ = nullptr, *fpart_ = nullptr, *fact_ = nullptr;
   float *flogits_ = nullptr, *fkc_ = nullptr, *fvc_ = nullptr;
@@ -310,7 +312,8 @@ Engine::Engine(const s2hip_config& cfg) {
   // activations
   const uint32_t NC = PREFILL_COLS;
   const uint64_t qkv_w = q + 2 * kv;
-  attn_chunks_ = (s.max_seq_len + 63) / 64;
+  attn_mode_ = getenv("S2HIP_ATTN_FUSED") ? ATTN_FUSED : ATTN_SPLIT;
+  attn_chunks_ = attention_chunks(s.max_seq_len, attn_mode_);
   h_ = dalloc<float>(size_t(NC) * s.dim);
   qkv_ = dalloc<float>(size_t(NC) * qkv_w);
   q_ = dalloc<float>(size_t(NC) * q);
@@ -336,7 +339,7 @@ Engine::Engine(const s2hip_config& cfg) {
   fqkv_ = dalloc<float>(2 * (fq + 2 * fkv));
   fq_ = dalloc<float>(2 * fq);
   fatt_ = dalloc<float>(2 * fq);
-  fpart_ = dalloc<float>(2 * size_t(s.fast_heads) * ((fctx_ + 63) / 64) * (s.fast_head_dim + 2));
+  fpart_ = dalloc<float>(2 * size_t(s.fast_heads) * attention_chunks(fctx_, attn_mode_) * (s.fast_head_dim + 2));
   fact_ = dalloc<float>(2 * size_t(s.fast_ffn));
   flogits_ = dalloc<float>(s.codebook_size);
   fkc_ = dalloc<float>(size_t(s.fast_layers) * fkv * fctx_);
@@ -498,6 +501,7 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
     aa.max_seq = s.max_seq_len;
     aa.ncol = ncol;
     aa.max_chunks = attn_chunks_;
+    aa.mode = attn_mode_;
     aa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
     aa.done = done;
     aa.err = &st_->err;
@@ -546,7 +550,8 @@ void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* don
     aa.hd = s.fast_head_dim;
     aa.max_seq = fctx_;
     aa.ncol = ncol;
-    aa.max_chunks = (fctx_ + 63) / 64;
+    aa.max_chunks = attention_chunks(fctx_, attn_mode_);
+    aa.mode = attn_mode_;
     aa.scale = 1.0f / std::sqrt(float(s.fast_head_dim));  // fast_ar.rs:60-62
     aa.done = done;
     aa.err = &st_->err;
@@ -1027,7 +1032,7 @@ void Engine::op_attention(const float* q, const float* k, const float* v, uint32
   memcpy(row.data() + size_t(H) * hd, k + size_t(T - 1) * Hkv * hd, size_t(Hkv) * hd * 4);
   memcpy(row.data() + size_t(H + Hkv) * hd, v + size_t(T - 1) * Hkv * hd, size_t(Hkv) * hd * 4);
   std::vector<float2> rope(size_t(T) * (hd / 2), make_float2(1.0f, 0.0f));
-  const uint32_t nch = (T + 63) / 64;
+  const uint32_t nch = attention_chunks(T, attn_mode_);
   TmpBuf drow(width * 4), dk(kc.size() * 4), dv(vc.size() * 4), dpart(size_t(Hkv) * nch * (H / Hkv) * (hd + 2) * 4),
       dout(size_t(H) * hd * 4), drope(rope.size() * sizeof(float2)), dctr(size_t(Hkv) * 4);
   HIPC(hipMemcpyAsync(drow.p, row.data(), width * 4, hipMemcpyHostToDevice, stream_));
@@ -1052,6 +1057,7 @@ void Engine::op_attention(const float* q, const float* k, const float* v, uint32
   aa.max_seq = T;
   aa.ncol = 1;
   aa.max_chunks = nch;
+  aa.mode = attn_mode_;
   aa.scale = scale;
   HIPC(launch_attention(aa, stream_));
   HIPC(hipMemcpyAsync(out, dout.p, size_t(H) * hd * 4, hipMemcpyDeviceToHost, stream_));
@@ -1110,6 +1116,55 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
       gemv(L.wo, nullptr, EPI_STORE, 1, att_, q, nullptr, 0.0f, act_, s.dim, 0, NO_ROW, L.wo.out, nullptr);
     else if (name == "slow_w2")
       gemv(L.w2, nullptr, EPI_STORE, 1, act_, s.ffn, nullptr, 0.0f, qkv_, s.dim, 0, NO_ROW, L.w2.out, nullptr);
+    else if (name == "slow_attn" || name == "fast_attn") {
+      const bool fast = name == "fast_attn";
+      AttnArgs aa{};
+      aa.qkv = fast ? fqkv_ : qkv_;
+      aa.q_norm = fast ? nullptr : L.q_norm;
+      aa.k_norm = fast ? nullptr : L.k_norm;
+      aa.eps = s.eps;
+      aa.rope = fast ? rope_fast_ : rope_slow_;
+      const uint32_t kvw = fast ? s.fast_kv_heads * s.fast_head_dim : kv;
+      aa.k_cache = fast ? fkc_ + size_t(l % s.fast_layers) * kvw * fctx_ : kc_ + size_t(l) * kv * s.max_seq_len;
+      aa.v_cache = fast ? fvc_ + size_t(l % s.fast_layers) * kvw * fctx_ : vc_ + size_t(l) * kv * s.max_seq_len;
+      aa.part = fast ? fpart_ : part_;
+      aa.counters = counters_;
+      aa.out = fast ? fatt_ : att_;
+      aa.pos_ptr = nullptr;
+      aa.pos_offset = fast ? 5u : std::min(s.max_seq_len - 1, 383u);
+      aa.H = fast ? s.fast_heads : s.heads;
+      aa.Hkv = fast ? s.fast_kv_heads : s.kv_heads;
+      aa.hd = fast ? s.fast_head_dim : s.head_dim;
+      aa.max_seq = fast ? fctx_ : s.max_seq_len;
+      aa.ncol = 1;
+      aa.max_chunks = fast ? attention_chunks(fctx_, attn_mode_) : attn_chunks_;
+      aa.mode = attn_mode_;
+      aa.scale = 0.08838834764831845f;
+      HIPC(launch_attention(aa, stream_));
+    } else if (name == "sample_fast" || name == "sample_slow") {
+      SampleArgs sa{};
+      const bool fast = name == "sample_fast";
+      sa.logits = fast ? flogits_ : logits_c_;
+      sa.ids = fast ? nullptr : head_rows_;
+      sa.n = fast ? s.codebook_size : n_cand_;
+      sa.vocab = fast ? s.codebook_size : s.vocab;
+      sa.cfg = SamplerCfg{0.0f, 1.0f, 0};
+      sa.st = st_;
+      sa.im_end = im_end_;
+      sa.cb_index = 1;
+      sa.fast_emb = fast_emb_;
+      sa.next_input = fast ? fh_ : nullptr;
+      sa.dim = s.dim;
+      sa.num_codebooks = s.num_codebooks;
+      HIPC(fast ? launch_sample_fast(sa, stream_) : launch_sample_slow(sa, stream_));
+    } else if (name == "fast_head") {
+      gemv(fast_out_, nullptr, EPI_STORE, 1, fh_, s.dim, fast_norm_, s.fast_eps, flogits_, s.codebook_size, 0, NO_ROW,
+           s.codebook_size, nullptr);
+    } else if (name == "fast_frame") {
+      enqueue_fast_frame(SamplerCfg{0.0f, 1.0f, 0}, nullptr);
+    } else if (name == "empty") {
+      HIPC(launch_add_position(st_, 0, stream_));
+    }
     else if (name == "slow_head")
       gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, s.semantic_begin, head_extra_,
            n_cand_,
@@ -1124,7 +1179,32 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   else if (name == "slow_wo") b = double(L0.wo.bytes) + 4.0 * (q + s.dim);
   else if (name == "slow_w2") b = double(L0.w2.bytes) + 4.0 * (s.ffn + s.dim);
   else if (name == "slow_head") b = double(n_cand_) * s.dim * 2 + 4.0 * (s.dim + n_cand_);
-  const uint32_t layers = name == "slow_head" ? 1u : s.slow_layers;
+  const bool per_layer = name.rfind("slow_", 0) == 0 && name != "slow_head" && name != "sample_slow";
+  const uint32_t layers = per_layer || name == "fast_attn" ? s.slow_layers : 1u;
+  if (name == "fast_frame" || name == "sample_fast" || name == "sample_slow" || name == "empty") {
+    // a clean state: nothing finished, frame counters at zero
+    HIPC(hipStreamSynchronize(stream_));
+    DevState init{};
+    init.max_new = 1u << 30;
+    init.min_tokens_before_end = 1u << 30;
+    *st_host_ = init;
+    HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
+    HIPC(hipMemsetAsync(hn_, 0, size_t(s.dim) * 4, stream_));
+    // distinct pseudo-random logits (the greedy path of a real frame)
+    std::vector<float> rl(std::max<size_t>(s.codebook_size, n_cand_));
+    uint64_t z = 0x9E3779B97F4A7C15ull;
+    for (float& v : rl) {
+      z = z * 6364136223846793005ull + 1442695040888963407ull;
+      v = float(int64_t(z >> 11) % 2000003) * 1e-6f;
+    }
+    HIPC(hipMemcpy(flogits_, rl.data(), size_t(s.codebook_size) * 4, hipMemcpyHostToDevice));
+    HIPC(hipMemcpy(logits_c_, rl.data(), size_t(n_cand_) * 4, hipMemcpyHostToDevice));
+    HIPC(hipMemsetAsync(fh_, 0, 2 * size_t(s.dim) * 4, stream_));
+  }
+  if (name == "slow_attn" || name == "fast_attn") {
+    HIPC(hipMemsetAsync(qkv_, 0, size_t(PREFILL_COLS) * (q + 2 * kv) * 4, stream_));
+    HIPC(hipMemsetAsync(fqkv_, 0, 2 * size_t(s.fast_heads + 2 * s.fast_kv_heads) * s.fast_head_dim * 4, stream_));
+  }
   for (uint32_t l = 0; l < layers; ++l) pass(l);  // warm-up
   hipEvent_t e0, e1;
   HIPC(hipEventCreate(&e0));

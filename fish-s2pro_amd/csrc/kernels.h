@@ -105,11 +105,14 @@ struct AttnArgs {
   const uint32_t* pos_ptr; // nullable
   uint32_t pos_offset;
   uint32_t H, Hkv, hd, max_seq, ncol;
-  uint32_t max_chunks;     // ceil(max_seq / 64)
+  uint32_t max_chunks;     // attention_chunks(max_seq, mode)
+  uint32_t mode;           // ATTN_SPLIT: partial + combine kernels; ATTN_FUSED: one kernel
   float scale;
   const uint32_t* done;
   uint32_t* err;
 };
+enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
+uint32_t attention_chunks(uint32_t max_seq, uint32_t mode);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
 // Slow-AR token embedding (time-major flat ids [n][cdim]).

@@ -1103,6 +1103,182 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention, two-kernel form (partials + combine).  Partial kernel:
+// grid (max_chunks, Hkv, ncol), 256 threads; block (c, g, col) covers cache
+// positions [CH c, CH c + CH).  Every global load goes out before any wait:
+// first the q-side operands, then the K/V tile of cached positions into
+// registers, then the k/v rows of positions that belong to this launch's
+// columns (their cache rows may still be in flight in another block).
+// With a single chunk the block writes the final output itself.
+// ---------------------------------------------------------------------------
+template <int HD, int CH>
+__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  constexpr int KS = HD + 1;
+  constexpr int PER = CH * HD / 4 / 256;  // float4 per thread per tile
+  static_assert(PER >= 1, "tile too small");
+  __shared__ float kt[CH * KS];
+  __shared__ float vt[CH * HD];
+  __shared__ float qs[GEMV_WAVES][HD];
+  __shared__ float ps[GEMV_WAVES][CH];
+  __shared__ float knew[4][HD], vnew[4][HD];
+  const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t done = a.done ? *a.done : 0u;
+  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
+  if (done) return;
+  if (pos >= a.max_seq) {
+    if (tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
+    return;
+  }
+  const uint32_t T = pos + 1;
+  const uint32_t nch = (T + CH - 1) / CH;
+  if (chunk >= nch) return;
+  const uint32_t t0 = chunk * CH, t1 = min(T, t0 + CH), nt = t1 - t0;
+  const uint32_t rep = a.H / a.Hkv;
+  const uint32_t width = (a.H + 2 * a.Hkv) * HD;
+  const uint32_t base = pos - col;          // first position of this launch
+  const uint32_t lo = max(t0, min(base, t1));  // [lo, t1): positions of this launch
+  const float* row = a.qkv + size_t(col) * width;
+  const float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
+  const float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
+
+  // 1. q-side operands: lane = rotation pair
+  const bool qlane = wave < rep && lane < HD / 2;
+  float2 qv = make_float2(0.f, 0.f), qn = make_float2(1.f, 1.f), rp = make_float2(1.f, 0.f);
+  if (qlane) {
+    qv = *reinterpret_cast<const float2*>(row + size_t(g * rep + wave) * HD + 2 * lane);
+    if (a.q_norm) qn = *reinterpret_cast<const float2*>(a.q_norm + 2 * lane);
+    rp = a.rope[size_t(pos) * (HD / 2) + lane];
+  }
+  // 2. K/V tile of cached positions, into registers
+  float4 kr[PER], vr[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t idx = j * 256 + tid;
+    const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
+    const uint32_t tt = t0 + t;
+    kr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    vr[j] = kr[j];
+    if (tt < lo) {
+      kr[j] = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
+      vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
+    }
+  }
+  // 3. q: QK-norm (optional) + rotation
+  if (wave < rep) {
+    float x0 = qv.x, x1 = qv.y;
+    if (a.q_norm) {
+      const float ss = wave_sum(x0 * x0 + x1 * x1);
+      const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(HD)), a.eps)));
+      x0 = __fmul_rn(__fmul_rn(x0, sc), qn.x);
+      x1 = __fmul_rn(__fmul_rn(x1, sc), qn.y);
+    }
+    if (qlane) {
+      qs[wave][2 * lane] = __fsub_rn(__fmul_rn(x0, rp.x), __fmul_rn(x1, rp.y));
+      qs[wave][2 * lane + 1] = __fadd_rn(__fmul_rn(x0, rp.y), __fmul_rn(x1, rp.x));
+    }
+  }
+  // 4. k / v of this launch's positions inside the chunk (at most 4)
+  for (uint32_t tt = lo + wave; tt < t1; tt += GEMV_WAVES) {
+    const float* r2 = a.qkv + size_t(tt - base) * width;
+    head_norm_rope(r2 + size_t(a.H + g) * HD, a.k_norm, a.eps, a.rope + size_t(tt) * (HD / 2), HD, lane,
+                   knew[tt - lo]);
+    const float* vs = r2 + size_t(a.H + a.Hkv + g) * HD;
+    for (uint32_t i = lane; i < HD; i += 64) vnew[tt - lo][i] = vs[i];
+  }
+  // 5. tiles to LDS
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t idx = j * 256 + tid;
+    const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
+    kt[t * KS + d] = kr[j].x;
+    kt[t * KS + d + 1] = kr[j].y;
+    kt[t * KS + d + 2] = kr[j].z;
+    kt[t * KS + d + 3] = kr[j].w;
+    *reinterpret_cast<float4*>(&vt[t * HD + d]) = vr[j];
+  }
+  __syncthreads();
+  for (uint32_t tt = lo; tt < t1; ++tt) {
+    const uint32_t tn = tt - t0;
+    for (uint32_t i = tid; i < HD; i += 256) {
+      kt[tn * KS + i] = knew[tt - lo][i];
+      vt[tn * HD + i] = vnew[tt - lo][i];
+      if (tt == pos) {  // SlowArKvCache::write_token for this column's position
+        a.k_cache[(size_t(g) * a.max_seq + pos) * HD + i] = knew[tt - lo][i];
+        a.v_cache[(size_t(g) * a.max_seq + pos) * HD + i] = vnew[tt - lo][i];
+      }
+    }
+  }
+  __syncthreads();
+  // 6. scores (lane = position) and chunk softmax
+  float m = -INFINITY, l = 0.0f;
+  if (wave < rep) {
+    float s = -INFINITY;
+    if (lane < nt) {
+      float dsum = 0.0f;
+#pragma unroll 16
+      for (int d = 0; d < HD; ++d) dsum = fmaf(qs[wave][d], kt[lane * KS + d], dsum);
+      s = dsum * a.scale;
+    }
+    m = wave_max(s);
+    const float p = (lane < nt) ? expf(s - m) : 0.0f;
+    l = wave_sum(p);
+    if (lane < CH) ps[wave][lane] = p;
+  }
+  __syncthreads();
+  // 7. PV (lane = head-dim element)
+  if (wave < rep) {
+    const uint32_t h = g * rep + wave;
+    float o[HD / 64];
+#pragma unroll
+    for (int j = 0; j < HD / 64; ++j) o[j] = 0.0f;
+    for (uint32_t t = 0; t < nt; ++t) {
+      const float pv = ps[wave][t];
+#pragma unroll
+      for (int j = 0; j < HD / 64; ++j) o[j] = fmaf(pv, vt[t * HD + lane + 64 * j], o[j]);
+    }
+    if (nch == 1) {
+      float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
+      const float inv = 1.0f / l;
+#pragma unroll
+      for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = o[j] * inv;
+    } else {
+      float* part = a.part + (((size_t(col) * a.Hkv + g) * a.max_chunks + chunk) * rep + wave) * (HD + 2);
+      if (lane == 0) {
+        part[0] = m;
+        part[1] = l;
+      }
+#pragma unroll
+      for (int j = 0; j < HD / 64; ++j) part[2 + lane + 64 * j] = o[j];
+    }
+  }
+}
+
+// Combine of the per-chunk (max, sum, o) partials: grid (H, ncol), HD threads.
+template <int HD, int CH>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
+  const uint32_t h = blockIdx.x, col = blockIdx.y, d = threadIdx.x;
+  const uint32_t done = a.done ? *a.done : 0u;
+  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
+  if (done || pos >= a.max_seq) return;
+  const uint32_t nch = (pos + CH) / CH;
+  if (nch <= 1) return;
+  const uint32_t rep = a.H / a.Hkv, g = h / rep, w = h % rep;
+  const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks * rep + w) * (HD + 2);
+  const size_t stride = size_t(rep) * (HD + 2);
+  float M = -INFINITY;
+  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, pbase[c * stride]);
+  float L = 0.0f, acc = 0.0f;
+  for (uint32_t c = 0; c < nch; ++c) {
+    const float* pc = pbase + c * stride;
+    const float f = expf(pc[0] - M);
+    L = fmaf(pc[1], f, L);
+    acc = fmaf(pc[2 + d], f, acc);
+  }
+  a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
+}
+
+// ---------------------------------------------------------------------------
 // Slow-AR embedding (time-major ids) -- one block per token.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
@@ -1593,14 +1769,36 @@ hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+uint32_t attention_chunks(uint32_t max_seq, uint32_t mode) {
+  const uint32_t ch = mode == ATTN_FUSED ? 64u : 32u;
+  return (max_seq + ch - 1) / ch;
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  if (a.H % a.Hkv || a.H / a.Hkv > 4 || !a.counters || a.ncol > 4) return hipErrorInvalidValue;
+  if (a.H % a.Hkv || a.H / a.Hkv > 4 || a.ncol > 4) return hipErrorInvalidValue;
+  if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
   const dim3 grid(a.max_chunks, a.Hkv, a.ncol);
+  if (a.mode == ATTN_FUSED) {
+    if (!a.counters) return hipErrorInvalidValue;
+    switch (a.hd) {
+      case 64: hipLaunchKernelGGL(attn_fused_kernel<64>, grid, dim3(256), 0, s, a); break;
+      case 128: hipLaunchKernelGGL(attn_fused_kernel<128>, grid, dim3(256), 0, s, a); break;
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   switch (a.hd) {
-    case 64: hipLaunchKernelGGL(attn_fused_kernel<64>, grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL(attn_fused_kernel<128>, grid, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attn_partial_kernel<64, 32>), grid, dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((attn_partial_kernel<128, 32>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.max_chunks == 1) return e;
+  const dim3 cgrid(a.H, a.ncol);
+  if (a.hd == 64)
+    hipLaunchKernelGGL((attn_combine_kernel<64, 32>), cgrid, dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_combine_kernel<128, 32>), cgrid, dim3(128), 0, s, a);
   return hipGetLastError();
 }
 
