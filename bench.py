@@ -13,6 +13,7 @@ the library).  Prints one JSON line.
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -52,6 +53,24 @@ def frame_bytes(spec, shape, avg_t, kv_bytes=4):
     return slow + fast
 
 
+def counter_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed FETCH_SIZE and
+    WRITE_SIZE summaries (rocprofv3 --pmc, calibrated against a plain copy),
+    or None when no summary exists for this kernel and workload."""
+    path = os.path.join(ROOT, "profiles", f"counters_{kernel}_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    got = {}
+    with open(path) as f:
+        for line in f:
+            m = re.match(r"(FETCH_SIZE|WRITE_SIZE): .* kernel bytes/launch (\d+)", line)
+            if m:
+                got[m.group(1)] = int(m.group(2))
+    if set(got) != {"FETCH_SIZE", "WRITE_SIZE"}:
+        return None
+    return got["FETCH_SIZE"] + got["WRITE_SIZE"]
+
+
 def cpu_baseline(path, shape, threads, prompt_len, frames):
     """The oracle in faithful mode (per-step Slow layer reload + f32 expansion,
     Fast-AR prefix recompute, row-parallel f32 linears) on a bounded sample."""
@@ -70,6 +89,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="frames in the timed run (default: workload's)")
+    ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: workload's)")
     ap.add_argument("--warmup", type=int, default=1, help="untimed warm-up generations")
     ap.add_argument("--workload", default="full", choices=sorted(WORKLOADS))
     ap.add_argument("--model-dir", default=os.environ.get("S2HIP_MODEL_DIR", "/tmp/s2hip_models"))
@@ -88,7 +108,9 @@ def main():
     shape_name, prompt_len, frames, max_seq, temp, top_p, top_k = WORKLOADS[args.workload]
     if args.steps:
         frames = args.steps
-        max_seq = max(max_seq, prompt_len + frames)
+    if args.prompt:
+        prompt_len = args.prompt
+    max_seq = max(max_seq, prompt_len + frames)
     shape = synth.SHAPES[shape_name]
     t0 = time.time()
     os.environ.setdefault("S2SYNTH_PROGRESS", "1")
@@ -117,7 +139,7 @@ def main():
     log(f"{kern}: {us:.2f} us/launch, {kb / 1e6:.2f} MB -> {achieved:.0f} GB/s")
     other = {}
     for k in ("slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn", "fast_head",
-              "sample_fast", "sample_slow", "fast_frame", "empty"):
+              "sample_fast", "sample_slow", "fast_frame", "empty", "hbm_copy"):
         ku, kbb = eng.time_kernel(k, reps=5)
         other[k] = {"us": round(ku, 3)}
         if kbb:
@@ -160,7 +182,7 @@ def main():
         "frame_roofline_frac": round(fb * fps / (HBM_PEAK_GBS * 1e9), 4),
         "roofline": {"bound": "hbm", "kernel": f"gemv {kern} (fused RMSNorm + w1/w3 + SwiGLU)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": counter_traffic(kern, args.workload),
                      "bytes_per_launch": round(kb), "avg_us": round(us, 3)},
         "kernels": other,
         "cpu_baseline": cpu,

@@ -312,6 +312,10 @@ Engine::Engine(const s2hip_config& cfg) {
   // activations
   const uint32_t NC = PREFILL_COLS;
   const uint64_t qkv_w = q + 2 * kv;
+  // two attention kernels per layer (partials, then merge) by default; with
+  // S2HIP_ATTN_FUSED=1 one kernel whose last block per kv head merges (its
+  // store-wait + counter + reload chain measures slower than the kernel
+  // boundary it replaces: 18.7 vs 13.2 us at T = 384 on the S2-Pro shape)
   attn_mode_ = getenv("S2HIP_ATTN_FUSED") ? ATTN_FUSED : ATTN_SPLIT;
   attn_chunks_ = attention_chunks(s.max_seq_len, attn_mode_);
   h_ = dalloc<float>(size_t(NC) * s.dim);
@@ -1105,6 +1109,17 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   HIPC(hipMemsetAsync(h_, 0, size_t(PREFILL_COLS) * s.dim * 4, stream_));
   HIPC(hipMemsetAsync(att_, 0, size_t(PREFILL_COLS) * q * 4, stream_));
   HIPC(hipMemsetAsync(act_, 0, size_t(PREFILL_COLS) * s.ffn * 4, stream_));
+  // hbm_copy: a 256 MiB device-to-device copy (counter calibration)
+  constexpr size_t COPY_BYTES = size_t(256) << 20;
+  std::unique_ptr<TmpBuf> copy_a, copy_b;
+  void *copy_src = nullptr, *copy_dst = nullptr;
+  if (name == "hbm_copy") {
+    copy_a.reset(new TmpBuf(COPY_BYTES));
+    copy_b.reset(new TmpBuf(COPY_BYTES));
+    copy_src = copy_a->p;
+    copy_dst = copy_b->p;
+    HIPC(hipMemsetAsync(copy_src, 0, COPY_BYTES, stream_));
+  }
   auto pass = [&](uint32_t l) {
     const SlowLayer& L = slow_[l];
     if (name == "slow_w13")
@@ -1164,6 +1179,8 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
       enqueue_fast_frame(SamplerCfg{0.0f, 1.0f, 0}, nullptr);
     } else if (name == "empty") {
       HIPC(launch_add_position(st_, 0, stream_));
+    } else if (name == "hbm_copy") {
+      HIPC(launch_copy(copy_src, copy_dst, COPY_BYTES, stream_));
     }
     else if (name == "slow_head")
       gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, s.semantic_begin, head_extra_,
@@ -1179,6 +1196,7 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   else if (name == "slow_wo") b = double(L0.wo.bytes) + 4.0 * (q + s.dim);
   else if (name == "slow_w2") b = double(L0.w2.bytes) + 4.0 * (s.ffn + s.dim);
   else if (name == "slow_head") b = double(n_cand_) * s.dim * 2 + 4.0 * (s.dim + n_cand_);
+  else if (name == "hbm_copy") b = 2.0 * double(COPY_BYTES);
   const bool per_layer = name.rfind("slow_", 0) == 0 && name != "slow_head" && name != "sample_slow";
   const uint32_t layers = per_layer || name == "fast_attn" ? s.slow_layers : 1u;
   if (name == "fast_frame" || name == "sample_fast" || name == "sample_slow" || name == "empty") {

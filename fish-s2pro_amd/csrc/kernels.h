@@ -106,7 +106,7 @@ struct AttnArgs {
   uint32_t pos_offset;
   uint32_t H, Hkv, hd, max_seq, ncol;
   uint32_t max_chunks;     // attention_chunks(max_seq, mode)
-  uint32_t mode;           // ATTN_SPLIT: partial + combine kernels; ATTN_FUSED: one kernel
+  uint32_t mode;           // ATTN_SPLIT: partial + merge kernels; ATTN_FUSED: one kernel, last block merges
   float scale;
   const uint32_t* done;
   uint32_t* err;
@@ -171,5 +171,7 @@ hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_byte
 
 hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n, int fast, hipStream_t s);
 hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s);
+// Plain device copy (bytes and both pointers 16-byte aligned).
+hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
 
 }  // namespace s2

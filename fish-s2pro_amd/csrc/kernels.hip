@@ -688,160 +688,147 @@ hipError_t gemv_k_launch(const GemvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV, LDS variant: x (and the RMSNorm gain) are loaded first, staged
-// in LDS and shared by the block's waves; the weight loads are issued before
-// the barrier so it overlaps their HBM latency.  Each wave derives the norm
-// scale from the staged x.
+// Decode GEMV with an RMS-normalised input, x shared through LDS.
+//   Each wave loads only the 512-element steps k = wave (mod WPB) of x and of
+//   the gain, then issues all of its weight loads; the block reduces the sum of
+//   squares, writes x * scale * gain once to LDS, and every wave reads the
+//   normalised x from there.  The x / gain loads are issued first, so the
+//   waits before the two barriers cover them and not the weights (vector
+//   memory counters retire in order), and the LDS staging overlaps the HBM
+//   latency of the weight rows.  One row (two for SwiGLU: w1 and w3) per wave.
 // ---------------------------------------------------------------------------
-template <uint32_t WT, int NCOL, int R, int EPI, int KIT, int WPB>
-__global__ __launch_bounds__(64 * WPB) void gemv_l_kernel(GemvArgs a) {
+template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB>
+__global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
-  constexpr int NT = 64 * WPB;
-  __shared__ float xs[NCOL][IN];
-  __shared__ float gs[IN];
-  const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
-  const uint32_t row0 = (blockIdx.x * WPB + wave) * R;
-  // 1. x / gain loads (16 B per thread per step)
-  constexpr int XS = (IN / 4 + NT - 1) / NT;
-  float4 xv4[NCOL][XS];
-  float4 gv4[XS];
+  constexpr int KW = (KIT + WPB - 1) / WPB;
+  __shared__ float4 xs[NCOL][IN / 4];
+  __shared__ float red[NCOL][WPB];
+  const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+  const uint32_t row = blockIdx.x * WPB + wave;
+
+  // 1. this wave's steps of x and of the gain (steps past KIT re-read the last
+  //    step; they are not used)
+  float4 xv[NCOL][KW][2], gv[KW][2];
 #pragma unroll
-  for (int j = 0; j < XS; ++j) {
-    const uint32_t i = (j * NT + tid) * 4;
-    if (i < IN) {
+  for (int j = 0; j < KW; ++j) {
+    const int k = min(wave + j * WPB, KIT - 1);
+    const uint32_t e = k * 512 + lane * 8;
 #pragma unroll
-      for (int c = 0; c < NCOL; ++c) xv4[c][j] = *reinterpret_cast<const float4*>(a.x + size_t(c) * a.ldx + i);
-      if (a.norm) gv4[j] = *reinterpret_cast<const float4*>(a.norm + i);
+    for (int c = 0; c < NCOL; ++c) {
+      const float* xc = a.x + size_t(c) * a.ldx + e;
+      xv[c][j][0] = *reinterpret_cast<const float4*>(xc);
+      xv[c][j][1] = *reinterpret_cast<const float4*>(xc + 4);
     }
+    gv[j][0] = *reinterpret_cast<const float4*>(a.norm + e);
+    gv[j][1] = *reinterpret_cast<const float4*>(a.norm + e + 4);
   }
-  // 2. weight loads
-  const uint8_t* rp[R];
-  const uint8_t* rp3[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    uint32_t lr = row0 + r;
-    if (lr >= a.out) lr = 0;
-    const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
-    rp[r] = a.w + size_t(wr) * a.row_bytes;
-    rp3[r] = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
-  }
-  Raw8<WT> wb[R][KIT];
-  Raw8<WT> wb3[DUAL ? R : 1][KIT];
+  // 2. weight loads of the wave's row
+  uint32_t lr = row < a.out ? row : a.out - 1;  // clamp; result discarded
+  const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
+  const uint8_t* rp = a.w + size_t(wr) * a.row_bytes;
+  const uint8_t* rp3 = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  Raw8<WT> wb[KIT];
+  Raw8<WT> wb3[DUAL ? KIT : 1];
 #pragma unroll
   for (int k = 0; k < KIT; ++k) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      wb[r][k] = load_raw<WT>(rp[r], k * 512 + lane * 8);
-      if constexpr (DUAL) wb3[r][k] = load_raw<WT>(rp3[r], k * 512 + lane * 8);
-    }
+    wb[k] = load_raw<WT>(rp, k * 512 + lane * 8);
+    if constexpr (DUAL) wb3[k] = load_raw<WT>(rp3, k * 512 + lane * 8);
   }
   const uint32_t done = a.done ? __builtin_nontemporal_load(a.done) : 0u;
-  // 3. stage (waits only for the x / gain loads)
+  // 3. block sum of squares -> scale
 #pragma unroll
-  for (int j = 0; j < XS; ++j) {
-    const uint32_t i = (j * NT + tid) * 4;
-    if (i < IN) {
+  for (int c = 0; c < NCOL; ++c) {
+    float ss = 0.0f;
 #pragma unroll
-      for (int c = 0; c < NCOL; ++c) *reinterpret_cast<float4*>(&xs[c][i]) = xv4[c][j];
-      if (a.norm) *reinterpret_cast<float4*>(&gs[i]) = gv4[j];
+    for (int j = 0; j < KW; ++j) {
+      if (wave + j * WPB < KIT) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4 u = xv[c][j][h];
+          ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[c][wave] = ss;
+  }
+  __syncthreads();
+  // 4. normalised x into LDS
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WPB; ++i) tot += red[c][i];
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), a.eps)));
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+      const int k = wave + j * WPB;
+      if (k < KIT) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float4 u = xv[c][j][h];
+          const float4 g = gv[j][h];
+          u.x = __fmul_rn(__fmul_rn(u.x, scale), g.x);
+          u.y = __fmul_rn(__fmul_rn(u.y, scale), g.y);
+          u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
+          u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
+          xs[c][(k * 512 + lane * 8) / 4 + h] = u;
+        }
+      }
     }
   }
   __syncthreads();
   if (done) return;
-  float scale[NCOL];
+  // 5. dot products against the LDS copy
+  float acc[NCOL], acc3[NCOL];
 #pragma unroll
-  for (int c = 0; c < NCOL; ++c) {
-    scale[c] = 1.0f;
-    if (a.norm) {
-      float ss = 0.0f;
-#pragma unroll
-      for (int k = 0; k < KIT; ++k) {
-        const float4 u = *reinterpret_cast<const float4*>(&xs[c][k * 512 + lane * 8]);
-        const float4 v = *reinterpret_cast<const float4*>(&xs[c][k * 512 + lane * 8 + 4]);
-        ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
-        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-      }
-      ss = wave_sum(ss);
-      scale[c] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(IN)), a.eps)));
-    }
-  }
-  float acc[R][NCOL];
-  float acc3[R][NCOL];
-#pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-      acc[r][c] = 0.0f;
-      acc3[r][c] = 0.0f;
-    }
+  for (int c = 0; c < NCOL; ++c) acc[c] = acc3[c] = 0.0f;
 #pragma unroll
   for (int k = 0; k < KIT; ++k) {
-    const uint32_t e = k * 512 + lane * 8;
-    float w[R][8];
-    float w3[DUAL ? R : 1][8];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      decode8<WT>(wb[r][k], w[r]);
-      if constexpr (DUAL) decode8<WT>(wb3[r][k], w3[r]);
-    }
-    float g[8];
-    if (a.norm) {
-      const float4 ga = *reinterpret_cast<const float4*>(&gs[e]);
-      const float4 gb = *reinterpret_cast<const float4*>(&gs[e + 4]);
-      g[0] = ga.x; g[1] = ga.y; g[2] = ga.z; g[3] = ga.w;
-      g[4] = gb.x; g[5] = gb.y; g[6] = gb.z; g[7] = gb.w;
-    }
+    float w[8], w3[8];
+    decode8<WT>(wb[k], w);
+    if constexpr (DUAL) decode8<WT>(wb3[k], w3);
 #pragma unroll
     for (int c = 0; c < NCOL; ++c) {
-      const float4 xa = *reinterpret_cast<const float4*>(&xs[c][e]);
-      const float4 xb = *reinterpret_cast<const float4*>(&xs[c][e + 4]);
-      float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-      if (a.norm) {
+      const float4 xa = xs[c][(k * 512 + lane * 8) / 4];
+      const float4 xb = xs[c][(k * 512 + lane * 8) / 4 + 1];
+      const float xv8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = __fmul_rn(__fmul_rn(xv[i], scale[c]), g[i]);
-      }
+      for (int i = 0; i < 8; ++i) acc[c] = fmaf(w[i], xv8[i], acc[c]);
+      if constexpr (DUAL) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[r][c] = fmaf(w[r][i], xv[i], acc[r][c]);
-        if constexpr (DUAL) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc3[r][c] = fmaf(w3[r][i], xv[i], acc3[r][c]);
-        }
+        for (int i = 0; i < 8; ++i) acc3[c] = fmaf(w3[i], xv8[i], acc3[c]);
       }
     }
   }
+  // 6. epilogue
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-#pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-      const float gsum = wave_sum(acc[r][c]);
-      float u = 0.0f;
-      if constexpr (DUAL) u = wave_sum(acc3[r][c]);
-      const uint32_t lr = row0 + r;
-      if (lane == 0 && lr < a.out) {
-        float* dst = a.y + size_t(c) * a.ldy + lr;
-        if constexpr (EPI == EPI_STORE) {
-          *dst = gsum;
-        } else if constexpr (EPI == EPI_RESID) {
-          *dst = __fadd_rn(*dst, gsum);
-        } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
-          *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
-        } else {
-          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
-        }
+  for (int c = 0; c < NCOL; ++c) {
+    const float gsum = wave_sum(acc[c]);
+    float u = 0.0f;
+    if constexpr (DUAL) u = wave_sum(acc3[c]);
+    if (lane == 0 && row < a.out) {
+      float* dst = a.y + size_t(c) * a.ldy + row;
+      if constexpr (EPI == EPI_STORE) {
+        *dst = gsum;
+      } else if constexpr (EPI == EPI_RESID) {
+        *dst = __fadd_rn(*dst, gsum);
+      } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+        *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
+      } else {
+        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
       }
     }
   }
 }
 
-template <uint32_t WT, int NCOL, int R, int EPI, int KIT, int WPB>
-hipError_t gemv_l_launch(const GemvArgs& a, hipStream_t s) {
-  const uint32_t rows_per_block = WPB * R;
-  const dim3 grid((a.out + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL((gemv_l_kernel<WT, NCOL, R, EPI, KIT, WPB>), grid, dim3(64 * WPB), 0, s, a);
+template <uint32_t WT, int NCOL, int EPI, int KIT>
+hipError_t gemv_n_launch(const GemvArgs& a, hipStream_t s) {
+  constexpr int WPB = 8;
+  const dim3 grid((a.out + WPB - 1) / WPB);
+  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB>), grid, dim3(64 * WPB), 0, s, a);
   return hipGetLastError();
 }
 
@@ -851,6 +838,14 @@ template <uint32_t WT, int NCOL, int EPI>
 hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr int RS = DUAL ? 1 : 2;  // rows per wave for short rows
+  if (a.norm) {
+    switch (a.in) {
+      case 512: return gemv_n_launch<WT, NCOL, EPI, 1>(a, s);
+      case 1536: return gemv_n_launch<WT, NCOL, EPI, 3>(a, s);
+      case 2560: return gemv_n_launch<WT, NCOL, EPI, 5>(a, s);
+      default: break;
+    }
+  }
   switch (a.in) {
     case 512: return gemv_k_launch<WT, NCOL, RS, EPI, 1, 4>(a, s);
     case 1536: return gemv_k_launch<WT, NCOL, RS, EPI, 3, 4>(a, s);
@@ -948,170 +943,24 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Fused decode attention for one layer: QK-norm + RoPE of the new position,
-// KV append, split-T GQA attention and the cross-chunk combine.
-//   grid (max_chunks, Hkv, ncol), 256 threads; block (c, g, col) owns cache
-//   positions [64c, 64c + 64) of kv head g for query column col, wave w serves
-//   q head g*rep + w.  K/V tiles are staged in LDS with coalesced loads; the
-//   last block to finish a (col, g) pair (device-scope counter) merges the
-//   per-chunk (max, sum, o) partials and resets the counter for the next launch.
+// Decode attention for one layer: QK-norm + RoPE of the new positions, KV
+// append, split-T GQA attention over the cache, cross-chunk combine.
+//   grid (max_chunks, Hkv, ncol), 256 threads; block (c, g, col) covers cache
+//   positions [CH c, CH c + CH) of kv head g for query column col, and wave w
+//   serves q head g * rep + w.  Every load that does not depend on the
+//   position goes out first and together: the state words, the q rows and the
+//   whole K/V tile (every tile position lies inside the cache, so the tile is
+//   read before the position is known and positions past it are ignored).
+//   Positions of this launch's own columns are recomputed from their qkv rows
+//   (another block may still be appending them).  With one chunk the block
+//   writes the output.  Otherwise it writes its (max, sum, o) partial and:
+//     LAST = false: attn_combine_kernel merges the partials afterwards;
+//     LAST = true:  the partials are written with agent-scope atomic stores
+//       (coherent across the XCD L2s without a cache write-back), a counter
+//       per (col, g) elects the last block of the pair, which merges them with
+//       agent-scope loads and resets the counter for the next launch.
 // ---------------------------------------------------------------------------
-template <int HD>
-__global__ __launch_bounds__(256) void attn_fused_kernel(AttnArgs a) {
-  constexpr int CH = 64;
-  constexpr int KS = HD + 1;  // padded K row: lane-per-position reads hit distinct banks
-  __shared__ float kt[CH * KS];
-  __shared__ float vt[CH * HD];
-  __shared__ float qs[GEMV_WAVES][HD];
-  __shared__ float ps[GEMV_WAVES][CH];
-  __shared__ float knew[4][HD], vnew[4][HD];  // positions of this launch's columns
-  __shared__ uint32_t last_flag;
-  if (a.done && *a.done) return;
-  const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
-  if (pos >= a.max_seq) {
-    if (tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
-    return;
-  }
-  const uint32_t T = pos + 1;
-  const uint32_t nch = (T + CH - 1) / CH;
-  if (chunk >= nch) return;
-  const uint32_t t0 = chunk * CH, t1 = min(T, t0 + CH), nt = t1 - t0;
-  const uint32_t rep = a.H / a.Hkv;
-  const float* row = a.qkv + size_t(col) * (a.H + 2 * a.Hkv) * HD;
-  const float2* rope_row = a.rope + size_t(pos) * (HD / 2);
-  float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
-  float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
-  // Positions [base, pos] belong to this launch's columns: their K/V come
-  // from the qkv rows (another block may still be writing them to the cache).
-  const uint32_t base = pos - col;
-  const uint32_t lo = max(t0, base);
-
-  if (wave < rep) head_norm_rope(row + size_t(g * rep + wave) * HD, a.q_norm, a.eps, rope_row, HD, lane, qs[wave]);
-  for (uint32_t tt = lo + wave; tt < t1; tt += GEMV_WAVES) {
-    const float* r2 = a.qkv + size_t(tt - base) * (a.H + 2 * a.Hkv) * HD;
-    head_norm_rope(r2 + size_t(a.H + g) * HD, a.k_norm, a.eps, a.rope + size_t(tt) * (HD / 2), HD, lane,
-                   knew[tt - lo]);
-    const float* vs = r2 + size_t(a.H + a.Hkv + g) * HD;
-    for (uint32_t i = lane; i < HD; i += 64) vnew[tt - lo][i] = vs[i];
-  }
-  // K/V tiles of the cached positions
-  for (uint32_t idx = tid; idx < CH * HD / 4; idx += 256) {
-    const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
-    const uint32_t tt = t0 + t;
-    float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
-    if (tt < lo) {
-      k4 = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
-      v4 = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
-    }
-    kt[t * KS + d] = k4.x;
-    kt[t * KS + d + 1] = k4.y;
-    kt[t * KS + d + 2] = k4.z;
-    kt[t * KS + d + 3] = k4.w;
-    *reinterpret_cast<float4*>(&vt[t * HD + d]) = v4;
-  }
-  __syncthreads();
-  for (uint32_t tt = lo; tt < t1; ++tt) {
-    const uint32_t tn = tt - t0;
-    for (uint32_t i = tid; i < HD; i += 256) {
-      kt[tn * KS + i] = knew[tt - lo][i];
-      vt[tn * HD + i] = vnew[tt - lo][i];
-      if (tt == pos) {  // SlowArKvCache::write_token for this column's position
-        kc[size_t(pos) * HD + i] = knew[tt - lo][i];
-        vc[size_t(pos) * HD + i] = vnew[tt - lo][i];
-      }
-    }
-  }
-  __syncthreads();
-
-  float m = -INFINITY, l = 0.0f;
-  if (wave < rep) {
-    float s = -INFINITY;
-    if (lane < nt) {
-      float dsum = 0.0f;
-#pragma unroll 16
-      for (int d = 0; d < HD; ++d) dsum = fmaf(qs[wave][d], kt[lane * KS + d], dsum);
-      s = dsum * a.scale;
-    }
-    m = wave_max(s);
-    const float p = (lane < nt) ? expf(s - m) : 0.0f;
-    l = wave_sum(p);
-    ps[wave][lane] = p;
-  }
-  __syncthreads();
-  const uint32_t h = g * rep + wave;
-  float o[HD / 64];
-  if (wave < rep) {
-#pragma unroll
-    for (int j = 0; j < HD / 64; ++j) o[j] = 0.0f;
-    for (uint32_t t = 0; t < nt; ++t) {
-      const float pv = ps[wave][t];
-#pragma unroll
-      for (int j = 0; j < HD / 64; ++j) o[j] = fmaf(pv, vt[t * HD + lane + 64 * j], o[j]);
-    }
-    if (nch == 1) {
-      float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
-      const float inv = 1.0f / l;
-#pragma unroll
-      for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = o[j] * inv;
-    } else {
-      float* part = a.part + (((size_t(col) * a.Hkv + g) * a.max_chunks + chunk) * rep + wave) * (HD + 2);
-      if (lane == 0) {
-        part[0] = m;
-        part[1] = l;
-      }
-#pragma unroll
-      for (int j = 0; j < HD / 64; ++j) part[2 + lane + 64 * j] = o[j];
-    }
-  }
-  if (nch == 1) return;
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t* ctr = a.counters + size_t(col) * a.Hkv + g;
-    const uint32_t old = atomicAdd(ctr, 1u);
-    last_flag = (old == nch - 1) ? 1u : 0u;
-    if (last_flag) atomicExch(ctr, 0u);
-  }
-  __syncthreads();
-  if (!last_flag) return;
-  __threadfence();
-  if (wave < rep) {
-    const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks) * rep * (HD + 2);
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; ++c)
-      M = fmaxf(M, pbase[(size_t(c) * rep + wave) * (HD + 2)]);
-    float L = 0.0f, acc[HD / 64];
-#pragma unroll
-    for (int j = 0; j < HD / 64; ++j) acc[j] = 0.0f;
-    for (uint32_t c = 0; c < nch; ++c) {
-      const float* pc = pbase + (size_t(c) * rep + wave) * (HD + 2);
-      const float mc = pc[0];
-      const float lc = pc[1];
-      const float f = expf(mc - M);
-      L = fmaf(lc, f, L);
-#pragma unroll
-      for (int j = 0; j < HD / 64; ++j)
-        acc[j] = fmaf(pc[2 + lane + 64 * j], f, acc[j]);
-    }
-    float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
-    const float inv = 1.0f / L;
-#pragma unroll
-    for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = acc[j] * inv;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Decode attention, two-kernel form (partials + combine).  Partial kernel:
-// grid (max_chunks, Hkv, ncol), 256 threads; block (c, g, col) covers cache
-// positions [CH c, CH c + CH).  Every global load goes out before any wait:
-// first the q-side operands, then the K/V tile of cached positions into
-// registers, then the k/v rows of positions that belong to this launch's
-// columns (their cache rows may still be in flight in another block).
-// With a single chunk the block writes the final output itself.
-// ---------------------------------------------------------------------------
-template <int HD, int CH>
+template <int HD, int CH, bool LAST>
 __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   constexpr int KS = HD + 1;
   constexpr int PER = CH * HD / 4 / 256;  // float4 per thread per tile
@@ -1121,10 +970,35 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   __shared__ float qs[GEMV_WAVES][HD];
   __shared__ float ps[GEMV_WAVES][CH];
   __shared__ float knew[4][HD], vnew[4][HD];
+  __shared__ uint32_t is_last;
   const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t rep = a.H / a.Hkv;
+  const uint32_t width = (a.H + 2 * a.Hkv) * HD;
+  const float* row = a.qkv + size_t(col) * width;
+  const float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
+  const float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
+  const uint32_t t0 = chunk * CH;
+
+  // 0. position-independent loads, all in flight together
   const uint32_t done = a.done ? *a.done : 0u;
-  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
+  const uint32_t pbase = a.pos_ptr ? *a.pos_ptr : 0u;
+  const bool qlane = wave < rep && lane < HD / 2;
+  float2 qv = make_float2(0.f, 0.f), qn = make_float2(1.f, 1.f);
+  if (qlane) {
+    qv = *reinterpret_cast<const float2*>(row + size_t(g * rep + wave) * HD + 2 * lane);
+    if (a.q_norm) qn = *reinterpret_cast<const float2*>(a.q_norm + 2 * lane);
+  }
+  float4 kr[PER], vr[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t idx = j * 256 + tid;
+    const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
+    const uint32_t tt = min(t0 + t, a.max_seq - 1);
+    kr[j] = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
+    vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
+  }
+  const uint32_t pos = pbase + a.pos_offset + col;
   if (done) return;
   if (pos >= a.max_seq) {
     if (tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
@@ -1133,40 +1007,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const uint32_t T = pos + 1;
   const uint32_t nch = (T + CH - 1) / CH;
   if (chunk >= nch) return;
-  const uint32_t t0 = chunk * CH, t1 = min(T, t0 + CH), nt = t1 - t0;
-  const uint32_t rep = a.H / a.Hkv;
-  const uint32_t width = (a.H + 2 * a.Hkv) * HD;
-  const uint32_t base = pos - col;          // first position of this launch
+  const uint32_t t1 = min(T, t0 + CH), nt = t1 - t0;
+  const uint32_t base = pos - col;             // first position of this launch
   const uint32_t lo = max(t0, min(base, t1));  // [lo, t1): positions of this launch
-  const float* row = a.qkv + size_t(col) * width;
-  const float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
-  const float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
 
-  // 1. q-side operands: lane = rotation pair
-  const bool qlane = wave < rep && lane < HD / 2;
-  float2 qv = make_float2(0.f, 0.f), qn = make_float2(1.f, 1.f), rp = make_float2(1.f, 0.f);
-  if (qlane) {
-    qv = *reinterpret_cast<const float2*>(row + size_t(g * rep + wave) * HD + 2 * lane);
-    if (a.q_norm) qn = *reinterpret_cast<const float2*>(a.q_norm + 2 * lane);
-    rp = a.rope[size_t(pos) * (HD / 2) + lane];
-  }
-  // 2. K/V tile of cached positions, into registers
-  float4 kr[PER], vr[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const uint32_t idx = j * 256 + tid;
-    const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
-    const uint32_t tt = t0 + t;
-    kr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    vr[j] = kr[j];
-    if (tt < lo) {
-      kr[j] = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
-      vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
-    }
-  }
-  // 3. q: QK-norm (optional) + rotation
+  // 1. q: QK-norm (optional) + rotation
   if (wave < rep) {
     float x0 = qv.x, x1 = qv.y;
+    const float2 rp = qlane ? a.rope[size_t(pos) * (HD / 2) + lane] : make_float2(1.f, 0.f);
     if (a.q_norm) {
       const float ss = wave_sum(x0 * x0 + x1 * x1);
       const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(HD)), a.eps)));
@@ -1178,7 +1026,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       qs[wave][2 * lane + 1] = __fadd_rn(__fmul_rn(x0, rp.y), __fmul_rn(x1, rp.x));
     }
   }
-  // 4. k / v of this launch's positions inside the chunk (at most 4)
+  // 2. k / v of this launch's positions inside the chunk (at most 4)
   for (uint32_t tt = lo + wave; tt < t1; tt += GEMV_WAVES) {
     const float* r2 = a.qkv + size_t(tt - base) * width;
     head_norm_rope(r2 + size_t(a.H + g) * HD, a.k_norm, a.eps, a.rope + size_t(tt) * (HD / 2), HD, lane,
@@ -1186,7 +1034,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     const float* vs = r2 + size_t(a.H + a.Hkv + g) * HD;
     for (uint32_t i = lane; i < HD; i += 64) vnew[tt - lo][i] = vs[i];
   }
-  // 5. tiles to LDS
+  // 3. tile to LDS (positions >= lo are replaced below or unused)
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint32_t idx = j * 256 + tid;
@@ -1210,7 +1058,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  // 6. scores (lane = position) and chunk softmax
+  // 4. scores (lane = position) and chunk softmax
   float m = -INFINITY, l = 0.0f;
   if (wave < rep) {
     float s = -INFINITY;
@@ -1226,7 +1074,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     if (lane < CH) ps[wave][lane] = p;
   }
   __syncthreads();
-  // 7. PV (lane = head-dim element)
+  // 5. PV (lane = head-dim element)
+  float* pair_part = a.part + (size_t(col) * a.Hkv + g) * a.max_chunks * rep * (HD + 2);
   if (wave < rep) {
     const uint32_t h = g * rep + wave;
     float o[HD / 64];
@@ -1243,13 +1092,57 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = o[j] * inv;
     } else {
-      float* part = a.part + (((size_t(col) * a.Hkv + g) * a.max_chunks + chunk) * rep + wave) * (HD + 2);
-      if (lane == 0) {
-        part[0] = m;
-        part[1] = l;
-      }
+      float* part = pair_part + (size_t(chunk) * rep + wave) * (HD + 2);
+      if constexpr (LAST) {
+        if (lane == 0) {
+          __hip_atomic_store(part, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(part + 1, l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
 #pragma unroll
-      for (int j = 0; j < HD / 64; ++j) part[2 + lane + 64 * j] = o[j];
+        for (int j = 0; j < HD / 64; ++j)
+          __hip_atomic_store(part + 2 + lane + 64 * j, o[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (lane == 0) {
+          part[0] = m;
+          part[1] = l;
+        }
+#pragma unroll
+        for (int j = 0; j < HD / 64; ++j) part[2 + lane + 64 * j] = o[j];
+      }
+    }
+  }
+  if constexpr (LAST) {
+    if (nch == 1) return;
+    // 6. the partial stores have completed before the block's arrival is counted
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t* cnt = a.counters + size_t(col) * a.Hkv + g;
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      is_last = prev + 1 == nch;
+      if (prev + 1 == nch) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!is_last) return;
+    // 7. merge: thread i -> (head w, element d) pairs
+    const size_t cstride = size_t(rep) * (HD + 2);
+    for (uint32_t i = tid; i < rep * HD; i += 256) {
+      const uint32_t w = i / HD, d = i % HD;
+      const float* pb = pair_part + size_t(w) * (HD + 2);
+      float M = -INFINITY;
+      for (uint32_t c = 0; c < nch; ++c)
+        M = fmaxf(M, __hip_atomic_load(pb + c * cstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      float L = 0.0f, acc = 0.0f;
+      for (uint32_t c = 0; c < nch; ++c) {
+        const float* pc = pb + c * cstride;
+        const float mc = __hip_atomic_load(pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float lc = __hip_atomic_load(pc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float oc = __hip_atomic_load(pc + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const float f = expf(mc - M);
+        L = fmaf(lc, f, L);
+        acc = fmaf(oc, f, acc);
+      }
+      a.out[size_t(col) * a.H * HD + size_t(g * rep + w) * HD + d] = acc / L;
     }
   }
 }
@@ -1723,6 +1616,14 @@ __global__ void add_position_kernel(DevState* st, uint32_t n) {
   if (threadIdx.x == 0) st->n_past += n;
 }
 
+// Streaming copy of n4 16-byte words: the reference kernel against which HBM
+// byte counters are calibrated (it reads and writes exactly 16 * n4 bytes).
+__global__ __launch_bounds__(256) void copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst,
+                                                   size_t n4) {
+  const size_t stride = size_t(gridDim.x) * 256;
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += stride) dst[i] = src[i];
+}
+
 template <class K>
 hipError_t set_max_lds(K kernel) {
   return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1770,8 +1671,8 @@ hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
 }
 
 uint32_t attention_chunks(uint32_t max_seq, uint32_t mode) {
-  const uint32_t ch = mode == ATTN_FUSED ? 64u : 32u;
-  return (max_seq + ch - 1) / ch;
+  (void)mode;
+  return (max_seq + 31u) / 32u;
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
@@ -1781,15 +1682,15 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.mode == ATTN_FUSED) {
     if (!a.counters) return hipErrorInvalidValue;
     switch (a.hd) {
-      case 64: hipLaunchKernelGGL(attn_fused_kernel<64>, grid, dim3(256), 0, s, a); break;
-      case 128: hipLaunchKernelGGL(attn_fused_kernel<128>, grid, dim3(256), 0, s, a); break;
+      case 64: hipLaunchKernelGGL((attn_partial_kernel<64, 32, true>), grid, dim3(256), 0, s, a); break;
+      case 128: hipLaunchKernelGGL((attn_partial_kernel<128, 32, true>), grid, dim3(256), 0, s, a); break;
       default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
   }
   switch (a.hd) {
-    case 64: hipLaunchKernelGGL((attn_partial_kernel<64, 32>), grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((attn_partial_kernel<128, 32>), grid, dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attn_partial_kernel<64, 32, false>), grid, dim3(256), 0, s, a); break;
+    case 128: hipLaunchKernelGGL((attn_partial_kernel<128, 32, false>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
@@ -1882,6 +1783,17 @@ hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n,
 
 hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s) {
   hipLaunchKernelGGL(add_position_kernel, dim3(1), dim3(64), 0, s, st, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s) {
+  if (bytes % 16 || (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16)
+    return hipErrorInvalidValue;
+  const size_t n4 = bytes / 16;
+  const size_t blocks = std::min<size_t>(4096, (n4 + 255) / 256);
+  if (blocks == 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_kernel, dim3(uint32_t(blocks)), dim3(256), 0, s, static_cast<const float4*>(src),
+                     static_cast<float4*>(dst), n4);
   return hipGetLastError();
 }
 

@@ -1,0 +1,105 @@
+"""Summaries of rocprofv3 CSV output for the decode kernels.
+
+    python3 -m s2hip.profiling stats  <dir>/<run>_kernel_stats.csv [--top N]
+    python3 -m s2hip.profiling counters <dir>/<run>_counter_collection.csv \
+        --kernel REGEX --copy-kernel REGEX --copy-bytes BYTES
+
+`stats` prints rocprofv3's per-kernel table (calls, average / min / max
+duration) with demangled template arguments kept, so a kernel instance can be
+matched against the engine's live timing.
+
+`counters` averages one HBM byte counter (FETCH_SIZE or WRITE_SIZE, reported
+in KiB per dispatch) over every dispatch of the kernel matching --kernel, and
+calibrates it against a plain copy kernel of known size: the copy reads and
+writes exactly --copy-bytes / 2 bytes each way, so
+    scale = (copy_bytes / 2) / (copy counter * 1024)
+and the kernel's HBM bytes per launch = counter * 1024 * scale.
+"""
+
+import argparse
+import csv
+import re
+import statistics
+import sys
+
+
+def _rows(path):
+    with open(path, newline="") as f:
+        return list(csv.DictReader(f))
+
+
+def _col(row, *names):
+    for n in names:
+        if n in row:
+            return row[n]
+    raise KeyError(f"none of {names} in CSV columns {sorted(row)}")
+
+
+def short_name(name):
+    name = re.sub(r"^void ", "", name)
+    name = name.replace("s2::(anonymous namespace)::", "")
+    return name
+
+
+def stats(path, top):
+    rows = _rows(path)
+    out = []
+    for r in rows:
+        out.append((short_name(_col(r, "Name", "KernelName")), int(_col(r, "Calls")),
+                    float(_col(r, "TotalDurationNs")), float(_col(r, "AverageNs")),
+                    float(_col(r, "MinNs")), float(_col(r, "MaxNs")), float(_col(r, "Percentage"))))
+    out.sort(key=lambda t: -t[2])
+    lines = [f"{'kernel':72s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'total_ms':>9s} {'%':>6s}"]
+    for name, calls, tot, avg, mn, mx, pct in out[:top]:
+        lines.append(f"{name[:72]:72s} {calls:7d} {avg / 1e3:9.2f} {mn / 1e3:9.2f} {mx / 1e3:9.2f} "
+                     f"{tot / 1e6:9.2f} {pct:6.2f}")
+    return "\n".join(lines)
+
+
+def counter_mean(rows, kernel_re, counter):
+    pat = re.compile(kernel_re)
+    vals = []
+    for r in rows:
+        if _col(r, "Counter_Name") != counter:
+            continue
+        if pat.search(_col(r, "Kernel_Name")):
+            vals.append(float(_col(r, "Counter_Value")))
+    if not vals:
+        raise SystemExit(f"no {counter} samples for kernels matching {kernel_re!r}")
+    return statistics.fmean(vals), len(vals)
+
+
+def counters(path, kernel_re, copy_re, copy_bytes):
+    rows = _rows(path)
+    names = sorted({_col(r, "Counter_Name") for r in rows})
+    lines = []
+    for counter in names:
+        k, nk = counter_mean(rows, kernel_re, counter)
+        c, nc = counter_mean(rows, copy_re, counter)
+        scale = (copy_bytes / 2) / (c * 1024.0)
+        lines.append(f"{counter}: kernel {k:.1f} KiB/dispatch over {nk} dispatches; copy {c:.1f} KiB/dispatch "
+                     f"over {nc} dispatches (copy moves {copy_bytes / 2 / 1024:.0f} KiB each way); "
+                     f"scale {scale:.4f}; kernel bytes/launch {k * 1024 * scale:.0f}")
+    return "\n".join(lines)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    a = sub.add_parser("stats")
+    a.add_argument("csv")
+    a.add_argument("--top", type=int, default=30)
+    b = sub.add_parser("counters")
+    b.add_argument("csv")
+    b.add_argument("--kernel", required=True)
+    b.add_argument("--copy-kernel", required=True)
+    b.add_argument("--copy-bytes", type=float, required=True)
+    args = ap.parse_args(argv)
+    if args.cmd == "stats":
+        print(stats(args.csv, args.top))
+    else:
+        print(counters(args.csv, args.kernel, args.copy_kernel, args.copy_bytes))
+
+
+if __name__ == "__main__":
+    sys.exit(main())

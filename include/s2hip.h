@@ -165,8 +165,12 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
 /* Measurement: average device time of one launch of a named decode kernel,
  * timed with HIP events on the engine stream over `reps` passes across every
  * layer (so no pass re-reads weights from cache).  kernel: "slow_w13",
- * "slow_wqkv", "slow_wo", "slow_w2", "slow_head".  bytes_per_launch receives
- * the algorithmic HBM bytes of one launch (weights + input + output). */
+ * "slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn",
+ * "fast_head", "sample_fast", "sample_slow", "fast_frame", "empty" (one
+ * one-wave launch), "hbm_copy" (a 256 MiB device copy, the calibration kernel
+ * for HBM byte counters).  bytes_per_launch receives the algorithmic HBM
+ * bytes of one launch (weights + input + output) where defined, else 0.
+ * No counterpart in the reference (a measurement hook). */
 int32_t s2hip_time_kernel(s2hip_engine* engine, const char* kernel, uint32_t reps, double* avg_us,
                           double* bytes_per_launch, char* err, size_t err_cap);
 

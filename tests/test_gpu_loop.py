@@ -158,3 +158,25 @@ def test_errors_match_reference_behaviour(tiny_gguf):
     e.reset()
     r = e.generate_codes(prompt[:11 * 8], 4, min_tokens_before_end=100)
     assert r["n_frames"] == 4
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_attention_modes_match_oracle(tiny_gguf, monkeypatch, fused):
+    """Two-kernel attention (partials + merge) and the one-kernel form (last
+    block merges), with contexts of up to 8 cache chunks of 32 positions."""
+    if fused:
+        monkeypatch.setenv("S2HIP_ATTN_FUSED", "1")
+    else:
+        monkeypatch.delenv("S2HIP_ATTN_FUSED", raising=False)
+    prompt = make_prompt(synth.TINY, 200, seed=16)
+    e, o = _engine(tiny_gguf, max_seq=256), _oracle(tiny_gguf, max_seq=256)
+    hg, lg = e.eval(prompt)
+    ho, lo = o.eval(prompt)
+    assert _rel(hg, ho) < 1e-4 and _rel(lg, lo) < 1e-4
+    e.reset()
+    o.reset()
+    kw = dict(temperature=0.7, top_p=0.9, top_k=0, min_tokens_before_end=100, rng_state=7)
+    rg = e.generate_codes(prompt, 40, **kw)
+    ro = o.generate_codes(prompt, 40, **kw)
+    assert rg["n_frames"] == ro["n_frames"] == 40
+    assert np.array_equal(rg["codes"], ro["codes"]) and rg["rng_state"] == ro["rng_state"]
