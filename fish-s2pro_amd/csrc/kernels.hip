@@ -42,6 +42,17 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
 // exp evaluated in double, rounded once to float.
 __device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
 
+// A zero word in device memory: optional state pointers are read through
+// `opt_word`, which selects the address instead of branching, so the load
+// can be issued together with a kernel's other independent loads.
+__device__ const uint32_t kZeroWord = 0u;
+// (The pointer is cast to the global address space: a generic pointer would
+// become a flat load, whose waits also drain every vector load in flight.)
+__device__ __forceinline__ uint32_t opt_word(const uint32_t* p) {
+  typedef const __attribute__((address_space(1))) uint32_t gword;
+  return *(gword*)(p ? p : &kZeroWord);
+}
+
 // ---------------------------------------------------------------------------
 // Raw weight payload for 8 consecutive elements, loaded first and decoded
 // later so a wave can keep many independent 16-byte loads in flight.
@@ -65,9 +76,12 @@ __device__ __forceinline__ Raw8<WT> load_raw(const uint8_t* row, uint32_t e) {
     const uint32_t b = e >> 5, p = (e >> 3) & 3u;
     const uint8_t* blk = row + size_t(b) * BB;
     const uint32_t qoff = (WT == W_Q8_0) ? 2 + p * 8 : 2 + (p & 1u) * 8;
-    const uintptr_t a = reinterpret_cast<uintptr_t>(blk + qoff);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~uintptr_t(3));
-    r.d = uint32_t(*reinterpret_cast<const uint16_t*>(blk)) | (uint32_t(a & 3u) << 16) | (p << 20);
+    // aligned window by pointer arithmetic (an integer round trip would lose
+    // the global address space and turn these into flat loads)
+    const uint8_t* q = blk + qoff;
+    const uint32_t mis = uint32_t(reinterpret_cast<uintptr_t>(q) & 3u);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(q - mis);
+    r.d = uint32_t(*reinterpret_cast<const uint16_t*>(blk)) | (mis << 16) | (p << 20);
     r.w0 = base[0];
     r.w1 = base[1];
     r.w2 = base[2];
@@ -981,13 +995,22 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const uint32_t t0 = chunk * CH;
 
   // 0. position-independent loads, all in flight together
-  const uint32_t done = a.done ? *a.done : 0u;
-  const uint32_t pbase = a.pos_ptr ? *a.pos_ptr : 0u;
+  const uint32_t done = opt_word(a.done);
+  const uint32_t pbase = opt_word(a.pos_ptr);
   const bool qlane = wave < rep && lane < HD / 2;
   float2 qv = make_float2(0.f, 0.f), qn = make_float2(1.f, 1.f);
   if (qlane) {
     qv = *reinterpret_cast<const float2*>(row + size_t(g * rep + wave) * HD + 2 * lane);
     if (a.q_norm) qn = *reinterpret_cast<const float2*>(a.q_norm + 2 * lane);
+  }
+  // k / v rows of this launch's columns (wave w <-> column w <= col)
+  const bool kwave = wave < a.ncol && wave <= col;
+  float2 kx = make_float2(0.f, 0.f), vx = kx, kn = make_float2(1.f, 1.f);
+  if (kwave && lane < HD / 2) {
+    const float* r2 = a.qkv + size_t(wave) * width;
+    kx = *reinterpret_cast<const float2*>(r2 + size_t(a.H + g) * HD + 2 * lane);
+    vx = *reinterpret_cast<const float2*>(r2 + size_t(a.H + a.Hkv + g) * HD + 2 * lane);
+    if (a.k_norm) kn = *reinterpret_cast<const float2*>(a.k_norm + 2 * lane);
   }
   float4 kr[PER], vr[PER];
 #pragma unroll
@@ -999,22 +1022,47 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
   }
   const uint32_t pos = pbase + a.pos_offset + col;
-  if (done) return;
-  if (pos >= a.max_seq) {
-    if (tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
-    return;
-  }
   const uint32_t T = pos + 1;
   const uint32_t nch = (T + CH - 1) / CH;
-  if (chunk >= nch) return;
+  if (done || pos >= a.max_seq || chunk >= nch) {
+    if (!done && pos >= a.max_seq && tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
+    // The exit path also reads the loaded values, so the compiler keeps the
+    // loads ahead of this branch (where they overlap the state read) instead
+    // of sinking them behind it.  The test is never true for finite data.
+    float keep = qv.x + qv.y + kx.x + kx.y + vx.x + vx.y;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      keep += (kr[j].x + kr[j].y) + (kr[j].z + kr[j].w) + (vr[j].x + vr[j].y) + (vr[j].z + vr[j].w);
+    if (keep == 3.0e38f && a.err) atomicOr(a.err, 0u);
+    return;
+  }
   const uint32_t t1 = min(T, t0 + CH), nt = t1 - t0;
   const uint32_t base = pos - col;             // first position of this launch
   const uint32_t lo = max(t0, min(base, t1));  // [lo, t1): positions of this launch
 
-  // 1. q: QK-norm (optional) + rotation
+  // 1. rotation rows (the only position-dependent loads), then q and the
+  //    new k: QK-norm (optional) + rotation
+  const uint32_t tk = base + wave;  // position of column `wave`
+  const bool khere = kwave && tk >= t0 && tk < t1;
+  const float2 rp = qlane ? a.rope[size_t(pos) * (HD / 2) + lane] : make_float2(1.f, 0.f);
+  const float2 rk = (khere && lane < HD / 2) ? a.rope[size_t(tk) * (HD / 2) + lane] : make_float2(1.f, 0.f);
+  if (khere) {
+    float x0 = kx.x, x1 = kx.y;
+    if (a.k_norm) {
+      const float ss = wave_sum(x0 * x0 + x1 * x1);
+      const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(HD)), a.eps)));
+      x0 = __fmul_rn(__fmul_rn(x0, sc), kn.x);
+      x1 = __fmul_rn(__fmul_rn(x1, sc), kn.y);
+    }
+    if (lane < HD / 2) {
+      knew[wave][2 * lane] = __fsub_rn(__fmul_rn(x0, rk.x), __fmul_rn(x1, rk.y));
+      knew[wave][2 * lane + 1] = __fadd_rn(__fmul_rn(x0, rk.y), __fmul_rn(x1, rk.x));
+      vnew[wave][2 * lane] = vx.x;
+      vnew[wave][2 * lane + 1] = vx.y;
+    }
+  }
   if (wave < rep) {
     float x0 = qv.x, x1 = qv.y;
-    const float2 rp = qlane ? a.rope[size_t(pos) * (HD / 2) + lane] : make_float2(1.f, 0.f);
     if (a.q_norm) {
       const float ss = wave_sum(x0 * x0 + x1 * x1);
       const float sc = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, float(HD)), a.eps)));
@@ -1026,15 +1074,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       qs[wave][2 * lane + 1] = __fadd_rn(__fmul_rn(x0, rp.y), __fmul_rn(x1, rp.x));
     }
   }
-  // 2. k / v of this launch's positions inside the chunk (at most 4)
-  for (uint32_t tt = lo + wave; tt < t1; tt += GEMV_WAVES) {
-    const float* r2 = a.qkv + size_t(tt - base) * width;
-    head_norm_rope(r2 + size_t(a.H + g) * HD, a.k_norm, a.eps, a.rope + size_t(tt) * (HD / 2), HD, lane,
-                   knew[tt - lo]);
-    const float* vs = r2 + size_t(a.H + a.Hkv + g) * HD;
-    for (uint32_t i = lane; i < HD; i += 64) vnew[tt - lo][i] = vs[i];
-  }
-  // 3. tile to LDS (positions >= lo are replaced below or unused)
+  // 2. tile to LDS (positions >= lo are replaced below or unused)
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint32_t idx = j * 256 + tid;
@@ -1046,14 +1086,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     *reinterpret_cast<float4*>(&vt[t * HD + d]) = vr[j];
   }
   __syncthreads();
-  for (uint32_t tt = lo; tt < t1; ++tt) {
-    const uint32_t tn = tt - t0;
+  // 3. this launch's positions in the chunk: columns lo - base .. t1 - base - 1
+  for (uint32_t c2 = lo - base; c2 < t1 - base; ++c2) {
+    const uint32_t tn = base + c2 - t0;
     for (uint32_t i = tid; i < HD; i += 256) {
-      kt[tn * KS + i] = knew[tt - lo][i];
-      vt[tn * HD + i] = vnew[tt - lo][i];
-      if (tt == pos) {  // SlowArKvCache::write_token for this column's position
-        a.k_cache[(size_t(g) * a.max_seq + pos) * HD + i] = knew[tt - lo][i];
-        a.v_cache[(size_t(g) * a.max_seq + pos) * HD + i] = vnew[tt - lo][i];
+      kt[tn * KS + i] = knew[c2][i];
+      vt[tn * HD + i] = vnew[c2][i];
+      if (c2 == col) {  // SlowArKvCache::write_token for this column's position
+        a.k_cache[(size_t(g) * a.max_seq + pos) * HD + i] = knew[c2][i];
+        a.v_cache[(size_t(g) * a.max_seq + pos) * HD + i] = vnew[c2][i];
       }
     }
   }
@@ -1147,28 +1188,65 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
 }
 
-// Combine of the per-chunk (max, sum, o) partials: grid (H, ncol), HD threads.
-template <int HD, int CH>
+// Merge of the per-chunk (max, sum, o) partials: grid (H, ncol), HD threads.
+// MAXC > 0: the state words and the partials of every chunk slot (up to
+// MAXC >= max_chunks) are loaded together before the position is known;
+// slots past this launch's chunk count hold stale data and are ignored.
+// MAXC == 0: a loop over the chunks (any max_chunks).
+template <int HD, int CH, int MAXC>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
   const uint32_t h = blockIdx.x, col = blockIdx.y, d = threadIdx.x;
-  const uint32_t done = a.done ? *a.done : 0u;
-  const uint32_t pos = (a.pos_ptr ? *a.pos_ptr : 0u) + a.pos_offset + col;
-  if (done || pos >= a.max_seq) return;
-  const uint32_t nch = (pos + CH) / CH;
-  if (nch <= 1) return;
   const uint32_t rep = a.H / a.Hkv, g = h / rep, w = h % rep;
   const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks * rep + w) * (HD + 2);
   const size_t stride = size_t(rep) * (HD + 2);
-  float M = -INFINITY;
-  for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, pbase[c * stride]);
-  float L = 0.0f, acc = 0.0f;
-  for (uint32_t c = 0; c < nch; ++c) {
-    const float* pc = pbase + c * stride;
-    const float f = expf(pc[0] - M);
-    L = fmaf(pc[1], f, L);
-    acc = fmaf(pc[2 + d], f, acc);
+  const uint32_t done = opt_word(a.done);
+  const uint32_t pb = opt_word(a.pos_ptr);
+  if constexpr (MAXC > 0) {
+    static_assert(MAXC <= HD, "one thread per chunk slot");
+    __shared__ float2 ml[MAXC];
+    // no branch before these loads: every slot is read, the result is
+    // discarded at the store when the launch has nothing to merge
+    float2 mlv = make_float2(0.f, 0.f);
+    if (d < uint32_t(MAXC))
+      mlv = *reinterpret_cast<const float2*>(pbase + size_t(min(d, a.max_chunks - 1)) * stride);
+    float oc[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) oc[c] = pbase[size_t(min(uint32_t(c), a.max_chunks - 1)) * stride + 2 + d];
+    if (d < uint32_t(MAXC)) ml[d] = mlv;
+    __syncthreads();
+    const uint32_t pos = pb + a.pos_offset + col;
+    const bool live = !done && pos < a.max_seq;
+    const uint32_t nch = live ? (pos + CH) / CH : 0u;
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c)
+      if (uint32_t(c) < nch) M = fmaxf(M, ml[c].x);
+    float L = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      if (uint32_t(c) < nch) {
+        const float f = expf(ml[c].x - M);
+        L = fmaf(ml[c].y, f, L);
+        acc = fmaf(oc[c], f, acc);
+      }
+    }
+    if (nch > 1) a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
+  } else {
+    const uint32_t pos = pb + a.pos_offset + col;
+    if (done || pos >= a.max_seq) return;
+    const uint32_t nch = (pos + CH) / CH;
+    if (nch <= 1) return;
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, pbase[c * stride]);
+    float L = 0.0f, acc = 0.0f;
+    for (uint32_t c = 0; c < nch; ++c) {
+      const float* pc = pbase + c * stride;
+      const float f = expf(pc[0] - M);
+      L = fmaf(pc[1], f, L);
+      acc = fmaf(pc[2 + d], f, acc);
+    }
+    a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
   }
-  a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
 }
 
 // ---------------------------------------------------------------------------
@@ -1675,6 +1753,20 @@ uint32_t attention_chunks(uint32_t max_seq, uint32_t mode) {
   return (max_seq + 31u) / 32u;
 }
 
+template <int HD>
+void launch_combine(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (a.max_chunks <= 8)
+    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 8>), grid, dim3(HD), 0, s, a);
+  else if (a.max_chunks <= 16)
+    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 16>), grid, dim3(HD), 0, s, a);
+  else if (a.max_chunks <= 32)
+    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 32>), grid, dim3(HD), 0, s, a);
+  else if (a.max_chunks <= 64)
+    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 64>), grid, dim3(HD), 0, s, a);
+  else
+    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 0>), grid, dim3(HD), 0, s, a);
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (a.H % a.Hkv || a.H / a.Hkv > 4 || a.ncol > 4) return hipErrorInvalidValue;
   if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
@@ -1697,9 +1789,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (e != hipSuccess || a.max_chunks == 1) return e;
   const dim3 cgrid(a.H, a.ncol);
   if (a.hd == 64)
-    hipLaunchKernelGGL((attn_combine_kernel<64, 32>), cgrid, dim3(64), 0, s, a);
+    launch_combine<64>(a, cgrid, s);
   else
-    hipLaunchKernelGGL((attn_combine_kernel<128, 32>), cgrid, dim3(128), 0, s, a);
+    launch_combine<128>(a, cgrid, s);
   return hipGetLastError();
 }
 
