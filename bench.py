@@ -139,7 +139,8 @@ def main():
     log(f"{kern}: {us:.2f} us/launch, {kb / 1e6:.2f} MB -> {achieved:.0f} GB/s")
     other = {}
     for k in ("slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn", "fast_head",
-              "sample_fast", "sample_slow", "fast_frame", "empty", "hbm_copy"):
+              "sample_fast", "sample_slow", "sample_fast_topp", "sample_slow_topp", "sample_fast_default",
+              "fast_frame", "empty", "hbm_copy"):
         ku, kbb = eng.time_kernel(k, reps=5)
         other[k] = {"us": round(ku, 3)}
         if kbb:

@@ -1156,14 +1156,18 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
       aa.mode = attn_mode_;
       aa.scale = 0.08838834764831845f;
       HIPC(launch_attention(aa, stream_));
-    } else if (name == "sample_fast" || name == "sample_slow") {
+    } else if (name.rfind("sample_fast", 0) == 0 || name.rfind("sample_slow", 0) == 0) {
       SampleArgs sa{};
-      const bool fast = name == "sample_fast";
+      const bool fast = name.rfind("sample_fast", 0) == 0;
       sa.logits = fast ? flogits_ : logits_c_;
       sa.ids = fast ? nullptr : head_rows_;
       sa.n = fast ? s.codebook_size : n_cand_;
       sa.vocab = fast ? s.codebook_size : s.vocab;
+      // greedy; "_topp": T 0.7, top-p 0.9; "_default": GenerateParams::default()
+      // (generate.rs:22-31: T 0.7, top-p 0.7, top-k 30)
       sa.cfg = SamplerCfg{0.0f, 1.0f, 0};
+      if (name.find("_topp") != std::string::npos) sa.cfg = SamplerCfg{0.7f, 0.9f, 0};
+      if (name.find("_default") != std::string::npos) sa.cfg = SamplerCfg{0.7f, 0.7f, 30};
       sa.st = st_;
       sa.im_end = im_end_;
       sa.cb_index = 1;
@@ -1199,7 +1203,7 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   else if (name == "hbm_copy") b = 2.0 * double(COPY_BYTES);
   const bool per_layer = name.rfind("slow_", 0) == 0 && name != "slow_head" && name != "sample_slow";
   const uint32_t layers = per_layer || name == "fast_attn" ? s.slow_layers : 1u;
-  if (name == "fast_frame" || name == "sample_fast" || name == "sample_slow" || name == "empty") {
+  if (name == "fast_frame" || name.rfind("sample_", 0) == 0 || name == "empty") {
     // a clean state: nothing finished, frame counters at zero
     HIPC(hipStreamSynchronize(stream_));
     DevState init{};

@@ -1325,26 +1325,34 @@ __global__ __launch_bounds__(256) void fast_begin_kernel(DevState* st, const flo
 // the candidate set (or masked) has logit -inf.  Sequential f32 sums are
 // done by one thread in the reference's order.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint64_t encode_key(float v, uint32_t id) {
-  if (v == 0.0f) v = 0.0f;  // -0 == +0 for the sort
+// Sort key of a finite logit: ascending key == descending value (-0 == +0).
+// Non-finite / masked / padding entries use 0xffffffff, above every finite key.
+__device__ __forceinline__ uint32_t value_key(float v) {
+  if (v == 0.0f) v = 0.0f;
   const uint32_t bits = __float_as_uint(v);
   const uint32_t ord = (bits & 0x80000000u) ? ~bits : (bits | 0x80000000u);
-  return (uint64_t(~ord) << 32) | id;  // ascending key == descending value, then ascending id
+  return ~ord;
 }
 
-__device__ __forceinline__ float decode_key(uint64_t k) {
-  const uint32_t ord = ~uint32_t(k >> 32);
+__device__ __forceinline__ float key_value(uint32_t k) {
+  const uint32_t ord = ~k;
   const uint32_t bits = (ord & 0x80000000u) ? (ord & 0x7fffffffu) : ~ord;
   return __uint_as_float(bits);
 }
 
+constexpr uint32_t NO_KEY = 0xffffffffu;
+
 struct SampleShared {
-  uint64_t keys[SAMPLE_MAX];
-  float probs[SAMPLE_MAX + 1];
+  uint32_t ckey[SAMPLE_MAX];   // candidate keys in candidate (ascending id) order
+  uint32_t skey[SAMPLE_MAX];   // keys in sorted order
+  float probs[SAMPLE_MAX + 4]; // probs and pref double as the sort's exchange buffer
+  float pref[SAMPLE_MAX + 4];  // running sums
   float redf[SAMPLE_THREADS / WAVE];
   uint32_t redu[SAMPLE_THREADS / WAVE];
+  uint32_t redk[SAMPLE_THREADS / WAVE];
   float bcast_f;
   uint32_t bcast_u[4];
+  uint64_t rng;                // SeededRng state (read and advanced by thread 0)
 };
 
 __device__ __forceinline__ double lcg_next_unit(uint64_t* s) {
@@ -1353,20 +1361,391 @@ __device__ __forceinline__ double lcg_next_unit(uint64_t* s) {
   return double(mant) / double(1ull << 53);
 }
 
-// j-th id (ascending) of [0, vocab) minus the ids of the n_fin sorted keys.
-__device__ uint32_t masked_id(const uint64_t* keys, uint32_t n_fin, uint32_t j, uint32_t vocab) {
+// Block-wide sum of one uint32 per thread (result in every thread).
+__device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, SampleShared& sh) {
+  constexpr uint32_t NW = SAMPLE_THREADS / WAVE;
+  const uint32_t lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += uint32_t(__shfl_xor(int(v), off, WAVE));
+  __syncthreads();
+  if (lane == 0) sh.redk[wave] = v;
+  __syncthreads();
+  uint32_t t = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < NW; ++w) t += sh.redk[w];
+  return t;
+}
+
+// Ascending bitonic sort of P = E * SAMPLE_THREADS 32-bit keys in registers:
+// element r * SAMPLE_THREADS + tid is register r of thread tid.  Partners
+// j >= SAMPLE_THREADS apart sit in the same thread, WAVE <= j < SAMPLE_THREADS
+// in another wave (exchanged through `xbuf`, 2 * P words, double-buffered:
+// one barrier per step), and j < WAVE in the same wave (shuffles).  The
+// stage sizes K and J are template constants, so register indices are static.
+template <int E, uint32_t K, uint32_t J>
+__device__ __forceinline__ void bitonic_step(uint32_t (&key)[E], uint32_t* xbuf, uint32_t& par) {
+  constexpr uint32_t NT = SAMPLE_THREADS;
+  constexpr uint32_t P = uint32_t(E) * NT;
+  const uint32_t tid = threadIdx.x;
+  if constexpr (J >= NT) {
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      constexpr int RJ = int(J / NT);
+      const int rp = r ^ RJ;
+      if (rp > r) {
+        const bool up = ((uint32_t(r) * NT) & K) == 0;
+        const uint32_t x = key[r], y = key[rp];
+        key[r] = up ? min(x, y) : max(x, y);
+        key[rp] = up ? max(x, y) : min(x, y);
+      }
+    }
+  } else if constexpr (J >= WAVE) {
+    uint32_t* buf = xbuf + par * P;
+#pragma unroll
+    for (int r = 0; r < E; ++r) buf[r * NT + tid] = key[r];
+    __syncthreads();
+    const bool lower = (tid & J) == 0;
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const uint32_t o = buf[r * NT + (tid ^ J)];
+      const bool up = ((uint32_t(r) * NT + tid) & K) == 0;
+      key[r] = (lower == up) ? min(key[r], o) : max(key[r], o);
+    }
+    par ^= 1u;
+  } else {
+    const bool lower = (tid & J) == 0;
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const uint32_t o = uint32_t(__shfl_xor(int(key[r]), int(J), WAVE));
+      const bool up = ((uint32_t(r) * NT + tid) & K) == 0;
+      key[r] = (lower == up) ? min(key[r], o) : max(key[r], o);
+    }
+  }
+}
+
+template <int E, uint32_t K, uint32_t J>
+__device__ __forceinline__ void bitonic_merge(uint32_t (&key)[E], uint32_t* xbuf, uint32_t& par) {
+  bitonic_step<E, K, J>(key, xbuf, par);
+  if constexpr (J > 1) bitonic_merge<E, K, J / 2>(key, xbuf, par);
+}
+
+template <int E, uint32_t K>
+__device__ __forceinline__ void bitonic_stages(uint32_t (&key)[E], uint32_t* xbuf, uint32_t& par) {
+  bitonic_merge<E, K, K / 2>(key, xbuf, par);
+  if constexpr (K < uint32_t(E) * SAMPLE_THREADS) bitonic_stages<E, 2 * K>(key, xbuf, par);
+}
+
+template <int E>
+__device__ __forceinline__ void bitonic_sort_regs(uint32_t (&key)[E], uint32_t* xbuf) {
+  uint32_t par = 0;
+  bitonic_stages<E, 2>(key, xbuf, par);
+}
+
+// One 32-element step of a sequential sum: add the batch into cs in order,
+// leave the running sums in the batch registers, write them to `prefix`.
+__device__ __forceinline__ void chain_batch(float4 (&v)[8], float& cs, float* prefix) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    cs = __fadd_rn(cs, v[t].x);
+    v[t].x = cs;
+    cs = __fadd_rn(cs, v[t].y);
+    v[t].y = cs;
+    cs = __fadd_rn(cs, v[t].z);
+    v[t].z = cs;
+    cs = __fadd_rn(cs, v[t].w);
+    v[t].w = cs;
+  }
+  if (prefix) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) *reinterpret_cast<float4*>(prefix + 4 * t) = v[t];
+  }
+}
+
+__device__ __forceinline__ void chain_load(float4 (&v)[8], const float* p) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) v[t] = *reinterpret_cast<const float4*>(p + 4 * t);
+}
+
+// Sequential f32 sums in index order (one lane; one rounding per add).
+// Values are read from LDS 32 at a time into one of two register sets, the
+// next batch's reads in flight while the current one is added; `prefix`
+// (nullable) receives every running sum.  The chain stops after the first
+// batch whose last running sum reaches `stop` (use_stop), or as soon as the
+// next term is below half an ulp of the running sum (absorb: the terms are
+// non-negative and non-increasing, so that term and every later one leave
+// the sum unchanged).  *done_count receives the count of running sums made.
+__device__ __forceinline__ float seq_chain(const float* p, float* prefix, uint32_t n, bool use_stop, float stop,
+                                           bool absorb, uint32_t* done_count) {
+  constexpr uint32_t B = 32;
+  float cs = 0.0f;
+  uint32_t i = 0;
+  float4 va[8], vb[8];
+  auto finish_batch = [&](uint32_t next) -> bool {  // true: stop here
+    if (use_stop && cs >= stop) return true;
+    if (absorb && next < n && cs > 0.0f) {
+      const float half_ulp = __uint_as_float(__float_as_uint(cs) & 0x7f800000u) * 0x1p-24f;
+      if (p[next] < half_ulp) return true;
+    }
+    return false;
+  };
+  if (n >= B) chain_load(va, p);
+  while (i + B <= n) {
+    if (i + 2 * B <= n) chain_load(vb, p + i + B);
+    chain_batch(va, cs, prefix ? prefix + i : nullptr);
+    i += B;
+    if (finish_batch(i)) {
+      *done_count = i;
+      return cs;
+    }
+    if (i + B > n) break;
+    if (i + 2 * B <= n) chain_load(va, p + i + B);
+    chain_batch(vb, cs, prefix ? prefix + i : nullptr);
+    i += B;
+    if (finish_batch(i)) {
+      *done_count = i;
+      return cs;
+    }
+  }
+  for (; i < n; ++i) {
+    cs = __fadd_rn(cs, p[i]);
+    if (prefix) prefix[i] = cs;
+  }
+  *done_count = n;
+  return cs;
+}
+
+// First index i < n whose prefix[i] satisfies (prefix >= thr) when ge, else
+// (thr < prefix); n if none.  Whole block; result broadcast through *slot.
+__device__ __forceinline__ uint32_t block_first_index(const float* prefix, uint32_t n, float thr, bool ge,
+                                                      uint32_t* slot) {
+  __syncthreads();  // earlier readers of *slot are done
+  if (threadIdx.x == 0) *slot = 0xffffffffu;
+  __syncthreads();
+  uint32_t best = 0xffffffffu;
+  for (uint32_t i = threadIdx.x; i < n; i += SAMPLE_THREADS) {
+    const float c = prefix[i];
+    if (ge ? (c >= thr) : (thr < c)) {
+      best = i;
+      break;
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) best = min(best, uint32_t(__shfl_xor(int(best), off, WAVE)));
+  if ((threadIdx.x & (WAVE - 1)) == 0 && best != 0xffffffffu) atomicMin(slot, best);
+  __syncthreads();
+  const uint32_t r = *slot;
+  return r == 0xffffffffu ? n : r;
+}
+
+// Candidate index of the m-th (0-based, ascending index) candidate whose key
+// is kc; candidates ascend in id, so this is the m-th smallest id among the
+// candidates with that value.  Whole block.
+__device__ __forceinline__ uint32_t block_nth_match(SampleShared& sh, uint32_t n, uint32_t kc, uint32_t m) {
+  constexpr uint32_t NT = SAMPLE_THREADS, NW = SAMPLE_THREADS / WAVE;
+  const uint32_t tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid >> 6;
+  uint32_t base = 0;
+  __syncthreads();  // earlier readers of bcast_u[2] are done
+  if (tid == 0) sh.bcast_u[2] = 0xffffffffu;
+  for (uint32_t r0 = 0; r0 < n; r0 += NT) {
+    const uint32_t j = r0 + tid;
+    const bool match = j < n && sh.ckey[j] == kc;
+    const uint64_t b = __ballot(match);
+    __syncthreads();
+    if (lane == 0) sh.redk[wave] = uint32_t(__popcll(b));
+    __syncthreads();
+    uint32_t before = base, total = base;
+#pragma unroll
+    for (uint32_t w = 0; w < NW; ++w) {
+      before += w < wave ? sh.redk[w] : 0u;
+      total += sh.redk[w];
+    }
+    if (match && before + uint32_t(__popcll(b & ((1ull << lane) - 1ull))) == m) sh.bcast_u[2] = j;
+    base = total;
+    if (total > m) break;
+  }
+  __syncthreads();
+  return sh.bcast_u[2];
+}
+
+// j-th id (ascending) of [0, vocab) that is not the id of a finite candidate
+// (the masked tail of the item list).  Whole block; binary search with a
+// block-wide count per step.
+template <int E>
+__device__ uint32_t block_masked_id(SampleShared& sh, const uint32_t (&cid)[E], const uint32_t (&ckey_r)[E],
+                                    uint32_t j, uint32_t vocab) {
   uint32_t lo = 0, hi = vocab ? vocab - 1 : 0;
   while (lo < hi) {
     const uint32_t mid = lo + (hi - lo) / 2;
     uint32_t le = 0;
-    for (uint32_t i = 0; i < n_fin; ++i) le += (uint32_t(keys[i]) <= mid) ? 1u : 0u;
+#pragma unroll
+    for (int r = 0; r < E; ++r) le += (ckey_r[r] != NO_KEY && cid[r] <= mid) ? 1u : 0u;
+    le = block_sum_u32(le, sh);
     const uint32_t masked_le = mid + 1 - le;
     if (masked_le >= j + 1) hi = mid; else lo = mid + 1;
   }
   return lo;
 }
 
-__device__ uint32_t sample_core(SampleShared& sh, const float* logits, const uint32_t* ids, uint32_t n,
+// General path of sample_token (sampling.rs:120-241) for n <= E * SAMPLE_THREADS.
+// Candidates are sorted by value only (32-bit keys): equal values make equal
+// softmax terms, so every sum is independent of the order among them, and the
+// id of a chosen position is resolved afterwards as the m-th smallest id
+// among the candidates with that value (the reference's stable sort order).
+template <int E>
+__device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float* logits, const uint32_t* ids,
+                                                   uint32_t n, uint32_t vocab, SamplerCfg cfg, int64_t masked,
+                                                   int64_t force, uint64_t* rng, uint32_t n_fin) {
+  constexpr uint32_t NT = SAMPLE_THREADS;
+  const uint32_t tid = threadIdx.x;
+  uint32_t key[E], cid[E], ckr[E];
+  uint32_t fi_local = 0xffffffffu;
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const uint32_t i = uint32_t(r) * NT + tid;
+    key[r] = NO_KEY;
+    cid[r] = 0xffffffffu;
+    if (i < n) {
+      const uint32_t id = ids ? ids[i] : i;
+      cid[r] = id;
+      const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
+      if (v > -INFINITY) key[r] = value_key(v);
+      if (force >= 0 && int64_t(id) == force) fi_local = i;
+    }
+    ckr[r] = key[r];
+    sh.ckey[i] = key[r];
+  }
+  if (tid == 0) sh.bcast_u[1] = 0xffffffffu;
+  __syncthreads();
+  if (fi_local != 0xffffffffu) sh.bcast_u[1] = fi_local;  // ids are unique
+  bitonic_sort_regs<E>(key, reinterpret_cast<uint32_t*>(sh.probs));
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < E; ++r) sh.skey[uint32_t(r) * NT + tid] = key[r];
+  __syncthreads();
+
+  // item list: sorted finite (first min(k, n_fin)), then masked ids (if k > n_fin),
+  // or the appended always-include item.
+  const uint32_t k_lim = cfg.top_k > 0 ? min(uint32_t(cfg.top_k), vocab) : vocab;
+  const uint32_t n_top = min(k_lim, n_fin);
+  uint32_t force_pos = 0xffffffffu, appended = 0;
+  const uint32_t fi = sh.bcast_u[1];
+  uint32_t kf = NO_KEY;
+  if (force >= 0 && uint64_t(force) < vocab && fi != 0xffffffffu && sh.ckey[fi] != NO_KEY) {
+    // rank of the always-include item in the stable order
+    kf = sh.ckey[fi];
+    uint32_t c = 0;
+#pragma unroll
+    for (int r = 0; r < E; ++r) {
+      const uint32_t i = uint32_t(r) * NT + tid;
+      c += (ckr[r] < kf || (ckr[r] == kf && i < fi)) ? 1u : 0u;
+    }
+    const uint32_t rank = block_sum_u32(c, sh);
+    if (rank < n_top) {
+      force_pos = rank;
+    } else if (key_value(kf) > -1e30f) {
+      appended = 1;
+      force_pos = n_top;
+    }
+  }
+  const uint32_t n_items = appended ? n_top + 1 : k_lim;  // masked tail when k_lim > n_fin
+  const uint32_t n_valued = appended ? n_top + 1 : n_top;  // items with a finite logit
+  const float vmax = key_value(sh.skey[0]);
+  // softmax numerators in parallel (elementwise), sums sequential
+  for (uint32_t i = tid; i < n_valued; i += NT) {
+    const float v = key_value((appended && i == n_top) ? kf : sh.skey[i]);
+    float p;
+    if (cfg.temperature > 0.0f)
+      p = expf_cr(__fdiv_rn(__fsub_rn(v, vmax), cfg.temperature));
+    else
+      p = fabsf(__fsub_rn(v, vmax)) < 1e-6f ? 1.0f : 0.0f;
+    sh.probs[i] = p;
+  }
+  __syncthreads();
+  // softmax denominator: sequential sum over all valued items (the appended
+  // item may break the non-increasing order, so it disables the early stop)
+  if (tid == 0) {
+    uint32_t cnt;
+    sh.bcast_f = seq_chain(sh.probs, nullptr, n_valued, false, 0.0f, !appended, &cnt);
+  }
+  __syncthreads();
+  const float sum = sh.bcast_f;
+  if (sum > 0.0f)
+    for (uint32_t i = tid; i < n_valued; i += NT) sh.probs[i] = __fdiv_rn(sh.probs[i], sum);
+  __syncthreads();
+  // top-p: running sums of the probabilities (into sh.pref) until one reaches
+  // top_p; the cut is the first such index, found by the whole block
+  if (tid == 0) {
+    uint32_t cnt;
+    sh.bcast_f = seq_chain(sh.probs, sh.pref, n_valued, true, cfg.top_p, !appended, &cnt);
+    sh.bcast_u[3] = cnt;
+  }
+  __syncthreads();
+  const uint32_t pref_n = sh.bcast_u[3];
+  const float pref_last = sh.bcast_f;  // running sum after pref_n terms (the total when not cut)
+  const uint32_t cut = block_first_index(sh.pref, pref_n, cfg.top_p, true, &sh.bcast_u[2]);
+  uint32_t p_idx = cut < pref_n ? cut + 1 : n_items;  // zero-probability tail never reaches top_p either
+  if (p_idx == 0) p_idx = 1;
+  if (force_pos != 0xffffffffu && force_pos >= p_idx) p_idx = force_pos + 1;
+  const uint32_t n_pv = min(p_idx, n_valued);
+  // kept mass: the running sum at n_pv (past the computed prefix the terms
+  // were absorbed, or the always-include item extends the cut)
+  if (tid == 0) {
+    float sp = 0.0f;
+    if (n_pv > 0) {
+      if (n_pv <= pref_n) {
+        sp = sh.pref[n_pv - 1];
+      } else {
+        sp = pref_last;
+        // not cut: the chain stopped because every later term is absorbed;
+        // cut (the always-include item extends it): add the remaining terms
+        if (cut < pref_n)
+          for (uint32_t i = pref_n; i < n_pv; ++i) sp = __fadd_rn(sp, sh.probs[i]);
+      }
+    }
+    sh.bcast_f = sp;
+  }
+  __syncthreads();
+  const float sum_p = sh.bcast_f;
+  if (sum_p > 0.0f)
+    for (uint32_t i = tid; i < n_pv; i += NT) sh.probs[i] = __fdiv_rn(sh.probs[i], sum_p);
+  __syncthreads();
+  // draw: first index whose running sum exceeds the target; items past
+  // n_valued carry probability 0 and never raise the sum
+  if (tid == 0) {
+    const double draw = lcg_next_unit(rng);
+    sh.bcast_f = fminf(fmaxf(float(draw), 0.0f), 1.0f - 1e-7f);
+  }
+  __syncthreads();
+  const float target = sh.bcast_f;
+  if (tid == 0) {
+    uint32_t cnt;
+    (void)seq_chain(sh.probs, sh.pref, n_pv, true, __uint_as_float(__float_as_uint(target) + 1u), !appended, &cnt);
+    sh.bcast_u[3] = cnt;
+  }
+  __syncthreads();
+  const uint32_t draw_n = sh.bcast_u[3];
+  const uint32_t hit = block_first_index(sh.pref, draw_n, target, false, &sh.bcast_u[2]);
+  const uint32_t choice = hit < draw_n ? hit : p_idx - 1;
+  uint32_t tok;
+  if (choice < n_top) {
+    // id of sorted position `choice`: the (choice - first)-th smallest id
+    // among the candidates with the same value
+    const uint32_t kc = sh.skey[choice];
+    uint32_t lo = 0, hi = choice;  // first sorted position holding kc
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (sh.skey[mid] < kc) lo = mid + 1; else hi = mid;
+    }
+    const uint32_t j = block_nth_match(sh, n, kc, choice - lo);
+    tok = j < n ? (ids ? ids[j] : j) : 0u;  // a match always exists
+  } else if (appended) {
+    tok = uint32_t(force);
+  } else {
+    tok = block_masked_id<E>(sh, cid, ckr, choice - n_fin, vocab);
+  }
+  return tok;
+}
+
+__device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* logits, const uint32_t* ids, uint32_t n,
                                 uint32_t vocab, SamplerCfg cfg, int64_t masked, int64_t force, uint64_t* rng,
                                 uint32_t* err) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1428,14 +1807,14 @@ __device__ uint32_t sample_core(SampleShared& sh, const float* logits, const uin
     for (int off = 32; off >= 1; off >>= 1) arg = min(arg, uint32_t(__shfl_xor(int(arg), off, 64)));
     if (lane == 0) {
       sh.redu[wave] = cnt;
-      sh.keys[wave] = arg;
+      sh.redk[wave] = arg;
     }
     __syncthreads();
     if (tid == 0) {
       uint32_t c = 0, a = 0xffffffffu;
       for (uint32_t w = 0; w < NW; ++w) {
         c += sh.redu[w];
-        a = min(a, uint32_t(sh.keys[w]));
+        a = min(a, sh.redk[w]);
       }
       sh.bcast_u[1] = c;
       sh.bcast_u[2] = a;
@@ -1455,144 +1834,10 @@ __device__ uint32_t sample_core(SampleShared& sh, const float* logits, const uin
     if (tid == 0 && err) atomicOr(err, ERR_SAMPLER);
     return 0;
   }
-  uint32_t P = 1;
-  while (P < n_fin) P <<= 1;
-  // compact finite keys: write all, non-finite become +inf keys (sorted last)
-  for (uint32_t i = tid; i < P; i += SAMPLE_THREADS) sh.keys[i] = ~0ull;
-  __syncthreads();
-  if (tid == 0) sh.bcast_u[3] = 0;
-  __syncthreads();
-  for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
-    const uint32_t id = ids ? ids[i] : i;
-    const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
-    if (v > -INFINITY) {
-      const uint32_t slot = atomicAdd(&sh.bcast_u[3], 1u);
-      sh.keys[slot] = encode_key(v, id);
-    }
-  }
-  __syncthreads();
-  for (uint32_t k = 2; k <= P; k <<= 1) {
-    for (uint32_t j = k >> 1; j > 0; j >>= 1) {
-      for (uint32_t i = tid; i < P; i += SAMPLE_THREADS) {
-        const uint32_t ixj = i ^ j;
-        if (ixj > i) {
-          const uint64_t a = sh.keys[i], b = sh.keys[ixj];
-          const bool up = (i & k) == 0;
-          if ((a > b) == up) {
-            sh.keys[i] = b;
-            sh.keys[ixj] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
-
-  // item list: sorted finite (first min(k, n_fin)), then masked ids (if k > n_fin),
-  // or the appended always-include item.
-  const uint32_t k_lim = cfg.top_k > 0 ? min(uint32_t(cfg.top_k), vocab) : vocab;
-  const uint32_t n_top = min(k_lim, n_fin);
-  // force-include: present within the first k?  (thread 0 decides)
-  if (tid == 0) {
-    uint32_t force_pos = 0xffffffffu, appended = 0;
-    if (force >= 0 && uint64_t(force) < vocab) {
-      uint32_t rank = 0xffffffffu;
-      for (uint32_t i = 0; i < n_fin; ++i)
-        if (uint32_t(sh.keys[i]) == uint32_t(force)) {
-          rank = i;
-          break;
-        }
-      if (rank != 0xffffffffu) {
-        if (rank < n_top) {
-          force_pos = rank;
-        } else if (decode_key(sh.keys[rank]) > -1e30f) {
-          appended = 1;
-          force_pos = n_top;
-          sh.keys[SAMPLE_MAX - 1] = sh.keys[rank];  // stash the appended item
-        }
-      }
-    }
-    sh.bcast_u[1] = force_pos;
-    sh.bcast_u[2] = appended;
-  }
-  __syncthreads();
-  const uint32_t force_pos = sh.bcast_u[1];
-  const uint32_t appended = sh.bcast_u[2];
-  const uint32_t n_items = appended ? n_top + 1 : k_lim;  // masked tail when k_lim > n_fin
-  const uint32_t n_valued = appended ? n_top + 1 : n_top;  // items with a finite logit
-  const float vmax = decode_key(sh.keys[0]);
-  // softmax numerators in parallel (elementwise), sums sequential
-  for (uint32_t i = tid; i < n_valued; i += SAMPLE_THREADS) {
-    const uint64_t key = (appended && i == n_top) ? sh.keys[SAMPLE_MAX - 1] : sh.keys[i];
-    const float v = decode_key(key);
-    float p;
-    if (cfg.temperature > 0.0f)
-      p = expf_cr(__fdiv_rn(__fsub_rn(v, vmax), cfg.temperature));
-    else
-      p = fabsf(__fsub_rn(v, vmax)) < 1e-6f ? 1.0f : 0.0f;
-    sh.probs[i] = p;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float sum = 0.0f;
-    for (uint32_t i = 0; i < n_valued; ++i) sum = __fadd_rn(sum, sh.probs[i]);
-    sh.bcast_f = sum;
-  }
-  __syncthreads();
-  const float sum = sh.bcast_f;
-  if (sum > 0.0f)
-    for (uint32_t i = tid; i < n_valued; i += SAMPLE_THREADS) sh.probs[i] = __fdiv_rn(sh.probs[i], sum);
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t p_idx = 0;
-    float cs = 0.0f;
-    bool reached = false;
-    while (p_idx < n_valued) {
-      cs = __fadd_rn(cs, sh.probs[p_idx]);
-      p_idx += 1;
-      if (cs >= cfg.top_p) {
-        reached = true;
-        break;
-      }
-    }
-    if (!reached) p_idx = n_items;  // zero-probability tail never reaches top_p either
-    if (p_idx == 0) p_idx = 1;
-    if (force_pos != 0xffffffffu && force_pos >= p_idx) p_idx = force_pos + 1;
-    sh.bcast_u[1] = p_idx;
-    float sp = 0.0f;
-    for (uint32_t i = 0; i < min(p_idx, n_valued); ++i) sp = __fadd_rn(sp, sh.probs[i]);
-    sh.bcast_f = sp;
-  }
-  __syncthreads();
-  const uint32_t p_idx = sh.bcast_u[1];
-  const float sum_p = sh.bcast_f;
-  const uint32_t n_pv = min(p_idx, n_valued);
-  if (sum_p > 0.0f)
-    for (uint32_t i = tid; i < n_pv; i += SAMPLE_THREADS) sh.probs[i] = __fdiv_rn(sh.probs[i], sum_p);
-  __syncthreads();
-  if (tid == 0) {
-    const double draw = lcg_next_unit(rng);
-    const float target = fminf(fmaxf(float(draw), 0.0f), 1.0f - 1e-7f);
-    float cs = 0.0f;
-    uint32_t choice = p_idx - 1;
-    for (uint32_t i = 0; i < p_idx; ++i) {
-      cs = __fadd_rn(cs, i < n_valued ? sh.probs[i] : 0.0f);
-      if (target < cs) {
-        choice = i;
-        break;
-      }
-    }
-    uint32_t tok;
-    if (choice < n_top)
-      tok = uint32_t(sh.keys[choice]);
-    else if (appended)
-      tok = uint32_t(sh.keys[SAMPLE_MAX - 1]);
-    else
-      tok = masked_id(sh.keys, n_fin, choice - n_fin, vocab);
-    sh.bcast_u[0] = tok;
-  }
-  __syncthreads();
-  return sh.bcast_u[0];
+  if (n <= SAMPLE_THREADS) return sample_general<1>(sh, logits, ids, n, vocab, cfg, masked, force, rng, n_fin);
+  if (n <= 2 * SAMPLE_THREADS) return sample_general<2>(sh, logits, ids, n, vocab, cfg, masked, force, rng, n_fin);
+  if (n <= 4 * SAMPLE_THREADS) return sample_general<4>(sh, logits, ids, n, vocab, cfg, masked, force, rng, n_fin);
+  return sample_general<8>(sh, logits, ids, n, vocab, cfg, masked, force, rng, n_fin);
 }
 
 __global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs a) {
@@ -1618,10 +1863,10 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs 
   const bool block = gen < st->min_tokens_before_end;
   const int64_t masked = block ? int64_t(a.im_end) : -1;
   const int64_t force = block ? -1 : int64_t(a.im_end);
-  uint64_t rng_local = st->rng;
-  const uint32_t tok = sample_core(sh, a.logits, a.ids, a.n, a.vocab, a.cfg, masked, force, &rng_local, &st->err);
+  if (threadIdx.x == 0) sh.rng = st->rng;
+  const uint32_t tok = sample_core(sh, a.logits, a.ids, a.n, a.vocab, a.cfg, masked, force, &sh.rng, &st->err);
   if (threadIdx.x == 0) {
-    st->rng = rng_local;
+    st->rng = sh.rng;
     st->main_token = tok;
     if (a.token_out) *a.token_out = tok;
     if (tok == a.im_end || st->step_index >= st->max_new) st->done = 1;
@@ -1633,11 +1878,11 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_fast_kernel(SampleArgs 
   SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
   DevState* st = a.st;
   if (st->done) return;
-  uint64_t rng_local = st->rng;
-  const uint32_t tok = sample_core(sh, a.logits, nullptr, a.n, a.vocab, a.cfg, -1, -1, &rng_local, &st->err);
+  if (threadIdx.x == 0) sh.rng = st->rng;
+  const uint32_t tok = sample_core(sh, a.logits, nullptr, a.n, a.vocab, a.cfg, -1, -1, &sh.rng, &st->err);
   __shared__ uint32_t tok_s;
   if (threadIdx.x == 0) {
-    st->rng = rng_local;
+    st->rng = sh.rng;
     uint32_t t = tok;
     if (t >= a.n) {
       atomicOr(&st->err, ERR_SAMPLER);
@@ -1660,10 +1905,10 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_plain_kernel(const floa
                                                                       uint32_t* token_out, uint32_t* err) {
   extern __shared__ uint8_t smem_raw[];
   SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
-  uint64_t r = *rng;
-  const uint32_t tok = sample_core(sh, logits, nullptr, n, n, cfg, -1, always_include, &r, err);
+  if (threadIdx.x == 0) sh.rng = *rng;
+  const uint32_t tok = sample_core(sh, logits, nullptr, n, n, cfg, -1, always_include, &sh.rng, err);
   if (threadIdx.x == 0) {
-    *rng = r;
+    *rng = sh.rng;
     *token_out = tok;
   }
 }

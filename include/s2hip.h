@@ -166,7 +166,8 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
  * timed with HIP events on the engine stream over `reps` passes across every
  * layer (so no pass re-reads weights from cache).  kernel: "slow_w13",
  * "slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn",
- * "fast_head", "sample_fast", "sample_slow", "fast_frame", "empty" (one
+ * "fast_head", "sample_fast", "sample_slow" (greedy; with suffix "_topp":
+ * T 0.7, top-p 0.9; "_default": T 0.7, top-p 0.7, top-k 30), "fast_frame", "empty" (one
  * one-wave launch), "hbm_copy" (a 256 MiB device copy, the calibration kernel
  * for HBM byte counters).  bytes_per_launch receives the algorithmic HBM
  * bytes of one launch (weights + input + output) where defined, else 0.
