@@ -39,7 +39,8 @@ void hip_check(hipError_t e, const char* what) {
 
 [[noreturn]] void fail(const std::string& m) { throw std::runtime_error(m); }
 
-constexpr uint32_t PREFILL_COLS = 4;
+constexpr uint32_t PREFILL_COLS = 4;     // decode-path columns (Fast-AR positions 0 and 1, op tests)
+constexpr uint32_t PREFILL_CHUNK = 512;  // prompt tokens per MFMA prefill pass
 constexpr uint32_t FRAME_BATCH = 4;
 constexpr size_t WEIGHT_PAD = 256;  // trailing bytes so block loads never leave a buffer
 
@@ -135,6 +136,9 @@ class Engine {
   void enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done);
   void enqueue_frame(const SamplerCfg& cfg);
   void enqueue_prefill(const int32_t* prompt_dev, size_t n_tok);
+  void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok);
+  void mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
+          uint32_t n, uint32_t npad, float* y, uint32_t ldy);
   void ensure_prompt(size_t n_int);
   void ensure_codes(size_t n_int);
   void check_state_err();
@@ -165,7 +169,11 @@ class Engine {
   float2 *rope_slow_ = nullptr, *rope_fast_ = nullptr;
   uint32_t attn_chunks_ = 1;
   uint32_t attn_mode_ = ATTN_SPLIT;
+  bool prefill_gemv_ = false;
   uint32_t* counters_ = nullptr;
+  // prompt prefill (MFMA path): chunk activations and the split planes
+  float *ph_ = nullptr, *pqkv_ = nullptr, *pq_ = nullptr, *patt_ = nullptr, *pact_ = nullptr, *prs_ = nullptr;
+  _Float16 *pxh_ = nullptr, *pxl_ = nullptr;
   float *fh_ = nullptr, *fqkv_ = nullptr, *fq_ = nullptr, *fatt_ = nullptr, *fpart_ = nullptr, *fact_ = nullptr;
   float *flogits_ = nullptr, *fkc_ = nullptr, *fvc_ = nullptr;
   uint32_t fctx_ = 11;
@@ -317,6 +325,7 @@ Engine::Engine(const s2hip_config& cfg) {
   // store-wait + counter + reload chain measures slower than the kernel
   // boundary it replaces: 18.7 vs 13.2 us at T = 384 on the S2-Pro shape)
   attn_mode_ = getenv("S2HIP_ATTN_FUSED") ? ATTN_FUSED : ATTN_SPLIT;
+  prefill_gemv_ = getenv("S2HIP_PREFILL_GEMV") != nullptr;
   attn_chunks_ = attention_chunks(s.max_seq_len, attn_mode_);
   h_ = dalloc<float>(size_t(NC) * s.dim);
   qkv_ = dalloc<float>(size_t(NC) * qkv_w);
@@ -326,6 +335,19 @@ Engine::Engine(const s2hip_config& cfg) {
   counters_ = dalloc<uint32_t>(size_t(NC) * std::max(s.kv_heads, s.fast_kv_heads));
   HIPC(hipMemset(counters_, 0, size_t(NC) * std::max(s.kv_heads, s.fast_kv_heads) * 4));
   act_ = dalloc<float>(size_t(NC) * s.ffn);
+  {
+    const size_t CH = PREFILL_CHUNK, CHP = gemm_rows_pad(PREFILL_CHUNK);
+    const size_t kmax = std::max<size_t>({s.dim, q, s.ffn});
+    ph_ = dalloc<float>(CH * s.dim);
+    pqkv_ = dalloc<float>(CH * qkv_w);
+    pq_ = dalloc<float>(CH * q);
+    patt_ = dalloc<float>(CH * q);
+    pact_ = dalloc<float>(CH * s.ffn);
+    prs_ = dalloc<float>(CHP);
+    pxh_ = dalloc<_Float16>(CHP * kmax);
+    pxl_ = dalloc<_Float16>(CHP * kmax);
+    if (s.dim % 32 || q % 32 || s.ffn % 32) fail("prefill needs embedding, attention and FFN widths divisible by 32");
+  }
   hn_ = dalloc<float>(s.dim);
   logits_c_ = dalloc<float>(n_cand_);
   logits_full_ = dalloc<float>(s.vocab);
@@ -636,13 +658,39 @@ void Engine::enqueue_frame(const SamplerCfg& cfg) {
   HIPC(launch_sample_slow(sa, stream_));
 }
 
-void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
+// Prompt prefill (forward_slow_ar_block_prefill_layers_cached, slow_ar.rs:1002-1039):
+// chunks of up to PREFILL_CHUNK tokens go through each layer together: every
+// linear is one MFMA product over the chunk (weights read once per chunk),
+// QK-norm + RoPE + KV append for all of the chunk's positions, then causal
+// attention of each token over the cache.  Leaves the last token's residual
+// row in decode column 0 for the output head.
+void Engine::mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
+                uint32_t n, uint32_t npad, float* y, uint32_t ldy) {
+  HIPC(launch_split_rows(x, ldx, norm, eps, n, npad, L.in, pxh_, pxl_, prs_, stream_));
+  GemmArgs g{};
+  g.w = L.w;
+  g.w3 = L3 ? L3->w : nullptr;
+  g.row_bytes = L.row_bytes;
+  g.M = L.out;
+  g.K = L.in;
+  g.xh = pxh_;
+  g.xl = pxl_;
+  g.rs = prs_;
+  g.N = n;
+  g.y = y;
+  g.ldy = ldy;
+  HIPC(launch_gemm_mfma(L.type, epi, g, stream_));
+}
+
+// The decode kernels over 4 columns at a time (weights re-read every 4
+// tokens); S2HIP_PREFILL_GEMV=1 selects it, for comparisons.
+void Engine::enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok) {
   const s2hip_spec& s = spec;
   const uint32_t cdim = s.num_codebooks + 1;
   size_t t = 0;
-  uint32_t last_cols = 1;
+  uint32_t nc = 0;
   while (t < n_tok) {
-    const uint32_t nc = uint32_t(std::min<size_t>(PREFILL_COLS, n_tok - t));
+    nc = uint32_t(std::min<size_t>(PREFILL_COLS, n_tok - t));
     EmbedArgs ea{};
     ea.tokens = prompt_dev + t * cdim;
     ea.emb = emb_;
@@ -662,9 +710,85 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
     HIPC(launch_embed(ea, stream_));
     enqueue_slow_layers(nc, nullptr);
     t += nc;
-    last_cols = nc;
   }
-  (void)last_cols;
+  if (nc > 1) HIPC(hipMemcpyAsync(h_, h_ + size_t(nc - 1) * s.dim, size_t(s.dim) * 4, hipMemcpyDeviceToDevice, stream_));
+}
+
+void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
+  if (prefill_gemv_) {
+    enqueue_prefill_gemv(prompt_dev, n_tok);
+    return;
+  }
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim, qkv_w = q + 2 * kv;
+  size_t t = 0;
+  uint32_t nc = 0;
+  while (t < n_tok) {
+    nc = uint32_t(std::min<size_t>(PREFILL_CHUNK, n_tok - t));
+    const uint32_t npad = gemm_rows_pad(nc);
+    EmbedArgs ea{};
+    ea.tokens = prompt_dev + t * cdim;
+    ea.emb = emb_;
+    ea.cb_emb = cb_emb_;
+    ea.h = ph_;
+    ea.n = nc;
+    ea.dim = s.dim;
+    ea.vocab = s.vocab;
+    ea.cb_rows = uint32_t(cb_rows_);
+    ea.num_codebooks = s.num_codebooks;
+    ea.codebook_size = s.codebook_size;
+    ea.sem_begin = s.semantic_begin;
+    ea.sem_end = s.semantic_end;
+    ea.sem_scale = 1.0f / std::sqrt(float(cdim));
+    ea.scale_enabled = s.scale_codebook_embeddings;
+    ea.err = &st_->err;
+    HIPC(launch_embed(ea, stream_));
+    for (uint32_t l = 0; l < s.slow_layers; ++l) {
+      const SlowLayer& L = slow_[l];
+      float* kcl = kc_ + size_t(l) * kv * s.max_seq_len;
+      float* vcl = vc_ + size_t(l) * kv * s.max_seq_len;
+      mm(L.wqkv, nullptr, EPI_STORE, ph_, s.dim, L.attn_norm, s.eps, nc, npad, pqkv_, qkv_w);
+      QkvPostArgs qa{};
+      qa.qkv = pqkv_;
+      qa.q_out = pq_;
+      qa.k_cache = kcl;
+      qa.v_cache = vcl;
+      qa.q_norm = L.q_norm;
+      qa.k_norm = L.k_norm;
+      qa.rope = rope_slow_;
+      qa.pos_ptr = &st_->n_past;
+      qa.pos_offset = 0;
+      qa.H = s.heads;
+      qa.Hkv = s.kv_heads;
+      qa.hd = s.head_dim;
+      qa.max_seq = s.max_seq_len;
+      qa.ncol = nc;
+      qa.eps = s.eps;
+      qa.err = &st_->err;
+      HIPC(launch_qkv_post(qa, stream_));
+      PrefillAttnArgs pa{};
+      pa.q = pq_;
+      pa.k_cache = kcl;
+      pa.v_cache = vcl;
+      pa.out = patt_;
+      pa.pos_ptr = &st_->n_past;
+      pa.pos_offset = 0;
+      pa.N = nc;
+      pa.H = s.heads;
+      pa.Hkv = s.kv_heads;
+      pa.hd = s.head_dim;
+      pa.max_seq = s.max_seq_len;
+      pa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
+      HIPC(launch_attention_prefill(pa, stream_));
+      mm(L.wo, nullptr, EPI_RESID, patt_, q, nullptr, 0.0f, nc, npad, ph_, s.dim);
+      mm(L.w1, &L.w3, EPI_SWIGLU_SLOW, ph_, s.dim, L.ffn_norm, s.eps, nc, npad, pact_, s.ffn);
+      mm(L.w2, nullptr, EPI_RESID, pact_, s.ffn, nullptr, 0.0f, nc, npad, ph_, s.dim);
+    }
+    HIPC(launch_add_position(st_, nc, stream_));
+    t += nc;
+  }
+  if (nc) HIPC(hipMemcpyAsync(h_, ph_ + size_t(nc - 1) * s.dim, size_t(s.dim) * 4, hipMemcpyDeviceToDevice, stream_));
 }
 
 void Engine::ensure_prompt(size_t n_int) {
@@ -727,8 +851,7 @@ void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* l
   HIPC(hipMemsetAsync(&st_->done, 0, sizeof(uint32_t), stream_));
   HIPC(hipMemsetAsync(&st_->err, 0, sizeof(uint32_t), stream_));
   enqueue_prefill(prompt_dev_, n_tok);
-  const uint32_t last_col = uint32_t((n_tok - 1) % PREFILL_COLS);
-  enqueue_head(last_col, logits_out != nullptr, nullptr);
+  enqueue_head(0, logits_out != nullptr, nullptr);
   HIPC(hipMemcpyAsync(hidden_out, hn_, s.dim * 4, hipMemcpyDeviceToHost, stream_));
   if (logits_out) HIPC(hipMemcpyAsync(logits_out, logits_full_, size_t(s.vocab) * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
@@ -819,7 +942,7 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
   for (auto& e : ev) HIPC(hipEventCreate(&e));
   HIPC(hipEventRecord(ev[0], stream_));
   enqueue_prefill(prompt_dev_, cols);
-  enqueue_head(uint32_t((cols - 1) % PREFILL_COLS), false, nullptr);
+  enqueue_head(0, false, nullptr);
   SampleArgs sa{};
   sa.logits = logits_c_;
   sa.ids = head_rows_;

@@ -174,4 +174,42 @@ hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s);
 // Plain device copy (bytes and both pointers 16-byte aligned).
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
 
+// ---- prompt prefill (prefill.hip) ----
+// Activation rows -> f16 hi / lo planes [Npad][K] and a power-of-two row
+// scale rs[Npad] (optionally RMSNorm first); rows N..Npad-1 are zero.
+// Npad = gemm_rows_pad(N); K must be a multiple of 32.
+uint32_t gemm_rows_pad(uint32_t n);
+hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, float eps, uint32_t N, uint32_t Npad,
+                             uint32_t K, _Float16* xh, _Float16* xl, float* rs, hipStream_t s);
+
+// MFMA product y[n][m] (op)= rs[n] * sum_k W[m][k] * x[n][k] for n < N, m < M,
+// x given as the split planes; epilogues as for launch_gemv (SwiGLU uses w3).
+struct GemmArgs {
+  const uint8_t* w;
+  const uint8_t* w3;
+  size_t row_bytes;
+  uint32_t M, K;
+  const _Float16* xh;
+  const _Float16* xl;
+  const float* rs;
+  uint32_t N;
+  float* y;
+  uint32_t ldy;
+};
+hipError_t launch_gemm_mfma(uint32_t wtype, int epi, const GemmArgs& a, hipStream_t s);
+
+// Causal GQA attention of N prompt queries at positions *pos_ptr + pos_offset
+// + c over the KV cache (their own K/V already appended).
+struct PrefillAttnArgs {
+  const float* q;          // [N][H hd], QK-normed and rotated
+  const float* k_cache;    // [Hkv][max_seq][hd] for this layer
+  const float* v_cache;
+  float* out;              // [N][H hd]
+  const uint32_t* pos_ptr;
+  uint32_t pos_offset;
+  uint32_t N, H, Hkv, hd, max_seq;
+  float scale;
+};
+hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s);
+
 }  // namespace s2

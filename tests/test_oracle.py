@@ -343,3 +343,23 @@ def test_im_end_blocking_yields_exact_frame_count(tiny_gguf):
     assert r["n_frames"] == 5 and r["codes"].shape == (10, 5)
     # codebook 0 is the semantic code of each frame's main token
     assert (r["codes"] >= 0).all() and (r["codes"] < synth.TINY.codebook_size).all()
+
+
+def test_teacher_forced_replay_of_oracle_trajectory_is_exact(tiny_gguf):
+    """The draw-by-draw replay used for sampled GPU trajectories reproduces
+    the oracle's own sampled trajectory with zero mismatches (same draw order
+    and RNG steps as generate_codes)."""
+    from loop_util import teacher_forced_mismatches
+
+    o = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    prompt = make_prompt(synth.TINY, 16, seed=21)
+    r = o.generate_codes(prompt, 8, temperature=0.7, top_p=0.9, top_k=0, min_tokens_before_end=4, rng_state=3)
+    assert r["n_frames"] >= 1
+    mism, total = teacher_forced_mismatches(o, prompt, r["codes"], r["n_frames"], 0.7, 0.9, 0, 4, 3,
+                                            synth.TINY.im_end_id)
+    assert mism == 0 and total == 10 * r["n_frames"]
+    # a planted wrong code is caught
+    bad = r["codes"].copy()
+    bad[3, 0] = (bad[3, 0] + 1) % synth.TINY.codebook_size
+    mism2, _ = teacher_forced_mismatches(o, prompt, bad, r["n_frames"], 0.7, 0.9, 0, 4, 3, synth.TINY.im_end_id)
+    assert mism2 >= 1
