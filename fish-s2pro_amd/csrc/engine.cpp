@@ -139,6 +139,10 @@ class Engine {
   void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok);
   void mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
           uint32_t n, uint32_t npad, float* y, uint32_t ldy);
+  // batched columns (3..16): split planes + skinny MFMA product
+  void mm_skinny(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
+                 float eps, uint32_t n, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
+                 uint32_t out_rows, const uint32_t* done);
   void ensure_prompt(size_t n_int);
   void ensure_codes(size_t n_int);
   void check_state_err();
@@ -684,6 +688,28 @@ void Engine::mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint
 
 // The decode kernels over 4 columns at a time (weights re-read every 4
 // tokens); S2HIP_PREFILL_GEMV=1 selects it, for comparisons.
+void Engine::mm_skinny(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
+                       float eps, uint32_t n, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
+                       uint32_t out_rows, const uint32_t* done) {
+  HIPC(launch_split_rows(x, ldx, norm, eps, n, 16, L.in, pxh_, pxl_, prs_, stream_));
+  SkinnyArgs g{};
+  g.w = L.w;
+  g.w3 = L3 ? L3->w : nullptr;
+  g.row_bytes = L.row_bytes;
+  g.row_base = row_base;
+  g.extra_row = extra_row;
+  g.M = out_rows;
+  g.K = L.in;
+  g.xh = pxh_;
+  g.xl = pxl_;
+  g.rs = prs_;
+  g.N = n;
+  g.y = y;
+  g.ldy = ldy;
+  g.done = done;
+  HIPC(launch_skinny_mfma(L.type, epi, g, stream_));
+}
+
 void Engine::enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok) {
   const s2hip_spec& s = spec;
   const uint32_t cdim = s.num_codebooks + 1;
@@ -1071,8 +1097,12 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
   L.in = uint32_t(in);
   L.out = uint32_t(out);
   L.row_bytes = rb;
-  gemv(L, nullptr, EPI_STORE, uint32_t(ncol), dx.as<float>(), uint32_t(in), nullptr, 0.0f, dy.as<float>(),
-       uint32_t(out), 0, NO_ROW, uint32_t(out), nullptr);
+  if (ncol >= 3 && ncol <= 16 && in % 256 == 0)  // batched-decode product
+    mm_skinny(L, nullptr, EPI_STORE, dx.as<float>(), uint32_t(in), nullptr, 0.0f, uint32_t(ncol), dy.as<float>(),
+              uint32_t(out), 0, NO_ROW, uint32_t(out), nullptr);
+  else
+    gemv(L, nullptr, EPI_STORE, uint32_t(ncol), dx.as<float>(), uint32_t(in), nullptr, 0.0f, dy.as<float>(),
+         uint32_t(out), 0, NO_ROW, uint32_t(out), nullptr);
   HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
 }

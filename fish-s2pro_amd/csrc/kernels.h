@@ -177,7 +177,8 @@ hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
 // ---- prompt prefill (prefill.hip) ----
 // Activation rows -> f16 hi / lo planes [Npad][K] and a power-of-two row
 // scale rs[Npad] (optionally RMSNorm first); rows N..Npad-1 are zero.
-// Npad = gemm_rows_pad(N); K must be a multiple of 32.
+// Npad >= N, a multiple of 16 (gemm_rows_pad(N) for launch_gemm_mfma, 16 for
+// launch_skinny_mfma); K must be a multiple of 32.
 uint32_t gemm_rows_pad(uint32_t n);
 hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, float eps, uint32_t N, uint32_t Npad,
                              uint32_t K, _Float16* xh, _Float16* xl, float* rs, hipStream_t s);
@@ -197,6 +198,24 @@ struct GemmArgs {
   uint32_t ldy;
 };
 hipError_t launch_gemm_mfma(uint32_t wtype, int epi, const GemmArgs& a, hipStream_t s);
+
+// Skinny MFMA product for 1..16 columns (batched decode): x as split planes
+// with 16 rows ([16][K], rows N..15 zero); K a multiple of 256.
+struct SkinnyArgs {
+  const uint8_t* w;
+  const uint8_t* w3;
+  size_t row_bytes;
+  uint32_t row_base, extra_row;  // logical row -> weight row, as in GemvArgs
+  uint32_t M, K;
+  const _Float16* xh;
+  const _Float16* xl;
+  const float* rs;
+  uint32_t N;
+  float* y;
+  uint32_t ldy;
+  const uint32_t* done;
+};
+hipError_t launch_skinny_mfma(uint32_t wtype, int epi, const SkinnyArgs& a, hipStream_t s);
 
 // Causal GQA attention of N prompt queries at positions *pos_ptr + pos_offset
 // + c over the KV cache (their own K/V already appended).

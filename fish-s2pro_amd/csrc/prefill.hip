@@ -242,6 +242,126 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Skinny MFMA product for 1..16 columns (batched decode):
+//   y[c][m] (op)= rs[c] * sum_k W[m][k] * x[c][k],  x as split planes [16][K].
+// Block = 16 weight rows x 8 waves; wave w covers K range [w K/8, (w+1) K/8)
+// in steps of 32 (one v_mfma_f32_16x16x32_f16 per plane and weight part),
+// with two 4-step register batches in flight (loads of the next batch issue
+// before the current batch's MFMAs); the 8 partial 16x16 tiles are summed in
+// LDS and wave 0 applies the epilogue.  Row mapping as in the decode GEMV
+// (row_base / extra_row).
+// ---------------------------------------------------------------------------
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int SK_WAVES = 8, SK_D = 4;
+
+template <uint32_t WT, int EPI>
+__global__ __launch_bounds__(SK_WAVES * 64) void skinny_mfma_kernel(SkinnyArgs a) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr bool WSPLIT = WT != W_F16;
+  constexpr int NW = DUAL ? 2 : 1;
+  __shared__ floatx4 red[SK_WAVES][2 * NW][64];
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t m0 = blockIdx.x * 16;
+  uint32_t lr = min(m0 + (lane & 15u), a.M - 1);
+  const uint32_t wr = (a.extra_row != NO_ROW && lr == a.M - 1) ? a.extra_row : a.row_base + lr;
+  const uint8_t* wp[NW];
+  wp[0] = a.w + size_t(wr) * a.row_bytes;
+  if constexpr (DUAL) wp[NW - 1] = a.w3 + size_t(wr) * a.row_bytes;
+  const uint32_t koff = 8u * (lane >> 4);
+  const uint32_t tok = lane & 15u;
+  const _Float16* xhp = a.xh + size_t(tok) * a.K + koff;
+  const _Float16* xlp = a.xl + size_t(tok) * a.K + koff;
+  const uint32_t kq = a.K / SK_WAVES, kbeg = wave * kq, steps = kq / 32;
+  const uint32_t done = a.done ? *a.done : 0u;
+
+  struct Step {
+    half8 wh[NW], wl[NW], bh, bl;
+  };
+  auto load = [&](Step& st, uint32_t s) {
+    const uint32_t k = kbeg + 32u * min(s, steps - 1);  // clamped: past-the-end steps reload the last one
+#pragma unroll
+    for (int m = 0; m < NW; ++m) weight8<WT>(wp[m], k + koff, st.wh[m], st.wl[m]);
+    st.bh = *reinterpret_cast<const half8*>(xhp + k);
+    st.bl = *reinterpret_cast<const half8*>(xlp + k);
+  };
+  floatx4 acc[NW], accl[NW];
+#pragma unroll
+  for (int m = 0; m < NW; ++m) {
+    acc[m] = floatx4{};
+    accl[m] = floatx4{};
+  }
+  auto compute = [&](const Step& st) {
+#pragma unroll
+    for (int m = 0; m < NW; ++m) {
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.wh[m], st.bh, acc[m], 0, 0, 0);
+      acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.wh[m], st.bl, acc[m], 0, 0, 0);
+      if constexpr (WSPLIT) accl[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(st.wl[m], st.bh, accl[m], 0, 0, 0);
+    }
+  };
+  Step x0[SK_D], x1[SK_D];
+#pragma unroll
+  for (int i = 0; i < SK_D; ++i) load(x0[i], i);
+  for (uint32_t s = 0; s < steps; s += 2 * SK_D) {
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i) load(x1[i], s + SK_D + i);
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i)
+      if (s + i < steps) compute(x0[i]);
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i) load(x0[i], s + 2 * SK_D + i);
+#pragma unroll
+    for (int i = 0; i < SK_D; ++i)
+      if (s + SK_D + i < steps) compute(x1[i]);
+  }
+#pragma unroll
+  for (int m = 0; m < NW; ++m) {
+    red[wave][2 * m][lane] = acc[m];
+    red[wave][2 * m + 1][lane] = accl[m];
+  }
+  __syncthreads();
+  if (wave != 0 || done) return;
+#pragma unroll
+  for (int m = 0; m < NW; ++m) {
+    floatx4 t = red[0][2 * m][lane], tl = red[0][2 * m + 1][lane];
+#pragma unroll
+    for (int w = 1; w < SK_WAVES; ++w) {
+      t += red[w][2 * m][lane];
+      tl += red[w][2 * m + 1][lane];
+    }
+    acc[m] = t;
+    accl[m] = tl;
+  }
+  // lane holds D[4 (lane / 16) + v][lane % 16]: rows 4 (lane/16) + v, column lane % 16
+  const uint32_t c = lane & 15u;
+  if (c >= a.N) return;
+  const float r = a.rs[c];
+  float* yrow = a.y + size_t(c) * a.ldy;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t m = m0 + 4 * (lane >> 4) + v;
+    if (m >= a.M) continue;
+    float g = acc[0][v];
+    if constexpr (WSPLIT) g = g + accl[0][v] * (1.0f / 2048.0f);
+    g *= r;
+    if constexpr (EPI == EPI_STORE) {
+      yrow[m] = g;
+    } else if constexpr (EPI == EPI_RESID) {
+      yrow[m] = __fadd_rn(yrow[m], g);
+    } else {
+      float u = acc[NW - 1][v];
+      if constexpr (WSPLIT) u = u + accl[NW - 1][v] * (1.0f / 2048.0f);
+      u *= r;
+      if constexpr (EPI == EPI_SWIGLU_SLOW) {
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+        yrow[m] = __fmul_rn(__fmul_rn(g, sig), u);
+      } else {
+        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Causal GQA attention for a prompt chunk: query c (0 <= c < N) sits at
 // position base + c and attends cache positions 0 .. base + c (its own K/V
 // already appended).  Block (query tile of 8, kv head g): wave w serves q
@@ -352,7 +472,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
 
 hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, float eps, uint32_t N, uint32_t Npad,
                              uint32_t K, _Float16* xh, _Float16* xl, float* rs, hipStream_t s) {
-  if (Npad < N || Npad % GN || K % GK) return hipErrorInvalidValue;
+  if (Npad < N || Npad % 16 || K % GK) return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_rows_kernel, dim3(Npad), dim3(256), 0, s, x, ldx, norm, eps, N, K, xh, xl, rs);
   return hipGetLastError();
 }
@@ -384,6 +504,32 @@ hipError_t launch_gemm_mfma(uint32_t wtype, int epi, const GemmArgs& a, hipStrea
     case W_F16: return gemm_epi<W_F16>(epi, a, grid, s);
     case W_Q8_0: return gemm_epi<W_Q8_0>(epi, a, grid, s);
     case W_Q4_0: return gemm_epi<W_Q4_0>(epi, a, grid, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <uint32_t WT>
+static hipError_t skinny_epi(int epi, const SkinnyArgs& a, dim3 grid, hipStream_t s) {
+  const dim3 block(SK_WAVES * 64);
+  switch (epi) {
+    case EPI_STORE: hipLaunchKernelGGL((skinny_mfma_kernel<WT, EPI_STORE>), grid, block, 0, s, a); break;
+    case EPI_RESID: hipLaunchKernelGGL((skinny_mfma_kernel<WT, EPI_RESID>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU_SLOW: hipLaunchKernelGGL((skinny_mfma_kernel<WT, EPI_SWIGLU_SLOW>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU_FAST: hipLaunchKernelGGL((skinny_mfma_kernel<WT, EPI_SWIGLU_FAST>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_skinny_mfma(uint32_t wtype, int epi, const SkinnyArgs& a, hipStream_t s) {
+  if (a.N == 0 || a.N > 16 || a.M == 0 || a.K % (SK_WAVES * 32)) return hipErrorInvalidValue;
+  const bool dual = epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST;
+  if (dual && !a.w3) return hipErrorInvalidValue;
+  const dim3 grid((a.M + 15) / 16);
+  switch (wtype) {
+    case W_F16: return skinny_epi<W_F16>(epi, a, grid, s);
+    case W_Q8_0: return skinny_epi<W_Q8_0>(epi, a, grid, s);
+    case W_Q4_0: return skinny_epi<W_Q4_0>(epi, a, grid, s);
     default: return hipErrorInvalidValue;
   }
 }
