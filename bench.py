@@ -8,6 +8,12 @@ uniform-random prompt, greedy, KV cache 768.  One step = one frame (one
 Slow-AR decode step + the Fast-AR's 9 codebook passes + sampling); the timed
 window runs from after prefill to the last frame's codes (HIP events inside
 the library).  Prints one JSON line.
+
+Workload "full_b8": the voice-clone batch shape: 8 concurrent requests on
+the same f16 model, each a 1500-position prompt (250 text ids, 1000
+reference frames with uniform random codes, 250 text ids), MFMA prefill,
+then 1024 frames per request decoded together at batch 8, KV cache 2560.
+`value` is then the aggregate frames/s of the batch.
 """
 
 import argparse
@@ -23,11 +29,13 @@ sys.path[:0] = [os.path.join(ROOT, "fish-s2pro_amd"), ROOT]
 HBM_PEAK_GBS = 8000.0
 
 WORKLOADS = {
-    # name: (shape, prompt, frames, max_seq, temperature, top_p, top_k)
-    "full": ("full", 256, 512, 768, 0.0, 1.0, 0),
-    "full_q8": ("full_q8", 256, 512, 768, 0.7, 0.9, 0),
-    "full_q4": ("full_q4", 256, 1024, 1280, 0.0, 1.0, 0),
-    "tiny": ("tiny", 32, 16, 64, 0.0, 1.0, 0),
+    # name: (shape, prompt, frames, max_seq, temperature, top_p, top_k, requests, reference frames)
+    "full": ("full", 256, 512, 768, 0.0, 1.0, 0, 1, 0),
+    "full_q8": ("full_q8", 256, 512, 768, 0.7, 0.9, 0, 1, 0),
+    "full_q4": ("full_q4", 256, 1024, 1280, 0.0, 1.0, 0, 1, 0),
+    "full_b8": ("full", 1500, 1024, 2560, 0.0, 1.0, 0, 8, 1000),
+    "tiny": ("tiny", 32, 16, 64, 0.0, 1.0, 0, 1, 0),
+    "tiny_b8": ("tiny", 48, 16, 80, 0.0, 1.0, 0, 8, 32),
 }
 
 
@@ -35,22 +43,33 @@ def log(msg):
     print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
 
 
-def frame_bytes(spec, shape, avg_t, kv_bytes=4):
-    """Algorithmic HBM bytes of one frame: Slow weights once, Fast weights for
-    9 passes (positions 0 and 1 share one pass), the candidate head rows,
-    embeddings, norms and KV reads/writes at the stored KV dtype."""
+def frame_bytes(spec, shape, avg_t, kv_bytes=4, nseq=1):
+    """Algorithmic HBM bytes of one decode step of nseq requests: Slow weights
+    once, Fast weights for 9 passes (positions 0 and 1 share one pass), the
+    candidate head rows and norms once; per request the embeddings and the KV
+    reads/writes at the stored KV dtype."""
     b_w = {1: 2.0, 8: 34 / 32, 2: 18 / 32}[spec["linear_type"]]
     d, L, Lf = spec["dim"], spec["slow_layers"], spec["fast_layers"]
     ncb, C = spec["num_codebooks"], spec["codebook_size"]
     kv = spec["kv_heads"] * spec["head_dim"]
     slow = L * shape.linear_params_per_slow_layer() * b_w
-    slow += L * (2 * d + 2 * spec["head_dim"]) * 2 + 2 * d + (ncb + 1) * d * 2
+    slow += L * (2 * d + 2 * spec["head_dim"]) * 2 + 2 * d + nseq * (ncb + 1) * d * 2
     slow += (C + 1) * d * 2  # semantic rows + im_end of the tied head
-    slow += avg_t * L * 2 * kv * kv_bytes + L * 2 * kv * kv_bytes
-    fast_pass = Lf * shape.linear_params_per_fast_layer() * b_w + d * C * b_w + Lf * 2 * d * 2 + 2 * d + d * 2
+    slow += nseq * (avg_t * L * 2 * kv * kv_bytes + L * 2 * kv * kv_bytes)
+    fast_pass = Lf * shape.linear_params_per_fast_layer() * b_w + d * C * b_w + Lf * 2 * d * 2 + 2 * d + nseq * d * 2
     fkv = spec["fast_kv_heads"] * spec["fast_head_dim"]
-    fast = (ncb - 1) * fast_pass + Lf * 2 * fkv * kv_bytes * (ncb * (ncb + 1) // 2 + ncb)
+    fast = (ncb - 1) * fast_pass + nseq * Lf * 2 * fkv * kv_bytes * (ncb * (ncb + 1) // 2 + ncb)
     return slow + fast
+
+
+def prefill_flops(spec, shape, n_tok, nseq=1):
+    """Useful FLOPs of prompt prefill: 2 per weight per token in the Slow-AR
+    linears, plus causal attention (QK and PV, 4 hd per query-key pair per
+    head)."""
+    L = spec["slow_layers"]
+    lin = 2.0 * L * shape.linear_params_per_slow_layer() * n_tok
+    attn = 2.0 * L * spec["heads"] * spec["head_dim"] * n_tok * (n_tok + 1)
+    return nseq * (lin + attn)
 
 
 def counter_traffic(kernel, workload):
@@ -105,7 +124,7 @@ def main():
 
     from s2hip import Engine, synth
 
-    shape_name, prompt_len, frames, max_seq, temp, top_p, top_k = WORKLOADS[args.workload]
+    shape_name, prompt_len, frames, max_seq, temp, top_p, top_k, nseq, ref_frames = WORKLOADS[args.workload]
     if args.steps:
         frames = args.steps
     if args.prompt:
@@ -120,27 +139,44 @@ def main():
     eng = Engine(path, max_seq, shape.im_end_id, use_graph=not args.no_graph)
     spec = eng.spec
     log(f"engine loaded in {time.time() - t0:.1f}s ({spec['weight_bytes'] / 1e9:.2f} GB in HBM)")
-    prompt = synth.synthetic_prompt(shape, prompt_len, seed=shape.seed)
-    kw = dict(temperature=temp, top_p=top_p, top_k=top_k, min_tokens_before_end=1 << 30, rng_state=shape.seed)
+    kw = dict(temperature=temp, top_p=top_p, top_k=top_k, min_tokens_before_end=1 << 30)
+    if nseq == 1:
+        prompt = synth.synthetic_prompt(shape, prompt_len, seed=shape.seed)
+
+        def run():
+            return eng.generate_codes(prompt, frames, rng_state=shape.seed, **kw)
+    else:
+        prompts = [synth.voice_clone_prompt(shape, prompt_len - ref_frames, ref_frames, seed=shape.seed + 100 * b)
+                   for b in range(nseq)]
+
+        def run():
+            rb = eng.generate_codes_batch(prompts, frames, rng_states=[shape.seed + b for b in range(nseq)], **kw)
+            return {"n_frames": rb["total_frames"], "prefill_ms": rb["prefill_ms"], "decode_ms": rb["decode_ms"],
+                    "graph_used": rb["graph_used"]}
     for i in range(args.warmup):
-        r = eng.generate_codes(prompt, frames, **kw)
+        r = run()
         log(f"warmup {i}: {r['n_frames']} frames, prefill {r['prefill_ms']:.1f} ms, decode {r['decode_ms']:.1f} ms")
-    r = eng.generate_codes(prompt, frames, **kw)
+    r = run()
     n = r["n_frames"]
     dec_s = r["decode_ms"] / 1e3
     fps = n / dec_s
-    log(f"timed: {n} frames in {dec_s * 1e3:.1f} ms -> {fps:.1f} frames/s (prefill {r['prefill_ms']:.1f} ms)")
+    log(f"timed: {n} frames ({nseq} requests) in {dec_s * 1e3:.1f} ms -> {fps:.1f} frames/s "
+        f"(prefill {r['prefill_ms']:.1f} ms)")
 
-    avg_t = prompt_len + n / 2.0
-    fb = frame_bytes(spec, shape, avg_t)
-    kern = "slow_w13"
+    steps = n // nseq  # decode steps (frames per request)
+    avg_t = prompt_len + steps / 2.0
+    fb = frame_bytes(spec, shape, avg_t, nseq=nseq)  # bytes per decode step
+    kern = "slow_w13" if nseq == 1 else f"slow_w13_b{nseq}"
     us, kb = eng.time_kernel(kern, reps=5)
     achieved = kb / (us * 1e-6) / 1e9
     log(f"{kern}: {us:.2f} us/launch, {kb / 1e6:.2f} MB -> {achieved:.0f} GB/s")
     other = {}
-    for k in ("slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn", "fast_head",
-              "sample_fast", "sample_slow", "sample_fast_topp", "sample_slow_topp", "sample_fast_default",
-              "fast_frame", "empty", "hbm_copy"):
+    names = ["slow_wqkv", "slow_wo", "slow_w2", "slow_head", "slow_attn", "fast_attn", "fast_head",
+             "sample_fast", "sample_slow", "sample_fast_topp", "sample_slow_topp", "sample_fast_default",
+             "fast_frame", "empty", "hbm_copy"]
+    if nseq > 1:
+        names = [f"{k}_b{nseq}" for k in ("slow_wqkv", "slow_wo", "slow_w2")] + names
+    for k in names:
         ku, kbb = eng.time_kernel(k, reps=5)
         other[k] = {"us": round(ku, 3)}
         if kbb:
@@ -165,23 +201,26 @@ def main():
         "value": round(fps, 2),
         "unit": "frames/s",
         "n_gpus": 1,
-        "steps": n,
+        "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dec_s * 1e3 / max(1, n), 4),
+        "ms_per_step": round(dec_s * 1e3 / max(1, steps), 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {1: "f16", 8: "q8_0", 2: "q4_0"}[spec["linear_type"]] + " weights, f32 accumulate",
         "data": "synthetic (random-init N(0,0.02) weights, uniform random prompt ids)",
         "config": {"workload": f"{args.workload}: {spec['slow_layers']}+{spec['fast_layers']} layers d={spec['dim']}, "
-                               f"{prompt_len}-token prompt, {n} frames, KV {max_seq}",
-                   "prompt_tokens": prompt_len, "frames": n, "kv_cache": max_seq, "sampler":
+                               f"{nseq} x {prompt_len}-token prompt, {steps} frames per request, KV {max_seq}",
+                   "requests": nseq, "prompt_tokens": prompt_len, "reference_frames": ref_frames,
+                   "frames": steps, "kv_cache": max_seq, "sampler":
                        {"temperature": temp, "top_p": top_p, "top_k": top_k}, "parallelism": "single GPU"},
         "codes_per_s": round(fps * spec["num_codebooks"], 1),
         "prefill_ms": round(r["prefill_ms"], 2),
+        "prefill_tflops": round(prefill_flops(spec, shape, prompt_len, nseq) / (r["prefill_ms"] * 1e-3) / 1e12, 2),
         "frame_bytes": round(fb),
-        "frame_roofline_frac": round(fb * fps / (HBM_PEAK_GBS * 1e9), 4),
-        "roofline": {"bound": "hbm", "kernel": f"gemv {kern} (fused RMSNorm + w1/w3 + SwiGLU)",
+        "frame_roofline_frac": round(fb * (steps / dec_s) / (HBM_PEAK_GBS * 1e9), 4),
+        "roofline": {"bound": "hbm", "kernel": (f"gemv {kern}" if nseq == 1 else f"skinny MFMA {kern}") +
+                     " (fused RMSNorm + w1/w3 + SwiGLU)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": counter_traffic(kern, args.workload),
                      "bytes_per_launch": round(kb), "avg_us": round(us, 3)},

@@ -3,12 +3,14 @@
 // One engine = one loaded transformer GGUF on one device:
 //   * every tensor uploaded once in its GGUF layout (F16 / Q8_0 / Q4_0 rows),
 //     RMSNorm gains expanded to f32;
-//   * Slow-AR KV cache f32 [layer][kv_head][max_seq][head_dim];
-//   * Fast-AR KV cache f32 [layer][kv_head][num_codebooks + 1][head_dim],
+//   * Slow-AR KV cache f32 [slot][layer][kv_head][max_seq][head_dim];
+//   * Fast-AR KV cache f32 [slot][layer][kv_head][num_codebooks + 1][head_dim],
 //     filled incrementally (9 weight passes per frame instead of the
 //     reference's prefix recompute, crates/fish_s2_infer/src/fast_ar.rs:417-424);
-//   * a DevState block (positions, frame counter, RNG state, frame codes) so
-//     one captured HIP graph replays every frame with no host round trip.
+//   * a DevState block per slot (positions, frame counter, RNG state, frame
+//     codes) so one captured HIP graph replays every frame with no host round
+//     trip.  A batch of requests decodes together, one slot each: every frame
+//     kernel reads a weight matrix once for all of the batch's columns.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -39,7 +41,9 @@ void hip_check(hipError_t e, const char* what) {
 
 [[noreturn]] void fail(const std::string& m) { throw std::runtime_error(m); }
 
-constexpr uint32_t PREFILL_COLS = 4;     // decode-path columns (Fast-AR positions 0 and 1, op tests)
+constexpr uint32_t PREFILL_COLS = 4;     // decode-path columns per pass of the GEMV prefill
+constexpr uint32_t MAX_SEQS = 16;        // requests per batched generate call
+constexpr uint32_t ACT_COLS = 2 * MAX_SEQS;  // activation columns (Fast-AR pass 0 has two per request)
 constexpr uint32_t PREFILL_CHUNK = 512;  // prompt tokens per MFMA prefill pass
 constexpr uint32_t FRAME_BATCH = 4;
 constexpr size_t WEIGHT_PAD = 256;  // trailing bytes so block loads never leave a buffer
@@ -95,8 +99,8 @@ class Engine {
   void eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out);
   void fast_logits(const float* hidden, const uint32_t* prefix, size_t plen, float* logits);
   void fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampler& smp, uint64_t* rng, uint32_t* codes);
-  void generate(const int32_t* prompt, size_t cols, const s2hip_gen_params& p, uint64_t* rng, int32_t* codes,
-                uint32_t* n_frames, s2hip_gen_stats* stats);
+  void generate(uint32_t nseq, const int32_t* const* prompts, const size_t* cols, const s2hip_gen_params& p,
+                uint64_t* rngs, int32_t* const* codes, uint32_t* n_frames, s2hip_gen_stats* stats);
   uint32_t n_past_host = 0;
 
   // op level
@@ -130,13 +134,20 @@ class Engine {
   void gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
             const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row, uint32_t out_rows,
             const uint32_t* done);
-  void enqueue_slow_layers(uint32_t ncol, const uint32_t* done);
-  void enqueue_head(uint32_t col, bool full, const uint32_t* done);
-  void enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* done);
-  void enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done);
-  void enqueue_frame(const SamplerCfg& cfg);
-  void enqueue_prefill(const int32_t* prompt_dev, size_t n_tok);
-  void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok);
+  // linear over ncol columns: GEMV kernels for 1-2, skinny MFMA for more
+  void lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
+           const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
+           uint32_t out_rows, const uint32_t* done);
+  // ncol = nseq * cps columns of slots seq0 .. seq0 + nseq - 1 in h_
+  void enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done);
+  void enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done);
+  void enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done);
+  void enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint32_t* done);
+  void enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_stride);
+  void enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
+  void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
+  void ensure_slots(uint32_t n);
+  void validate_prompt(const int32_t* prompt, size_t cols);
   void mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
           uint32_t n, uint32_t npad, float* y, uint32_t ldy);
   // batched columns (3..16): split planes + skinny MFMA product
@@ -145,7 +156,7 @@ class Engine {
                  uint32_t out_rows, const uint32_t* done);
   void ensure_prompt(size_t n_int);
   void ensure_codes(size_t n_int);
-  void check_state_err();
+  void check_state_err(uint32_t nseq = 1);
 
   hipStream_t stream_ = nullptr;
   std::vector<void*> allocs_;
@@ -170,6 +181,9 @@ class Engine {
   float *h_ = nullptr, *qkv_ = nullptr, *q_ = nullptr, *att_ = nullptr, *part_ = nullptr, *act_ = nullptr;
   float *hn_ = nullptr, *logits_c_ = nullptr, *logits_full_ = nullptr;
   float *kc_ = nullptr, *vc_ = nullptr;
+  size_t slot_kv_ = 0, fslot_kv_ = 0;  // floats per slot in the slow / fast caches
+  uint32_t kv_slots_ = 0;
+  uint64_t kv_gen_ = 0;  // bumped whenever the caches are reallocated
   float2 *rope_slow_ = nullptr, *rope_fast_ = nullptr;
   uint32_t attn_chunks_ = 1;
   uint32_t attn_mode_ = ATTN_SPLIT;
@@ -182,8 +196,9 @@ class Engine {
   float *flogits_ = nullptr, *fkc_ = nullptr, *fvc_ = nullptr;
   uint32_t fctx_ = 11;
 
-  DevState* st_ = nullptr;
-  DevState* st_host_ = nullptr;  // pinned
+  DevState* st_ = nullptr;        // [MAX_SEQS]
+  DevState* st_host_ = nullptr;   // pinned [MAX_SEQS]
+  BatchState* batch_ = nullptr;
   uint32_t* done_host_ = nullptr;  // pinned [2]
   int32_t* codes_dev_ = nullptr;
   size_t codes_cap_ = 0;
@@ -192,8 +207,12 @@ class Engine {
 
   hipGraphExec_t graph_exec_ = nullptr;
   hipGraph_t graph_ = nullptr;
+  // what the captured frame depends on
   SamplerCfg graph_cfg_{};
   int32_t* graph_codes_ = nullptr;
+  size_t graph_codes_stride_ = 0;
+  uint32_t graph_nseq_ = 0;
+  uint64_t graph_kv_gen_ = 0;
 };
 
 Engine::Engine(const s2hip_config& cfg) {
@@ -321,8 +340,11 @@ Engine::Engine(const s2hip_config& cfg) {
   head_rows_ = dalloc<uint32_t>(rows.size());
   HIPC(hipMemcpy(head_rows_, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
 
-  // activations
-  const uint32_t NC = PREFILL_COLS;
+  // activations: Slow-AR decode columns for a batch of MAX_SEQS requests,
+  // Fast-AR columns for twice that (two per request in the first pass of a
+  // frame)
+  static_assert(PREFILL_COLS <= MAX_SEQS, "GEMV prefill columns");
+  const uint32_t NC = MAX_SEQS;
   const uint64_t qkv_w = q + 2 * kv;
   // two attention kernels per layer (partials, then merge) by default; with
   // S2HIP_ATTN_FUSED=1 one kernel whose last block per kv head merges (its
@@ -336,8 +358,8 @@ Engine::Engine(const s2hip_config& cfg) {
   q_ = dalloc<float>(size_t(NC) * q);
   att_ = dalloc<float>(size_t(NC) * q);
   part_ = dalloc<float>(size_t(NC) * s.heads * attn_chunks_ * (s.head_dim + 2));
-  counters_ = dalloc<uint32_t>(size_t(NC) * std::max(s.kv_heads, s.fast_kv_heads));
-  HIPC(hipMemset(counters_, 0, size_t(NC) * std::max(s.kv_heads, s.fast_kv_heads) * 4));
+  counters_ = dalloc<uint32_t>(size_t(ACT_COLS) * std::max(s.kv_heads, s.fast_kv_heads));
+  HIPC(hipMemset(counters_, 0, size_t(ACT_COLS) * std::max(s.kv_heads, s.fast_kv_heads) * 4));
   act_ = dalloc<float>(size_t(NC) * s.ffn);
   {
     const size_t CH = PREFILL_CHUNK, CHP = gemm_rows_pad(PREFILL_CHUNK);
@@ -352,33 +374,31 @@ Engine::Engine(const s2hip_config& cfg) {
     pxl_ = dalloc<_Float16>(CHP * kmax);
     if (s.dim % 32 || q % 32 || s.ffn % 32) fail("prefill needs embedding, attention and FFN widths divisible by 32");
   }
-  hn_ = dalloc<float>(s.dim);
-  logits_c_ = dalloc<float>(n_cand_);
+  hn_ = dalloc<float>(size_t(MAX_SEQS) * s.dim);
+  logits_c_ = dalloc<float>(size_t(MAX_SEQS) * n_cand_);
   logits_full_ = dalloc<float>(s.vocab);
-  const size_t kv_elems = size_t(s.slow_layers) * kv * s.max_seq_len;
-  kc_ = dalloc<float>(kv_elems);
-  vc_ = dalloc<float>(kv_elems);
-  HIPC(hipMemset(kc_, 0, kv_elems * 4));
-  HIPC(hipMemset(vc_, 0, kv_elems * 4));
   fctx_ = s.num_codebooks + 1;
+  slot_kv_ = size_t(s.slow_layers) * kv * s.max_seq_len;
+  fslot_kv_ = size_t(s.fast_layers) * fkv * fctx_;
   rope_slow_ = dalloc<float2>(size_t(s.max_seq_len) * (s.head_dim / 2));
   rope_fast_ = dalloc<float2>(size_t(fctx_) * (s.fast_head_dim / 2));
   build_rope(rope_slow_, s.max_seq_len, s.head_dim, s.rope_base);
   build_rope(rope_fast_, fctx_, s.fast_head_dim, s.fast_rope_base);
-  fh_ = dalloc<float>(2 * size_t(s.dim));
-  fqkv_ = dalloc<float>(2 * (fq + 2 * fkv));
-  fq_ = dalloc<float>(2 * fq);
-  fatt_ = dalloc<float>(2 * fq);
-  fpart_ = dalloc<float>(2 * size_t(s.fast_heads) * attention_chunks(fctx_, attn_mode_) * (s.fast_head_dim + 2));
-  fact_ = dalloc<float>(2 * size_t(s.fast_ffn));
-  flogits_ = dalloc<float>(s.codebook_size);
-  fkc_ = dalloc<float>(size_t(s.fast_layers) * fkv * fctx_);
-  fvc_ = dalloc<float>(size_t(s.fast_layers) * fkv * fctx_);
-  HIPC(hipMemset(fkc_, 0, size_t(s.fast_layers) * fkv * fctx_ * 4));
-  HIPC(hipMemset(fvc_, 0, size_t(s.fast_layers) * fkv * fctx_ * 4));
-  st_ = dalloc<DevState>(1);
-  HIPC(hipMemset(st_, 0, sizeof(DevState)));
-  HIPC(hipHostMalloc(reinterpret_cast<void**>(&st_host_), sizeof(DevState), hipHostMallocDefault));
+  const uint32_t FC = ACT_COLS;
+  fh_ = dalloc<float>(size_t(FC) * s.dim);
+  fqkv_ = dalloc<float>(size_t(FC) * (fq + 2 * fkv));
+  fq_ = dalloc<float>(size_t(FC) * fq);
+  fatt_ = dalloc<float>(size_t(FC) * fq);
+  fpart_ = dalloc<float>(size_t(FC) * s.fast_heads * attention_chunks(fctx_, attn_mode_) * (s.fast_head_dim + 2));
+  fact_ = dalloc<float>(size_t(FC) * s.fast_ffn);
+  flogits_ = dalloc<float>(size_t(MAX_SEQS) * s.codebook_size);
+  ensure_slots(1);
+  static_assert(sizeof(DevState) % 4 == 0, "DevState words");
+  st_ = dalloc<DevState>(MAX_SEQS);
+  HIPC(hipMemset(st_, 0, MAX_SEQS * sizeof(DevState)));
+  batch_ = dalloc<BatchState>(1);
+  HIPC(hipMemset(batch_, 0, sizeof(BatchState)));
+  HIPC(hipHostMalloc(reinterpret_cast<void**>(&st_host_), MAX_SEQS * sizeof(DevState), hipHostMallocDefault));
   HIPC(hipHostMalloc(reinterpret_cast<void**>(&done_host_), 2 * sizeof(uint32_t), hipHostMallocDefault));
   s.weight_bytes = 0;
   for (auto& L : slow_) s.weight_bytes += L.wqkv.bytes + L.wo.bytes + L.w1.bytes + L.w2.bytes + L.w3.bytes;
@@ -506,24 +526,44 @@ void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, con
   }
 }
 
-void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
+void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
+                 const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
+                 uint32_t out_rows, const uint32_t* done) {
+  if (ncol <= 2 || L.in % 256) {
+    gemv(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, row_base, extra_row, out_rows, done);
+    return;
+  }
+  for (uint32_t c = 0; c < ncol; c += 16) {
+    const uint32_t n = std::min(16u, ncol - c);
+    mm_skinny(L, L3, epi, x + size_t(c) * ldx, ldx, norm, eps, n, y + size_t(c) * ldy, ldy, row_base, extra_row,
+              out_rows, done);
+  }
+}
+
+// Slow-AR layers (forward_decode_sequence, slow_ar.rs:539-556) over nseq
+// slots from seq0 with cps consecutive positions each, then n_past += cps per
+// slot.  done (nullable) stops the linears; attention and the position
+// update skip each finished slot by its own done word.
+void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done) {
   const s2hip_spec& s = spec;
   const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim, qkv_w = q + 2 * kv;
+  const uint32_t ncol = nseq * cps;
+  DevState* st = st_ + seq0;
   for (uint32_t l = 0; l < s.slow_layers; ++l) {
     const SlowLayer& L = slow_[l];
-    gemv(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, 0, NO_ROW, L.wqkv.out, done);
+    lin(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, 0, NO_ROW, L.wqkv.out, done);
     AttnArgs aa{};
     aa.qkv = qkv_;
     aa.q_norm = L.q_norm;
     aa.k_norm = L.k_norm;
     aa.eps = s.eps;
     aa.rope = rope_slow_;
-    aa.k_cache = kc_ + size_t(l) * kv * s.max_seq_len;
-    aa.v_cache = vc_ + size_t(l) * kv * s.max_seq_len;
+    aa.k_cache = kc_ + size_t(seq0) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
+    aa.v_cache = vc_ + size_t(seq0) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
     aa.part = part_;
     aa.counters = counters_;
     aa.out = att_;
-    aa.pos_ptr = &st_->n_past;
+    aa.pos_ptr = &st->n_past;
     aa.pos_offset = 0;
     aa.H = s.heads;
     aa.Hkv = s.kv_heads;
@@ -533,35 +573,42 @@ void Engine::enqueue_slow_layers(uint32_t ncol, const uint32_t* done) {
     aa.max_chunks = attn_chunks_;
     aa.mode = attn_mode_;
     aa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
-    aa.done = done;
-    aa.err = &st_->err;
+    aa.done = done ? &st->done : nullptr;
+    aa.err = &st->err;
+    aa.cols_per_seq = cps;
+    aa.seq_stride_words = sizeof(DevState) / 4;
+    aa.seq_stride_kv = slot_kv_;
     HIPC(launch_attention(aa, stream_));
-    gemv(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.wo.out, done);
-    gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, done);
-    gemv(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.w2.out, done);
+    lin(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.wo.out, done);
+    lin(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, done);
+    lin(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.w2.out, done);
   }
-  HIPC(launch_add_position(st_, ncol, stream_));
+  HIPC(launch_add_position(st, cps, nseq, stream_));
 }
 
 // SlowArOutputHeadF16Weights::forward_logits (slow_ar.rs:943-955): post-norm
-// hidden -> tied embedding rows.  Generation only needs the candidate rows
-// (semantic ids + im_end); every other id is masked to -inf before sampling.
-void Engine::enqueue_head(uint32_t col, bool full, const uint32_t* done) {
+// hidden of the first ncol columns of h_ -> tied embedding rows.  Generation
+// only needs the candidate rows (semantic ids + im_end); every other id is
+// masked to -inf before sampling.  hn [ncol][dim], logits [ncol][n_cand].
+void Engine::enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done) {
   const s2hip_spec& s = spec;
-  HIPC(launch_rms_norm(h_ + size_t(col) * s.dim, norm_, hn_, s.dim, 1, s.eps, done, stream_));
-  gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_c_, n_cand_, s.semantic_begin, head_extra_,
-       n_cand_, done);
+  HIPC(launch_rms_norm(h_, norm_, hn, s.dim, ncol, s.eps, done, stream_));
+  lin(head_full_, nullptr, EPI_STORE, ncol, hn, s.dim, nullptr, 0.0f, logits, n_cand_, s.semantic_begin, head_extra_,
+      n_cand_, done);
   if (full)
-    gemv(head_full_, nullptr, EPI_STORE, 1, hn_, s.dim, nullptr, 0.0f, logits_full_, s.vocab, 0, NO_ROW, s.vocab, done);
+    gemv(head_full_, nullptr, EPI_STORE, 1, hn, s.dim, nullptr, 0.0f, logits_full_, s.vocab, 0, NO_ROW, s.vocab, done);
 }
 
-void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* done) {
+// Fast-AR layers (forward_prefill, fast_ar.rs:245-358) over nseq slots with cps consecutive
+// positions each from p0 (every slot is at the same Fast-AR position).
+void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done) {
   const s2hip_spec& s = spec;
   const uint32_t fq = s.fast_heads * s.fast_head_dim, fkv = s.fast_kv_heads * s.fast_head_dim;
   const uint32_t w = fq + 2 * fkv;
+  const uint32_t ncol = nseq * cps;
   for (uint32_t l = 0; l < s.fast_layers; ++l) {
     const FastLayer& L = fast_[l];
-    gemv(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out, done);
+    lin(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out, done);
     AttnArgs aa{};
     aa.qkv = fqkv_;
     aa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
@@ -583,28 +630,33 @@ void Engine::enqueue_fast_layers(uint32_t ncol, uint32_t p0, const uint32_t* don
     aa.max_chunks = attention_chunks(fctx_, attn_mode_);
     aa.mode = attn_mode_;
     aa.scale = 1.0f / std::sqrt(float(s.fast_head_dim));  // fast_ar.rs:60-62
-    aa.done = done;
+    aa.done = done ? &st_->done : nullptr;
     aa.err = &st_->err;
+    aa.cols_per_seq = cps;
+    aa.seq_stride_words = sizeof(DevState) / 4;
+    aa.seq_stride_kv = fslot_kv_;
     HIPC(launch_attention(aa, stream_));
-    gemv(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
-    gemv(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
-         L.w1.out, done);
-    gemv(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.w2.out, done);
+    lin(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
+    lin(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
+        L.w1.out, done);
+    lin(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.w2.out, done);
   }
 }
 
-// generate_codebooks_for_semantic (fast_ar.rs:440-470), incremental: sub-step 1
-// runs positions 0 (slow hidden) and 1 (fast_emb[code0]) together, each later
-// sub-step appends one position.  The sampler writes the next input row.
-void Engine::enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done) {
+// generate_codebooks_for_semantic (fast_ar.rs:440-470), incremental, for the
+// slots 0 .. nseq - 1: sub-step 1 runs positions 0 (slow hidden) and 1
+// (fast_emb[code0]) together, each later sub-step appends one position.  The
+// sampler writes each slot's next input row.
+void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint32_t* done) {
   const s2hip_spec& s = spec;
-  HIPC(launch_fast_begin(st_, hn_, fast_emb_, fh_, s.dim, s.codebook_size, s.semantic_begin, s.semantic_end,
+  HIPC(launch_fast_begin(st_, hn_, fast_emb_, fh_, s.dim, s.codebook_size, s.semantic_begin, s.semantic_end, nseq,
                          stream_));
-  uint32_t ncol = 2, p0 = 0;
+  uint32_t cps = 2, p0 = 0;
   for (uint32_t cb = 1; cb < s.num_codebooks; ++cb) {
-    enqueue_fast_layers(ncol, p0, done);
-    gemv(fast_out_, nullptr, EPI_STORE, 1, fh_ + size_t(ncol - 1) * s.dim, s.dim, fast_norm_, s.fast_eps, flogits_,
-         s.codebook_size, 0, NO_ROW, s.codebook_size, done);
+    enqueue_fast_layers(nseq, cps, p0, done);
+    // the last position of each slot: rows cps - 1, 2 cps - 1, ...
+    lin(fast_out_, nullptr, EPI_STORE, nseq, fh_ + size_t(cps - 1) * s.dim, cps * s.dim, fast_norm_, s.fast_eps,
+        flogits_, s.codebook_size, 0, NO_ROW, s.codebook_size, done);
     SampleArgs sa{};
     sa.logits = flogits_;
     sa.n = s.codebook_size;
@@ -615,25 +667,28 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, const uint32_t* done) {
     sa.fast_emb = fast_emb_;
     sa.next_input = (cb + 1 < s.num_codebooks) ? fh_ : nullptr;
     sa.dim = s.dim;
+    sa.n_seq = nseq;
     HIPC(launch_sample_fast(sa, stream_));
-    p0 += ncol;
-    ncol = 1;
+    p0 += cps;
+    cps = 1;
   }
 }
 
-// One generate_codes loop iteration (generate.rs:165-211): Fast-AR codebooks
-// for the current main token, Slow-AR step on [main, codes...], next sample.
-void Engine::enqueue_frame(const SamplerCfg& cfg) {
+// One generate_codes loop iteration (generate.rs:165-211) for the slots
+// 0 .. nseq - 1: Fast-AR codebooks for each current main token, one Slow-AR
+// step on each [main, codes...], the next samples.  Every kernel stops once
+// the whole batch is done; finished slots are skipped by their own state.
+void Engine::enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_stride) {
   const s2hip_spec& s = spec;
-  const uint32_t* done = &st_->done;
-  enqueue_fast_frame(cfg, done);
+  const uint32_t* done = &batch_->done_all;
+  enqueue_fast_frame(cfg, nseq, done);
   EmbedArgs ea{};
   ea.tokens = nullptr;
   ea.state = st_;
   ea.emb = emb_;
   ea.cb_emb = cb_emb_;
   ea.h = h_;
-  ea.n = 1;
+  ea.n = nseq;
   ea.dim = s.dim;
   ea.vocab = s.vocab;
   ea.cb_rows = uint32_t(cb_rows_);
@@ -646,8 +701,8 @@ void Engine::enqueue_frame(const SamplerCfg& cfg) {
   ea.done = done;
   ea.err = &st_->err;
   HIPC(launch_embed(ea, stream_));
-  enqueue_slow_layers(1, done);
-  enqueue_head(0, false, done);
+  enqueue_slow_layers(nseq, 1, 0, done);
+  enqueue_head(nseq, hn_, logits_c_, false, done);
   SampleArgs sa{};
   sa.logits = logits_c_;
   sa.ids = head_rows_;
@@ -659,6 +714,9 @@ void Engine::enqueue_frame(const SamplerCfg& cfg) {
   sa.after_step = 1;
   sa.codes_out = codes_dev_;
   sa.num_codebooks = s.num_codebooks;
+  sa.n_seq = nseq;
+  sa.codes_stride = codes_stride;
+  sa.batch = batch_;
   HIPC(launch_sample_slow(sa, stream_));
 }
 
@@ -666,8 +724,8 @@ void Engine::enqueue_frame(const SamplerCfg& cfg) {
 // chunks of up to PREFILL_CHUNK tokens go through each layer together: every
 // linear is one MFMA product over the chunk (weights read once per chunk),
 // QK-norm + RoPE + KV append for all of the chunk's positions, then causal
-// attention of each token over the cache.  Leaves the last token's residual
-// row in decode column 0 for the output head.
+// attention of each token over the cache.  One slot (`seq`) at a time;
+// leaves the last token's residual row in decode column 0 for the output head.
 void Engine::mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
                 uint32_t n, uint32_t npad, float* y, uint32_t ldy) {
   HIPC(launch_split_rows(x, ldx, norm, eps, n, npad, L.in, pxh_, pxl_, prs_, stream_));
@@ -710,7 +768,7 @@ void Engine::mm_skinny(const DevLin& L, const DevLin* L3, int epi, const float* 
   HIPC(launch_skinny_mfma(L.type, epi, g, stream_));
 }
 
-void Engine::enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok) {
+void Engine::enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok, uint32_t seq) {
   const s2hip_spec& s = spec;
   const uint32_t cdim = s.num_codebooks + 1;
   size_t t = 0;
@@ -732,22 +790,23 @@ void Engine::enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok) {
     ea.sem_end = s.semantic_end;
     ea.sem_scale = 1.0f / std::sqrt(float(cdim));
     ea.scale_enabled = s.scale_codebook_embeddings;
-    ea.err = &st_->err;
+    ea.err = &st_[seq].err;
     HIPC(launch_embed(ea, stream_));
-    enqueue_slow_layers(nc, nullptr);
+    enqueue_slow_layers(1, nc, seq, nullptr);
     t += nc;
   }
   if (nc > 1) HIPC(hipMemcpyAsync(h_, h_ + size_t(nc - 1) * s.dim, size_t(s.dim) * 4, hipMemcpyDeviceToDevice, stream_));
 }
 
-void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
+void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t seq) {
   if (prefill_gemv_) {
-    enqueue_prefill_gemv(prompt_dev, n_tok);
+    enqueue_prefill_gemv(prompt_dev, n_tok, seq);
     return;
   }
   const s2hip_spec& s = spec;
   const uint32_t cdim = s.num_codebooks + 1;
   const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim, qkv_w = q + 2 * kv;
+  DevState* st = st_ + seq;
   size_t t = 0;
   uint32_t nc = 0;
   while (t < n_tok) {
@@ -768,12 +827,12 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
     ea.sem_end = s.semantic_end;
     ea.sem_scale = 1.0f / std::sqrt(float(cdim));
     ea.scale_enabled = s.scale_codebook_embeddings;
-    ea.err = &st_->err;
+    ea.err = &st->err;
     HIPC(launch_embed(ea, stream_));
     for (uint32_t l = 0; l < s.slow_layers; ++l) {
       const SlowLayer& L = slow_[l];
-      float* kcl = kc_ + size_t(l) * kv * s.max_seq_len;
-      float* vcl = vc_ + size_t(l) * kv * s.max_seq_len;
+      float* kcl = kc_ + size_t(seq) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
+      float* vcl = vc_ + size_t(seq) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
       mm(L.wqkv, nullptr, EPI_STORE, ph_, s.dim, L.attn_norm, s.eps, nc, npad, pqkv_, qkv_w);
       QkvPostArgs qa{};
       qa.qkv = pqkv_;
@@ -783,7 +842,7 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
       qa.q_norm = L.q_norm;
       qa.k_norm = L.k_norm;
       qa.rope = rope_slow_;
-      qa.pos_ptr = &st_->n_past;
+      qa.pos_ptr = &st->n_past;
       qa.pos_offset = 0;
       qa.H = s.heads;
       qa.Hkv = s.kv_heads;
@@ -791,14 +850,14 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
       qa.max_seq = s.max_seq_len;
       qa.ncol = nc;
       qa.eps = s.eps;
-      qa.err = &st_->err;
+      qa.err = &st->err;
       HIPC(launch_qkv_post(qa, stream_));
       PrefillAttnArgs pa{};
       pa.q = pq_;
       pa.k_cache = kcl;
       pa.v_cache = vcl;
       pa.out = patt_;
-      pa.pos_ptr = &st_->n_past;
+      pa.pos_ptr = &st->n_past;
       pa.pos_offset = 0;
       pa.N = nc;
       pa.H = s.heads;
@@ -811,7 +870,7 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok) {
       mm(L.w1, &L.w3, EPI_SWIGLU_SLOW, ph_, s.dim, L.ffn_norm, s.eps, nc, npad, pact_, s.ffn);
       mm(L.w2, nullptr, EPI_RESID, pact_, s.ffn, nullptr, 0.0f, nc, npad, ph_, s.dim);
     }
-    HIPC(launch_add_position(st_, nc, stream_));
+    HIPC(launch_add_position(st, nc, 1, stream_));
     t += nc;
   }
   if (nc) HIPC(hipMemcpyAsync(h_, ph_ + size_t(nc - 1) * s.dim, size_t(s.dim) * 4, hipMemcpyDeviceToDevice, stream_));
@@ -839,10 +898,35 @@ void Engine::ensure_codes(size_t n_int) {
   codes_dev_ = dalloc<int32_t>(codes_cap_);
 }
 
-void Engine::check_state_err() {
-  if (st_host_->err & ERR_TOKEN_RANGE) fail("token id out of range");
-  if (st_host_->err & ERR_KV_OVERFLOW) fail("KV cache overflow");
-  if (st_host_->err & ERR_SAMPLER) fail("sampler failure");
+void Engine::ensure_slots(uint32_t n) {
+  if (n <= kv_slots_) return;
+  HIPC(hipStreamSynchronize(stream_));
+  for (float** p : {&kc_, &vc_, &fkc_, &fvc_}) {
+    if (*p) {
+      HIPC(hipFree(*p));
+      allocs_.erase(std::find(allocs_.begin(), allocs_.end(), static_cast<void*>(*p)));
+      *p = nullptr;
+    }
+  }
+  kc_ = dalloc<float>(n * slot_kv_);
+  vc_ = dalloc<float>(n * slot_kv_);
+  fkc_ = dalloc<float>(n * fslot_kv_);
+  fvc_ = dalloc<float>(n * fslot_kv_);
+  HIPC(hipMemset(kc_, 0, n * slot_kv_ * 4));
+  HIPC(hipMemset(vc_, 0, n * slot_kv_ * 4));
+  HIPC(hipMemset(fkc_, 0, n * fslot_kv_ * 4));
+  HIPC(hipMemset(fvc_, 0, n * fslot_kv_ * 4));
+  kv_slots_ = n;
+  ++kv_gen_;
+}
+
+void Engine::check_state_err(uint32_t nseq) {
+  for (uint32_t b = 0; b < nseq; ++b) {
+    const std::string who = nseq > 1 ? " (request " + std::to_string(b) + ")" : std::string();
+    if (st_host_[b].err & ERR_TOKEN_RANGE) fail("token id out of range" + who);
+    if (st_host_[b].err & ERR_KV_OVERFLOW) fail("KV cache overflow" + who);
+    if (st_host_[b].err & ERR_SAMPLER) fail("sampler failure" + who);
+  }
 }
 
 void Engine::reset() {
@@ -876,8 +960,8 @@ void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* l
   // done = 0, err = 0 (eval never runs under a finished frame loop)
   HIPC(hipMemsetAsync(&st_->done, 0, sizeof(uint32_t), stream_));
   HIPC(hipMemsetAsync(&st_->err, 0, sizeof(uint32_t), stream_));
-  enqueue_prefill(prompt_dev_, n_tok);
-  enqueue_head(0, logits_out != nullptr, nullptr);
+  enqueue_prefill(prompt_dev_, n_tok, 0);
+  enqueue_head(1, hn_, logits_c_, logits_out != nullptr, nullptr);
   HIPC(hipMemcpyAsync(hidden_out, hn_, s.dim * 4, hipMemcpyDeviceToHost, stream_));
   if (logits_out) HIPC(hipMemcpyAsync(logits_out, logits_full_, size_t(s.vocab) * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
@@ -893,7 +977,7 @@ void Engine::fast_logits(const float* hidden, const uint32_t* prefix, size_t ple
   std::vector<uint16_t> row(s.dim);
   std::vector<float> rowf(s.dim);
   HIPC(hipMemcpyAsync(fh_, hidden, s.dim * 4, hipMemcpyHostToDevice, stream_));
-  enqueue_fast_layers(1, 0, nullptr);
+  enqueue_fast_layers(1, 1, 0, nullptr);
   for (size_t j = 0; j < plen; ++j) {
     if (prefix[j] >= s.codebook_size) fail("fast prefix code out of range");
     HIPC(hipMemcpyAsync(row.data(), fast_emb_ + size_t(prefix[j]) * s.dim, s.dim * 2, hipMemcpyDeviceToHost,
@@ -901,7 +985,7 @@ void Engine::fast_logits(const float* hidden, const uint32_t* prefix, size_t ple
     HIPC(hipStreamSynchronize(stream_));
     for (uint32_t i = 0; i < s.dim; ++i) rowf[i] = f16_to_f32(row[i]);
     HIPC(hipMemcpyAsync(fh_, rowf.data(), s.dim * 4, hipMemcpyHostToDevice, stream_));
-    enqueue_fast_layers(1, uint32_t(j + 1), nullptr);
+    enqueue_fast_layers(1, 1, uint32_t(j + 1), nullptr);
   }
   gemv(fast_out_, nullptr, EPI_STORE, 1, fh_, s.dim, fast_norm_, s.fast_eps, flogits_, s.codebook_size, 0, NO_ROW,
        s.codebook_size, nullptr);
@@ -923,7 +1007,7 @@ void Engine::fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampl
   *st_host_ = init;
   HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
   HIPC(hipMemcpyAsync(hn_, hidden, s.dim * 4, hipMemcpyHostToDevice, stream_));
-  enqueue_fast_frame(SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, nullptr);
+  enqueue_fast_frame(SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, 1, nullptr);
   HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
   check_state_err();
@@ -931,10 +1015,7 @@ void Engine::fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampl
   *rng = st_host_->rng;
 }
 
-// generate_codes (crates/fish_s2_infer/src/generate.rs:117-221)
-void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params& p, uint64_t* rng, int32_t* codes,
-                      uint32_t* n_frames, s2hip_gen_stats* stats) {
-  select();
+void Engine::validate_prompt(const int32_t* prompt, size_t cols) {
   const s2hip_spec& s = spec;
   const uint32_t cdim = s.num_codebooks + 1;
   if (cols == 0) fail("expected at least one token");
@@ -949,37 +1030,75 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
             uint64_t(prompt[t * cdim + 1 + cb]) + uint64_t(cb) * s.codebook_size >= cb_rows_)
           fail("prompt codebook token out of range");
   }
+}
+
+// generate_codes (crates/fish_s2_infer/src/generate.rs:117-221) for nseq
+// independent requests, one slot each, decoded together.  Every request's
+// codes are those of its own generate_codes call; one request is the nseq = 1
+// case of the same kernels.
+void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t* cols, const s2hip_gen_params& p,
+                      uint64_t* rngs, int32_t* const* codes, uint32_t* n_frames, s2hip_gen_stats* stats) {
+  select();
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  if (nseq == 0 || nseq > MAX_SEQS) fail("batch of " + std::to_string(nseq) + " requests (1.." +
+                                         std::to_string(MAX_SEQS) + " supported)");
+  size_t total_cols = 0;
+  for (uint32_t b = 0; b < nseq; ++b) {
+    validate_prompt(prompts[b], cols[b]);
+    total_cols += cols[b];
+  }
   const SamplerCfg cfg{p.temperature, p.top_p, p.top_k};
   const size_t ncodes = size_t(s.num_codebooks) * p.max_new_tokens;
-  ensure_codes(ncodes);
-  ensure_prompt(cols * cdim);
+  ensure_slots(nseq);
+  ensure_codes(ncodes * nseq);
+  ensure_prompt(total_cols * cdim);
   HIPC(hipStreamSynchronize(stream_));
-  // SlowArState::reset + sampler state
-  DevState init{};
-  init.rng = *rng;
-  init.prompt_cols = uint32_t(cols);
-  init.max_new = p.max_new_tokens;
-  init.min_tokens_before_end = p.min_tokens_before_end;
-  *st_host_ = init;
-  HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
-  if (ncodes) HIPC(hipMemsetAsync(codes_dev_, 0, ncodes * 4, stream_));
-  HIPC(hipMemcpyAsync(prompt_dev_, prompt, cols * cdim * 4, hipMemcpyHostToDevice, stream_));
+  // SlowArState::reset + sampler state, per slot
+  for (uint32_t b = 0; b < nseq; ++b) {
+    DevState init{};
+    init.rng = rngs[b];
+    init.prompt_cols = uint32_t(cols[b]);
+    init.max_new = p.max_new_tokens;
+    init.min_tokens_before_end = p.min_tokens_before_end;
+    st_host_[b] = init;
+  }
+  HIPC(hipMemcpyAsync(st_, st_host_, nseq * sizeof(DevState), hipMemcpyHostToDevice, stream_));
+  const BatchState bs{0u, 0u, nseq};
+  HIPC(hipMemcpyAsync(batch_, &bs, sizeof(bs), hipMemcpyHostToDevice, stream_));
+  if (ncodes) HIPC(hipMemsetAsync(codes_dev_, 0, ncodes * nseq * 4, stream_));
+  {
+    size_t off = 0;
+    for (uint32_t b = 0; b < nseq; ++b) {
+      HIPC(hipMemcpyAsync(prompt_dev_ + off, prompts[b], cols[b] * cdim * 4, hipMemcpyHostToDevice, stream_));
+      off += cols[b] * cdim;
+    }
+  }
   hipEvent_t ev[3];
   for (auto& e : ev) HIPC(hipEventCreate(&e));
   HIPC(hipEventRecord(ev[0], stream_));
-  enqueue_prefill(prompt_dev_, cols);
-  enqueue_head(0, false, nullptr);
-  SampleArgs sa{};
-  sa.logits = logits_c_;
-  sa.ids = head_rows_;
-  sa.n = n_cand_;
-  sa.vocab = s.vocab;
-  sa.cfg = cfg;
-  sa.st = st_;
-  sa.im_end = im_end_;
-  sa.after_step = 0;
-  sa.num_codebooks = s.num_codebooks;
-  HIPC(launch_sample_slow(sa, stream_));
+  // prompt prefill and the first semantic sample, request by request
+  {
+    size_t off = 0;
+    for (uint32_t b = 0; b < nseq; ++b) {
+      enqueue_prefill(prompt_dev_ + off, cols[b], b);
+      off += cols[b] * cdim;
+      enqueue_head(1, hn_ + size_t(b) * s.dim, logits_c_ + size_t(b) * n_cand_, false, nullptr);
+      SampleArgs sa{};
+      sa.logits = logits_c_ + size_t(b) * n_cand_;
+      sa.ids = head_rows_;
+      sa.n = n_cand_;
+      sa.vocab = s.vocab;
+      sa.cfg = cfg;
+      sa.st = st_ + b;
+      sa.im_end = im_end_;
+      sa.after_step = 0;
+      sa.num_codebooks = s.num_codebooks;
+      sa.n_seq = 1;
+      sa.batch = batch_;
+      HIPC(launch_sample_slow(sa, stream_));
+    }
+  }
   HIPC(hipEventRecord(ev[1], stream_));
 
   // No cap at the KV capacity: a frame that would write past max_seq_len sets
@@ -989,11 +1108,12 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
   bool use_graph = !(flags_ & S2HIP_FLAG_NO_GRAPH);
   uint32_t launched = 0;
   if (max_frames > 0) {
-    enqueue_frame(cfg);  // frame 0 eagerly (also configures every kernel)
+    enqueue_frame(cfg, nseq, ncodes);  // frame 0 eagerly (also configures every kernel)
     launched = 1;
   }
   if (use_graph && launched < max_frames) {
-    const bool stale = !graph_exec_ || graph_codes_ != codes_dev_ || graph_cfg_.temperature != cfg.temperature ||
+    const bool stale = !graph_exec_ || graph_codes_ != codes_dev_ || graph_codes_stride_ != ncodes ||
+                       graph_nseq_ != nseq || graph_kv_gen_ != kv_gen_ || graph_cfg_.temperature != cfg.temperature ||
                        graph_cfg_.top_p != cfg.top_p || graph_cfg_.top_k != cfg.top_k;
     if (stale) {
       if (graph_exec_) {
@@ -1006,7 +1126,7 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
       }
       HIPC(hipStreamBeginCapture(stream_, hipStreamCaptureModeRelaxed));
       try {
-        enqueue_frame(cfg);
+        enqueue_frame(cfg, nseq, ncodes);
       } catch (...) {
         hipGraph_t g = nullptr;
         (void)hipStreamEndCapture(stream_, &g);
@@ -1017,6 +1137,9 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
       HIPC(hipGraphInstantiate(&graph_exec_, graph_, nullptr, nullptr, 0));
       graph_cfg_ = cfg;
       graph_codes_ = codes_dev_;
+      graph_codes_stride_ = ncodes;
+      graph_nseq_ = nseq;
+      graph_kv_gen_ = kv_gen_;
     }
   }
   // Frames in batches; the done flag of batch i is read while batch i+1 runs.
@@ -1031,10 +1154,10 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
       if (use_graph)
         HIPC(hipGraphLaunch(graph_exec_, stream_));
       else
-        enqueue_frame(cfg);
+        enqueue_frame(cfg, nseq, ncodes);
     }
     launched += n;
-    HIPC(hipMemcpyAsync(&done_host_[slot], &st_->done, 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipMemcpyAsync(&done_host_[slot], &batch_->done_all, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipEventRecord(flag_ev[slot], stream_));
     if (pending >= 0) {
       HIPC(hipEventSynchronize(flag_ev[pending]));
@@ -1044,27 +1167,32 @@ void Engine::generate(const int32_t* prompt, size_t cols, const s2hip_gen_params
     slot ^= 1;
   }
   HIPC(hipEventRecord(ev[2], stream_));
-  HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(st_host_, st_, nseq * sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
   for (auto& e : flag_ev) (void)hipEventDestroy(e);
   float ms_prefill = 0.0f, ms_decode = 0.0f;
   HIPC(hipEventElapsedTime(&ms_prefill, ev[0], ev[1]));
   HIPC(hipEventElapsedTime(&ms_decode, ev[1], ev[2]));
   for (auto& e : ev) (void)hipEventDestroy(e);
-  check_state_err();
-  const uint32_t nf = st_host_->step_index;
-  std::vector<int32_t> full(ncodes);
-  if (ncodes) HIPC(hipMemcpy(full.data(), codes_dev_, ncodes * 4, hipMemcpyDeviceToHost));
-  // compact_codes (generate.rs:346-390): codebook-major [num_codebooks][n_frames]
-  for (uint32_t cb = 0; cb < s.num_codebooks; ++cb)
-    for (uint32_t t = 0; t < nf; ++t) codes[size_t(cb) * nf + t] = full[size_t(cb) * p.max_new_tokens + t];
-  *n_frames = nf;
-  *rng = st_host_->rng;
-  n_past_host = st_host_->n_past;
+  check_state_err(nseq);
+  std::vector<int32_t> full(ncodes * nseq);
+  if (ncodes) HIPC(hipMemcpy(full.data(), codes_dev_, ncodes * nseq * 4, hipMemcpyDeviceToHost));
+  uint32_t total = 0;
+  for (uint32_t b = 0; b < nseq; ++b) {
+    const uint32_t nf = st_host_[b].step_index;
+    const int32_t* src = full.data() + size_t(b) * ncodes;
+    // compact_codes (generate.rs:346-390): codebook-major [num_codebooks][n_frames]
+    for (uint32_t cb = 0; cb < s.num_codebooks; ++cb)
+      for (uint32_t t = 0; t < nf; ++t) codes[b][size_t(cb) * nf + t] = src[size_t(cb) * p.max_new_tokens + t];
+    n_frames[b] = nf;
+    rngs[b] = st_host_[b].rng;
+    total += nf;
+  }
+  n_past_host = st_host_[0].n_past;  // the engine's sequence state is request 0's
   if (stats) {
     stats->prefill_ms = ms_prefill;
     stats->decode_ms = ms_decode;
-    stats->n_frames = nf;
+    stats->n_frames = total;
     stats->graph_used = use_graph ? 1u : 0u;
   }
 }
@@ -1254,14 +1382,40 @@ void Engine::op_sample(const float* logits, size_t n, const s2hip_sampler& smp, 
   if (e) fail("sampler failure");
 }
 
-void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes) {
+void Engine::time_kernel(const std::string& full_name, uint32_t reps, double* avg_us, double* bytes) {
   select();
   const s2hip_spec& s = spec;
   if (reps == 0) reps = 1;
+  // "<name>_b<N>": the Slow-AR linears over N columns (a decode batch of N)
+  // by the engine's routing; "<name>_s<N>": the skinny MFMA product for N
+  // columns whatever N is
+  std::string name = full_name;
+  uint32_t ncol = 1;
+  bool force_skinny = false;
+  {
+    const size_t at = full_name.rfind('_');
+    if (full_name.rfind("slow_w", 0) == 0 && at != std::string::npos && at + 2 < full_name.size() &&
+        (full_name[at + 1] == 'b' || full_name[at + 1] == 's') &&
+        full_name.find_first_not_of("0123456789", at + 2) == std::string::npos) {
+      ncol = uint32_t(std::stoul(full_name.substr(at + 2)));
+      force_skinny = full_name[at + 1] == 's';
+      name = full_name.substr(0, at);
+      if (ncol == 0 || ncol > MAX_SEQS) fail("batch columns out of range in " + full_name);
+    }
+  }
+  auto tlin = [&](const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
+                  float eps, float* y, uint32_t ldy) {
+    if (force_skinny) {
+      if (L.in % 256) fail("skinny product needs in % 256 == 0");
+      mm_skinny(L, L3, epi, x, ldx, norm, eps, ncol, y, ldy, 0, NO_ROW, L.out, nullptr);
+    } else {
+      lin(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, 0, NO_ROW, L.out, nullptr);
+    }
+  };
   const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim;
-  HIPC(hipMemsetAsync(h_, 0, size_t(PREFILL_COLS) * s.dim * 4, stream_));
-  HIPC(hipMemsetAsync(att_, 0, size_t(PREFILL_COLS) * q * 4, stream_));
-  HIPC(hipMemsetAsync(act_, 0, size_t(PREFILL_COLS) * s.ffn * 4, stream_));
+  HIPC(hipMemsetAsync(h_, 0, size_t(MAX_SEQS) * s.dim * 4, stream_));
+  HIPC(hipMemsetAsync(att_, 0, size_t(MAX_SEQS) * q * 4, stream_));
+  HIPC(hipMemsetAsync(act_, 0, size_t(MAX_SEQS) * s.ffn * 4, stream_));
   // hbm_copy: a 256 MiB device-to-device copy (counter calibration)
   constexpr size_t COPY_BYTES = size_t(256) << 20;
   std::unique_ptr<TmpBuf> copy_a, copy_b;
@@ -1276,14 +1430,13 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   auto pass = [&](uint32_t l) {
     const SlowLayer& L = slow_[l];
     if (name == "slow_w13")
-      gemv(L.w1, &L.w3, EPI_SWIGLU_SLOW, 1, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, nullptr);
+      tlin(L.w1, &L.w3, EPI_SWIGLU_SLOW, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn);
     else if (name == "slow_wqkv")
-      gemv(L.wqkv, nullptr, EPI_STORE, 1, h_, s.dim, L.attn_norm, s.eps, qkv_, q + 2 * kv, 0, NO_ROW, L.wqkv.out,
-           nullptr);
+      tlin(L.wqkv, nullptr, EPI_STORE, h_, s.dim, L.attn_norm, s.eps, qkv_, q + 2 * kv);
     else if (name == "slow_wo")
-      gemv(L.wo, nullptr, EPI_STORE, 1, att_, q, nullptr, 0.0f, act_, s.dim, 0, NO_ROW, L.wo.out, nullptr);
+      tlin(L.wo, nullptr, EPI_STORE, att_, q, nullptr, 0.0f, h_, s.dim);
     else if (name == "slow_w2")
-      gemv(L.w2, nullptr, EPI_STORE, 1, act_, s.ffn, nullptr, 0.0f, qkv_, s.dim, 0, NO_ROW, L.w2.out, nullptr);
+      tlin(L.w2, nullptr, EPI_STORE, act_, s.ffn, nullptr, 0.0f, qkv_, s.dim);
     else if (name == "slow_attn" || name == "fast_attn") {
       const bool fast = name == "fast_attn";
       AttnArgs aa{};
@@ -1333,9 +1486,9 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
       gemv(fast_out_, nullptr, EPI_STORE, 1, fh_, s.dim, fast_norm_, s.fast_eps, flogits_, s.codebook_size, 0, NO_ROW,
            s.codebook_size, nullptr);
     } else if (name == "fast_frame") {
-      enqueue_fast_frame(SamplerCfg{0.0f, 1.0f, 0}, nullptr);
+      enqueue_fast_frame(SamplerCfg{0.0f, 1.0f, 0}, 1, nullptr);
     } else if (name == "empty") {
-      HIPC(launch_add_position(st_, 0, stream_));
+      HIPC(launch_add_position(st_, 0, 1, stream_));
     } else if (name == "hbm_copy") {
       HIPC(launch_copy(copy_src, copy_dst, COPY_BYTES, stream_));
     }
@@ -1348,10 +1501,10 @@ void Engine::time_kernel(const std::string& name, uint32_t reps, double* avg_us,
   };
   double b = 0;
   const SlowLayer& L0 = slow_[0];
-  if (name == "slow_w13") b = double(L0.w1.bytes + L0.w3.bytes) + 4.0 * (s.dim + s.ffn + s.dim);
-  else if (name == "slow_wqkv") b = double(L0.wqkv.bytes) + 4.0 * (s.dim + s.dim + q + 2 * kv);
-  else if (name == "slow_wo") b = double(L0.wo.bytes) + 4.0 * (q + s.dim);
-  else if (name == "slow_w2") b = double(L0.w2.bytes) + 4.0 * (s.ffn + s.dim);
+  if (name == "slow_w13") b = double(L0.w1.bytes + L0.w3.bytes) + 4.0 * ncol * (s.dim + s.ffn) + 4.0 * s.dim;
+  else if (name == "slow_wqkv") b = double(L0.wqkv.bytes) + 4.0 * ncol * (s.dim + q + 2 * kv) + 4.0 * s.dim;
+  else if (name == "slow_wo") b = double(L0.wo.bytes) + 4.0 * ncol * (q + s.dim);
+  else if (name == "slow_w2") b = double(L0.w2.bytes) + 4.0 * ncol * (s.ffn + s.dim);
   else if (name == "slow_head") b = double(n_cand_) * s.dim * 2 + 4.0 * (s.dim + n_cand_);
   else if (name == "hbm_copy") b = 2.0 * double(COPY_BYTES);
   const bool per_layer = name.rfind("slow_", 0) == 0 && name != "slow_head" && name != "sample_slow";
@@ -1493,7 +1646,24 @@ int32_t s2hip_generate_codes(s2hip_engine* engine, const int32_t* prompt, size_t
     set_err(err, err_cap, "NULL argument");
     return 0;
   }
-  return guarded(err, err_cap, [&] { engine->e->generate(prompt, cols, *p, rng, codes, n_frames, stats); });
+  return guarded(err, err_cap, [&] { engine->e->generate(1, &prompt, &cols, *p, rng, &codes, n_frames, stats); });
+}
+
+int32_t s2hip_generate_codes_batch(s2hip_engine* engine, uint32_t n_requests, const int32_t* const* prompts,
+                                   const size_t* prompt_cols, const s2hip_gen_params* p, uint64_t* rng_states,
+                                   int32_t* const* codes, uint32_t* n_frames, s2hip_gen_stats* stats, char* err,
+                                   size_t err_cap) {
+  if (!engine || !prompts || !prompt_cols || !p || !rng_states || !codes || !n_frames) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  for (uint32_t b = 0; b < n_requests; ++b)
+    if (!prompts[b] || !codes[b]) {
+      set_err(err, err_cap, "NULL argument");
+      return 0;
+    }
+  return guarded(err, err_cap,
+                 [&] { engine->e->generate(n_requests, prompts, prompt_cols, *p, rng_states, codes, n_frames, stats); });
 }
 
 int32_t s2hip_op_linear(s2hip_engine* engine, const void* w, uint32_t type, size_t in, size_t out, const float* x,

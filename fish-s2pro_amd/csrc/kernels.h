@@ -86,30 +86,37 @@ struct QkvPostArgs {
 };
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 
-// Fused decode attention for `ncol` consecutive query positions starting at
-// *pos_ptr + pos_offset: QK-norm (optional) + RoPE of q and of the new k,
-// KV append at the position, split-T GQA attention over positions
-// [0, pos] and the cross-chunk combine.  qkv: [ncol][(H + 2 Hkv) hd] raw
-// wqkv output.  hd must be 64 or 128 and H / Hkv <= 4.
+// Fused decode attention for ncol / cols_per_seq sequences, each with
+// cols_per_seq consecutive query positions starting at its *pos_ptr +
+// pos_offset: QK-norm (optional) + RoPE of q and of the new k, KV append at
+// the position, split-T GQA attention over positions [0, pos] and the
+// cross-chunk combine.  qkv: [ncol][(H + 2 Hkv) hd] raw wqkv output,
+// sequence-major.  hd must be 64 or 128, H / Hkv <= 4, cols_per_seq <= 4.
 struct AttnArgs {
   const float* qkv;
   const float* q_norm;     // nullable
   const float* k_norm;     // nullable
   float eps;
   const float2* rope;      // [max_pos][hd/2] (cos, sin)
-  float* k_cache;          // [Hkv][max_seq][hd] for this layer
+  float* k_cache;          // [Hkv][max_seq][hd] for this layer, sequence 0
   float* v_cache;
   float* part;             // [ncol][Hkv][max_chunks][rep][hd + 2]
   uint32_t* counters;      // [ncol][Hkv], zero between launches
   float* out;              // [ncol][H hd]
-  const uint32_t* pos_ptr; // nullable
+  const uint32_t* pos_ptr; // nullable (positions from pos_offset alone)
   uint32_t pos_offset;
   uint32_t H, Hkv, hd, max_seq, ncol;
   uint32_t max_chunks;     // attention_chunks(max_seq, mode)
   uint32_t mode;           // ATTN_SPLIT: partial + merge kernels; ATTN_FUSED: one kernel, last block merges
   float scale;
-  const uint32_t* done;
+  const uint32_t* done;    // nullable
   uint32_t* err;
+  // sequences: 0 = one sequence of ncol columns.  Sequence b uses the caches
+  // at + b * seq_stride_kv floats and the pos / done / err words at
+  // + b * seq_stride_words.
+  uint32_t cols_per_seq;
+  uint32_t seq_stride_words;
+  size_t seq_stride_kv;
 };
 enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
 uint32_t attention_chunks(uint32_t max_seq, uint32_t mode);
@@ -118,7 +125,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 // Slow-AR token embedding (time-major flat ids [n][cdim]).
 struct EmbedArgs {
   const int32_t* tokens;       // nullable: use the device step input built from state
-  const DevState* state;       // used when tokens == nullptr
+  const DevState* state;       // used when tokens == nullptr: row t from state[t]
   const uint16_t* emb;         // [vocab][dim] f16
   const uint16_t* cb_emb;      // [cb_rows][dim] f16
   float* h;                    // [n][dim]
@@ -130,11 +137,18 @@ struct EmbedArgs {
 };
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 
-// Fast-AR frame start: codes_frame[0] = semantic code of main_token,
-// fh[0] = slow hidden, fh[1] = fast_emb[code0].
+// Fast-AR frame start of n_seq sequences: st[b].codes_frame[0] = semantic code
+// of st[b].main_token, fh[b][0] = slow_hidden[b], fh[b][1] = fast_emb[code0].
 hipError_t launch_fast_begin(DevState* st, const float* slow_hidden, const uint16_t* fast_emb, float* fh,
                              uint32_t dim, uint32_t codebook_size, uint32_t sem_begin, uint32_t sem_end,
-                             hipStream_t s);
+                             uint32_t n_seq, hipStream_t s);
+
+// Batch completion word set when every sequence of a batch is done.
+struct BatchState {
+  uint32_t done_all;
+  uint32_t done_count;
+  uint32_t n_seq;
+};
 
 // Sampling.  Slow mode: logits over candidate rows `ids` (ascending vocab ids),
 // full vocab `vocab`; applies the semantic mask / im_end rule and updates the
@@ -158,6 +172,11 @@ struct SampleArgs {
   float* next_input;
   uint32_t dim;
   uint32_t* token_out;       // optional copy of the sampled id
+  // n_seq sequences (0 means 1): sequence b reads logits + b * n and uses
+  // st[b], codes_out + b * codes_stride, next_input + b * dim, token_out[b]
+  uint32_t n_seq;
+  size_t codes_stride;
+  BatchState* batch;         // nullable: counts finished sequences
 };
 hipError_t launch_sample_slow(const SampleArgs& a, hipStream_t s);
 hipError_t launch_sample_fast(const SampleArgs& a, hipStream_t s);
@@ -170,7 +189,8 @@ hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_byte
                                float* out, hipStream_t s);
 
 hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n, int fast, hipStream_t s);
-hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s);
+// n_past += n for each of the n_seq sequences not done
+hipError_t launch_add_position(DevState* st, uint32_t n, uint32_t n_seq, hipStream_t s);
 // Plain device copy (bytes and both pointers 16-byte aligned).
 hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
 

@@ -989,25 +989,30 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t rep = a.H / a.Hkv;
   const uint32_t width = (a.H + 2 * a.Hkv) * HD;
+  // column col = (sequence seq, its column lc); each sequence has its own
+  // KV cache, position word and done word
+  const uint32_t cps = a.cols_per_seq, seq = col / cps, lc = col % cps;
   const float* row = a.qkv + size_t(col) * width;
-  const float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
-  const float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
+  float* kseq = a.k_cache + size_t(seq) * a.seq_stride_kv;
+  float* vseq = a.v_cache + size_t(seq) * a.seq_stride_kv;
+  const float* kc = kseq + size_t(g) * a.max_seq * HD;
+  const float* vc = vseq + size_t(g) * a.max_seq * HD;
   const uint32_t t0 = chunk * CH;
 
   // 0. position-independent loads, all in flight together
-  const uint32_t done = opt_word(a.done);
-  const uint32_t pbase = opt_word(a.pos_ptr);
+  const uint32_t done = opt_word(a.done ? a.done + size_t(seq) * a.seq_stride_words : nullptr);
+  const uint32_t pbase = opt_word(a.pos_ptr ? a.pos_ptr + size_t(seq) * a.seq_stride_words : nullptr);
   const bool qlane = wave < rep && lane < HD / 2;
   float2 qv = make_float2(0.f, 0.f), qn = make_float2(1.f, 1.f);
   if (qlane) {
     qv = *reinterpret_cast<const float2*>(row + size_t(g * rep + wave) * HD + 2 * lane);
     if (a.q_norm) qn = *reinterpret_cast<const float2*>(a.q_norm + 2 * lane);
   }
-  // k / v rows of this launch's columns (wave w <-> column w <= col)
-  const bool kwave = wave < a.ncol && wave <= col;
+  // k / v rows of this sequence's columns (wave w <-> column w <= lc)
+  const bool kwave = wave < cps && wave <= lc;
   float2 kx = make_float2(0.f, 0.f), vx = kx, kn = make_float2(1.f, 1.f);
   if (kwave && lane < HD / 2) {
-    const float* r2 = a.qkv + size_t(wave) * width;
+    const float* r2 = a.qkv + size_t(seq * cps + wave) * width;
     kx = *reinterpret_cast<const float2*>(r2 + size_t(a.H + g) * HD + 2 * lane);
     vx = *reinterpret_cast<const float2*>(r2 + size_t(a.H + a.Hkv + g) * HD + 2 * lane);
     if (a.k_norm) kn = *reinterpret_cast<const float2*>(a.k_norm + 2 * lane);
@@ -1021,11 +1026,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     kr[j] = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
     vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
   }
-  const uint32_t pos = pbase + a.pos_offset + col;
+  const uint32_t pos = pbase + a.pos_offset + lc;
   const uint32_t T = pos + 1;
   const uint32_t nch = (T + CH - 1) / CH;
   if (done || pos >= a.max_seq || chunk >= nch) {
-    if (!done && pos >= a.max_seq && tid == 0 && chunk == 0 && a.err) atomicOr(a.err, ERR_KV_OVERFLOW);
+    if (!done && pos >= a.max_seq && tid == 0 && chunk == 0 && a.err)
+      atomicOr(a.err + size_t(seq) * a.seq_stride_words, ERR_KV_OVERFLOW);
     // The exit path also reads the loaded values, so the compiler keeps the
     // loads ahead of this branch (where they overlap the state read) instead
     // of sinking them behind it.  The test is never true for finite data.
@@ -1037,7 +1043,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     return;
   }
   const uint32_t t1 = min(T, t0 + CH), nt = t1 - t0;
-  const uint32_t base = pos - col;             // first position of this launch
+  const uint32_t base = pos - lc;              // first position of this sequence's columns
   const uint32_t lo = max(t0, min(base, t1));  // [lo, t1): positions of this launch
 
   // 1. rotation rows (the only position-dependent loads), then q and the
@@ -1092,9 +1098,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     for (uint32_t i = tid; i < HD; i += 256) {
       kt[tn * KS + i] = knew[c2][i];
       vt[tn * HD + i] = vnew[c2][i];
-      if (c2 == col) {  // SlowArKvCache::write_token for this column's position
-        a.k_cache[(size_t(g) * a.max_seq + pos) * HD + i] = knew[c2][i];
-        a.v_cache[(size_t(g) * a.max_seq + pos) * HD + i] = vnew[c2][i];
+      if (c2 == lc) {  // SlowArKvCache::write_token for this column's position
+        kseq[(size_t(g) * a.max_seq + pos) * HD + i] = knew[c2][i];
+        vseq[(size_t(g) * a.max_seq + pos) * HD + i] = vnew[c2][i];
       }
     }
   }
@@ -1199,8 +1205,9 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
   const uint32_t rep = a.H / a.Hkv, g = h / rep, w = h % rep;
   const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks * rep + w) * (HD + 2);
   const size_t stride = size_t(rep) * (HD + 2);
-  const uint32_t done = opt_word(a.done);
-  const uint32_t pb = opt_word(a.pos_ptr);
+  const uint32_t seq = col / a.cols_per_seq, lc = col % a.cols_per_seq;
+  const uint32_t done = opt_word(a.done ? a.done + size_t(seq) * a.seq_stride_words : nullptr);
+  const uint32_t pb = opt_word(a.pos_ptr ? a.pos_ptr + size_t(seq) * a.seq_stride_words : nullptr);
   if constexpr (MAXC > 0) {
     static_assert(MAXC <= HD, "one thread per chunk slot");
     __shared__ float2 ml[MAXC];
@@ -1214,7 +1221,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
     for (int c = 0; c < MAXC; ++c) oc[c] = pbase[size_t(min(uint32_t(c), a.max_chunks - 1)) * stride + 2 + d];
     if (d < uint32_t(MAXC)) ml[d] = mlv;
     __syncthreads();
-    const uint32_t pos = pb + a.pos_offset + col;
+    const uint32_t pos = pb + a.pos_offset + lc;
     const bool live = !done && pos < a.max_seq;
     const uint32_t nch = live ? (pos + CH) / CH : 0u;
     float M = -INFINITY;
@@ -1232,7 +1239,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
     }
     if (nch > 1) a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
   } else {
-    const uint32_t pos = pb + a.pos_offset + col;
+    const uint32_t pos = pb + a.pos_offset + lc;
     if (done || pos >= a.max_seq) return;
     const uint32_t nch = (pos + CH) / CH;
     if (nch <= 1) return;
@@ -1261,10 +1268,11 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     for (uint32_t i = 0; i < cdim && i < 17; ++i) tok[i] = a.tokens[size_t(t) * cdim + i];
   } else {
     // build_step_input: [main, cb0..cb(n-1)] when main is semantic, else [main, 0..]
-    const uint32_t main = a.state->main_token;
+    const DevState* st = a.state + t;  // one sequence per token row
+    const uint32_t main = st->main_token;
     const bool sem = main >= a.sem_begin && main <= a.sem_end;
     tok[0] = int32_t(main);
-    for (uint32_t i = 0; i < a.num_codebooks && i < 16; ++i) tok[1 + i] = sem ? int32_t(a.state->codes_frame[i]) : 0;
+    for (uint32_t i = 0; i < a.num_codebooks && i < 16; ++i) tok[1 + i] = sem ? int32_t(st->codes_frame[i]) : 0;
   }
   uint32_t id = uint32_t(tok[0]);
   if (tok[0] < 0 || id >= a.vocab) {
@@ -1305,16 +1313,23 @@ __device__ __forceinline__ uint32_t sem_to_code(uint32_t tok, uint32_t sem_begin
   return c >= codebook_size ? codebook_size - 1 : c;
 }
 
-__global__ __launch_bounds__(256) void fast_begin_kernel(DevState* st, const float* slow_hidden,
+// grid (blocks over dim, sequences): sequence b reads slow_hidden[b] and
+// writes its two Fast-AR input rows fh[b][0..1].  A finished sequence keeps
+// its codes but its rows are still rewritten, so the Fast-AR passes that
+// run for the rest of a batch see bounded inputs.
+__global__ __launch_bounds__(256) void fast_begin_kernel(DevState* st0, const float* slow_hidden,
                                                          const uint16_t* fast_emb, float* fh, uint32_t dim,
                                                          uint32_t codebook_size, uint32_t sem_begin,
                                                          uint32_t sem_end) {
-  if (st->done) return;
+  const uint32_t b = blockIdx.y;
+  DevState* st = st0 + b;
   const uint32_t code = sem_to_code(st->main_token, sem_begin, sem_end, codebook_size);
-  if (blockIdx.x == 0 && threadIdx.x == 0) st->codes_frame[0] = code;
+  if (!st->done && blockIdx.x == 0 && threadIdx.x == 0) st->codes_frame[0] = code;
+  const float* hid = slow_hidden + size_t(b) * dim;
+  float* f = fh + size_t(b) * 2 * dim;
   for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < dim; i += gridDim.x * 256) {
-    fh[i] = slow_hidden[i];
-    fh[dim + i] = half_bits_to_float(fast_emb[size_t(code) * dim + i]);
+    f[i] = hid[i];
+    f[dim + i] = half_bits_to_float(fast_emb[size_t(code) * dim + i]);
   }
 }
 
@@ -1840,10 +1855,15 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
   return sample_general<8>(sh, logits, ids, n, vocab, cfg, masked, force, rng, n_fin);
 }
 
+// Block b samples sequence b (its logits row, state and code output).
 __global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs a) {
   extern __shared__ uint8_t smem_raw[];
   SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
-  DevState* st = a.st;
+  const uint32_t b = blockIdx.x;
+  DevState* st = a.st + b;
+  a.logits += size_t(b) * a.n;
+  if (a.codes_out) a.codes_out += size_t(b) * a.codes_stride;
+  if (a.token_out) a.token_out += b;
   if (st->done) return;
   __shared__ uint32_t gen;
   if (threadIdx.x == 0) {
@@ -1869,14 +1889,22 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs 
     st->rng = sh.rng;
     st->main_token = tok;
     if (a.token_out) *a.token_out = tok;
-    if (tok == a.im_end || st->step_index >= st->max_new) st->done = 1;
+    if (tok == a.im_end || st->step_index >= st->max_new) {
+      st->done = 1;
+      // the batch is done once every sequence is
+      if (a.batch && atomicAdd(&a.batch->done_count, 1u) + 1 == a.batch->n_seq) a.batch->done_all = 1;
+    }
   }
 }
 
 __global__ __launch_bounds__(SAMPLE_THREADS) void sample_fast_kernel(SampleArgs a) {
   extern __shared__ uint8_t smem_raw[];
   SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
-  DevState* st = a.st;
+  const uint32_t b = blockIdx.x;
+  DevState* st = a.st + b;
+  a.logits += size_t(b) * a.n;
+  if (a.next_input) a.next_input += size_t(b) * a.dim;
+  if (a.token_out) a.token_out += b;
   if (st->done) return;
   if (threadIdx.x == 0) sh.rng = st->rng;
   const uint32_t tok = sample_core(sh, a.logits, nullptr, a.n, a.vocab, a.cfg, -1, -1, &sh.rng, &st->err);
@@ -1934,9 +1962,9 @@ __global__ void swiglu_kernel(const float* g, const float* u, float* out, uint32
     out[i] = __fmul_rn(__fmul_rn(gv, __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gv)))), u[i]);
 }
 
-__global__ void add_position_kernel(DevState* st, uint32_t n) {
-  if (st->done) return;
-  if (threadIdx.x == 0) st->n_past += n;
+__global__ void add_position_kernel(DevState* st, uint32_t n, uint32_t n_seq) {
+  for (uint32_t b = threadIdx.x; b < n_seq; b += blockDim.x)
+    if (!st[b].done) st[b].n_past += n;
 }
 
 // Streaming copy of n4 16-byte words: the reference kernel against which HBM
@@ -2012,8 +2040,12 @@ void launch_combine(const AttnArgs& a, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 0>), grid, dim3(HD), 0, s, a);
 }
 
-hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  if (a.H % a.Hkv || a.H / a.Hkv > 4 || a.ncol > 4) return hipErrorInvalidValue;
+hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
+  AttnArgs a = args;
+  if (a.cols_per_seq == 0) a.cols_per_seq = a.ncol;  // one sequence
+  if (a.ncol == 0 || a.ncol % a.cols_per_seq || a.cols_per_seq > 4 || a.ncol > 64) return hipErrorInvalidValue;
+  if (a.ncol > a.cols_per_seq && a.seq_stride_words == 0 && (a.pos_ptr || a.done)) return hipErrorInvalidValue;
+  if (a.H % a.Hkv || a.H / a.Hkv > 4) return hipErrorInvalidValue;
   if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
   const dim3 grid(a.max_chunks, a.Hkv, a.ncol);
   if (a.mode == ATTN_FUSED) {
@@ -2048,9 +2080,9 @@ hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
 
 hipError_t launch_fast_begin(DevState* st, const float* slow_hidden, const uint16_t* fast_emb, float* fh,
                              uint32_t dim, uint32_t codebook_size, uint32_t sem_begin, uint32_t sem_end,
-                             hipStream_t s) {
-  hipLaunchKernelGGL(fast_begin_kernel, dim3((dim + 255) / 256), dim3(256), 0, s, st, slow_hidden, fast_emb, fh,
-                     dim, codebook_size, sem_begin, sem_end);
+                             uint32_t n_seq, hipStream_t s) {
+  hipLaunchKernelGGL(fast_begin_kernel, dim3((dim + 255) / 256, n_seq), dim3(256), 0, s, st, slow_hidden, fast_emb,
+                     fh, dim, codebook_size, sem_begin, sem_end);
   return hipGetLastError();
 }
 
@@ -2062,7 +2094,7 @@ hipError_t launch_sample_slow(const SampleArgs& a, hipStream_t s) {
     configured = true;
   }
   if (a.n > SAMPLE_MAX - 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sample_slow_kernel, dim3(1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
+  hipLaunchKernelGGL(sample_slow_kernel, dim3(a.n_seq ? a.n_seq : 1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
   return hipGetLastError();
 }
 
@@ -2074,7 +2106,7 @@ hipError_t launch_sample_fast(const SampleArgs& a, hipStream_t s) {
     configured = true;
   }
   if (a.n > SAMPLE_MAX - 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sample_fast_kernel, dim3(1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
+  hipLaunchKernelGGL(sample_fast_kernel, dim3(a.n_seq ? a.n_seq : 1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
   return hipGetLastError();
 }
 
@@ -2118,8 +2150,8 @@ hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n,
   return hipGetLastError();
 }
 
-hipError_t launch_add_position(DevState* st, uint32_t n, hipStream_t s) {
-  hipLaunchKernelGGL(add_position_kernel, dim3(1), dim3(64), 0, s, st, n);
+hipError_t launch_add_position(DevState* st, uint32_t n, uint32_t n_seq, hipStream_t s) {
+  hipLaunchKernelGGL(add_position_kernel, dim3(1), dim3(64), 0, s, st, n, n_seq);
   return hipGetLastError();
 }
 

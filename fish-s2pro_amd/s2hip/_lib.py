@@ -100,6 +100,9 @@ def load():
     L.s2hip_fast_codebooks.argtypes = [vp, vp, u32, ctypes.POINTER(Sampler), u64p, vp, cp, sz]
     L.s2hip_generate_codes.argtypes = [vp, vp, sz, ctypes.POINTER(GenParams), u64p, vp,
                                        ctypes.POINTER(u32), ctypes.POINTER(GenStats), cp, sz]
+    L.s2hip_generate_codes_batch.argtypes = [vp, u32, ctypes.POINTER(vp), ctypes.POINTER(sz),
+                                             ctypes.POINTER(GenParams), u64p, ctypes.POINTER(vp),
+                                             ctypes.POINTER(u32), ctypes.POINTER(GenStats), cp, sz]
     L.s2hip_op_linear.argtypes = [vp, vp, u32, sz, sz, vp, sz, vp, cp, sz]
     L.s2hip_op_rms_norm.argtypes = [vp, vp, vp, sz, sz, f32, vp, cp, sz]
     L.s2hip_op_dequant_rows.argtypes = [vp, vp, u32, sz, sz, vp, cp, sz]
@@ -111,7 +114,8 @@ def load():
     L.s2hip_time_kernel.argtypes = [vp, cp, u32, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double), cp, sz]
     for name in ("s2hip_get_spec", "s2hip_reset", "s2hip_eval", "s2hip_fast_logits",
-                 "s2hip_fast_codebooks", "s2hip_generate_codes", "s2hip_op_linear",
+                 "s2hip_fast_codebooks", "s2hip_generate_codes", "s2hip_generate_codes_batch",
+                 "s2hip_op_linear",
                  "s2hip_op_rms_norm", "s2hip_op_dequant_rows", "s2hip_op_qk_rope",
                  "s2hip_op_attention", "s2hip_op_swiglu", "s2hip_op_sample", "s2hip_time_kernel"):
         getattr(L, name).restype = i32

@@ -140,6 +140,51 @@ class Engine:
             "graph_used": bool(stats.graph_used),
         }
 
+    def generate_codes_batch(self, prompts, max_new_tokens, temperature=0.0, top_p=1.0, top_k=0,
+                             min_tokens_before_end=0, rng_states=None):
+        """Several independent generate_codes requests decoded together (one KV
+        slot each).  Returns one result dict per request, as generate_codes
+        does, plus the batch's prefill / decode times and total frames."""
+        flats = []
+        for pr in prompts:
+            flat = np.ascontiguousarray(pr, dtype=np.int32).ravel()
+            if flat.size % self.codebook_dim:
+                raise S2HipError("prompt length is not a multiple of codebook_dim")
+            flats.append(flat)
+        nb = len(flats)
+        if nb == 0:
+            raise S2HipError("expected at least one request")
+        ncb = self.spec["num_codebooks"]
+        if rng_states is None:
+            rng_states = [0] * nb
+        if len(rng_states) != nb:
+            raise S2HipError("one rng state per request expected")
+        codes = [np.zeros(max(1, ncb * max_new_tokens), np.int32) for _ in range(nb)]
+        prompt_ptrs = (ctypes.c_void_p * nb)(*[f.ctypes.data for f in flats])
+        cols = (ctypes.c_size_t * nb)(*[f.size // self.codebook_dim for f in flats])
+        code_ptrs = (ctypes.c_void_p * nb)(*[c.ctypes.data for c in codes])
+        states = (ctypes.c_uint64 * nb)(*[int(r) for r in rng_states])
+        nf = (ctypes.c_uint32 * nb)()
+        params = _lib.GenParams(max_new_tokens, temperature, top_p, top_k, min_tokens_before_end)
+        stats = _lib.GenStats()
+        self._call(self._L.s2hip_generate_codes_batch, nb, prompt_ptrs, cols, ctypes.byref(params), states,
+                   code_ptrs, nf, ctypes.byref(stats))
+        out = []
+        for b in range(nb):
+            n = nf[b]
+            out.append({
+                "codes": codes[b][: ncb * n].reshape(ncb, n).copy(),
+                "n_frames": n,
+                "rng_state": states[b],
+            })
+        return {
+            "requests": out,
+            "prefill_ms": stats.prefill_ms,
+            "decode_ms": stats.decode_ms,
+            "total_frames": stats.n_frames,
+            "graph_used": bool(stats.graph_used),
+        }
+
     # -- op level -------------------------------------------------------------
     def linear(self, weight_rows: np.ndarray, ggml_type: int, in_dim: int, out_dim: int, x):
         w = np.ascontiguousarray(weight_rows)

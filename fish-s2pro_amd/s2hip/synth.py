@@ -172,6 +172,26 @@ def quantize_block(ggml_type: int, values) -> bytes:
     return out.tobytes()
 
 
+def voice_clone_prompt(shape: ModelShape, n_text: int, n_frames: int, seed: int):
+    """Time-major flat voice-clone prompt in the layout of build_prompt's
+    reference-audio branch (prompt.rs:105-192): n_text // 2 text ids, then
+    n_frames reference frames (row 0 = semantic_begin + code0, rows 1..ncb =
+    the frame's codes, uniform in [0, codebook_size)), then the remaining text
+    ids.  Text ids are uniform in [0, semantic_begin)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    ncb = shape.num_codebooks
+    pre, post = n_text // 2, n_text - n_text // 2
+    flat = np.zeros((pre + n_frames + post, ncb + 1), np.int32)
+    flat[:pre, 0] = rng.integers(0, shape.semantic_begin, pre)
+    codes = rng.integers(0, shape.codebook_size, (n_frames, ncb))
+    flat[pre:pre + n_frames, 0] = shape.semantic_begin + codes[:, 0]
+    flat[pre:pre + n_frames, 1:] = codes
+    flat[pre + n_frames:, 0] = rng.integers(0, shape.semantic_begin, post)
+    return flat.ravel()
+
+
 def synthetic_prompt(shape: ModelShape, n_tokens: int, seed: int):
     """Time-major flat prompt ([n_tokens][num_codebooks + 1], prompt.rs:77-103)
     of uniform random text ids in [0, semantic_begin) with codebook rows 0."""

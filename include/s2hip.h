@@ -127,6 +127,25 @@ int32_t s2hip_generate_codes(s2hip_engine* engine, const int32_t* prompt_flat, s
                              const s2hip_gen_params* params, uint64_t* rng_state, int32_t* codes_out,
                              uint32_t* n_frames_out, s2hip_gen_stats* stats, char* err, size_t err_cap);
 
+/* Batched generate_codes: n_requests (1..16) independent requests decoded
+ * together, each in its own KV slot, so every frame reads each weight matrix
+ * once for the whole batch.  Request b is prompts[b] ([prompt_cols[b]]
+ * [num_codebooks + 1], time-major), its SeededRng state rng_states[b]
+ * (updated in place), and its output codes[b] / n_frames_out[b] exactly as
+ * for s2hip_generate_codes; params are shared.  A finished request stops
+ * contributing codes while the others continue.  The reference serves one
+ * request at a time (single SlowArState, slow_ar.rs:387-438); this entry
+ * point has no counterpart there and is for callers serving concurrent
+ * requests, which the reference's server runs one at a time behind a Mutex
+ * (server.rs:57).  stats->n_frames is
+ * the total over requests.  Slot KV memory (max_seq_len positions per
+ * request) is allocated on the first call with a larger batch; afterwards the
+ * engine's sequence state (s2hip_n_past, s2hip_eval) is request 0's. */
+int32_t s2hip_generate_codes_batch(s2hip_engine* engine, uint32_t n_requests, const int32_t* const* prompts,
+                                   const size_t* prompt_cols, const s2hip_gen_params* params,
+                                   uint64_t* rng_states, int32_t* const* codes_out, uint32_t* n_frames_out,
+                                   s2hip_gen_stats* stats, char* err, size_t err_cap);
+
 /* ---- op level: the MatmulBackend seam (crates/fish_s2_infer/src/backend.rs:5-39)
  * and the other per-op functions, run on the engine's device with host
  * inputs/outputs.  Used by parity dumps and tests. */
