@@ -68,6 +68,9 @@ struct DevLin {
   uint32_t in = 0, out = 0;
   size_t row_bytes = 0;
   uint64_t bytes = 0;
+  // F16 weights in MFMA fragment order for the batched product (built on
+  // first use); its rows are the logical rows (any row mapping baked in)
+  _Float16* wt = nullptr;
 };
 
 struct SlowLayer {
@@ -147,6 +150,10 @@ class Engine {
   void enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
   void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
   void ensure_slots(uint32_t n);
+  void ensure_tiled();
+  void tile(DevLin& L, uint32_t rows, uint32_t row_base, uint32_t extra_row);
+  void bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx, const float* norm,
+           float eps, float* y, uint32_t ldy, const uint32_t* done, uint32_t* err, uint32_t waves = 0);
   void validate_prompt(const int32_t* prompt, size_t cols);
   void mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
           uint32_t n, uint32_t npad, float* y, uint32_t ldy);
@@ -171,6 +178,9 @@ class Engine {
   uint64_t cb_rows_ = 0;
   float *norm_ = nullptr, *fast_norm_ = nullptr;
   DevLin head_full_, fast_out_;
+  DevLin head_cand_;  // the candidate rows of the head (tiled copy only)
+  bool tiled_ = false;
+  uint32_t bmm_min_cols_ = 2;  // columns from which F16 linears use the batched product
   std::vector<SlowLayer> slow_;
   std::vector<FastLayer> fast_;
   uint32_t* head_rows_ = nullptr;  // vocabulary id of each candidate logit
@@ -337,6 +347,8 @@ Engine::Engine(const s2hip_config& cfg) {
   }
   n_cand_ = uint32_t(rows.size());
   if (n_cand_ > 8191) fail("too many sampling candidates");
+  head_cand_ = head_full_;
+  head_cand_.out = n_cand_;
   head_rows_ = dalloc<uint32_t>(rows.size());
   HIPC(hipMemcpy(head_rows_, rows.data(), rows.size() * 4, hipMemcpyHostToDevice));
 
@@ -353,6 +365,9 @@ Engine::Engine(const s2hip_config& cfg) {
   attn_mode_ = getenv("S2HIP_ATTN_FUSED") ? ATTN_FUSED : ATTN_SPLIT;
   prefill_gemv_ = getenv("S2HIP_PREFILL_GEMV") != nullptr;
   attn_chunks_ = attention_chunks(s.max_seq_len, attn_mode_);
+  // S2HIP_BMM_MIN_COLS=n: F16 linears over >= n columns use the batched MFMA
+  // product (0 disables it)
+  if (const char* v = getenv("S2HIP_BMM_MIN_COLS")) bmm_min_cols_ = uint32_t(strtoul(v, nullptr, 10));
   h_ = dalloc<float>(size_t(NC) * s.dim);
   qkv_ = dalloc<float>(size_t(NC) * qkv_w);
   q_ = dalloc<float>(size_t(NC) * q);
@@ -526,9 +541,36 @@ void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, con
   }
 }
 
+void Engine::bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
+                 const float* norm, float eps, float* y, uint32_t ldy, const uint32_t* done, uint32_t* err,
+                 uint32_t waves) {
+  for (uint32_t c = 0; c < ncol; c += 16) {
+    BmmArgs b{};
+    b.wt = L.wt;
+    b.wt3 = L3 ? L3->wt : nullptr;
+    b.M = L.out;
+    b.K = L.in;
+    b.x = x + size_t(c) * ldx;
+    b.ldx = ldx;
+    b.N = std::min(16u, ncol - c);
+    b.norm = norm;
+    b.eps = eps;
+    b.y = y + size_t(c) * ldy;
+    b.ldy = ldy;
+    b.done = done;
+    b.err = err;
+    b.waves = waves;
+    HIPC(launch_bmm(epi, b, stream_));
+  }
+}
+
 void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
                  const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
                  uint32_t out_rows, const uint32_t* done) {
+  if (L.wt && bmm_min_cols_ && ncol >= bmm_min_cols_ && (!L3 || L3->wt)) {
+    bmm(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, done, &st_->err);
+    return;
+  }
   if (ncol <= 2 || L.in % 256) {
     gemv(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, row_base, extra_row, out_rows, done);
     return;
@@ -593,7 +635,7 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
 void Engine::enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done) {
   const s2hip_spec& s = spec;
   HIPC(launch_rms_norm(h_, norm_, hn, s.dim, ncol, s.eps, done, stream_));
-  lin(head_full_, nullptr, EPI_STORE, ncol, hn, s.dim, nullptr, 0.0f, logits, n_cand_, s.semantic_begin, head_extra_,
+  lin(head_cand_, nullptr, EPI_STORE, ncol, hn, s.dim, nullptr, 0.0f, logits, n_cand_, s.semantic_begin, head_extra_,
       n_cand_, done);
   if (full)
     gemv(head_full_, nullptr, EPI_STORE, 1, hn, s.dim, nullptr, 0.0f, logits_full_, s.vocab, 0, NO_ROW, s.vocab, done);
@@ -920,12 +962,34 @@ void Engine::ensure_slots(uint32_t n) {
   ++kv_gen_;
 }
 
+void Engine::tile(DevLin& L, uint32_t rows, uint32_t row_base, uint32_t extra_row) {
+  if (L.type != W_F16 || L.in % 256 || L.wt) return;
+  L.wt = dalloc<_Float16>(size_t(bmm_rows_pad(rows)) * L.in);
+  HIPC(launch_tile_f16(reinterpret_cast<const uint16_t*>(L.w), L.in, rows, row_base, extra_row,
+                       reinterpret_cast<uint16_t*>(L.wt), stream_));
+}
+
+// The batched product's copies of the F16 linears (one more HBM copy of the
+// weights), built once, the first time a decode needs them.
+void Engine::ensure_tiled() {
+  if (tiled_ || !bmm_min_cols_) return;
+  for (auto& L : slow_)
+    for (DevLin* d : {&L.wqkv, &L.wo, &L.w1, &L.w2, &L.w3}) tile(*d, d->out, 0, NO_ROW);
+  for (auto& L : fast_)
+    for (DevLin* d : {&L.wqkv, &L.wo, &L.w1, &L.w2, &L.w3}) tile(*d, d->out, 0, NO_ROW);
+  tile(fast_out_, fast_out_.out, 0, NO_ROW);
+  tile(head_cand_, n_cand_, spec.semantic_begin, head_extra_);
+  HIPC(hipStreamSynchronize(stream_));
+  tiled_ = true;
+}
+
 void Engine::check_state_err(uint32_t nseq) {
   for (uint32_t b = 0; b < nseq; ++b) {
     const std::string who = nseq > 1 ? " (request " + std::to_string(b) + ")" : std::string();
     if (st_host_[b].err & ERR_TOKEN_RANGE) fail("token id out of range" + who);
     if (st_host_[b].err & ERR_KV_OVERFLOW) fail("KV cache overflow" + who);
     if (st_host_[b].err & ERR_SAMPLER) fail("sampler failure" + who);
+    if (st_host_[b].err & ERR_F16_RANGE) fail("activation outside the f16 range of the batched product");
   }
 }
 
@@ -1051,6 +1115,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   const SamplerCfg cfg{p.temperature, p.top_p, p.top_k};
   const size_t ncodes = size_t(s.num_codebooks) * p.max_new_tokens;
   ensure_slots(nseq);
+  ensure_tiled();
   ensure_codes(ncodes * nseq);
   ensure_prompt(total_cols * cdim);
   HIPC(hipStreamSynchronize(stream_));
@@ -1225,7 +1290,23 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
   L.in = uint32_t(in);
   L.out = uint32_t(out);
   L.row_bytes = rb;
-  if (ncol >= 3 && ncol <= 16 && in % 256 == 0)  // batched-decode product
+  const bool batched = bmm_min_cols_ && ncol >= bmm_min_cols_ && in % 256 == 0;
+  if (batched && type == W_F16) {  // batched-decode product on a tiled copy
+    TmpBuf dt(size_t(bmm_rows_pad(uint32_t(out))) * in * 2), derr(4);
+    L.wt = dt.as<_Float16>();
+    HIPC(launch_tile_f16(reinterpret_cast<const uint16_t*>(L.w), uint32_t(in), uint32_t(out), 0, NO_ROW,
+                         reinterpret_cast<uint16_t*>(L.wt), stream_));
+    HIPC(hipMemsetAsync(derr.p, 0, 4, stream_));
+    bmm(L, nullptr, EPI_STORE, uint32_t(ncol), dx.as<float>(), uint32_t(in), nullptr, 0.0f, dy.as<float>(),
+        uint32_t(out), nullptr, derr.as<uint32_t>());
+    uint32_t herr = 0;
+    HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipMemcpyAsync(&herr, derr.p, 4, hipMemcpyDeviceToHost, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+    if (herr & ERR_F16_RANGE) fail("activation outside the f16 range of the batched product");
+    return;
+  }
+  if (ncol >= 3 && ncol <= 16 && in % 256 == 0)  // batched-decode product (quantized rows)
     mm_skinny(L, nullptr, EPI_STORE, dx.as<float>(), uint32_t(in), nullptr, 0.0f, uint32_t(ncol), dy.as<float>(),
               uint32_t(out), 0, NO_ROW, uint32_t(out), nullptr);
   else
@@ -1388,26 +1469,44 @@ void Engine::time_kernel(const std::string& full_name, uint32_t reps, double* av
   if (reps == 0) reps = 1;
   // "<name>_b<N>": the Slow-AR linears over N columns (a decode batch of N)
   // by the engine's routing; "<name>_s<N>": the skinny MFMA product for N
-  // columns whatever N is
+  // columns whatever N is; "<name>_g<N>": the GEMV kernels for N columns;
+  // "<name>_t<N>[w<W>]": the batched product (W waves per block)
   std::string name = full_name;
-  uint32_t ncol = 1;
-  bool force_skinny = false;
+  uint32_t ncol = 1, waves = 0;
+  char force = 'b';
   {
     const size_t at = full_name.rfind('_');
     if (full_name.rfind("slow_w", 0) == 0 && at != std::string::npos && at + 2 < full_name.size() &&
-        (full_name[at + 1] == 'b' || full_name[at + 1] == 's') &&
-        full_name.find_first_not_of("0123456789", at + 2) == std::string::npos) {
-      ncol = uint32_t(std::stoul(full_name.substr(at + 2)));
-      force_skinny = full_name[at + 1] == 's';
-      name = full_name.substr(0, at);
-      if (ncol == 0 || ncol > MAX_SEQS) fail("batch columns out of range in " + full_name);
+        std::string("bsgt").find(full_name[at + 1]) != std::string::npos) {
+      const std::string arg = full_name.substr(at + 2);
+      const size_t wpos = arg.find('w');
+      const std::string cols = arg.substr(0, wpos), wv = wpos == std::string::npos ? "" : arg.substr(wpos + 1);
+      const bool ok = !cols.empty() && cols.find_first_not_of("0123456789") == std::string::npos &&
+                      wv.find_first_not_of("0123456789") == std::string::npos &&
+                      (wpos == std::string::npos || (!wv.empty() && full_name[at + 1] == 't'));
+      if (ok) {
+        ncol = uint32_t(std::stoul(cols));
+        waves = wv.empty() ? 0u : uint32_t(std::stoul(wv));
+        force = full_name[at + 1];
+        name = full_name.substr(0, at);
+        if (ncol == 0 || ncol > MAX_SEQS) fail("batch columns out of range in " + full_name);
+      }
     }
+  }
+  if (force == 't') {
+    ensure_tiled();
+    if (!tiled_) fail("the batched product is disabled");
   }
   auto tlin = [&](const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
                   float eps, float* y, uint32_t ldy) {
-    if (force_skinny) {
+    if (force == 's') {
       if (L.in % 256) fail("skinny product needs in % 256 == 0");
       mm_skinny(L, L3, epi, x, ldx, norm, eps, ncol, y, ldy, 0, NO_ROW, L.out, nullptr);
+    } else if (force == 'g') {
+      gemv(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, 0, NO_ROW, L.out, nullptr);
+    } else if (force == 't') {
+      if (!L.wt) fail("no batched-product copy of this matrix (F16 with in % 256 == 0 only)");
+      bmm(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, nullptr, &st_->err, waves);
     } else {
       lin(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, 0, NO_ROW, L.out, nullptr);
     }

@@ -33,7 +33,7 @@ struct DevState {
   uint32_t codes_frame[16];  // codebook ids of the frame being built
 };
 
-enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u };
+enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u, ERR_F16_RANGE = 8u };
 constexpr uint32_t NO_ROW = 0xffffffffu;
 
 struct GemvArgs {
@@ -236,6 +236,35 @@ struct SkinnyArgs {
   const uint32_t* done;
 };
 hipError_t launch_skinny_mfma(uint32_t wtype, int epi, const SkinnyArgs& a, hipStream_t s);
+
+// ---- batched decode products (batched.hip) ----
+// Weights in MFMA fragment order: tile (tm, tk) of 16 rows x 32 k is 512
+// contiguous halfs, lane l's 8 at l * 8 = W[16 tm + l % 16][32 tk + 8 (l / 16)
+// + e]; rows padded to bmm_rows_pad(M) with zeros.  launch_tile_f16 builds it
+// from F16 rows [*][K] (logical row r -> row_base + r, the last logical row
+// -> extra_row unless NO_ROW).
+uint32_t bmm_rows_pad(uint32_t m);
+hipError_t launch_tile_f16(const uint16_t* src, uint32_t K, uint32_t M, uint32_t row_base, uint32_t extra_row,
+                           uint16_t* dst, hipStream_t s);
+// y[n][m] (op)= sum_k W[m][k] xn[n][k] for n < N <= 16, m < M; xn = x, or
+// RMSNorm(x) with gain `norm`; epilogues as for launch_gemv.  K % 256 == 0.
+// Activations beyond the f16 range (or NaN) set ERR_F16_RANGE in *err.
+struct BmmArgs {
+  const _Float16* wt;
+  const _Float16* wt3;   // second matrix for SwiGLU epilogues
+  uint32_t M, K;
+  const float* x;        // [N][ldx]
+  uint32_t ldx, N;
+  const float* norm;     // nullable
+  float eps;
+  float* y;              // [N][ldy]
+  uint32_t ldy;
+  const uint32_t* done;  // nullable: skip the stores once set
+  uint32_t* err;         // nullable
+  uint32_t waves;        // 0: bmm_waves(M, K)
+};
+uint32_t bmm_waves(uint32_t M, uint32_t K);
+hipError_t launch_bmm(int epi, const BmmArgs& a, hipStream_t s);
 
 // Causal GQA attention of N prompt queries at positions *pos_ptr + pos_offset
 // + c over the KV cache (their own K/V already appended).

@@ -62,6 +62,36 @@ def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
         assert _rel(got[c], want) < min(tol, 1e-4), c
 
 
+def test_batched_linear_f16_range(eng):
+    """Batched F16 columns go through the MFMA product with activations split
+    into f16 hi + lo: large values inside the f16 range stay accurate, and a
+    value beyond it makes the call fail instead of returning a wrong result."""
+    from s2hip import S2HipError
+
+    rng = np.random.default_rng(31)
+    in_dim, out_dim, ncol = 2560, 256, 4
+    wf = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
+    raw = _rows(1, wf)
+    x = rng.standard_normal((ncol, in_dim)).astype(np.float32)
+    x[1, 7] = 6.0e4
+    x[2, 100] = -6.5e4
+    x[3, :] *= 1e-4  # small values: absolute split error ~2^-25
+    got = eng.linear(raw, 1, in_dim, out_dim, x)
+    for c in range(ncol):
+        want = O.linear(x[c], raw, 1, in_dim, out_dim)
+        assert _rel(got[c], want) < 1e-4, c
+    x[0, 5] = 7.0e4
+    with pytest.raises(S2HipError, match="f16 range"):
+        eng.linear(raw, 1, in_dim, out_dim, x)
+    x[0, 5] = np.nan
+    with pytest.raises(S2HipError, match="f16 range"):
+        eng.linear(raw, 1, in_dim, out_dim, x)
+    # the engine still works
+    x[0, 5] = 1.0
+    got = eng.linear(raw, 1, in_dim, out_dim, x)
+    assert _rel(got[0], O.linear(x[0], raw, 1, in_dim, out_dim)) < 1e-4
+
+
 def test_rms_norm_matches_oracle(eng):
     rng = np.random.default_rng(20)
     x = rng.standard_normal((3, 2560)).astype(np.float32) * 3
