@@ -9,19 +9,24 @@
 // 8 (l / 16) + e], e < 8 -- every wave load is one contiguous KiB and a wave
 // walking k streams consecutive KiB.
 //
-// Activations stay f32 rows; each lane splits its own 8 elements per step
-// into f16 hi = f16(x) and lo = f16((x - hi) 2^11), kept normal down to
-// |x| ~ 2^-14 by the 2^11 (x = hi + 2^-11 lo to ~2^-22 |x|, absolute ~2^-35
-// below); hi and lo go through the MFMA with the same weight fragment into
-// two accumulators, combined as acc_hi + 2^-11 acc_lo.  A value outside the f16 range turns its column's results
-// non-finite; the epilogue then sets ERR_F16_RANGE, so the call fails
-// instead of returning a wrong product.  RMSNorm inputs: the sum of squares of
-// each column is accumulated from the same loaded values and the RMS scale
-// is applied to the result (W.((x s) g) = s W.(x g)).
+// Activations stay f32 rows [N][ldx].  Each wave stages its k range of
+// them through a private LDS double buffer with coalesced loads (512
+// contiguous bytes per row and chunk of 4 steps, issued one chunk ahead), so
+// the activation loads neither scatter over rows (the MFMA fragment puts the
+// column in the fastest lane bits) nor hold up the weight loads' wait
+// counter.  Each lane then splits its 8 elements per step into f16 hi =
+// f16(x) and lo = f16((x - hi) 2^11) (x = hi + 2^-11 lo to ~2^-22 |x| for
+// |x| >= 2^-14, absolute ~2^-35 below); hi and lo go through the MFMA with
+// the same weight fragment into two accumulators.  RMSNorm inputs: the sum
+// of squares of each column is accumulated from the same values and the RMS
+// scale is applied to the result (W.((x s) g) = s W.(x g)).  A value beyond
+// the f16 range makes its column's sums non-finite; the epilogue reports
+// that as ERR_F16_RANGE instead of returning a wrong product.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -60,9 +65,11 @@ __global__ __launch_bounds__(256) void tile_f16_kernel(const uint16_t* src, uint
 // activation steps in flight (the schedule is pinned so the loads stay
 // ahead of their MFMAs).  Lane l: column n = l % 16, k group l / 16.
 // ---------------------------------------------------------------------------
-constexpr int WIN = 8, XW = 4;
+constexpr int WIN = 8;        // weight steps in flight (two chunks)
+constexpr int XC = 4;         // steps per staged activation chunk
+constexpr int RS = 36;        // LDS floats per staged row and step (32 + 4: conflict-free fragment reads)
 
-__device__ __forceinline__ void split8(const float4& a, const float4& b, half8& hi, half8& lo) {
+__device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8& hi, half8& lo) {
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -72,10 +79,23 @@ __device__ __forceinline__ void split8(const float4& a, const float4& b, half8& 
   }
 }
 
-template <int EPI, bool NORM, int WAVES>
+// ---------------------------------------------------------------------------
+// Product.  Block = WAVES waves on one 16-row tile; wave w takes the k steps
+// [w KS, (w + 1) KS) (KS = K / 32 / WAVES).  The loop body has no branches
+// (a branch around a load makes the compiler wait for every outstanding
+// load at the join): steps run in pairs of chunks (WIN steps), loads past
+// the end re-read in-bounds data, and a step past the end, or a column >= N,
+// gets a zero activation by a select.  Lane l: column n = l % 16, k group
+// l / 16.  NB = activation rows staged (8 when N <= 8, else 16).
+// ---------------------------------------------------------------------------
+template <int EPI, bool NORM, int WAVES, int NB>
 __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr int NW = DUAL ? 2 : 1;
+  constexpr int CHF = XC * NB * RS;  // floats per chunk buffer
+  constexpr int LDX = NB / 2;        // staging loads per chunk (2 rows x 512 B each)
+  __shared__ float xs[WAVES][2][CHF];
+  __shared__ float gs[WAVES][2][NORM ? XC * 32 : 1];
   __shared__ floatx4 red[WAVES][2 * NW][64];
   __shared__ float ssq[WAVES][64];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
@@ -85,39 +105,53 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   const size_t tile0 = (size_t(tm) * kt + size_t(wave) * KS) * 512 + size_t(lane) * 8;
   const _Float16* wp0 = a.wt + tile0;
   const _Float16* wp1 = DUAL ? a.wt3 + tile0 : wp0;
-  const bool xon = n < a.N;
-  const uint32_t kbeg = wave * KS * 32 + 8 * grp;
-  const float* xp = a.x + size_t(xon ? n : 0u) * a.ldx + kbeg;
-  const float* gp = NORM ? a.norm + kbeg : nullptr;
-  // The loop body has no branches (a branch around a load makes the compiler
-  // wait for every outstanding load at the join): steps run to a multiple of
-  // WIN, loads past the last step re-read it (in bounds), and the activation
-  // of a step past the end, or of a column >= N, is zeroed by a select.
   const uint32_t last = KS - 1;
-  const uint32_t KSR = (KS + WIN - 1) / WIN * WIN;
+  const uint32_t nsc = (KS + WIN - 1) / WIN;  // pairs of chunks
+  const uint32_t kbase = wave * KS * 32;
+  // staging: load j of a chunk covers rows 2 j + lane / 32, 4-float group lane % 32
+  const uint32_t srow = lane >> 5, sq = lane & 31u;
+  float* xsw = &xs[wave][0][0];
+  float* gsw = &gs[wave][0][0];
 
-  // loads complete in issue order for the wait counter: activations (short
-  // L2 latency) go out before the weights of the same step, so waiting for
-  // a step's activations does not wait for the deeper weight prefetch
-  half8 wb[WIN][NW];
-  float4 xv[XW][2], gv[XW][2];
+  auto stage_load = [&](floatx4 (&r)[LDX], floatx4& gr, uint32_t chunk) __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < XW; ++i) {
-    const uint32_t t = min(uint32_t(i), last);
-    xv[i][0] = *reinterpret_cast<const float4*>(xp + 32 * t);
-    xv[i][1] = *reinterpret_cast<const float4*>(xp + 32 * t + 4);
-    if constexpr (NORM) {
-      gv[i][0] = *reinterpret_cast<const float4*>(gp + 32 * t);
-      gv[i][1] = *reinterpret_cast<const float4*>(gp + 32 * t + 4);
+    for (int j = 0; j < LDX; ++j) {
+      const uint32_t row = 2 * j + srow;
+      const uint32_t rr = row < a.N ? row : 0u;
+      const uint32_t k = min(kbase + chunk * (XC * 32) + 4 * sq, a.K - 4);
+      r[j] = *reinterpret_cast<const floatx4*>(a.x + size_t(rr) * a.ldx + k);
     }
-  }
+    if constexpr (NORM) {
+      const uint32_t k = min(kbase + chunk * (XC * 32) + 4 * (sq & 31u), a.K - 4);
+      gr = *reinterpret_cast<const floatx4*>(a.norm + k);
+    }
+  };
+  auto stage_store = [&](const floatx4 (&r)[LDX], const floatx4& gr, int buf) __attribute__((always_inline)) {
+    // element (row, k = 4 sq + e) of the chunk -> step k / 32, offset k % 32
+    const uint32_t st = sq / 8, off = 4 * (sq % 8);
+#pragma unroll
+    for (int j = 0; j < LDX; ++j) {
+      const uint32_t row = 2 * j + srow;
+      *reinterpret_cast<floatx4*>(xsw + buf * CHF + (st * NB + row) * RS + off) = r[j];
+    }
+    // both lane halves hold the same gain values: no branch around the store
+    if constexpr (NORM) *reinterpret_cast<floatx4*>(gsw + buf * (XC * 32) + 4 * sq) = gr;
+  };
+
+  half8 wb[WIN][NW];
+  floatx4 sxa[LDX], sxb[LDX], sga, sgb;  // staged chunks in flight (even, odd)
+  // chunk 0 and 1 activations, then the first WIN weight steps
+  stage_load(sxa, sga, 0);
+  stage_load(sxb, sgb, 1);
 #pragma unroll
   for (int i = 0; i < WIN; ++i) {
     const uint32_t t = min(uint32_t(i), last);
     wb[i][0] = *reinterpret_cast<const half8*>(wp0 + 512 * t);
     if constexpr (DUAL) wb[i][1] = *reinterpret_cast<const half8*>(wp1 + 512 * t);
   }
+  stage_store(sxa, sga, 0);
   __builtin_amdgcn_sched_barrier(0);
+
   floatx4 acc[NW], accl[NW];
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
@@ -125,40 +159,72 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     accl[m] = floatx4{};
   }
   float ss = 0.0f;
-  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t base = 0; base < KSR; base += WIN) {
+  const floatx4 z4 = floatx4{};
+  const uint32_t rrow = n < NB ? n : n - NB;  // a valid staged row for every lane
+  // the steps of chunk c from LDS buffer h (weight slots h XC .. h XC + 3)
+  // the steps of chunk c from LDS buffer h (weight slots h XC .. h XC + 3);
+  // each step's fragments are read from LDS one step ahead of their use
+  auto chunk_steps = [&](uint32_t c, auto hc) __attribute__((always_inline)) {
+    constexpr int h = decltype(hc)::value;
+    const float* xb = xsw + h * CHF + rrow * RS + 8 * grp;
+    const float* gb = gsw + h * (XC * 32) + 8 * grp;
+    floatx4 cx0 = *reinterpret_cast<const floatx4*>(xb), cx1 = *reinterpret_cast<const floatx4*>(xb + 4);
+    floatx4 cg0 = z4, cg1 = z4;
+    if constexpr (NORM) {
+      cg0 = *reinterpret_cast<const floatx4*>(gb);
+      cg1 = *reinterpret_cast<const floatx4*>(gb + 4);
+    }
 #pragma unroll
-    for (int i = 0; i < WIN; ++i) {
-      const uint32_t s = base + i;
-      const int xi = i % XW;  // base is a multiple of WIN, WIN of XW
-      const bool live = xon && s < KS;
-      float4 x0 = live ? xv[xi][0] : z4, x1 = live ? xv[xi][1] : z4;
+    for (int i = 0; i < XC; ++i) {
+      const uint32_t s = c * XC + i;
+      const int wi = h * XC + i;
+      floatx4 nx0 = z4, nx1 = z4, ng0 = z4, ng1 = z4;
+      if (i + 1 < XC) {
+        nx0 = *reinterpret_cast<const floatx4*>(xb + (i + 1) * NB * RS);
+        nx1 = *reinterpret_cast<const floatx4*>(xb + (i + 1) * NB * RS + 4);
+        if constexpr (NORM) {
+          ng0 = *reinterpret_cast<const floatx4*>(gb + (i + 1) * 32);
+          ng1 = *reinterpret_cast<const floatx4*>(gb + (i + 1) * 32 + 4);
+        }
+      }
+      const bool live = n < a.N && s < KS;
+      floatx4 x0 = live ? cx0 : z4, x1 = live ? cx1 : z4;
       if constexpr (NORM) {
         ss += (x0.x * x0.x + x0.y * x0.y) + (x0.z * x0.z + x0.w * x0.w);
         ss += (x1.x * x1.x + x1.y * x1.y) + (x1.z * x1.z + x1.w * x1.w);
-        const float4 g0 = gv[xi][0], g1 = gv[xi][1];
-        x0 = make_float4(x0.x * g0.x, x0.y * g0.y, x0.z * g0.z, x0.w * g0.w);
-        x1 = make_float4(x1.x * g1.x, x1.y * g1.y, x1.z * g1.z, x1.w * g1.w);
+        x0 = x0 * cg0;
+        x1 = x1 * cg1;
       }
       half8 bh, bl;
       split8(x0, x1, bh, bl);
 #pragma unroll
       for (int m = 0; m < NW; ++m) {
-        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[i][m], bh, acc[m], 0, 0, 0);
-        accl[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[i][m], bl, accl[m], 0, 0, 0);
+        acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bh, acc[m], 0, 0, 0);
+        accl[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bl, accl[m], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      const uint32_t tw = min(s + WIN, last), tx = min(s + XW, last);
-      xv[xi][0] = *reinterpret_cast<const float4*>(xp + 32 * tx);
-      xv[xi][1] = *reinterpret_cast<const float4*>(xp + 32 * tx + 4);
-      if constexpr (NORM) {
-        gv[xi][0] = *reinterpret_cast<const float4*>(gp + 32 * tx);
-        gv[xi][1] = *reinterpret_cast<const float4*>(gp + 32 * tx + 4);
-      }
-      wb[i][0] = *reinterpret_cast<const half8*>(wp0 + 512 * tw);
-      if constexpr (DUAL) wb[i][1] = *reinterpret_cast<const half8*>(wp1 + 512 * tw);
+      const uint32_t tw = min(s + WIN, last);
+      wb[wi][0] = *reinterpret_cast<const half8*>(wp0 + 512 * tw);
+      if constexpr (DUAL) wb[wi][1] = *reinterpret_cast<const half8*>(wp1 + 512 * tw);
       __builtin_amdgcn_sched_barrier(0);
+      cx0 = nx0;
+      cx1 = nx1;
+      cg0 = ng0;
+      cg1 = ng1;
     }
+  };
+  for (uint32_t sc = 0; sc < nsc; ++sc) {
+    // chunk 2 sc from buffer 0: first the odd chunk (loaded one chunk ago)
+    // into buffer 1, then the loads of chunk 2 sc + 2
+    stage_store(sxb, sgb, 1);
+    stage_load(sxa, sga, 2 * sc + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_steps(2 * sc, std::integral_constant<int, 0>{});
+    // chunk 2 sc + 1 from buffer 1
+    stage_store(sxa, sga, 0);
+    stage_load(sxb, sgb, 2 * sc + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_steps(2 * sc + 1, std::integral_constant<int, 1>{});
   }
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
@@ -220,17 +286,23 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   }
 }
 
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, int NB>
 hipError_t launch_bmm_waves(const BmmArgs& a, uint32_t waves, hipStream_t s) {
   const dim3 grid((a.M + 15) / 16);
   switch (waves) {
-    case 1: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 1>), grid, dim3(64), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 2>), grid, dim3(128), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 4>), grid, dim3(256), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 8>), grid, dim3(512), 0, s, a); break;
+    case 1: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 1, NB>), grid, dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 2, NB>), grid, dim3(128), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((bmm_kernel<EPI, NORM, 4, NB>), grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int EPI>
+hipError_t launch_bmm_epi(const BmmArgs& a, uint32_t waves, hipStream_t s) {
+  const bool norm = a.norm != nullptr;
+  if (a.N <= 8) return norm ? launch_bmm_waves<EPI, true, 8>(a, waves, s) : launch_bmm_waves<EPI, false, 8>(a, waves, s);
+  return norm ? launch_bmm_waves<EPI, true, 16>(a, waves, s) : launch_bmm_waves<EPI, false, 16>(a, waves, s);
 }
 
 }  // namespace
@@ -248,31 +320,25 @@ hipError_t launch_tile_f16(const uint16_t* src, uint32_t K, uint32_t M, uint32_t
 }
 
 uint32_t bmm_waves(uint32_t M, uint32_t K) {
-  // enough blocks x waves to cover the CUs several times over: one wave per
-  // 16-row tile for tall matrices, the k range split over more waves (and
-  // summed in LDS) when there are few tiles
+  // one wave per 16-row tile for tall matrices; the k range split over more
+  // waves (summed in LDS) when there are few tiles
   const uint32_t tiles = (M + 15) / 16, steps = K / 32;
-  uint32_t w = 1;
-  while (w < 8 && tiles * w < 2048 && steps % (2 * w) == 0 && steps / (2 * w) >= 8) w *= 2;
+  uint32_t w = tiles >= 512 ? 1u : 4u;
+  while (steps % w) w /= 2;
   return w;
 }
 
 hipError_t launch_bmm(int epi, const BmmArgs& a, hipStream_t s) {
-  if (a.N == 0 || a.N > 16 || a.M == 0 || a.K % 256 || !a.wt) return hipErrorInvalidValue;
+  if (a.N == 0 || a.N > 16 || a.M == 0 || a.K % 256 || !a.wt || !a.x) return hipErrorInvalidValue;
   const bool dual = epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST;
   if (dual && !a.wt3) return hipErrorInvalidValue;
   const uint32_t waves = a.waves ? a.waves : bmm_waves(a.M, a.K);
   if ((a.K / 32) % waves) return hipErrorInvalidValue;
-  const bool norm = a.norm != nullptr;
   switch (epi) {
-    case EPI_STORE: return norm ? launch_bmm_waves<EPI_STORE, true>(a, waves, s)
-                                : launch_bmm_waves<EPI_STORE, false>(a, waves, s);
-    case EPI_RESID: return norm ? launch_bmm_waves<EPI_RESID, true>(a, waves, s)
-                                : launch_bmm_waves<EPI_RESID, false>(a, waves, s);
-    case EPI_SWIGLU_SLOW: return norm ? launch_bmm_waves<EPI_SWIGLU_SLOW, true>(a, waves, s)
-                                      : launch_bmm_waves<EPI_SWIGLU_SLOW, false>(a, waves, s);
-    case EPI_SWIGLU_FAST: return norm ? launch_bmm_waves<EPI_SWIGLU_FAST, true>(a, waves, s)
-                                      : launch_bmm_waves<EPI_SWIGLU_FAST, false>(a, waves, s);
+    case EPI_STORE: return launch_bmm_epi<EPI_STORE>(a, waves, s);
+    case EPI_RESID: return launch_bmm_epi<EPI_RESID>(a, waves, s);
+    case EPI_SWIGLU_SLOW: return launch_bmm_epi<EPI_SWIGLU_SLOW>(a, waves, s);
+    case EPI_SWIGLU_FAST: return launch_bmm_epi<EPI_SWIGLU_FAST>(a, waves, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -43,6 +43,7 @@ void hip_check(hipError_t e, const char* what) {
 
 constexpr uint32_t PREFILL_COLS = 4;     // decode-path columns per pass of the GEMV prefill
 constexpr uint32_t MAX_SEQS = 16;        // requests per batched generate call
+constexpr uint32_t BMM_MAX_K = 10240;    // input width limit of the batched product
 constexpr uint32_t ACT_COLS = 2 * MAX_SEQS;  // activation columns (Fast-AR pass 0 has two per request)
 constexpr uint32_t PREFILL_CHUNK = 512;  // prompt tokens per MFMA prefill pass
 constexpr uint32_t FRAME_BATCH = 4;
@@ -963,7 +964,7 @@ void Engine::ensure_slots(uint32_t n) {
 }
 
 void Engine::tile(DevLin& L, uint32_t rows, uint32_t row_base, uint32_t extra_row) {
-  if (L.type != W_F16 || L.in % 256 || L.wt) return;
+  if (L.type != W_F16 || L.in % 256 || L.in > BMM_MAX_K || L.wt) return;
   L.wt = dalloc<_Float16>(size_t(bmm_rows_pad(rows)) * L.in);
   HIPC(launch_tile_f16(reinterpret_cast<const uint16_t*>(L.w), L.in, rows, row_base, extra_row,
                        reinterpret_cast<uint16_t*>(L.wt), stream_));
@@ -1290,7 +1291,7 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
   L.in = uint32_t(in);
   L.out = uint32_t(out);
   L.row_bytes = rb;
-  const bool batched = bmm_min_cols_ && ncol >= bmm_min_cols_ && in % 256 == 0;
+  const bool batched = bmm_min_cols_ && ncol >= bmm_min_cols_ && in % 256 == 0 && in <= BMM_MAX_K;
   if (batched && type == W_F16) {  // batched-decode product on a tiled copy
     TmpBuf dt(size_t(bmm_rows_pad(uint32_t(out))) * in * 2), derr(4);
     L.wt = dt.as<_Float16>();

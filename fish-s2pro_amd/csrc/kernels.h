@@ -261,7 +261,7 @@ struct BmmArgs {
   uint32_t ldy;
   const uint32_t* done;  // nullable: skip the stores once set
   uint32_t* err;         // nullable
-  uint32_t waves;        // 0: bmm_waves(M, K)
+  uint32_t waves;        // 0: bmm_waves(M, K); else 1, 2 or 4
 };
 uint32_t bmm_waves(uint32_t M, uint32_t K);
 hipError_t launch_bmm(int epi, const BmmArgs& a, hipStream_t s);

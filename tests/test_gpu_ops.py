@@ -64,8 +64,9 @@ def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
 
 def test_batched_linear_f16_range(eng):
     """Batched F16 columns go through the MFMA product with activations split
-    into f16 hi + lo: large values inside the f16 range stay accurate, and a
-    value beyond it makes the call fail instead of returning a wrong result."""
+    into f16 hi + 2^11-scaled lo: large values inside the f16 range and tiny
+    ones stay accurate, and a value beyond the range (or NaN) makes the call
+    fail instead of returning a wrong result."""
     from s2hip import S2HipError
 
     rng = np.random.default_rng(31)
@@ -75,7 +76,7 @@ def test_batched_linear_f16_range(eng):
     x = rng.standard_normal((ncol, in_dim)).astype(np.float32)
     x[1, 7] = 6.0e4
     x[2, 100] = -6.5e4
-    x[3, :] *= 1e-4  # small values: absolute split error ~2^-25
+    x[3, :] *= 1e-4
     got = eng.linear(raw, 1, in_dim, out_dim, x)
     for c in range(ncol):
         want = O.linear(x[c], raw, 1, in_dim, out_dim)
