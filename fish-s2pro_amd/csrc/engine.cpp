@@ -229,6 +229,8 @@ class Engine {
 Engine::Engine(const s2hip_config& cfg) {
   if (!cfg.gguf_path) fail("gguf_path is NULL");
   if (cfg.max_seq_len == 0) fail("max_seq_len must be non-zero");
+  if (cfg.max_seq_len > 32u * ATTN_MAX_CHUNKS)
+    fail("max_seq_len above " + std::to_string(32u * ATTN_MAX_CHUNKS) + " is not supported");
   device = cfg.device;
   flags_ = cfg.flags;
   im_end_ = cfg.im_end_id;

@@ -119,6 +119,7 @@ struct AttnArgs {
   size_t seq_stride_kv;
 };
 enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
+constexpr uint32_t ATTN_MAX_CHUNKS = 1024;  // max_seq <= 32768
 uint32_t attention_chunks(uint32_t max_seq, uint32_t mode);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 

@@ -1239,18 +1239,43 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
     }
     if (nch > 1) a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
   } else {
+    // many chunks: the chunk maxima and weights in parallel over the
+    // threads, then the weighted sum of the partials with 16 loads in flight
+    constexpr int NWV = HD / 64;
+    __shared__ float fs[ATTN_MAX_CHUNKS];
+    __shared__ float rm[NWV], rl[NWV];
     const uint32_t pos = pb + a.pos_offset + lc;
     if (done || pos >= a.max_seq) return;
     const uint32_t nch = (pos + CH) / CH;
     if (nch <= 1) return;
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, pbase[c * stride]);
-    float L = 0.0f, acc = 0.0f;
-    for (uint32_t c = 0; c < nch; ++c) {
-      const float* pc = pbase + c * stride;
-      const float f = expf(pc[0] - M);
-      L = fmaf(pc[1], f, L);
-      acc = fmaf(pc[2 + d], f, acc);
+    const uint32_t lane = d & 63u, wv = d >> 6;
+    float mloc = -INFINITY;
+    for (uint32_t c = d; c < nch; c += HD) mloc = fmaxf(mloc, pbase[c * stride]);
+    mloc = wave_max(mloc);
+    if (lane == 0) rm[wv] = mloc;
+    __syncthreads();
+    float M = rm[0];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) M = fmaxf(M, rm[w]);
+    float lloc = 0.0f;
+    for (uint32_t c = d; c < nch; c += HD) {
+      const float f = expf(pbase[c * stride] - M);
+      fs[c] = f;
+      lloc = fmaf(pbase[c * stride + 1], f, lloc);
+    }
+    lloc = wave_sum(lloc);
+    if (lane == 0) rl[wv] = lloc;
+    __syncthreads();
+    float L = rl[0];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) L += rl[w];
+    float acc = 0.0f;
+    for (uint32_t c0 = 0; c0 < nch; c0 += 16) {
+      float ov[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) ov[j] = pbase[size_t(min(c0 + j, nch - 1)) * stride + 2 + d];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = fmaf(c0 + j < nch ? fs[c0 + j] : 0.0f, ov[j], acc);
     }
     a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
   }
@@ -2042,6 +2067,7 @@ void launch_combine(const AttnArgs& a, dim3 grid, hipStream_t s) {
 
 hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   AttnArgs a = args;
+  if (a.max_chunks > ATTN_MAX_CHUNKS) return hipErrorInvalidValue;
   if (a.cols_per_seq == 0) a.cols_per_seq = a.ncol;  // one sequence
   if (a.ncol == 0 || a.ncol % a.cols_per_seq || a.cols_per_seq > 4 || a.ncol > 64) return hipErrorInvalidValue;
   if (a.ncol > a.cols_per_seq && a.seq_stride_words == 0 && (a.pos_ptr || a.done)) return hipErrorInvalidValue;

@@ -40,7 +40,7 @@ typedef struct s2hip_engine s2hip_engine;
 
 typedef struct {
   const char* gguf_path;  /* transformer GGUF: F16, Q8_0 or Q4_0 linear weights */
-  uint32_t max_seq_len;   /* Slow-AR KV capacity (positions) */
+  uint32_t max_seq_len;   /* Slow-AR KV capacity (positions), 1..32768 (SLOW_CONTEXT_LENGTH, registry.rs:10) */
   uint32_t im_end_id;     /* tokenizer <|im_end|> id (tokenizer.rs:36-62) */
   int32_t device;         /* HIP device ordinal */
   uint32_t flags;         /* S2HIP_FLAG_* */

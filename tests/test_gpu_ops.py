@@ -120,7 +120,7 @@ def test_qk_norm_rope_matches_oracle(eng, hd, H, Hkv, qk, pos):
 
 
 @pytest.mark.parametrize("H,Hkv,hd,T", [(32, 8, 128, 1), (32, 8, 128, 200), (32, 8, 128, 768), (8, 2, 64, 37),
-                                        (32, 8, 128, 10)])
+                                        (32, 8, 128, 10), (32, 8, 128, 2000), (32, 8, 128, 2560), (8, 2, 64, 4100)])
 def test_attention_matches_oracle(eng, H, Hkv, hd, T):
     rng = np.random.default_rng(T + hd)
     q = rng.standard_normal(H * hd).astype(np.float32)
