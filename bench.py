@@ -129,6 +129,7 @@ def main():
         frames = args.steps
     if args.prompt:
         prompt_len = args.prompt
+        ref_frames = min(ref_frames, prompt_len * 2 // 3)  # keep some text ids around the reference frames
     max_seq = max(max_seq, prompt_len + frames)
     shape = synth.SHAPES[shape_name]
     t0 = time.time()

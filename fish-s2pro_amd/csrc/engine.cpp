@@ -1515,9 +1515,21 @@ void Engine::time_kernel(const std::string& full_name, uint32_t reps, double* av
     }
   };
   const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim;
-  HIPC(hipMemsetAsync(h_, 0, size_t(MAX_SEQS) * s.dim * 4, stream_));
-  HIPC(hipMemsetAsync(att_, 0, size_t(MAX_SEQS) * q * 4, stream_));
-  HIPC(hipMemsetAsync(act_, 0, size_t(MAX_SEQS) * s.ffn * 4, stream_));
+  // activations: pseudo-random values in [-1, 1] (what the decode feeds the
+  // kernels; all-zero operands would let the MFMA kernels run cooler)
+  auto fill = [&](float* dst, size_t count, uint64_t seed) {
+    std::vector<float> v(count);
+    uint64_t z = seed * 0x9E3779B97F4A7C15ull + 1;
+    for (float& f : v) {
+      z = z * 6364136223846793005ull + 1442695040888963407ull;
+      f = float(int64_t(z >> 40) % 2001 - 1000) * 1e-3f;
+    }
+    HIPC(hipMemcpyAsync(dst, v.data(), count * 4, hipMemcpyHostToDevice, stream_));
+    HIPC(hipStreamSynchronize(stream_));
+  };
+  fill(h_, size_t(MAX_SEQS) * s.dim, 1);
+  fill(att_, size_t(MAX_SEQS) * q, 2);
+  fill(act_, size_t(MAX_SEQS) * s.ffn, 3);
   // hbm_copy: a 256 MiB device-to-device copy (counter calibration)
   constexpr size_t COPY_BYTES = size_t(256) << 20;
   std::unique_ptr<TmpBuf> copy_a, copy_b;
@@ -1632,8 +1644,8 @@ void Engine::time_kernel(const std::string& full_name, uint32_t reps, double* av
     HIPC(hipMemsetAsync(fh_, 0, 2 * size_t(s.dim) * 4, stream_));
   }
   if (name == "slow_attn" || name == "fast_attn") {
-    HIPC(hipMemsetAsync(qkv_, 0, size_t(PREFILL_COLS) * (q + 2 * kv) * 4, stream_));
-    HIPC(hipMemsetAsync(fqkv_, 0, 2 * size_t(s.fast_heads + 2 * s.fast_kv_heads) * s.fast_head_dim * 4, stream_));
+    fill(qkv_, size_t(PREFILL_COLS) * (q + 2 * kv), 4);
+    fill(fqkv_, 2 * size_t(s.fast_heads + 2 * s.fast_kv_heads) * s.fast_head_dim, 5);
   }
   for (uint32_t l = 0; l < layers; ++l) pass(l);  // warm-up
   hipEvent_t e0, e1;
