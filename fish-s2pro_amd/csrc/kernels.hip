@@ -892,13 +892,39 @@ bool gemv_k_supported(uint32_t in) { return in == 512 || in == 1536 || in == 256
 // ---------------------------------------------------------------------------
 // RMSNorm over `ncol` vectors (one block per column).
 // ---------------------------------------------------------------------------
+// One block per column.  Rows of up to 256 * RN_REG elements are held in
+// registers (x and the gain loaded in one batch); longer rows loop.
+constexpr int RN_REG = 16;
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const float* w, float* y, uint32_t n,
                                                        float eps, const uint32_t* done) {
-  if (done && *done) return;
   __shared__ float red[4];
   const uint32_t c = blockIdx.x;
   const float* xc = x + size_t(c) * n;
   float ss = 0.0f;
+  if (n <= 256u * RN_REG) {
+    float xv[RN_REG], gv[RN_REG];
+#pragma unroll
+    for (int j = 0; j < RN_REG; ++j) {
+      const uint32_t i = threadIdx.x + 256u * j;
+      xv[j] = i < n ? xc[i] : 0.0f;
+      gv[j] = i < n ? w[i] : 0.0f;
+    }
+    if (done && *done) return;
+#pragma unroll
+    for (int j = 0; j < RN_REG; ++j) ss += xv[j] * xv[j];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(n)), eps)));
+#pragma unroll
+    for (int j = 0; j < RN_REG; ++j) {
+      const uint32_t i = threadIdx.x + 256u * j;
+      if (i < n) y[size_t(c) * n + i] = __fmul_rn(__fmul_rn(xv[j], scale), gv[j]);
+    }
+    return;
+  }
+  if (done && *done) return;
   for (uint32_t i = threadIdx.x; i < n; i += 256) ss += xc[i] * xc[i];
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -1305,7 +1331,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
     id = 0;
   }
   const bool sem = id >= a.sem_begin && id <= a.sem_end;
-  uint32_t rows[16];
+  uint32_t rows[16] = {};
   if (sem) {
     for (uint32_t cb = 0; cb < a.num_codebooks && cb < 16; ++cb) {
       uint32_t r = uint32_t(tok[1 + cb]) + cb * a.codebook_size;
@@ -1318,17 +1344,24 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   }
   const float sc = (a.scale_enabled && sem) ? a.sem_scale : 1.0f;
   float* h = a.h + size_t(t) * a.dim;
-  for (uint32_t i = threadIdx.x; i < a.dim; i += 256) {
-    float v = half_bits_to_float(a.emb[size_t(id) * a.dim + i]);
-    if (sem) {
-      float cs = 0.0f;
-      for (uint32_t cb = 0; cb < a.num_codebooks && cb < 16; ++cb)
-        cs = __fadd_rn(cs, half_bits_to_float(a.cb_emb[size_t(rows[cb]) * a.dim + i]));
-      v = __fadd_rn(v, cs);
-    }
-    if (a.scale_enabled) v = __fmul_rn(v, sc);
-    h[i] = v;
+  // grid (256-element chunks, tokens): one element per thread, every row's
+  // element loaded in one batch, then the sums in the reference's order
+  const uint32_t i = blockIdx.y * 256 + threadIdx.x;
+  if (i >= a.dim) return;
+  float v = half_bits_to_float(a.emb[size_t(id) * a.dim + i]);
+  if (sem) {
+    float e[16];
+#pragma unroll
+    for (int cb = 0; cb < 16; ++cb)
+      e[cb] = uint32_t(cb) < a.num_codebooks ? half_bits_to_float(a.cb_emb[size_t(rows[cb]) * a.dim + i]) : 0.0f;
+    float cs = 0.0f;
+#pragma unroll
+    for (int cb = 0; cb < 16; ++cb)
+      if (uint32_t(cb) < a.num_codebooks) cs = __fadd_rn(cs, e[cb]);
+    v = __fadd_rn(v, cs);
   }
+  if (a.scale_enabled) v = __fmul_rn(v, sc);
+  h[i] = v;
 }
 
 __device__ __forceinline__ uint32_t sem_to_code(uint32_t tok, uint32_t sem_begin, uint32_t sem_end,
@@ -2100,7 +2133,7 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
 
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
   if (a.num_codebooks > 16) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(embed_kernel, dim3(a.n), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(embed_kernel, dim3(a.n, (a.dim + 255) / 256), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
