@@ -162,6 +162,8 @@ class Engine {
   void mm_skinny(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
                  float eps, uint32_t n, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
                  uint32_t out_rows, const uint32_t* done);
+  L2Warm warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool norm, uint32_t pct_begin,
+                  uint32_t pct_end) const;
   void ensure_prompt(size_t n_int);
   void ensure_codes(size_t n_int);
   void check_state_err(uint32_t nseq = 1);
@@ -182,6 +184,13 @@ class Engine {
   DevLin head_cand_;  // the candidate rows of the head (tiled copy only)
   bool tiled_ = false;
   uint32_t bmm_min_cols_ = 2;  // columns from which F16 linears use the batched product
+  // L2 warming of the output projection by decode attention
+  uint32_t warm_blocks_ = 256;            // warming blocks per kernel (0: off)
+  uint32_t warm_depth_ = 4;               // 16-byte loads per thread in flight
+  uint32_t warm_split_ = 100;             // % of the Slow-AR rows warmed by the partial kernel (rest: merge)
+  uint32_t warm_fast_ = 100;              // % of the Fast-AR rows warmed (one attention kernel)
+  uint32_t warm_step_ = 0;                // % of the first linear's rows warmed by embedding / sampler (no measured gain: off)
+  size_t warm_bytes_ = size_t(24) << 20;  // at most this many weight bytes warmed (8 L2s of 4 MiB)
   std::vector<SlowLayer> slow_;
   std::vector<FastLayer> fast_;
   uint32_t* head_rows_ = nullptr;  // vocabulary id of each candidate logit
@@ -371,6 +380,19 @@ Engine::Engine(const s2hip_config& cfg) {
   // S2HIP_BMM_MIN_COLS=n: F16 linears over >= n columns use the batched MFMA
   // product (0 disables it)
   if (const char* v = getenv("S2HIP_BMM_MIN_COLS")) bmm_min_cols_ = uint32_t(strtoul(v, nullptr, 10));
+  // S2HIP_L2_WARM=blocks[,depth[,slow%[,fast%[,step%]]]]: the warming blocks
+  // that decode attention, the step embedding and the Fast-AR sampler carry
+  // to read the next linear's rows into L2 (blocks rounded down to a
+  // multiple of 8; 0: off)
+  if (const char* v = getenv("S2HIP_L2_WARM")) {
+    unsigned b = 0, d = warm_depth_, sp = warm_split_, fp = warm_fast_, ep = warm_step_;
+    const int n = sscanf(v, "%u,%u,%u,%u,%u", &b, &d, &sp, &fp, &ep);
+    if (n >= 1) warm_blocks_ = b & ~7u;
+    if (n >= 2) warm_depth_ = d;
+    if (n >= 3) warm_split_ = std::min(sp, 100u);
+    if (n >= 4) warm_fast_ = std::min(fp, 100u);
+    if (n >= 5) warm_step_ = std::min(ep, 100u);
+  }
   h_ = dalloc<float>(size_t(NC) * s.dim);
   qkv_ = dalloc<float>(size_t(NC) * qkv_w);
   q_ = dalloc<float>(size_t(NC) * q);
@@ -585,6 +607,34 @@ void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, cons
   }
 }
 
+// The rows lin() reads next for L over ncol columns, as the warming blocks of
+// a kernel before it should read them: only when lin() takes the decode GEMV
+// (1-2 columns, no batched product), whose block shape fixes the span.  The
+// consumer blocks from pct_begin % to pct_end % of the warmed range (at most
+// warm_bytes_) are covered.
+L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool norm, uint32_t pct_begin,
+                        uint32_t pct_end) const {
+  L2Warm w{};
+  if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin) return w;
+  if (L.wt && bmm_min_cols_ && ncol >= bmm_min_cols_ && (!L3 || L3->wt)) return w;
+  const uint32_t rpb = gemv_rows_per_block(L.in, norm, L3 != nullptr);
+  const size_t span = size_t(rpb) * L.row_bytes;
+  if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||
+      (L3 && reinterpret_cast<uintptr_t>(L3->w) % 16))
+    return w;
+  const size_t nb = std::min<size_t>(L.out / rpb, warm_bytes_ / (span * (L3 ? 2 : 1)));  // whole blocks only
+  const uint32_t b0 = uint32_t(nb * pct_begin / 100) & ~7u, b1 = uint32_t(nb * pct_end / 100);
+  if (b1 <= b0) return w;
+  w.base = L.w;
+  w.base3 = L3 ? L3->w : nullptr;
+  w.span = uint32_t(span);
+  w.cb_begin = b0;
+  w.cb_end = b1;
+  w.blocks = warm_blocks_;
+  w.depth = warm_depth_;
+  return w;
+}
+
 // Slow-AR layers (forward_decode_sequence, slow_ar.rs:539-556) over nseq
 // slots from seq0 with cps consecutive positions each, then n_past += cps per
 // slot.  done (nullable) stops the linears; attention and the position
@@ -623,6 +673,9 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     aa.cols_per_seq = cps;
     aa.seq_stride_words = sizeof(DevState) / 4;
     aa.seq_stride_kv = slot_kv_;
+    const bool merge = attn_chunks_ > 1 && attn_mode_ == ATTN_SPLIT;  // a merge kernel follows the partials
+    aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, merge ? warm_split_ : 100);
+    if (merge) aa.warm2 = warm_for(L.wo, nullptr, ncol, false, warm_split_, 100);
     HIPC(launch_attention(aa, stream_));
     lin(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.wo.out, done);
     lin(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, done);
@@ -680,6 +733,7 @@ void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const
     aa.cols_per_seq = cps;
     aa.seq_stride_words = sizeof(DevState) / 4;
     aa.seq_stride_kv = fslot_kv_;
+    aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, warm_fast_);
     HIPC(launch_attention(aa, stream_));
     lin(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
     lin(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
@@ -713,6 +767,8 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint
     sa.next_input = (cb + 1 < s.num_codebooks) ? fh_ : nullptr;
     sa.dim = s.dim;
     sa.n_seq = nseq;
+    // the next sub-step's first linear (one column per slot)
+    if (sa.next_input) sa.warm = warm_for(fast_[0].wqkv, nullptr, nseq, true, 0, warm_step_);
     HIPC(launch_sample_fast(sa, stream_));
     p0 += cps;
     cps = 1;
@@ -745,6 +801,7 @@ void Engine::enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_st
   ea.scale_enabled = s.scale_codebook_embeddings;
   ea.done = done;
   ea.err = &st_->err;
+  ea.warm = warm_for(slow_[0].wqkv, nullptr, nseq, true, 0, warm_step_);
   HIPC(launch_embed(ea, stream_));
   enqueue_slow_layers(nseq, 1, 0, done);
   enqueue_head(nseq, hn_, logits_c_, false, done);

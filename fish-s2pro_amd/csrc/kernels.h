@@ -86,6 +86,31 @@ struct QkvPostArgs {
 };
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 
+// Weight rows of the GEMV launched next, read into L2 by extra blocks of a
+// latency-bound kernel (decode attention) while HBM would otherwise idle.
+// GEMV block cb covers bytes [cb span, cb span + span) from base (and from
+// base3) and runs on XCD cb % 8: workgroups go to the 8 XCDs round-robin by
+// linear index, each XCD with its own L2.  The warming block at linear index
+// L reads only consumer blocks with cb % 8 == L % 8, so each row lands in the
+// L2 that reads it next.  Reads only: a different mapping costs bandwidth,
+// never results.
+struct L2Warm {
+  const uint8_t* base;   // nullptr: no warming blocks
+  const uint8_t* base3;  // nullable: second matrix, same layout (w3 of SwiGLU)
+  uint32_t span;         // bytes per consumer block, multiple of 16
+  uint32_t cb_begin;     // consumer blocks [cb_begin, cb_end) are warmed;
+  uint32_t cb_end;       //   cb_begin is a multiple of 8
+  uint32_t blocks;       // warming blocks, multiple of 8
+  uint32_t depth;        // 16-byte loads per thread in flight: 4, 8 or 16
+};
+// Warming planes a kernel of `plane` blocks per plane appends for w (0 when
+// w.base is null); hipErrorInvalidValue in *err for a malformed descriptor.
+uint32_t l2_warm_planes(const L2Warm& w, uint32_t plane, hipError_t* err);
+// Rows per block of the decode GEMV launch_gemv picks for 1-2 columns and
+// this row length (norm: RMS-normalised input; dual: SwiGLU pair), or 0 when
+// another kernel serves the shape.
+uint32_t gemv_rows_per_block(uint32_t in, bool norm, bool dual);
+
 // Fused decode attention for ncol / cols_per_seq sequences, each with
 // cols_per_seq consecutive query positions starting at its *pos_ptr +
 // pos_offset: QK-norm (optional) + RoPE of q and of the new k, KV append at
@@ -117,6 +142,8 @@ struct AttnArgs {
   uint32_t cols_per_seq;
   uint32_t seq_stride_words;
   size_t seq_stride_kv;
+  L2Warm warm;             // rows of the next GEMV (wo) warmed by extra blocks of the partial kernel
+  L2Warm warm2;            // ... and of the merge kernel
 };
 enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
 constexpr uint32_t ATTN_MAX_CHUNKS = 1024;  // max_seq <= 32768
@@ -135,6 +162,7 @@ struct EmbedArgs {
   uint32_t scale_enabled;
   const uint32_t* done;
   uint32_t* err;
+  L2Warm warm;                 // rows of the next GEMV (layer 0 wqkv), warmed by extra blocks
 };
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s);
 
@@ -178,6 +206,7 @@ struct SampleArgs {
   uint32_t n_seq;
   size_t codes_stride;
   BatchState* batch;         // nullable: counts finished sequences
+  L2Warm warm;               // rows of the next GEMV, warmed by extra blocks
 };
 hipError_t launch_sample_slow(const SampleArgs& a, hipStream_t s);
 hipError_t launch_sample_fast(const SampleArgs& a, hipStream_t s);

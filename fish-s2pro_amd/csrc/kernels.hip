@@ -889,6 +889,55 @@ hipError_t gemv_k_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
 
 bool gemv_k_supported(uint32_t in) { return in == 512 || in == 1536 || in == 2560 || in == 4096 || in == 9728; }
 
+// Warming block r (of w.blocks) at linear grid index L: consumer blocks
+// cb = cb_begin + 8 q + (L % 8) for q = r / 8, r / 8 + blocks / 8, ...  The
+// block's loads (per consumer block and matrix, `per` loads of 16 bytes per
+// thread) are walked as one list, D distinct loads per thread in flight; the
+// walk position is uniform over the block (scalar registers) and past the end
+// of the list stays on the last load.
+template <int D>
+__device__ __forceinline__ void l2_warm_walk(const L2Warm& w, uint32_t L, uint32_t r, uint32_t tid, uint32_t nthr) {
+  const uint32_t stride = nthr * 16u;
+  const uint32_t per = (w.span + stride - 1) / stride;
+  const uint32_t mats = w.base3 ? 2u : 1u;
+  const uint32_t cb0 = w.cb_begin + 8u * (r >> 3) + (L & 7u);
+  if (cb0 >= w.cb_end) return;
+  const uint32_t total = (w.cb_end - cb0 + w.blocks - 1) / w.blocks * mats * per;
+  const uint32_t off0 = tid * 16u, last = w.span - 16u;
+  uint32_t i = 0, m = 0, j = 0, acc = 0;
+  for (uint32_t u0 = 0; u0 < total; u0 += D) {
+    uint32_t v[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const uint8_t* p = (m ? w.base3 : w.base) + size_t(cb0 + i * w.blocks) * w.span;
+      // one word per 16 bytes: every 64-byte sector of the rows is read
+      v[k] = *reinterpret_cast<const uint32_t*>(p + min(off0 + j * stride, last));
+      if (u0 + k + 1 < total) {
+        if (++j == per) {
+          j = 0;
+          if (++m == mats) {
+            m = 0;
+            ++i;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k) acc ^= v[k];
+  }
+  asm volatile("" : : "v"(acc));  // the loads are kept; nothing is stored
+}
+
+__device__ __forceinline__ void l2_warm(const L2Warm& w, uint32_t L, uint32_t r, uint32_t tid, uint32_t nthr) {
+  if (r >= w.blocks) return;
+  if (w.depth >= 16)
+    l2_warm_walk<16>(w, L, r, tid, nthr);
+  else if (w.depth >= 8)
+    l2_warm_walk<8>(w, L, r, tid, nthr);
+  else
+    l2_warm_walk<4>(w, L, r, tid, nthr);
+}
+
 // ---------------------------------------------------------------------------
 // RMSNorm over `ncol` vectors (one block per column).
 // ---------------------------------------------------------------------------
@@ -1011,6 +1060,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   __shared__ float ps[GEMV_WAVES][CH];
   __shared__ float knew[4][HD], vnew[4][HD];
   __shared__ uint32_t is_last;
+  if (blockIdx.z >= a.ncol) {  // warming planes after the attention blocks
+    const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    l2_warm(a.warm, L, L - gridDim.x * gridDim.y * a.ncol, threadIdx.x, 256u);
+    return;
+  }
   const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t rep = a.H / a.Hkv;
@@ -1227,6 +1281,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 // MAXC == 0: a loop over the chunks (any max_chunks).
 template <int HD, int CH, int MAXC>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
+  if (blockIdx.y >= a.ncol) {  // warming planes after the merge blocks
+    const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
+    l2_warm(a.warm2, L, L - gridDim.x * a.ncol, threadIdx.x, HD);
+    return;
+  }
   const uint32_t h = blockIdx.x, col = blockIdx.y, d = threadIdx.x;
   const uint32_t rep = a.H / a.Hkv, g = h / rep, w = h % rep;
   const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks * rep + w) * (HD + 2);
@@ -1311,57 +1370,73 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
 // Slow-AR embedding (time-major ids) -- one block per token.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
-  if (a.done && *a.done) return;
+  const uint32_t chunks = (a.dim + 255) / 256;
+  if (blockIdx.y >= chunks) {  // warming rows after the embedding blocks
+    const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
+    l2_warm(a.warm, L, L - gridDim.x * chunks, threadIdx.x, 256u);
+    return;
+  }
   const uint32_t t = blockIdx.x;
+  const uint32_t ncb = min(a.num_codebooks, 16u);
   const uint32_t cdim = a.num_codebooks + 1;
+  // 1. the done word and the token ids in one round of loads
+  const uint32_t done = a.done ? *a.done : 0u;
   int32_t tok[17];
   if (a.tokens) {
-    for (uint32_t i = 0; i < cdim && i < 17; ++i) tok[i] = a.tokens[size_t(t) * cdim + i];
+    const int32_t* tr = a.tokens + size_t(t) * cdim;
+#pragma unroll
+    for (int k = 0; k < 17; ++k) tok[k] = tr[min(uint32_t(k), ncb)];
   } else {
     // build_step_input: [main, cb0..cb(n-1)] when main is semantic, else [main, 0..]
     const DevState* st = a.state + t;  // one sequence per token row
-    const uint32_t main = st->main_token;
-    const bool sem = main >= a.sem_begin && main <= a.sem_end;
-    tok[0] = int32_t(main);
-    for (uint32_t i = 0; i < a.num_codebooks && i < 16; ++i) tok[1 + i] = sem ? int32_t(st->codes_frame[i]) : 0;
+    tok[0] = int32_t(st->main_token);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) tok[1 + k] = int32_t(st->codes_frame[k]);
+    const uint32_t main = uint32_t(tok[0]);
+    if (!(main >= a.sem_begin && main <= a.sem_end)) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) tok[1 + k] = 0;
+    }
   }
+  if (done) return;
   uint32_t id = uint32_t(tok[0]);
   if (tok[0] < 0 || id >= a.vocab) {
-    if (threadIdx.x == 0 && a.err) atomicOr(a.err, ERR_TOKEN_RANGE);
+    if (threadIdx.x == 0 && blockIdx.y == 0 && a.err) atomicOr(a.err, ERR_TOKEN_RANGE);
     id = 0;
   }
   const bool sem = id >= a.sem_begin && id <= a.sem_end;
-  uint32_t rows[16] = {};
-  if (sem) {
-    for (uint32_t cb = 0; cb < a.num_codebooks && cb < 16; ++cb) {
-      uint32_t r = uint32_t(tok[1 + cb]) + cb * a.codebook_size;
-      if (tok[1 + cb] < 0 || r >= a.cb_rows) {
-        if (threadIdx.x == 0 && a.err) atomicOr(a.err, ERR_TOKEN_RANGE);
-        r = 0;
-      }
-      rows[cb] = r;
+  // codebook rows; unused slots read row 0 (their values are not summed)
+  uint32_t rows[16];
+  bool bad = false;
+#pragma unroll
+  for (int cb = 0; cb < 16; ++cb) {
+    uint32_t r = uint32_t(tok[1 + cb]) + uint32_t(cb) * a.codebook_size;
+    const bool used = sem && uint32_t(cb) < ncb;
+    if (used && (tok[1 + cb] < 0 || r >= a.cb_rows)) {
+      bad = true;
+      r = 0;
     }
+    rows[cb] = used ? r : 0u;
   }
+  if (bad && threadIdx.x == 0 && blockIdx.y == 0 && a.err) atomicOr(a.err, ERR_TOKEN_RANGE);
   const float sc = (a.scale_enabled && sem) ? a.sem_scale : 1.0f;
-  float* h = a.h + size_t(t) * a.dim;
-  // grid (256-element chunks, tokens): one element per thread, every row's
-  // element loaded in one batch, then the sums in the reference's order
-  const uint32_t i = blockIdx.y * 256 + threadIdx.x;
-  if (i >= a.dim) return;
+  // 2. grid (tokens, 256-element chunks): one element per thread; the
+  //    element of every row is loaded in one batch (no branch around the
+  //    loads), then summed in the reference's order
+  const uint32_t i0 = blockIdx.y * 256 + threadIdx.x;
+  const uint32_t i = min(i0, a.dim - 1);
   float v = half_bits_to_float(a.emb[size_t(id) * a.dim + i]);
-  if (sem) {
-    float e[16];
+  float e[16];
 #pragma unroll
-    for (int cb = 0; cb < 16; ++cb)
-      e[cb] = uint32_t(cb) < a.num_codebooks ? half_bits_to_float(a.cb_emb[size_t(rows[cb]) * a.dim + i]) : 0.0f;
-    float cs = 0.0f;
+  for (int cb = 0; cb < 16; ++cb) e[cb] = half_bits_to_float(a.cb_emb[size_t(rows[cb]) * a.dim + i]);
+  // the sum is formed on both paths, so no branch separates the loads
+  float cs = 0.0f;
 #pragma unroll
-    for (int cb = 0; cb < 16; ++cb)
-      if (uint32_t(cb) < a.num_codebooks) cs = __fadd_rn(cs, e[cb]);
-    v = __fadd_rn(v, cs);
-  }
+  for (int cb = 0; cb < 16; ++cb)
+    if (uint32_t(cb) < ncb) cs = __fadd_rn(cs, e[cb]);
+  if (sem) v = __fadd_rn(v, cs);
   if (a.scale_enabled) v = __fmul_rn(v, sc);
-  h[i] = v;
+  if (i0 < a.dim) a.h[size_t(t) * a.dim + i0] = v;
 }
 
 __device__ __forceinline__ uint32_t sem_to_code(uint32_t tok, uint32_t sem_begin, uint32_t sem_end,
@@ -1958,6 +2033,11 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs 
 __global__ __launch_bounds__(SAMPLE_THREADS) void sample_fast_kernel(SampleArgs a) {
   extern __shared__ uint8_t smem_raw[];
   SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
+  const uint32_t nseq = a.n_seq ? a.n_seq : 1u;
+  if (blockIdx.x >= nseq) {  // warming blocks after the sampling blocks
+    l2_warm(a.warm, blockIdx.x, blockIdx.x - nseq, threadIdx.x, SAMPLE_THREADS);
+    return;
+  }
   const uint32_t b = blockIdx.x;
   DevState* st = a.st + b;
   a.logits += size_t(b) * a.n;
@@ -2041,6 +2121,29 @@ hipError_t set_max_lds(K kernel) {
 
 }  // namespace
 
+uint32_t l2_warm_planes(const L2Warm& w, uint32_t plane, hipError_t* err) {
+  if (!w.base) return 0;
+  if (w.blocks == 0 || w.blocks % 8 || w.cb_begin % 8 || w.cb_end <= w.cb_begin || w.span < 16 || w.span % 16 ||
+      reinterpret_cast<uintptr_t>(w.base) % 16 || reinterpret_cast<uintptr_t>(w.base3) % 16 || plane == 0) {
+    *err = hipErrorInvalidValue;
+    return 0;
+  }
+  return (w.blocks + plane - 1) / plane;
+}
+
+// The block shapes gemv_k_pick launches (rows per wave x waves per block).
+uint32_t gemv_rows_per_block(uint32_t in, bool norm, bool dual) {
+  const uint32_t rs = dual ? 1u : 2u;
+  switch (in) {
+    case 512:
+    case 1536:
+    case 2560: return norm ? 8u : rs * 4u;
+    case 4096: return 2u;
+    case 9728: return 1u;
+    default: return 0u;
+  }
+}
+
 hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
   if (wtype != W_F16 && wtype != W_Q8_0 && wtype != W_Q4_0) return hipErrorInvalidValue;
   if (a.in % (wtype == W_F16 ? 8 : 32)) return hipErrorInvalidValue;
@@ -2106,7 +2209,11 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   if (a.ncol > a.cols_per_seq && a.seq_stride_words == 0 && (a.pos_ptr || a.done)) return hipErrorInvalidValue;
   if (a.H % a.Hkv || a.H / a.Hkv > 4) return hipErrorInvalidValue;
   if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
-  const dim3 grid(a.max_chunks, a.Hkv, a.ncol);
+  hipError_t werr = hipSuccess;
+  const uint32_t planes = l2_warm_planes(a.warm, a.max_chunks * a.Hkv, &werr);  // z-planes of warming blocks
+  const uint32_t planes2 = a.max_chunks > 1 ? l2_warm_planes(a.warm2, a.H, &werr) : 0u;
+  if (werr != hipSuccess) return werr;
+  const dim3 grid(a.max_chunks, a.Hkv, a.ncol + planes);
   if (a.mode == ATTN_FUSED) {
     if (!a.counters) return hipErrorInvalidValue;
     switch (a.hd) {
@@ -2123,7 +2230,7 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.max_chunks == 1) return e;
-  const dim3 cgrid(a.H, a.ncol);
+  const dim3 cgrid(a.H, a.ncol + planes2);
   if (a.hd == 64)
     launch_combine<64>(a, cgrid, s);
   else
@@ -2132,8 +2239,11 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
 }
 
 hipError_t launch_embed(const EmbedArgs& a, hipStream_t s) {
-  if (a.num_codebooks > 16) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(embed_kernel, dim3(a.n, (a.dim + 255) / 256), dim3(256), 0, s, a);
+  if (a.num_codebooks > 16 || a.n == 0 || a.dim == 0) return hipErrorInvalidValue;
+  hipError_t werr = hipSuccess;
+  const uint32_t planes = l2_warm_planes(a.warm, a.n, &werr);
+  if (werr != hipSuccess) return werr;
+  hipLaunchKernelGGL(embed_kernel, dim3(a.n, (a.dim + 255) / 256 + planes), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -2165,7 +2275,11 @@ hipError_t launch_sample_fast(const SampleArgs& a, hipStream_t s) {
     configured = true;
   }
   if (a.n > SAMPLE_MAX - 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(sample_fast_kernel, dim3(a.n_seq ? a.n_seq : 1), dim3(SAMPLE_THREADS), sizeof(SampleShared), s, a);
+  hipError_t werr = hipSuccess;
+  const uint32_t wblocks = l2_warm_planes(a.warm, 1u, &werr);  // planes of one block
+  if (werr != hipSuccess) return werr;
+  hipLaunchKernelGGL(sample_fast_kernel, dim3((a.n_seq ? a.n_seq : 1) + wblocks), dim3(SAMPLE_THREADS),
+                     sizeof(SampleShared), s, a);
   return hipGetLastError();
 }
 

@@ -194,3 +194,25 @@ def test_attention_modes_match_oracle(tiny_gguf, monkeypatch, fused):
     assert rg["n_frames"] == 40
     mism, total = teacher_forced_mismatches(o, prompt, rg["codes"], 40, 0.7, 0.9, 0, 100, 7, synth.TINY.im_end_id)
     assert total == 400 and mism <= MAX_SAMPLED_MISMATCH * total, (mism, total)
+
+
+@pytest.mark.parametrize("warm", ["8,16,50,50,100", "256,4,100,100,100", "16,8,0,100,30"])
+@pytest.mark.parametrize("which", ["f16", "q8"])
+def test_l2_warming_leaves_codes_unchanged(request, monkeypatch, which, warm):
+    """The blocks that read the next linear's rows into L2 (carried by the
+    attention partial / merge kernels, the step embedding and the Fast-AR
+    sampler) only read: codes and RNG state equal those of a run without them,
+    and greedy codes stay bit-exact against the oracle."""
+    path = request.getfixturevalue("tiny_gguf" if which == "f16" else "tiny_q8_gguf")
+    prompt = make_prompt(synth.TINY, 70, seed=17)
+    kw = dict(temperature=0.7, top_p=0.9, top_k=0, min_tokens_before_end=100, rng_state=9)
+    runs = {}
+    for setting in ("0", warm):
+        monkeypatch.setenv("S2HIP_L2_WARM", setting)
+        e = _engine(path, max_seq=128)
+        runs[setting] = (e.generate_codes(prompt, 12, **kw), e.generate_codes(prompt, 12, min_tokens_before_end=100))
+    (s0, g0), (s1, g1) = runs["0"], runs[warm]
+    assert np.array_equal(s0["codes"], s1["codes"]) and s0["rng_state"] == s1["rng_state"]
+    assert np.array_equal(g0["codes"], g1["codes"])
+    ro = _oracle(path, max_seq=128).generate_codes(prompt, 12, 0.0, 1.0, 0, 100, 0)
+    assert np.array_equal(g1["codes"], ro["codes"])
