@@ -702,16 +702,16 @@ hipError_t gemv_k_launch(const GemvArgs& a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV with an RMS-normalised input, x shared through LDS.
+// Decode GEMV with x shared through LDS (NORM: RMS-normalised input).
 //   Each wave loads only the 512-element steps k = wave (mod WPB) of x and of
 //   the gain, then issues all of its weight loads; the block reduces the sum of
-//   squares, writes x * scale * gain once to LDS, and every wave reads the
-//   normalised x from there.  The x / gain loads are issued first, so the
+//   squares, writes x * scale * gain (NORM) or x once to LDS, and every wave
+//   reads x from there.  The x / gain loads are issued first, so the
 //   waits before the two barriers cover them and not the weights (vector
 //   memory counters retire in order), and the LDS staging overlaps the HBM
 //   latency of the weight rows.  One row (two for SwiGLU: w1 and w3) per wave.
 // ---------------------------------------------------------------------------
-template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB>
+template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, bool NORM>
 __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
@@ -734,8 +734,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
       xv[c][j][0] = *reinterpret_cast<const float4*>(xc);
       xv[c][j][1] = *reinterpret_cast<const float4*>(xc + 4);
     }
-    gv[j][0] = *reinterpret_cast<const float4*>(a.norm + e);
-    gv[j][1] = *reinterpret_cast<const float4*>(a.norm + e + 4);
+    if constexpr (NORM) {
+      gv[j][0] = *reinterpret_cast<const float4*>(a.norm + e);
+      gv[j][1] = *reinterpret_cast<const float4*>(a.norm + e + 4);
+    }
   }
   // 2. weight loads of the wave's row
   uint32_t lr = row < a.out ? row : a.out - 1;  // clamp; result discarded
@@ -752,7 +754,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
   const uint32_t done = a.done ? __builtin_nontemporal_load(a.done) : 0u;
   // 3. block sum of squares -> scale
 #pragma unroll
-  for (int c = 0; c < NCOL; ++c) {
+  for (int c = 0; c < NCOL && NORM; ++c) {
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < KW; ++j) {
@@ -767,14 +769,17 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
     ss = wave_sum(ss);
     if (lane == 0) red[c][wave] = ss;
   }
-  __syncthreads();
-  // 4. normalised x into LDS
+  if constexpr (NORM) __syncthreads();
+  // 4. (normalised) x into LDS
 #pragma unroll
   for (int c = 0; c < NCOL; ++c) {
-    float tot = 0.0f;
+    float scale = 1.0f;
+    if constexpr (NORM) {
+      float tot = 0.0f;
 #pragma unroll
-    for (int i = 0; i < WPB; ++i) tot += red[c][i];
-    const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), a.eps)));
+      for (int i = 0; i < WPB; ++i) tot += red[c][i];
+      scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), a.eps)));
+    }
 #pragma unroll
     for (int j = 0; j < KW; ++j) {
       const int k = wave + j * WPB;
@@ -782,11 +787,13 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float4 u = xv[c][j][h];
-          const float4 g = gv[j][h];
-          u.x = __fmul_rn(__fmul_rn(u.x, scale), g.x);
-          u.y = __fmul_rn(__fmul_rn(u.y, scale), g.y);
-          u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
-          u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
+          if constexpr (NORM) {
+            const float4 g = gv[j][h];
+            u.x = __fmul_rn(__fmul_rn(u.x, scale), g.x);
+            u.y = __fmul_rn(__fmul_rn(u.y, scale), g.y);
+            u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
+            u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
+          }
           xs[c][(k * 512 + lane * 8) / 4 + h] = u;
         }
       }
@@ -838,11 +845,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
   }
 }
 
-template <uint32_t WT, int NCOL, int EPI, int KIT>
+template <uint32_t WT, int NCOL, int EPI, int KIT, bool NORM = true, int WPB = 8>
 hipError_t gemv_n_launch(const GemvArgs& a, hipStream_t s) {
-  constexpr int WPB = 8;
   const dim3 grid((a.out + WPB - 1) / WPB);
-  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB>), grid, dim3(64 * WPB), 0, s, a);
+  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB, NORM>), grid, dim3(64 * WPB), 0, s, a);
   return hipGetLastError();
 }
 
@@ -864,8 +870,12 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
     case 512: return gemv_k_launch<WT, NCOL, RS, EPI, 1, 4>(a, s);
     case 1536: return gemv_k_launch<WT, NCOL, RS, EPI, 3, 4>(a, s);
     case 2560: return gemv_k_launch<WT, NCOL, RS, EPI, 5, 4>(a, s);
-    case 4096: return gemv_k_launch<WT, NCOL, 1, EPI, 8, 2>(a, s);
-    case 9728: return gemv_k_launch<WT, NCOL, 1, EPI, 19, 1>(a, s);
+    // long rows (wo, w2): x staged once per block in LDS.  Per-wave x reads
+    // from L2/L1 were 2x the weight bytes; 2 / 4 waves per block keep 1280 /
+    // 640 blocks for the 256 CUs (8 left a quarter of the CUs with two
+    // blocks): w2 12.1 -> 10.9 us, wo 6.3 -> 5.9 us
+    case 4096: return gemv_n_launch<WT, NCOL, EPI, 8, false, 2>(a, s);
+    case 9728: return gemv_n_launch<WT, NCOL, EPI, 19, false, 4>(a, s);
     default: return hipErrorNotSupported;
   }
 }
@@ -2138,8 +2148,8 @@ uint32_t gemv_rows_per_block(uint32_t in, bool norm, bool dual) {
     case 512:
     case 1536:
     case 2560: return norm ? 8u : rs * 4u;
-    case 4096: return 2u;
-    case 9728: return 1u;
+    case 4096: return norm ? 8u : 2u;
+    case 9728: return norm ? 8u : 4u;
     default: return 0u;
   }
 }
