@@ -1,0 +1,255 @@
+"""The reference's dump comparators, restated (crates/fish_s2_parity/src/lib.rs).
+
+Same checks, tolerances and failure texts as compare_generated_codes_dumps
+(:709-804), compare_fast_ar_frame_dumps (:1211-1289),
+compare_semantic_token_dumps (:1291-1348) and compare_slow_ar_dumps
+(:1365-1710), over the JSON files that `s2hip.dumps` and the reference's
+dump tools write.  Command line as `fish_s2_parity`'s subcommands:
+
+    python -m s2hip.parity compare-generated-codes expected.json actual.json
+    python -m s2hip.parity compare-semantic-tokens expected.json actual.json
+    python -m s2hip.parity compare-fast-ar-frame expected.json actual.json
+    python -m s2hip.parity compare-slow-ar expected.json actual.json
+"""
+
+import json
+import math
+import sys
+from dataclasses import dataclass, field, replace
+from typing import List, Optional
+
+
+@dataclass
+class Report:
+    passed: bool
+    failures: List[str]
+    tensor_deltas: list = field(default_factory=list)
+
+
+@dataclass(frozen=True)
+class SlowArTensorTolerance:
+    """SlowArTensorTolerance::default (lib.rs:155-172)."""
+    max_l2_delta: float = 6e-2
+    max_mean_abs_delta: float = 5e-4
+    max_max_abs_delta: float = 1.5e-2
+    max_first8_mae: float = 8e-4
+
+
+@dataclass
+class TensorDelta:
+    name: str
+    l2_delta: float
+    mean_abs_delta: float
+    max_abs_delta: float
+    first8_mae: float
+
+
+def _f32(x) -> float:
+    """f32 fields compare after an f32 round trip, as serde reads them."""
+    import numpy as np
+    return float(np.float32(x))
+
+
+def _meta(failures, name, expected, actual, close=False):
+    if close:
+        if abs(_f32(expected) - _f32(actual)) > 1e-6:
+            failures.append(f"{name} mismatch: expected {expected}, actual {actual}")
+    elif expected != actual:
+        failures.append(f"{name} mismatch: expected {expected!r}, actual {actual!r}")
+
+
+def compare_generated_codes_dumps(expected: dict, actual: dict) -> Report:
+    f = []
+    _meta(f, "text", expected["text"], actual["text"])
+    _meta(f, "prompt_text", expected.get("prompt_text"), actual.get("prompt_text"))
+    _meta(f, "prompt_code_cols", expected.get("prompt_code_cols"), actual.get("prompt_code_cols"))
+    _meta(f, "temperature", expected["temperature"], actual["temperature"], close=True)
+    _meta(f, "top_p", expected["top_p"], actual["top_p"], close=True)
+    for k in ("top_k", "max_new_tokens", "min_tokens_before_end", "prompt_cols", "num_codebooks", "n_frames"):
+        _meta(f, k, expected[k], actual[k])
+    for side, d in (("expected", expected), ("actual", actual)):
+        n = d["num_codebooks"] * d["n_frames"]
+        if len(d["codes"]) != n:
+            f.append(f"{side} codes length {len(d['codes'])} does not match num_codebooks*n_frames {n}")
+    if expected["codes"] != actual["codes"]:
+        f.append(f"codes mismatch: expected {expected['codes']}, actual {actual['codes']}")
+    return Report(not f, f)
+
+
+def compare_fast_ar_frame_dumps(expected: dict, actual: dict) -> Report:
+    f = []
+    _meta(f, "text", expected["text"], actual["text"])
+    _meta(f, "temperature", expected["temperature"], actual["temperature"], close=True)
+    _meta(f, "top_p", expected["top_p"], actual["top_p"], close=True)
+    for k in ("top_k", "min_tokens_before_end", "prompt_cols", "main_token_id"):
+        _meta(f, k, expected[k], actual[k])
+    e, a = expected["slow_hidden"], actual["slow_hidden"]
+    if len(e) != len(a):
+        f.append(f"slow_hidden length mismatch: expected {len(e)}, actual {len(a)}")
+    else:
+        max_abs, l2 = 0.0, 0.0
+        for x, y in zip(e, a):
+            d = _f32(x) - _f32(y)
+            max_abs = max(max_abs, abs(d))
+            l2 += d * d
+        l2 = math.sqrt(l2)
+        if max_abs > 1e-2 or l2 > 0.5:
+            f.append(f"slow_hidden mismatch: max_abs={max_abs:.8f} l2={l2:.8f}")
+    if expected["codebook_ids"] != actual["codebook_ids"]:
+        f.append(f"codebook_ids mismatch: expected {expected['codebook_ids']}, actual {actual['codebook_ids']}")
+    return Report(not f, f)
+
+
+def compare_semantic_token_dumps(expected: dict, actual: dict) -> Report:
+    f = []
+    _meta(f, "text", expected["text"], actual["text"])
+    _meta(f, "temperature", expected["temperature"], actual["temperature"], close=True)
+    _meta(f, "top_p", expected["top_p"], actual["top_p"], close=True)
+    for k in ("top_k", "max_new_tokens", "min_tokens_before_end", "prompt_cols", "main_token_ids"):
+        _meta(f, k, expected[k], actual[k])
+    return Report(not f, f)
+
+
+# -- Slow-AR tensor statistics ---------------------------------------------------
+_REQUIRED = ("normalized", "query", "key", "value", "attention", "projected", "hidden")
+_OPTIONAL = ("ffn_normalized", "ffn_gate", "ffn_up", "ffn_activated", "ffn_projected", "block_hidden")
+
+
+def _effective_tolerance(expected: dict, actual: dict, tol: SlowArTensorTolerance) -> SlowArTensorTolerance:
+    """Looser bounds for full 36-layer stacks (lib.rs:1516-1534)."""
+    layers = max(expected.get("layer_count") or 1, actual.get("layer_count") or 1)
+    if layers < 36:
+        return tol
+    return SlowArTensorTolerance(max(tol.max_l2_delta, 0.75), max(tol.max_mean_abs_delta, 6e-3),
+                                 max(tol.max_max_abs_delta, 1.0), max(tol.max_first8_mae, 0.20))
+
+
+def _tokens(dump: dict, side: str, failures: list):
+    """normalized_slow_ar_tokens (lib.rs:1536-1592)."""
+    seq = dump.get("sequence") or []
+    if seq:
+        tc = dump.get("token_count")
+        if tc is not None and tc != len(seq):
+            failures.append(f"{side}.token_count mismatch: declared {tc}, sequence has {len(seq)}")
+        return seq
+    if all(dump.get(k) is not None for k in _REQUIRED):
+        tok = {"position": dump["position"]}
+        for k in _REQUIRED + _OPTIONAL:
+            tok[k] = dump.get(k)
+        return [tok]
+    failures.append(f"{side} Slow-AR dump has no top-level stats or sequence")
+    return []
+
+
+def _first8_mae(e, a) -> float:
+    n = max(len(e), len(a))
+    if n == 0:
+        return 0.0
+    return sum(abs((e[i] if i < len(e) else 0.0) - (a[i] if i < len(a) else 0.0)) for i in range(n)) / n
+
+
+def _compare_stats(name, e, a, tol, failures) -> TensorDelta:
+    if e["len"] != a["len"]:
+        failures.append(f"{name}.len mismatch: expected {e['len']}, actual {a['len']}")
+    d = TensorDelta(name, abs(e["l2"] - a["l2"]), abs(e["mean_abs"] - a["mean_abs"]),
+                    abs(e["max_abs"] - a["max_abs"]), _first8_mae(e["first8"], a["first8"]))
+    if d.l2_delta > tol.max_l2_delta:
+        failures.append(f"{name}.l2 delta {d.l2_delta:.8f} exceeds {tol.max_l2_delta:.8f}")
+    if d.mean_abs_delta > tol.max_mean_abs_delta:
+        failures.append(f"{name}.mean_abs delta {d.mean_abs_delta:.8f} exceeds {tol.max_mean_abs_delta:.8f}")
+    if d.max_abs_delta > tol.max_max_abs_delta:
+        failures.append(f"{name}.max_abs delta {d.max_abs_delta:.8f} exceeds {tol.max_max_abs_delta:.8f}")
+    if d.first8_mae > tol.max_first8_mae:
+        failures.append(f"{name}.first8 MAE {d.first8_mae:.8f} exceeds {tol.max_first8_mae:.8f}")
+    return d
+
+
+def _compare_optional(name, e, a, tol, failures) -> Optional[TensorDelta]:
+    if e is not None and a is not None:
+        return _compare_stats(name, e, a, tol, failures)
+    if e is not None:
+        failures.append(f"{name} missing from actual dump")
+    elif a is not None:
+        failures.append(f"{name} missing from expected dump")
+    return None
+
+
+def compare_slow_ar_dumps(expected: dict, actual: dict, tolerance: SlowArTensorTolerance = None) -> Report:
+    tol = tolerance or SlowArTensorTolerance()
+    f = []
+    for k in ("layer", "position", "hidden_size", "head_count", "head_count_kv", "head_dim"):
+        if expected[k] != actual[k]:
+            f.append(f"{k} mismatch: expected {expected[k]}, actual {actual[k]}")
+    el, al = expected.get("layer_count"), actual.get("layer_count")
+    if el is not None and al is not None and el != al:
+        f.append(f"layer_count mismatch: expected {el}, actual {al}")
+    elif el is not None and al is None:
+        f.append("layer_count missing from actual dump")
+    elif el is None and al is not None:
+        f.append("layer_count missing from expected dump")
+    tol = _effective_tolerance(expected, actual, tol)
+    et, at = _tokens(expected, "expected", f), _tokens(actual, "actual", f)
+    if len(et) != len(at):
+        f.append(f"token count mismatch: expected {len(et)}, actual {len(at)}")
+    deltas = []
+    for i, (e, a) in enumerate(zip(et, at)):
+        if e["position"] != a["position"]:
+            f.append(f"token{i}.position mismatch: expected {e['position']}, actual {a['position']}")
+        for k in _REQUIRED:
+            deltas.append(_compare_stats(f"token{i}.{k}", e[k], a[k], tol, f))
+        for k in _OPTIONAL:
+            d = _compare_optional(f"token{i}.{k}", e.get(k), a.get(k), tol, f)
+            if d:
+                deltas.append(d)
+    d = _compare_optional("final_normalized", expected.get("final_normalized"), actual.get("final_normalized"),
+                          tol, f)
+    if d:
+        deltas.append(d)
+    d = _compare_optional("logits", expected.get("logits"), actual.get("logits"),
+                          replace(tol, max_l2_delta=max(tol.max_l2_delta, 2.5)), f)
+    if d:
+        deltas.append(d)
+    et_top, at_top = expected.get("top_logits") or [], actual.get("top_logits") or []
+    if et_top or at_top:
+        if len(et_top) != len(at_top):
+            f.append(f"top_logits length mismatch: expected {len(et_top)}, actual {len(at_top)}")
+        for i, (e, a) in enumerate(zip(et_top, at_top)):
+            if e["token_id"] != a["token_id"]:
+                f.append(f"top_logits[{i}].token_id mismatch: expected {e['token_id']}, actual {a['token_id']}")
+            dv = abs(e["value"] - a["value"])
+            if dv > tol.max_max_abs_delta:
+                f.append(f"top_logits[{i}].value delta {dv:.8f} exceeds {tol.max_max_abs_delta:.8f}")
+    return Report(not f, f, deltas)
+
+
+_COMMANDS = {
+    "compare-generated-codes": (compare_generated_codes_dumps, "generated codebook parity failed"),
+    "compare-semantic-tokens": (compare_semantic_token_dumps, "semantic token parity failed"),
+    "compare-fast-ar-frame": (compare_fast_ar_frame_dumps, "Fast-AR frame parity failed"),
+    "compare-slow-ar": (compare_slow_ar_dumps, "Slow-AR tensor parity failed"),
+}
+
+
+def main(argv=None) -> int:
+    argv = sys.argv[1:] if argv is None else argv
+    if len(argv) != 3 or argv[0] not in _COMMANDS:
+        print("usage:\n" + "\n".join(f"  python -m s2hip.parity {c} <expected.json> <actual.json>"
+                                     for c in _COMMANDS), file=sys.stderr)
+        return 2
+    fn, msg = _COMMANDS[argv[0]]
+    with open(argv[1]) as fe, open(argv[2]) as fa:
+        report = fn(json.load(fe), json.load(fa))
+    print(f"passed={'true' if report.passed else 'false'}")
+    for d in report.tensor_deltas:
+        print(f"tensor={d.name} l2_delta={d.l2_delta:.8f} mean_abs_delta={d.mean_abs_delta:.8f} "
+              f"max_abs_delta={d.max_abs_delta:.8f} first8_mae={d.first8_mae:.8f}")
+    for x in report.failures:
+        print(f"failure={x}")
+    if not report.passed:
+        print(msg, file=sys.stderr)
+        return 1
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
