@@ -162,6 +162,7 @@ class Engine {
   void mm_skinny(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
                  float eps, uint32_t n, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
                  uint32_t out_rows, const uint32_t* done);
+  bool uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const;
   L2Warm warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool norm, uint32_t pct_begin,
                   uint32_t pct_end) const;
   void ensure_prompt(size_t n_int);
@@ -589,10 +590,19 @@ void Engine::bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, cons
   }
 }
 
+// Whether lin() runs L over ncol columns on the batched MFMA product.  At
+// two columns the two-column GEMV is faster for single matrices with rows of
+// up to 4096 (S2-Pro wqkv 9.2 vs 12.9 us, wo 7.7 vs 8.3 us); w1/w3 and w2
+// stay on the product (22.6 vs 25.8 us, 15.9 vs 17.9 us).
+bool Engine::uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const {
+  if (!L.wt || !bmm_min_cols_ || ncol < bmm_min_cols_ || (L3 && !L3->wt)) return false;
+  return !(ncol == 2 && !L3 && L.in <= 4096 && gemv_rows_per_block(L.in, false, false) != 0);
+}
+
 void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
                  const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
                  uint32_t out_rows, const uint32_t* done) {
-  if (L.wt && bmm_min_cols_ && ncol >= bmm_min_cols_ && (!L3 || L3->wt)) {
+  if (uses_bmm(L, L3, ncol)) {
     bmm(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, done, &st_->err);
     return;
   }
@@ -615,8 +625,7 @@ void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, cons
 L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool norm, uint32_t pct_begin,
                         uint32_t pct_end) const {
   L2Warm w{};
-  if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin) return w;
-  if (L.wt && bmm_min_cols_ && ncol >= bmm_min_cols_ && (!L3 || L3->wt)) return w;
+  if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin || uses_bmm(L, L3, ncol)) return w;
   const uint32_t rpb = gemv_rows_per_block(L.in, norm, L3 != nullptr);
   const size_t span = size_t(rpb) * L.row_bytes;
   if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||
