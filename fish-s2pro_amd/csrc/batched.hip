@@ -320,10 +320,13 @@ hipError_t launch_tile_f16(const uint16_t* src, uint32_t K, uint32_t M, uint32_t
 }
 
 uint32_t bmm_waves(uint32_t M, uint32_t K) {
-  // one wave per 16-row tile for tall matrices; the k range split over more
-  // waves (summed in LDS) when there are few tiles
+  // the k range of each 16-row tile split over waves (summed in LDS): two
+  // for tall matrices, four when there are few tiles.  One wave per tile is
+  // fastest back to back (w13 at 8 columns: 24.5 vs 26.2 us), but right
+  // after a heavy streaming kernel it measured 33.1 us against 27.4 us with
+  // two, and inside the decode step two waves win (batch 8: +2.5 % frames/s)
   const uint32_t tiles = (M + 15) / 16, steps = K / 32;
-  uint32_t w = tiles >= 512 ? 1u : 4u;
+  uint32_t w = tiles >= 512 ? 2u : 4u;
   while (steps % w) w /= 2;
   return w;
 }

@@ -139,9 +139,10 @@ class Engine {
             const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row, uint32_t out_rows,
             const uint32_t* done);
   // linear over ncol columns: GEMV kernels for 1-2, skinny MFMA for more
+  // (bmm_waves: waves per tile when the batched product serves it, 0 = its default)
   void lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
            const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
-           uint32_t out_rows, const uint32_t* done);
+           uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves = 0);
   // ncol = nseq * cps columns of slots seq0 .. seq0 + nseq - 1 in h_
   void enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done);
   void enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done);
@@ -601,9 +602,9 @@ bool Engine::uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const {
 
 void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
                  const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
-                 uint32_t out_rows, const uint32_t* done) {
+                 uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves) {
   if (uses_bmm(L, L3, ncol)) {
-    bmm(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, done, &st_->err);
+    bmm(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, done, &st_->err, bmm_waves);
     return;
   }
   if (ncol <= 2 || L.in % 256) {
@@ -745,8 +746,12 @@ void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const
     aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, warm_fast_);
     HIPC(launch_attention(aa, stream_));
     lin(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
+    // one wave per tile from 8 columns: the Fast-AR weights are re-read every
+    // sub-step and this product runs warm (batch 8: 22.3 us against 24.2 us
+    // with the two waves that suit the Slow-AR layers; at 2 columns two
+    // waves stay faster)
     lin(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
-        L.w1.out, done);
+        L.w1.out, done, ncol >= 8 && (L.w1.out + 15) / 16 >= 512 ? 1u : 0u);
     lin(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.w2.out, done);
   }
 }
