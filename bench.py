@@ -220,7 +220,7 @@ def main():
         "prefill_tflops": round(prefill_flops(spec, shape, prompt_len, nseq) / (r["prefill_ms"] * 1e-3) / 1e12, 2),
         "frame_bytes": round(fb),
         "frame_roofline_frac": round(fb * (steps / dec_s) / (HBM_PEAK_GBS * 1e9), 4),
-        "roofline": {"bound": "hbm", "kernel": (f"gemv {kern}" if nseq == 1 else f"skinny MFMA {kern}") +
+        "roofline": {"bound": "hbm", "kernel": (f"gemv {kern}" if nseq == 1 else f"batched MFMA product {kern}") +
                      " (fused RMSNorm + w1/w3 + SwiGLU)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": counter_traffic(kern, args.workload),
