@@ -47,7 +47,8 @@ def frame_bytes(spec, shape, avg_t, kv_bytes=4, nseq=1):
     """Algorithmic HBM bytes of one decode step of nseq requests: Slow weights
     once, Fast weights for 9 passes (positions 0 and 1 share one pass), the
     candidate head rows and norms once; per request the embeddings and the KV
-    reads/writes at the stored KV dtype."""
+    reads/writes at the stored KV dtype (kv_bytes for the Slow-AR cache; the
+    Fast-AR cache is f32)."""
     b_w = {1: 2.0, 8: 34 / 32, 2: 18 / 32}[spec["linear_type"]]
     d, L, Lf = spec["dim"], spec["slow_layers"], spec["fast_layers"]
     ncb, C = spec["num_codebooks"], spec["codebook_size"]
@@ -58,7 +59,7 @@ def frame_bytes(spec, shape, avg_t, kv_bytes=4, nseq=1):
     slow += nseq * (avg_t * L * 2 * kv * kv_bytes + L * 2 * kv * kv_bytes)
     fast_pass = Lf * shape.linear_params_per_fast_layer() * b_w + d * C * b_w + Lf * 2 * d * 2 + 2 * d + nseq * d * 2
     fkv = spec["fast_kv_heads"] * spec["fast_head_dim"]
-    fast = (ncb - 1) * fast_pass + nseq * Lf * 2 * fkv * kv_bytes * (ncb * (ncb + 1) // 2 + ncb)
+    fast = (ncb - 1) * fast_pass + nseq * Lf * 2 * fkv * 4 * (ncb * (ncb + 1) // 2 + ncb)
     return slow + fast
 
 
@@ -113,6 +114,8 @@ def main():
     ap.add_argument("--workload", default="full", choices=sorted(WORKLOADS))
     ap.add_argument("--model-dir", default=os.environ.get("S2HIP_MODEL_DIR", "/tmp/s2hip_models"))
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--kv", choices=("f32", "f16"), default="f32",
+                    help="Slow-AR KV cache dtype (f32 as the reference; f16 halves KV traffic)")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-frames", type=int, default=2)
     ap.add_argument("--cpu-prompt", type=int, default=4)
@@ -137,7 +140,7 @@ def main():
     path = synth.ensure_gguf(shape, args.model_dir, threads=min(16, os.cpu_count() or 1))
     log(f"model {path} ready in {time.time() - t0:.1f}s")
     t0 = time.time()
-    eng = Engine(path, max_seq, shape.im_end_id, use_graph=not args.no_graph)
+    eng = Engine(path, max_seq, shape.im_end_id, use_graph=not args.no_graph, kv_f16=args.kv == "f16")
     spec = eng.spec
     log(f"engine loaded in {time.time() - t0:.1f}s ({spec['weight_bytes'] / 1e9:.2f} GB in HBM)")
     kw = dict(temperature=temp, top_p=top_p, top_k=top_k, min_tokens_before_end=1 << 30)
@@ -166,7 +169,7 @@ def main():
 
     steps = n // nseq  # decode steps (frames per request)
     avg_t = prompt_len + steps / 2.0
-    fb = frame_bytes(spec, shape, avg_t, nseq=nseq)  # bytes per decode step
+    fb = frame_bytes(spec, shape, avg_t, kv_bytes=2 if args.kv == "f16" else 4, nseq=nseq)  # bytes per decode step
     kern = "slow_w13" if nseq == 1 else f"slow_w13_b{nseq}"
     us, kb = eng.time_kernel(kern, reps=5)
     achieved = kb / (us * 1e-6) / 1e9
@@ -213,7 +216,7 @@ def main():
         "config": {"workload": f"{args.workload}: {spec['slow_layers']}+{spec['fast_layers']} layers d={spec['dim']}, "
                                f"{nseq} x {prompt_len}-token prompt, {steps} frames per request, KV {max_seq}",
                    "requests": nseq, "prompt_tokens": prompt_len, "reference_frames": ref_frames,
-                   "frames": steps, "kv_cache": max_seq, "sampler":
+                   "frames": steps, "kv_cache": max_seq, "kv_dtype": args.kv, "sampler":
                        {"temperature": temp, "top_p": top_p, "top_k": top_k}, "parallelism": "single GPU"},
         "codes_per_s": round(fps * spec["num_codebooks"], 1),
         "prefill_ms": round(r["prefill_ms"], 2),

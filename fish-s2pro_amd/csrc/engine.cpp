@@ -177,6 +177,11 @@ class Engine {
   static constexpr size_t STAGING = 64u << 20;
   uint32_t im_end_ = 0;
   uint32_t flags_ = 0;
+  uint32_t kv_f16_ = 0;   // Slow-AR KV cache stored as f16 (S2HIP_FLAG_KV_F16)
+  // element `elems` of a Slow-AR cache buffer (f32 or f16 elements)
+  float* kvp(float* base, size_t elems) const {
+    return reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(base) + elems * (kv_f16_ ? 2 : 4));
+  }
 
   // weights
   uint16_t *emb_ = nullptr, *cb_emb_ = nullptr, *fast_emb_ = nullptr;
@@ -244,6 +249,7 @@ Engine::Engine(const s2hip_config& cfg) {
     fail("max_seq_len above " + std::to_string(32u * ATTN_MAX_CHUNKS) + " is not supported");
   device = cfg.device;
   flags_ = cfg.flags;
+  kv_f16_ = (cfg.flags & S2HIP_FLAG_KV_F16) ? 1u : 0u;
   im_end_ = cfg.im_end_id;
   int ndev = 0;
   HIPC(hipGetDeviceCount(&ndev));
@@ -663,8 +669,9 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     aa.k_norm = L.k_norm;
     aa.eps = s.eps;
     aa.rope = rope_slow_;
-    aa.k_cache = kc_ + size_t(seq0) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
-    aa.v_cache = vc_ + size_t(seq0) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
+    aa.k_cache = kvp(kc_, size_t(seq0) * slot_kv_ + size_t(l) * kv * s.max_seq_len);
+    aa.v_cache = kvp(vc_, size_t(seq0) * slot_kv_ + size_t(l) * kv * s.max_seq_len);
+    aa.kv_f16 = kv_f16_;
     aa.part = part_;
     aa.counters = counters_;
     aa.out = att_;
@@ -947,8 +954,8 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t s
     HIPC(launch_embed(ea, stream_));
     for (uint32_t l = 0; l < s.slow_layers; ++l) {
       const SlowLayer& L = slow_[l];
-      float* kcl = kc_ + size_t(seq) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
-      float* vcl = vc_ + size_t(seq) * slot_kv_ + size_t(l) * kv * s.max_seq_len;
+      float* kcl = kvp(kc_, size_t(seq) * slot_kv_ + size_t(l) * kv * s.max_seq_len);
+      float* vcl = kvp(vc_, size_t(seq) * slot_kv_ + size_t(l) * kv * s.max_seq_len);
       mm(L.wqkv, nullptr, EPI_STORE, ph_, s.dim, L.attn_norm, s.eps, nc, npad, pqkv_, qkv_w);
       QkvPostArgs qa{};
       qa.qkv = pqkv_;
@@ -967,6 +974,7 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t s
       qa.ncol = nc;
       qa.eps = s.eps;
       qa.err = &st->err;
+      qa.kv_f16 = kv_f16_;
       HIPC(launch_qkv_post(qa, stream_));
       PrefillAttnArgs pa{};
       pa.q = pq_;
@@ -981,6 +989,7 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t s
       pa.hd = s.head_dim;
       pa.max_seq = s.max_seq_len;
       pa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
+      pa.kv_f16 = kv_f16_;
       HIPC(launch_attention_prefill(pa, stream_));
       mm(L.wo, nullptr, EPI_RESID, patt_, q, nullptr, 0.0f, nc, npad, ph_, s.dim);
       mm(L.w1, &L.w3, EPI_SWIGLU_SLOW, ph_, s.dim, L.ffn_norm, s.eps, nc, npad, pact_, s.ffn);
@@ -1024,12 +1033,13 @@ void Engine::ensure_slots(uint32_t n) {
       *p = nullptr;
     }
   }
-  kc_ = dalloc<float>(n * slot_kv_);
-  vc_ = dalloc<float>(n * slot_kv_);
+  const size_t kv_bytes = n * slot_kv_ * (kv_f16_ ? 2 : 4);
+  kc_ = dalloc<float>((kv_bytes + 3) / 4);
+  vc_ = dalloc<float>((kv_bytes + 3) / 4);
   fkc_ = dalloc<float>(n * fslot_kv_);
   fvc_ = dalloc<float>(n * fslot_kv_);
-  HIPC(hipMemset(kc_, 0, n * slot_kv_ * 4));
-  HIPC(hipMemset(vc_, 0, n * slot_kv_ * 4));
+  HIPC(hipMemset(kc_, 0, kv_bytes));
+  HIPC(hipMemset(vc_, 0, kv_bytes));
   HIPC(hipMemset(fkc_, 0, n * fslot_kv_ * 4));
   HIPC(hipMemset(fvc_, 0, n * fslot_kv_ * 4));
   kv_slots_ = n;
@@ -1631,8 +1641,9 @@ void Engine::time_kernel(const std::string& full_name, uint32_t reps, double* av
       aa.eps = s.eps;
       aa.rope = fast ? rope_fast_ : rope_slow_;
       const uint32_t kvw = fast ? s.fast_kv_heads * s.fast_head_dim : kv;
-      aa.k_cache = fast ? fkc_ + size_t(l % s.fast_layers) * kvw * fctx_ : kc_ + size_t(l) * kv * s.max_seq_len;
-      aa.v_cache = fast ? fvc_ + size_t(l % s.fast_layers) * kvw * fctx_ : vc_ + size_t(l) * kv * s.max_seq_len;
+      aa.k_cache = fast ? fkc_ + size_t(l % s.fast_layers) * kvw * fctx_ : kvp(kc_, size_t(l) * kv * s.max_seq_len);
+      aa.v_cache = fast ? fvc_ + size_t(l % s.fast_layers) * kvw * fctx_ : kvp(vc_, size_t(l) * kv * s.max_seq_len);
+      aa.kv_f16 = fast ? 0u : kv_f16_;
       aa.part = fast ? fpart_ : part_;
       aa.counters = counters_;
       aa.out = fast ? fatt_ : att_;

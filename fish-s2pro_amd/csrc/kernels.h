@@ -83,6 +83,7 @@ struct QkvPostArgs {
   float eps;
   const uint32_t* done;
   uint32_t* err;
+  uint32_t kv_f16;         // 1: the caches hold f16 (K and V rounded to nearest even when written)
 };
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 
@@ -144,6 +145,7 @@ struct AttnArgs {
   size_t seq_stride_kv;
   L2Warm warm;             // rows of the next GEMV (wo) warmed by extra blocks of the partial kernel
   L2Warm warm2;            // ... and of the merge kernel
+  uint32_t kv_f16;         // 1: k_cache / v_cache hold f16 (seq_stride_kv and offsets in elements)
 };
 enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
 constexpr uint32_t ATTN_MAX_CHUNKS = 1024;  // max_seq <= 32768
@@ -307,6 +309,7 @@ struct PrefillAttnArgs {
   uint32_t pos_offset;
   uint32_t N, H, Hkv, hd, max_seq;
   float scale;
+  uint32_t kv_f16;         // 1: the caches hold f16
 };
 hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s);
 

@@ -9,6 +9,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace s2 {
@@ -997,8 +999,21 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const flo
 // Per-head QK-norm (optional) + NORMAL RoPE for one wave: pairs (2p, 2p+1)
 // rotated by the host-built (cos, sin) row of the position.
 // ---------------------------------------------------------------------------
+// f32 -> f16 bits, round to nearest even (v_cvt_f16_f32), and back
+__device__ __forceinline__ uint16_t f16_bits_rn(float x) { return __half_as_ushort(__float2half_rn(x)); }
+__device__ __forceinline__ float f16_round(float x) { return __half2float(__float2half_rn(x)); }
+
+// Four f16 values (8 bytes) as a float4 (exact)
+__device__ __forceinline__ float4 load_half4(const uint16_t* p) {
+  const uint2 r = *reinterpret_cast<const uint2*>(p);
+  return make_float4(half_bits_to_float(uint16_t(r.x & 0xffffu)), half_bits_to_float(uint16_t(r.x >> 16)),
+                     half_bits_to_float(uint16_t(r.y & 0xffffu)), half_bits_to_float(uint16_t(r.y >> 16)));
+}
+
+// dst16 non-null: the result is stored as f16 bits there instead of dst
 __device__ __forceinline__ void head_norm_rope(const float* src, const float* norm, float eps,
-                                               const float2* rope_row, uint32_t hd, uint32_t lane, float* dst) {
+                                               const float2* rope_row, uint32_t hd, uint32_t lane, float* dst,
+                                               uint16_t* dst16 = nullptr) {
   float scale = 1.0f;
   if (norm) {
     float ss = 0.0f;
@@ -1013,8 +1028,15 @@ __device__ __forceinline__ void head_norm_rope(const float* src, const float* no
       x1 = __fmul_rn(__fmul_rn(x1, scale), norm[2 * p + 1]);
     }
     const float cs = rope_row[p].x, sn = rope_row[p].y;
-    dst[2 * p] = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
-    dst[2 * p + 1] = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+    const float y0 = __fsub_rn(__fmul_rn(x0, cs), __fmul_rn(x1, sn));
+    const float y1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, cs));
+    if (dst16) {
+      dst16[2 * p] = f16_bits_rn(y0);
+      dst16[2 * p + 1] = f16_bits_rn(y1);
+    } else {
+      dst[2 * p] = y0;
+      dst[2 * p + 1] = y1;
+    }
   }
 }
 
@@ -1034,10 +1056,20 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
   if (hi < a.H) {
     head_norm_rope(src, a.q_norm, a.eps, rope_row, hd, lane, a.q_out + size_t(col) * a.H * hd + size_t(hi) * hd);
   } else if (hi < a.H + a.Hkv) {
-    head_norm_rope(src, a.k_norm, a.eps, rope_row, hd, lane, a.k_cache + (size_t(hi - a.H) * a.max_seq + pos) * hd);
+    const size_t off = (size_t(hi - a.H) * a.max_seq + pos) * hd;
+    if (a.kv_f16)
+      head_norm_rope(src, a.k_norm, a.eps, rope_row, hd, lane, nullptr, reinterpret_cast<uint16_t*>(a.k_cache) + off);
+    else
+      head_norm_rope(src, a.k_norm, a.eps, rope_row, hd, lane, a.k_cache + off);
   } else {
-    float* vd = a.v_cache + (size_t(hi - a.H - a.Hkv) * a.max_seq + pos) * hd;
-    for (uint32_t i = lane; i < hd; i += 64) vd[i] = src[i];
+    const size_t off = (size_t(hi - a.H - a.Hkv) * a.max_seq + pos) * hd;
+    if (a.kv_f16) {
+      uint16_t* vd = reinterpret_cast<uint16_t*>(a.v_cache) + off;
+      for (uint32_t i = lane; i < hd; i += 64) vd[i] = f16_bits_rn(src[i]);
+    } else {
+      float* vd = a.v_cache + off;
+      for (uint32_t i = lane; i < hd; i += 64) vd[i] = src[i];
+    }
   }
 }
 
@@ -1059,8 +1091,9 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 //       per (col, g) elects the last block of the pair, which merges them with
 //       agent-scope loads and resets the counter for the next launch.
 // ---------------------------------------------------------------------------
-template <int HD, int CH, bool LAST>
+template <int HD, int CH, bool LAST, bool KH>
 __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+  using KT = std::conditional_t<KH, uint16_t, float>;  // cache element: f16 bits or f32
   constexpr int KS = HD + 1;
   constexpr int PER = CH * HD / 4 / 256;  // float4 per thread per tile
   static_assert(PER >= 1, "tile too small");
@@ -1083,10 +1116,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   // KV cache, position word and done word
   const uint32_t cps = a.cols_per_seq, seq = col / cps, lc = col % cps;
   const float* row = a.qkv + size_t(col) * width;
-  float* kseq = a.k_cache + size_t(seq) * a.seq_stride_kv;
-  float* vseq = a.v_cache + size_t(seq) * a.seq_stride_kv;
-  const float* kc = kseq + size_t(g) * a.max_seq * HD;
-  const float* vc = vseq + size_t(g) * a.max_seq * HD;
+  KT* kseq = reinterpret_cast<KT*>(a.k_cache) + size_t(seq) * a.seq_stride_kv;
+  KT* vseq = reinterpret_cast<KT*>(a.v_cache) + size_t(seq) * a.seq_stride_kv;
+  const KT* kc = kseq + size_t(g) * a.max_seq * HD;
+  const KT* vc = vseq + size_t(g) * a.max_seq * HD;
   const uint32_t t0 = chunk * CH;
 
   // 0. position-independent loads, all in flight together
@@ -1113,8 +1146,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     const uint32_t idx = j * 256 + tid;
     const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
     const uint32_t tt = min(t0 + t, a.max_seq - 1);
-    kr[j] = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
-    vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
+    if constexpr (KH) {
+      kr[j] = load_half4(kc + size_t(tt) * HD + d);
+      vr[j] = load_half4(vc + size_t(tt) * HD + d);
+    } else {
+      kr[j] = *reinterpret_cast<const float4*>(kc + size_t(tt) * HD + d);
+      vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
+    }
   }
   const uint32_t pos = pbase + a.pos_offset + lc;
   const uint32_t T = pos + 1;
@@ -1186,11 +1224,19 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   for (uint32_t c2 = lo - base; c2 < t1 - base; ++c2) {
     const uint32_t tn = base + c2 - t0;
     for (uint32_t i = tid; i < HD; i += 256) {
-      kt[tn * KS + i] = knew[c2][i];
-      vt[tn * HD + i] = vnew[c2][i];
+      // an f16 cache holds the rounded values, and this step reads them so
+      const float kn = KH ? f16_round(knew[c2][i]) : knew[c2][i];
+      const float vn = KH ? f16_round(vnew[c2][i]) : vnew[c2][i];
+      kt[tn * KS + i] = kn;
+      vt[tn * HD + i] = vn;
       if (c2 == lc) {  // SlowArKvCache::write_token for this column's position
-        kseq[(size_t(g) * a.max_seq + pos) * HD + i] = knew[c2][i];
-        vseq[(size_t(g) * a.max_seq + pos) * HD + i] = vnew[c2][i];
+        if constexpr (KH) {
+          kseq[(size_t(g) * a.max_seq + pos) * HD + i] = f16_bits_rn(kn);
+          vseq[(size_t(g) * a.max_seq + pos) * HD + i] = f16_bits_rn(vn);
+        } else {
+          kseq[(size_t(g) * a.max_seq + pos) * HD + i] = kn;
+          vseq[(size_t(g) * a.max_seq + pos) * HD + i] = vn;
+        }
       }
     }
   }
@@ -2224,20 +2270,23 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   const uint32_t planes2 = a.max_chunks > 1 ? l2_warm_planes(a.warm2, a.H, &werr) : 0u;
   if (werr != hipSuccess) return werr;
   const dim3 grid(a.max_chunks, a.Hkv, a.ncol + planes);
+  if (a.hd != 64 && a.hd != 128) return hipErrorInvalidValue;
   if (a.mode == ATTN_FUSED) {
     if (!a.counters) return hipErrorInvalidValue;
-    switch (a.hd) {
-      case 64: hipLaunchKernelGGL((attn_partial_kernel<64, 32, true>), grid, dim3(256), 0, s, a); break;
-      case 128: hipLaunchKernelGGL((attn_partial_kernel<128, 32, true>), grid, dim3(256), 0, s, a); break;
-      default: return hipErrorInvalidValue;
-    }
+    if (a.hd == 64)
+      hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<64, 32, true, true> : attn_partial_kernel<64, 32, true, false>),
+                         grid, dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<128, 32, true, true> : attn_partial_kernel<128, 32, true, false>),
+                         grid, dim3(256), 0, s, a);
     return hipGetLastError();
   }
-  switch (a.hd) {
-    case 64: hipLaunchKernelGGL((attn_partial_kernel<64, 32, false>), grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL((attn_partial_kernel<128, 32, false>), grid, dim3(256), 0, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  if (a.hd == 64)
+    hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<64, 32, false, true> : attn_partial_kernel<64, 32, false, false>),
+                       grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<128, 32, false, true> : attn_partial_kernel<128, 32, false, false>),
+                       grid, dim3(256), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.max_chunks == 1) return e;
   const dim3 cgrid(a.H, a.ncol + planes2);

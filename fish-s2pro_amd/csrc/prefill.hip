@@ -12,8 +12,11 @@
 // scaled by 2^11 so it stays a normal f16 (W.x = Whi.xhi + Whi.xlo +
 // 2^-11 (Wlo'.xhi)).  Each token row is scaled by a power of two before the
 // split so that no value overflows f16; the epilogue undoes the scale.
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
+
+#include <type_traits>
 
 #include "kernels.h"
 
@@ -370,8 +373,17 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_mfma_kernel(SkinnyArgs a
 // ---------------------------------------------------------------------------
 constexpr int PQ = 8, PT = 64;
 
-template <int HD>
+// Four f16 values (8 bytes) as a float4 (exact)
+__device__ __forceinline__ float4 prefill_half4(const uint16_t* p) {
+  const uint2 r = *reinterpret_cast<const uint2*>(p);
+  const __half2 lo = *reinterpret_cast<const __half2*>(&r.x), hi = *reinterpret_cast<const __half2*>(&r.y);
+  const float2 a = __half22float2(lo), b = __half22float2(hi);
+  return make_float4(a.x, a.y, b.x, b.y);
+}
+
+template <int HD, bool KH>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
+  using KT = std::conditional_t<KH, uint16_t, float>;  // cache element: f16 bits or f32
   __shared__ float kt[PT][HD + 1];
   __shared__ float vt[PT][HD];
   __shared__ float qs[4][PQ][HD];
@@ -397,16 +409,21 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
     for (int j = 0; j < HD / 64; ++j) o[c][j] = 0.0f;
   }
   const uint32_t t_end = base + q0 + nq;  // keys needed by the last query
-  const float* kc = a.k_cache + size_t(g) * a.max_seq * HD;
-  const float* vc = a.v_cache + size_t(g) * a.max_seq * HD;
+  const KT* kc = reinterpret_cast<const KT*>(a.k_cache) + size_t(g) * a.max_seq * HD;
+  const KT* vc = reinterpret_cast<const KT*>(a.v_cache) + size_t(g) * a.max_seq * HD;
   for (uint32_t t0 = 0; t0 < t_end; t0 += PT) {
     __syncthreads();  // previous tile consumed (and qs written on the first pass)
     for (uint32_t i = tid; i < PT * HD / 4; i += 256) {
       const uint32_t t = i / (HD / 4), d = (i % (HD / 4)) * 4;
       float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
       if (t0 + t < t_end) {
-        kv = *reinterpret_cast<const float4*>(kc + size_t(t0 + t) * HD + d);
-        vv = *reinterpret_cast<const float4*>(vc + size_t(t0 + t) * HD + d);
+        if constexpr (KH) {
+          kv = prefill_half4(kc + size_t(t0 + t) * HD + d);
+          vv = prefill_half4(vc + size_t(t0 + t) * HD + d);
+        } else {
+          kv = *reinterpret_cast<const float4*>(kc + size_t(t0 + t) * HD + d);
+          vv = *reinterpret_cast<const float4*>(vc + size_t(t0 + t) * HD + d);
+        }
       }
       kt[t][d] = kv.x;
       kt[t][d + 1] = kv.y;
@@ -538,8 +555,14 @@ hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s) {
   if (!a.pos_ptr || a.H % a.Hkv || a.H / a.Hkv > 4 || a.N == 0) return hipErrorInvalidValue;
   const dim3 grid((a.N + PQ - 1) / PQ, a.Hkv);
   switch (a.hd) {
-    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, a); break;
-    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, a); break;
+    case 64:
+      hipLaunchKernelGGL((a.kv_f16 ? attn_prefill_kernel<64, true> : attn_prefill_kernel<64, false>), grid, dim3(256),
+                         0, s, a);
+      break;
+    case 128:
+      hipLaunchKernelGGL((a.kv_f16 ? attn_prefill_kernel<128, true> : attn_prefill_kernel<128, false>), grid,
+                         dim3(256), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

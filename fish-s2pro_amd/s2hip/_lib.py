@@ -63,6 +63,7 @@ class GenStats(ctypes.Structure):
 
 
 FLAG_NO_GRAPH = 1
+FLAG_KV_F16 = 2
 
 _lib = None
 

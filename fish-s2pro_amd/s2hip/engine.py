@@ -31,10 +31,11 @@ def _f32(a) -> np.ndarray:
 
 class Engine:
     def __init__(self, gguf_path: str, max_seq_len: int, im_end_id: int, device: int = 0,
-                 use_graph: bool = True):
+                 use_graph: bool = True, kv_f16: bool = False):
+        """kv_f16: store the Slow-AR KV cache as f16 (S2HIP_FLAG_KV_F16)."""
         L = _lib.load()
-        cfg = _lib.Config(gguf_path.encode(), max_seq_len, im_end_id, device,
-                          0 if use_graph else _lib.FLAG_NO_GRAPH)
+        flags = (0 if use_graph else _lib.FLAG_NO_GRAPH) | (_lib.FLAG_KV_F16 if kv_f16 else 0)
+        cfg = _lib.Config(gguf_path.encode(), max_seq_len, im_end_id, device, flags)
         err = ctypes.create_string_buffer(_lib.ERR_CAP)
         h = L.s2hip_create(ctypes.byref(cfg), err, len(err))
         if not h:

@@ -35,6 +35,11 @@ extern "C" {
 
 /* s2hip_config.flags */
 #define S2HIP_FLAG_NO_GRAPH 1u /* launch every frame kernel directly instead of replaying a HIP graph */
+/* Store the Slow-AR KV cache as f16 (K and V rounded to nearest even when
+ * written): half the KV bytes of the f32 SlowArKvCache (attention.rs:42-43),
+ * in the layout KvCacheSpec describes (registry.rs:83,292-302).  Results then
+ * follow an f32 cache only to about 1e-3; the Fast-AR cache stays f32. */
+#define S2HIP_FLAG_KV_F16 2u
 
 typedef struct s2hip_engine s2hip_engine;
 

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "build", "libs2oracle.so")
 
 FAITHFUL_SLOW_RELOAD = 1
 FAITHFUL_FAST_RECOMPUTE = 2
+KV_F16 = 4  # Slow-AR K/V rounded to f16 when cached
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)

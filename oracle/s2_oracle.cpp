@@ -941,10 +941,17 @@ void slow_layer(orc_model* m, uint32_t layer, float* hid, size_t n_tok, uint32_t
     }
     rope_normal(qt, q, hd, pos, s.rope_base);
     rope_normal(kh.data(), kv, hd, pos, s.rope_base);
-    // SlowArKvCache::write_token (attention.rs:56-76)
+    // SlowArKvCache::write_token (attention.rs:56-76); with ORC_KV_F16 the
+    // stored values are the f16 roundings of K and V
     size_t off = (size_t(layer) * m->max_seq + pos) * kv;
     memcpy(m->kc.data() + off, kh.data(), kv * 4);
     memcpy(m->vc.data() + off, row + q + kv, kv * 4);
+    if (m->flags & ORC_KV_F16) {
+      for (size_t i = 0; i < kv; ++i) {
+        m->kc[off + i] = f16_to_f32(f32_to_f16(m->kc[off + i]));
+        m->vc[off + i] = f16_to_f32(f32_to_f16(m->vc[off + i]));
+      }
+    }
   }
   for (size_t t = 0; t < n_tok; ++t) {
     size_t visible = start + t + 1;

@@ -71,7 +71,9 @@ typedef struct {
 
 enum {
   ORC_FAITHFUL_SLOW_RELOAD = 1, /* re-read + expand each Slow layer from the file per call */
-  ORC_FAITHFUL_FAST_RECOMPUTE = 2 /* Fast-AR prefix recompute (no KV) */
+  ORC_FAITHFUL_FAST_RECOMPUTE = 2, /* Fast-AR prefix recompute (no KV) */
+  ORC_KV_F16 = 4 /* Slow-AR K/V rounded to f16 (RNE) when written to the cache, as an f16 KV store holds
+                    them (KvCacheSpec's f16 layout, registry.rs:83,292-302); off: f32 as SlowArKvCache */
 };
 
 orc_model* orc_open(const char* gguf_path, uint32_t max_seq_len, uint32_t im_end_id,

@@ -131,3 +131,15 @@ def test_batch_errors_and_recovery(tiny_gguf):
     assert [q["n_frames"] for q in r["requests"]] == [4, 4]
     assert np.array_equal(r["requests"][0]["codes"], r["requests"][1]["codes"])
     assert e.generate_codes(ok, 4, min_tokens_before_end=100)["n_frames"] == 4
+
+
+def test_batch_kv_f16_greedy_codes_match_oracle(tiny_gguf):
+    from s2hip import Engine
+
+    prompts = _prompts(3, seed=170)
+    e = Engine(tiny_gguf, 96, synth.TINY.im_end_id, kv_f16=True)
+    o = O.OracleModel(tiny_gguf, 96, synth.TINY.im_end_id, flags=O.KV_F16)
+    rb = e.generate_codes_batch(prompts, 12, min_tokens_before_end=100)
+    for b, pr in enumerate(prompts):
+        ro = o.generate_codes(pr, 12, 0.0, 1.0, 0, 100, 0)
+        assert np.array_equal(rb["requests"][b]["codes"], ro["codes"]), b

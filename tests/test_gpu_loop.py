@@ -216,3 +216,31 @@ def test_l2_warming_leaves_codes_unchanged(request, monkeypatch, which, warm):
     assert np.array_equal(g0["codes"], g1["codes"])
     ro = _oracle(path, max_seq=128).generate_codes(prompt, 12, 0.0, 1.0, 0, 100, 0)
     assert np.array_equal(g1["codes"], ro["codes"])
+
+
+def test_kv_f16_cache_matches_oracle_with_f16_kv(tiny_gguf):
+    """S2HIP_FLAG_KV_F16 against the oracle's ORC_KV_F16 (the same K/V
+    roundings): prefill and decode hidden states and logits to 1e-4, and
+    bit-exact greedy codes over a context that spans several cache chunks."""
+    from s2hip import Engine
+
+    prompt = make_prompt(synth.TINY, 150, seed=18)
+    e = Engine(tiny_gguf, 256, synth.TINY.im_end_id, kv_f16=True)
+    o = O.OracleModel(tiny_gguf, 256, synth.TINY.im_end_id, flags=O.KV_F16)
+    hg, lg = e.eval(prompt)
+    ho, lo = o.eval(prompt)
+    assert _rel(hg, ho) < 1e-4 and _rel(lg, lo) < 1e-4
+    step = make_prompt(synth.TINY, 1, seed=19)
+    hg, lg = e.step(step)
+    ho, lo = o.eval(step)
+    assert _rel(hg, ho) < 1e-4 and _rel(lg, lo) < 1e-4
+    e.reset()
+    r = e.generate_codes(prompt, 24, min_tokens_before_end=100)
+    ro = o.generate_codes(prompt, 24, 0.0, 1.0, 0, 100, 0)
+    assert r["n_frames"] == 24 and np.array_equal(r["codes"], ro["codes"])
+    # the f32 cache is the default, and the two modes differ
+    f = Engine(tiny_gguf, 256, synth.TINY.im_end_id)
+    hf, _ = f.eval(prompt)
+    e.reset()
+    hg, _ = e.eval(prompt)
+    assert 0 < _rel(hg, hf) < 2e-2

@@ -336,6 +336,23 @@ def test_tiny_prefill_chunking_is_exact(tiny_gguf):
     assert np.array_equal(ha, hb) and np.array_equal(la, lb)
 
 
+def test_kv_f16_mode_rounds_the_cache_only(tiny_gguf):
+    """ORC_KV_F16: K and V are stored as their f16 roundings, so the hidden
+    state moves by about f16 precision (nonzero, below 2e-2), and prefill
+    chunking stays exact."""
+    prompt = make_prompt(synth.TINY, 10, seed=6)
+    a = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
+    f = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id, flags=O.KV_F16)
+    ha, _ = a.eval(prompt)
+    hf, _ = f.eval(prompt)
+    rel = float(np.max(np.abs(ha - hf)) / np.max(np.abs(ha)))
+    assert 0 < rel < 2e-2
+    b = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id, flags=O.KV_F16)
+    for t in range(10):
+        hb, _ = b.eval(prompt[t * 11:(t + 1) * 11])
+    assert np.array_equal(hf, hb)
+
+
 def test_im_end_blocking_yields_exact_frame_count(tiny_gguf):
     prompt = make_prompt(synth.TINY, 8, seed=9)
     m = O.OracleModel(tiny_gguf, 64, synth.TINY.im_end_id)
