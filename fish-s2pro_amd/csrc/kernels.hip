@@ -55,6 +55,16 @@ __device__ __forceinline__ uint32_t opt_word(const uint32_t* p) {
   return *(gword*)(p ? p : &kZeroWord);
 }
 
+// Unit gains: the stand-in for an absent QK-norm gain, so that the gain loads
+// need no branch.
+__device__ const float kUnitGain[256] = {
+#define S2_ONE8 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f
+#define S2_ONE64 S2_ONE8, S2_ONE8, S2_ONE8, S2_ONE8, S2_ONE8, S2_ONE8, S2_ONE8, S2_ONE8
+    S2_ONE64, S2_ONE64, S2_ONE64, S2_ONE64
+#undef S2_ONE64
+#undef S2_ONE8
+};
+
 // ---------------------------------------------------------------------------
 // Raw weight payload for 8 consecutive elements, loaded first and decoded
 // later so a wave can keep many independent 16-byte loads in flight.
@@ -714,7 +724,9 @@ hipError_t gemv_k_launch(const GemvArgs& a, hipStream_t s) {
 //   latency of the weight rows.  One row (two for SwiGLU: w1 and w3) per wave.
 // ---------------------------------------------------------------------------
 template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, bool NORM>
-__global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
+__global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows, const uint8_t* w3_rows, const float* x_in,
+                                                              const float* gain, uint32_t row_bytes, uint32_t out,
+                                                              uint32_t row_base, uint32_t extra_row, GemvArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
   constexpr int KW = (KIT + WPB - 1) / WPB;
@@ -732,20 +744,20 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
     const uint32_t e = k * 512 + lane * 8;
 #pragma unroll
     for (int c = 0; c < NCOL; ++c) {
-      const float* xc = a.x + size_t(c) * a.ldx + e;
+      const float* xc = x_in + size_t(c) * a.ldx + e;
       xv[c][j][0] = *reinterpret_cast<const float4*>(xc);
       xv[c][j][1] = *reinterpret_cast<const float4*>(xc + 4);
     }
     if constexpr (NORM) {
-      gv[j][0] = *reinterpret_cast<const float4*>(a.norm + e);
-      gv[j][1] = *reinterpret_cast<const float4*>(a.norm + e + 4);
+      gv[j][0] = *reinterpret_cast<const float4*>(gain + e);
+      gv[j][1] = *reinterpret_cast<const float4*>(gain + e + 4);
     }
   }
   // 2. weight loads of the wave's row
-  uint32_t lr = row < a.out ? row : a.out - 1;  // clamp; result discarded
-  const uint32_t wr = (a.extra_row != NO_ROW && lr == a.out - 1) ? a.extra_row : a.row_base + lr;
-  const uint8_t* rp = a.w + size_t(wr) * a.row_bytes;
-  const uint8_t* rp3 = DUAL ? a.w3 + size_t(wr) * a.row_bytes : nullptr;
+  uint32_t lr = row < out ? row : out - 1;  // clamp; result discarded
+  const uint32_t wr = (extra_row != NO_ROW && lr == out - 1) ? extra_row : row_base + lr;
+  const uint8_t* rp = w_rows + size_t(wr) * row_bytes;
+  const uint8_t* rp3 = DUAL ? w3_rows + size_t(wr) * row_bytes : nullptr;
   Raw8<WT> wb[KIT];
   Raw8<WT> wb3[DUAL ? KIT : 1];
 #pragma unroll
@@ -831,7 +843,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
     const float gsum = wave_sum(acc[c]);
     float u = 0.0f;
     if constexpr (DUAL) u = wave_sum(acc3[c]);
-    if (lane == 0 && row < a.out) {
+    if (lane == 0 && row < out) {
       float* dst = a.y + size_t(c) * a.ldy + row;
       if constexpr (EPI == EPI_STORE) {
         *dst = gsum;
@@ -850,7 +862,9 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(GemvArgs a) {
 template <uint32_t WT, int NCOL, int EPI, int KIT, bool NORM = true, int WPB = 8>
 hipError_t gemv_n_launch(const GemvArgs& a, hipStream_t s) {
   const dim3 grid((a.out + WPB - 1) / WPB);
-  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB, NORM>), grid, dim3(64 * WPB), 0, s, a);
+  if (a.row_bytes > UINT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB, NORM>), grid, dim3(64 * WPB), 0, s, a.w, a.w3, a.x,
+                     a.norm, uint32_t(a.row_bytes), a.out, a.row_base, a.extra_row, a);
   return hipGetLastError();
 }
 
@@ -1092,7 +1106,10 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 //       agent-scope loads and resets the counter for the next launch.
 // ---------------------------------------------------------------------------
 template <int HD, int CH, bool LAST, bool KH>
-__global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, void* k_cache, void* v_cache,
+                                                             const uint32_t* pos_ptr, const uint32_t* done_ptr,
+                                                             uint32_t ncol, uint32_t max_seq, uint32_t kv_stride,
+                                                             uint32_t shape, AttnArgs a) {
   using KT = std::conditional_t<KH, uint16_t, float>;  // cache element: f16 bits or f32
   constexpr int KS = HD + 1;
   constexpr int PER = CH * HD / 4 / 256;  // float4 per thread per tile
@@ -1103,49 +1120,38 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   __shared__ float ps[GEMV_WAVES][CH];
   __shared__ float knew[4][HD], vnew[4][HD];
   __shared__ uint32_t is_last;
-  if (blockIdx.z >= a.ncol) {  // warming planes after the attention blocks
+  if (blockIdx.z >= ncol) {  // warming planes after the attention blocks
     const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    l2_warm(a.warm, L, L - gridDim.x * gridDim.y * a.ncol, threadIdx.x, 256u);
+    l2_warm(a.warm, L, L - gridDim.x * gridDim.y * ncol, threadIdx.x, 256u);
     return;
   }
+  const uint32_t H = shape & 0xffu, Hkv = (shape >> 8) & 0xffu, cps_ = (shape >> 16) & 0xffu, sw = shape >> 24;
   const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t rep = a.H / a.Hkv;
-  const uint32_t width = (a.H + 2 * a.Hkv) * HD;
+  const uint32_t rep = H / Hkv;
+  const uint32_t width = (H + 2 * Hkv) * HD;
   // column col = (sequence seq, its column lc); each sequence has its own
   // KV cache, position word and done word
-  const uint32_t cps = a.cols_per_seq, seq = col / cps, lc = col % cps;
-  const float* row = a.qkv + size_t(col) * width;
-  KT* kseq = reinterpret_cast<KT*>(a.k_cache) + size_t(seq) * a.seq_stride_kv;
-  KT* vseq = reinterpret_cast<KT*>(a.v_cache) + size_t(seq) * a.seq_stride_kv;
-  const KT* kc = kseq + size_t(g) * a.max_seq * HD;
-  const KT* vc = vseq + size_t(g) * a.max_seq * HD;
+  const uint32_t cps = cps_, seq = col / cps, lc = col % cps;
+  const float* row = qkv + size_t(col) * width;
+  KT* kseq = reinterpret_cast<KT*>(k_cache) + size_t(seq) * kv_stride;
+  KT* vseq = reinterpret_cast<KT*>(v_cache) + size_t(seq) * kv_stride;
+  const KT* kc = kseq + size_t(g) * max_seq * HD;
+  const KT* vc = vseq + size_t(g) * max_seq * HD;
   const uint32_t t0 = chunk * CH;
 
-  // 0. position-independent loads, all in flight together
-  const uint32_t done = opt_word(a.done ? a.done + size_t(seq) * a.seq_stride_words : nullptr);
-  const uint32_t pbase = opt_word(a.pos_ptr ? a.pos_ptr + size_t(seq) * a.seq_stride_words : nullptr);
-  const bool qlane = wave < rep && lane < HD / 2;
-  float2 qv = make_float2(0.f, 0.f), qn = make_float2(1.f, 1.f);
-  if (qlane) {
-    qv = *reinterpret_cast<const float2*>(row + size_t(g * rep + wave) * HD + 2 * lane);
-    if (a.q_norm) qn = *reinterpret_cast<const float2*>(a.q_norm + 2 * lane);
-  }
-  // k / v rows of this sequence's columns (wave w <-> column w <= lc)
-  const bool kwave = wave < cps && wave <= lc;
-  float2 kx = make_float2(0.f, 0.f), vx = kx, kn = make_float2(1.f, 1.f);
-  if (kwave && lane < HD / 2) {
-    const float* r2 = a.qkv + size_t(seq * cps + wave) * width;
-    kx = *reinterpret_cast<const float2*>(r2 + size_t(a.H + g) * HD + 2 * lane);
-    vx = *reinterpret_cast<const float2*>(r2 + size_t(a.H + a.Hkv + g) * HD + 2 * lane);
-    if (a.k_norm) kn = *reinterpret_cast<const float2*>(a.k_norm + 2 * lane);
-  }
+  // 0. position-independent loads, all in flight together: the state words
+  //    and the K/V tile (addresses from the preloaded arguments) first, then
+  //    the new rows and the QK-norm gains (gain pointers from the argument
+  //    block)
+  const uint32_t done = opt_word(done_ptr ? done_ptr + size_t(seq) * sw : nullptr);
+  const uint32_t pbase = opt_word(pos_ptr ? pos_ptr + size_t(seq) * sw : nullptr);
   float4 kr[PER], vr[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint32_t idx = j * 256 + tid;
     const uint32_t t = idx / (HD / 4), d = (idx % (HD / 4)) * 4;
-    const uint32_t tt = min(t0 + t, a.max_seq - 1);
+    const uint32_t tt = min(t0 + t, max_seq - 1);
     if constexpr (KH) {
       kr[j] = load_half4(kc + size_t(tt) * HD + d);
       vr[j] = load_half4(vc + size_t(tt) * HD + d);
@@ -1154,12 +1160,29 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
     }
   }
+  // q row of head g * rep + wave and the k / v rows of this sequence's
+  // columns (wave w <-> column w <= lc): every lane loads from a clamped,
+  // valid address and lanes outside the ranges drop the value, so no branch
+  // holds the loads back
+  const uint32_t e2 = 2 * (lane & (HD / 2 - 1));
+  const bool qlane = wave < rep && lane < HD / 2;
+  const bool kwave = wave < cps && wave <= lc;
+  const float2 qraw = *reinterpret_cast<const float2*>(row + size_t(g * rep + min(wave, rep - 1)) * HD + e2);
+  const float* r2 = qkv + size_t(seq * cps + min(wave, lc)) * width;
+  const float2 kraw = *reinterpret_cast<const float2*>(r2 + size_t(H + g) * HD + e2);
+  const float2 vraw = *reinterpret_cast<const float2*>(r2 + size_t(H + Hkv + g) * HD + e2);
+  const float2 qn = *reinterpret_cast<const float2*>((a.q_norm ? a.q_norm : kUnitGain) + e2);
+  const float2 kn = *reinterpret_cast<const float2*>((a.k_norm ? a.k_norm : kUnitGain) + e2);
+  const float2 zero2 = make_float2(0.f, 0.f);
+  const float2 qv = qlane ? qraw : zero2;
+  const float2 kx = (kwave && lane < HD / 2) ? kraw : zero2;
+  const float2 vx = (kwave && lane < HD / 2) ? vraw : zero2;
   const uint32_t pos = pbase + a.pos_offset + lc;
   const uint32_t T = pos + 1;
   const uint32_t nch = (T + CH - 1) / CH;
-  if (done || pos >= a.max_seq || chunk >= nch) {
-    if (!done && pos >= a.max_seq && tid == 0 && chunk == 0 && a.err)
-      atomicOr(a.err + size_t(seq) * a.seq_stride_words, ERR_KV_OVERFLOW);
+  if (done || pos >= max_seq || chunk >= nch) {
+    if (!done && pos >= max_seq && tid == 0 && chunk == 0 && a.err)
+      atomicOr(a.err + size_t(seq) * sw, ERR_KV_OVERFLOW);
     // The exit path also reads the loaded values, so the compiler keeps the
     // loads ahead of this branch (where they overlap the state read) instead
     // of sinking them behind it.  The test is never true for finite data.
@@ -1231,11 +1254,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       vt[tn * HD + i] = vn;
       if (c2 == lc) {  // SlowArKvCache::write_token for this column's position
         if constexpr (KH) {
-          kseq[(size_t(g) * a.max_seq + pos) * HD + i] = f16_bits_rn(kn);
-          vseq[(size_t(g) * a.max_seq + pos) * HD + i] = f16_bits_rn(vn);
+          kseq[(size_t(g) * max_seq + pos) * HD + i] = f16_bits_rn(kn);
+          vseq[(size_t(g) * max_seq + pos) * HD + i] = f16_bits_rn(vn);
         } else {
-          kseq[(size_t(g) * a.max_seq + pos) * HD + i] = kn;
-          vseq[(size_t(g) * a.max_seq + pos) * HD + i] = vn;
+          kseq[(size_t(g) * max_seq + pos) * HD + i] = kn;
+          vseq[(size_t(g) * max_seq + pos) * HD + i] = vn;
         }
       }
     }
@@ -1258,7 +1281,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
   }
   __syncthreads();
   // 5. PV (lane = head-dim element)
-  float* pair_part = a.part + (size_t(col) * a.Hkv + g) * a.max_chunks * rep * (HD + 2);
+  float* pair_part = a.part + (size_t(col) * Hkv + g) * a.max_chunks * rep * (HD + 2);
   if (wave < rep) {
     const uint32_t h = g * rep + wave;
     float o[HD / 64];
@@ -1270,7 +1293,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
       for (int j = 0; j < HD / 64; ++j) o[j] = fmaf(pv, vt[t * HD + lane + 64 * j], o[j]);
     }
     if (nch == 1) {
-      float* dst = a.out + size_t(col) * a.H * HD + size_t(h) * HD;
+      float* dst = a.out + size_t(col) * H * HD + size_t(h) * HD;
       const float inv = 1.0f / l;
 #pragma unroll
       for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = o[j] * inv;
@@ -1299,7 +1322,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
     // 6. the partial stores have completed before the block's arrival is counted
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    uint32_t* cnt = a.counters + size_t(col) * a.Hkv + g;
+    uint32_t* cnt = a.counters + size_t(col) * Hkv + g;
     if (tid == 0) {
       const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       is_last = prev + 1 == nch;
@@ -1325,7 +1348,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
         L = fmaf(lc, f, L);
         acc = fmaf(oc, f, acc);
       }
-      a.out[size_t(col) * a.H * HD + size_t(g * rep + w) * HD + d] = acc / L;
+      a.out[size_t(col) * H * HD + size_t(g * rep + w) * HD + d] = acc / L;
     }
   }
 }
@@ -1336,19 +1359,22 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(AttnArgs a) {
 // slots past this launch's chunk count hold stale data and are ignored.
 // MAXC == 0: a loop over the chunks (any max_chunks).
 template <int HD, int CH, int MAXC>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
-  if (blockIdx.y >= a.ncol) {  // warming planes after the merge blocks
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, float* out, const uint32_t* pos_ptr,
+                                                            const uint32_t* done_ptr, uint32_t ncol, uint32_t max_chunks,
+                                                            uint32_t shape, uint32_t pos_offset, AttnArgs a) {
+  if (blockIdx.y >= ncol) {  // warming planes after the merge blocks
     const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
-    l2_warm(a.warm2, L, L - gridDim.x * a.ncol, threadIdx.x, HD);
+    l2_warm(a.warm2, L, L - gridDim.x * ncol, threadIdx.x, HD);
     return;
   }
+  const uint32_t H = shape & 0xffu, Hkv = (shape >> 8) & 0xffu, cps = (shape >> 16) & 0xffu, sw = shape >> 24;
   const uint32_t h = blockIdx.x, col = blockIdx.y, d = threadIdx.x;
-  const uint32_t rep = a.H / a.Hkv, g = h / rep, w = h % rep;
-  const float* pbase = a.part + ((size_t(col) * a.Hkv + g) * a.max_chunks * rep + w) * (HD + 2);
+  const uint32_t rep = H / Hkv, g = h / rep, w = h % rep;
+  const float* pbase = part + ((size_t(col) * Hkv + g) * max_chunks * rep + w) * (HD + 2);
   const size_t stride = size_t(rep) * (HD + 2);
-  const uint32_t seq = col / a.cols_per_seq, lc = col % a.cols_per_seq;
-  const uint32_t done = opt_word(a.done ? a.done + size_t(seq) * a.seq_stride_words : nullptr);
-  const uint32_t pb = opt_word(a.pos_ptr ? a.pos_ptr + size_t(seq) * a.seq_stride_words : nullptr);
+  const uint32_t seq = col / cps, lc = col % cps;
+  const uint32_t done = opt_word(done_ptr ? done_ptr + size_t(seq) * sw : nullptr);
+  const uint32_t pb = opt_word(pos_ptr ? pos_ptr + size_t(seq) * sw : nullptr);
   if constexpr (MAXC > 0) {
     static_assert(MAXC <= HD, "one thread per chunk slot");
     __shared__ float2 ml[MAXC];
@@ -1356,13 +1382,13 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
     // discarded at the store when the launch has nothing to merge
     float2 mlv = make_float2(0.f, 0.f);
     if (d < uint32_t(MAXC))
-      mlv = *reinterpret_cast<const float2*>(pbase + size_t(min(d, a.max_chunks - 1)) * stride);
+      mlv = *reinterpret_cast<const float2*>(pbase + size_t(min(d, max_chunks - 1)) * stride);
     float oc[MAXC];
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) oc[c] = pbase[size_t(min(uint32_t(c), a.max_chunks - 1)) * stride + 2 + d];
+    for (int c = 0; c < MAXC; ++c) oc[c] = pbase[size_t(min(uint32_t(c), max_chunks - 1)) * stride + 2 + d];
     if (d < uint32_t(MAXC)) ml[d] = mlv;
     __syncthreads();
-    const uint32_t pos = pb + a.pos_offset + lc;
+    const uint32_t pos = pb + pos_offset + lc;
     const bool live = !done && pos < a.max_seq;
     const uint32_t nch = live ? (pos + CH) / CH : 0u;
     float M = -INFINITY;
@@ -1378,14 +1404,14 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
         acc = fmaf(oc[c], f, acc);
       }
     }
-    if (nch > 1) a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
+    if (nch > 1) out[size_t(col) * H * HD + size_t(h) * HD + d] = acc / L;
   } else {
     // many chunks: the chunk maxima and weights in parallel over the
     // threads, then the weighted sum of the partials with 16 loads in flight
     constexpr int NWV = HD / 64;
     __shared__ float fs[ATTN_MAX_CHUNKS];
     __shared__ float rm[NWV], rl[NWV];
-    const uint32_t pos = pb + a.pos_offset + lc;
+    const uint32_t pos = pb + pos_offset + lc;
     if (done || pos >= a.max_seq) return;
     const uint32_t nch = (pos + CH) / CH;
     if (nch <= 1) return;
@@ -1418,7 +1444,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc = fmaf(c0 + j < nch ? fs[c0 + j] : 0.0f, ov[j], acc);
     }
-    a.out[size_t(col) * a.H * HD + size_t(h) * HD + d] = acc / L;
+    out[size_t(col) * H * HD + size_t(h) * HD + d] = acc / L;
   }
 }
 
@@ -2243,18 +2269,36 @@ uint32_t attention_chunks(uint32_t max_seq, uint32_t mode) {
   return (max_seq + 31u) / 32u;
 }
 
+// H | Hkv << 8 | cols_per_seq << 16 | seq_stride_words << 24: the shape word
+// the attention kernels take among their preloaded arguments
+uint32_t attn_shape_word(const AttnArgs& a) {
+  return a.H | a.Hkv << 8 | a.cols_per_seq << 16 | a.seq_stride_words << 24;
+}
+
 template <int HD>
 void launch_combine(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  const uint32_t sh = attn_shape_word(a);
+  auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(HD), 0, s, a.part, a.out, a.pos_ptr, a.done, a.ncol, a.max_chunks, sh,
+                       a.pos_offset, a);
+  };
   if (a.max_chunks <= 8)
-    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 8>), grid, dim3(HD), 0, s, a);
+    go(attn_combine_kernel<HD, 32, 8>);
   else if (a.max_chunks <= 16)
-    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 16>), grid, dim3(HD), 0, s, a);
+    go(attn_combine_kernel<HD, 32, 16>);
   else if (a.max_chunks <= 32)
-    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 32>), grid, dim3(HD), 0, s, a);
+    go(attn_combine_kernel<HD, 32, 32>);
   else if (a.max_chunks <= 64)
-    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 64>), grid, dim3(HD), 0, s, a);
+    go(attn_combine_kernel<HD, 32, 64>);
   else
-    hipLaunchKernelGGL((attn_combine_kernel<HD, 32, 0>), grid, dim3(HD), 0, s, a);
+    go(attn_combine_kernel<HD, 32, 0>);
+}
+
+template <int HD, bool LAST>
+void launch_partial(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<HD, 32, LAST, true> : attn_partial_kernel<HD, 32, LAST, false>),
+                     grid, dim3(256), 0, s, a.qkv, static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache),
+                     a.pos_ptr, a.done, a.ncol, a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
 }
 
 hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
@@ -2263,7 +2307,8 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   if (a.cols_per_seq == 0) a.cols_per_seq = a.ncol;  // one sequence
   if (a.ncol == 0 || a.ncol % a.cols_per_seq || a.cols_per_seq > 4 || a.ncol > 64) return hipErrorInvalidValue;
   if (a.ncol > a.cols_per_seq && a.seq_stride_words == 0 && (a.pos_ptr || a.done)) return hipErrorInvalidValue;
-  if (a.H % a.Hkv || a.H / a.Hkv > 4) return hipErrorInvalidValue;
+  if (a.H % a.Hkv || a.H / a.Hkv > 4 || a.H > 255 || a.seq_stride_words > 255 || a.seq_stride_kv > UINT32_MAX)
+    return hipErrorInvalidValue;
   if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
   hipError_t werr = hipSuccess;
   const uint32_t planes = l2_warm_planes(a.warm, a.max_chunks * a.Hkv, &werr);  // z-planes of warming blocks
@@ -2274,19 +2319,15 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   if (a.mode == ATTN_FUSED) {
     if (!a.counters) return hipErrorInvalidValue;
     if (a.hd == 64)
-      hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<64, 32, true, true> : attn_partial_kernel<64, 32, true, false>),
-                         grid, dim3(256), 0, s, a);
+      launch_partial<64, true>(a, grid, s);
     else
-      hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<128, 32, true, true> : attn_partial_kernel<128, 32, true, false>),
-                         grid, dim3(256), 0, s, a);
+      launch_partial<128, true>(a, grid, s);
     return hipGetLastError();
   }
   if (a.hd == 64)
-    hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<64, 32, false, true> : attn_partial_kernel<64, 32, false, false>),
-                       grid, dim3(256), 0, s, a);
+    launch_partial<64, false>(a, grid, s);
   else
-    hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<128, 32, false, true> : attn_partial_kernel<128, 32, false, false>),
-                       grid, dim3(256), 0, s, a);
+    launch_partial<128, false>(a, grid, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.max_chunks == 1) return e;
   const dim3 cgrid(a.H, a.ncol + planes2);
