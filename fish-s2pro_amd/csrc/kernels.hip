@@ -725,8 +725,9 @@ hipError_t gemv_k_launch(const GemvArgs& a, hipStream_t s) {
 // ---------------------------------------------------------------------------
 template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, bool NORM>
 __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows, const uint8_t* w3_rows, const float* x_in,
-                                                              const float* gain, uint32_t row_bytes, uint32_t out,
-                                                              uint32_t row_base, uint32_t extra_row, GemvArgs a) {
+                                                              const float* gain, const uint32_t* done_ptr,
+                                                              uint32_t row_bytes, uint32_t out, uint32_t row_base,
+                                                              uint32_t extra_row, GemvArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
   constexpr int KW = (KIT + WPB - 1) / WPB;
@@ -765,7 +766,13 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
     wb[k] = load_raw<WT>(rp, k * 512 + lane * 8);
     if constexpr (DUAL) wb3[k] = load_raw<WT>(rp3, k * 512 + lane * 8);
   }
-  const uint32_t done = a.done ? __builtin_nontemporal_load(a.done) : 0u;
+  const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
+  // the argument-block fields used later are read now, while the loads above
+  // are in flight (left to the compiler, the y pointer is read at the store)
+  float eps = a.eps;
+  float* ybase = a.y;
+  uint32_t ldy = a.ldy;
+  asm volatile("" : "+s"(eps), "+s"(ybase), "+s"(ldy));
   // 3. block sum of squares -> scale
 #pragma unroll
   for (int c = 0; c < NCOL && NORM; ++c) {
@@ -792,7 +799,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
       float tot = 0.0f;
 #pragma unroll
       for (int i = 0; i < WPB; ++i) tot += red[c][i];
-      scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), a.eps)));
+      scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), eps)));
     }
 #pragma unroll
     for (int j = 0; j < KW; ++j) {
@@ -844,7 +851,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
     float u = 0.0f;
     if constexpr (DUAL) u = wave_sum(acc3[c]);
     if (lane == 0 && row < out) {
-      float* dst = a.y + size_t(c) * a.ldy + row;
+      float* dst = ybase + size_t(c) * ldy + row;
       if constexpr (EPI == EPI_STORE) {
         *dst = gsum;
       } else if constexpr (EPI == EPI_RESID) {
@@ -864,7 +871,7 @@ hipError_t gemv_n_launch(const GemvArgs& a, hipStream_t s) {
   const dim3 grid((a.out + WPB - 1) / WPB);
   if (a.row_bytes > UINT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB, NORM>), grid, dim3(64 * WPB), 0, s, a.w, a.w3, a.x,
-                     a.norm, uint32_t(a.row_bytes), a.out, a.row_base, a.extra_row, a);
+                     a.norm, a.done, uint32_t(a.row_bytes), a.out, a.row_base, a.extra_row, a);
   return hipGetLastError();
 }
 
@@ -1186,7 +1193,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
     // The exit path also reads the loaded values, so the compiler keeps the
     // loads ahead of this branch (where they overlap the state read) instead
     // of sinking them behind it.  The test is never true for finite data.
-    float keep = qv.x + qv.y + kx.x + kx.y + vx.x + vx.y;
+    float keep = qv.x + qv.y + kx.x + kx.y + vx.x + vx.y + qn.x + qn.y + kn.x + kn.y;
 #pragma unroll
     for (int j = 0; j < PER; ++j)
       keep += (kr[j].x + kr[j].y) + (kr[j].z + kr[j].w) + (vr[j].x + vr[j].y) + (vr[j].z + vr[j].w);
