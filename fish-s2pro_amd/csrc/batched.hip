@@ -88,6 +88,11 @@ __device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8
 // gets a zero activation by a select.  Lane l: column n = l % 16, k group
 // l / 16.  NB = activation rows staged (8 when N <= 8, else 16).
 // ---------------------------------------------------------------------------
+// Weight fragments are read once per launch: non-temporal loads stream them
+// past L2 without evicting the staged activations (8 columns: w13 24.4 ->
+// 23.2 us).
+__device__ __forceinline__ half8 bmm_wload(const half8* p) { return __builtin_nontemporal_load(p); }
+
 template <int EPI, bool NORM, int WAVES, int NB>
 __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
@@ -146,8 +151,8 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
 #pragma unroll
   for (int i = 0; i < WIN; ++i) {
     const uint32_t t = min(uint32_t(i), last);
-    wb[i][0] = *reinterpret_cast<const half8*>(wp0 + 512 * t);
-    if constexpr (DUAL) wb[i][1] = *reinterpret_cast<const half8*>(wp1 + 512 * t);
+    wb[i][0] = bmm_wload(reinterpret_cast<const half8*>(wp0 + 512 * t));
+    if constexpr (DUAL) wb[i][1] = bmm_wload(reinterpret_cast<const half8*>(wp1 + 512 * t));
   }
   stage_store(sxa, sga, 0);
   __builtin_amdgcn_sched_barrier(0);
@@ -204,8 +209,8 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t tw = min(s + WIN, last);
-      wb[wi][0] = *reinterpret_cast<const half8*>(wp0 + 512 * tw);
-      if constexpr (DUAL) wb[wi][1] = *reinterpret_cast<const half8*>(wp1 + 512 * tw);
+      wb[wi][0] = bmm_wload(reinterpret_cast<const half8*>(wp0 + 512 * tw));
+      if constexpr (DUAL) wb[wi][1] = bmm_wload(reinterpret_cast<const half8*>(wp1 + 512 * tw));
       __builtin_amdgcn_sched_barrier(0);
       cx0 = nx0;
       cx1 = nx1;
