@@ -603,7 +603,7 @@ void Engine::bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, cons
 // stay on the product (22.6 vs 25.8 us, 15.9 vs 17.9 us).
 bool Engine::uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const {
   if (!L.wt || !bmm_min_cols_ || ncol < bmm_min_cols_ || (L3 && !L3->wt)) return false;
-  return !(ncol == 2 && !L3 && L.in <= 4096 && gemv_rows_per_block(L.in, false, false) != 0);
+  return !(ncol == 2 && !L3 && L.in <= 4096 && gemv_rows_per_block(L.in, L.out, false, false, ncol) != 0);
 }
 
 void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
@@ -633,7 +633,7 @@ L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool n
                         uint32_t pct_end) const {
   L2Warm w{};
   if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin || uses_bmm(L, L3, ncol)) return w;
-  const uint32_t rpb = gemv_rows_per_block(L.in, norm, L3 != nullptr);
+  const uint32_t rpb = gemv_rows_per_block(L.in, L.out, norm, L3 != nullptr, ncol);
   const size_t span = size_t(rpb) * L.row_bytes;
   if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||
       (L3 && reinterpret_cast<uintptr_t>(L3->w) % 16))

@@ -890,7 +890,16 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
     switch (a.in) {
       case 512: return gemv_n_launch<WT, NCOL, EPI, 1>(a, s);
       case 1536: return gemv_n_launch<WT, NCOL, EPI, 3>(a, s);
-      case 2560: return gemv_n_launch<WT, NCOL, EPI, 5>(a, s);
+      case 2560:
+        // one column, one matrix: whole blocks per CU on 256 CUs (wqkv, 6144
+        // rows: 12 waves, 512 blocks, 7.1 -> 6.6 us; a 4096-row head: 16
+        // waves, 256 blocks, 5.6 -> 5.4 us); w1/w3 keep 8 (4 and 16 waves:
+        // 18.9 and 20.3 us against 16.5)
+        if constexpr (NCOL == 1 && !DUAL) {
+          if (a.out <= 4096) return gemv_n_launch<WT, 1, EPI, 5, true, 16>(a, s);
+          return gemv_n_launch<WT, 1, EPI, 5, true, 12>(a, s);
+        }
+        return gemv_n_launch<WT, NCOL, EPI, 5>(a, s);
       default: break;
     }
   }
@@ -902,7 +911,10 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
     // from L2/L1 were 2x the weight bytes; 2 / 4 waves per block keep 1280 /
     // 640 blocks for the 256 CUs (8 left a quarter of the CUs with two
     // blocks): w2 12.1 -> 10.9 us, wo 6.3 -> 5.9 us
-    case 4096: return gemv_n_launch<WT, NCOL, EPI, 8, false, 2>(a, s);
+    // wo at one column: 10 waves, one 256-block round with x staged 256
+    // times instead of 1280 (5.3 -> 5.0 us); w2 keeps 4 (5 and 10 waves: 10.5
+    // and 10.9 us against 10.3)
+    case 4096: return gemv_n_launch<WT, NCOL, EPI, 8, false, (NCOL == 1 ? 10 : 2)>(a, s);
     case 9728: return gemv_n_launch<WT, NCOL, EPI, 19, false, 4>(a, s);
     default: return hipErrorNotSupported;
   }
@@ -2226,13 +2238,15 @@ uint32_t l2_warm_planes(const L2Warm& w, uint32_t plane, hipError_t* err) {
 }
 
 // The block shapes gemv_k_pick launches (rows per wave x waves per block).
-uint32_t gemv_rows_per_block(uint32_t in, bool norm, bool dual) {
+uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, uint32_t ncol) {
   const uint32_t rs = dual ? 1u : 2u;
   switch (in) {
     case 512:
-    case 1536:
-    case 2560: return norm ? 8u : rs * 4u;
-    case 4096: return norm ? 8u : 2u;
+    case 1536: return norm ? 8u : rs * 4u;
+    case 2560:
+      if (!norm) return rs * 4u;
+      return (ncol == 1 && !dual) ? (out <= 4096 ? 16u : 12u) : 8u;
+    case 4096: return norm ? 8u : (ncol == 1 ? 10u : 2u);
     case 9728: return norm ? 8u : 4u;
     default: return 0u;
   }
