@@ -116,6 +116,7 @@ class Engine {
   void op_attention(const float* q, const float* k, const float* v, uint32_t H, uint32_t Hkv, uint32_t hd,
                     uint32_t T, float scale, float* out);
   void op_swiglu(const float* g, const float* u, size_t n, int fast, float* out);
+  void op_running_sums(const float* terms, size_t n, float* prefix, float* total);
   void op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
                  uint32_t* tok);
   void time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes);
@@ -1525,6 +1526,21 @@ void Engine::op_swiglu(const float* g, const float* u, size_t n, int fast, float
   HIPC(hipStreamSynchronize(stream_));
 }
 
+void Engine::op_running_sums(const float* terms, size_t n, float* prefix, float* total) {
+  select();
+  if (n == 0) {
+    *total = 0.0f;
+    return;
+  }
+  if (n > 8192) fail("running sums support at most 8192 terms on the device");
+  TmpBuf dt(n * 4), dp(n * 4), ds(4);
+  HIPC(hipMemcpyAsync(dt.p, terms, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(launch_running_sum(dt.as<float>(), uint32_t(n), dp.as<float>(), ds.as<float>(), stream_));
+  HIPC(hipMemcpyAsync(prefix, dp.p, n * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(total, ds.p, 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
 void Engine::op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
                        uint32_t* tok) {
   select();
@@ -1924,6 +1940,15 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
     return 0;
   }
   return guarded(err, err_cap, [&] { engine->e->op_sample(logits, n, *smp, always, rng, tok); });
+}
+
+int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,
+                              float* total_out, char* err, size_t err_cap) {
+  if (!engine || (n && (!terms || !prefix_out)) || !total_out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_running_sums(terms, n, prefix_out, total_out); });
 }
 
 int32_t s2hip_time_kernel(s2hip_engine* engine, const char* kernel, uint32_t reps, double* avg_us, double* bytes,

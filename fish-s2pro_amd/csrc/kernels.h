@@ -221,6 +221,8 @@ hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_byte
                                float* out, hipStream_t s);
 
 hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n, int fast, hipStream_t s);
+// Sequential f32 running sums of n <= 8192 terms (the samplers' summation routine).
+hipError_t launch_running_sum(const float* terms, uint32_t n, float* prefix, float* total, hipStream_t s);
 // n_past += n for each of the n_seq sequences not done
 hipError_t launch_add_position(DevState* st, uint32_t n, uint32_t n_seq, hipStream_t s);
 // Plain device copy (bytes and both pointers 16-byte aligned).

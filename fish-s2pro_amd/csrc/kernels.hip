@@ -2185,6 +2185,23 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_plain_kernel(const floa
   }
 }
 
+// Running sums of n <= SAMPLE_MAX terms through seq_chain (the samplers'
+// sequential sums), for the parity test of that routine: terms and sums
+// staged in LDS, one lane adding as the samplers do.
+__global__ __launch_bounds__(WAVE) void running_sum_kernel(const float* terms, uint32_t n, float* prefix,
+                                                              float* total) {
+  __shared__ __align__(16) float t[SAMPLE_MAX];
+  __shared__ __align__(16) float ps[SAMPLE_MAX];
+  for (uint32_t i = threadIdx.x; i < n; i += WAVE) t[i] = terms[i];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t cnt;
+    *total = seq_chain(t, ps, n, false, 0.0f, false, &cnt);
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < n; i += WAVE) prefix[i] = ps[i];
+}
+
 template <uint32_t WT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* w, size_t row_bytes, uint32_t in, float* out) {
   const uint32_t r = blockIdx.x;
@@ -2441,6 +2458,12 @@ hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_byte
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_running_sum(const float* terms, uint32_t n, float* prefix, float* total, hipStream_t s) {
+  if (n == 0 || n > SAMPLE_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(running_sum_kernel, dim3(1), dim3(WAVE), 0, s, terms, n, prefix, total);
   return hipGetLastError();
 }
 

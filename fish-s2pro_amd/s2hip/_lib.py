@@ -112,13 +112,15 @@ def load():
     L.s2hip_op_swiglu.argtypes = [vp, vp, vp, sz, i32, vp, cp, sz]
     L.s2hip_op_sample.argtypes = [vp, vp, sz, ctypes.POINTER(Sampler), ctypes.c_int64, u64p,
                                   ctypes.POINTER(u32), cp, sz]
+    L.s2hip_op_running_sums.argtypes = [vp, vp, sz, vp, ctypes.POINTER(f32), cp, sz]
     L.s2hip_time_kernel.argtypes = [vp, cp, u32, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double), cp, sz]
     for name in ("s2hip_get_spec", "s2hip_reset", "s2hip_eval", "s2hip_fast_logits",
                  "s2hip_fast_codebooks", "s2hip_generate_codes", "s2hip_generate_codes_batch",
                  "s2hip_op_linear",
                  "s2hip_op_rms_norm", "s2hip_op_dequant_rows", "s2hip_op_qk_rope",
-                 "s2hip_op_attention", "s2hip_op_swiglu", "s2hip_op_sample", "s2hip_time_kernel"):
+                 "s2hip_op_attention", "s2hip_op_swiglu", "s2hip_op_sample", "s2hip_op_running_sums",
+                 "s2hip_time_kernel"):
         getattr(L, name).restype = i32
     _lib = L
     return L

@@ -233,6 +233,15 @@ class Engine:
         self._call(self._L.s2hip_op_swiglu, _p(g), _p(u), g.size, 1 if fast else 0, _p(out))
         return out
 
+    def running_sums(self, terms):
+        """Sequential f32 running sums of `terms` on the device (the samplers'
+        summation routine): returns (prefix sums, total)."""
+        t = _f32(terms)
+        out = np.zeros_like(t)
+        total = ctypes.c_float(0)
+        self._call(self._L.s2hip_op_running_sums, _p(t), t.size, _p(out), ctypes.byref(total))
+        return out, total.value
+
     def sample(self, logits, temperature, top_p, top_k, always_include=None, rng_state=0):
         x = _f32(logits)
         smp = _lib.Sampler(temperature, top_p, top_k)

@@ -186,6 +186,14 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
                         int64_t always_include, uint64_t* rng_state, uint32_t* token_out, char* err,
                         size_t err_cap);
 
+/* The samplers' sequential f32 running sums (softmax normaliser, top-p
+ * cumulative sum and draw of sample_token, sampling.rs:202-241, whose Rust
+ * loops add term by term in index order): prefix_out[i] = fl(prefix_out[i-1]
+ * + terms[i]) for n <= 8192 terms, total_out = the last one (0 for n = 0).
+ * A test hook for the device summation routine. */
+int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,
+                              float* total_out, char* err, size_t err_cap);
+
 /* Measurement: average device time of one launch of a named decode kernel,
  * timed with HIP events on the engine stream over `reps` passes across every
  * layer (so no pass re-reads weights from cache).  kernel: "slow_w13",

@@ -140,6 +140,40 @@ def test_swiglu_matches_oracle(eng, fast):
     np.testing.assert_allclose(eng.swiglu(g, u, fast), O.swiglu(g, u, fast), rtol=1e-6, atol=1e-6)
 
 
+def _running_sum_cases():
+    rng = np.random.default_rng(77)
+    cases = []
+    for n in (1, 37, 255, 256, 257, 4096, 8192):
+        lg = rng.standard_normal(n).astype(np.float32)
+        p = np.exp((lg - lg.max()) / np.float32(0.7)).astype(np.float32)
+        cases.append(("softmax_sorted", np.sort(p / p.sum())[::-1].astype(np.float32)))
+        cases.append(("uniform", rng.random(n).astype(np.float32)))
+        cases.append(("wide_exponents", (rng.random(n) * 2.0 ** rng.integers(-149, 20, n)).astype(np.float32)))
+        t = (rng.integers(0, 8, n) * 2.0 ** -25).astype(np.float32)
+        t[0] = 1.0
+        cases.append(("half_ulp_ties", t))
+        z = np.zeros(n, np.float32)
+        z[rng.integers(0, n, 3)] = rng.random(3).astype(np.float32)
+        cases.append(("mostly_zero", z))
+        cases.append(("subnormal", (rng.integers(0, 1 << 20, n) * 2.0 ** -149).astype(np.float32)))
+        cases.append(("growing", (2.0 ** (np.arange(n) % 40) * 1e-30).astype(np.float32)))
+        cases.append(("mixed_sign", rng.standard_normal(n).astype(np.float32)))
+    cases.append(("overflow", np.array([3e38, 3e38, 1.0, 2.0], np.float32)))
+    cases.append(("equal_terms", np.full(8192, 1.0 / 3.0, np.float32)))
+    return cases
+
+
+@pytest.mark.parametrize("name,terms", _running_sum_cases(), ids=lambda v: v if isinstance(v, str) else str(len(v)))
+def test_running_sums_bit_exact(eng, name, terms):
+    # The samplers' sums (sampling.rs:202-241) add term by term in index
+    # order; numpy's add.accumulate in float32 is that sequential loop.
+    want = np.add.accumulate(terms, dtype=np.float32)
+    got, total = eng.running_sums(terms)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (
+        name, int(np.argmax(got.view(np.uint32) != want.view(np.uint32))))
+    assert np.float32(total).view(np.uint32) == want[-1].view(np.uint32)
+
+
 SAMPLER_CASES = [
     (0.0, 1.0, 0), (0.0, 0.9, 0), (0.0, 1.0, 30), (0.7, 0.9, 0), (0.7, 0.7, 30), (1.0, 1.0, 0),
     (0.3, 0.5, 5), (0.7, 1.0, 4096), (1.5, 0.95, 1),
