@@ -72,6 +72,10 @@ struct DevLin {
   // F16 weights in MFMA fragment order for the batched product (built on
   // first use); its rows are the logical rows (any row mapping baked in)
   _Float16* wt = nullptr;
+  // Q8_0 / Q4_0 rows repacked for the one-column decode GEMV (built on
+  // first use): 16-byte-aligned block values and an f16 scale plane
+  uint8_t* qp = nullptr;
+  uint16_t* qs = nullptr;
 };
 
 struct SlowLayer {
@@ -154,6 +158,7 @@ class Engine {
   void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
   void ensure_slots(uint32_t n);
   void ensure_tiled();
+  void repack(DevLin& L);
   void tile(DevLin& L, uint32_t rows, uint32_t row_base, uint32_t extra_row);
   void bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx, const float* norm,
            float eps, float* y, uint32_t ldy, const uint32_t* done, uint32_t* err, uint32_t waves = 0);
@@ -570,6 +575,10 @@ void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, con
     a.y = y + size_t(c) * ldy;
     a.ldy = ldy;
     a.done = done;
+    a.qp = L.qp;
+    a.qs = L.qs;
+    a.qp3 = L3 ? L3->qp : nullptr;
+    a.qs3 = L3 ? L3->qs : nullptr;
     HIPC(launch_gemv(L.type, epi, int(w), a, stream_));
     c += w;
   }
@@ -634,6 +643,7 @@ L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool n
                         uint32_t pct_end) const {
   L2Warm w{};
   if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin || uses_bmm(L, L3, ncol)) return w;
+  if (L.qp && ncol == 1) return w;  // the repacked planes are read, not these rows
   const uint32_t rpb = gemv_rows_per_block(L.in, L.out, norm, L3 != nullptr, ncol);
   const size_t span = size_t(rpb) * L.row_bytes;
   if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||
@@ -1047,6 +1057,15 @@ void Engine::ensure_slots(uint32_t n) {
   ++kv_gen_;
 }
 
+void Engine::repack(DevLin& L) {
+  const uint32_t qb = repack_quant_bytes(L.type);
+  if (!qb || L.in % 32 || L.qp) return;
+  const size_t nblk = size_t(L.in / 32) * L.out;
+  L.qp = dalloc<uint8_t>(nblk * qb);
+  L.qs = dalloc<uint16_t>(nblk);
+  HIPC(launch_repack_q(L.w, L.row_bytes, L.type, L.in, L.out, L.qp, L.qs, stream_));
+}
+
 void Engine::tile(DevLin& L, uint32_t rows, uint32_t row_base, uint32_t extra_row) {
   if (L.type != W_F16 || L.in % 256 || L.in > BMM_MAX_K || L.wt) return;
   L.wt = dalloc<_Float16>(size_t(bmm_rows_pad(rows)) * L.in);
@@ -1054,10 +1073,21 @@ void Engine::tile(DevLin& L, uint32_t rows, uint32_t row_base, uint32_t extra_ro
                        reinterpret_cast<uint16_t*>(L.wt), stream_));
 }
 
-// The batched product's copies of the F16 linears (one more HBM copy of the
-// weights), built once, the first time a decode needs them.
+// The batched product's copies of the F16 linears and the repacked Q8_0 /
+// Q4_0 linears of the one-column GEMV (one more HBM copy of the weights),
+// built once, the first time a decode needs them.
 void Engine::ensure_tiled() {
-  if (tiled_ || !bmm_min_cols_) return;
+  if (tiled_) return;
+  for (auto& L : slow_)
+    for (DevLin* d : {&L.wqkv, &L.wo, &L.w1, &L.w2, &L.w3}) repack(*d);
+  for (auto& L : fast_)
+    for (DevLin* d : {&L.wqkv, &L.wo, &L.w1, &L.w2, &L.w3}) repack(*d);
+  repack(fast_out_);
+  if (!bmm_min_cols_) {
+    HIPC(hipStreamSynchronize(stream_));
+    tiled_ = true;
+    return;
+  }
   for (auto& L : slow_)
     for (DevLin* d : {&L.wqkv, &L.wo, &L.w1, &L.w2, &L.w3}) tile(*d, d->out, 0, NO_ROW);
   for (auto& L : fast_)
@@ -1390,6 +1420,16 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
     HIPC(hipStreamSynchronize(stream_));
     if (herr & ERR_F16_RANGE) fail("activation outside the f16 range of the batched product");
     return;
+  }
+  // quantized rows: the repacked planes that one-column decode GEMVs read
+  std::unique_ptr<TmpBuf> dq, dsc;
+  if (const uint32_t qb = repack_quant_bytes(type); qb && in % 32 == 0) {
+    const size_t nblk = in / 32 * out;
+    dq = std::make_unique<TmpBuf>(nblk * qb);
+    dsc = std::make_unique<TmpBuf>(nblk * 2);
+    L.qp = dq->as<uint8_t>();
+    L.qs = dsc->as<uint16_t>();
+    HIPC(launch_repack_q(L.w, rb, type, uint32_t(in), uint32_t(out), L.qp, L.qs, stream_));
   }
   if (ncol >= 3 && ncol <= 16 && in % 256 == 0)  // batched-decode product (quantized rows)
     mm_skinny(L, nullptr, EPI_STORE, dx.as<float>(), uint32_t(in), nullptr, 0.0f, uint32_t(ncol), dy.as<float>(),

@@ -52,7 +52,21 @@ struct GemvArgs {
   float* y;              // [ncol][ldy]
   uint32_t ldy;
   const uint32_t* done;  // optional early-exit flag
+  // Q8_0 / Q4_0 only, nullable: the rows repacked by launch_repack_q (quant
+  // plane, f16 scale plane); with them, one column runs gemv_q_kernel
+  const uint8_t* qp;
+  const uint8_t* qp3;
+  const uint16_t* qs;
+  const uint16_t* qs3;
 };
+
+// Q8_0 / Q4_0 rows repacked for the decode GEMV: block b of row r (32
+// elements) -> quant plane at (r * in / 32 + b) * QB bytes (QB = 32 for Q8_0:
+// the int8 values; 16 for Q4_0: the 16 nibble bytes, GGML order) and its f16
+// scale at scale plane index r * in / 32 + b.
+uint32_t repack_quant_bytes(uint32_t wtype);  // QB, 0 for other types
+hipError_t launch_repack_q(const uint8_t* rows, size_t row_bytes, uint32_t wtype, uint32_t in, uint32_t nrows,
+                           uint8_t* qplane, uint16_t* splane, hipStream_t s);
 
 struct SamplerCfg {
   float temperature;

@@ -937,6 +937,233 @@ hipError_t gemv_k_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV over repacked Q8_0 / Q4_0 rows (one column).
+//   Lane l of a wave takes whole 32-element blocks b = 64 s + l (s = 0, 1,
+//   ...) of its row: one 16-byte load (two for Q8_0) of the block's values
+//   and one 2-byte scale load, all issued up front.  The block's sum
+//   sum_j q_j x_j (Q4_0: q_j - 8) is taken in f32 and scaled once by d.
+//   x (RMS-normalised when NORM, as in gemv_n_kernel) is staged once per
+//   block in LDS with one spare float per 32 (block b at 33 b), so the
+//   lanes' reads of their blocks fall in distinct banks.  One row (two for
+//   SwiGLU: w1 and w3) per wave.
+// ---------------------------------------------------------------------------
+template <uint32_t WT>
+__device__ __forceinline__ float qblock_dot(const uint4 (&q)[WT == W_Q8_0 ? 2 : 1], const float* xb) {
+  float accb = 0.0f;
+  if constexpr (WT == W_Q8_0) {
+    const uint32_t qw[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        accb = fmaf(float(int8_t((qw[m] >> (8 * i)) & 0xffu)), xb[4 * m + i], accb);
+  } else {
+    const uint32_t qw[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t lo = qw[m] & 0x0f0f0f0fu, hi = (qw[m] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) accb = fmaf(float((lo >> (8 * i)) & 0xffu) - 8.0f, xb[4 * m + i], accb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) accb = fmaf(float((hi >> (8 * i)) & 0xffu) - 8.0f, xb[16 + 4 * m + i], accb);
+    }
+  }
+  return accb;
+}
+
+template <uint32_t WT, int EPI, int KIT, int WPB, bool NORM>
+__global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, const uint8_t* qp3, const uint16_t* qs,
+                                                          const uint16_t* qs3, const float* x_in, const float* gain,
+                                                          const uint32_t* done_ptr, uint32_t out, GemvArgs a) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8, NB = IN / 32, NS = (NB + WAVE - 1) / WAVE;
+  constexpr uint32_t QW = WT == W_Q8_0 ? 2 : 1;  // 16-byte loads per block
+  constexpr int KW = (KIT + WPB - 1) / WPB;
+  __shared__ float xs[NB * 33];
+  __shared__ float red[WPB];
+  const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
+  const uint32_t row = blockIdx.x * WPB + wave;
+
+  // 1. this wave's 512-element steps of x and of the gain
+  float4 xv[KW][2], gv[KW][2];
+#pragma unroll
+  for (int j = 0; j < KW; ++j) {
+    const int k = min(wave + j * WPB, KIT - 1);
+    const uint32_t e = k * 512 + lane * 8;
+    xv[j][0] = *reinterpret_cast<const float4*>(x_in + e);
+    xv[j][1] = *reinterpret_cast<const float4*>(x_in + e + 4);
+    if constexpr (NORM) {
+      gv[j][0] = *reinterpret_cast<const float4*>(gain + e);
+      gv[j][1] = *reinterpret_cast<const float4*>(gain + e + 4);
+    }
+  }
+  // 2. block values and scales of the wave's row (clamped; unused past NB)
+  const uint32_t lr = row < out ? row : out - 1;
+  const uint4* qrow = reinterpret_cast<const uint4*>(qp + size_t(lr) * NB * QW * 16);
+  const uint4* qrow3 = DUAL ? reinterpret_cast<const uint4*>(qp3 + size_t(lr) * NB * QW * 16) : nullptr;
+  uint4 wq[NS][QW], wq3[DUAL ? NS : 1][QW];
+  uint16_t wd[NS], wd3[DUAL ? NS : 1];
+#pragma unroll
+  for (uint32_t st = 0; st < NS; ++st) {
+    const uint32_t b = min(st * WAVE + lane, NB - 1);
+#pragma unroll
+    for (uint32_t j = 0; j < QW; ++j) {
+      wq[st][j] = qrow[b * QW + j];
+      if constexpr (DUAL) wq3[st][j] = qrow3[b * QW + j];
+    }
+    wd[st] = qs[size_t(lr) * NB + b];
+    if constexpr (DUAL) wd3[st] = qs3[size_t(lr) * NB + b];
+  }
+  const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
+  float eps = a.eps;
+  float* ybase = a.y;
+  asm volatile("" : "+s"(eps), "+s"(ybase));
+  // 3. block sum of squares -> scale
+  if constexpr (NORM) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+      if (wave + j * WPB < KIT) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float4 u = xv[j][h];
+          ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+  }
+  // 4. (normalised) x into LDS, element e at e + e / 32
+  float scale = 1.0f;
+  if constexpr (NORM) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WPB; ++i) tot += red[i];
+    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), eps)));
+  }
+#pragma unroll
+  for (int j = 0; j < KW; ++j) {
+    const int k = wave + j * WPB;
+    if (k < KIT) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float4 u = xv[j][h];
+        if constexpr (NORM) {
+          const float4 g = gv[j][h];
+          u.x = __fmul_rn(__fmul_rn(u.x, scale), g.x);
+          u.y = __fmul_rn(__fmul_rn(u.y, scale), g.y);
+          u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
+          u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
+        }
+        const uint32_t e = k * 512 + lane * 8 + 4 * h;
+        float* d = xs + e + e / 32;
+        d[0] = u.x;
+        d[1] = u.y;
+        d[2] = u.z;
+        d[3] = u.w;
+      }
+    }
+  }
+  __syncthreads();
+  if (done) return;
+  // 5. blocks: f32 sum of q_j x_j, scaled by d
+  float acc = 0.0f, acc3 = 0.0f;
+#pragma unroll
+  for (uint32_t st = 0; st < NS; ++st) {
+    const uint32_t b = st * WAVE + lane;
+    const bool live = b < NB;
+    const float* xb = xs + (live ? b : 0u) * 33;
+    const float s1 = fmaf(half_bits_to_float(wd[st]), qblock_dot<WT>(wq[st], xb), acc);
+    acc = live ? s1 : acc;
+    if constexpr (DUAL) {
+      const float s3 = fmaf(half_bits_to_float(wd3[st]), qblock_dot<WT>(wq3[st], xb), acc3);
+      acc3 = live ? s3 : acc3;
+    }
+  }
+  // 6. epilogue (as gemv_n_kernel)
+  const float gsum = wave_sum(acc);
+  float u = 0.0f;
+  if constexpr (DUAL) u = wave_sum(acc3);
+  if (lane == 0 && row < out) {
+    float* dst = ybase + row;
+    if constexpr (EPI == EPI_STORE) {
+      *dst = gsum;
+    } else if constexpr (EPI == EPI_RESID) {
+      *dst = __fadd_rn(*dst, gsum);
+    } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+      const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+      *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
+    } else {
+      *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+    }
+  }
+}
+
+template <uint32_t WT, int EPI, int KIT, int WPB, bool NORM>
+hipError_t gemv_q_launch(const GemvArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((gemv_q_kernel<WT, EPI, KIT, WPB, NORM>), dim3((a.out + WPB - 1) / WPB), dim3(64 * WPB), 0, s,
+                     a.qp, a.qp3, a.qs, a.qs3, a.x, a.norm, a.done, a.out, a);
+  return hipGetLastError();
+}
+
+// Block shapes as the F16 GEMV (whole blocks per CU on the S2-Pro shapes);
+// hipErrorNotSupported for row lengths or epilogues without an instance.
+template <uint32_t WT, int EPI>
+hipError_t gemv_q_pick(const GemvArgs& a, hipStream_t s) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  if (a.norm) {
+    switch (a.in) {
+      case 512: return gemv_q_launch<WT, EPI, 1, 8, true>(a, s);
+      case 1536: return gemv_q_launch<WT, EPI, 3, 8, true>(a, s);
+      case 2560:
+        // 80 blocks per row leave the second lane group a quarter full; one
+        // matrix (wqkv, heads) is faster on the GGUF-layout kernel (Q8_0
+        // wqkv 5.9 against 6.6 us), w1 / w3 share the x reads and gain
+        // (Q8_0 15.4 -> 12.6 us)
+        if constexpr (DUAL) return gemv_q_launch<WT, EPI, 5, 8, true>(a, s);
+        return hipErrorNotSupported;
+      default: return hipErrorNotSupported;
+    }
+  }
+  if constexpr (DUAL) return hipErrorNotSupported;
+  switch (a.in) {
+    case 512: return gemv_q_launch<WT, EPI, 1, 4, false>(a, s);
+    case 1536: return gemv_q_launch<WT, EPI, 3, 4, false>(a, s);
+    case 4096: return gemv_q_launch<WT, EPI, 8, 10, false>(a, s);
+    case 9728: return gemv_q_launch<WT, EPI, 19, 4, false>(a, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+template <uint32_t WT>
+hipError_t gemv_q_epi(int epi, const GemvArgs& a, hipStream_t s) {
+  switch (epi) {
+    case EPI_STORE: return gemv_q_pick<WT, EPI_STORE>(a, s);
+    case EPI_RESID: return gemv_q_pick<WT, EPI_RESID>(a, s);
+    case EPI_SWIGLU_SLOW: return gemv_q_pick<WT, EPI_SWIGLU_SLOW>(a, s);
+    case EPI_SWIGLU_FAST: return gemv_q_pick<WT, EPI_SWIGLU_FAST>(a, s);
+    default: return hipErrorNotSupported;
+  }
+}
+
+// One thread per (row, block): the GGUF block's values and scale into the
+// two planes.
+__global__ __launch_bounds__(256) void repack_q_kernel(const uint8_t* rows, size_t row_bytes, uint32_t wt,
+                                                       uint32_t nb, uint32_t nrows, uint8_t* qplane,
+                                                       uint16_t* splane) {
+  const size_t i = size_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= size_t(nb) * nrows) return;
+  const size_t r = i / nb, b = i % nb;
+  const uint32_t bb = wt == W_Q8_0 ? 34u : 18u, qb = bb - 2u;
+  const uint8_t* blk = rows + r * row_bytes + b * bb;
+  splane[i] = uint16_t(blk[0] | (uint32_t(blk[1]) << 8));
+  uint8_t* dst = qplane + i * qb;
+  for (uint32_t j = 0; j < qb; ++j) dst[j] = blk[2 + j];
+}
+
 bool gemv_k_supported(uint32_t in) { return in == 512 || in == 1536 || in == 2560 || in == 4096 || in == 9728; }
 
 // Warming block r (of w.blocks) at linear grid index L: consumer blocks
@@ -2272,6 +2499,11 @@ uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, ui
 hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
   if (wtype != W_F16 && wtype != W_Q8_0 && wtype != W_Q4_0) return hipErrorInvalidValue;
   if (a.in % (wtype == W_F16 ? 8 : 32)) return hipErrorInvalidValue;
+  if (wtype != W_F16 && ncol == 1 && a.qp && a.qs && a.row_base == 0 && a.extra_row == NO_ROW &&
+      a.ldx % 4 == 0 && !((epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST) && (!a.qp3 || !a.qs3))) {
+    const hipError_t e = wtype == W_Q8_0 ? gemv_q_epi<W_Q8_0>(epi, a, s) : gemv_q_epi<W_Q4_0>(epi, a, s);
+    if (e != hipErrorNotSupported) return e;  // else the GGUF-layout kernels below
+  }
   if (ncol <= 2 && a.ldx % 4 == 0 && gemv_k_supported(a.in)) {
     switch (wtype) {
       case W_F16: return gemv_k_epi<W_F16>(epi, ncol, a, s);
@@ -2458,6 +2690,17 @@ hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_byte
     default:
       return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+uint32_t repack_quant_bytes(uint32_t wtype) { return wtype == W_Q8_0 ? 32u : wtype == W_Q4_0 ? 16u : 0u; }
+
+hipError_t launch_repack_q(const uint8_t* rows, size_t row_bytes, uint32_t wtype, uint32_t in, uint32_t nrows,
+                           uint8_t* qplane, uint16_t* splane, hipStream_t s) {
+  if ((wtype != W_Q8_0 && wtype != W_Q4_0) || in % 32 || nrows == 0) return hipErrorInvalidValue;
+  const size_t n = size_t(in / 32) * nrows;
+  hipLaunchKernelGGL(repack_q_kernel, dim3(uint32_t((n + 255) / 256)), dim3(256), 0, s, rows, row_bytes, wtype,
+                     in / 32, nrows, qplane, splane);
   return hipGetLastError();
 }
 
