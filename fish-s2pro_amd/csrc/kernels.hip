@@ -942,7 +942,8 @@ hipError_t gemv_k_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
 //   Lane l of a wave takes whole 32-element blocks b = 64 s + l (s = 0, 1,
 //   ...) of its row: one 16-byte load (two for Q8_0) of the block's values
 //   and one 2-byte scale load, all issued up front.  The block's sum
-//   sum_j q_j x_j (Q4_0: q_j - 8) is taken in f32 and scaled once by d.
+//   sum_j q_j x_j (Q4_0: q_j - 8) is taken in f32, scaled once by d and
+//   added to the lane's running sum.
 //   x (RMS-normalised when NORM, as in gemv_n_kernel) is staged once per
 //   block in LDS with one spare float per 32 (block b at 33 b), so the
 //   lanes' reads of their blocks fall in distinct banks.  One row (two for
@@ -977,7 +978,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
                                                           const uint16_t* qs3, const float* x_in, const float* gain,
                                                           const uint32_t* done_ptr, uint32_t out, GemvArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
-  constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8, NB = IN / 32, NS = (NB + WAVE - 1) / WAVE;
+  constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8, NB = IN / 32;
   constexpr uint32_t QW = WT == W_Q8_0 ? 2 : 1;  // 16-byte loads per block
   constexpr int KW = (KIT + WPB - 1) / WPB;
   __shared__ float xs[NB * 33];
@@ -998,22 +999,27 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
       gv[j][1] = *reinterpret_cast<const float4*>(gain + e + 4);
     }
   }
-  // 2. block values and scales of the wave's row (clamped; unused past NB)
+  // 2. block values and scales of the wave's row (clamped; unused past the
+  //    end).  SwiGLU rows index w1's and w3's blocks as one list of 2 NB
+  //    (i < NB: w1 block i, else w3 block i - NB), which fills the lanes
+  //    better than two lists of NB (80 blocks per row: 3 groups against 4)
+  constexpr uint32_t NL = DUAL ? 2 * NB : NB, NG = (NL + WAVE - 1) / WAVE;
   const uint32_t lr = row < out ? row : out - 1;
   const uint4* qrow = reinterpret_cast<const uint4*>(qp + size_t(lr) * NB * QW * 16);
-  const uint4* qrow3 = DUAL ? reinterpret_cast<const uint4*>(qp3 + size_t(lr) * NB * QW * 16) : nullptr;
-  uint4 wq[NS][QW], wq3[DUAL ? NS : 1][QW];
-  uint16_t wd[NS], wd3[DUAL ? NS : 1];
+  const uint4* qrow3 = DUAL ? reinterpret_cast<const uint4*>(qp3 + size_t(lr) * NB * QW * 16) : qrow;
+  const uint16_t* srow = qs + size_t(lr) * NB;
+  const uint16_t* srow3 = DUAL ? qs3 + size_t(lr) * NB : srow;
+  uint4 wq[NG][QW];
+  uint16_t wd[NG];
 #pragma unroll
-  for (uint32_t st = 0; st < NS; ++st) {
-    const uint32_t b = min(st * WAVE + lane, NB - 1);
+  for (uint32_t st = 0; st < NG; ++st) {
+    const uint32_t i = min(st * WAVE + lane, NL - 1);
+    const bool second = DUAL && i >= NB;
+    const uint32_t b = second ? i - NB : i;
+    const uint4* src = second ? qrow3 : qrow;
 #pragma unroll
-    for (uint32_t j = 0; j < QW; ++j) {
-      wq[st][j] = qrow[b * QW + j];
-      if constexpr (DUAL) wq3[st][j] = qrow3[b * QW + j];
-    }
-    wd[st] = qs[size_t(lr) * NB + b];
-    if constexpr (DUAL) wd3[st] = qs3[size_t(lr) * NB + b];
+    for (uint32_t j = 0; j < QW; ++j) wq[st][j] = src[b * QW + j];
+    wd[st] = (second ? srow3 : srow)[b];
   }
   const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
   float eps = a.eps;
@@ -1069,19 +1075,17 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
   }
   __syncthreads();
   if (done) return;
-  // 5. blocks: f32 sum of q_j x_j, scaled by d
+  // 5. blocks: f32 sum of q_j x_j, scaled by d, into w1's (acc) or w3's
+  //    (acc3) sum
   float acc = 0.0f, acc3 = 0.0f;
 #pragma unroll
-  for (uint32_t st = 0; st < NS; ++st) {
-    const uint32_t b = st * WAVE + lane;
-    const bool live = b < NB;
-    const float* xb = xs + (live ? b : 0u) * 33;
-    const float s1 = fmaf(half_bits_to_float(wd[st]), qblock_dot<WT>(wq[st], xb), acc);
-    acc = live ? s1 : acc;
-    if constexpr (DUAL) {
-      const float s3 = fmaf(half_bits_to_float(wd3[st]), qblock_dot<WT>(wq3[st], xb), acc3);
-      acc3 = live ? s3 : acc3;
-    }
+  for (uint32_t st = 0; st < NG; ++st) {
+    const uint32_t i = st * WAVE + lane;
+    const bool live = i < NL, second = DUAL && i >= NB;
+    const uint32_t b = live ? (second ? i - NB : i) : 0u;
+    const float v = half_bits_to_float(wd[st]) * qblock_dot<WT>(wq[st], xs + b * 33);
+    acc = (live && !second) ? __fadd_rn(acc, v) : acc;
+    if constexpr (DUAL) acc3 = (live && second) ? __fadd_rn(acc3, v) : acc3;
   }
   // 6. epilogue (as gemv_n_kernel)
   const float gsum = wave_sum(acc);
