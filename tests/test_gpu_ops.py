@@ -47,7 +47,7 @@ def test_dequant_bit_exact(eng, gtype):
 
 
 @pytest.mark.parametrize("gtype,tol", [(1, 1e-2), (8, 2e-2), (2, 2e-2)])
-@pytest.mark.parametrize("in_dim,out_dim,ncol", [(512, 768, 1), (2560, 6144, 1), (9728, 2560, 1),
+@pytest.mark.parametrize("in_dim,out_dim,ncol", [(512, 768, 1), (2560, 6144, 1), (9728, 2560, 1), (4096, 2560, 1),
                                                  (4096, 2560, 2), (2560, 9728, 4), (1536, 100, 3),
                                                  (9728, 2560, 8), (4096, 2560, 16), (512, 1029, 11),
                                                  (1056, 64, 5)])
