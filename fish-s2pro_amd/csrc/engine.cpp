@@ -643,7 +643,7 @@ L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool n
                         uint32_t pct_end) const {
   L2Warm w{};
   if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin || uses_bmm(L, L3, ncol)) return w;
-  if (L.qp && ncol == 1) return w;  // the repacked planes are read, not these rows
+  if (L.qp && ncol <= 2) return w;  // the repacked planes are read, not these rows
   const uint32_t rpb = gemv_rows_per_block(L.in, L.out, norm, L3 != nullptr, ncol);
   const size_t span = size_t(rpb) * L.row_bytes;
   if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||

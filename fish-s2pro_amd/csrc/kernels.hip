@@ -949,31 +949,45 @@ hipError_t gemv_k_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
 //   lanes' reads of their blocks fall in distinct banks.  One row (two for
 //   SwiGLU: w1 and w3) per wave.
 // ---------------------------------------------------------------------------
-template <uint32_t WT>
-__device__ __forceinline__ float qblock_dot(const uint4 (&q)[WT == W_Q8_0 ? 2 : 1], const float* xb) {
-  float accb = 0.0f;
+// sum_j q_j x[c][j] of one block for NC columns (column c's block at
+// xb + c * xstride), each value decoded once
+template <uint32_t WT, int NC>
+__device__ __forceinline__ void qblock_dot(const uint4 (&q)[WT == W_Q8_0 ? 2 : 1], const float* xb, uint32_t xstride,
+                                           float (&accb)[NC]) {
+#pragma unroll
+  for (int c = 0; c < NC; ++c) accb[c] = 0.0f;
   if constexpr (WT == W_Q8_0) {
     const uint32_t qw[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
 #pragma unroll
     for (int m = 0; m < 8; ++m)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        accb = fmaf(float(int8_t((qw[m] >> (8 * i)) & 0xffu)), xb[4 * m + i], accb);
+      for (int i = 0; i < 4; ++i) {
+        const float w = float(int8_t((qw[m] >> (8 * i)) & 0xffu));
+#pragma unroll
+        for (int c = 0; c < NC; ++c) accb[c] = fmaf(w, xb[c * xstride + 4 * m + i], accb[c]);
+      }
   } else {
     const uint32_t qw[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const uint32_t lo = qw[m] & 0x0f0f0f0fu, hi = (qw[m] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) accb = fmaf(float((lo >> (8 * i)) & 0xffu) - 8.0f, xb[4 * m + i], accb);
+      for (int i = 0; i < 4; ++i) {
+        const float w = float((lo >> (8 * i)) & 0xffu) - 8.0f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) accb = fmaf(float((hi >> (8 * i)) & 0xffu) - 8.0f, xb[16 + 4 * m + i], accb);
+        for (int c = 0; c < NC; ++c) accb[c] = fmaf(w, xb[c * xstride + 4 * m + i], accb[c]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float w = float((hi >> (8 * i)) & 0xffu) - 8.0f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) accb[c] = fmaf(w, xb[c * xstride + 16 + 4 * m + i], accb[c]);
+      }
     }
   }
-  return accb;
 }
 
-template <uint32_t WT, int EPI, int KIT, int WPB, bool NORM>
+template <uint32_t WT, int EPI, int KIT, int WPB, bool NORM, int NC = 1>
 __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, const uint8_t* qp3, const uint16_t* qs,
                                                           const uint16_t* qs3, const float* x_in, const float* gain,
                                                           const uint32_t* done_ptr, uint32_t out, GemvArgs a) {
@@ -981,19 +995,23 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8, NB = IN / 32;
   constexpr uint32_t QW = WT == W_Q8_0 ? 2 : 1;  // 16-byte loads per block
   constexpr int KW = (KIT + WPB - 1) / WPB;
-  __shared__ float xs[NB * 33];
-  __shared__ float red[WPB];
+  constexpr uint32_t XS = NB * 33;  // floats per staged column
+  __shared__ float xs[NC * XS];
+  __shared__ float red[NC][WPB];
   const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
   const uint32_t row = blockIdx.x * WPB + wave;
 
-  // 1. this wave's 512-element steps of x and of the gain
-  float4 xv[KW][2], gv[KW][2];
+  // 1. this wave's 512-element steps of x (every column) and of the gain
+  float4 xv[NC][KW][2], gv[KW][2];
 #pragma unroll
   for (int j = 0; j < KW; ++j) {
     const int k = min(wave + j * WPB, KIT - 1);
     const uint32_t e = k * 512 + lane * 8;
-    xv[j][0] = *reinterpret_cast<const float4*>(x_in + e);
-    xv[j][1] = *reinterpret_cast<const float4*>(x_in + e + 4);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      xv[c][j][0] = *reinterpret_cast<const float4*>(x_in + size_t(c) * a.ldx + e);
+      xv[c][j][1] = *reinterpret_cast<const float4*>(x_in + size_t(c) * a.ldx + e + 4);
+    }
     if constexpr (NORM) {
       gv[j][0] = *reinterpret_cast<const float4*>(gain + e);
       gv[j][1] = *reinterpret_cast<const float4*>(gain + e + 4);
@@ -1024,52 +1042,59 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
   const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
   float eps = a.eps;
   float* ybase = a.y;
-  asm volatile("" : "+s"(eps), "+s"(ybase));
-  // 3. block sum of squares -> scale
+  uint32_t ldy = a.ldy;
+  asm volatile("" : "+s"(eps), "+s"(ybase), "+s"(ldy));
+  // 3. block sum of squares -> scale (per column)
   if constexpr (NORM) {
-    float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < KW; ++j) {
-      if (wave + j * WPB < KIT) {
+    for (int c = 0; c < NC; ++c) {
+      float ss = 0.0f;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const float4 u = xv[j][h];
-          ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+      for (int j = 0; j < KW; ++j) {
+        if (wave + j * WPB < KIT) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const float4 u = xv[c][j][h];
+            ss += u.x * u.x + u.y * u.y + u.z * u.z + u.w * u.w;
+          }
         }
       }
+      ss = wave_sum(ss);
+      if (lane == 0) red[c][wave] = ss;
     }
-    ss = wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
     __syncthreads();
   }
-  // 4. (normalised) x into LDS, element e at e + e / 32
-  float scale = 1.0f;
-  if constexpr (NORM) {
-    float tot = 0.0f;
+  // 4. (normalised) x into LDS, element e of column c at c XS + e + e / 32
 #pragma unroll
-    for (int i = 0; i < WPB; ++i) tot += red[i];
-    scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), eps)));
-  }
+  for (int c = 0; c < NC; ++c) {
+    float scale = 1.0f;
+    if constexpr (NORM) {
+      float tot = 0.0f;
 #pragma unroll
-  for (int j = 0; j < KW; ++j) {
-    const int k = wave + j * WPB;
-    if (k < KIT) {
+      for (int i = 0; i < WPB; ++i) tot += red[c][i];
+      scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(IN)), eps)));
+    }
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float4 u = xv[j][h];
-        if constexpr (NORM) {
-          const float4 g = gv[j][h];
-          u.x = __fmul_rn(__fmul_rn(u.x, scale), g.x);
-          u.y = __fmul_rn(__fmul_rn(u.y, scale), g.y);
-          u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
-          u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
+    for (int j = 0; j < KW; ++j) {
+      const int k = wave + j * WPB;
+      if (k < KIT) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float4 u = xv[c][j][h];
+          if constexpr (NORM) {
+            const float4 g = gv[j][h];
+            u.x = __fmul_rn(__fmul_rn(u.x, scale), g.x);
+            u.y = __fmul_rn(__fmul_rn(u.y, scale), g.y);
+            u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
+            u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
+          }
+          const uint32_t e = k * 512 + lane * 8 + 4 * h;
+          float* d = xs + c * XS + e + e / 32;
+          d[0] = u.x;
+          d[1] = u.y;
+          d[2] = u.z;
+          d[3] = u.w;
         }
-        const uint32_t e = k * 512 + lane * 8 + 4 * h;
-        float* d = xs + e + e / 32;
-        d[0] = u.x;
-        d[1] = u.y;
-        d[2] = u.z;
-        d[3] = u.w;
       }
     }
   }
@@ -1077,80 +1102,98 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
   if (done) return;
   // 5. blocks: f32 sum of q_j x_j, scaled by d, into w1's (acc) or w3's
   //    (acc3) sum
-  float acc = 0.0f, acc3 = 0.0f;
+  float acc[NC], acc3[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = acc3[c] = 0.0f;
 #pragma unroll
   for (uint32_t st = 0; st < NG; ++st) {
     const uint32_t i = st * WAVE + lane;
     const bool live = i < NL, second = DUAL && i >= NB;
     const uint32_t b = live ? (second ? i - NB : i) : 0u;
-    const float v = half_bits_to_float(wd[st]) * qblock_dot<WT>(wq[st], xs + b * 33);
-    acc = (live && !second) ? __fadd_rn(acc, v) : acc;
-    if constexpr (DUAL) acc3 = (live && second) ? __fadd_rn(acc3, v) : acc3;
+    const float d = half_bits_to_float(wd[st]);
+    float bs[NC];
+    qblock_dot<WT, NC>(wq[st], xs + b * 33, XS, bs);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const float v = d * bs[c];
+      acc[c] = (live && !second) ? __fadd_rn(acc[c], v) : acc[c];
+      if constexpr (DUAL) acc3[c] = (live && second) ? __fadd_rn(acc3[c], v) : acc3[c];
+    }
   }
   // 6. epilogue (as gemv_n_kernel)
-  const float gsum = wave_sum(acc);
-  float u = 0.0f;
-  if constexpr (DUAL) u = wave_sum(acc3);
-  if (lane == 0 && row < out) {
-    float* dst = ybase + row;
-    if constexpr (EPI == EPI_STORE) {
-      *dst = gsum;
-    } else if constexpr (EPI == EPI_RESID) {
-      *dst = __fadd_rn(*dst, gsum);
-    } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-      const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
-      *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
-    } else {
-      *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float gsum = wave_sum(acc[c]);
+    float u = 0.0f;
+    if constexpr (DUAL) u = wave_sum(acc3[c]);
+    if (lane == 0 && row < out) {
+      float* dst = ybase + size_t(c) * ldy + row;
+      if constexpr (EPI == EPI_STORE) {
+        *dst = gsum;
+      } else if constexpr (EPI == EPI_RESID) {
+        *dst = __fadd_rn(*dst, gsum);
+      } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+        *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
+      } else {
+        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+      }
     }
   }
 }
 
-template <uint32_t WT, int EPI, int KIT, int WPB, bool NORM>
+template <uint32_t WT, int EPI, int KIT, int WPB, bool NORM, int NC = 1>
 hipError_t gemv_q_launch(const GemvArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_q_kernel<WT, EPI, KIT, WPB, NORM>), dim3((a.out + WPB - 1) / WPB), dim3(64 * WPB), 0, s,
-                     a.qp, a.qp3, a.qs, a.qs3, a.x, a.norm, a.done, a.out, a);
+  hipLaunchKernelGGL((gemv_q_kernel<WT, EPI, KIT, WPB, NORM, NC>), dim3((a.out + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                     s, a.qp, a.qp3, a.qs, a.qs3, a.x, a.norm, a.done, a.out, a);
   return hipGetLastError();
 }
 
 // Block shapes as the F16 GEMV (whole blocks per CU on the S2-Pro shapes);
 // hipErrorNotSupported for row lengths or epilogues without an instance.
-template <uint32_t WT, int EPI>
+template <uint32_t WT, int EPI, int NC>
 hipError_t gemv_q_pick(const GemvArgs& a, hipStream_t s) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   if (a.norm) {
     switch (a.in) {
-      case 512: return gemv_q_launch<WT, EPI, 1, 8, true>(a, s);
-      case 1536: return gemv_q_launch<WT, EPI, 3, 8, true>(a, s);
+      case 512: return gemv_q_launch<WT, EPI, 1, 8, true, NC>(a, s);
+      case 1536: return gemv_q_launch<WT, EPI, 3, 8, true, NC>(a, s);
       case 2560:
         // 80 blocks per row leave the second lane group a quarter full; one
         // matrix (wqkv, heads) is faster on the GGUF-layout kernel (Q8_0
         // wqkv 5.9 against 6.6 us), w1 / w3 share the x reads and gain
         // (Q8_0 15.4 -> 12.6 us)
-        if constexpr (DUAL) return gemv_q_launch<WT, EPI, 5, 8, true>(a, s);
+        if constexpr (DUAL) return gemv_q_launch<WT, EPI, 5, 8, true, NC>(a, s);
         return hipErrorNotSupported;
       default: return hipErrorNotSupported;
     }
   }
-  if constexpr (DUAL) return hipErrorNotSupported;
-  switch (a.in) {
-    case 512: return gemv_q_launch<WT, EPI, 1, 4, false>(a, s);
-    case 1536: return gemv_q_launch<WT, EPI, 3, 4, false>(a, s);
-    case 4096: return gemv_q_launch<WT, EPI, 8, 10, false>(a, s);
-    // 4 waves as the F16 w2 (8 and 10 waves: Q4_0 8.1 and 7.5 us, Q8_0 10.1
-    // and 9.3 us, against 7.3 and 8.0)
-    case 9728: return gemv_q_launch<WT, EPI, 19, 4, false>(a, s);
-    default: return hipErrorNotSupported;
+  if constexpr (DUAL) {
+    return hipErrorNotSupported;
+  } else {
+    switch (a.in) {
+      case 512: return gemv_q_launch<WT, EPI, 1, 4, false, NC>(a, s);
+      case 1536: return gemv_q_launch<WT, EPI, 3, 4, false, NC>(a, s);
+      case 4096: return gemv_q_launch<WT, EPI, 8, 10, false, NC>(a, s);
+      // 4 waves as the F16 w2 (8 and 10 waves: Q4_0 8.1 and 7.5 us, Q8_0
+      // 10.1 and 9.3 us, against 7.3 and 8.0).  Two columns of 9728-wide
+      // rows would hold 80 x registers per lane (one wave per SIMD): the
+      // GGUF-layout kernel takes them
+      case 9728:
+        if constexpr (NC == 1) return gemv_q_launch<WT, EPI, 19, 4, false, 1>(a, s);
+        return hipErrorNotSupported;
+      default: return hipErrorNotSupported;
+    }
   }
 }
 
-template <uint32_t WT>
+template <uint32_t WT, int NC>
 hipError_t gemv_q_epi(int epi, const GemvArgs& a, hipStream_t s) {
   switch (epi) {
-    case EPI_STORE: return gemv_q_pick<WT, EPI_STORE>(a, s);
-    case EPI_RESID: return gemv_q_pick<WT, EPI_RESID>(a, s);
-    case EPI_SWIGLU_SLOW: return gemv_q_pick<WT, EPI_SWIGLU_SLOW>(a, s);
-    case EPI_SWIGLU_FAST: return gemv_q_pick<WT, EPI_SWIGLU_FAST>(a, s);
+    case EPI_STORE: return gemv_q_pick<WT, EPI_STORE, NC>(a, s);
+    case EPI_RESID: return gemv_q_pick<WT, EPI_RESID, NC>(a, s);
+    case EPI_SWIGLU_SLOW: return gemv_q_pick<WT, EPI_SWIGLU_SLOW, NC>(a, s);
+    case EPI_SWIGLU_FAST: return gemv_q_pick<WT, EPI_SWIGLU_FAST, NC>(a, s);
     default: return hipErrorNotSupported;
   }
 }
@@ -2505,9 +2548,11 @@ uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, ui
 hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
   if (wtype != W_F16 && wtype != W_Q8_0 && wtype != W_Q4_0) return hipErrorInvalidValue;
   if (a.in % (wtype == W_F16 ? 8 : 32)) return hipErrorInvalidValue;
-  if (wtype != W_F16 && ncol == 1 && a.qp && a.qs && a.row_base == 0 && a.extra_row == NO_ROW &&
+  if (wtype != W_F16 && (ncol == 1 || ncol == 2) && a.qp && a.qs && a.row_base == 0 && a.extra_row == NO_ROW &&
       a.ldx % 4 == 0 && !((epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST) && (!a.qp3 || !a.qs3))) {
-    const hipError_t e = wtype == W_Q8_0 ? gemv_q_epi<W_Q8_0>(epi, a, s) : gemv_q_epi<W_Q4_0>(epi, a, s);
+    const hipError_t e = ncol == 1
+        ? (wtype == W_Q8_0 ? gemv_q_epi<W_Q8_0, 1>(epi, a, s) : gemv_q_epi<W_Q4_0, 1>(epi, a, s))
+        : (wtype == W_Q8_0 ? gemv_q_epi<W_Q8_0, 2>(epi, a, s) : gemv_q_epi<W_Q4_0, 2>(epi, a, s));
     if (e != hipErrorNotSupported) return e;  // else the GGUF-layout kernels below
   }
   if (ncol <= 2 && a.ldx % 4 == 0 && gemv_k_supported(a.in)) {
