@@ -90,3 +90,26 @@ def test_create_rejects_bad_config_without_gpu():
     err = ctypes.create_string_buffer(256)
     assert not L.s2hip_create(None, err, len(err))
     assert b"NULL" in err.value
+
+
+# Algorithmic HBM bytes per launch of each profiled w13 kernel: w1 and w3
+# rows (9728 x 2560 weights each, at 2 B, 34/32 B or 2 B per weight), plus
+# the f32 input and output columns.
+_W13_ALGO_BYTES = {
+    ("slow_w13", "full"): 2 * 9728 * 2560 * 2 + 2560 * 4 + 9728 * 4,
+    ("slow_w13", "full_q8"): 2 * 9728 * 80 * 34 + 2560 * 4 + 9728 * 4,
+    ("slow_w13_b8", "full_b8"): 2 * 9728 * 2560 * 2 + 8 * (2560 + 9728) * 4,
+}
+
+
+@pytest.mark.parametrize("kernel,workload", sorted(_W13_ALGO_BYTES))
+def test_committed_counter_summaries_parse_and_match_algorithmic_bytes(kernel, workload):
+    # bench.py reports FETCH_SIZE + WRITE_SIZE from these summaries as
+    # roofline.traffic; a kernel streaming its weights once reads within a few
+    # percent of its algorithmic bytes
+    import bench
+
+    traffic = bench.counter_traffic(kernel, workload)
+    assert traffic is not None, f"profiles/counters_{kernel}_{workload}.txt missing or malformed"
+    algo = _W13_ALGO_BYTES[(kernel, workload)]
+    assert 0.99 * algo <= traffic <= 1.05 * algo, (traffic, algo)
