@@ -9,6 +9,13 @@ Slow-AR decode step + the Fast-AR's 9 codebook passes + sampling); the timed
 window runs from after prefill to the last frame's codes (HIP events inside
 the library).  Prints one JSON line.
 
+--steps K asks for at least K timed frames: the timed region is the smallest
+number of whole generations of the workload (512 frames for "full") that
+holds K frames, so the workload's frame count and KV length are never
+shortened; "steps" in the output is the number of frames actually timed.
+--warmup W runs the smallest number of untimed generations holding W frames
+(at least one).
+
 Workload "full_b8": the voice-clone batch shape: 8 concurrent requests on
 the same f16 model, each a 1500-position prompt (250 text ids, 1000
 reference frames with uniform random codes, 250 text ids), MFMA prefill,
@@ -91,6 +98,30 @@ def counter_traffic(kernel, workload):
     return got["FETCH_SIZE"] + got["WRITE_SIZE"]
 
 
+def cpu_threads():
+    """Threads for the CPU baseline: the box's CPU share as OMP_NUM_THREADS
+    states it (the reference's Rayon pool defaults to every CPU the process
+    may use), else the CPUs this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(path, shape, threads, prompt_len, frames):
     """The oracle in faithful mode (per-step Slow layer reload + f32 expansion,
     Fast-AR prefix recompute, row-parallel f32 linears) on a bounded sample."""
@@ -108,9 +139,11 @@ def cpu_baseline(path, shape, threads, prompt_len, frames):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="frames in the timed run (default: workload's)")
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed frames at least (whole generations of the workload's frame count)")
+    ap.add_argument("--frames", type=int, default=None, help="frames per generation (default: workload's)")
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: workload's)")
-    ap.add_argument("--warmup", type=int, default=1, help="untimed warm-up generations")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed warm-up frames (whole generations, at least one)")
     ap.add_argument("--workload", default="full", choices=sorted(WORKLOADS))
     ap.add_argument("--model-dir", default=os.environ.get("S2HIP_MODEL_DIR", "/tmp/s2hip_models"))
     ap.add_argument("--no-graph", action="store_true")
@@ -118,7 +151,7 @@ def main():
                     help="Slow-AR KV cache dtype (f32 as the reference; f16 halves KV traffic)")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-frames", type=int, default=2)
-    ap.add_argument("--cpu-prompt", type=int, default=4)
+    ap.add_argument("--cpu-prompt", type=int, default=None, help="CPU baseline prompt tokens (default: workload's)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the dual-AR loop is a single-GPU "
@@ -128,8 +161,10 @@ def main():
     from s2hip import Engine, synth
 
     shape_name, prompt_len, frames, max_seq, temp, top_p, top_k, nseq, ref_frames = WORKLOADS[args.workload]
-    if args.steps:
-        frames = args.steps
+    if args.frames:
+        frames = args.frames
+    timed_gens = max(1, -(-(args.steps or frames) // frames))
+    warm_gens = max(1, -(-args.warmup // frames))
     if args.prompt:
         prompt_len = args.prompt
         ref_frames = min(ref_frames, prompt_len * 2 // 3)  # keep some text ids around the reference frames
@@ -157,18 +192,24 @@ def main():
             rb = eng.generate_codes_batch(prompts, frames, rng_states=[shape.seed + b for b in range(nseq)], **kw)
             return {"n_frames": rb["total_frames"], "prefill_ms": rb["prefill_ms"], "decode_ms": rb["decode_ms"],
                     "graph_used": rb["graph_used"]}
-    for i in range(args.warmup):
+    for i in range(warm_gens):
         r = run()
         log(f"warmup {i}: {r['n_frames']} frames, prefill {r['prefill_ms']:.1f} ms, decode {r['decode_ms']:.1f} ms")
-    r = run()
-    n = r["n_frames"]
-    dec_s = r["decode_ms"] / 1e3
+    n = 0
+    dec_ms = prefill_ms = 0.0
+    for i in range(timed_gens):
+        r = run()
+        n += r["n_frames"]
+        dec_ms += r["decode_ms"]
+        prefill_ms += r["prefill_ms"]
+    dec_s = dec_ms / 1e3
     fps = n / dec_s
-    log(f"timed: {n} frames ({nseq} requests) in {dec_s * 1e3:.1f} ms -> {fps:.1f} frames/s "
-        f"(prefill {r['prefill_ms']:.1f} ms)")
+    log(f"timed: {timed_gens} generation(s), {n} frames ({nseq} requests) in {dec_ms:.1f} ms -> {fps:.1f} frames/s "
+        f"(prefill {prefill_ms / timed_gens:.1f} ms per generation)")
 
-    steps = n // nseq  # decode steps (frames per request)
-    avg_t = prompt_len + steps / 2.0
+    steps = n // nseq  # decode steps timed (frames per request over all timed generations)
+    gen_steps = steps // timed_gens
+    avg_t = prompt_len + gen_steps / 2.0
     fb = frame_bytes(spec, shape, avg_t, kv_bytes=2 if args.kv == "f16" else 4, nseq=nseq)  # bytes per decode step
     kern = "slow_w13" if nseq == 1 else f"slow_w13_b{nseq}"
     us, kb = eng.time_kernel(kern, reps=5)
@@ -189,16 +230,20 @@ def main():
 
     cpu = None
     if args.cpu_baseline:
-        threads = min(16, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)))
-        log(f"cpu baseline: oracle faithful mode, {threads} threads, prompt {args.cpu_prompt}, "
+        threads = cpu_threads()
+        cpu_prompt = args.cpu_prompt or min(prompt_len, 256)
+        model = cpu_model()
+        log(f"cpu baseline: oracle faithful mode, {threads} threads ({model}), prompt {cpu_prompt}, "
             f"{args.cpu_frames} frames")
         t0 = time.time()
-        cfps, cr = cpu_baseline(path, shape, threads, args.cpu_prompt, args.cpu_frames)
-        log(f"cpu baseline {cfps:.4f} frames/s ({time.time() - t0:.1f}s wall)")
+        cfps, cr = cpu_baseline(path, shape, threads, cpu_prompt, args.cpu_frames)
+        log(f"cpu baseline {cfps:.4f} frames/s ({time.time() - t0:.1f}s wall, prefill {cr['prefill_seconds']:.1f}s)")
         cpu = {"value": round(cfps, 5), "unit": "frames/s", "cores": threads, "kind": "port",
-               "sample": f"{shape_name} model, {args.cpu_prompt}-token prompt, {cr['n_frames']} greedy frames "
-                         f"after prefill; faithful mode (Slow layers re-read + expanded to f32 every step, "
-                         f"Fast-AR prefix recompute)"}
+               "cpu_model": model,
+               "sample": f"{shape_name} model, {cpu_prompt}-token prompt, {cr['n_frames']} greedy frames "
+                         f"after prefill (frames timed; prefill {cr['prefill_seconds']:.1f} s untimed); "
+                         f"faithful mode (Slow layers re-read + expanded to f32 every step, Fast-AR prefix "
+                         f"recompute), one row-parallel thread pool"}
 
     out = {
         "metric": "audio frames/sec (Slow+Fast AR) batch-1 f16; % of HBM roofline",
@@ -208,19 +253,21 @@ def main():
         "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(dec_s * 1e3 / max(1, steps), 4),
+        "timed_generations": timed_gens,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": {1: "f16", 8: "q8_0", 2: "q4_0"}[spec["linear_type"]] + " weights, f32 accumulate",
         "data": "synthetic (random-init N(0,0.02) weights, uniform random prompt ids)",
         "config": {"workload": f"{args.workload}: {spec['slow_layers']}+{spec['fast_layers']} layers d={spec['dim']}, "
-                               f"{nseq} x {prompt_len}-token prompt, {steps} frames per request, KV {max_seq}",
+                               f"{nseq} x {prompt_len}-token prompt, {gen_steps} frames per request, KV {max_seq}",
                    "requests": nseq, "prompt_tokens": prompt_len, "reference_frames": ref_frames,
-                   "frames": steps, "kv_cache": max_seq, "kv_dtype": args.kv, "sampler":
+                   "frames": gen_steps, "kv_cache": max_seq, "kv_dtype": args.kv, "sampler":
                        {"temperature": temp, "top_p": top_p, "top_k": top_k}, "parallelism": "single GPU"},
         "codes_per_s": round(fps * spec["num_codebooks"], 1),
-        "prefill_ms": round(r["prefill_ms"], 2),
-        "prefill_tflops": round(prefill_flops(spec, shape, prompt_len, nseq) / (r["prefill_ms"] * 1e-3) / 1e12, 2),
+        "prefill_ms": round(prefill_ms / timed_gens, 2),
+        "prefill_tflops": round(prefill_flops(spec, shape, prompt_len, nseq) / (prefill_ms / timed_gens * 1e-3) / 1e12,
+                                2),
         "frame_bytes": round(fb),
         "frame_roofline_frac": round(fb * (steps / dec_s) / (HBM_PEAK_GBS * 1e9), 4),
         "roofline": {"bound": "hbm", "kernel": (f"gemv {kern}" if nseq == 1 else f"batched MFMA product {kern}") +

@@ -14,20 +14,26 @@
 // contiguous bytes per row and chunk of 4 steps, issued one chunk ahead), so
 // the activation loads neither scatter over rows (the MFMA fragment puts the
 // column in the fastest lane bits) nor hold up the weight loads' wait
-// counter.  Each lane then splits its 8 elements per step into f16 hi =
-// f16(x) and lo = f16((x - hi) 2^11) (x = hi + 2^-11 lo to ~2^-22 |x| for
-// |x| >= 2^-14, absolute ~2^-35 below); hi and lo go through the MFMA with
-// the same weight fragment into two accumulators.  RMSNorm inputs: the sum
-// of squares of each column is accumulated from the same values and the RMS
-// scale is applied to the result (W.((x s) g) = s W.(x g)).  A value beyond
-// the f16 range makes its column's sums non-finite; the epilogue reports
-// that as ERR_F16_RANGE instead of returning a wrong product.
+// counter.  Each lane then splits its 8 elements per step into three f16
+// parts, x = 2^16 t + m + 2^-11 l:
+//   t = f16(2^-16 x), m = f16(x - 2^16 t), l = f16(2^11 (x - 2^16 t - m))
+// (both differences are exact in f32), and the three go through the MFMA
+// with the same weight fragment into three accumulators.  The split carries
+// x to ~2^-22 relative for |x| >= 2^-14 (~2^-35 absolute below) for every
+// |x| up to ~1.3e8 with no per-column scale pass: t takes the magnitude of
+// large activations (a raw pre-norm residual of 1e5 and more), m and l stay
+// inside the f16 range.  RMSNorm inputs: the sum of squares of each column
+// is accumulated from the same values and the RMS scale is applied to the
+// result (W.((x s) g) = s W.(x g)).  A non-finite activation (or one beyond
+// the split's range) makes its column's sums non-finite; the epilogue
+// reports that as ERR_F16_RANGE instead of returning a wrong product.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
 #include <algorithm>
 #include <type_traits>
 
+#include "expf_glibc.h"
 #include "kernels.h"
 
 namespace s2 {
@@ -69,13 +75,18 @@ constexpr int WIN = 8;        // weight steps in flight (two chunks)
 constexpr int XC = 4;         // steps per staged activation chunk
 constexpr int RS = 36;        // LDS floats per staged row and step (32 + 4: conflict-free fragment reads)
 
-__device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8& hi, half8& lo) {
+// x = 2^16 t + m + 2^-11 l (see the file comment); fmaf(-t, 2^16, x) and
+// r - m are exact, so the parts differ from x only by the rounding of l.
+__device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8& top, half8& hi, half8& lo) {
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const _Float16 h = _Float16(v[e]);
+    const _Float16 t = _Float16(v[e] * (1.0f / 65536.0f));
+    const float r = fmaf(-float(t), 65536.0f, v[e]);
+    const _Float16 h = _Float16(r);
+    top[e] = t;
     hi[e] = h;
-    lo[e] = _Float16((v[e] - float(h)) * 2048.0f);
+    lo[e] = _Float16((r - float(h)) * 2048.0f);
   }
 }
 
@@ -99,9 +110,11 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   constexpr int NW = DUAL ? 2 : 1;
   constexpr int CHF = XC * NB * RS;  // floats per chunk buffer
   constexpr int LDX = NB / 2;        // staging loads per chunk (2 rows x 512 B each)
-  __shared__ float xs[WAVES][2][CHF];
+  // each wave's staging buffers take its partial sums after its loop (3 NW x
+  // 64 floatx4 = at most 6 KiB, inside the 2 CHF floats of the wave)
+  static_assert(3 * NW * 64 * 4 <= 2 * CHF, "partials must fit the staging buffers");
+  __shared__ __align__(16) float xs[WAVES][2][CHF];
   __shared__ float gs[WAVES][2][NORM ? XC * 32 : 1];
-  __shared__ floatx4 red[WAVES][2 * NW][64];
   __shared__ float ssq[WAVES][64];
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t tm = blockIdx.x, m0 = tm * 16;
@@ -157,11 +170,12 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   stage_store(sxa, sga, 0);
   __builtin_amdgcn_sched_barrier(0);
 
-  floatx4 acc[NW], accl[NW];
+  floatx4 acc[NW], accl[NW], acct[NW];
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
     acc[m] = floatx4{};
     accl[m] = floatx4{};
+    acct[m] = floatx4{};
   }
   float ss = 0.0f;
   const floatx4 z4 = floatx4{};
@@ -200,10 +214,11 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
         x0 = x0 * cg0;
         x1 = x1 * cg1;
       }
-      half8 bh, bl;
-      split8(x0, x1, bh, bl);
+      half8 bt, bh, bl;
+      split8(x0, x1, bt, bh, bl);
 #pragma unroll
       for (int m = 0; m < NW; ++m) {
+        acct[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bt, acct[m], 0, 0, 0);
         acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bh, acc[m], 0, 0, 0);
         accl[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bl, accl[m], 0, 0, 0);
       }
@@ -231,23 +246,29 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     chunk_steps(2 * sc + 1, std::integral_constant<int, 1>{});
   }
+  // partials of wave w: slot (3 m + part) lane of its own staging region
+  auto red = [&](uint32_t w, int slot) __attribute__((always_inline)) -> floatx4* {
+    return reinterpret_cast<floatx4*>(&xs[w][0][0]) + slot * 64 + lane;
+  };
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
-    red[wave][2 * m][lane] = acc[m];
-    red[wave][2 * m + 1][lane] = accl[m];
+    *red(wave, 3 * m) = acc[m];
+    *red(wave, 3 * m + 1) = accl[m];
+    *red(wave, 3 * m + 2) = acct[m];
   }
   if constexpr (NORM) ssq[wave][lane] = ss;
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
-    floatx4 t = red[0][2 * m][lane], tl = red[0][2 * m + 1][lane];
+    floatx4 t = *red(0, 3 * m), tl = *red(0, 3 * m + 1), tt = *red(0, 3 * m + 2);
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
-      t += red[w][2 * m][lane];
-      tl += red[w][2 * m + 1][lane];
+      t += *red(w, 3 * m);
+      tl += *red(w, 3 * m + 1);
+      tt += *red(w, 3 * m + 2);
     }
-    acc[m] = t + tl * (1.0f / 2048.0f);
+    acc[m] = (t + tl * (1.0f / 2048.0f)) + tt * 65536.0f;
   }
   float r = 1.0f;
   if constexpr (NORM) {
@@ -259,7 +280,8 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     t = t + __shfl_xor(t, 32, 64);
     r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(t, float(a.K)), a.eps)));
   }
-  // an activation beyond the f16 range (or NaN) leaves non-finite sums
+  // a non-finite activation (or one beyond the split's range) leaves
+  // non-finite sums
   bool bad = false;
 #pragma unroll
   for (int m = 0; m < NW; ++m)
@@ -282,10 +304,10 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     } else {
       const float u = acc[NW - 1][v] * r;
       if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-g)));
         yrow[m] = __fmul_rn(__fmul_rn(g, sig), u);
       } else {
-        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_glibc(-g))), u);
       }
     }
   }

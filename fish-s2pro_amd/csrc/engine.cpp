@@ -23,6 +23,7 @@
 #include <string>
 #include <vector>
 
+#include "expf_glibc.h"
 #include "gguf.h"
 #include "kernels.h"
 #include "s2hip.h"
@@ -121,6 +122,7 @@ class Engine {
                     uint32_t T, float scale, float* out);
   void op_swiglu(const float* g, const float* u, size_t n, int fast, float* out);
   void op_running_sums(const float* terms, size_t n, float* prefix, float* total);
+  void op_expf(const float* x, size_t n, float* y);
   void op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
                  uint32_t* tok);
   void time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes);
@@ -257,6 +259,9 @@ Engine::Engine(const s2hip_config& cfg) {
   flags_ = cfg.flags;
   kv_f16_ = (cfg.flags & S2HIP_FLAG_KV_F16) ? 1u : 0u;
   im_end_ = cfg.im_end_id;
+  // the file is parsed and validated (host only) before any device resource is taken
+  GgufFile g;
+  g.open(cfg.gguf_path);
   int ndev = 0;
   HIPC(hipGetDeviceCount(&ndev));
   if (device < 0 || device >= ndev) fail("HIP device " + std::to_string(device) + " not present");
@@ -267,8 +272,6 @@ Engine::Engine(const s2hip_config& cfg) {
     HIPC(hipEventCreateWithFlags(&staging_ev_[i], hipEventDisableTiming));
   }
 
-  GgufFile g;
-  g.open(cfg.gguf_path);
   // DualArGraphSpec::from_gguf (crates/fish_s2_infer/src/registry.rs:45-214), shape-generic.
   if (g.str("general.architecture") != "fish-speech")
     fail("expected fish-speech transformer GGUF, got " + g.str("general.architecture"));
@@ -1104,7 +1107,7 @@ void Engine::check_state_err(uint32_t nseq) {
     if (st_host_[b].err & ERR_TOKEN_RANGE) fail("token id out of range" + who);
     if (st_host_[b].err & ERR_KV_OVERFLOW) fail("KV cache overflow" + who);
     if (st_host_[b].err & ERR_SAMPLER) fail("sampler failure" + who);
-    if (st_host_[b].err & ERR_F16_RANGE) fail("activation outside the f16 range of the batched product");
+    if (st_host_[b].err & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product (|x| < 1.3e8)");
   }
 }
 
@@ -1418,7 +1421,7 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
     HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipMemcpyAsync(&herr, derr.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
-    if (herr & ERR_F16_RANGE) fail("activation outside the f16 range of the batched product");
+    if (herr & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product (|x| < 1.3e8)");
     return;
   }
   // quantized rows: the repacked planes that one-column decode GEMVs read
@@ -1578,6 +1581,16 @@ void Engine::op_running_sums(const float* terms, size_t n, float* prefix, float*
   HIPC(launch_running_sum(dt.as<float>(), uint32_t(n), dp.as<float>(), ds.as<float>(), stream_));
   HIPC(hipMemcpyAsync(prefix, dp.p, n * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipMemcpyAsync(total, ds.p, 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_expf(const float* x, size_t n, float* y) {
+  select();
+  if (n == 0) return;
+  TmpBuf dx(n * 4), dy(n * 4);
+  HIPC(hipMemcpyAsync(dx.p, x, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(launch_expf(dx.as<float>(), dy.as<float>(), n, stream_));
+  HIPC(hipMemcpyAsync(y, dy.p, n * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
 }
 
@@ -1989,6 +2002,18 @@ int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n
     return 0;
   }
   return guarded(err, err_cap, [&] { engine->e->op_running_sums(terms, n, prefix_out, total_out); });
+}
+
+int32_t s2hip_op_expf(s2hip_engine* engine, const float* x, size_t n, float* y, char* err, size_t err_cap) {
+  if (!engine || (n && (!x || !y))) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_expf(x, n, y); });
+}
+
+void s2hip_expf_host(const float* x, size_t n, float* y) {
+  for (size_t i = 0; i < n; ++i) y[i] = s2::expf_glibc(x[i]);
 }
 
 int32_t s2hip_time_kernel(s2hip_engine* engine, const char* kernel, uint32_t reps, double* avg_us, double* bytes,

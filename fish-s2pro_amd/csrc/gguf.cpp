@@ -6,6 +6,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cstdint>
 #include <cstring>
 #include <stdexcept>
 
@@ -55,6 +56,7 @@ struct Cursor {
 
 // GgmlType::byte_len (crates/fish_s2_core/src/gguf.rs:233-258)
 uint64_t type_bytes(uint32_t type, uint64_t n) {
+  if (n > UINT64_MAX / 8) bad("tensor byte length overflows");
   switch (type) {
     case 0: case 18: return n * 4;
     case 1: case 17: case 30: return n * 2;
@@ -72,9 +74,14 @@ uint64_t type_bytes(uint32_t type, uint64_t n) {
 
 }  // namespace
 
+// Element counts and byte ranges are checked for overflow, as the reference
+// does with checked_mul / checked_add (crates/fish_s2_core/src/gguf.rs:161,
+// 254, 351): a malformed header fails with the tensor's name instead of
+// wrapping into an in-range offset.
 uint64_t GgufTensor::elements() const {
   uint64_t n = 1;
-  for (uint64_t d : dims) n *= d;
+  for (uint64_t d : dims)
+    if (__builtin_mul_overflow(n, d, &n)) bad("tensor " + name + ": element count overflows");
   return n;
 }
 
@@ -147,8 +154,8 @@ void GgufFile::open(const std::string& path) {
   const uint64_t data_start = (uint64_t(c.p - map_) + 31) / 32 * 32;
   for (GgufTensor& t : tensors_) {
     t.bytes = type_bytes(t.type, t.elements());
-    t.offset += data_start;
-    if (t.offset + t.bytes > size_) bad("tensor " + t.name + " extends past file end");
+    if (__builtin_add_overflow(t.offset, data_start, &t.offset) || t.offset > size_ || t.bytes > size_ - t.offset)
+      bad("tensor " + t.name + " extends past file end");
     t.data = map_ + t.offset;
   }
 }

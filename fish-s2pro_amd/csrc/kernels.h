@@ -235,6 +235,8 @@ hipError_t launch_dequant_rows(uint32_t wtype, const uint8_t* w, size_t row_byte
                                float* out, hipStream_t s);
 
 hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n, int fast, hipStream_t s);
+// y[i] = expf_glibc(x[i]) (the device exp of the samplers and SwiGLU epilogues).
+hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
 // Sequential f32 running sums of n <= 8192 terms (the samplers' summation routine).
 hipError_t launch_running_sum(const float* terms, uint32_t n, float* prefix, float* total, hipStream_t s);
 // n_past += n for each of the n_seq sequences not done
@@ -296,7 +298,8 @@ hipError_t launch_tile_f16(const uint16_t* src, uint32_t K, uint32_t M, uint32_t
                            uint16_t* dst, hipStream_t s);
 // y[n][m] (op)= sum_k W[m][k] xn[n][k] for n < N <= 16, m < M; xn = x, or
 // RMSNorm(x) with gain `norm`; epilogues as for launch_gemv.  K % 256 == 0.
-// Activations beyond the f16 range (or NaN) set ERR_F16_RANGE in *err.
+// Activations are split into three f16 parts (any |x| < ~1.3e8 keeps
+// ~2^-22 relative accuracy); a non-finite one sets ERR_F16_RANGE in *err.
 struct BmmArgs {
   const _Float16* wt;
   const _Float16* wt3;   // second matrix for SwiGLU epilogues

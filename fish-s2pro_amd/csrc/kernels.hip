@@ -11,6 +11,7 @@
 
 #include <type_traits>
 
+#include "expf_glibc.h"
 #include "kernels.h"
 
 namespace s2 {
@@ -39,10 +40,6 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
-
-// Correctly rounded (in all but vanishingly rare double-rounding cases) expf:
-// exp evaluated in double, rounded once to float.
-__device__ __forceinline__ float expf_cr(float x) { return static_cast<float>(exp(static_cast<double>(x))); }
 
 // A zero word in device memory: optional state pointers are read through
 // `opt_word`, which selects the address instead of branching, so the load
@@ -278,10 +275,10 @@ __global__ __launch_bounds__(GEMV_THREADS) void gemv_kernel(GemvArgs a) {
         } else if constexpr (EPI == EPI_RESID) {
           *dst = __fadd_rn(*dst, g);
         } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-g)));
           *dst = __fmul_rn(__fmul_rn(g, sig), u);
         } else {
-          *dst = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+          *dst = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_glibc(-g))), u);
         }
       }
     }
@@ -514,10 +511,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_direct_kernel(GemvArgs a) {
         } else if constexpr (EPI == EPI_RESID) {
           *dst = __fadd_rn(*dst, gsum);
         } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
           *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
         } else {
-          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
         }
       }
     }
@@ -697,10 +694,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_k_kernel(GemvArgs a) {
         } else if constexpr (EPI == EPI_RESID) {
           *dst = __fadd_rn(*dst, gsum);
         } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
           *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
         } else {
-          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
         }
       }
     }
@@ -862,10 +859,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
       } else if constexpr (EPI == EPI_RESID) {
         *dst = __fadd_rn(*dst, gsum);
       } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
         *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
       } else {
-        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
       }
     }
   }
@@ -1133,10 +1130,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
       } else if constexpr (EPI == EPI_RESID) {
         *dst = __fadd_rn(*dst, gsum);
       } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gsum)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
         *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
       } else {
-        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf(-gsum))), u);
+        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
       }
     }
   }
@@ -2184,7 +2181,7 @@ __device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float
     const float v = key_value((appended && i == n_top) ? kf : sh.skey[i]);
     float p;
     if (cfg.temperature > 0.0f)
-      p = expf_cr(__fdiv_rn(__fsub_rn(v, vmax), cfg.temperature));
+      p = expf_glibc(__fdiv_rn(__fsub_rn(v, vmax), cfg.temperature));
     else
       p = fabsf(__fsub_rn(v, vmax)) < 1e-6f ? 1.0f : 0.0f;
     sh.probs[i] = p;
@@ -2478,6 +2475,12 @@ __global__ __launch_bounds__(WAVE) void running_sum_kernel(const float* terms, u
   for (uint32_t i = threadIdx.x; i < n; i += WAVE) prefix[i] = ps[i];
 }
 
+// expf_glibc over n inputs: the test hook of the device exp used by the
+// samplers' softmax and the SwiGLU sigmoids.
+__global__ __launch_bounds__(256) void expf_kernel(const float* x, float* y, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) y[i] = expf_glibc(x[i]);
+}
+
 template <uint32_t WT>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* w, size_t row_bytes, uint32_t in, float* out) {
   const uint32_t r = blockIdx.x;
@@ -2494,9 +2497,9 @@ __global__ void swiglu_kernel(const float* g, const float* u, float* out, uint32
   if (i >= n) return;
   const float gv = g[i];
   if (fast)
-    out[i] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf(-gv))), u[i]);
+    out[i] = __fmul_rn(__fdiv_rn(gv, __fadd_rn(1.0f, expf_glibc(-gv))), u[i]);
   else
-    out[i] = __fmul_rn(__fmul_rn(gv, __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-gv)))), u[i]);
+    out[i] = __fmul_rn(__fmul_rn(gv, __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gv)))), u[i]);
 }
 
 __global__ void add_position_kernel(DevState* st, uint32_t n, uint32_t n_seq) {
@@ -2758,6 +2761,13 @@ hipError_t launch_repack_q(const uint8_t* rows, size_t row_bytes, uint32_t wtype
 hipError_t launch_running_sum(const float* terms, uint32_t n, float* prefix, float* total, hipStream_t s) {
   if (n == 0 || n > SAMPLE_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(running_sum_kernel, dim3(1), dim3(WAVE), 0, s, terms, n, prefix, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+  hipLaunchKernelGGL(expf_kernel, dim3(uint32_t(blocks)), dim3(256), 0, s, x, y, n);
   return hipGetLastError();
 }
 

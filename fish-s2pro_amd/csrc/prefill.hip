@@ -18,6 +18,7 @@
 
 #include <type_traits>
 
+#include "expf_glibc.h"
 #include "kernels.h"
 
 namespace s2 {
@@ -235,10 +236,10 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
       if constexpr (WSPLIT) u = u + accl[NW - 1][v] * (1.0f / 2048.0f);
       u *= r;
       if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-g)));
         yrow[m] = __fmul_rn(__fmul_rn(g, sig), u);
       } else {
-        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_glibc(-g))), u);
       }
     }
   }
@@ -355,10 +356,10 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_mfma_kernel(SkinnyArgs a
       if constexpr (WSPLIT) u = u + accl[NW - 1][v] * (1.0f / 2048.0f);
       u *= r;
       if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-g)));
         yrow[m] = __fmul_rn(__fmul_rn(g, sig), u);
       } else {
-        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_glibc(-g))), u);
       }
     }
   }

@@ -86,7 +86,7 @@ struct Tensor {
   std::string name;
   std::vector<uint64_t> dims;  // ne0 (contiguous) first
   uint32_t type;               // 1 F16, 2 Q4_0, 8 Q8_0
-  bool ones;                   // RMSNorm gain
+  uint16_t fill;               // RMSNorm gain: every element this f16 value (0: random weights)
   uint64_t offset = 0;
   uint64_t bytes = 0;
 };
@@ -196,7 +196,7 @@ void fill_rows(const Tensor& t, uint64_t tkey, double stdv, uint64_t r0, uint64_
     uint8_t* out = dst + (r - r0) * rb;
     if (t.type == 1) {
       uint16_t* o = reinterpret_cast<uint16_t*>(out);
-      for (uint64_t i = 0; i < in; ++i) o[i] = t.ones ? uint16_t(0x3c00u) : weight_half(tkey, r * in + i, stdv);
+      for (uint64_t i = 0; i < in; ++i) o[i] = t.fill ? t.fill : weight_half(tkey, r * in + i, stdv);
       continue;
     }
     for (uint64_t i = 0; i < in; ++i) row[i] = from_half(weight_half(tkey, r * in + i, stdv));
@@ -222,37 +222,39 @@ void write_gguf(const char* path, const s2synth_config& c, unsigned threads) {
   const uint64_t q = uint64_t(c.heads) * c.head_dim, kv = uint64_t(c.kv_heads) * c.head_dim;
   const uint64_t fq = uint64_t(c.fast_heads) * c.fast_head_dim, fkv = uint64_t(c.fast_kv_heads) * c.fast_head_dim;
   std::vector<Tensor> ts;
-  auto add = [&](const std::string& n, std::vector<uint64_t> dims, uint32_t type, bool ones) {
-    ts.push_back(Tensor{n, dims, type, ones});
+  // gains: 0 = random weights, 1 = unit gain (QK-norm), 2 = the residual-stream gain
+  const uint16_t gain_bits = to_half(c.norm_gain != 0.0f ? c.norm_gain : 1.0f);
+  auto add = [&](const std::string& n, std::vector<uint64_t> dims, uint32_t type, int gain) {
+    ts.push_back(Tensor{n, dims, type, uint16_t(gain == 0 ? 0u : gain == 1 ? 0x3c00u : gain_bits)});
   };
   const uint32_t lt = c.linear_type;
-  add("embeddings.weight", {d, c.vocab}, 1, false);
-  add("codebook_embeddings.weight", {d, uint64_t(c.codebook_size) * c.num_codebooks}, 1, false);
-  add("norm.weight", {d}, 1, true);
-  add("fast_embeddings.weight", {d, c.codebook_size}, 1, false);
-  add("fast_norm.weight", {d}, 1, true);
-  add("fast_output.weight", {d, c.codebook_size}, lt, false);
+  add("embeddings.weight", {d, c.vocab}, 1, 0);
+  add("codebook_embeddings.weight", {d, uint64_t(c.codebook_size) * c.num_codebooks}, 1, 0);
+  add("norm.weight", {d}, 1, 2);
+  add("fast_embeddings.weight", {d, c.codebook_size}, 1, 0);
+  add("fast_norm.weight", {d}, 1, 2);
+  add("fast_output.weight", {d, c.codebook_size}, lt, 0);
   for (uint32_t l = 0; l < c.slow_layers; ++l) {
     const std::string p = "layers." + std::to_string(l) + ".";
-    add(p + "attention_norm.weight", {d}, 1, true);
-    add(p + "attention.q_norm.weight", {c.head_dim}, 1, true);
-    add(p + "attention.k_norm.weight", {c.head_dim}, 1, true);
-    add(p + "attention.wqkv.weight", {d, q + 2 * kv}, lt, false);
-    add(p + "attention.wo.weight", {q, d}, lt, false);
-    add(p + "ffn_norm.weight", {d}, 1, true);
-    add(p + "feed_forward.w1.weight", {d, c.ffn}, lt, false);
-    add(p + "feed_forward.w2.weight", {c.ffn, d}, lt, false);
-    add(p + "feed_forward.w3.weight", {d, c.ffn}, lt, false);
+    add(p + "attention_norm.weight", {d}, 1, 2);
+    add(p + "attention.q_norm.weight", {c.head_dim}, 1, 1);
+    add(p + "attention.k_norm.weight", {c.head_dim}, 1, 1);
+    add(p + "attention.wqkv.weight", {d, q + 2 * kv}, lt, 0);
+    add(p + "attention.wo.weight", {q, d}, lt, 0);
+    add(p + "ffn_norm.weight", {d}, 1, 2);
+    add(p + "feed_forward.w1.weight", {d, c.ffn}, lt, 0);
+    add(p + "feed_forward.w2.weight", {c.ffn, d}, lt, 0);
+    add(p + "feed_forward.w3.weight", {d, c.ffn}, lt, 0);
   }
   for (uint32_t l = 0; l < c.fast_layers; ++l) {
     const std::string p = "fast_layers." + std::to_string(l) + ".";
-    add(p + "attention_norm.weight", {d}, 1, true);
-    add(p + "attention.wqkv.weight", {d, fq + 2 * fkv}, lt, false);
-    add(p + "attention.wo.weight", {fq, d}, lt, false);
-    add(p + "ffn_norm.weight", {d}, 1, true);
-    add(p + "feed_forward.w1.weight", {d, c.fast_ffn}, lt, false);
-    add(p + "feed_forward.w2.weight", {c.fast_ffn, d}, lt, false);
-    add(p + "feed_forward.w3.weight", {d, c.fast_ffn}, lt, false);
+    add(p + "attention_norm.weight", {d}, 1, 2);
+    add(p + "attention.wqkv.weight", {d, fq + 2 * fkv}, lt, 0);
+    add(p + "attention.wo.weight", {fq, d}, lt, 0);
+    add(p + "ffn_norm.weight", {d}, 1, 2);
+    add(p + "feed_forward.w1.weight", {d, c.fast_ffn}, lt, 0);
+    add(p + "feed_forward.w2.weight", {c.fast_ffn, d}, lt, 0);
+    add(p + "feed_forward.w3.weight", {d, c.fast_ffn}, lt, 0);
   }
   uint64_t off = 0;
   for (Tensor& t : ts) {

@@ -17,6 +17,7 @@ typedef struct {
   uint32_t linear_type; /* GGML type of every linear weight: 1 F16, 8 Q8_0, 2 Q4_0 */
   float rope_base, fast_rope_base, eps, fast_eps;
   float init_std;
+  float norm_gain; /* value of every residual-stream RMSNorm gain (attention/ffn/final norms); 0 means 1 */
   uint64_t seed;
 } s2synth_config;
 

@@ -113,6 +113,9 @@ def load():
     L.s2hip_op_sample.argtypes = [vp, vp, sz, ctypes.POINTER(Sampler), ctypes.c_int64, u64p,
                                   ctypes.POINTER(u32), cp, sz]
     L.s2hip_op_running_sums.argtypes = [vp, vp, sz, vp, ctypes.POINTER(f32), cp, sz]
+    L.s2hip_op_expf.argtypes = [vp, vp, sz, vp, cp, sz]
+    L.s2hip_expf_host.argtypes = [vp, sz, vp]
+    L.s2hip_expf_host.restype = None
     L.s2hip_time_kernel.argtypes = [vp, cp, u32, ctypes.POINTER(ctypes.c_double),
                                     ctypes.POINTER(ctypes.c_double), cp, sz]
     for name in ("s2hip_get_spec", "s2hip_reset", "s2hip_eval", "s2hip_fast_logits",
@@ -120,7 +123,7 @@ def load():
                  "s2hip_op_linear",
                  "s2hip_op_rms_norm", "s2hip_op_dequant_rows", "s2hip_op_qk_rope",
                  "s2hip_op_attention", "s2hip_op_swiglu", "s2hip_op_sample", "s2hip_op_running_sums",
-                 "s2hip_time_kernel"):
+                 "s2hip_op_expf", "s2hip_time_kernel"):
         getattr(L, name).restype = i32
     _lib = L
     return L

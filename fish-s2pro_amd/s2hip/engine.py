@@ -242,6 +242,13 @@ class Engine:
         self._call(self._L.s2hip_op_running_sums, _p(t), t.size, _p(out), ctypes.byref(total))
         return out, total.value
 
+    def expf(self, x):
+        """The device exp of the samplers and SwiGLU epilogues over an array."""
+        a = _f32(x)
+        out = np.empty_like(a)
+        self._call(self._L.s2hip_op_expf, _p(a), a.size, _p(out))
+        return out
+
     def sample(self, logits, temperature, top_p, top_k, always_include=None, rng_state=0):
         x = _f32(logits)
         smp = _lib.Sampler(temperature, top_p, top_k)
@@ -257,6 +264,14 @@ class Engine:
         nbytes = ctypes.c_double(0)
         self._call(self._L.s2hip_time_kernel, name.encode(), reps, ctypes.byref(avg), ctypes.byref(nbytes))
         return avg.value, nbytes.value
+
+
+def expf_host(x) -> np.ndarray:
+    """The device exp routine compiled for the host (no device needed)."""
+    a = _f32(x)
+    out = np.empty_like(a)
+    _lib.load().s2hip_expf_host(_p(a), a.size, _p(out))
+    return out
 
 
 def version() -> str:

@@ -12,7 +12,8 @@ The named shapes are the workloads this library is measured and checked on:
   GGML Q8_0 / Q4_0 blocks (norms and embeddings stay f16).
 
 Weights are N(0, 0.02) rounded to f16 (round to nearest even); RMSNorm gains
-are 1.  Tensor names, shapes and metadata keys follow the reference's
+are 1 (``norm_gain`` sets the residual-stream gains -- attention, FFN and final
+norms -- to another value; QK-norm gains stay 1).  Tensor names, shapes and metadata keys follow the reference's
 registry (crates/fish_s2_infer/src/registry.rs:45-99, 360-496, 625-650).
 ``im_end_id`` comes from the tokenizer in the reference
 (crates/fish_s2_infer/src/tokenizer.rs:36-62); here it is a fixed
@@ -47,6 +48,7 @@ class _SynthConfig(ctypes.Structure):
         ("eps", ctypes.c_float),
         ("fast_eps", ctypes.c_float),
         ("init_std", ctypes.c_float),
+        ("norm_gain", ctypes.c_float),
         ("seed", ctypes.c_uint64),
     ]
 
@@ -78,6 +80,7 @@ class ModelShape:
     eps: float = 1.0e-6
     fast_eps: float = 1.0e-6
     init_std: float = 0.02
+    norm_gain: float = 1.0
     context_length: int = 32768
 
     def with_(self, **kw) -> "ModelShape":
@@ -93,7 +96,8 @@ class ModelShape:
 
     def file_name(self) -> str:
         tag = {GGML_F16: "f16", GGML_Q8_0: "q8_0", GGML_Q4_0: "q4_0"}[self.linear_type]
-        return f"s2synth-{self.name}-{tag}-seed{self.seed}.gguf"
+        gain = "" if self.norm_gain == 1.0 else f"-gain{self.norm_gain:g}"
+        return f"s2synth-{self.name}-{tag}{gain}-seed{self.seed}.gguf"
 
 
 TINY = ModelShape(

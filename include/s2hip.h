@@ -194,6 +194,15 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
 int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,
                               float* total_out, char* err, size_t err_cap);
 
+/* The device exp of the samplers' softmax (sampling.rs:202-225) and the
+ * SwiGLU sigmoids (slow_ar.rs:1215-1232, fast_ar.rs:472-485), whose Rust code
+ * calls f32::exp, i.e. the C library's expf: y[i] = exp(x[i]) with the
+ * results of glibc's expf, computed on the device.  A test hook. */
+int32_t s2hip_op_expf(s2hip_engine* engine, const float* x, size_t n, float* y, char* err, size_t err_cap);
+/* The same routine compiled for the host (no device needed): the CPU test of
+ * its bits against the C library's expf.  A test hook. */
+void s2hip_expf_host(const float* x, size_t n, float* y);
+
 /* Measurement: average device time of one launch of a named decode kernel,
  * timed with HIP events on the engine stream over `reps` passes across every
  * layer (so no pass re-reads weights from cache).  kernel: "slow_w13",

@@ -66,6 +66,12 @@ def lib():
     L.orc_rng_next_unit.restype = ctypes.c_double
     L.orc_sample_token.argtypes = [vp, sz, ctypes.c_float, ctypes.c_float, ctypes.c_int32,
                                    ctypes.c_int64, _u64p, _u32p]
+    L.orc_sample_token_margins.argtypes = [vp, sz, ctypes.c_float, ctypes.c_float, ctypes.c_int32,
+                                           ctypes.c_int64, _u64p, _u32p, vp]
+    L.orc_semantic_bias.argtypes = [vp, sz, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int64, ctypes.c_int32]
+    L.orc_semantic_bias.restype = None
+    L.orc_expf.argtypes = [vp, sz, vp]
+    L.orc_expf.restype = None
     L.orc_transpose_to_time_major.argtypes = [vp, ctypes.c_uint32, sz, vp]
     L.orc_compact_codes.argtypes = [vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
     L.orc_compact_codes.restype = sz
@@ -88,7 +94,7 @@ def lib():
                                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                      ctypes.c_char_p, sz]
     for name in ("orc_dequant_row", "orc_rms_norm", "orc_rms_norm_heads", "orc_linear",
-                 "orc_rope_normal", "orc_gqa_attention", "orc_sample_token",
+                 "orc_rope_normal", "orc_gqa_attention", "orc_sample_token", "orc_sample_token_margins",
                  "orc_transpose_to_time_major", "orc_get_spec", "orc_eval", "orc_fast_logits",
                  "orc_fast_codebooks", "orc_generate_codes"):
         getattr(L, name).restype = ctypes.c_int32
@@ -177,6 +183,37 @@ def sample_token(logits, temperature, top_p, top_k, always_include=None, rng_sta
                            -1 if always_include is None else always_include,
                            ctypes.byref(st), ctypes.byref(tok))
     return tok.value, st.value
+
+
+def sample_token_margins(logits, temperature, top_p, top_k, always_include=None, rng_state=0):
+    """sample_token plus its margins: returns (token, new_rng_state, (draw, cut, tie))
+    -- the distance of the draw target from the cumulative-sum boundaries
+    around the chosen item, of the top-p sums from top_p around the cut, and
+    the logit gap between the chosen item and its sort-order neighbours."""
+    x = np.ascontiguousarray(logits, np.float32)
+    st = ctypes.c_uint64(rng_state)
+    tok = ctypes.c_uint32(0)
+    mg = np.zeros(3, np.float32)
+    lib().orc_sample_token_margins(_p(x), x.size, temperature, top_p, top_k,
+                                   -1 if always_include is None else always_include,
+                                   ctypes.byref(st), ctypes.byref(tok), _p(mg))
+    return tok.value, st.value, tuple(float(v) for v in mg)
+
+
+def semantic_bias(logits, sem_begin, sem_end, im_end=None, block_im_end=False):
+    """build_semantic_bias + apply_semantic_bias on a copy of `logits`."""
+    x = np.array(logits, np.float32)
+    lib().orc_semantic_bias(_p(x), x.size, sem_begin, sem_end, -1 if im_end is None else im_end,
+                            1 if block_im_end else 0)
+    return x
+
+
+def expf(x):
+    """The C library's expf (what Rust's f32::exp calls) over an array."""
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    lib().orc_expf(_p(a), a.size, _p(out))
+    return out
 
 
 def next_unit(rng_state):

@@ -361,9 +361,22 @@ void apply_softmax(std::vector<float>& p, float temperature) {
   }
 }
 
+// How far one draw of sample_token lies from the nearest point where a
+// perturbation of the logits could change its result (all in the sampler's
+// own f32 values; a diagnostic for parity checks, not part of the reference):
+//   draw: distance of the draw target from the cumulative-sum boundaries
+//         around the chosen item (sample_discrete, sampling.rs:227-241);
+//   cut:  distance of the top-p cumulative sums from top_p around the cut
+//         (sampling.rs:172-181), +inf when top_p never cuts;
+//   tie:  logit gap between the chosen item and its neighbours in the stable
+//         descending order (sampling.rs:132-160), +inf without neighbours.
+struct SampleMargins {
+  float draw = INFINITY, cut = INFINITY, tie = INFINITY;
+};
+
 // sample_token (sampling.rs:120-200) + sample_discrete (sampling.rs:227-241)
 uint32_t sample_token(const float* logits, size_t n, float temperature, float top_p, int32_t top_k,
-                      int64_t always_include, uint64_t* rng) {
+                      int64_t always_include, uint64_t* rng, SampleMargins* mg = nullptr) {
   if (n == 0) return 0;
   struct Item {
     float v;
@@ -373,6 +386,8 @@ uint32_t sample_token(const float* logits, size_t n, float temperature, float to
   for (size_t i = 0; i < n; ++i) items[i] = {logits[i], uint32_t(i)};
   auto desc = [](const Item& a, const Item& b) { return a.v > b.v; };  // stable, descending
   std::stable_sort(items.begin(), items.end(), desc);
+  std::vector<Item> all;
+  if (mg) all = items;
   size_t k = top_k > 0 ? std::min(size_t(top_k), n) : n;
   items.resize(k);
   if (always_include >= 0 && size_t(always_include) < n) {
@@ -396,11 +411,22 @@ uint32_t sample_token(const float* logits, size_t n, float temperature, float to
       }
   }
   size_t p_idx = 0;
-  float cumsum = 0.0f;
+  float cumsum = 0.0f, prev = 0.0f;
+  bool cut = false;
   while (p_idx < m) {
+    prev = cumsum;
     cumsum += probs[p_idx];
     p_idx += 1;
-    if (cumsum >= top_p) break;
+    if (cumsum >= top_p) {
+      cut = true;
+      break;
+    }
+  }
+  if (mg) {
+    if (cut)
+      mg->cut = std::min(cumsum - top_p, p_idx > 1 ? top_p - prev : INFINITY);
+    else if (m > 0)
+      mg->cut = top_p - cumsum;
   }
   if (p_idx == 0) p_idx = 1;
   if (always_pos >= 0 && size_t(always_pos) >= p_idx) p_idx = size_t(always_pos) + 1;
@@ -414,11 +440,30 @@ uint32_t sample_token(const float* logits, size_t n, float temperature, float to
   double draw = rng_next_unit(rng);
   float target = std::min(std::max(float(draw), 0.0f), 1.0f - 1e-7f);
   float cs = 0.0f;
+  size_t chosen = probs.size() - 1;
+  float lo = 0.0f, hi = 0.0f;
+  bool hit = false;
   for (size_t i = 0; i < probs.size(); ++i) {
+    lo = cs;
     cs += probs[i];
-    if (target < cs) return items[i].id;
+    if (target < cs) {
+      chosen = i;
+      hi = cs;
+      hit = true;
+      break;
+    }
   }
-  return items[probs.size() - 1].id;
+  if (mg) {
+    mg->draw = hit ? std::min(target - lo, hi - target) : target - cs;
+    const uint32_t id = items[chosen].id;
+    for (size_t j = 0; j < all.size(); ++j) {
+      if (all[j].id != id) continue;
+      if (j > 0) mg->tie = std::min(mg->tie, std::fabs(all[j - 1].v - all[j].v));
+      if (j + 1 < all.size()) mg->tie = std::min(mg->tie, std::fabs(all[j + 1].v - all[j].v));
+      break;
+    }
+  }
+  return items[chosen].id;
 }
 
 // Linear over n_tok inputs: y[t][o] = sum_i x[t][i] * W[o][i] with W stored as
@@ -1110,18 +1155,25 @@ void fast_codebooks(orc_model* m, const float* hidden, uint32_t sem, float T, fl
   }
 }
 
+// build_semantic_bias + apply_semantic_bias (sampling.rs:54-100): bias 0 on
+// [sem_begin, sem_end] and on im_end, -inf elsewhere, added to the logits;
+// im_end then forced to -inf when blocked.  im_end < 0 means None.
+void semantic_bias(float* l, size_t n, uint32_t sem_begin, uint32_t sem_end, int64_t im_end, bool block) {
+  for (size_t i = 0; i < n; ++i) {
+    bool allowed = (i >= sem_begin && i <= sem_end) || (im_end >= 0 && i == size_t(im_end));
+    l[i] += allowed ? 0.0f : -INFINITY;
+  }
+  if (block && im_end >= 0 && size_t(im_end) < n) l[im_end] = -INFINITY;
+}
+
 // sample_semantic_token (generate.rs:284-298) with build_semantic_bias /
 // apply_semantic_bias (sampling.rs:54-100).
 uint32_t sample_semantic(orc_model* m, const float* logits_full, size_t generated_after_prefill,
                          uint32_t min_before_end, float T, float top_p, int32_t top_k, uint64_t* rng) {
   const orc_spec& s = m->spec;
   std::vector<float> l(logits_full, logits_full + s.vocab);
-  for (size_t i = 0; i < s.vocab; ++i) {
-    bool allowed = (i >= s.semantic_begin && i <= s.semantic_end) || i == m->im_end;
-    l[i] += allowed ? 0.0f : -INFINITY;
-  }
   bool block = uint32_t(generated_after_prefill) < min_before_end;
-  if (block && m->im_end < s.vocab) l[m->im_end] = -INFINITY;
+  semantic_bias(l.data(), s.vocab, s.semantic_begin, s.semantic_end, int64_t(m->im_end), block);
   return sample_token(l.data(), s.vocab, T, top_p, top_k, block ? -1 : int64_t(m->im_end), rng);
 }
 
@@ -1206,6 +1258,26 @@ int32_t orc_sample_token(const float* logits, size_t n, float T, float top_p, in
                          int64_t always_include, uint64_t* rng, uint32_t* out) {
   *out = sample_token(logits, n, T, top_p, top_k, always_include, rng);
   return 1;
+}
+
+int32_t orc_sample_token_margins(const float* logits, size_t n, float T, float top_p, int32_t top_k,
+                                 int64_t always_include, uint64_t* rng, uint32_t* out, float* margins) {
+  SampleMargins mg;
+  *out = sample_token(logits, n, T, top_p, top_k, always_include, rng, &mg);
+  margins[0] = mg.draw;
+  margins[1] = mg.cut;
+  margins[2] = mg.tie;
+  return 1;
+}
+
+void orc_semantic_bias(float* logits, size_t n, uint32_t sem_begin, uint32_t sem_end, int64_t im_end,
+                       int32_t block_im_end) {
+  semantic_bias(logits, n, sem_begin, sem_end, im_end, block_im_end != 0);
+}
+
+// f32::exp of the reference: the C library's expf
+void orc_expf(const float* x, size_t n, float* y) {
+  for (size_t i = 0; i < n; ++i) y[i] = expf(x[i]);
 }
 
 int32_t orc_transpose_to_time_major(const uint32_t* data, uint32_t rows, size_t cols, int32_t* flat) {

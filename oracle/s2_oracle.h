@@ -49,6 +49,18 @@ double orc_rng_next_unit(uint64_t* state);
 int32_t orc_sample_token(const float* logits, size_t n, float temperature, float top_p,
                          int32_t top_k, int64_t always_include, uint64_t* rng_state,
                          uint32_t* token_out);
+/* sample_token plus margins[3] = {draw, cut, tie}: how far the draw target
+ * lies from the cumulative-sum boundaries around the chosen item, how far the
+ * top-p cumulative sums lie from top_p around the cut (+inf: no cut), and the
+ * logit gap between the chosen item and its neighbours in the sort order. */
+int32_t orc_sample_token_margins(const float* logits, size_t n, float temperature, float top_p,
+                                 int32_t top_k, int64_t always_include, uint64_t* rng_state,
+                                 uint32_t* token_out, float* margins);
+/* build_semantic_bias + apply_semantic_bias in place; im_end < 0 means None */
+void orc_semantic_bias(float* logits, size_t n, uint32_t sem_begin, uint32_t sem_end, int64_t im_end,
+                       int32_t block_im_end);
+/* the C library's expf, which Rust's f32::exp calls */
+void orc_expf(const float* x, size_t n, float* y);
 int32_t orc_transpose_to_time_major(const uint32_t* data, uint32_t rows, size_t cols,
                                     int32_t* flat_out);
 /* codes is resized in place: returns the number of kept entries */

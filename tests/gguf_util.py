@@ -110,6 +110,92 @@ def toy_dual_ar(path, wqkv_rows, wo_rows, attention_norm, head_norm, eps=0.0):
     write(path, meta, tensors)
 
 
+def toy_model(path, d, vocab, slow=None, fast=None, emb=None, cb_emb=None, fast_emb=None, fast_output=None,
+              eps=0.0, fast_eps=0.0, rope_base=1e6, fast_rope_base=1e6, num_codebooks=1, codebook_size=1,
+              semantic=(2, 3), heads=(2, 1, 2), fast_heads=(2, 1, 2), ffn=2, fast_ffn=2, qk_norm=True):
+    """A hand-built dual-AR GGUF of width d with at most one Slow and one
+    Fast layer.  slow / fast: dicts of the layer's tensors by suffix
+    ("attention.wqkv.weight" [rows][d], "attention.wo.weight", "feed_forward.w1/w2/w3.weight",
+    "attention_norm.weight", "ffn_norm.weight", and for Slow "attention.q_norm.weight" /
+    "attention.k_norm.weight"); missing ones are zero (gains: one).  heads =
+    (q heads, kv heads, head_dim)."""
+    f32 = np.float32
+    H, Hkv, hd = heads
+    fH, fHkv, fhd = fast_heads
+
+    def layer(prefix, spec, H, Hkv, hd, ffn, qk):
+        spec = dict(spec or {})
+        q, kv = H * hd, Hkv * hd
+        shapes = {
+            "attention_norm.weight": (d,), "ffn_norm.weight": (d,),
+            "attention.wqkv.weight": (q + 2 * kv, d), "attention.wo.weight": (d, q),
+            "feed_forward.w1.weight": (ffn, d), "feed_forward.w3.weight": (ffn, d),
+            "feed_forward.w2.weight": (d, ffn),
+        }
+        if qk:
+            shapes["attention.q_norm.weight"] = (hd,)
+            shapes["attention.k_norm.weight"] = (hd,)
+        out = []
+        for suf, shp in shapes.items():
+            if suf in spec:
+                arr = np.asarray(spec[suf], f32).reshape(shp)
+            elif len(shp) == 1:
+                arr = np.ones(shp, f32)
+            else:
+                arr = np.zeros(shp, f32)
+            out.append((f"{prefix}.0.{suf}", tuple(reversed(shp)), arr))
+        return out
+
+    meta = [
+        ("general.architecture", STR, "fish-speech"),
+        ("fish-speech.context_length", U32, 16),
+        ("fish-speech.embedding_length", U32, d),
+        ("fish-speech.feed_forward_length", U32, ffn),
+        ("fish-speech.block_count", U32, 1),
+        ("fish-speech.attention.head_count", U32, H),
+        ("fish-speech.attention.head_count_kv", U32, Hkv),
+        ("fish-speech.rope.freq_base", F32, rope_base),
+        ("fish-speech.attention.layer_norm_rms_epsilon", F32, eps),
+        ("fish_speech.attention_qk_norm", BOOL, qk_norm),
+        ("fish_speech.fast_context_length", U32, num_codebooks + 1),
+        ("fish_speech.fast_embedding_length", U32, d),
+        ("fish_speech.fast_feed_forward_length", U32, fast_ffn),
+        ("fish_speech.fast_block_count", U32, 1 if fast is not None else 0),
+        ("fish_speech.fast_head_count", U32, fH),
+        ("fish_speech.fast_head_count_kv", U32, fHkv),
+        ("fish_speech.fast_head_dim", U32, fhd),
+        ("fish_speech.fast_rope_freq_base", F32, fast_rope_base),
+        ("fish_speech.fast_layer_norm_rms_eps", F32, fast_eps),
+        ("fish_speech.fast_attention_qk_norm", BOOL, False),
+        ("fish_speech.codebook_size", U32, codebook_size),
+        ("fish_speech.num_codebooks", U32, num_codebooks),
+        ("fish_speech.semantic_begin_id", U32, semantic[0]),
+        ("fish_speech.semantic_end_id", U32, semantic[1]),
+        ("fish_speech.scale_codebook_embeddings", BOOL, True),
+        ("fish_speech.tie_word_embeddings", BOOL, True),
+        ("fish_speech.fast_project_in", BOOL, False),
+    ]
+
+    def table(arr, rows):
+        a = np.zeros((rows, d), np.float16) if arr is None else np.asarray(arr, np.float16).reshape(rows, d)
+        return (tuple(reversed(a.shape)), a)
+
+    cb_rows = num_codebooks * codebook_size
+    tensors = [
+        ("embeddings.weight",) + table(emb, vocab),
+        ("codebook_embeddings.weight",) + table(cb_emb, cb_rows),
+        ("norm.weight", (d,), np.ones(d, f32)),
+        ("fast_embeddings.weight",) + table(fast_emb, codebook_size),
+        ("fast_norm.weight", (d,), np.ones(d, f32)),
+        ("fast_output.weight", (d, codebook_size),
+         np.zeros((codebook_size, d), f32) if fast_output is None else np.asarray(fast_output, f32)),
+    ]
+    tensors += layer("layers", slow, H, Hkv, hd, ffn, qk_norm)
+    if fast is not None:
+        tensors += layer("fast_layers", fast, fH, fHkv, fhd, fast_ffn, False)
+    write(path, meta, tensors)
+
+
 def read_tensors(path):
     """name -> numpy array ([ne1][ne0] for matrices) for F32 / F16 tensors."""
     raw = open(path, "rb").read()

@@ -113,3 +113,46 @@ def test_committed_counter_summaries_parse_and_match_algorithmic_bytes(kernel, w
     assert traffic is not None, f"profiles/counters_{kernel}_{workload}.txt missing or malformed"
     algo = _W13_ALGO_BYTES[(kernel, workload)]
     assert 0.99 * algo <= traffic <= 1.05 * algo, (traffic, algo)
+
+
+def _create_err(path):
+    L = _lib.load()
+    err = ctypes.create_string_buffer(512)
+    cfg = _lib.Config(path.encode(), 16, 0, 0, 0)
+    h = L.s2hip_create(ctypes.byref(cfg), err, len(err))
+    assert not h
+    return err.value.decode()
+
+
+def test_malformed_gguf_headers_fail_by_name(tmp_path):
+    """The GGUF header is validated on the host before any device call:
+    element counts and offsets that would wrap 64 bits fail with the tensor's
+    name (the reference's checked_mul / checked_add, gguf.rs:161,254,351)."""
+    import struct
+
+    import gguf_util
+
+    base = str(tmp_path / "ok.gguf")
+    gguf_util.write(base, [("general.architecture", gguf_util.STR, "fish-speech")],
+                    [("a.weight", (4, 2), np.zeros((2, 4), np.float32))])
+    raw = bytearray(open(base, "rb").read())
+    name = b"a.weight"
+    at = raw.index(name) + len(name)  # then n_dims u32, dims u64 x2, type u32, offset u64
+    # dims whose product wraps to a small number: 2^33 x 2^31 = 2^64 -> 0
+    bad = bytearray(raw)
+    struct.pack_into("<QQ", bad, at + 4, 1 << 33, 1 << 31)
+    p = str(tmp_path / "dims.gguf")
+    open(p, "wb").write(bad)
+    assert "a.weight" in _create_err(p) and "overflow" in _create_err(p)
+    # an offset that wraps past the end of the address space
+    bad = bytearray(raw)
+    struct.pack_into("<Q", bad, at + 4 + 16 + 4, (1 << 64) - 16)
+    p = str(tmp_path / "offset.gguf")
+    open(p, "wb").write(bad)
+    assert "a.weight extends past file end" in _create_err(p)
+    # an offset just past the data
+    bad = bytearray(raw)
+    struct.pack_into("<Q", bad, at + 4 + 16 + 4, 64)
+    p = str(tmp_path / "past.gguf")
+    open(p, "wb").write(bad)
+    assert "a.weight extends past file end" in _create_err(p)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 from conftest import make_prompt
-from loop_util import teacher_forced_mismatches
+from loop_util import assert_draws_match, teacher_forced_mismatches
 from oracle import oracle as O
 from s2hip import synth
 
@@ -88,11 +88,6 @@ def test_greedy_codes_bit_exact_and_golden(tiny_gguf):
     assert np.array_equal(r["codes"], ro["codes"]) and r["rng_state"] == ro["rng_state"]
 
 
-# A sampled trajectory may diverge from the oracle's at a draw that lands
-# within f32 reordering noise of a probability boundary; draws are therefore
-# compared one by one on the GPU trajectory (teacher forcing), and at most 3 %
-# may differ (an unrelated sampler would disagree on nearly all).
-MAX_SAMPLED_MISMATCH = 0.03
 
 
 def test_sampled_codes_match_oracle(tiny_gguf):
@@ -108,7 +103,7 @@ def test_sampled_codes_match_oracle(tiny_gguf):
     assert rg["n_frames"] == 20
     mism, total = teacher_forced_mismatches(o, prompt, rg["codes"], rg["n_frames"], 0.7, 0.9, 0, 40, 1,
                                             synth.TINY.im_end_id)
-    assert total == 200 and mism <= MAX_SAMPLED_MISMATCH * total, (mism, total)
+    assert_draws_match(mism, total, 200)
 
 
 def test_repeated_generate_is_deterministic(tiny_gguf):
@@ -149,7 +144,7 @@ def test_quantized_codes_bit_exact(request, which):
     rs = e.generate_codes(prompt, 16, min_tokens_before_end=100, temperature=0.7, top_p=0.9, rng_state=5)
     mism, total = teacher_forced_mismatches(o, prompt, rs["codes"], rs["n_frames"], 0.7, 0.9, 0, 100, 5,
                                             synth.TINY.im_end_id)
-    assert total == 160 and mism <= MAX_SAMPLED_MISMATCH * total, (mism, total)
+    assert_draws_match(mism, total, 160)
 
 
 def test_errors_match_reference_behaviour(tiny_gguf):
@@ -193,7 +188,7 @@ def test_attention_modes_match_oracle(tiny_gguf, monkeypatch, fused):
     rg = e.generate_codes(prompt, 40, **kw)
     assert rg["n_frames"] == 40
     mism, total = teacher_forced_mismatches(o, prompt, rg["codes"], 40, 0.7, 0.9, 0, 100, 7, synth.TINY.im_end_id)
-    assert total == 400 and mism <= MAX_SAMPLED_MISMATCH * total, (mism, total)
+    assert_draws_match(mism, total, 400)
 
 
 @pytest.mark.parametrize("warm", ["8,16,50,50,100", "256,4,100,100,100", "16,8,0,100,30"])
@@ -244,3 +239,26 @@ def test_kv_f16_cache_matches_oracle_with_f16_kv(tiny_gguf):
     e.reset()
     hg, _ = e.eval(prompt)
     assert 0 < _rel(hg, hf) < 2e-2
+
+
+@pytest.fixture(scope="module")
+def tiny_gain_gguf(model_dir):
+    # every residual-stream RMSNorm gain 1e3: residuals of ~1e4..1e5 and
+    # normalised inputs of ~1e3, far outside what N(0, 0.02) weights produce
+    return synth.ensure_gguf(synth.TINY.with_(norm_gain=1000.0), model_dir)
+
+
+def test_large_norm_gains_keep_greedy_codes_bit_exact(tiny_gain_gguf):
+    """The first Fast-AR pass runs the batched MFMA product on the raw
+    pre-norm residual times the gain (~1e6 here): its three-part f16 split
+    must carry that without a range failure, and codes stay bit-exact."""
+    prompt = make_prompt(synth.TINY, 24, seed=31)
+    e, o = _engine(tiny_gain_gguf), _oracle(tiny_gain_gguf)
+    hg, _ = e.eval(prompt)
+    ho, _ = o.eval(prompt)
+    assert _rel(hg, ho) < 1e-4
+    e.reset()
+    rg = e.generate_codes(prompt, 16, min_tokens_before_end=100)
+    ro = o.generate_codes(prompt, 16, min_tokens_before_end=100)
+    assert rg["n_frames"] == ro["n_frames"] == 16
+    assert np.array_equal(rg["codes"], ro["codes"]) and rg["rng_state"] == ro["rng_state"]

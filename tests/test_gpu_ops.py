@@ -62,31 +62,38 @@ def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
         assert _rel(got[c], want) < min(tol, 1e-4), c
 
 
-def test_batched_linear_f16_range(eng):
+@pytest.mark.parametrize("ncol", [2, 8])
+def test_batched_linear_activation_range(eng, ncol):
     """Batched F16 columns go through the MFMA product with activations split
-    into f16 hi + 2^11-scaled lo: large values inside the f16 range and tiny
-    ones stay accurate, and a value beyond the range (or NaN) makes the call
-    fail instead of returning a wrong result."""
+    into three f16 parts: columns whose values span 1e-6 .. 1e6 (and single
+    entries up to 1e8) match the oracle to 1e-4, and a non-finite value makes
+    the call fail instead of returning a wrong result."""
     from s2hip import S2HipError
 
-    rng = np.random.default_rng(31)
-    in_dim, out_dim, ncol = 2560, 256, 4
+    rng = np.random.default_rng(31 + ncol)
+    in_dim, out_dim = 2560, 256
     wf = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
     raw = _rows(1, wf)
+    for lo_exp, hi_exp in ((-6, 6), (-6, -5), (5, 6), (-1, 1)):
+        x = rng.standard_normal((ncol, in_dim)).astype(np.float32)
+        x *= (10.0 ** rng.uniform(lo_exp, hi_exp, (ncol, in_dim))).astype(np.float32)
+        x[0, 7] = 6.0e4 * 10.0 ** (hi_exp - 1)
+        x[-1, 100] = -1.0e8 if hi_exp == 6 else x[-1, 100]
+        got = eng.linear(raw, 1, in_dim, out_dim, x)
+        for c in range(ncol):
+            want = O.linear(x[c], raw, 1, in_dim, out_dim)
+            assert _rel(got[c], want) < 1e-4, (lo_exp, hi_exp, c, _rel(got[c], want))
+    # one column of tiny values next to one of huge values
     x = rng.standard_normal((ncol, in_dim)).astype(np.float32)
-    x[1, 7] = 6.0e4
-    x[2, 100] = -6.5e4
-    x[3, :] *= 1e-4
+    x[0] *= 1e-6
+    x[-1] *= 1e6
     got = eng.linear(raw, 1, in_dim, out_dim, x)
     for c in range(ncol):
-        want = O.linear(x[c], raw, 1, in_dim, out_dim)
-        assert _rel(got[c], want) < 1e-4, c
-    x[0, 5] = 7.0e4
-    with pytest.raises(S2HipError, match="f16 range"):
-        eng.linear(raw, 1, in_dim, out_dim, x)
-    x[0, 5] = np.nan
-    with pytest.raises(S2HipError, match="f16 range"):
-        eng.linear(raw, 1, in_dim, out_dim, x)
+        assert _rel(got[c], O.linear(x[c], raw, 1, in_dim, out_dim)) < 1e-4, c
+    for bad in (np.nan, np.inf):
+        x[0, 5] = bad
+        with pytest.raises(S2HipError, match="batched product"):
+            eng.linear(raw, 1, in_dim, out_dim, x)
     # the engine still works
     x[0, 5] = 1.0
     got = eng.linear(raw, 1, in_dim, out_dim, x)
@@ -134,10 +141,26 @@ def test_attention_matches_oracle(eng, H, Hkv, hd, T):
 
 @pytest.mark.parametrize("fast", [False, True])
 def test_swiglu_matches_oracle(eng, fast):
+    # same operation order and the same expf bits as the reference: bit-exact
     rng = np.random.default_rng(30)
-    g = (rng.standard_normal(9728) * 4).astype(np.float32)
-    u = rng.standard_normal(9728).astype(np.float32)
-    np.testing.assert_allclose(eng.swiglu(g, u, fast), O.swiglu(g, u, fast), rtol=1e-6, atol=1e-6)
+    g = (rng.standard_normal(97280) * 4).astype(np.float32)
+    u = rng.standard_normal(97280).astype(np.float32)
+    got, want = eng.swiglu(g, u, fast), O.swiglu(g, u, fast)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_expf_bit_exact_on_device(eng):
+    # the device exp of the samplers and SwiGLU sigmoids reproduces the C
+    # library's expf (what Rust's f32::exp calls) bit for bit: every 397th
+    # float bit pattern (10.8 M inputs over all binades, inf, NaN) plus 4 M
+    # softmax arguments in [-104, 0]
+    u = np.arange(0, 1 << 32, 397, dtype=np.uint64).astype(np.uint32)
+    rng = np.random.default_rng(8)
+    x = np.concatenate([u.view(np.float32), -rng.exponential(4.0, 2_000_000).astype(np.float32),
+                        -rng.uniform(0, 104, 2_000_000).astype(np.float32)])
+    got, want = eng.expf(x), O.expf(x)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert x.size >= 10_000_000 and same.all(), x[~same][:5]
 
 
 def _running_sum_cases():
@@ -197,3 +220,23 @@ def test_sampler_bit_exact(eng, T, top_p, top_k, n):
         to, st_o = O.sample_token(logits, T, top_p, top_k, always, st_o)
         tg, st_g = eng.sample(logits, T, top_p, top_k, always, st_g)
         assert (tg, st_g) == (to, st_o), (trial, tg, to)
+
+
+def test_sampler_exact_on_the_draws_nearest_a_boundary(eng):
+    # Draws whose target lies closest to a cumulative-probability boundary (or
+    # whose top-p sums lie closest to top_p) are the ones a probability that is
+    # off by one ulp would flip.  Pick the 64 most sensitive of 3000 seeded
+    # cases with the oracle's own margins and require identical draws.
+    rng = np.random.default_rng(404)
+    cases = []
+    for i in range(3000):
+        n = 4096
+        logits = (rng.standard_normal(n) * 2).astype(np.float32)
+        T, top_p, top_k = [(0.7, 0.9, 0), (0.7, 0.7, 30), (1.0, 0.95, 0)][i % 3]
+        st = int(rng.integers(1, 1 << 62))
+        tok, st_after, (draw, cut, tie) = O.sample_token_margins(logits, T, top_p, top_k, None, st)
+        cases.append((min(draw, cut), logits, T, top_p, top_k, st, tok, st_after))
+    cases.sort(key=lambda c: c[0])
+    for margin, logits, T, top_p, top_k, st, tok, st_after in cases[:64]:
+        assert margin < 1e-4
+        assert eng.sample(logits, T, top_p, top_k, None, st) == (tok, st_after), margin

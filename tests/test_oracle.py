@@ -374,9 +374,148 @@ def test_teacher_forced_replay_of_oracle_trajectory_is_exact(tiny_gguf):
     assert r["n_frames"] >= 1
     mism, total = teacher_forced_mismatches(o, prompt, r["codes"], r["n_frames"], 0.7, 0.9, 0, 4, 3,
                                             synth.TINY.im_end_id)
-    assert mism == 0 and total == 10 * r["n_frames"]
-    # a planted wrong code is caught
+    assert mism == [] and total == 10 * r["n_frames"]
+    # a planted wrong code is caught, and is not excused as a boundary draw
     bad = r["codes"].copy()
     bad[3, 0] = (bad[3, 0] + 1) % synth.TINY.codebook_size
     mism2, _ = teacher_forced_mismatches(o, prompt, bad, r["n_frames"], 0.7, 0.9, 0, 4, 3, synth.TINY.im_end_id)
-    assert mism2 >= 1
+    assert len(mism2) >= 1 and not all(m[5] for m in mism2)
+
+
+# ------------------------------------------- hand-derived model KATs ------
+def test_rms_norm_heads_kat():
+    # rms_norm_heads_f32 (backend.rs:104-121): each head normalised on its own
+    # with the shared per-head gain.  Head 0 = [3, 4]: ms 12.5; head 1 = [0, 2]:
+    # ms 2; gain [1, 0.5], eps 0.
+    got = O.rms_norm_heads(np.array([3, 4, 0, 2], np.float32), np.array([1, 0.5], np.float32), 2, 0.0)
+    want = [3 / math.sqrt(12.5), 4 / math.sqrt(12.5) * 0.5, 0.0, 2 / math.sqrt(2.0) * 0.5]
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
+    # a whole-vector norm would give ms = 7.25 for every element
+    assert abs(got[0] - 3 / math.sqrt(7.25)) > 1e-2
+
+
+def test_semantic_mask_kats():
+    # sampling.rs:248-274 (semantic_mask_leaves_only_allowed_ids_finite,
+    # semantic_mask_can_block_im_end, apply_semantic_bias_zeros_disallowed_logits)
+    m = O.semantic_bias([1.0, 2.0, 3.0, 4.0, 5.0], 1, 2, im_end=4, block_im_end=False)
+    assert np.isneginf(m[0]) and m[1] == 2.0 and m[2] == 3.0 and np.isneginf(m[3]) and m[4] == 5.0
+    m = O.semantic_bias([0.1, 0.2, 0.3, 0.4, 0.5], 1, 2, im_end=4, block_im_end=True)
+    assert np.isneginf(m[4]) and np.isneginf(m[0]) and np.float32(m[1]) == np.float32(0.2)
+    m = O.semantic_bias([0.1, 0.2, 0.3, 0.4, 0.5], 1, 2, im_end=4, block_im_end=False)
+    assert np.isinf(m[0]) and m[1] == np.float32(0.2) and m[4] == np.float32(0.5)
+    # None: nothing outside the semantic range survives
+    m = O.semantic_bias([0.1, 0.2, 0.3, 0.4, 0.5], 1, 2)
+    assert np.isneginf(m[[0, 3, 4]]).all() and np.isfinite(m[[1, 2]]).all()
+
+
+@pytest.fixture(scope="module")
+def embed_toy_gguf(tmp_path_factory):
+    # width 4, vocab 8, semantic ids [4, 6], 2 codebooks of 3 codes; every
+    # Slow-layer weight zero (the layer passes the embedding through), eps 1
+    # so the final RMSNorm keeps the embedding's scale visible.
+    emb = np.zeros((8, 4), np.float32)
+    emb[0] = [2, 0, 0, 0]  # a text id
+    emb[5] = [1, 0, 0, 0]  # a semantic id
+    cb = np.zeros((6, 4), np.float32)
+    cb[:, 1] = np.arange(6)  # codebook row r = [0, r, 0, 0]
+    p = str(tmp_path_factory.mktemp("embtoy") / "embed_toy.gguf")
+    gguf_util.toy_model(p, 4, 8, emb=emb, cb_emb=cb, eps=1.0, num_codebooks=2, codebook_size=3,
+                        semantic=(4, 6))
+    return p
+
+
+def test_semantic_token_embedding_kat(embed_toy_gguf):
+    # embed_slow_ar_time_major (slow_ar.rs:1041-1133) by hand: token [5 | 2, 1]
+    # is semantic, so h = emb[5] + (cb[0*3 + 2] + cb[1*3 + 1]) = [1, 6, 0, 0],
+    # scaled by 1/sqrt(2 + 1); final RMSNorm with eps 1: ms = 37/12, so
+    # hidden = [1, 6, 0, 0] / sqrt(3) / sqrt(49/12) = [2/7, 12/7, 0, 0].
+    m = O.OracleModel(embed_toy_gguf, 4, im_end_id=7)
+    hidden, logits = m.eval([5, 2, 1])
+    np.testing.assert_allclose(hidden, [2 / 7, 12 / 7, 0, 0], rtol=1e-6, atol=1e-7)
+    # tied head: logits[i] = emb[i] . hidden
+    np.testing.assert_allclose(logits, [4 / 7, 0, 0, 0, 0, 2 / 7, 0, 0], rtol=1e-6, atol=1e-7)
+    # a text id takes no codebook rows and no scale: [2, 0, 0, 0] / sqrt(1 + 1)
+    m.reset()
+    hidden, _ = m.eval([0, 2, 1])
+    np.testing.assert_allclose(hidden, [math.sqrt(2), 0, 0, 0], rtol=1e-6)
+    # the mistakes this pins: no cb * codebook_size offset would sum rows 2 and
+    # 1 ([1, 3, 0, 0]); 1/sqrt(num_codebooks) would give [1, 6, 0, 0] / sqrt(45/4)
+    assert abs(2 / 7 - 1 / math.sqrt(3) / math.sqrt(10 / 12 / 1 + 1)) > 1e-3
+    assert abs(2 / 7 - 1 / math.sqrt(45 / 4)) > 1e-3
+
+
+FAST_TOY = dict(
+    # one Fast layer, width 4, 1 q head / 1 kv head of head_dim 4, FFN zero
+    # (it passes through), Wo = I.  q[2] = 1.5 n[0]; k[2] = n[1]; v[0] = n[3],
+    # v[1] = 0.5 n[0], where n is the RMS-normalised input (eps 0, gain 1).
+    wqkv=[[0, 0, 0, 0], [0, 0, 0, 0], [1.5, 0, 0, 0], [0, 0, 0, 0],
+          [0, 0, 0, 0], [0, 0, 0, 0], [0, 1, 0, 0], [0, 0, 0, 0],
+          [0, 0, 0, 1], [0.5, 0, 0, 0], [0, 0, 0, 0], [0, 0, 0, 0]],
+    fast_emb=[[1, 1, 1, 1], [2, 0, 0, 0], [0, 0, 0, 2], [0, 2, 0, 0]],
+    out=[[1, 0, 0, 0], [0, 1, 0, 0], [0, 0, 1, 0], [1, 1, 0, 0]],
+)
+
+
+@pytest.fixture(scope="module")
+def fast_toy_gguf(tmp_path_factory):
+    # Fast RoPE base 4 (Slow: 1e6), so position 1 rotates the second pair of a
+    # head_dim-4 head by 1 / 4^(2/4) = 0.5 rad
+    p = str(tmp_path_factory.mktemp("fasttoy") / "fast_toy.gguf")
+    gguf_util.toy_model(p, 4, 8, fast={"attention.wqkv.weight": FAST_TOY["wqkv"],
+                                       "attention.wo.weight": np.eye(4)},
+                        fast_emb=FAST_TOY["fast_emb"], fast_output=FAST_TOY["out"], num_codebooks=3,
+                        codebook_size=4, semantic=(4, 7), fast_heads=(1, 1, 4), fast_rope_base=4.0,
+                        rope_base=1e6)
+    return p
+
+
+def _fast_toy_logits(h):
+    # fast_output . rmsnorm(h) with rows [1,0,0,0], [0,1,0,0], [0,0,1,0], [1,1,0,0]
+    n = np.asarray(h, np.float64) / math.sqrt(float(np.mean(np.square(h))))
+    return np.array([n[0], n[1], n[2], n[0] + n[1]])
+
+
+@pytest.mark.parametrize("flags", [0, O.FAITHFUL_FAST_RECOMPUTE])
+def test_fast_ar_toy_layer_kat(fast_toy_gguf, flags):
+    """forward_codebook_prefix (fast_ar.rs:360-437) on a one-layer toy, derived
+    by hand.  Slow hidden h0 = [1,1,1,1] (rms 1): q0 = [0,0,1.5,0], k0 =
+    [0,0,1,0], v0 = [1,0.5,0,0]."""
+    m = O.OracleModel(fast_toy_gguf, 4, im_end_id=7, flags=flags)
+    h0 = np.ones(4, np.float32)
+    # no prefix: one position attends to itself, out = h0 + v0 = [2, 1.5, 1, 1]
+    np.testing.assert_allclose(m.fast_logits(h0, []), _fast_toy_logits([2, 1.5, 1, 1]), rtol=1e-6, atol=1e-6)
+    # prefix [1]: position 1 holds fast_emb[1] = [2,0,0,0] (no codebook offset,
+    # fast_ar.rs:396-401): q1 = [0,0,3,0] rotated at position 1 with the FAST
+    # base 4 -> pair (2,3) = 3 (cos .5, sin .5); k1 = 0, v1 = [0,1,0,0]; no
+    # QK-norm on the Fast path.  Scores (scale 1/sqrt(4)): s0 = 1.5 cos(.5),
+    # s1 = 0 -> p0 = 1 / (1 + e^-s0); out = [2 + p0, 0.5 p0 + p1, 0, 0].
+    s0 = 1.5 * math.cos(0.5)
+    p0 = 1.0 / (1.0 + math.exp(-s0))
+    p1 = 1.0 - p0
+    want = _fast_toy_logits([2 + p0, 0.5 * p0 + p1, 0, 0])
+    np.testing.assert_allclose(m.fast_logits(h0, [1]), want, rtol=1e-6, atol=1e-6)
+    # prefix [1, 2]: position 2 holds fast_emb[2] = [0,0,0,2]: q2 = 0, so the
+    # three causal positions get weight 1/3 each: attn = (v0 + v1 + v2) / 3 with
+    # v2 = [2,0,0,0] -> [1, 0.5, 0, 0]; out = [1, 0.5, 0, 2]
+    np.testing.assert_allclose(m.fast_logits(h0, [1, 2]), _fast_toy_logits([1, 0.5, 0, 2]), rtol=1e-6, atol=1e-6)
+    # what the case at prefix [1] separates: a QK-norm'd Fast path (s0 = 2 cos .5)
+    # and the Slow RoPE base (s0 = 1.5 cos 1e-3) both move the logits by > 1e-2
+    for s_bad in (2 * math.cos(0.5), 1.5 * math.cos(1e-3)):
+        pb = 1.0 / (1.0 + math.exp(-s_bad))
+        assert np.abs(_fast_toy_logits([2 + pb, 0.5 * pb + 1 - pb, 0, 0]) - want).max() > 1e-2
+
+
+def test_sampler_margins_kat():
+    # two equal logits at T = 1: probabilities [0.5, 0.5]; the draw target t
+    # (the LCG's first unit value) picks item 0 iff t < 0.5, and its margin is
+    # the distance to 0 or 0.5 (or 0.5 and 1); top_p 1 never cuts before the end
+    u, _ = O.next_unit(7)
+    t = np.float32(u)
+    tok, _, (draw, cut, tie) = O.sample_token_margins([1.0, 1.0], 1.0, 1.0, 0, None, 7)
+    assert tok == (0 if t < 0.5 else 1)
+    want = min(t, 0.5 - t) if t < 0.5 else min(t - 0.5, 1.0 - t)
+    assert abs(draw - want) < 1e-7 and tie == 0.0
+    assert abs(cut - 0.0) < 1e-7  # cumsum reaches exactly 1.0 = top_p at the last item
+    # top_p 0.6 over [0.5, 0.5]: the cut falls after item 1 with sums 0.5 / 1.0
+    _, _, (_, cut, _) = O.sample_token_margins([1.0, 1.0], 1.0, 0.6, 0, None, 7)
+    assert abs(cut - 0.1) < 1e-6
