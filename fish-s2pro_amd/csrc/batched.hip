@@ -14,19 +14,21 @@
 // contiguous bytes per row and chunk of 4 steps, issued one chunk ahead), so
 // the activation loads neither scatter over rows (the MFMA fragment puts the
 // column in the fastest lane bits) nor hold up the weight loads' wait
-// counter.  Each lane then splits its 8 elements per step into three f16
-// parts, x = 2^16 t + m + 2^-11 l:
-//   t = f16(2^-16 x), m = f16(x - 2^16 t), l = f16(2^11 (x - 2^16 t - m))
-// (both differences are exact in f32), and the three go through the MFMA
-// with the same weight fragment into three accumulators.  The split carries
-// x to ~2^-22 relative for |x| >= 2^-14 (~2^-35 absolute below) for every
-// |x| up to ~1.3e8 with no per-column scale pass: t takes the magnitude of
-// large activations (a raw pre-norm residual of 1e5 and more), m and l stay
-// inside the f16 range.  RMSNorm inputs: the sum of squares of each column
-// is accumulated from the same values and the RMS scale is applied to the
-// result (W.((x s) g) = s W.(x g)).  A non-finite activation (or one beyond
-// the split's range) makes its column's sums non-finite; the epilogue
-// reports that as ERR_F16_RANGE instead of returning a wrong product.
+// counter.  Each wave scales each column by a power of two that brings the
+// largest |x| of its first two staged chunks (256 elements of its k range)
+// to [1, 2).  Each lane then splits its 8 scaled elements per step into f16
+// hi = f16(x) and lo = f16((x - hi) 2^11) (x = hi + 2^-11 lo to ~2^-22 |x|
+// for |x| >= 2^-14 of that maximum, absolute ~2^-35 of it below); hi and lo
+// go through the MFMA with the same weight fragment into two accumulators,
+// and each wave's sums are scaled back exactly before the waves' sums are
+// added.  So columns of any magnitude keep the same relative accuracy (1e-6
+// or a raw pre-norm residual of 1e7 times its gain), and an element may be
+// up to 2^15 times the maximum of the first chunks.  RMSNorm inputs: the sum
+// of squares of each column is accumulated from the same values and the RMS
+// scale is applied to the result (W.((x s) g) = s W.(x g)).  A non-finite
+// activation (or one beyond that headroom) makes its column's sums
+// non-finite; the epilogue reports that as ERR_F16_RANGE instead of
+// returning a wrong product.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -75,18 +77,13 @@ constexpr int WIN = 8;        // weight steps in flight (two chunks)
 constexpr int XC = 4;         // steps per staged activation chunk
 constexpr int RS = 36;        // LDS floats per staged row and step (32 + 4: conflict-free fragment reads)
 
-// x = 2^16 t + m + 2^-11 l (see the file comment); fmaf(-t, 2^16, x) and
-// r - m are exact, so the parts differ from x only by the rounding of l.
-__device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8& top, half8& hi, half8& lo) {
+__device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8& hi, half8& lo) {
   const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const _Float16 t = _Float16(v[e] * (1.0f / 65536.0f));
-    const float r = fmaf(-float(t), 65536.0f, v[e]);
-    const _Float16 h = _Float16(r);
-    top[e] = t;
+    const _Float16 h = _Float16(v[e]);
     hi[e] = h;
-    lo[e] = _Float16((r - float(h)) * 2048.0f);
+    lo[e] = _Float16((v[e] - float(h)) * 2048.0f);
   }
 }
 
@@ -110,9 +107,9 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   constexpr int NW = DUAL ? 2 : 1;
   constexpr int CHF = XC * NB * RS;  // floats per chunk buffer
   constexpr int LDX = NB / 2;        // staging loads per chunk (2 rows x 512 B each)
-  // each wave's staging buffers take its partial sums after its loop (3 NW x
-  // 64 floatx4 = at most 6 KiB, inside the 2 CHF floats of the wave)
-  static_assert(3 * NW * 64 * 4 <= 2 * CHF, "partials must fit the staging buffers");
+  // each wave's staging buffers take its partial sums after its loop (2 NW x
+  // 64 floatx4 = at most 4 KiB, inside the 2 CHF floats of the wave)
+  static_assert(2 * NW * 64 * 4 <= 2 * CHF, "partials must fit the staging buffers");
   __shared__ __align__(16) float xs[WAVES][2][CHF];
   __shared__ float gs[WAVES][2][NORM ? XC * 32 : 1];
   __shared__ float ssq[WAVES][64];
@@ -168,14 +165,43 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     if constexpr (DUAL) wb[i][1] = bmm_wload(reinterpret_cast<const half8*>(wp1 + 512 * t));
   }
   stage_store(sxa, sga, 0);
+  // Per-(wave, column) power-of-two scale: the largest |x g| of the first two
+  // chunks of this wave's range (already in registers) is brought to [1, 2),
+  // leaving 2^15 of headroom in the f16 hi part for the rest of the range.
+  float rm[LDX];
+#pragma unroll
+  for (int j = 0; j < LDX; ++j) {
+    floatx4 va = sxa[j], vb = sxb[j];
+    if constexpr (NORM) {
+      va = va * sga;
+      vb = vb * sgb;
+    }
+    float m = fmaxf(fmaxf(fabsf(va.x), fabsf(va.y)), fmaxf(fabsf(va.z), fabsf(va.w)));
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(vb.x), fabsf(vb.y)), fmaxf(fabsf(vb.z), fabsf(vb.w))));
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    rm[j] = m;  // max of staged row 2 j + (lane >> 5)
+  }
+  float cmax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < LDX; ++j) {
+    const float v = __shfl(rm[j], int((n & 1u) << 5), 64);
+    cmax = (uint32_t(j) == (n >> 1)) ? v : cmax;
+  }
+  // cmax in [2^e, 2^(e+1)): scale by 2^-e (e clamped to +-100; 0 for zero,
+  // subnormal or non-finite maxima -- a non-finite value still ends as a
+  // non-finite sum)
+  int cexp = int((__float_as_uint(cmax) >> 23) & 0xffu) - 127;
+  cexp = (cmax >= 1.0e-30f && cmax <= 1.0e30f) ? cexp : 0;
+  const float cinv = __uint_as_float(uint32_t(127 - cexp) << 23);
+  const float cscale = __uint_as_float(uint32_t(127 + cexp) << 23);
   __builtin_amdgcn_sched_barrier(0);
 
-  floatx4 acc[NW], accl[NW], acct[NW];
+  floatx4 acc[NW], accl[NW];
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
     acc[m] = floatx4{};
     accl[m] = floatx4{};
-    acct[m] = floatx4{};
   }
   float ss = 0.0f;
   const floatx4 z4 = floatx4{};
@@ -214,11 +240,12 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
         x0 = x0 * cg0;
         x1 = x1 * cg1;
       }
-      half8 bt, bh, bl;
-      split8(x0, x1, bt, bh, bl);
+      x0 = x0 * cinv;
+      x1 = x1 * cinv;
+      half8 bh, bl;
+      split8(x0, x1, bh, bl);
 #pragma unroll
       for (int m = 0; m < NW; ++m) {
-        acct[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bt, acct[m], 0, 0, 0);
         acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bh, acc[m], 0, 0, 0);
         accl[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], bl, accl[m], 0, 0, 0);
       }
@@ -246,29 +273,27 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     chunk_steps(2 * sc + 1, std::integral_constant<int, 1>{});
   }
-  // partials of wave w: slot (3 m + part) lane of its own staging region
+  // partials of wave w: slot (2 m + part) lane of its own staging region
   auto red = [&](uint32_t w, int slot) __attribute__((always_inline)) -> floatx4* {
     return reinterpret_cast<floatx4*>(&xs[w][0][0]) + slot * 64 + lane;
   };
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
-    *red(wave, 3 * m) = acc[m];
-    *red(wave, 3 * m + 1) = accl[m];
-    *red(wave, 3 * m + 2) = acct[m];
+    *red(wave, 2 * m) = acc[m] * cscale;
+    *red(wave, 2 * m + 1) = accl[m] * cscale;
   }
   if constexpr (NORM) ssq[wave][lane] = ss;
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int m = 0; m < NW; ++m) {
-    floatx4 t = *red(0, 3 * m), tl = *red(0, 3 * m + 1), tt = *red(0, 3 * m + 2);
+    floatx4 t = *red(0, 2 * m), tl = *red(0, 2 * m + 1);
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) {
-      t += *red(w, 3 * m);
-      tl += *red(w, 3 * m + 1);
-      tt += *red(w, 3 * m + 2);
+      t += *red(w, 2 * m);
+      tl += *red(w, 2 * m + 1);
     }
-    acc[m] = (t + tl * (1.0f / 2048.0f)) + tt * 65536.0f;
+    acc[m] = t + tl * (1.0f / 2048.0f);
   }
   float r = 1.0f;
   if constexpr (NORM) {

@@ -1107,7 +1107,7 @@ void Engine::check_state_err(uint32_t nseq) {
     if (st_host_[b].err & ERR_TOKEN_RANGE) fail("token id out of range" + who);
     if (st_host_[b].err & ERR_KV_OVERFLOW) fail("KV cache overflow" + who);
     if (st_host_[b].err & ERR_SAMPLER) fail("sampler failure" + who);
-    if (st_host_[b].err & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product (|x| < 1.3e8)");
+    if (st_host_[b].err & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
   }
 }
 
@@ -1421,7 +1421,7 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
     HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipMemcpyAsync(&herr, derr.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
-    if (herr & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product (|x| < 1.3e8)");
+    if (herr & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
     return;
   }
   // quantized rows: the repacked planes that one-column decode GEMVs read

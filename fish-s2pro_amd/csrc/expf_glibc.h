@@ -43,7 +43,9 @@ static constexpr uint64_t kExp2fTab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__host__ __device__ inline float expf_glibc(float x) {
+// `sel` maps the table index (identity, or made wave-uniform on the device).
+template <class Sel>
+__host__ __device__ inline float expf_glibc_impl(float x, Sel sel) {
   const uint32_t ux = __builtin_bit_cast(uint32_t, x);
   const uint32_t abstop = (ux >> 20) & 0x7ffu;
   if (abstop >= 0x42bu) {  // |x| >= 88 or NaN (0x42b = top 12 bits of 88.0f)
@@ -59,7 +61,7 @@ __host__ __device__ inline float expf_glibc(float x) {
   const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
   kd -= shift;
   const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-  const double s = __builtin_bit_cast(double, kExp2fTab[ki & 31u] + (ki << 47));
+  const double s = __builtin_bit_cast(double, kExp2fTab[sel(uint32_t(ki & 31u))] + (ki << 47));
   const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);
   const double c1 = 0x1.ebfce50fac4f3p-3 / (32.0 * 32.0);
   const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
@@ -67,6 +69,17 @@ __host__ __device__ inline float expf_glibc(float x) {
   double y = __builtin_fma(c2, r, 1.0);
   y = __builtin_fma(z, r * r, y);
   return static_cast<float>(y * s);
+}
+
+__host__ __device__ inline float expf_glibc(float x) {
+  return expf_glibc_impl(x, [](uint32_t i) { return i; });
+}
+
+// For an x that is the same in every lane of the wave (a GEMV epilogue after
+// a wave reduction): the table index is made wave-uniform, so the entry is a
+// scalar-cache load instead of a vector load at the kernel's tail.
+__device__ inline float expf_glibc_wave(float x) {
+  return expf_glibc_impl(x, [](uint32_t i) { return uint32_t(__builtin_amdgcn_readfirstlane(int(i))); });
 }
 
 }  // namespace s2

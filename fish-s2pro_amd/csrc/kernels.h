@@ -298,8 +298,9 @@ hipError_t launch_tile_f16(const uint16_t* src, uint32_t K, uint32_t M, uint32_t
                            uint16_t* dst, hipStream_t s);
 // y[n][m] (op)= sum_k W[m][k] xn[n][k] for n < N <= 16, m < M; xn = x, or
 // RMSNorm(x) with gain `norm`; epilogues as for launch_gemv.  K % 256 == 0.
-// Activations are split into three f16 parts (any |x| < ~1.3e8 keeps
-// ~2^-22 relative accuracy); a non-finite one sets ERR_F16_RANGE in *err.
+// Each wave scales each column by a power of two from its first activations
+// (any magnitude keeps ~2^-22 relative accuracy); a non-finite activation,
+// or one 2^15 times larger than those, sets ERR_F16_RANGE in *err.
 struct BmmArgs {
   const _Float16* wt;
   const _Float16* wt3;   // second matrix for SwiGLU epilogues

@@ -511,10 +511,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_direct_kernel(GemvArgs a) {
         } else if constexpr (EPI == EPI_RESID) {
           *dst = __fadd_rn(*dst, gsum);
         } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc_wave(-gsum)));
           *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
         } else {
-          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc_wave(-gsum))), u);
         }
       }
     }
@@ -694,10 +694,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_k_kernel(GemvArgs a) {
         } else if constexpr (EPI == EPI_RESID) {
           *dst = __fadd_rn(*dst, gsum);
         } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc_wave(-gsum)));
           *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
         } else {
-          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
+          *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc_wave(-gsum))), u);
         }
       }
     }
@@ -859,10 +859,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
       } else if constexpr (EPI == EPI_RESID) {
         *dst = __fadd_rn(*dst, gsum);
       } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc_wave(-gsum)));
         *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
       } else {
-        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
+        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc_wave(-gsum))), u);
       }
     }
   }
@@ -1130,10 +1130,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
       } else if constexpr (EPI == EPI_RESID) {
         *dst = __fadd_rn(*dst, gsum);
       } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gsum)));
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc_wave(-gsum)));
         *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
       } else {
-        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc(-gsum))), u);
+        *dst = __fmul_rn(__fdiv_rn(gsum, __fadd_rn(1.0f, expf_glibc_wave(-gsum))), u);
       }
     }
   }
