@@ -104,13 +104,14 @@ class Engine {
   int device = 0;
 
   void select() { HIPC(hipSetDevice(device)); }
-  void reset();
-  void eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out);
+  void reset(uint32_t slot = 0);
+  void eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out, uint32_t slot = 0);
   void fast_logits(const float* hidden, const uint32_t* prefix, size_t plen, float* logits);
   void fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampler& smp, uint64_t* rng, uint32_t* codes);
   void generate(uint32_t nseq, const int32_t* const* prompts, const size_t* cols, const s2hip_gen_params& p,
                 uint64_t* rngs, int32_t* const* codes, uint32_t* n_frames, s2hip_gen_stats* stats);
-  uint32_t n_past_host = 0;
+  uint32_t n_past_host[16] = {};  // per KV slot (MAX_SEQS)
+  s2hip_slow_profile slow_prof{};  // last generate call (S2HIP_FLAG_PROFILE)
 
   // op level
   void op_linear(const void* w, uint32_t type, size_t in, size_t out, const float* x, size_t ncol, float* y);
@@ -123,6 +124,7 @@ class Engine {
   void op_swiglu(const float* g, const float* u, size_t n, int fast, float* out);
   void op_running_sums(const float* terms, size_t n, float* prefix, float* total);
   void op_expf(const float* x, size_t n, float* y);
+  void op_embed(const int32_t* flat, size_t n_tok, float* out);
   void op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
                  uint32_t* tok);
   void time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes);
@@ -165,6 +167,7 @@ class Engine {
   void bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx, const float* norm,
            float eps, float* y, uint32_t ldy, const uint32_t* done, uint32_t* err, uint32_t waves = 0);
   void validate_prompt(const int32_t* prompt, size_t cols);
+  void validate_tokens(const int32_t* flat, size_t n_tok);
   void mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
           uint32_t n, uint32_t npad, float* y, uint32_t ldy);
   // batched columns (3..16): split planes + skinny MFMA product
@@ -180,6 +183,13 @@ class Engine {
 
   hipStream_t stream_ = nullptr;
   std::vector<void*> allocs_;
+  // S2HIP_FLAG_PROFILE: events between the Slow-AR kernel groups of one frame
+  // (booked after each frame into slow_prof)
+  bool profiling_ = false;
+  std::vector<hipEvent_t> prof_ev_;
+  std::vector<int> prof_kind_;  // field the interval that ends at event i goes to (-1: none)
+  void prof_mark(int kind);
+  void prof_book(uint32_t nseq);
   uint8_t* staging_[2] = {nullptr, nullptr};
   hipEvent_t staging_ev_[2] = {nullptr, nullptr};
   static constexpr size_t STAGING = 64u << 20;
@@ -467,6 +477,7 @@ Engine::Engine(const s2hip_config& cfg) {
 Engine::~Engine() {
   if (device >= 0) (void)hipSetDevice(device);
   if (stream_) (void)hipStreamSynchronize(stream_);
+  for (hipEvent_t e : prof_ev_) (void)hipEventDestroy(e);
   if (graph_exec_) (void)hipGraphExecDestroy(graph_exec_);
   if (graph_) (void)hipGraphDestroy(graph_);
   for (void* p : allocs_) (void)hipFree(p);
@@ -665,6 +676,38 @@ L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool n
   return w;
 }
 
+enum { PROF_NONE = -1, PROF_LINEAR = 0, PROF_ATTN = 1, PROF_HEAD = 2 };
+
+// Marks the end of the interval since the previous mark; `kind` names what
+// ran in it (PROF_NONE for the first mark of a group).
+void Engine::prof_mark(int kind) {
+  if (!profiling_) return;
+  const size_t i = prof_kind_.size();
+  if (i == prof_ev_.size()) {
+    hipEvent_t e;
+    HIPC(hipEventCreate(&e));
+    prof_ev_.push_back(e);
+  }
+  HIPC(hipEventRecord(prof_ev_[i], stream_));
+  prof_kind_.push_back(kind);
+}
+
+void Engine::prof_book(uint32_t nseq) {
+  if (!profiling_ || prof_kind_.empty()) return;
+  HIPC(hipEventSynchronize(prof_ev_[prof_kind_.size() - 1]));
+  for (size_t i = 1; i < prof_kind_.size(); ++i) {
+    if (prof_kind_[i] == PROF_NONE) continue;
+    float ms = 0.0f;
+    HIPC(hipEventElapsedTime(&ms, prof_ev_[i - 1], prof_ev_[i]));
+    double* f = prof_kind_[i] == PROF_LINEAR ? &slow_prof.linear_ms
+              : prof_kind_[i] == PROF_ATTN   ? &slow_prof.gqa_attention_ms
+                                             : &slow_prof.output_head_ms;
+    *f += ms;
+  }
+  slow_prof.steps += nseq;
+  prof_kind_.clear();
+}
+
 // Slow-AR layers (forward_decode_sequence, slow_ar.rs:539-556) over nseq
 // slots from seq0 with cps consecutive positions each, then n_past += cps per
 // slot.  done (nullable) stops the linears; attention and the position
@@ -676,7 +719,9 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
   DevState* st = st_ + seq0;
   for (uint32_t l = 0; l < s.slow_layers; ++l) {
     const SlowLayer& L = slow_[l];
+    prof_mark(PROF_NONE);
     lin(L.wqkv, nullptr, EPI_STORE, ncol, h_, s.dim, L.attn_norm, s.eps, qkv_, qkv_w, 0, NO_ROW, L.wqkv.out, done);
+    prof_mark(PROF_LINEAR);
     AttnArgs aa{};
     aa.qkv = qkv_;
     aa.q_norm = L.q_norm;
@@ -708,9 +753,11 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, merge ? warm_split_ : 100);
     if (merge) aa.warm2 = warm_for(L.wo, nullptr, ncol, false, warm_split_, 100);
     HIPC(launch_attention(aa, stream_));
+    prof_mark(PROF_ATTN);
     lin(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.wo.out, done);
     lin(L.w1, &L.w3, EPI_SWIGLU_SLOW, ncol, h_, s.dim, L.ffn_norm, s.eps, act_, s.ffn, 0, NO_ROW, L.w1.out, done);
     lin(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.w2.out, done);
+    prof_mark(PROF_LINEAR);
   }
   HIPC(launch_add_position(st, cps, nseq, stream_));
 }
@@ -839,7 +886,9 @@ void Engine::enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_st
   ea.warm = warm_for(slow_[0].wqkv, nullptr, nseq, true, 0, warm_step_);
   HIPC(launch_embed(ea, stream_));
   enqueue_slow_layers(nseq, 1, 0, done);
+  prof_mark(PROF_NONE);
   enqueue_head(nseq, hn_, logits_c_, false, done);
+  prof_mark(PROF_HEAD);
   SampleArgs sa{};
   sa.logits = logits_c_;
   sa.ids = head_rows_;
@@ -1040,22 +1089,29 @@ void Engine::ensure_codes(size_t n_int) {
 void Engine::ensure_slots(uint32_t n) {
   if (n <= kv_slots_) return;
   HIPC(hipStreamSynchronize(stream_));
-  for (float** p : {&kc_, &vc_, &fkc_, &fvc_}) {
+  // the Slow-AR caches grow with the existing slots' contents kept (slot-major
+  // layout: the old buffer is a prefix of the new one); the Fast-AR caches are
+  // per-frame scratch
+  const size_t eb = kv_f16_ ? 2 : 4;
+  const size_t old_bytes = size_t(kv_slots_) * slot_kv_ * eb, kv_bytes = size_t(n) * slot_kv_ * eb;
+  for (float** p : {&kc_, &vc_}) {
+    float* nb = dalloc<float>((kv_bytes + 3) / 4);
+    HIPC(hipMemset(nb, 0, kv_bytes));
+    if (*p) {
+      HIPC(hipMemcpy(nb, *p, old_bytes, hipMemcpyDeviceToDevice));
+      HIPC(hipFree(*p));
+      allocs_.erase(std::find(allocs_.begin(), allocs_.end(), static_cast<void*>(*p)));
+    }
+    *p = nb;
+  }
+  for (float** p : {&fkc_, &fvc_}) {
     if (*p) {
       HIPC(hipFree(*p));
       allocs_.erase(std::find(allocs_.begin(), allocs_.end(), static_cast<void*>(*p)));
-      *p = nullptr;
     }
+    *p = dalloc<float>(size_t(n) * fslot_kv_);
+    HIPC(hipMemset(*p, 0, size_t(n) * fslot_kv_ * 4));
   }
-  const size_t kv_bytes = n * slot_kv_ * (kv_f16_ ? 2 : 4);
-  kc_ = dalloc<float>((kv_bytes + 3) / 4);
-  vc_ = dalloc<float>((kv_bytes + 3) / 4);
-  fkc_ = dalloc<float>(n * fslot_kv_);
-  fvc_ = dalloc<float>(n * fslot_kv_);
-  HIPC(hipMemset(kc_, 0, kv_bytes));
-  HIPC(hipMemset(vc_, 0, kv_bytes));
-  HIPC(hipMemset(fkc_, 0, n * fslot_kv_ * 4));
-  HIPC(hipMemset(fvc_, 0, n * fslot_kv_ * 4));
   kv_slots_ = n;
   ++kv_gen_;
 }
@@ -1111,22 +1167,20 @@ void Engine::check_state_err(uint32_t nseq) {
   }
 }
 
-void Engine::reset() {
+void Engine::reset(uint32_t slot) {
   select();
+  if (slot >= MAX_SEQS) fail("slot " + std::to_string(slot) + " out of range (0.." + std::to_string(MAX_SEQS - 1) + ")");
   HIPC(hipStreamSynchronize(stream_));
-  HIPC(hipMemsetAsync(st_, 0, sizeof(DevState), stream_));
+  HIPC(hipMemsetAsync(st_ + slot, 0, sizeof(DevState), stream_));
   HIPC(hipStreamSynchronize(stream_));
-  n_past_host = 0;
+  n_past_host[slot] = 0;
 }
 
-void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out) {
-  select();
+// Token ids of a time-major [n_tok][num_codebooks + 1] block, checked as
+// embed_slow_ar_time_major does (slow_ar.rs:1041-1133).
+void Engine::validate_tokens(const int32_t* flat, size_t n_tok) {
   const s2hip_spec& s = spec;
   const uint32_t cdim = s.num_codebooks + 1;
-  if (n_tok == 0) fail("expected at least one token");
-  if (n_past_host + n_tok > s.max_seq_len)
-    fail("KV cache overflow: n_past=" + std::to_string(n_past_host) + " n_tokens=" + std::to_string(n_tok) +
-         " max_seq_len=" + std::to_string(s.max_seq_len));
   for (size_t t = 0; t < n_tok; ++t) {
     const int32_t id = flat[t * cdim];
     if (id < 0) fail("semantic token id must be non-negative, got " + std::to_string(id));
@@ -1137,19 +1191,35 @@ void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* l
             uint64_t(flat[t * cdim + 1 + cb]) + uint64_t(cb) * s.codebook_size >= cb_rows_)
           fail("codebook token out of range");
   }
+}
+
+void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* logits_out, uint32_t slot) {
+  select();
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  if (slot >= MAX_SEQS) fail("slot " + std::to_string(slot) + " out of range (0.." + std::to_string(MAX_SEQS - 1) + ")");
+  if (n_tok == 0) fail("expected at least one token");
+  if (n_past_host[slot] + n_tok > s.max_seq_len)
+    fail("KV cache overflow: n_past=" + std::to_string(n_past_host[slot]) + " n_tokens=" + std::to_string(n_tok) +
+         " max_seq_len=" + std::to_string(s.max_seq_len));
+  validate_tokens(flat, n_tok);
+  ensure_slots(slot + 1);
   ensure_prompt(n_tok * cdim);
   HIPC(hipMemcpyAsync(prompt_dev_, flat, n_tok * cdim * 4, hipMemcpyHostToDevice, stream_));
   // done = 0, err = 0 (eval never runs under a finished frame loop)
-  HIPC(hipMemsetAsync(&st_->done, 0, sizeof(uint32_t), stream_));
-  HIPC(hipMemsetAsync(&st_->err, 0, sizeof(uint32_t), stream_));
-  enqueue_prefill(prompt_dev_, n_tok, 0);
+  HIPC(hipMemsetAsync(&st_[slot].done, 0, sizeof(uint32_t), stream_));
+  HIPC(hipMemsetAsync(&st_[slot].err, 0, sizeof(uint32_t), stream_));
+  enqueue_prefill(prompt_dev_, n_tok, slot);
   enqueue_head(1, hn_, logits_c_, logits_out != nullptr, nullptr);
   HIPC(hipMemcpyAsync(hidden_out, hn_, s.dim * 4, hipMemcpyDeviceToHost, stream_));
   if (logits_out) HIPC(hipMemcpyAsync(logits_out, logits_full_, size_t(s.vocab) * 4, hipMemcpyDeviceToHost, stream_));
-  HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(st_host_ + slot, st_ + slot, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
-  check_state_err();
-  n_past_host += uint32_t(n_tok);
+  const uint32_t e = st_host_[slot].err;
+  if (e & ERR_TOKEN_RANGE) fail("token id out of range");
+  if (e & ERR_KV_OVERFLOW) fail("KV cache overflow");
+  if (e & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
+  n_past_host[slot] += uint32_t(n_tok);
 }
 
 void Engine::fast_logits(const float* hidden, const uint32_t* prefix, size_t plen, float* logits) {
@@ -1288,10 +1358,15 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   // ERR_KV_OVERFLOW on the device and the call fails, as SlowArState::eval does
   // (slow_ar.rs:469-474).
   const uint32_t max_frames = p.max_new_tokens;
-  bool use_graph = !(flags_ & S2HIP_FLAG_NO_GRAPH);
+  const bool profile = (flags_ & S2HIP_FLAG_PROFILE) != 0;
+  bool use_graph = !(flags_ & S2HIP_FLAG_NO_GRAPH) && !profile;
+  slow_prof = s2hip_slow_profile{};
+  profiling_ = profile;
+  prof_kind_.clear();
   uint32_t launched = 0;
   if (max_frames > 0) {
     enqueue_frame(cfg, nseq, ncodes);  // frame 0 eagerly (also configures every kernel)
+    prof_book(nseq);
     launched = 1;
   }
   if (use_graph && launched < max_frames) {
@@ -1332,12 +1407,14 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   int slot = 0;
   bool finished = false;
   while (launched < max_frames && !finished) {
-    const uint32_t n = std::min(FRAME_BATCH, max_frames - launched);
+    const uint32_t n = std::min(profile ? 1u : FRAME_BATCH, max_frames - launched);
     for (uint32_t i = 0; i < n; ++i) {
-      if (use_graph)
+      if (use_graph) {
         HIPC(hipGraphLaunch(graph_exec_, stream_));
-      else
+      } else {
         enqueue_frame(cfg, nseq, ncodes);
+        prof_book(nseq);
+      }
     }
     launched += n;
     HIPC(hipMemcpyAsync(&done_host_[slot], &batch_->done_all, 4, hipMemcpyDeviceToHost, stream_));
@@ -1350,6 +1427,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
     slot ^= 1;
   }
   HIPC(hipEventRecord(ev[2], stream_));
+  profiling_ = false;
   HIPC(hipMemcpyAsync(st_host_, st_, nseq * sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
   for (auto& e : flag_ev) (void)hipEventDestroy(e);
@@ -1371,7 +1449,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
     rngs[b] = st_host_[b].rng;
     total += nf;
   }
-  n_past_host = st_host_[0].n_past;  // the engine's sequence state is request 0's
+  for (uint32_t b = 0; b < nseq; ++b) n_past_host[b] = st_host_[b].n_past;  // request b's state is slot b's
   if (stats) {
     stats->prefill_ms = ms_prefill;
     stats->decode_ms = ms_decode;
@@ -1582,6 +1660,40 @@ void Engine::op_running_sums(const float* terms, size_t n, float* prefix, float*
   HIPC(hipMemcpyAsync(prefix, dp.p, n * 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipMemcpyAsync(total, ds.p, 4, hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
+}
+
+void Engine::op_embed(const int32_t* flat, size_t n_tok, float* out) {
+  select();
+  const s2hip_spec& s = spec;
+  const uint32_t cdim = s.num_codebooks + 1;
+  if (n_tok == 0) return;
+  if (n_tok > 65535) fail("embed supports at most 65535 tokens per call");
+  validate_tokens(flat, n_tok);
+  TmpBuf dt(n_tok * cdim * 4), dh(n_tok * s.dim * 4), de(4);
+  HIPC(hipMemcpyAsync(dt.p, flat, n_tok * cdim * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemsetAsync(de.p, 0, 4, stream_));
+  EmbedArgs ea{};
+  ea.tokens = dt.as<int32_t>();
+  ea.emb = emb_;
+  ea.cb_emb = cb_emb_;
+  ea.h = dh.as<float>();
+  ea.n = uint32_t(n_tok);
+  ea.dim = s.dim;
+  ea.vocab = s.vocab;
+  ea.cb_rows = uint32_t(cb_rows_);
+  ea.num_codebooks = s.num_codebooks;
+  ea.codebook_size = s.codebook_size;
+  ea.sem_begin = s.semantic_begin;
+  ea.sem_end = s.semantic_end;
+  ea.sem_scale = 1.0f / std::sqrt(float(s.num_codebooks + 1));  // scale_codebook_embeddings (registry.rs:94-97)
+  ea.scale_enabled = s.scale_codebook_embeddings;
+  ea.err = de.as<uint32_t>();
+  HIPC(launch_embed(ea, stream_));
+  uint32_t e = 0;
+  HIPC(hipMemcpyAsync(out, dh.p, n_tok * s.dim * 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(&e, de.p, 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  if (e) fail("token id out of range");
 }
 
 void Engine::op_expf(const float* x, size_t n, float* y) {
@@ -1875,7 +1987,43 @@ int32_t s2hip_reset(s2hip_engine* engine, char* err, size_t err_cap) {
   return guarded(err, err_cap, [&] { engine->e->reset(); });
 }
 
-uint32_t s2hip_n_past(const s2hip_engine* engine) { return engine ? engine->e->n_past_host : 0u; }
+uint32_t s2hip_n_past(const s2hip_engine* engine) { return engine ? engine->e->n_past_host[0] : 0u; }
+
+int32_t s2hip_last_slow_profile(const s2hip_engine* engine, s2hip_slow_profile* out) {
+  if (!engine || !out) return 0;
+  *out = engine->e->slow_prof;
+  return 1;
+}
+
+int32_t s2hip_reset_slot(s2hip_engine* engine, uint32_t slot, char* err, size_t err_cap) {
+  if (!engine) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->reset(slot); });
+}
+
+uint32_t s2hip_n_past_slot(const s2hip_engine* engine, uint32_t slot) {
+  return engine && slot < 16 ? engine->e->n_past_host[slot] : 0u;
+}
+
+int32_t s2hip_eval_slot(s2hip_engine* engine, uint32_t slot, const int32_t* flat, size_t n_tokens, float* hidden_out,
+                        float* logits_out, char* err, size_t err_cap) {
+  if (!engine || !flat || !hidden_out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->eval(flat, n_tokens, hidden_out, logits_out, slot); });
+}
+
+int32_t s2hip_op_embed(s2hip_engine* engine, const int32_t* flat, size_t n_tokens, float* out, char* err,
+                       size_t err_cap) {
+  if (!engine || (n_tokens && (!flat || !out))) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_embed(flat, n_tokens, out); });
+}
 
 int32_t s2hip_eval(s2hip_engine* engine, const int32_t* flat, size_t n_tokens, float* hidden_out, float* logits_out,
                    char* err, size_t err_cap) {

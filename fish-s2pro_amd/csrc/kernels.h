@@ -36,6 +36,23 @@ struct DevState {
 enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u, ERR_F16_RANGE = 8u };
 constexpr uint32_t NO_ROW = 0xffffffffu;
 
+// Weight rows of the GEMV launched next, read into L2 by extra blocks of a
+// latency-bound kernel (decode attention) while HBM would otherwise idle.
+// GEMV block cb covers bytes [cb span, cb span + span) from base (and from
+// base3) and runs on XCD cb % 8: workgroups go to the 8 XCDs round-robin by
+// linear index, each XCD with its own L2.  The warming block at linear index
+// L reads only consumer blocks with cb % 8 == L % 8, so each row lands in the
+// L2 that reads it next.  Reads only: a different mapping costs bandwidth,
+// never results.
+struct L2Warm {
+  const uint8_t* base;   // nullptr: no warming blocks
+  const uint8_t* base3;  // nullable: second matrix, same layout (w3 of SwiGLU)
+  uint32_t span;         // bytes per consumer block, multiple of 16
+  uint32_t cb_begin;     // consumer blocks [cb_begin, cb_end) are warmed;
+  uint32_t cb_end;       //   cb_begin is a multiple of 8
+  uint32_t blocks;       // warming blocks, multiple of 8
+  uint32_t depth;        // 16-byte loads per thread in flight: 4, 8 or 16
+};
 struct GemvArgs {
   const uint8_t* w;      // weight rows
   const uint8_t* w3;     // second matrix for SwiGLU epilogues (same shape)
@@ -101,23 +118,6 @@ struct QkvPostArgs {
 };
 hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 
-// Weight rows of the GEMV launched next, read into L2 by extra blocks of a
-// latency-bound kernel (decode attention) while HBM would otherwise idle.
-// GEMV block cb covers bytes [cb span, cb span + span) from base (and from
-// base3) and runs on XCD cb % 8: workgroups go to the 8 XCDs round-robin by
-// linear index, each XCD with its own L2.  The warming block at linear index
-// L reads only consumer blocks with cb % 8 == L % 8, so each row lands in the
-// L2 that reads it next.  Reads only: a different mapping costs bandwidth,
-// never results.
-struct L2Warm {
-  const uint8_t* base;   // nullptr: no warming blocks
-  const uint8_t* base3;  // nullable: second matrix, same layout (w3 of SwiGLU)
-  uint32_t span;         // bytes per consumer block, multiple of 16
-  uint32_t cb_begin;     // consumer blocks [cb_begin, cb_end) are warmed;
-  uint32_t cb_end;       //   cb_begin is a multiple of 8
-  uint32_t blocks;       // warming blocks, multiple of 8
-  uint32_t depth;        // 16-byte loads per thread in flight: 4, 8 or 16
-};
 // Warming planes a kernel of `plane` blocks per plane appends for w (0 when
 // w.base is null); hipErrorInvalidValue in *err for a malformed descriptor.
 uint32_t l2_warm_planes(const L2Warm& w, uint32_t plane, hipError_t* err);

@@ -715,6 +715,55 @@ hipError_t gemv_k_launch(const GemvArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Warming block r (of w.blocks) at linear grid index L: consumer blocks
+// cb = cb_begin + 8 q + (L % 8) for q = r / 8, r / 8 + blocks / 8, ...  The
+// block's loads (per consumer block and matrix, `per` loads of 16 bytes per
+// thread) are walked as one list, D distinct loads per thread in flight; the
+// walk position is uniform over the block (scalar registers) and past the end
+// of the list stays on the last load.
+template <int D>
+__device__ __forceinline__ void l2_warm_walk(const L2Warm& w, uint32_t L, uint32_t r, uint32_t tid, uint32_t nthr) {
+  const uint32_t stride = nthr * 16u;
+  const uint32_t per = (w.span + stride - 1) / stride;
+  const uint32_t mats = w.base3 ? 2u : 1u;
+  const uint32_t cb0 = w.cb_begin + 8u * (r >> 3) + (L & 7u);
+  if (cb0 >= w.cb_end) return;
+  const uint32_t total = (w.cb_end - cb0 + w.blocks - 1) / w.blocks * mats * per;
+  const uint32_t off0 = tid * 16u, last = w.span - 16u;
+  uint32_t i = 0, m = 0, j = 0, acc = 0;
+  for (uint32_t u0 = 0; u0 < total; u0 += D) {
+    uint32_t v[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const uint8_t* p = (m ? w.base3 : w.base) + size_t(cb0 + i * w.blocks) * w.span;
+      // one word per 16 bytes: every 64-byte sector of the rows is read
+      v[k] = *reinterpret_cast<const uint32_t*>(p + min(off0 + j * stride, last));
+      if (u0 + k + 1 < total) {
+        if (++j == per) {
+          j = 0;
+          if (++m == mats) {
+            m = 0;
+            ++i;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k) acc ^= v[k];
+  }
+  asm volatile("" : : "v"(acc));  // the loads are kept; nothing is stored
+}
+
+__device__ __forceinline__ void l2_warm(const L2Warm& w, uint32_t L, uint32_t r, uint32_t tid, uint32_t nthr) {
+  if (r >= w.blocks) return;
+  if (w.depth >= 16)
+    l2_warm_walk<16>(w, L, r, tid, nthr);
+  else if (w.depth >= 8)
+    l2_warm_walk<8>(w, L, r, tid, nthr);
+  else
+    l2_warm_walk<4>(w, L, r, tid, nthr);
+}
+
 // ---------------------------------------------------------------------------
 // Decode GEMV with x shared through LDS (NORM: RMS-normalised input).
 //   Each wave loads only the 512-element steps k = wave (mod WPB) of x and of
@@ -1212,54 +1261,6 @@ __global__ __launch_bounds__(256) void repack_q_kernel(const uint8_t* rows, size
 
 bool gemv_k_supported(uint32_t in) { return in == 512 || in == 1536 || in == 2560 || in == 4096 || in == 9728; }
 
-// Warming block r (of w.blocks) at linear grid index L: consumer blocks
-// cb = cb_begin + 8 q + (L % 8) for q = r / 8, r / 8 + blocks / 8, ...  The
-// block's loads (per consumer block and matrix, `per` loads of 16 bytes per
-// thread) are walked as one list, D distinct loads per thread in flight; the
-// walk position is uniform over the block (scalar registers) and past the end
-// of the list stays on the last load.
-template <int D>
-__device__ __forceinline__ void l2_warm_walk(const L2Warm& w, uint32_t L, uint32_t r, uint32_t tid, uint32_t nthr) {
-  const uint32_t stride = nthr * 16u;
-  const uint32_t per = (w.span + stride - 1) / stride;
-  const uint32_t mats = w.base3 ? 2u : 1u;
-  const uint32_t cb0 = w.cb_begin + 8u * (r >> 3) + (L & 7u);
-  if (cb0 >= w.cb_end) return;
-  const uint32_t total = (w.cb_end - cb0 + w.blocks - 1) / w.blocks * mats * per;
-  const uint32_t off0 = tid * 16u, last = w.span - 16u;
-  uint32_t i = 0, m = 0, j = 0, acc = 0;
-  for (uint32_t u0 = 0; u0 < total; u0 += D) {
-    uint32_t v[D];
-#pragma unroll
-    for (int k = 0; k < D; ++k) {
-      const uint8_t* p = (m ? w.base3 : w.base) + size_t(cb0 + i * w.blocks) * w.span;
-      // one word per 16 bytes: every 64-byte sector of the rows is read
-      v[k] = *reinterpret_cast<const uint32_t*>(p + min(off0 + j * stride, last));
-      if (u0 + k + 1 < total) {
-        if (++j == per) {
-          j = 0;
-          if (++m == mats) {
-            m = 0;
-            ++i;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < D; ++k) acc ^= v[k];
-  }
-  asm volatile("" : : "v"(acc));  // the loads are kept; nothing is stored
-}
-
-__device__ __forceinline__ void l2_warm(const L2Warm& w, uint32_t L, uint32_t r, uint32_t tid, uint32_t nthr) {
-  if (r >= w.blocks) return;
-  if (w.depth >= 16)
-    l2_warm_walk<16>(w, L, r, tid, nthr);
-  else if (w.depth >= 8)
-    l2_warm_walk<8>(w, L, r, tid, nthr);
-  else
-    l2_warm_walk<4>(w, L, r, tid, nthr);
-}
 
 // ---------------------------------------------------------------------------
 // RMSNorm over `ncol` vectors (one block per column).
@@ -1417,7 +1418,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
   __shared__ float ps[GEMV_WAVES][CH];
   __shared__ float knew[4][HD], vnew[4][HD];
   __shared__ uint32_t is_last;
-  if (blockIdx.z >= ncol) {  // warming planes after the attention blocks
+  if (__builtin_expect(blockIdx.z >= ncol, 0)) {  // warming planes after the attention blocks (laid out last)
     const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
     l2_warm(a.warm, L, L - gridDim.x * gridDim.y * ncol, threadIdx.x, 256u);
     return;
@@ -1659,7 +1660,7 @@ template <int HD, int CH, int MAXC>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, float* out, const uint32_t* pos_ptr,
                                                             const uint32_t* done_ptr, uint32_t ncol, uint32_t max_chunks,
                                                             uint32_t shape, uint32_t pos_offset, AttnArgs a) {
-  if (blockIdx.y >= ncol) {  // warming planes after the merge blocks
+  if (__builtin_expect(blockIdx.y >= ncol, 0)) {  // warming planes after the merge blocks (laid out last)
     const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
     l2_warm(a.warm2, L, L - gridDim.x * ncol, threadIdx.x, HD);
     return;
@@ -1750,7 +1751,7 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, flo
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs a) {
   const uint32_t chunks = (a.dim + 255) / 256;
-  if (blockIdx.y >= chunks) {  // warming rows after the embedding blocks
+  if (__builtin_expect(blockIdx.y >= chunks, 0)) {  // warming rows after the embedding blocks (laid out last)
     const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
     l2_warm(a.warm, L, L - gridDim.x * chunks, threadIdx.x, 256u);
     return;
@@ -2413,7 +2414,7 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_fast_kernel(SampleArgs 
   extern __shared__ uint8_t smem_raw[];
   SampleShared& sh = *reinterpret_cast<SampleShared*>(smem_raw);
   const uint32_t nseq = a.n_seq ? a.n_seq : 1u;
-  if (blockIdx.x >= nseq) {  // warming blocks after the sampling blocks
+  if (__builtin_expect(blockIdx.x >= nseq, 0)) {  // warming blocks after the sampling blocks (laid out last)
     l2_warm(a.warm, blockIdx.x, blockIdx.x - nseq, threadIdx.x, SAMPLE_THREADS);
     return;
   }

@@ -5,5 +5,5 @@ include/s2hip.h); this package is its host-side binding plus the seeded
 synthetic-model writer.
 """
 
-from .engine import Engine, S2HipError, version  # noqa: F401
+from .engine import Engine, S2HipError, transpose_to_time_major, version  # noqa: F401
 from . import synth  # noqa: F401

@@ -64,6 +64,13 @@ class GenStats(ctypes.Structure):
 
 FLAG_NO_GRAPH = 1
 FLAG_KV_F16 = 2
+FLAG_PROFILE = 4
+
+
+class SlowProfile(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in ("rms_norm_ms", "linear_ms", "gqa_attention_ms", "rope_ms",
+                                               "kv_write_ms", "swiglu_ms", "output_head_ms")] + [
+        ("steps", ctypes.c_uint32)]
 
 _lib = None
 
@@ -114,6 +121,14 @@ def load():
                                   ctypes.POINTER(u32), cp, sz]
     L.s2hip_op_running_sums.argtypes = [vp, vp, sz, vp, ctypes.POINTER(f32), cp, sz]
     L.s2hip_op_expf.argtypes = [vp, vp, sz, vp, cp, sz]
+    L.s2hip_op_embed.argtypes = [vp, vp, sz, vp, cp, sz]
+    L.s2hip_last_slow_profile.argtypes = [vp, ctypes.POINTER(SlowProfile)]
+    L.s2hip_last_slow_profile.restype = i32
+    L.s2hip_reset_slot.argtypes = [vp, u32, cp, sz]
+    L.s2hip_n_past_slot.argtypes = [vp, u32]
+    L.s2hip_n_past_slot.restype = u32
+    L.s2hip_eval_slot.argtypes = [vp, u32, vp, sz, vp, vp, cp, sz]
+    L.s2hip_transpose_to_time_major.argtypes = [vp, sz, u32, sz, vp, cp, sz]
     L.s2hip_expf_host.argtypes = [vp, sz, vp]
     L.s2hip_expf_host.restype = None
     L.s2hip_time_kernel.argtypes = [vp, cp, u32, ctypes.POINTER(ctypes.c_double),
@@ -123,7 +138,8 @@ def load():
                  "s2hip_op_linear",
                  "s2hip_op_rms_norm", "s2hip_op_dequant_rows", "s2hip_op_qk_rope",
                  "s2hip_op_attention", "s2hip_op_swiglu", "s2hip_op_sample", "s2hip_op_running_sums",
-                 "s2hip_op_expf", "s2hip_time_kernel"):
+                 "s2hip_op_expf", "s2hip_op_embed", "s2hip_reset_slot", "s2hip_eval_slot",
+                 "s2hip_transpose_to_time_major", "s2hip_time_kernel"):
         getattr(L, name).restype = i32
     _lib = L
     return L

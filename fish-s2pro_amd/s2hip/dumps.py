@@ -75,22 +75,37 @@ def semantic_sample(engine: Engine, logits, generated_after_prefill: int, min_to
     build_semantic_bias / apply_semantic_bias (sampling.rs:54-100) leave the
     semantic ids and im_end finite and every other logit -inf; im_end is
     masked too while generated_after_prefill < min_tokens_before_end, and is
-    the force-included id otherwise.  The masked ids are dropped before
-    sampling: the remaining candidates keep their ascending-id order, so the
-    stable descending sort, top-k, softmax and top-p see the same finite
-    values in the same order.  Returns (token id, new RNG state)."""
+    the force-included id otherwise.  The sampler runs on the finite
+    candidates in ascending-id order (the stable descending sort, top-k,
+    softmax and top-p see the same finite values in the same order) plus, when
+    the reference's list reaches into the masked ids, the one masked id its
+    list would end with: the -inf entries sort last in ascending-id order and
+    add nothing to any sum, so the only way one is drawn is the fall-through
+    of sample_discrete (sampling.rs:227-241), which returns the list's last
+    entry.  Returns (token id, new RNG state)."""
     sp = engine.spec
     im_end = engine.im_end_id
+    vocab = sp["vocab"]
     block = generated_after_prefill < min_tokens_before_end
     ids = np.arange(sp["semantic_begin"], sp["semantic_end"] + 1, dtype=np.int64)
     if block:
         ids = ids[ids != im_end]
-    elif im_end < sp["vocab"]:
+    elif im_end < vocab:
         ids = np.union1d(ids, np.array([im_end], np.int64))
     force = None
-    if not block and im_end < sp["vocab"]:
+    if not block and im_end < vocab:
         force = int(np.searchsorted(ids, im_end))
-    sub = np.ascontiguousarray(np.asarray(logits, np.float32)[ids])
+    sub = np.asarray(logits, np.float32)[ids]
+    n_fin = int(np.isfinite(sub).sum())
+    n_list = min(top_k, vocab) if top_k > 0 else vocab  # entries after top-k (before force-include)
+    if n_list > n_fin and n_fin == ids.size:
+        # the masked entry at the end of the reference's list: the
+        # (n_list - n_fin)-th masked id in ascending order
+        k = n_list - n_fin - 1
+        masked = np.setdiff1d(np.arange(vocab, dtype=np.int64), ids, assume_unique=True)
+        ids = np.append(ids, masked[k])
+        sub = np.append(sub, np.float32(-np.inf))
+    sub = np.ascontiguousarray(sub, np.float32)
     idx, rng = engine.sample(sub, temperature, top_p, top_k, force, rng_state)
     return int(ids[idx]), rng
 

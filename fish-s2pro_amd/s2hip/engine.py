@@ -31,10 +31,13 @@ def _f32(a) -> np.ndarray:
 
 class Engine:
     def __init__(self, gguf_path: str, max_seq_len: int, im_end_id: int, device: int = 0,
-                 use_graph: bool = True, kv_f16: bool = False):
-        """kv_f16: store the Slow-AR KV cache as f16 (S2HIP_FLAG_KV_F16)."""
+                 use_graph: bool = True, kv_f16: bool = False, profile: bool = False):
+        """kv_f16: store the Slow-AR KV cache as f16 (S2HIP_FLAG_KV_F16).
+        profile: collect the SlowArDecodeProfile counterpart of each generate
+        call (S2HIP_FLAG_PROFILE; frames then run without graph replay)."""
         L = _lib.load()
-        flags = (0 if use_graph else _lib.FLAG_NO_GRAPH) | (_lib.FLAG_KV_F16 if kv_f16 else 0)
+        flags = ((0 if use_graph else _lib.FLAG_NO_GRAPH) | (_lib.FLAG_KV_F16 if kv_f16 else 0) |
+                 (_lib.FLAG_PROFILE if profile else 0))
         cfg = _lib.Config(gguf_path.encode(), max_seq_len, im_end_id, device, flags)
         err = ctypes.create_string_buffer(_lib.ERR_CAP)
         h = L.s2hip_create(ctypes.byref(cfg), err, len(err))
@@ -72,12 +75,50 @@ class Engine:
             raise S2HipError(err.value.decode())
 
     # -- SlowArState ----------------------------------------------------------
-    def reset(self):
-        self._call(self._L.s2hip_reset)
+    def reset(self, slot: int = 0):
+        """SlowArState::reset (slow_ar.rs:434-438) of KV slot `slot`."""
+        if slot == 0:
+            self._call(self._L.s2hip_reset)
+        else:
+            self._call(self._L.s2hip_reset_slot, slot)
 
     @property
     def n_past(self) -> int:
         return int(self._L.s2hip_n_past(self._h))
+
+    def last_slow_profile(self) -> dict:
+        """SlowArDecodeProfile (slow_ar.rs:248-319) of the last generate call, in
+        milliseconds per operation (all zero without profile=True)."""
+        p = _lib.SlowProfile()
+        self._L.s2hip_last_slow_profile(self._h, ctypes.byref(p))
+        return {f[0]: getattr(p, f[0]) for f in _lib.SlowProfile._fields_}
+
+    def n_past_slot(self, slot: int) -> int:
+        return int(self._L.s2hip_n_past_slot(self._h, slot))
+
+    def eval_slot(self, slot: int, flat_tokens, want_logits: bool = True):
+        """eval on KV slot `slot` (0..15); slot 0 is the state eval uses."""
+        flat = np.ascontiguousarray(flat_tokens, dtype=np.int32).ravel()
+        if flat.size % self.codebook_dim:
+            raise S2HipError(
+                f"flat token length {flat.size} is not a multiple of codebook_dim {self.codebook_dim}")
+        hidden = np.zeros(self.spec["dim"], np.float32)
+        logits = np.zeros(self.spec["vocab"], np.float32) if want_logits else None
+        self._call(self._L.s2hip_eval_slot, slot, _p(flat), flat.size // self.codebook_dim, _p(hidden),
+                   _p(logits) if want_logits else None)
+        return hidden, logits
+
+    def embed(self, flat_tokens):
+        """embed_slow_ar_time_major (slow_ar.rs:1041-1133) on the device:
+        [n_tokens][dim] f32 for time-major flat ids."""
+        flat = np.ascontiguousarray(flat_tokens, dtype=np.int32).ravel()
+        if flat.size % self.codebook_dim:
+            raise S2HipError(
+                f"flat token length {flat.size} is not a multiple of codebook_dim {self.codebook_dim}")
+        n = flat.size // self.codebook_dim
+        out = np.zeros((n, self.spec["dim"]), np.float32)
+        self._call(self._L.s2hip_op_embed, _p(flat), n, _p(out))
+        return out
 
     def eval(self, flat_tokens, want_logits: bool = True):
         flat = np.ascontiguousarray(flat_tokens, dtype=np.int32).ravel()
@@ -264,6 +305,20 @@ class Engine:
         nbytes = ctypes.c_double(0)
         self._call(self._L.s2hip_time_kernel, name.encode(), reps, ctypes.byref(avg), ctypes.byref(nbytes))
         return avg.value, nbytes.value
+
+
+def transpose_to_time_major(data, rows: int, cols: int) -> np.ndarray:
+    """transpose_to_time_major (crates/fish_s2_infer/src/prompt.rs:79-103):
+    the codebook-major (rows x cols) prompt tensor of build_prompt to the
+    time-major flat i32 layout the engine takes, flat[t * rows + r] =
+    data[r * cols + t].  Raises S2HipError with the reference's messages."""
+    d = np.ascontiguousarray(data, dtype=np.uint32).ravel()
+    out = np.zeros(max(1, d.size), np.int32)
+    err = ctypes.create_string_buffer(_lib.ERR_CAP)
+    if not _lib.load().s2hip_transpose_to_time_major(_p(d) if d.size else None, d.size, rows, cols, _p(out), err,
+                                                     len(err)):
+        raise S2HipError(err.value.decode())
+    return out[: d.size]
 
 
 def expf_host(x) -> np.ndarray:

@@ -40,6 +40,10 @@ extern "C" {
  * in the layout KvCacheSpec describes (registry.rs:83,292-302).  Results then
  * follow an f32 cache only to about 1e-3; the Fast-AR cache stays f32. */
 #define S2HIP_FLAG_KV_F16 2u
+/* Collect the SlowArDecodeProfile counterpart (s2hip_last_slow_profile):
+ * frames are then launched directly, one at a time, with HIP events between
+ * the Slow-AR kernel groups (slower; for profiling). */
+#define S2HIP_FLAG_PROFILE 4u
 
 typedef struct s2hip_engine s2hip_engine;
 
@@ -89,6 +93,20 @@ typedef struct {
   uint32_t graph_used;
 } s2hip_gen_stats;
 
+/* SlowArDecodeProfile (crates/fish_s2_infer/src/slow_ar.rs:248-319, filled by
+ * generate_codes at generate.rs:129,195 and shown by the GUI at app.rs:664-669):
+ * device time of the Slow-AR decode steps of the last generate call, by
+ * operation, in milliseconds.  The kernels fuse the reference's operations,
+ * so each kernel's time goes to one field: linear = wqkv (with the attention
+ * RMSNorm), wo (+ residual), w1/w3 (with the FFN RMSNorm and SwiGLU) and w2
+ * (+ residual); gqa_attention = QK-norm, RoPE, KV write, attention and the
+ * cross-chunk merge; output_head = final RMSNorm + head rows.  rms_norm,
+ * rope, kv_write and swiglu are 0: they run inside those kernels. */
+typedef struct {
+  double rms_norm_ms, linear_ms, gqa_attention_ms, rope_ms, kv_write_ms, swiglu_ms, output_head_ms;
+  uint32_t steps; /* Slow-AR decode steps (frames x requests) covered */
+} s2hip_slow_profile;
+
 const char* s2hip_version(void);
 
 /* SlowArState::open (crates/fish_s2_infer/src/slow_ar.rs:387-412) +
@@ -103,6 +121,27 @@ int32_t s2hip_get_spec(const s2hip_engine* engine, s2hip_spec* out);
 int32_t s2hip_reset(s2hip_engine* engine, char* err, size_t err_cap);
 /* SlowArState::n_past (slow_ar.rs:418-420). */
 uint32_t s2hip_n_past(const s2hip_engine* engine);
+
+/* The same on KV slot `slot` (0..15).  The engine holds up to 16 independent
+ * sequence states: slot 0 is the one s2hip_reset / s2hip_eval / s2hip_n_past
+ * act on, and request b of s2hip_generate_codes_batch leaves its state in
+ * slot b.  The reference's SlowArState holds one sequence
+ * (slow_ar.rs:372-438); a caller keeping several sequences open (a server
+ * with concurrent requests) uses one slot per sequence. */
+int32_t s2hip_reset_slot(s2hip_engine* engine, uint32_t slot, char* err, size_t err_cap);
+uint32_t s2hip_n_past_slot(const s2hip_engine* engine, uint32_t slot);
+int32_t s2hip_eval_slot(s2hip_engine* engine, uint32_t slot, const int32_t* flat_tokens, size_t n_tokens,
+                        float* hidden_out, float* logits_out, char* err, size_t err_cap);
+
+/* transpose_to_time_major (crates/fish_s2_infer/src/prompt.rs:79-103):
+ * data holds the codebook-major prompt tensor of build_prompt, rows x cols
+ * (row 0 vocabulary ids, rows 1.. codes); flat_out[t * rows + r] =
+ * data[r * cols + t], the layout the entry points below take.  Fails (0) with
+ * the reference's messages when rows == 0, rows * cols overflows or differs
+ * from data_len, or a value does not fit i32.  Host only: no engine, no
+ * device. */
+int32_t s2hip_transpose_to_time_major(const uint32_t* data, size_t data_len, uint32_t rows, size_t cols,
+                                      int32_t* flat_out, char* err, size_t err_cap);
 
 /* SlowArState::prefill / step / eval (slow_ar.rs:440-527): flat_tokens is
  * time-major [n_tokens][num_codebooks + 1].  hidden_out receives the
@@ -131,6 +170,11 @@ int32_t s2hip_fast_codebooks(s2hip_engine* engine, const float* slow_hidden, uin
 int32_t s2hip_generate_codes(s2hip_engine* engine, const int32_t* prompt_flat, size_t prompt_cols,
                              const s2hip_gen_params* params, uint64_t* rng_state, int32_t* codes_out,
                              uint32_t* n_frames_out, s2hip_gen_stats* stats, char* err, size_t err_cap);
+
+/* The profile of the last s2hip_generate_codes / _batch call on an engine
+ * created with S2HIP_FLAG_PROFILE (all zero otherwise); engine.rs:221
+ * (last_slow_ar_profile). */
+int32_t s2hip_last_slow_profile(const s2hip_engine* engine, s2hip_slow_profile* out);
 
 /* Batched generate_codes: n_requests (1..16) independent requests decoded
  * together, each in its own KV slot, so every frame reads each weight matrix
@@ -193,6 +237,13 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
  * A test hook for the device summation routine. */
 int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,
                               float* total_out, char* err, size_t err_cap);
+
+/* embed_slow_ar_time_major (crates/fish_s2_infer/src/slow_ar.rs:1041-1133):
+ * out[t][dim] = emb[id] (+ the sum of the token's codebook rows, then the
+ * 1/sqrt(num_codebooks + 1) scale, for semantic ids) for flat_tokens
+ * time-major [n_tokens][num_codebooks + 1]; the token checks of eval. */
+int32_t s2hip_op_embed(s2hip_engine* engine, const int32_t* flat_tokens, size_t n_tokens, float* out, char* err,
+                       size_t err_cap);
 
 /* The device exp of the samplers' softmax (sampling.rs:202-225) and the
  * SwiGLU sigmoids (slow_ar.rs:1215-1232, fast_ar.rs:472-485), whose Rust code

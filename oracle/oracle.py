@@ -87,6 +87,7 @@ def lib():
     L.orc_n_past.restype = ctypes.c_uint32
     L.orc_eval.argtypes = [vp, vp, sz, vp, vp, ctypes.c_char_p, sz]
     L.orc_fast_logits.argtypes = [vp, vp, vp, sz, vp, ctypes.c_char_p, sz]
+    L.orc_embed.argtypes = [vp, vp, sz, vp, ctypes.c_char_p, sz]
     L.orc_fast_codebooks.argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_float, ctypes.c_float,
                                      ctypes.c_int32, _u64p, vp, ctypes.c_char_p, sz]
     L.orc_generate_codes.argtypes = [vp, vp, sz, ctypes.c_uint32, ctypes.c_float, ctypes.c_float,
@@ -95,7 +96,7 @@ def lib():
                                      ctypes.c_char_p, sz]
     for name in ("orc_dequant_row", "orc_rms_norm", "orc_rms_norm_heads", "orc_linear",
                  "orc_rope_normal", "orc_gqa_attention", "orc_sample_token", "orc_sample_token_margins",
-                 "orc_transpose_to_time_major", "orc_get_spec", "orc_eval", "orc_fast_logits",
+                 "orc_transpose_to_time_major", "orc_get_spec", "orc_eval", "orc_fast_logits", "orc_embed",
                  "orc_fast_codebooks", "orc_generate_codes"):
         getattr(L, name).restype = ctypes.c_int32
     _lib = L
@@ -280,6 +281,16 @@ class OracleModel:
         if not ok:
             raise RuntimeError(err.value.decode())
         return hidden, logits
+
+    def embed(self, flat_tokens):
+        """embed_slow_ar_time_major alone: [n_tokens][dim]."""
+        flat = np.ascontiguousarray(flat_tokens, np.int32)
+        n = flat.size // (self.spec.num_codebooks + 1)
+        out = np.zeros((n, self.spec.dim), np.float32)
+        err = ctypes.create_string_buffer(1024)
+        if not lib().orc_embed(self._h, _p(flat), n, _p(out), err, len(err)):
+            raise RuntimeError(err.value.decode())
+        return out
 
     def fast_logits(self, hidden, prefix):
         h = np.ascontiguousarray(hidden, np.float32)

@@ -1359,6 +1359,23 @@ int32_t orc_eval(orc_model* m, const int32_t* flat, size_t n_tok, float* hidden,
   }
 }
 
+// embed_slow_ar_time_major (slow_ar.rs:1041-1133) on its own: out [n_tok][dim]
+int32_t orc_embed(orc_model* m, const int32_t* flat, size_t n_tok, float* out, char* err, size_t cap) {
+  try {
+    if (n_tok == 0) return 1;
+    for (size_t t = 0; t < n_tok; ++t) {
+      const int32_t* tok = flat + t * (m->spec.num_codebooks + 1);
+      if (tok[0] >= 0 && uint32_t(tok[0]) >= m->spec.vocab)
+        fail("embedding index %d out of range for vocab_dim %u", tok[0], m->spec.vocab);
+    }
+    embed(m, flat, n_tok, out);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
 int32_t orc_fast_logits(orc_model* m, const float* hidden, const uint32_t* prefix, size_t plen, float* logits,
                         char* err, size_t cap) {
   try {

@@ -97,6 +97,9 @@ uint32_t orc_n_past(const orc_model* m);
 /* hidden_out: post-final-norm hidden [dim]; logits_out: full vocab (nullable) */
 int32_t orc_eval(orc_model* m, const int32_t* flat_tokens, size_t n_tokens, float* hidden_out,
                  float* logits_out, char* err, size_t err_cap);
+/* embed_slow_ar_time_major alone: out [n_tokens][dim] */
+int32_t orc_embed(orc_model* m, const int32_t* flat_tokens, size_t n_tokens, float* out, char* err,
+                  size_t err_cap);
 int32_t orc_fast_logits(orc_model* m, const float* slow_hidden, const uint32_t* prefix,
                         size_t prefix_len, float* logits_out, char* err, size_t err_cap);
 int32_t orc_fast_codebooks(orc_model* m, const float* slow_hidden, uint32_t semantic_code,

@@ -156,3 +156,24 @@ def test_malformed_gguf_headers_fail_by_name(tmp_path):
     p = str(tmp_path / "past.gguf")
     open(p, "wb").write(bad)
     assert "a.weight extends past file end" in _create_err(p)
+
+
+def test_transpose_to_time_major_matches_reference_kat_and_oracle():
+    from s2hip import S2HipError, transpose_to_time_major
+
+    # prompt.rs:289-303 (transpose_matches_time_major_layout)
+    assert transpose_to_time_major([10, 20, 1, 2, 3, 4], 3, 2).tolist() == [10, 1, 3, 20, 2, 4]
+    # against the oracle's restatement on a prompt-shaped tensor (11 x 61)
+    rng = np.random.default_rng(3)
+    data = rng.integers(0, 155776, (11, 61)).astype(np.uint32)
+    got = transpose_to_time_major(data, 11, 61)
+    assert np.array_equal(got, O.transpose_to_time_major(data.ravel(), 11, 61))
+    assert np.array_equal(got.reshape(61, 11), data.T.astype(np.int32))
+    # the reference's errors
+    with pytest.raises(S2HipError, match="prompt rows must be non-zero"):
+        transpose_to_time_major([], 0, 0)
+    with pytest.raises(S2HipError, match="prompt data length mismatch: expected 6, got 5"):
+        transpose_to_time_major([1, 2, 3, 4, 5], 3, 2)
+    with pytest.raises(S2HipError, match="does not fit i32"):
+        transpose_to_time_major([1, 2 ** 31], 1, 2)
+    assert transpose_to_time_major([], 3, 0).size == 0

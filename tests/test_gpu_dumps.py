@@ -193,3 +193,31 @@ def test_dump_and_parity_command_lines(tiny_gguf, tmp_path, capsys):
     assert d["token_count"] == 2 and len(d["sequence"]) == 2 and len(d["top_logits"]) == 8
     assert parity.main(["compare-slow-ar", str(slow), str(slow)]) == 0
     assert "passed=true" in capsys.readouterr().out
+
+
+def test_semantic_sample_keeps_the_reference_masked_tail(tiny_gguf):
+    """sample_discrete's fall-through (sampling.rs:227-241) returns the last
+    entry of the reference's list, which is a masked id when the top-p loop
+    runs past the finite candidates: the dump sampler must return that id too.
+    The RNG state is chosen so the draw target is the largest one (0.99999988),
+    and the cases where the oracle falls through are checked along with
+    ordinary ones."""
+    from s2hip import Engine
+    from s2hip.dumps import semantic_sample
+
+    sp = synth.TINY
+    a = 6364136223846793005
+    s0 = ((0xFFFFFFFFFFFFF800 - 1) * pow(a, -1, 1 << 64)) % (1 << 64)  # next unit value 1 - 2^-53
+    rng = np.random.default_rng(1)
+    fall = 0
+    with Engine(tiny_gguf, 64, sp.im_end_id) as e:
+        for trial in range(60):
+            logits = (rng.standard_normal(sp.vocab) * rng.uniform(0.5, 3)).astype(np.float32)
+            block = trial % 2 == 0
+            st = s0 if trial % 3 else int(rng.integers(1, 1 << 62))
+            lg = O.semantic_bias(logits, sp.semantic_begin, sp.semantic_end, sp.im_end_id, block)
+            want = O.sample_token(lg, 1.0, 1.0, 0, None if block else sp.im_end_id, st)
+            got = semantic_sample(e, logits, 0 if block else 10, 5, 1.0, 1.0, 0, st)
+            assert got == want, (trial, got, want)
+            fall += not (sp.semantic_begin <= want[0] <= sp.semantic_end or want[0] == sp.im_end_id)
+    assert fall >= 2

@@ -262,3 +262,66 @@ def test_large_norm_gains_keep_greedy_codes_bit_exact(tiny_gain_gguf):
     ro = o.generate_codes(prompt, 16, min_tokens_before_end=100)
     assert rg["n_frames"] == ro["n_frames"] == 16
     assert np.array_equal(rg["codes"], ro["codes"]) and rg["rng_state"] == ro["rng_state"]
+
+
+def test_op_embed_matches_oracle(tiny_gguf):
+    """embed_slow_ar_time_major at op level: text ids, semantic ids with
+    codebook rows (cb * codebook_size offset, 1/sqrt(11) scale) -- the same
+    f32 order as the reference, so bit-exact."""
+    e, o = _engine(tiny_gguf), _oracle(tiny_gguf)
+    rng = np.random.default_rng(41)
+    n, cdim = 24, synth.TINY.num_codebooks + 1
+    flat = np.zeros((n, cdim), np.int32)
+    flat[:, 0] = rng.integers(0, synth.TINY.vocab, n)
+    flat[::2, 0] = rng.integers(synth.TINY.semantic_begin, synth.TINY.semantic_end + 1, (n + 1) // 2)
+    flat[:, 1:] = rng.integers(0, synth.TINY.codebook_size, (n, cdim - 1))
+    got, want = e.embed(flat), o.embed(flat)
+    assert got.shape == (n, synth.TINY.dim)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    bad = flat.copy()
+    bad[3, 0] = synth.TINY.vocab
+    from s2hip import S2HipError
+    with pytest.raises(S2HipError, match="out of range"):
+        e.embed(bad)
+
+
+def test_slots_hold_independent_sequences(tiny_gguf):
+    """Two sequences in KV slots 0 and 1, prefilled and stepped in turn, each
+    follow their own oracle SlowArState."""
+    e = _engine(tiny_gguf)
+    oa, ob = _oracle(tiny_gguf), _oracle(tiny_gguf)
+    pa, pb = make_prompt(synth.TINY, 16, seed=51), make_prompt(synth.TINY, 21, seed=52)
+    ha, la = e.eval_slot(0, pa)
+    hb, lb = e.eval_slot(1, pb)
+    assert _rel(ha, oa.eval(pa)[0]) < 1e-4 and _rel(hb, ob.eval(pb)[0]) < 1e-4
+    rng = np.random.default_rng(53)
+    for i in range(4):
+        for slot, o in ((0, oa), (1, ob)):
+            tok = np.zeros(synth.TINY.num_codebooks + 1, np.int32)
+            tok[0] = int(rng.integers(synth.TINY.semantic_begin, synth.TINY.semantic_end + 1))
+            tok[1:] = rng.integers(0, synth.TINY.codebook_size, synth.TINY.num_codebooks)
+            hg, lg = e.eval_slot(slot, tok)
+            ho, lo = o.eval(tok)
+            assert _rel(hg, ho) < 1e-4 and _rel(lg, lo) < 1e-4, (i, slot)
+    assert e.n_past_slot(0) == 20 and e.n_past_slot(1) == 25 and e.n_past == 20
+    e.reset(1)
+    assert e.n_past_slot(1) == 0 and e.n_past_slot(0) == 20
+
+
+def test_slow_ar_decode_profile(tiny_gguf):
+    """The SlowArDecodeProfile counterpart: per-operation device time of the
+    Slow-AR decode steps of the last generate call (profile engines only),
+    with the fused operations booked to linear / attention / head."""
+    from s2hip import Engine
+
+    prompt = make_prompt(synth.TINY, 16, seed=61)
+    with Engine(tiny_gguf, 64, synth.TINY.im_end_id, profile=True) as ep:
+        rp = ep.generate_codes(prompt, 6, min_tokens_before_end=100)
+        prof = ep.last_slow_profile()
+    r = _engine(tiny_gguf).generate_codes(prompt, 6, min_tokens_before_end=100)
+    assert np.array_equal(rp["codes"], r["codes"]) and not rp["graph_used"]
+    assert prof["steps"] == 6
+    assert prof["linear_ms"] > 0 and prof["gqa_attention_ms"] > 0 and prof["output_head_ms"] > 0
+    assert prof["rms_norm_ms"] == prof["rope_ms"] == prof["kv_write_ms"] == prof["swiglu_ms"] == 0
+    assert prof["linear_ms"] + prof["gqa_attention_ms"] + prof["output_head_ms"] < rp["decode_ms"]
+    assert _engine(tiny_gguf).last_slow_profile()["steps"] == 0

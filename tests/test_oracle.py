@@ -434,6 +434,9 @@ def test_semantic_token_embedding_kat(embed_toy_gguf):
     np.testing.assert_allclose(hidden, [2 / 7, 12 / 7, 0, 0], rtol=1e-6, atol=1e-7)
     # tied head: logits[i] = emb[i] . hidden
     np.testing.assert_allclose(logits, [4 / 7, 0, 0, 0, 0, 2 / 7, 0, 0], rtol=1e-6, atol=1e-7)
+    # the embedding itself, before any layer: [1, 6, 0, 0] / sqrt(3) and [2, 0, 0, 0]
+    np.testing.assert_allclose(m.embed([5, 2, 1, 0, 0, 0]), [[1 / math.sqrt(3), 6 / math.sqrt(3), 0, 0],
+                                                             [2, 0, 0, 0]], rtol=1e-6)
     # a text id takes no codebook rows and no scale: [2, 0, 0, 0] / sqrt(1 + 1)
     m.reset()
     hidden, _ = m.eval([0, 2, 1])
