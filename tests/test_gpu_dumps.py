@@ -211,7 +211,7 @@ def test_semantic_sample_keeps_the_reference_masked_tail(tiny_gguf):
     rng = np.random.default_rng(1)
     fall = 0
     with Engine(tiny_gguf, 64, sp.im_end_id) as e:
-        for trial in range(60):
+        for trial in range(240):
             logits = (rng.standard_normal(sp.vocab) * rng.uniform(0.5, 3)).astype(np.float32)
             block = trial % 2 == 0
             st = s0 if trial % 3 else int(rng.integers(1, 1 << 62))
@@ -220,4 +220,4 @@ def test_semantic_sample_keeps_the_reference_masked_tail(tiny_gguf):
             got = semantic_sample(e, logits, 0 if block else 10, 5, 1.0, 1.0, 0, st)
             assert got == want, (trial, got, want)
             fall += not (sp.semantic_begin <= want[0] <= sp.semantic_end or want[0] == sp.im_end_id)
-    assert fall >= 2
+    assert fall >= 3
