@@ -50,6 +50,22 @@ constexpr uint32_t PREFILL_CHUNK = 512;  // prompt tokens per MFMA prefill pass
 constexpr uint32_t FRAME_BATCH = 4;
 constexpr size_t WEIGHT_PAD = 256;  // trailing bytes so block loads never leave a buffer
 
+// Device scratch of the allocation-free sampler entry point
+// (s2hip_op_sample_noalloc): the staged logits, then the RNG state, token and
+// error words.  One copy per GPU, for the process lifetime; host code uses the
+// address hipGetSymbolAddress returns for the current device (the array's name
+// is only a host-side stand-in).  Calls that overlap on one GPU race on it.
+constexpr size_t NOALLOC_MAX_LOGITS = 8191;  // the device sampler's limit
+constexpr size_t NOALLOC_STATE_OFF = 32768;  // after the logits (8191 * 4 B, padded)
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_STATE_OFF + 256;
+static_assert(NOALLOC_MAX_LOGITS * 4 <= NOALLOC_STATE_OFF, "logits overlap the state words");
+struct NoallocState {
+  uint64_t rng;
+  uint32_t token;
+  uint32_t err;
+};
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
 float f16_to_f32(uint16_t h) {
   const uint32_t sign = uint32_t(h & 0x8000u) << 16;
   const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
@@ -127,6 +143,8 @@ class Engine {
   void op_embed(const int32_t* flat, size_t n_tok, float* out);
   void op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
                  uint32_t* tok);
+  void op_sample_noalloc(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
+                         uint32_t* tok);
   void time_kernel(const std::string& name, uint32_t reps, double* avg_us, double* bytes);
 
  private:
@@ -183,6 +201,7 @@ class Engine {
 
   hipStream_t stream_ = nullptr;
   std::vector<void*> allocs_;
+  uint8_t* scratch_dev_ = nullptr;  // this device's `scratch` (hipGetSymbolAddress at set-up)
   // S2HIP_FLAG_PROFILE: events between the Slow-AR kernel groups of one frame
   // (booked after each frame into slow_prof)
   bool profiling_ = false;
@@ -277,6 +296,8 @@ Engine::Engine(const s2hip_config& cfg) {
   if (device < 0 || device >= ndev) fail("HIP device " + std::to_string(device) + " not present");
   select();
   HIPC(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  // this device's copy of the allocation-free entry point's scratch
+  HIPC(hipGetSymbolAddress(reinterpret_cast<void**>(&scratch_dev_), HIP_SYMBOL(scratch)));
   for (int i = 0; i < 2; ++i) {
     HIPC(hipHostMalloc(reinterpret_cast<void**>(&staging_[i]), STAGING, hipHostMallocDefault));
     HIPC(hipEventCreateWithFlags(&staging_ev_[i], hipEventDisableTiming));
@@ -1728,6 +1749,34 @@ void Engine::op_sample(const float* logits, size_t n, const s2hip_sampler& smp, 
   if (e) fail("sampler failure");
 }
 
+// op_sample with no device allocation: the logits and the state words are
+// staged in this device's `scratch` (the state words copied in whole, so the
+// token and error words start at zero without a memset).
+void Engine::op_sample_noalloc(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always,
+                               uint64_t* rng, uint32_t* tok) {
+  select();
+  if (n == 0) {
+    *tok = 0;
+    return;
+  }
+  if (n > NOALLOC_MAX_LOGITS)
+    fail("sample_token without allocation supports at most " + std::to_string(NOALLOC_MAX_LOGITS) + " logits, got " +
+         std::to_string(n));
+  if (!scratch_dev_) fail("scratch buffer not set up");
+  float* dl = reinterpret_cast<float*>(scratch_dev_);
+  NoallocState* ds = reinterpret_cast<NoallocState*>(scratch_dev_ + NOALLOC_STATE_OFF);
+  NoallocState hs{*rng, 0u, 0u};
+  HIPC(hipMemcpyAsync(dl, logits, n * 4, hipMemcpyHostToDevice, stream_));
+  HIPC(hipMemcpyAsync(ds, &hs, sizeof(hs), hipMemcpyHostToDevice, stream_));
+  HIPC(launch_sample_plain(dl, uint32_t(n), SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, always, &ds->rng,
+                           &ds->token, &ds->err, stream_));
+  HIPC(hipMemcpyAsync(&hs, ds, sizeof(hs), hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  if (hs.err) fail("sampler failure");
+  *rng = hs.rng;
+  *tok = hs.token;
+}
+
 void Engine::time_kernel(const std::string& full_name, uint32_t reps, double* avg_us, double* bytes) {
   select();
   const s2hip_spec& s = spec;
@@ -2141,6 +2190,15 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
     return 0;
   }
   return guarded(err, err_cap, [&] { engine->e->op_sample(logits, n, *smp, always, rng, tok); });
+}
+
+int32_t s2hip_op_sample_noalloc(s2hip_engine* engine, const float* logits, size_t n, const s2hip_sampler* smp,
+                                int64_t always, uint64_t* rng, uint32_t* tok, char* err, size_t err_cap) {
+  if (!engine || (n && !logits) || !smp || !rng || !tok) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] { engine->e->op_sample_noalloc(logits, n, *smp, always, rng, tok); });
 }
 
 int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,

@@ -300,6 +300,16 @@ class Engine:
                    ctypes.byref(tok))
         return tok.value, st.value
 
+    def sample_noalloc(self, logits, temperature, top_p, top_k, always_include=None, rng_state=0):
+        """sample() through the allocation-free entry point (at most 8191 logits)."""
+        x = _f32(logits)
+        smp = _lib.Sampler(temperature, top_p, top_k)
+        st = ctypes.c_uint64(rng_state)
+        tok = ctypes.c_uint32(0)
+        self._call(self._L.s2hip_op_sample_noalloc, _p(x), x.size, ctypes.byref(smp),
+                   -1 if always_include is None else always_include, ctypes.byref(st), ctypes.byref(tok))
+        return tok.value, st.value
+
     def time_kernel(self, name: str, reps: int = 10):
         avg = ctypes.c_double(0)
         nbytes = ctypes.c_double(0)

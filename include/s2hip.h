@@ -230,6 +230,17 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
                         int64_t always_include, uint64_t* rng_state, uint32_t* token_out, char* err,
                         size_t err_cap);
 
+/* s2hip_op_sample without any device allocation: no hipMalloc / hipFree, the
+ * logits and the RNG / token / error words are staged in a file-scope device
+ * array of 32 KiB + 256 B per GPU (held until the process ends), so n is at
+ * most 8191 (larger n fails with an error naming the limit).  Same results
+ * as s2hip_op_sample.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (tight serving loops, code that forbids
+ * hipMalloc).  Calls that overlap on one GPU race on the shared array. */
+int32_t s2hip_op_sample_noalloc(s2hip_engine* engine, const float* logits, size_t n, const s2hip_sampler* sampler,
+                                int64_t always_include, uint64_t* rng_state, uint32_t* token_out, char* err,
+                                size_t err_cap);
+
 /* The samplers' sequential f32 running sums (softmax normaliser, top-p
  * cumulative sum and draw of sample_token, sampling.rs:202-241, whose Rust
  * loops add term by term in index order): prefix_out[i] = fl(prefix_out[i-1]
