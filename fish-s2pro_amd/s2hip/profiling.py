@@ -8,6 +8,15 @@
 duration) with demangled template arguments kept, so a kernel instance can be
 matched against the engine's live timing.
 
+`traffic` reads a FETCH_SIZE run and a WRITE_SIZE run of the same command
+and prints, per --row 'LABEL|KERNEL_REGEX|GRID_SIZE|ALGORITHMIC_BYTES' (GRID_SIZE
+in threads, or * for any launch), the calibrated fetched + written bytes per
+launch against the algorithmic bytes.
+
+`mfma` averages per-dispatch SQ / GRBM counters (an MFMA counter run) for the
+kernels matching each --kernel and derives MFMA utilisation and f16 MFMA
+flops (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512) per dispatch.
+
 `counters` averages one HBM byte counter (FETCH_SIZE or WRITE_SIZE, reported
 in KiB per dispatch) over every dispatch of the kernel matching --kernel, and
 calibrates it against a plain copy kernel of known size: the copy reads and
@@ -83,6 +92,61 @@ def counters(path, kernel_re, copy_re, copy_bytes):
     return "\n".join(lines)
 
 
+def _scale(rows, counter, copy_re, copy_bytes):
+    c, _ = counter_mean(rows, copy_re, counter)
+    return (copy_bytes / 2) / (c * 1024.0)
+
+
+def _launch_bytes(rows, counter, kernel_re, grid, scale):
+    pat = re.compile(kernel_re)
+    vals = [float(_col(r, "Counter_Value")) for r in rows
+            if _col(r, "Counter_Name") == counter and pat.search(_col(r, "Kernel_Name"))
+            and (grid == "*" or _col(r, "Grid_Size") == grid)]
+    if not vals:
+        raise SystemExit(f"no {counter} samples for {kernel_re!r} at grid {grid}")
+    return statistics.fmean(vals) * 1024.0 * scale, len(vals)
+
+
+def traffic(fetch_csv, write_csv, copy_re, copy_bytes, specs):
+    fr, wr = _rows(fetch_csv), _rows(write_csv)
+    fs, ws = _scale(fr, "FETCH_SIZE", copy_re, copy_bytes), _scale(wr, "WRITE_SIZE", copy_re, copy_bytes)
+    lines = [f"calibration: FETCH_SIZE x {fs:.4f}, WRITE_SIZE x {ws:.4f} (copy kernel moving "
+             f"{copy_bytes / 2 / 2**20:.0f} MiB each way)",
+             f"{'kernel':34s} {'launches':>8s} {'fetch MB':>10s} {'write MB':>9s} {'total MB':>10s} "
+             f"{'algo MB':>9s} {'ratio':>6s}"]
+    for spec in specs:
+        label, kre, grid, algo = spec.split("|")
+        f, n = _launch_bytes(fr, "FETCH_SIZE", kre, grid, fs)
+        w, _ = _launch_bytes(wr, "WRITE_SIZE", kre, grid, ws)
+        a = float(algo)
+        lines.append(f"{label:34s} {n:8d} {f / 1e6:10.3f} {w / 1e6:9.3f} {(f + w) / 1e6:10.3f} {a / 1e6:9.3f} "
+                     f"{(f + w) / a:6.3f}")
+    return "\n".join(lines)
+
+
+def mfma(path, kernel_res):
+    rows = _rows(path)
+    lines = []
+    for kre in kernel_res:
+        pat = re.compile(kre)
+        per = {}
+        for r in rows:
+            if pat.search(_col(r, "Kernel_Name")):
+                per.setdefault(_col(r, "Counter_Name"), []).append(float(_col(r, "Counter_Value")))
+        if not per:
+            raise SystemExit(f"no samples for {kre!r}")
+        m = {k: statistics.fmean(v) for k, v in per.items()}
+        n = max(len(v) for v in per.values())
+        parts = [f"{k} {v:.0f}" for k, v in sorted(m.items())]
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in m and "GRBM_GUI_ACTIVE" in m:
+            # busy cycles summed over the SIMDs (4 per CU, 256 CUs)
+            parts.append(f"MFMA busy {100 * m['SQ_VALU_MFMA_BUSY_CYCLES'] / (m['GRBM_GUI_ACTIVE'] * 1024):.1f} %")
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in m:
+            parts.append(f"f16 MFMA {m['SQ_INSTS_VALU_MFMA_MOPS_F16'] * 512 / 1e9:.2f} GFLOP/dispatch")
+        lines.append(f"{short_name(kre)} ({n} dispatches): " + "; ".join(parts))
+    return "\n".join(lines)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -94,9 +158,22 @@ def main(argv=None):
     b.add_argument("--kernel", required=True)
     b.add_argument("--copy-kernel", required=True)
     b.add_argument("--copy-bytes", type=float, required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_csv")
+    t.add_argument("write_csv")
+    t.add_argument("--copy-kernel", required=True)
+    t.add_argument("--copy-bytes", type=float, required=True)
+    t.add_argument("--row", action="append", required=True)
+    m = sub.add_parser("mfma")
+    m.add_argument("csv")
+    m.add_argument("--kernel", action="append", required=True)
     args = ap.parse_args(argv)
     if args.cmd == "stats":
         print(stats(args.csv, args.top))
+    elif args.cmd == "traffic":
+        print(traffic(args.fetch_csv, args.write_csv, args.copy_kernel, args.copy_bytes, args.row))
+    elif args.cmd == "mfma":
+        print(mfma(args.csv, args.kernel))
     else:
         print(counters(args.csv, args.kernel, args.copy_kernel, args.copy_bytes))
 
