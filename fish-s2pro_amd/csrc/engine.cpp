@@ -256,6 +256,8 @@ class Engine {
   // prompt prefill (MFMA path): chunk activations and the split planes
   float *ph_ = nullptr, *pqkv_ = nullptr, *pq_ = nullptr, *patt_ = nullptr, *pact_ = nullptr, *prs_ = nullptr;
   _Float16 *pxh_ = nullptr, *pxl_ = nullptr;
+  float* ppart_ = nullptr;  // K-split partial sums of the prefill products
+  size_t ppart_cap_ = 0;
   float *fh_ = nullptr, *fqkv_ = nullptr, *fq_ = nullptr, *fatt_ = nullptr, *fpart_ = nullptr, *fact_ = nullptr;
   float *flogits_ = nullptr, *fkc_ = nullptr, *fvc_ = nullptr;
   uint32_t fctx_ = 11;
@@ -460,6 +462,9 @@ Engine::Engine(const s2hip_config& cfg) {
     prs_ = dalloc<float>(CHP);
     pxh_ = dalloc<_Float16>(CHP * kmax);
     pxl_ = dalloc<_Float16>(CHP * kmax);
+    ppart_cap_ = std::max(gemm_part_floats(uint32_t(CHP), std::max<uint32_t>(qkv_w, s.dim)),
+                          attn_prefill_part_floats(uint32_t(CH), s.heads, s.head_dim));
+    ppart_ = dalloc<float>(ppart_cap_);
     if (s.dim % 32 || q % 32 || s.ffn % 32) fail("prefill needs embedding, attention and FFN widths divisible by 32");
   }
   hn_ = dalloc<float>(size_t(MAX_SEQS) * s.dim);
@@ -948,6 +953,8 @@ void Engine::mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint
   g.N = n;
   g.y = y;
   g.ldy = ldy;
+  g.part = ppart_;
+  g.part_cap = ppart_cap_;
   HIPC(launch_gemm_mfma(L.type, epi, g, stream_));
 }
 
@@ -1074,6 +1081,9 @@ void Engine::enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t s
       pa.max_seq = s.max_seq_len;
       pa.scale = 1.0f / std::sqrt(float(s.head_dim));  // slow_ar.rs:59-61
       pa.kv_f16 = kv_f16_;
+      pa.err = &st->err;
+      pa.part = ppart_;
+      pa.part_cap = ppart_cap_;
       HIPC(launch_attention_prefill(pa, stream_));
       mm(L.wo, nullptr, EPI_RESID, patt_, q, nullptr, 0.0f, nc, npad, ph_, s.dim);
       mm(L.w1, &L.w3, EPI_SWIGLU_SLOW, ph_, s.dim, L.ffn_norm, s.eps, nc, npad, pact_, s.ffn);

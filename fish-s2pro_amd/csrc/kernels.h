@@ -255,6 +255,8 @@ hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, fl
 
 // MFMA product y[n][m] (op)= rs[n] * sum_k W[m][k] * x[n][k] for n < N, m < M,
 // x given as the split planes; epilogues as for launch_gemv (SwiGLU uses w3).
+// part (nullable): workspace of part_cap floats for K-split partial sums
+// (gemm_part_floats(Npad, M) floats lets every short-M product split).
 struct GemmArgs {
   const uint8_t* w;
   const uint8_t* w3;
@@ -266,7 +268,10 @@ struct GemmArgs {
   uint32_t N;
   float* y;
   uint32_t ldy;
+  float* part;
+  size_t part_cap;
 };
+size_t gemm_part_floats(uint32_t n_pad, uint32_t m);
 hipError_t launch_gemm_mfma(uint32_t wtype, int epi, const GemmArgs& a, hipStream_t s);
 
 // Skinny MFMA product for 1..16 columns (batched decode): x as split planes
@@ -330,7 +335,11 @@ struct PrefillAttnArgs {
   uint32_t N, H, Hkv, hd, max_seq;
   float scale;
   uint32_t kv_f16;         // 1: the caches hold f16
+  uint32_t* err;           // ERR_F16_RANGE when a q, k or v is beyond the f16 range (nullable)
+  float* part;             // key-split workspace of part_cap floats (nullable: no split)
+  size_t part_cap;
 };
 hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s);
+size_t attn_prefill_part_floats(uint32_t n, uint32_t heads, uint32_t hd);
 
 }  // namespace s2

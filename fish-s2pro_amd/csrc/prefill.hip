@@ -33,6 +33,9 @@ __device__ __forceinline__ float wave_sum_f(float v) {
   for (int off = WAVE / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
   return v;
 }
+__device__ __forceinline__ float half_bits_to_float_p(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, b));
+}
 __device__ __forceinline__ float wave_max_f(float v) {
 #pragma unroll
   for (int off = WAVE / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
@@ -136,112 +139,226 @@ __device__ __forceinline__ void weight8(const uint8_t* row, uint32_t e, half8& h
 
 // ---------------------------------------------------------------------------
 // MFMA GEMM  Y[n][m] (op)= rs[n] * sum_k W[m][k] * X[n][k]
-//   block tile 64 (m) x 64 (n), 4 waves in 2 x 2, each one 32 x 32 MFMA tile;
-//   K in stages of 32 staged through LDS (rows padded to 40 halfs so the
-//   16-byte fragment reads of 8 consecutive lanes hit distinct banks); the
-//   next stage's global loads are in flight while the current one computes.
+//   Block tile: 128 weight rows x 128 tokens, 4 waves in 2 x 2, each wave
+//   64 rows x 64 tokens = 2 x 2 tiles of v_mfma_f32_32x32x16_f16 with the
+//   token fragment as A and the weight fragment as B, so a lane's results
+//   are 16 tokens x one weight row and the 32 lanes of a row group store 32
+//   consecutive outputs.  Per 16-wide k step a wave reads 2 weight and 4
+//   token fragments (hi and lo planes) from LDS for 8 MFMAs (F16), about 3 KB
+//   per 1000 MFMA cycles per SIMD.  K goes in stages of 32 through a double
+//   buffer in LDS (rows padded to 40 halfs: the 16-byte fragment reads of 8
+//   consecutive lanes hit distinct banks); the next stage's global loads are
+//   in flight while the current one computes.
+//   SwiGLU (w1 and w3): the 128 row slots hold 64 outputs as [w1 32 | w3 32 |
+//   w1 32 | w3 32], so each wave holds w1 and w3 of the same outputs.
+//   Tile order: blocks L and L + 8 run on the same XCD, so the n tiles (and
+//   K splits) of one m tile are consecutive there and its weight rows are
+//   fetched into that XCD's L2 once.
+//   K split (short-M matrices): block (m, n, split) writes its unscaled sums
+//   to part[split][n][m]; gemm_split_reduce_kernel adds the splits in order
+//   and applies rs and the epilogue.
 // ---------------------------------------------------------------------------
-constexpr int GM = 64, GN = 64, GK = 32, GKP = 40;
+constexpr int TM = 128, TN = 128, KS = 32, KP = KS + 8;
+constexpr uint32_t GEMM_MAX_SPLITS = 4;
 
-template <uint32_t WT, int EPI>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs a) {
+template <uint32_t WT, int EPI, int D>
+__global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs a, uint32_t m_tiles, uint32_t n_tiles,
+                                                           uint32_t splits) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr bool WSPLIT = WT != W_F16;
-  constexpr int NW = DUAL ? 2 : 1;  // weight matrices
-  __shared__ _Float16 ws[2][NW][WSPLIT ? 2 : 1][GM][GKP];
-  __shared__ _Float16 xs[2][2][GN][GKP];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int WP = WSPLIT ? 2 : 1;  // weight planes in LDS (hi, lo * 2^11)
+  __shared__ _Float16 xs[2][2][TN][KP];
+  __shared__ _Float16 ws[2][WP][TM][KP];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wm = wave & 1u, wn = wave >> 1;
-  const uint32_t m_blk = blockIdx.x * GM, n_blk = blockIdx.y * GN;
+  const uint32_t L = blockIdx.x, inner = n_tiles * splits;
+  const uint32_t sidx = L >> 3, mt = (sidx / inner) * 8u + (L & 7u);
+  if (mt >= m_tiles) return;
+  const uint32_t rr = sidx % inner, nt = rr % n_tiles, sp = rr / n_tiles;
+  const uint32_t n_base = nt * TN;
+  const uint32_t nst = a.K / KS, st0 = sp * nst / splits, st1 = (sp + 1) * nst / splits;
 
-  // staging assignment: thread -> (row, 8-element part) of a 64 x 32 tile
-  const uint32_t srow = tid >> 2, spart = (tid & 3u) * 8u;
-  const uint32_t wrow = min(m_blk + srow, a.M - 1);
-  const uint8_t* wp[NW];
-  wp[0] = a.w + size_t(wrow) * a.row_bytes;
-  if constexpr (DUAL) wp[NW - 1] = a.w3 + size_t(wrow) * a.row_bytes;
-  const _Float16* xhp = a.xh + size_t(n_blk + srow) * a.K + spart;
-  const _Float16* xlp = a.xl + size_t(n_blk + srow) * a.K + spart;
-
-  half8 rw[NW][2], rxh, rxl;
-  auto load_stage = [&](uint32_t k0) {
+  // staging: weight chunks c = tid + 256 j (j < 2): slot c / 4, 8 elements at
+  // (c % 4) * 8; token chunks c = tid + 256 j (j < 4): plane c / 512, row
+  // (c / 4) % 128, 8 elements at (c % 4) * 8
+  const uint8_t* wrow[2];
 #pragma unroll
-    for (int mtx = 0; mtx < NW; ++mtx) weight8<WT>(wp[mtx], k0 + spart, rw[mtx][0], rw[mtx][1]);
-    rxh = *reinterpret_cast<const half8*>(xhp + k0);
-    rxl = *reinterpret_cast<const half8*>(xlp + k0);
-  };
-  auto store_stage = [&](uint32_t buf) {
-#pragma unroll
-    for (int mtx = 0; mtx < NW; ++mtx) {
-      *reinterpret_cast<half8*>(&ws[buf][mtx][0][srow][spart]) = rw[mtx][0];
-      if constexpr (WSPLIT) *reinterpret_cast<half8*>(&ws[buf][mtx][WSPLIT ? 1 : 0][srow][spart]) = rw[mtx][1];
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t slot = (tid + 256u * j) >> 2;
+    uint32_t row;
+    const uint8_t* base = a.w;
+    if constexpr (DUAL) {
+      const uint32_t grp = slot >> 5;
+      row = mt * 64u + (grp >> 1) * 32u + (slot & 31u);
+      base = (grp & 1u) ? a.w3 : a.w;
+    } else {
+      row = mt * TM + slot;
     }
-    *reinterpret_cast<half8*>(&xs[buf][0][srow][spart]) = rxh;
-    *reinterpret_cast<half8*>(&xs[buf][1][srow][spart]) = rxl;
+    wrow[j] = base + size_t(min(row, a.M - 1)) * a.row_bytes;
+  }
+  const uint32_t part8 = (tid & 3u) * 8u;
+  const _Float16* xrow[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t c = tid + 256u * j;
+    xrow[j] = ((c >> 9) ? a.xl : a.xh) + size_t(n_base + ((c >> 2) & 127u)) * a.K + part8;
+  }
+
+  // a ring of D register sets: the loads of stage st + D go out while stage
+  // st computes, so D stages of global latency are hidden
+  half8 rw[D][2][WP], rx[D][4];
+  auto load_stage = [&](int r, uint32_t st) {
+    const uint32_t k0 = min(st, st1 - 1u) * KS;  // past the range: a valid, unused stage
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      half8 lo;
+      weight8<WT>(wrow[j], k0 + part8, rw[r][j][0], lo);
+      if constexpr (WSPLIT) rw[r][j][WP - 1] = lo;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rx[r][j] = *reinterpret_cast<const half8*>(xrow[j] + k0);
+  };
+  auto store_stage = [&](int r, uint32_t buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t slot = (tid + 256u * j) >> 2;
+#pragma unroll
+      for (int p = 0; p < WP; ++p) *reinterpret_cast<half8*>(&ws[buf][p][slot][part8]) = rw[r][j][p];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t c = tid + 256u * j;
+      *reinterpret_cast<half8*>(&xs[buf][c >> 9][(c >> 2) & 127u][part8]) = rx[r][j];
+    }
   };
 
-  floatx16 acc[NW], accl[NW];
+  floatx16 acc[2][2], accl[WSPLIT ? 2 : 1][WSPLIT ? 2 : 1];
 #pragma unroll
-  for (int mtx = 0; mtx < NW; ++mtx) {
-    acc[mtx] = floatx16{};
-    accl[mtx] = floatx16{};
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
+  if constexpr (WSPLIT) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) accl[i][j] = floatx16{};
   }
   const uint32_t fr = lane & 31u, fk = 8u * (lane >> 5);  // fragment row / k offset
-  const uint32_t nst = a.K / GK;
-  load_stage(0);
-  store_stage(0);
+  auto compute = [&](uint32_t buf) {
+#pragma unroll
+    for (uint32_t kk = 0; kk < KS; kk += 16) {
+      half8 xa[2][2], wb[2][WP];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          xa[t][p] = *reinterpret_cast<const half8*>(&xs[buf][p][64 * wn + 32 * t + fr][kk + fk]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < WP; ++p)
+          wb[t][p] = *reinterpret_cast<const half8*>(&ws[buf][p][64 * wm + 32 * t + fr][kk + fk]);
+#pragma unroll
+      for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+          acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[tn][0], wb[tm][0], acc[tn][tm], 0, 0, 0);
+          acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[tn][1], wb[tm][0], acc[tn][tm], 0, 0, 0);
+          if constexpr (WSPLIT)
+            accl[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[tn][0], wb[tm][WP - 1], accl[tn][tm], 0, 0, 0);
+        }
+    }
+  };
+  // prologue: stages st0 .. st0 + D - 1 in flight, the first one in LDS
+#pragma unroll
+  for (int r = 0; r < D; ++r) load_stage(r, st0 + r);
+  store_stage(0, 0);
   __syncthreads();
-  for (uint32_t st = 0; st < nst; ++st) {
-    const uint32_t buf = st & 1u;
-    if (st + 1 < nst) load_stage((st + 1) * GK);
+  // stage st sits in LDS buffer (st - st0) & 1 and came from ring slot
+  // (st - st0) % D, which is reloaded with stage st + D once stored
+  for (uint32_t s0 = st0; s0 < st1; s0 += D) {
 #pragma unroll
-    for (uint32_t kk = 0; kk < GK; kk += 16) {
-      const half8 bh = *reinterpret_cast<const half8*>(&xs[buf][0][32 * wn + fr][kk + fk]);
-      const half8 bl = *reinterpret_cast<const half8*>(&xs[buf][1][32 * wn + fr][kk + fk]);
-#pragma unroll
-      for (int mtx = 0; mtx < NW; ++mtx) {
-        const half8 ah = *reinterpret_cast<const half8*>(&ws[buf][mtx][0][32 * wm + fr][kk + fk]);
-        acc[mtx] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc[mtx], 0, 0, 0);
-        acc[mtx] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc[mtx], 0, 0, 0);
-        if constexpr (WSPLIT) {
-          const half8 al = *reinterpret_cast<const half8*>(&ws[buf][mtx][WSPLIT ? 1 : 0][32 * wm + fr][kk + fk]);
-          accl[mtx] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, accl[mtx], 0, 0, 0);
+    for (int r = 0; r < D; ++r) {
+      const uint32_t st = s0 + r;
+      if (st < st1) {
+        load_stage(r, st + D);  // ring slot r is free: stage st went to LDS
+        compute((st - st0) & 1u);
+        if (st + 1 < st1) {
+          store_stage((r + 1) % D, (st + 1 - st0) & 1u);
+          __syncthreads();
         }
       }
     }
-    if (st + 1 < nst) {
-      store_stage(buf ^ 1u);
-      __syncthreads();
-    }
   }
 
-  // epilogue: lane holds D[8 (v/4) + 4 (lane/32) + v%4][lane%32]
-  const uint32_t n = n_blk + 32 * wn + (lane & 31u);
-  if (n >= a.N) return;
-  const float r = a.rs[n];
-  float* yrow = a.y + size_t(n) * a.ldy;
+  // epilogue: acc[tn][tm][v] = D[token 8 (v/4) + 4 (lane/32) + v%4][weight slot lane%32]
 #pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const uint32_t m = m_blk + 32 * wm + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-    if (m >= a.M) continue;
-    float g = acc[0][v];
-    if constexpr (WSPLIT) g = g + accl[0][v] * (1.0f / 2048.0f);
-    g *= r;
-    if constexpr (EPI == EPI_STORE) {
-      yrow[m] = g;
-    } else if constexpr (EPI == EPI_RESID) {
-      yrow[m] = __fadd_rn(yrow[m], g);
-    } else {
-      float u = acc[NW - 1][v];
-      if constexpr (WSPLIT) u = u + accl[NW - 1][v] * (1.0f / 2048.0f);
-      u *= r;
-      if constexpr (EPI == EPI_SWIGLU_SLOW) {
-        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-g)));
-        yrow[m] = __fmul_rn(__fmul_rn(g, sig), u);
+  for (int tn = 0; tn < 2; ++tn) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t n = n_base + 64 * wn + 32 * tn + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+      float g[2];
+#pragma unroll
+      for (int tm = 0; tm < 2; ++tm) {
+        g[tm] = acc[tn][tm][v];
+        if constexpr (WSPLIT) g[tm] = g[tm] + accl[tn][tm][v] * (1.0f / 2048.0f);
+      }
+      if constexpr (DUAL) {
+        const uint32_t m = mt * 64u + 32u * wm + fr;
+        if (n >= a.N || m >= a.M) continue;
+        const float r = a.rs[n];
+        const float gg = g[0] * r, u = g[1] * r;
+        float* dst = a.y + size_t(n) * a.ldy + m;
+        if constexpr (EPI == EPI_SWIGLU_SLOW) {
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gg)));
+          *dst = __fmul_rn(__fmul_rn(gg, sig), u);
+        } else {
+          *dst = __fmul_rn(__fdiv_rn(gg, __fadd_rn(1.0f, expf_glibc(-gg))), u);
+        }
       } else {
-        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_glibc(-g))), u);
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+          const uint32_t m = mt * TM + 64u * wm + 32u * tm + fr;
+          if (n >= a.N || m >= a.M) continue;
+          if (splits > 1) {
+            a.part[(size_t(sp) * a.N + n) * a.M + m] = g[tm];
+          } else {
+            const float gg = g[tm] * a.rs[n];
+            float* dst = a.y + size_t(n) * a.ldy + m;
+            if constexpr (EPI == EPI_STORE) *dst = gg;
+            else *dst = __fadd_rn(*dst, gg);
+          }
+        }
       }
     }
+  }
+}
+
+// y[n][m] (op)= rs[n] * (part[0][n][m] + part[1][n][m] + ...), splits added in
+// order; one thread per 4 consecutive outputs (M % 4 == 0).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(GemmArgs a, uint32_t splits) {
+  const uint32_t m4 = a.M / 4u;
+  const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+  if (i >= size_t(a.N) * m4) return;
+  const uint32_t n = uint32_t(i / m4), m = uint32_t(i % m4) * 4u;
+  const size_t plane = size_t(a.N) * a.M;
+  const float* p = a.part + size_t(n) * a.M + m;
+  float4 s = *reinterpret_cast<const float4*>(p);
+  for (uint32_t k = 1; k < splits; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(p + k * plane);
+    s.x += t.x;
+    s.y += t.y;
+    s.z += t.z;
+    s.w += t.w;
+  }
+  const float r = a.rs[n];
+  float* dst = a.y + size_t(n) * a.ldy + m;
+  const float v[4] = {s.x * r, s.y * r, s.z * r, s.w * r};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (EPI == EPI_STORE) dst[e] = v[e];
+    else dst[e] = __fadd_rn(dst[e], v[e]);
   }
 }
 
@@ -366,162 +483,344 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_mfma_kernel(SkinnyArgs a
 }
 
 // ---------------------------------------------------------------------------
-// Causal GQA attention for a prompt chunk: query c (0 <= c < N) sits at
-// position base + c and attends cache positions 0 .. base + c (its own K/V
-// already appended).  Block (query tile of 8, kv head g): wave w serves q
-// head g * rep + w; the 4 q heads share each 64-position K/V tile in LDS.
-// Online softmax per query (running max and sum), f32 throughout.
+// Causal GQA attention for a prompt chunk on the MFMA units: query c
+// (0 <= c < N) sits at position base + c and attends cache positions
+// 0 .. base + c (its own K/V already appended).
+//   Block (32 queries, kv head g, key split sp), wave w = q head g * rep + w;
+//   the waves share each 32-key K/V tile in LDS.  Per tile a wave computes
+//   the scores transposed, S^T = K Q^T (v_mfma_f32_32x32x16_f16, K as A from
+//   LDS, the wave's Q as B in registers), so a lane owns one query and 16 of
+//   the tile's keys: the online softmax (running max and sum per query, f32)
+//   is in-lane plus one exchange with the lane 32 away.  Then O^T += V^T P^T
+//   with P^T straight from the score registers as the B operand and V^T from
+//   LDS, stored transposed with bits 2 and 3 of the key index swapped (the
+//   key order of the score registers), so O^T also has a query per lane and
+//   the softmax rescale stays in-lane.
+//   Precision (the reference computes in f32): q, k, v and p are split into
+//   f16 x = hi + lo (lo = f16(x - hi)), and each product is accumulated as
+//   hi.hi + hi.lo + lo.hi in one f32 accumulator (~2^-22 relative per term
+//   for |x| >= 2^-3; below that lo is subnormal, absolute 2^-25).  A q, k or
+//   v beyond the f16 range sets ERR_F16_RANGE.
+//   Key split (splits > 1): the causal key range of the block's last query
+//   is cut into `splits` runs of whole tiles, one per block; each writes its
+//   running (max, sum) and unnormalised O to the workspace and
+//   attn_prefill_merge_kernel combines them in split order.
+//   The next tile's K/V loads are in flight while the current one computes.
 // ---------------------------------------------------------------------------
-constexpr int PQ = 8, PT = 64;
+constexpr int AQ = 32, AT = 32;  // queries per block, keys per tile
+constexpr uint32_t ATTN_MAX_SPLITS = 4;
 
-// Four f16 values (8 bytes) as a float4 (exact)
-__device__ __forceinline__ float4 prefill_half4(const uint16_t* p) {
-  const uint2 r = *reinterpret_cast<const uint2*>(p);
-  const __half2 lo = *reinterpret_cast<const __half2*>(&r.x), hi = *reinterpret_cast<const __half2*>(&r.y);
-  const float2 a = __half22float2(lo), b = __half22float2(hi);
-  return make_float4(a.x, a.y, b.x, b.y);
+__device__ __forceinline__ void split_h(float x, _Float16& h, _Float16& l) {
+  h = _Float16(x);
+  l = _Float16(x - float(h));
 }
 
+// position of key j (0..31) of a tile in the transposed V layout: bits 2 and 3 swapped
+__device__ __forceinline__ uint32_t vt_pos(uint32_t j) { return (j & ~12u) | ((j & 4u) << 1) | ((j & 8u) >> 1); }
+
 template <int HD, bool KH>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(PrefillAttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillAttnArgs a, uint32_t splits) {
   using KT = std::conditional_t<KH, uint16_t, float>;  // cache element: f16 bits or f32
-  __shared__ float kt[PT][HD + 1];
-  __shared__ float vt[PT][HD];
-  __shared__ float qs[4][PQ][HD];
-  __shared__ float ps[4][PQ][PT];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t q0 = blockIdx.x * PQ, g = blockIdx.y;
+  constexpr int DS = HD / 16;          // 16-wide k steps of the scores
+  constexpr int DT = HD / 32;          // 32-wide output tiles
+  constexpr int KP = HD + 8;           // padded K row (halfs)
+  constexpr int VP = AT + 8;           // padded V^T row (halfs)
+  constexpr int KF4 = AT * HD / 4 / 256;   // K float4 per thread per tile
+  constexpr int VG = HD * (AT / 4) / 256;  // V (dim, 4-key group) pairs per thread per tile
+  __shared__ _Float16 ks[2][AT][KP];   // hi, lo planes
+  __shared__ _Float16 vts[2][HD][VP];
+  __shared__ uint32_t bad;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t q0 = blockIdx.x * AQ, g = blockIdx.y, sp = blockIdx.z;
   const uint32_t rep = a.H / a.Hkv;
-  const uint32_t base = *a.pos_ptr + a.pos_offset;
-  const uint32_t nq = min(uint32_t(PQ), a.N - q0);
   const bool active = wave < rep;
   const uint32_t h = g * rep + (active ? wave : 0u);
-  // q rows of this wave's head
-  for (uint32_t i = lane; i < PQ * HD; i += 64) {
-    const uint32_t c = i / HD, d = i % HD;
-    qs[wave][c][d] = (active && c < nq) ? a.q[size_t(q0 + c) * a.H * HD + size_t(h) * HD + d] : 0.0f;
-  }
-  float m[PQ], l[PQ], o[PQ][HD / 64];
-#pragma unroll
-  for (int c = 0; c < PQ; ++c) {
-    m[c] = -INFINITY;
-    l[c] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < HD / 64; ++j) o[c][j] = 0.0f;
-  }
+  const uint32_t base = *a.pos_ptr + a.pos_offset;
+  const uint32_t nq = min(uint32_t(AQ), a.N - q0);
   const uint32_t t_end = base + q0 + nq;  // keys needed by the last query
+  // this block's run of whole tiles
+  const uint32_t n_tiles = (t_end + AT - 1) / AT, per = (n_tiles + splits - 1) / splits;
+  const uint32_t tile_lo = min(sp * per, n_tiles), tile_hi = min(tile_lo + per, n_tiles);
+  const uint32_t fr = lane & 31u, fk = 8u * (lane >> 5);
+  if (tid == 0) bad = 0;
+  uint32_t my_bad = 0;
+
+  // the wave's queries as the B operand of S^T: query q0 + fr, dims 16 ds + fk .. + 7
+  half8 qh[DS], ql[DS];
+  {
+    const uint32_t qi = q0 + min(fr, nq - 1u);
+    const float* qrow = a.q + size_t(qi) * a.H * HD + size_t(h) * HD + fk;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const float4 u = *reinterpret_cast<const float4*>(qrow + 16 * ds);
+      const float4 w = *reinterpret_cast<const float4*>(qrow + 16 * ds + 4);
+      const float x[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        _Float16 hh, ll;
+        split_h(x[e], hh, ll);
+        qh[ds][e] = hh;
+        ql[ds][e] = ll;
+        my_bad |= !(fabsf(x[e]) < 65504.0f);
+      }
+    }
+  }
+
   const KT* kc = reinterpret_cast<const KT*>(a.k_cache) + size_t(g) * a.max_seq * HD;
   const KT* vc = reinterpret_cast<const KT*>(a.v_cache) + size_t(g) * a.max_seq * HD;
-  for (uint32_t t0 = 0; t0 < t_end; t0 += PT) {
-    __syncthreads();  // previous tile consumed (and qs written on the first pass)
-    for (uint32_t i = tid; i < PT * HD / 4; i += 256) {
-      const uint32_t t = i / (HD / 4), d = (i % (HD / 4)) * 4;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (t0 + t < t_end) {
-        if constexpr (KH) {
-          kv = prefill_half4(kc + size_t(t0 + t) * HD + d);
-          vv = prefill_half4(vc + size_t(t0 + t) * HD + d);
-        } else {
-          kv = *reinterpret_cast<const float4*>(kc + size_t(t0 + t) * HD + d);
-          vv = *reinterpret_cast<const float4*>(vc + size_t(t0 + t) * HD + d);
-        }
-      }
-      kt[t][d] = kv.x;
-      kt[t][d + 1] = kv.y;
-      kt[t][d + 2] = kv.z;
-      kt[t][d + 3] = kv.w;
-      *reinterpret_cast<float4*>(&vt[t][d]) = vv;
-    }
-    __syncthreads();
-    if (active) {
-      // scores: lane = key position within the tile
-      const uint32_t t = t0 + lane;
-      float s[PQ];
+  // tile loads: K float4 f = tid + 256 j -> key f / (HD / 4), dims (f % (HD / 4)) * 4;
+  // V pair p = tid + 256 j -> dim p % HD, keys 4 (p / HD) .. + 3
+  float4 kr[KF4];
+  float vr[VG][4];
+  auto load_tile = [&](uint32_t t0) {
 #pragma unroll
-      for (int c = 0; c < PQ; ++c) s[c] = 0.0f;
-      for (int d = 0; d < HD; ++d) {
-        const float kd = kt[lane][d];
-#pragma unroll
-        for (int c = 0; c < PQ; ++c) s[c] = fmaf(qs[wave][c][d], kd, s[c]);
-      }
-#pragma unroll
-      for (int c = 0; c < PQ; ++c) {
-        const bool vis = uint32_t(c) < nq && t <= base + q0 + c;
-        const float sc = vis ? s[c] * a.scale : -INFINITY;
-        const float mt = wave_max_f(sc);
-        const float mn = fmaxf(m[c], mt);
-        const float p = vis ? expf(sc - mn) : 0.0f;
-        const float corr = (m[c] == -INFINITY) ? 0.0f : expf(m[c] - mn);
-        l[c] = l[c] * corr + wave_sum_f(p);
-#pragma unroll
-        for (int j = 0; j < HD / 64; ++j) o[c][j] *= corr;
-        m[c] = (mn == -INFINITY) ? m[c] : mn;
-        ps[wave][c][lane] = p;
+    for (int j = 0; j < KF4; ++j) {
+      const uint32_t f = tid + 256u * j, key = f / (HD / 4), d = (f % (HD / 4)) * 4u;
+      const uint32_t t = min(t0 + key, a.max_seq - 1u);
+      if constexpr (KH) {
+        const uint2 r = *reinterpret_cast<const uint2*>(kc + size_t(t) * HD + d);
+        const __half2 lo = *reinterpret_cast<const __half2*>(&r.x), hi = *reinterpret_cast<const __half2*>(&r.y);
+        const float2 x0 = __half22float2(lo), x1 = __half22float2(hi);
+        kr[j] = make_float4(x0.x, x0.y, x1.x, x1.y);
+      } else {
+        kr[j] = *reinterpret_cast<const float4*>(kc + size_t(t) * HD + d);
       }
     }
-    __syncthreads();
-    if (active) {
-      // PV: lane = head-dim element
-      for (int t = 0; t < PT; ++t) {
-        float vd[HD / 64];
 #pragma unroll
-        for (int j = 0; j < HD / 64; ++j) vd[j] = vt[t][lane + 64 * j];
+    for (int j = 0; j < VG; ++j) {
+      const uint32_t p = tid + 256u * j, d = p % HD, k0 = 4u * (p / HD);
 #pragma unroll
-        for (int c = 0; c < PQ; ++c) {
-          const float p = ps[wave][c][t];
-#pragma unroll
-          for (int j = 0; j < HD / 64; ++j) o[c][j] = fmaf(p, vd[j], o[c][j]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t = t0 + k0 + i;
+        float v;
+        if constexpr (KH) v = half_bits_to_float_p(vc[size_t(min(t, a.max_seq - 1u)) * HD + d]);
+        else v = vc[size_t(min(t, a.max_seq - 1u)) * HD + d];
+        vr[j][i] = t < t_end ? v : 0.0f;  // keys past the last query: zero (p is 0 there)
       }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int j = 0; j < KF4; ++j) {
+      const uint32_t f = tid + 256u * j, key = f / (HD / 4), d = (f % (HD / 4)) * 4u;
+      const float x[4] = {kr[j].x, kr[j].y, kr[j].z, kr[j].w};
+      _Float16 hh[4], ll[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        split_h(x[i], hh[i], ll[i]);
+        my_bad |= !(fabsf(x[i]) < 65504.0f);
+      }
+      *reinterpret_cast<uint2*>(&ks[0][key][d]) = *reinterpret_cast<const uint2*>(hh);
+      *reinterpret_cast<uint2*>(&ks[1][key][d]) = *reinterpret_cast<const uint2*>(ll);
+    }
+#pragma unroll
+    for (int j = 0; j < VG; ++j) {
+      const uint32_t p = tid + 256u * j, d = p % HD, k0 = 4u * (p / HD);
+      _Float16 hh[4], ll[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        split_h(vr[j][i], hh[i], ll[i]);
+        my_bad |= !(fabsf(vr[j][i]) < 65504.0f);
+      }
+      // keys k0 .. k0 + 3 (k0 % 4 == 0) stay consecutive under vt_pos
+      *reinterpret_cast<uint2*>(&vts[0][d][vt_pos(k0)]) = *reinterpret_cast<const uint2*>(hh);
+      *reinterpret_cast<uint2*>(&vts[1][d][vt_pos(k0)]) = *reinterpret_cast<const uint2*>(ll);
+    }
+  };
+
+  floatx16 o[DT];
+#pragma unroll
+  for (int i = 0; i < DT; ++i) o[i] = floatx16{};
+  float m = -INFINITY, lsum = 0.0f;
+  const uint32_t qpos = base + q0 + fr;  // this lane's query position
+  const bool qvalid = fr < nq;
+  if (tile_lo < tile_hi) load_tile(tile_lo * AT);
+  for (uint32_t tile = tile_lo; tile < tile_hi; ++tile) {
+    const uint32_t t0 = tile * AT;
+    __syncthreads();  // the previous tile is consumed
+    store_tile();
+    __syncthreads();
+    if (tile + 1 < tile_hi) load_tile(t0 + AT);  // in flight during this tile
+    if (!active) continue;
+    // S^T[key][query]: lane holds query fr, keys 8 (v / 4) + 4 (lane / 32) + v % 4
+    floatx16 sacc = floatx16{};
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      const half8 kh = *reinterpret_cast<const half8*>(&ks[0][fr][16 * ds + fk]);
+      const half8 kl = *reinterpret_cast<const half8*>(&ks[1][fr][16 * ds + fk]);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[ds], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[ds], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[ds], sacc, 0, 0, 0);
+    }
+    float s[16];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t key = t0 + 8u * (v / 4) + 4u * (lane >> 5) + (v % 4);
+      const bool vis = qvalid && key <= qpos;
+      s[v] = vis ? sacc[v] * a.scale : -INFINITY;
+      mt = fmaxf(mt, s[v]);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);
+    const float corr = (m == -INFINITY) ? 0.0f : expf(m - mn);
+    float ps = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      s[v] = (s[v] == -INFINITY) ? 0.0f : expf(s[v] - mn);
+      ps += s[v];
+    }
+    ps += __shfl_xor(ps, 32, 64);
+    lsum = lsum * corr + ps;
+    m = mn;
+    // a factor of exactly 1 (no query's max moved) changes nothing
+    if (__any(corr != 1.0f)) {
+#pragma unroll
+      for (int i = 0; i < DT; ++i) o[i] = o[i] * corr;
+    }
+    // P^T as the B operand: 16-key step st takes score registers 8 st .. 8 st + 7
+    half8 ph[2], pl[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        _Float16 hh, ll;
+        split_h(s[8 * st + e], hh, ll);
+        ph[st][e] = hh;
+        pl[st][e] = ll;
+      }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const half8 vh = *reinterpret_cast<const half8*>(&vts[0][32 * dt + fr][16 * st + fk]);
+        const half8 vl = *reinterpret_cast<const half8*>(&vts[1][32 * dt + fr][16 * st + fk]);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, ph[st], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pl[st], o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph[st], o[dt], 0, 0, 0);
+      }
+  }
+  if (my_bad) bad = 1;  // any writer sets it
+  __syncthreads();
+  if (tid == 0 && bad && a.err) atomicOr(a.err, ERR_F16_RANGE);
+  if (!active || !qvalid) return;
+  // O^T[dim][query]: lane holds query fr, dims 32 dt + 8 (v / 4) + 4 (lane / 32) + v % 4
+  if (splits == 1) {
+    float* dst = a.out + size_t(q0 + fr) * a.H * HD + size_t(h) * HD;
+    const float inv = 1.0f / lsum;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float4 v4 = make_float4(o[dt][4 * r] * inv, o[dt][4 * r + 1] * inv, o[dt][4 * r + 2] * inv,
+                                      o[dt][4 * r + 3] * inv);
+        *reinterpret_cast<float4*>(dst + 32 * dt + 8 * r + 4 * (lane >> 5)) = v4;
+      }
+  } else {
+    // partial: [split][query][head][HD + 2]: unnormalised O, then (max, sum)
+    float* dst = a.part + ((size_t(sp) * a.N + q0 + fr) * a.H + h) * (HD + 2);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) dst[32 * dt + 8 * r + 4 * (lane >> 5) + c] = o[dt][4 * r + c];
+    if (lane < 32) {
+      dst[HD] = m;
+      dst[HD + 1] = lsum;
     }
   }
-  if (!active) return;
-#pragma unroll
-  for (int c = 0; c < PQ; ++c) {
-    if (uint32_t(c) >= nq) continue;
-    float* dst = a.out + size_t(q0 + c) * a.H * HD + size_t(h) * HD;
-    const float inv = 1.0f / l[c];
-#pragma unroll
-    for (int j = 0; j < HD / 64; ++j) dst[lane + 64 * j] = o[c][j] * inv;
+}
+
+// Merges the key splits of attn_prefill_kernel: thread = (query, head, dim),
+// splits combined in order; a split that saw no key has max -inf and adds 0.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_prefill_merge_kernel(PrefillAttnArgs a, uint32_t splits) {
+  const uint32_t qh = blockIdx.x, q = qh / a.H, h = qh % a.H, d = threadIdx.x;
+  const size_t stride = size_t(a.N) * a.H * (HD + 2);
+  const float* p = a.part + (size_t(q) * a.H + h) * (HD + 2);
+  float M = -INFINITY;
+  for (uint32_t s = 0; s < splits; ++s) M = fmaxf(M, p[s * stride + HD]);
+  float L = 0.0f, acc = 0.0f;
+  for (uint32_t s = 0; s < splits; ++s) {
+    const float ms = p[s * stride + HD];
+    if (ms == -INFINITY) continue;
+    const float f = expf(ms - M);
+    L = fmaf(p[s * stride + HD + 1], f, L);
+    acc = fmaf(p[s * stride + d], f, acc);
   }
+  a.out[size_t(q) * a.H * HD + size_t(h) * HD + d] = acc / L;
 }
 
 }  // namespace
 
 hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, float eps, uint32_t N, uint32_t Npad,
                              uint32_t K, _Float16* xh, _Float16* xl, float* rs, hipStream_t s) {
-  if (Npad < N || Npad % 16 || K % GK) return hipErrorInvalidValue;
+  if (Npad < N || Npad % 16 || K % KS) return hipErrorInvalidValue;
   hipLaunchKernelGGL(split_rows_kernel, dim3(Npad), dim3(256), 0, s, x, ldx, norm, eps, N, K, xh, xl, rs);
   return hipGetLastError();
 }
 
+// Two register sets in flight (stage st + 2 loads while st computes): 3 and
+// 4 sets measured the same for 1536-token prefill (92.3 / 94.3 / 93.1 ms).
+constexpr int GEMM_DEPTH = 2;
+
 template <uint32_t WT>
-static hipError_t gemm_epi(int epi, const GemmArgs& a, dim3 grid, hipStream_t s) {
+static hipError_t gemm_epi(int epi, const GemmArgs& a, uint32_t m_tiles, uint32_t n_tiles, uint32_t splits,
+                           hipStream_t s) {
+  const dim3 grid((m_tiles + 7u) / 8u * 8u * n_tiles * splits), block(256);
   switch (epi) {
-    case EPI_STORE: hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_STORE>), grid, dim3(256), 0, s, a); break;
-    case EPI_RESID: hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_RESID>), grid, dim3(256), 0, s, a); break;
+    case EPI_STORE:
+      hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_STORE, GEMM_DEPTH>), grid, block, 0, s, a, m_tiles, n_tiles,
+                         splits);
+      break;
+    case EPI_RESID:
+      hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_RESID, GEMM_DEPTH>), grid, block, 0, s, a, m_tiles, n_tiles,
+                         splits);
+      break;
     case EPI_SWIGLU_SLOW:
-      hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_SWIGLU_SLOW>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_SWIGLU_SLOW, GEMM_DEPTH>), grid, block, 0, s, a, m_tiles, n_tiles,
+                         splits);
       break;
     case EPI_SWIGLU_FAST:
-      hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_SWIGLU_FAST>), grid, dim3(256), 0, s, a);
+      hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_SWIGLU_FAST, GEMM_DEPTH>), grid, block, 0, s, a, m_tiles, n_tiles,
+                         splits);
       break;
     default: return hipErrorInvalidValue;
   }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  const dim3 rgrid(uint32_t((size_t(a.N) * (a.M / 4u) + 255u) / 256u));
+  if (epi == EPI_STORE)
+    hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI_STORE>), rgrid, block, 0, s, a, splits);
+  else
+    hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI_RESID>), rgrid, block, 0, s, a, splits);
   return hipGetLastError();
 }
 
-uint32_t gemm_rows_pad(uint32_t n) { return (n + GN - 1) / GN * GN; }
+uint32_t gemm_rows_pad(uint32_t n) { return (n + TN - 1) / TN * TN; }
+
+size_t gemm_part_floats(uint32_t n_pad, uint32_t m) { return size_t(GEMM_MAX_SPLITS) * n_pad * m; }
 
 hipError_t launch_gemm_mfma(uint32_t wtype, int epi, const GemmArgs& a, hipStream_t s) {
-  if (a.K % GK || a.M == 0 || a.N == 0) return hipErrorInvalidValue;
+  if (a.K % KS || a.M == 0 || a.N == 0) return hipErrorInvalidValue;
   const bool dual = epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST;
   if (dual && !a.w3) return hipErrorInvalidValue;
-  const dim3 grid((a.M + GM - 1) / GM, gemm_rows_pad(a.N) / GN);
+  const uint32_t m_tiles = dual ? (a.M + 63u) / 64u : (a.M + TM - 1u) / TM;
+  const uint32_t n_tiles = gemm_rows_pad(a.N) / TN;
+  // short-M products: split K so that the grid covers the 256 CUs (each split
+  // keeps at least 8 stages of K)
+  uint32_t splits = 1;
+  if (!dual && a.part && a.M % 4u == 0) {
+    const uint32_t tiles = m_tiles * n_tiles;
+    while (splits < GEMM_MAX_SPLITS && tiles * splits < 256u && a.K / KS >= 8u * (splits + 1u) &&
+           size_t(splits + 1u) * a.N * a.M <= a.part_cap)
+      ++splits;
+  }
   switch (wtype) {
-    case W_F16: return gemm_epi<W_F16>(epi, a, grid, s);
-    case W_Q8_0: return gemm_epi<W_Q8_0>(epi, a, grid, s);
-    case W_Q4_0: return gemm_epi<W_Q4_0>(epi, a, grid, s);
+    case W_F16: return gemm_epi<W_F16>(epi, a, m_tiles, n_tiles, splits, s);
+    case W_Q8_0: return gemm_epi<W_Q8_0>(epi, a, m_tiles, n_tiles, splits, s);
+    case W_Q4_0: return gemm_epi<W_Q4_0>(epi, a, m_tiles, n_tiles, splits, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -552,18 +851,29 @@ hipError_t launch_skinny_mfma(uint32_t wtype, int epi, const SkinnyArgs& a, hipS
   }
 }
 
+size_t attn_prefill_part_floats(uint32_t n, uint32_t heads, uint32_t hd) {
+  return size_t(ATTN_MAX_SPLITS) * n * heads * (hd + 2);
+}
+
+template <int HD>
+static void attn_prefill_launch(const PrefillAttnArgs& a, uint32_t splits, hipStream_t s) {
+  const dim3 grid((a.N + AQ - 1) / AQ, a.Hkv, splits);
+  hipLaunchKernelGGL((a.kv_f16 ? attn_prefill_kernel<HD, true> : attn_prefill_kernel<HD, false>), grid, dim3(256), 0,
+                     s, a, splits);
+  if (splits > 1) hipLaunchKernelGGL((attn_prefill_merge_kernel<HD>), dim3(a.N * a.H), dim3(HD), 0, s, a, splits);
+}
+
 hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s) {
   if (!a.pos_ptr || a.H % a.Hkv || a.H / a.Hkv > 4 || a.N == 0) return hipErrorInvalidValue;
-  const dim3 grid((a.N + PQ - 1) / PQ, a.Hkv);
+  // key splits so that the grid covers the CUs twice over (two blocks fit a CU)
+  const uint32_t blocks = (a.N + AQ - 1) / AQ * a.Hkv;
+  uint32_t splits = 1;
+  while (splits < ATTN_MAX_SPLITS && blocks * splits < 512u &&
+         size_t(splits + 1) * a.N * a.H * (a.hd + 2) <= a.part_cap && a.part)
+    ++splits;
   switch (a.hd) {
-    case 64:
-      hipLaunchKernelGGL((a.kv_f16 ? attn_prefill_kernel<64, true> : attn_prefill_kernel<64, false>), grid, dim3(256),
-                         0, s, a);
-      break;
-    case 128:
-      hipLaunchKernelGGL((a.kv_f16 ? attn_prefill_kernel<128, true> : attn_prefill_kernel<128, false>), grid,
-                         dim3(256), 0, s, a);
-      break;
+    case 64: attn_prefill_launch<64>(a, splits, s); break;
+    case 128: attn_prefill_launch<128>(a, splits, s); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
