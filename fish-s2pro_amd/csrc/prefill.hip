@@ -144,11 +144,9 @@ __device__ __forceinline__ void weight8(const uint8_t* row, uint32_t e, half8& h
 //   token fragment as A and the weight fragment as B, so a lane's results
 //   are 16 tokens x one weight row and the 32 lanes of a row group store 32
 //   consecutive outputs.  Per 16-wide k step a wave reads 2 weight and 4
-//   token fragments (hi and lo planes) from LDS for 8 MFMAs (F16), about 3 KB
-//   per 1000 MFMA cycles per SIMD.  K goes in stages of 32 through a double
-//   buffer in LDS (rows padded to 40 halfs: the 16-byte fragment reads of 8
-//   consecutive lanes hit distinct banks); the next stage's global loads are
-//   in flight while the current one computes.
+//   token fragments (hi and lo planes) from LDS for 8 MFMAs (F16).  K goes in
+//   stages of 32 through a double buffer in LDS (swizzled rows, see tile_off);
+//   the loads of the stage after next are in flight while a stage computes.
 //   SwiGLU (w1 and w3): the 128 row slots hold 64 outputs as [w1 32 | w3 32 |
 //   w1 32 | w3 32], so each wave holds w1 and w3 of the same outputs.
 //   Tile order: blocks L and L + 8 run on the same XCD, so the n tiles (and
@@ -158,17 +156,79 @@ __device__ __forceinline__ void weight8(const uint8_t* row, uint32_t e, half8& h
 //   to part[split][n][m]; gemm_split_reduce_kernel adds the splits in order
 //   and applies rs and the epilogue.
 // ---------------------------------------------------------------------------
-constexpr int TM = 128, TN = 128, KS = 32, KP = KS + 8;
+constexpr int TM = 128, TN = 128, KS = 32;
+
+// LDS tile rows are KS halfs (four 16-byte chunks) with no padding; chunk j of
+// row r sits at chunk position j ^ swz(r).  Both access patterns then hit
+// distinct banks with 32 or 64 banks of 4 bytes: the staging stores (4 lanes
+// per row, consecutive rows) and the fragment reads (one row per lane, 32
+// consecutive rows, one chunk).
+__device__ __forceinline__ uint32_t swz(uint32_t r) { return ((r >> 1) ^ (r >> 3)) & 3u; }
+__device__ __forceinline__ uint32_t tile_off(uint32_t r, uint32_t k) {  // k: a multiple of 8
+  return r * KS + (((k >> 3) ^ swz(r)) << 3);
+}
 constexpr uint32_t GEMM_MAX_SPLITS = 4;
 
+// Epilogue of the MFMA GEMM: acc[tn][tm][v] = D[token 8 (v/4) + 4 (lane/32) +
+// v%4][weight slot lane%32] of the wave's 2 x 2 tiles.
+template <uint32_t WT, int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, const floatx16 (&acc)[2][2],
+                                              const floatx16 (&accl)[WT != W_F16 ? 2 : 1][WT != W_F16 ? 2 : 1],
+                                              uint32_t mt, uint32_t n_base, uint32_t sp, uint32_t splits,
+                                              uint32_t wm, uint32_t wn, uint32_t lane) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr bool WSPLIT = WT != W_F16;
+  const uint32_t fr = lane & 31u;
+#pragma unroll
+  for (int tn = 0; tn < 2; ++tn) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const uint32_t n = n_base + 64 * wn + 32 * tn + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+      float g[2];
+#pragma unroll
+      for (int tm = 0; tm < 2; ++tm) {
+        g[tm] = acc[tn][tm][v];
+        if constexpr (WSPLIT) g[tm] = g[tm] + accl[tn][tm][v] * (1.0f / 2048.0f);
+      }
+      if constexpr (DUAL) {
+        const uint32_t m = mt * 64u + 32u * wm + fr;
+        if (n >= a.N || m >= a.M) continue;
+        const float r = a.rs[n];
+        const float gg = g[0] * r, u = g[1] * r;
+        float* dst = a.y + size_t(n) * a.ldy + m;
+        if constexpr (EPI == EPI_SWIGLU_SLOW) {
+          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gg)));
+          *dst = __fmul_rn(__fmul_rn(gg, sig), u);
+        } else {
+          *dst = __fmul_rn(__fdiv_rn(gg, __fadd_rn(1.0f, expf_glibc(-gg))), u);
+        }
+      } else {
+#pragma unroll
+        for (int tm = 0; tm < 2; ++tm) {
+          const uint32_t m = mt * TM + 64u * wm + 32u * tm + fr;
+          if (n >= a.N || m >= a.M) continue;
+          if (splits > 1) {
+            a.part[(size_t(sp) * a.N + n) * a.M + m] = g[tm];
+          } else {
+            const float gg = g[tm] * a.rs[n];
+            float* dst = a.y + size_t(n) * a.ldy + m;
+            if constexpr (EPI == EPI_STORE) *dst = gg;
+            else *dst = __fadd_rn(*dst, gg);
+          }
+        }
+      }
+    }
+  }
+}
+
 template <uint32_t WT, int EPI, int D>
-__global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs a, uint32_t m_tiles, uint32_t n_tiles,
+__global__ __launch_bounds__(256, 3) void gemm_mfma_kernel(GemmArgs a, uint32_t m_tiles, uint32_t n_tiles,
                                                            uint32_t splits) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
   constexpr bool WSPLIT = WT != W_F16;
   constexpr int WP = WSPLIT ? 2 : 1;  // weight planes in LDS (hi, lo * 2^11)
-  __shared__ _Float16 xs[2][2][TN][KP];
-  __shared__ _Float16 ws[2][WP][TM][KP];
+  __shared__ _Float16 xs[2][2][TN * KS];
+  __shared__ _Float16 ws[2][WP][TM * KS];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wm = wave & 1u, wn = wave >> 1;
   const uint32_t L = blockIdx.x, inner = n_tiles * splits;
@@ -223,12 +283,12 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs a, uint32_t 
     for (int j = 0; j < 2; ++j) {
       const uint32_t slot = (tid + 256u * j) >> 2;
 #pragma unroll
-      for (int p = 0; p < WP; ++p) *reinterpret_cast<half8*>(&ws[buf][p][slot][part8]) = rw[r][j][p];
+      for (int p = 0; p < WP; ++p) *reinterpret_cast<half8*>(&ws[buf][p][tile_off(slot, part8)]) = rw[r][j][p];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t c = tid + 256u * j;
-      *reinterpret_cast<half8*>(&xs[buf][c >> 9][(c >> 2) & 127u][part8]) = rx[r][j];
+      *reinterpret_cast<half8*>(&xs[buf][c >> 9][tile_off((c >> 2) & 127u, part8)]) = rx[r][j];
     }
   };
 
@@ -252,12 +312,12 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs a, uint32_t 
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int p = 0; p < 2; ++p)
-          xa[t][p] = *reinterpret_cast<const half8*>(&xs[buf][p][64 * wn + 32 * t + fr][kk + fk]);
+          xa[t][p] = *reinterpret_cast<const half8*>(&xs[buf][p][tile_off(64 * wn + 32 * t + fr, kk + fk)]);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int p = 0; p < WP; ++p)
-          wb[t][p] = *reinterpret_cast<const half8*>(&ws[buf][p][64 * wm + 32 * t + fr][kk + fk]);
+          wb[t][p] = *reinterpret_cast<const half8*>(&ws[buf][p][tile_off(64 * wm + 32 * t + fr, kk + fk)]);
 #pragma unroll
       for (int tn = 0; tn < 2; ++tn)
 #pragma unroll
@@ -291,47 +351,181 @@ __global__ __launch_bounds__(256, 2) void gemm_mfma_kernel(GemmArgs a, uint32_t 
     }
   }
 
-  // epilogue: acc[tn][tm][v] = D[token 8 (v/4) + 4 (lane/32) + v%4][weight slot lane%32]
+  gemm_epilogue<WT, EPI>(a, acc, accl, mt, n_base, sp, splits, wm, wn, lane);
+}
+
+// F16 weights: the same tiles, staged by LDS-DMA loads (global_load_lds_dwordx4:
+// a wave's 64 lanes fill 1 KiB of LDS, lane i at byte 16 i of the wave's
+// destination), so staging takes no registers and no LDS store instructions.
+// A wave's 1 KiB is 16 consecutive tile rows of 64 bytes; lane i takes row
+// i / 4 and physical chunk i % 4 and loads the logical chunk (i % 4) ^ swz(row),
+// which puts the tile in the swizzled layout of tile_off.  Three LDS stages
+// rotate: while stage st computes, stage st + 1 is in flight and stage st + 2
+// is issued into the buffer that stage st - 1 has left.
+constexpr uint32_t GEMM_DMA_PER_STAGE = 6;  // 16-byte loads per thread per stage (4 token + 2 weight)
+
+constexpr bool DUAL_EPI(int epi) { return epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST; }
+
+// One LDS-DMA load: 16 bytes per lane from `src` into the wave's 1 KiB at
+// `lds` (lane i at byte 16 i).  Written as inline assembly so that the
+// compiler does not treat every later LDS read as dependent on it (it would
+// wait for all loads in flight first); the kernel waits for these loads
+// itself (vmcnt) before the barrier that publishes a stage.
+__device__ __forceinline__ void dma16(const void* src, const _Float16* lds) {
+  const uint32_t m0 = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(reinterpret_cast<uintptr_t>(lds)))));
+  asm volatile("s_nop 1\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src)
+               : "memory", "m0");
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef const __attribute__((address_space(1))) void glob_void_t;
+
+template <int B>
+struct StageTag {
+  static constexpr int value = B;
+};
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_f16_dma_kernel(GemmArgs a, uint32_t m_tiles, uint32_t n_tiles,
+                                                              uint32_t splits) {
+  // one LDS object per stage buffer, always addressed with a compile-time
+  // stage index: the compiler then knows which buffer a DMA writes and a
+  // fragment read reads, and waits only where they meet
+  __shared__ _Float16 xs0[2 * TN * KS], xs1[2 * TN * KS], xs2[2 * TN * KS];
+  __shared__ _Float16 ws0[TM * KS], ws1[TM * KS], ws2[TM * KS];
+  auto xbuf = [&](auto tag) -> _Float16* {
+    if constexpr (decltype(tag)::value == 0) return xs0;
+    else if constexpr (decltype(tag)::value == 1) return xs1;
+    else return xs2;
+  };
+  auto wbuf = [&](auto tag) -> _Float16* {
+    if constexpr (decltype(tag)::value == 0) return ws0;
+    else if constexpr (decltype(tag)::value == 1) return ws1;
+    else return ws2;
+  };
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wm = wave & 1u, wn = wave >> 1;
+  const uint32_t L = blockIdx.x, inner = n_tiles * splits;
+  const uint32_t sidx = L >> 3, mt = (sidx / inner) * 8u + (L & 7u);
+  if (mt >= m_tiles) return;
+  const uint32_t rr = sidx % inner, nt = rr % n_tiles, sp = rr / n_tiles;
+  const uint32_t n_base = nt * TN;
+  const uint32_t nst = a.K / KS, st0 = sp * nst / splits, st1 = (sp + 1) * nst / splits;
+
+  // this lane's rows and logical chunks: token chunk c = tid + 256 j (j < 4):
+  // plane c / 512, row (c / 4) % 128; weight chunk c = tid + 256 j (j < 2):
+  // slot c / 4.  The LDS destination of the wave's load j is the 1 KiB at the
+  // tile row of its lane 0.
+  // Source addresses are a wave-uniform base (scalar registers, advanced by
+  // the stage's k offset) plus a loop-invariant 32-bit lane offset, so the
+  // loads take the scalar-base form and no address register is rebuilt.
+  const uint32_t pc = lane & 3u;  // physical chunk
+  const uint8_t* xbase[4];
+  uint32_t xoff[4], xdst[4];
 #pragma unroll
-  for (int tn = 0; tn < 2; ++tn) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const uint32_t n = n_base + 64 * wn + 32 * tn + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-      float g[2];
-#pragma unroll
-      for (int tm = 0; tm < 2; ++tm) {
-        g[tm] = acc[tn][tm][v];
-        if constexpr (WSPLIT) g[tm] = g[tm] + accl[tn][tm][v] * (1.0f / 2048.0f);
-      }
-      if constexpr (DUAL) {
-        const uint32_t m = mt * 64u + 32u * wm + fr;
-        if (n >= a.N || m >= a.M) continue;
-        const float r = a.rs[n];
-        const float gg = g[0] * r, u = g[1] * r;
-        float* dst = a.y + size_t(n) * a.ldy + m;
-        if constexpr (EPI == EPI_SWIGLU_SLOW) {
-          const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-gg)));
-          *dst = __fmul_rn(__fmul_rn(gg, sig), u);
-        } else {
-          *dst = __fmul_rn(__fdiv_rn(gg, __fadd_rn(1.0f, expf_glibc(-gg))), u);
-        }
-      } else {
-#pragma unroll
-        for (int tm = 0; tm < 2; ++tm) {
-          const uint32_t m = mt * TM + 64u * wm + 32u * tm + fr;
-          if (n >= a.N || m >= a.M) continue;
-          if (splits > 1) {
-            a.part[(size_t(sp) * a.N + n) * a.M + m] = g[tm];
-          } else {
-            const float gg = g[tm] * a.rs[n];
-            float* dst = a.y + size_t(n) * a.ldy + m;
-            if constexpr (EPI == EPI_STORE) *dst = gg;
-            else *dst = __fadd_rn(*dst, gg);
-          }
-        }
-      }
-    }
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t c = tid + 256u * j, plane = c >> 9, row = (c >> 2) & 127u;
+    xbase[j] = reinterpret_cast<const uint8_t*>((plane ? a.xl : a.xh) + size_t(n_base) * a.K);
+    xoff[j] = (row * a.K + ((pc ^ swz(row)) << 3)) * 2u;
+    xdst[j] = plane * (TN * KS) + (((c & ~63u) >> 2) & 127u) * KS;  // halfs, wave-uniform
   }
+  const uint8_t* wbase[2];
+  uint32_t woff[2], wdst[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t c = tid + 256u * j, slot = c >> 2;
+    uint32_t row;
+    const uint8_t* base = a.w;
+    if constexpr (DUAL_EPI(EPI)) {
+      const uint32_t grp = slot >> 5;  // w1 / w3 alternate every 32 slots: uniform over a wave
+      row = mt * 64u + (grp >> 1) * 32u + (slot & 31u);
+      base = (grp & 1u) ? a.w3 : a.w;
+      const uint64_t bu = reinterpret_cast<uint64_t>(base);
+      base = reinterpret_cast<const uint8_t*>(
+          uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(bu))))) |
+          (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(bu >> 32))))) << 32));
+    } else {
+      row = mt * TM + slot;
+    }
+    wbase[j] = base;
+    woff[j] = uint32_t(min(row, a.M - 1) * a.row_bytes) + ((pc ^ swz(slot)) << 4);
+    wdst[j] = ((c & ~63u) >> 2) * KS;
+  }
+  // The address registers of a stage's loads are kept live until the end of
+  // the step that issued them (`hold`): were they reused for a fragment
+  // read's result, the compiler would first wait for every load in flight.
+  const uint8_t* src[6];
+  auto issue = [&](uint32_t st, auto tag) {
+    const uint32_t kb = min(st, st1 - 1u) * (KS * 2u);  // bytes; past the range: a valid, unused stage
+    _Float16* xb = xbuf(tag);
+    _Float16* wb = wbuf(tag);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) src[j] = xbase[j] + kb + xoff[j];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) src[4 + j] = wbase[j] + kb + woff[j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(src[j], xb + xdst[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(src[4 + j], wb + wdst[j]);
+  };
+  auto hold = [&]() {
+    asm volatile("" : : "v"(src[0]), "v"(src[1]), "v"(src[2]), "v"(src[3]), "v"(src[4]), "v"(src[5]));
+  };
+
+  floatx16 acc[2][2], accl[1][1];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
+  const uint32_t fr = lane & 31u, fk = 8u * (lane >> 5);
+  // stage st in buffer B: wait until it has landed in every thread (only the
+  // next stage's loads may still be in flight), then the buffer of stage st - 1
+  // is free for stage st + 2
+  auto step = [&](uint32_t st, auto tag) {
+    constexpr int B = decltype(tag)::value;
+    __builtin_amdgcn_s_waitcnt(0x0F70 | GEMM_DMA_PER_STAGE);  // vmcnt(6); lgkmcnt / expcnt unconstrained
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // every fragment of the stage is read before the next loads are issued
+    // (an LDS read behind an LDS-DMA load makes the compiler wait for it)
+    const _Float16* xb = xbuf(tag);
+    const _Float16* wb = wbuf(tag);
+    half8 xa[2][2][2], wf[2][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const uint32_t kk = 16u * q;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+          xa[q][t][p] = *reinterpret_cast<const half8*>(xb + p * (TN * KS) + tile_off(64 * wn + 32 * t + fr, kk + fk));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        wf[q][t] = *reinterpret_cast<const half8*>(wb + tile_off(64 * wm + 32 * t + fr, kk + fk));
+    }
+    issue(st + 2, StageTag<(B + 2) % 3>{});
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+      // the four accumulators' hi products first, then their lo products
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int tn = 0; tn < 2; ++tn)
+#pragma unroll
+          for (int tm = 0; tm < 2; ++tm)
+            acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[q][tn][p], wf[q][tm], acc[tn][tm], 0, 0, 0);
+    hold();
+  };
+  issue(st0, StageTag<0>{});
+  issue(st0 + 1, StageTag<1>{});
+  for (uint32_t st = st0; st < st1; st += 3) {
+    step(st, StageTag<0>{});
+    if (st + 1 < st1) step(st + 1, StageTag<1>{});
+    if (st + 2 < st1) step(st + 2, StageTag<2>{});
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // the unused tail loads have landed before the block ends
+  gemm_epilogue<W_F16, EPI>(a, acc, accl, mt, n_base, sp, splits, wm, wn, lane);
 }
 
 // y[n][m] (op)= rs[n] * (part[0][n][m] + part[1][n][m] + ...), splits added in
@@ -765,10 +959,35 @@ hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, fl
 // 4 sets measured the same for 1536-token prefill (92.3 / 94.3 / 93.1 ms).
 constexpr int GEMM_DEPTH = 2;
 
+static hipError_t gemm_f16(int epi, const GemmArgs& a, uint32_t m_tiles, uint32_t n_tiles, uint32_t splits,
+                           hipStream_t s) {
+  const dim3 grid((m_tiles + 7u) / 8u * 8u * n_tiles * splits), block(256);
+  switch (epi) {
+    case EPI_STORE:
+      hipLaunchKernelGGL((gemm_f16_dma_kernel<EPI_STORE>), grid, block, 0, s, a, m_tiles, n_tiles, splits);
+      break;
+    case EPI_RESID:
+      hipLaunchKernelGGL((gemm_f16_dma_kernel<EPI_RESID>), grid, block, 0, s, a, m_tiles, n_tiles, splits);
+      break;
+    case EPI_SWIGLU_SLOW:
+      hipLaunchKernelGGL((gemm_f16_dma_kernel<EPI_SWIGLU_SLOW>), grid, block, 0, s, a, m_tiles, n_tiles, splits);
+      break;
+    case EPI_SWIGLU_FAST:
+      hipLaunchKernelGGL((gemm_f16_dma_kernel<EPI_SWIGLU_FAST>), grid, block, 0, s, a, m_tiles, n_tiles, splits);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <uint32_t WT>
 static hipError_t gemm_epi(int epi, const GemmArgs& a, uint32_t m_tiles, uint32_t n_tiles, uint32_t splits,
                            hipStream_t s) {
   const dim3 grid((m_tiles + 7u) / 8u * 8u * n_tiles * splits), block(256);
+  if (WT == W_F16) {
+    const hipError_t e = gemm_f16(epi, a, m_tiles, n_tiles, splits, s);
+    if (e != hipSuccess) return e;
+  } else {
   switch (epi) {
     case EPI_STORE:
       hipLaunchKernelGGL((gemm_mfma_kernel<WT, EPI_STORE, GEMM_DEPTH>), grid, block, 0, s, a, m_tiles, n_tiles,
@@ -787,6 +1006,7 @@ static hipError_t gemm_epi(int epi, const GemmArgs& a, uint32_t m_tiles, uint32_
                          splits);
       break;
     default: return hipErrorInvalidValue;
+  }
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
