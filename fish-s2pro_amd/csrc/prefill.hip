@@ -911,8 +911,8 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillAttnArgs a,
         *reinterpret_cast<float4*>(dst + 32 * dt + 8 * r + 4 * (lane >> 5)) = v4;
       }
   } else {
-    // partial: [split][query][head][HD + 2]: unnormalised O, then (max, sum)
-    float* dst = a.part + ((size_t(sp) * a.N + q0 + fr) * a.H + h) * (HD + 2);
+    // partial: [split][query][head][HD + 4]: unnormalised O, then (max, sum) (rows 16-byte aligned)
+    float* dst = a.part + ((size_t(sp) * a.N + q0 + fr) * a.H + h) * (HD + 4);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -926,24 +926,45 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillAttnArgs a,
   }
 }
 
-// Merges the key splits of attn_prefill_kernel: thread = (query, head, dim),
-// splits combined in order; a split that saw no key has max -inf and adds 0.
+// Merges the key splits of attn_prefill_kernel: 32 threads per (query, head)
+// pair, 4 dims each; every split's partial is loaded in one batch, then
+// combined in split order (a split that saw no key has max -inf and adds 0).
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_prefill_merge_kernel(PrefillAttnArgs a, uint32_t splits) {
-  const uint32_t qh = blockIdx.x, q = qh / a.H, h = qh % a.H, d = threadIdx.x;
-  const size_t stride = size_t(a.N) * a.H * (HD + 2);
-  const float* p = a.part + (size_t(q) * a.H + h) * (HD + 2);
-  float M = -INFINITY;
-  for (uint32_t s = 0; s < splits; ++s) M = fmaxf(M, p[s * stride + HD]);
-  float L = 0.0f, acc = 0.0f;
-  for (uint32_t s = 0; s < splits; ++s) {
-    const float ms = p[s * stride + HD];
-    if (ms == -INFINITY) continue;
-    const float f = expf(ms - M);
-    L = fmaf(p[s * stride + HD + 1], f, L);
-    acc = fmaf(p[s * stride + d], f, acc);
+__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(PrefillAttnArgs a, uint32_t splits) {
+  constexpr uint32_t TPP = HD / 4;  // threads per pair
+  const uint32_t pair = blockIdx.x * (256 / TPP) + threadIdx.x / TPP, d = (threadIdx.x % TPP) * 4;
+  if (pair >= a.N * a.H) return;
+  const uint32_t q = pair / a.H, h = pair % a.H;
+  const size_t stride = size_t(a.N) * a.H * (HD + 4);
+  const float* p = a.part + (size_t(q) * a.H + h) * (HD + 4);
+  float ms[ATTN_MAX_SPLITS], ls[ATTN_MAX_SPLITS];
+  float4 os[ATTN_MAX_SPLITS];
+#pragma unroll
+  for (uint32_t s = 0; s < ATTN_MAX_SPLITS; ++s) {
+    const float* ps = p + min(s, splits - 1u) * stride;
+    ms[s] = ps[HD];
+    ls[s] = ps[HD + 1];
+    os[s] = *reinterpret_cast<const float4*>(ps + d);
   }
-  a.out[size_t(q) * a.H * HD + size_t(h) * HD + d] = acc / L;
+  float M = -INFINITY;
+#pragma unroll
+  for (uint32_t s = 0; s < ATTN_MAX_SPLITS; ++s)
+    if (s < splits) M = fmaxf(M, ms[s]);
+  float L = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (uint32_t s = 0; s < ATTN_MAX_SPLITS; ++s) {
+    if (s >= splits || ms[s] == -INFINITY) continue;
+    const float f = expf(ms[s] - M);
+    L = fmaf(ls[s], f, L);
+    acc.x = fmaf(os[s].x, f, acc.x);
+    acc.y = fmaf(os[s].y, f, acc.y);
+    acc.z = fmaf(os[s].z, f, acc.z);
+    acc.w = fmaf(os[s].w, f, acc.w);
+  }
+  const float inv = 1.0f / L;
+  *reinterpret_cast<float4*>(a.out + size_t(q) * a.H * HD + size_t(h) * HD + d) =
+      make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 }  // namespace
@@ -1072,7 +1093,7 @@ hipError_t launch_skinny_mfma(uint32_t wtype, int epi, const SkinnyArgs& a, hipS
 }
 
 size_t attn_prefill_part_floats(uint32_t n, uint32_t heads, uint32_t hd) {
-  return size_t(ATTN_MAX_SPLITS) * n * heads * (hd + 2);
+  return size_t(ATTN_MAX_SPLITS) * n * heads * (hd + 4);
 }
 
 template <int HD>
@@ -1080,7 +1101,9 @@ static void attn_prefill_launch(const PrefillAttnArgs& a, uint32_t splits, hipSt
   const dim3 grid((a.N + AQ - 1) / AQ, a.Hkv, splits);
   hipLaunchKernelGGL((a.kv_f16 ? attn_prefill_kernel<HD, true> : attn_prefill_kernel<HD, false>), grid, dim3(256), 0,
                      s, a, splits);
-  if (splits > 1) hipLaunchKernelGGL((attn_prefill_merge_kernel<HD>), dim3(a.N * a.H), dim3(HD), 0, s, a, splits);
+  if (splits > 1)
+    hipLaunchKernelGGL((attn_prefill_merge_kernel<HD>), dim3((a.N * a.H * (HD / 4) + 255) / 256), dim3(256), 0, s, a,
+                       splits);
 }
 
 hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s) {
@@ -1089,7 +1112,7 @@ hipError_t launch_attention_prefill(const PrefillAttnArgs& a, hipStream_t s) {
   const uint32_t blocks = (a.N + AQ - 1) / AQ * a.Hkv;
   uint32_t splits = 1;
   while (splits < ATTN_MAX_SPLITS && blocks * splits < 512u &&
-         size_t(splits + 1) * a.N * a.H * (a.hd + 2) <= a.part_cap && a.part)
+         size_t(splits + 1) * a.N * a.H * (a.hd + 4) <= a.part_cap && a.part)
     ++splits;
   switch (a.hd) {
     case 64: attn_prefill_launch<64>(a, splits, s); break;
