@@ -48,11 +48,46 @@ __device__ __forceinline__ float wave_max_f(float v) {
 //   rs[n] = power of two with max|xn| / rs[n] in [2^13, 2^14),
 //   xh[n] = f16(xn / rs), xl[n] = f16(xn / rs - xh);  rows N..Npad-1 are zero.
 // ---------------------------------------------------------------------------
+// The row is read once: thread t holds elements 4 (t + 256 i) .. + 3 (float4
+// loads, all issued together) for rows of up to 4 * 256 * SR_REG elements;
+// longer rows take the looped form below.
+constexpr int SR_REG = 10;  // float4 per thread: rows up to 10240 elements
+
+__device__ __forceinline__ float block_reduce_sum4(float v, float* red) {
+  v = wave_sum_f(v);
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+__device__ __forceinline__ float block_reduce_max4(float v, float* red) {
+  v = wave_max_f(v);
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const float t = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return t;
+}
+
+// power-of-two row scale: exact to apply and to undo; max|x| / r in [2^13, 2^14)
+__device__ __forceinline__ float split_scale(float mx) {
+  float r = 1.0f;
+  if (mx > 0.0f && mx < 3.0e38f) {
+    int e;
+    (void)frexpf(mx, &e);  // mx in [2^(e-1), 2^e)
+    r = ldexpf(1.0f, e - 14);
+  }
+  return r;
+}
+
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_t ldx, const float* norm, float eps,
                                                          uint32_t N, uint32_t K, _Float16* xh, _Float16* xl,
                                                          float* rs) {
-  __shared__ float red[8];
-  const uint32_t n = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float red[4];
+  const uint32_t n = blockIdx.x, tid = threadIdx.x;
   _Float16* hr = xh + size_t(n) * K;
   _Float16* lr = xl + size_t(n) * K;
   if (n >= N) {
@@ -64,16 +99,59 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_
     return;
   }
   const float* xr = x + size_t(n) * ldx;
+  const uint32_t K4 = K / 4;  // K is a multiple of 32
+  if (K4 <= 256u * SR_REG) {
+    float4 v[SR_REG], g[SR_REG];
+#pragma unroll
+    for (int i = 0; i < SR_REG; ++i) {
+      const uint32_t j = tid + 256u * i;
+      v[i] = j < K4 ? *reinterpret_cast<const float4*>(xr + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+      g[i] = (norm && j < K4) ? *reinterpret_cast<const float4*>(norm + 4 * j) : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+    float scale = 1.0f;
+    if (norm) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < SR_REG; ++i) ss += v[i].x * v[i].x + v[i].y * v[i].y + v[i].z * v[i].z + v[i].w * v[i].w;
+      const float tot = block_reduce_sum4(ss, red);
+      scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(K)), eps)));
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < SR_REG; ++i) {
+      if (norm) {
+        v[i].x = __fmul_rn(__fmul_rn(v[i].x, scale), g[i].x);
+        v[i].y = __fmul_rn(__fmul_rn(v[i].y, scale), g[i].y);
+        v[i].z = __fmul_rn(__fmul_rn(v[i].z, scale), g[i].z);
+        v[i].w = __fmul_rn(__fmul_rn(v[i].w, scale), g[i].w);
+      }
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    const float r = split_scale(block_reduce_max4(mx, red));
+    const float inv = 1.0f / r;
+#pragma unroll
+    for (int i = 0; i < SR_REG; ++i) {
+      const uint32_t j = tid + 256u * i;
+      if (j >= K4) continue;
+      const float e[4] = {v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv};
+      _Float16 h[4], l[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        h[c] = _Float16(e[c]);
+        l[c] = _Float16(e[c] - float(h[c]));
+      }
+      *reinterpret_cast<uint2*>(hr + 4 * j) = *reinterpret_cast<const uint2*>(h);
+      *reinterpret_cast<uint2*>(lr + 4 * j) = *reinterpret_cast<const uint2*>(l);
+    }
+    if (tid == 0) rs[n] = r;
+    return;
+  }
   float scale = 1.0f;
   if (norm) {
     float ss = 0.0f;
     for (uint32_t i = tid; i < K; i += 256) ss += xr[i] * xr[i];
-    ss = wave_sum_f(ss);
-    if (lane == 0) red[wave] = ss;
-    __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float tot = block_reduce_sum4(ss, red);
     scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(K)), eps)));
-    __syncthreads();
   }
   float mx = 0.0f;
   for (uint32_t i = tid; i < K; i += 256) {
@@ -81,17 +159,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_
     if (norm) v = __fmul_rn(__fmul_rn(v, scale), norm[i]);
     mx = fmaxf(mx, fabsf(v));
   }
-  mx = wave_max_f(mx);
-  if (lane == 0) red[4 + wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[4], red[5]), fmaxf(red[6], red[7]));
-  // power-of-two scale: exact to apply and to undo
-  float r = 1.0f;
-  if (mx > 0.0f && mx < 3.0e38f) {
-    int e;
-    (void)frexpf(mx, &e);  // mx in [2^(e-1), 2^e)
-    r = ldexpf(1.0f, e - 14);
-  }
+  const float r = split_scale(block_reduce_max4(mx, red));
   const float inv = 1.0f / r;
   for (uint32_t i = tid; i < K; i += 256) {
     float v = xr[i];
