@@ -995,39 +995,52 @@ hipError_t gemv_k_epi(int epi, int ncol, const GemvArgs& a, hipStream_t s) {
 //   lanes' reads of their blocks fall in distinct banks.  One row (two for
 //   SwiGLU: w1 and w3) per wave.
 // ---------------------------------------------------------------------------
-// sum_j q_j x[c][j] of one block for NC columns (column c's block at
-// xb + c * xstride), each value decoded once
+// x of a Q GEMV in LDS: the 32 elements of block b as eight 16-byte chunks,
+// chunk c at position c ^ qswz(b), so that the chunk reads of 8 (or 16)
+// consecutive lanes -- consecutive blocks -- hit distinct banks with 32 (or
+// 64) banks; block b's sum of x follows the blocks (qsum_base).
+__device__ __forceinline__ uint32_t qswz(uint32_t b) { return (b ^ (b >> 3)) & 7u; }
+
+// sum_j q'_j x[c][j] of one block for NC columns, q' the stored unsigned value
+// (Q4_0: the nibble, Q8_0: the byte + 128), each byte converted to f32 in one
+// instruction; the caller subtracts 8 (128) times the block's sum of x.
 template <uint32_t WT, int NC>
-__device__ __forceinline__ void qblock_dot(const uint4 (&q)[WT == W_Q8_0 ? 2 : 1], const float* xb, uint32_t xstride,
-                                           float (&accb)[NC]) {
+__device__ __forceinline__ void qblock_dot(const uint4 (&q)[WT == W_Q8_0 ? 2 : 1], const float* xs, uint32_t b,
+                                           uint32_t xstride, float (&accb)[NC]) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) accb[c] = 0.0f;
+  const float* xb = xs + b * 32u;
+  const uint32_t sw = qswz(b);
+  auto chunk = [&](int c, uint32_t ch) -> float4 {
+    return *reinterpret_cast<const float4*>(xb + c * xstride + ((ch ^ sw) << 2));
+  };
+  auto dot4 = [&](uint32_t w, int c, uint32_t ch) {
+    const float4 x = chunk(c, ch);
+    float a = accb[c];
+    // (w >> 8 i) & 0xff as f32 is one v_cvt_f32_ubyte<i>
+    a = fmaf(float(w & 0xffu), x.x, a);
+    a = fmaf(float((w >> 8) & 0xffu), x.y, a);
+    a = fmaf(float((w >> 16) & 0xffu), x.z, a);
+    a = fmaf(float(w >> 24), x.w, a);
+    accb[c] = a;
+  };
   if constexpr (WT == W_Q8_0) {
     const uint32_t qw[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < 8; ++m) {
+      const uint32_t u = qw[m] ^ 0x80808080u;  // int8 q -> q + 128
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float w = float(int8_t((qw[m] >> (8 * i)) & 0xffu));
-#pragma unroll
-        for (int c = 0; c < NC; ++c) accb[c] = fmaf(w, xb[c * xstride + 4 * m + i], accb[c]);
-      }
+      for (int c = 0; c < NC; ++c) dot4(u, c, uint32_t(m));
+    }
   } else {
     const uint32_t qw[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const uint32_t lo = qw[m] & 0x0f0f0f0fu, hi = (qw[m] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float w = float((lo >> (8 * i)) & 0xffu) - 8.0f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) accb[c] = fmaf(w, xb[c * xstride + 4 * m + i], accb[c]);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float w = float((hi >> (8 * i)) & 0xffu) - 8.0f;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) accb[c] = fmaf(w, xb[c * xstride + 16 + 4 * m + i], accb[c]);
+      for (int c = 0; c < NC; ++c) {
+        dot4(lo, c, uint32_t(m));      // elements 4 m .. 4 m + 3
+        dot4(hi, c, uint32_t(4 + m));  // elements 16 + 4 m ..
       }
     }
   }
@@ -1041,7 +1054,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8, NB = IN / 32;
   constexpr uint32_t QW = WT == W_Q8_0 ? 2 : 1;  // 16-byte loads per block
   constexpr int KW = (KIT + WPB - 1) / WPB;
-  constexpr uint32_t XS = NB * 33;  // floats per staged column
+  constexpr uint32_t XS = NB * 32 + NB;  // floats per staged column: the blocks, then their sums
   __shared__ float xs[NC * XS];
   __shared__ float red[NC][WPB];
   const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
@@ -1110,7 +1123,8 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
     }
     __syncthreads();
   }
-  // 4. (normalised) x into LDS, element e of column c at c XS + e + e / 32
+  // 4. (normalised) x into LDS in swizzled chunks (qswz), and each block's sum
+  //    of x (the lane's 8 elements, then the 4 lanes of a block)
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     float scale = 1.0f;
@@ -1124,6 +1138,8 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
     for (int j = 0; j < KW; ++j) {
       const int k = wave + j * WPB;
       if (k < KIT) {
+        float part = 0.0f;
+        const uint32_t e0 = k * 512 + lane * 8, b = e0 >> 5;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           float4 u = xv[c][j][h];
@@ -1134,13 +1150,13 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
             u.z = __fmul_rn(__fmul_rn(u.z, scale), g.z);
             u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
           }
-          const uint32_t e = k * 512 + lane * 8 + 4 * h;
-          float* d = xs + c * XS + e + e / 32;
-          d[0] = u.x;
-          d[1] = u.y;
-          d[2] = u.z;
-          d[3] = u.w;
+          const uint32_t ch = ((e0 & 31u) >> 2) + h;  // chunk of the block
+          *reinterpret_cast<float4*>(xs + c * XS + b * 32u + ((ch ^ qswz(b)) << 2)) = u;
+          part += (u.x + u.y) + (u.z + u.w);
         }
+        part += __shfl_xor(part, 1, WAVE);
+        part += __shfl_xor(part, 2, WAVE);
+        if ((lane & 3) == 0) xs[c * XS + NB * 32u + b] = part;
       }
     }
   }
@@ -1158,10 +1174,10 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
     const uint32_t b = live ? (second ? i - NB : i) : 0u;
     const float d = half_bits_to_float(wd[st]);
     float bs[NC];
-    qblock_dot<WT, NC>(wq[st], xs + b * 33, XS, bs);
+    qblock_dot<WT, NC>(wq[st], xs, b, XS, bs);
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      const float v = d * bs[c];
+      const float v = d * fmaf(-(WT == W_Q8_0 ? 128.0f : 8.0f), xs[c * XS + NB * 32u + b], bs[c]);
       acc[c] = (live && !second) ? __fadd_rn(acc[c], v) : acc[c];
       if constexpr (DUAL) acc3[c] = (live && second) ? __fadd_rn(acc3[c], v) : acc3[c];
     }
