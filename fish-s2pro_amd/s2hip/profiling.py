@@ -17,6 +17,10 @@ launch against the algorithmic bytes.
 kernels matching each --kernel and derives MFMA utilisation and f16 MFMA
 flops (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512) per dispatch.
 
+`tail` averages the durations of the last --count dispatches of one kernel
+in a kernel-trace CSV (e.g. bench.py's timing loop, which runs after the
+decode generations).
+
 `counters` averages one HBM byte counter (FETCH_SIZE or WRITE_SIZE, reported
 in KiB per dispatch) over every dispatch of the kernel matching --kernel, and
 calibrates it against a plain copy kernel of known size: the copy reads and
@@ -147,6 +151,20 @@ def mfma(path, kernel_res):
     return "\n".join(lines)
 
 
+def tail(path, kernel_re, count):
+    pat = re.compile(kernel_re)
+    durs = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            if pat.search(_col(r, "Kernel_Name")):
+                durs.append((int(_col(r, "End_Timestamp")) - int(_col(r, "Start_Timestamp"))) / 1e3)
+    if not durs:
+        raise SystemExit(f"no dispatches of {kernel_re!r}")
+    last = durs[-count:]
+    return (f"{kernel_re}: {len(durs)} dispatches, mean {statistics.fmean(durs):.3f} us; "
+            f"last {len(last)}: mean {statistics.fmean(last):.3f} us, min {min(last):.3f}, max {max(last):.3f}")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -164,6 +182,10 @@ def main(argv=None):
     t.add_argument("--copy-kernel", required=True)
     t.add_argument("--copy-bytes", type=float, required=True)
     t.add_argument("--row", action="append", required=True)
+    tl = sub.add_parser("tail")
+    tl.add_argument("csv")
+    tl.add_argument("--kernel", required=True)
+    tl.add_argument("--count", type=int, required=True)
     m = sub.add_parser("mfma")
     m.add_argument("csv")
     m.add_argument("--kernel", action="append", required=True)
@@ -172,6 +194,8 @@ def main(argv=None):
         print(stats(args.csv, args.top))
     elif args.cmd == "traffic":
         print(traffic(args.fetch_csv, args.write_csv, args.copy_kernel, args.copy_bytes, args.row))
+    elif args.cmd == "tail":
+        print(tail(args.csv, args.kernel, args.count))
     elif args.cmd == "mfma":
         print(mfma(args.csv, args.kernel))
     else:
