@@ -87,13 +87,20 @@ struct Tensor {
   std::vector<uint64_t> dims;  // ne0 (contiguous) first
   uint32_t type;               // 1 F16, 2 Q4_0, 8 Q8_0
   uint16_t fill;               // RMSNorm gain: every element this f16 value (0: random weights)
+  double stdv = -1.0;          // random weights: N(mean, stdv); negative: the file's default std
+  double mean = 0.0;
+  bool zero_first = false;     // element 0 written as +0 (a zero snake alpha, for instance)
   uint64_t offset = 0;
   uint64_t bytes = 0;
+  uint64_t elements() const {
+    uint64_t n = 1;
+    for (uint64_t d : dims) n *= d;
+    return n;
+  }
 };
 
 uint64_t tensor_bytes(const Tensor& t) {
-  uint64_t n = 1;
-  for (uint64_t d : t.dims) n *= d;
+  const uint64_t n = t.elements();
   if (t.type == 1) return n * 2;
   if (t.type == 8) return n / 32 * 34;
   if (t.type == 2) return n / 32 * 18;
@@ -141,8 +148,8 @@ struct Meta {
   std::string s;
 };
 
-// One f16 weight value: N(0, std) from (seed, tensor, element).
-inline uint16_t weight_half(uint64_t tkey, uint64_t e, double stdv) {
+// One f16 weight value: N(mean, std) from (seed, tensor, element).
+inline uint16_t weight_half(uint64_t tkey, uint64_t e, double stdv, double mean = 0.0) {
   const uint64_t p = e >> 1;
   const uint64_t h1 = splitmix64(tkey + 2 * p), h2 = splitmix64(tkey + 2 * p + 1);
   const double u1 = double((h1 >> 11) + 1) * 0x1.0p-53;  // (0, 1]
@@ -150,7 +157,7 @@ inline uint16_t weight_half(uint64_t tkey, uint64_t e, double stdv) {
   const double r = std::sqrt(-2.0 * std::log(u1));
   const double a = 6.283185307179586 * u2;
   const double z = (e & 1) ? r * std::sin(a) : r * std::cos(a);
-  return to_half(float(stdv * z));
+  return to_half(float(mean + stdv * z));
 }
 
 // GGML Q8_0: d = max|x| / 127, q = round(x / d) (round half away from zero).
@@ -190,13 +197,15 @@ void quant_q4_0(const float* x, uint8_t* out) {
 
 void fill_rows(const Tensor& t, uint64_t tkey, double stdv, uint64_t r0, uint64_t r1, uint8_t* dst) {
   const uint64_t in = t.dims[0];
+  if (t.stdv >= 0.0) stdv = t.stdv;
   std::vector<float> row(in);
   const uint64_t rb = t.type == 1 ? in * 2 : (t.type == 8 ? in / 32 * 34 : in / 32 * 18);
   for (uint64_t r = r0; r < r1; ++r) {
     uint8_t* out = dst + (r - r0) * rb;
     if (t.type == 1) {
       uint16_t* o = reinterpret_cast<uint16_t*>(out);
-      for (uint64_t i = 0; i < in; ++i) o[i] = t.fill ? t.fill : weight_half(tkey, r * in + i, stdv);
+      for (uint64_t i = 0; i < in; ++i) o[i] = t.fill ? t.fill : weight_half(tkey, r * in + i, stdv, t.mean);
+      if (t.zero_first && r == 0) o[0] = 0;
       continue;
     }
     for (uint64_t i = 0; i < in; ++i) row[i] = from_half(weight_half(tkey, r * in + i, stdv));
@@ -207,6 +216,67 @@ void fill_rows(const Tensor& t, uint64_t tkey, double stdv, uint64_t r0, uint64_
         quant_q4_0(row.data() + b * 32, out + b * 18);
     }
   }
+}
+
+// Writes the GGUF v3 header (metadata, tensor table) and every tensor's
+// seeded values.  Tensor values depend on (seed, table position, element).
+void emit_gguf(const char* path, const std::vector<Meta>& meta, std::vector<Tensor>& ts, uint64_t seed,
+               double stdv, unsigned threads) {
+  uint64_t off = 0;
+  for (Tensor& t : ts) {
+    t.offset = off;
+    t.bytes = tensor_bytes(t);
+    off = (off + t.bytes + 31) / 32 * 32;
+  }
+  Writer w(path);
+  w.bytes("GGUF", 4);
+  w.put<uint32_t>(3);
+  w.put<uint64_t>(ts.size());
+  w.put<uint64_t>(meta.size());
+  for (const Meta& m : meta) {
+    w.str(m.key);
+    w.put<uint32_t>(m.type);
+    if (m.type == 4) w.put<uint32_t>(m.u);
+    if (m.type == 6) w.put<float>(m.f);
+    if (m.type == 7) w.put<uint8_t>(uint8_t(m.u));
+    if (m.type == 8) w.str(m.s);
+  }
+  for (const Tensor& t : ts) {
+    w.str(t.name);
+    w.put<uint32_t>(uint32_t(t.dims.size()));
+    for (uint64_t dd : t.dims) w.put<uint64_t>(dd);
+    w.put<uint32_t>(t.type);
+    w.put<uint64_t>(t.offset);
+  }
+  w.pad(32);
+  const uint64_t data_start = w.pos();
+  const unsigned nt = threads ? threads : std::max(1u, std::thread::hardware_concurrency());
+  std::vector<uint8_t> buf;
+  const bool progress = getenv("S2SYNTH_PROGRESS") != nullptr;
+  uint64_t reported = 0;
+  for (size_t ti = 0; ti < ts.size(); ++ti) {
+    const Tensor& t = ts[ti];
+    const uint64_t tkey = splitmix64(seed ^ splitmix64(0x5EED0000ull + ti));
+    const uint64_t rows = t.dims.empty() ? 1 : t.elements() / t.dims[0];
+    const uint64_t rb = t.bytes / rows;
+    buf.resize(t.bytes);
+    std::vector<std::thread> pool;
+    const uint64_t per = (rows + nt - 1) / nt;
+    for (unsigned k = 0; k < nt; ++k) {
+      const uint64_t r0 = k * per, r1 = std::min(rows, r0 + per);
+      if (r0 >= r1) break;
+      pool.emplace_back([&, r0, r1] { fill_rows(t, tkey, stdv, r0, r1, buf.data() + r0 * rb); });
+    }
+    for (auto& th : pool) th.join();
+    if (w.pos() != data_start + t.offset) fail("internal offset mismatch for %s", t.name.c_str());
+    w.bytes(buf.data(), buf.size());
+    w.pad(32);
+    if (progress && (w.pos() >> 30) != reported) {
+      reported = w.pos() >> 30;
+      fprintf(stderr, "[s2synth] %s: %.2f GB written\n", path, double(w.pos()) / 1e9);
+    }
+  }
+  w.close();
 }
 
 void write_gguf(const char* path, const s2synth_config& c, unsigned threads) {
@@ -256,12 +326,6 @@ void write_gguf(const char* path, const s2synth_config& c, unsigned threads) {
     add(p + "feed_forward.w2.weight", {c.fast_ffn, d}, lt, 0);
     add(p + "feed_forward.w3.weight", {d, c.fast_ffn}, lt, 0);
   }
-  uint64_t off = 0;
-  for (Tensor& t : ts) {
-    t.offset = off;
-    t.bytes = tensor_bytes(t);
-    off = (off + t.bytes + 31) / 32 * 32;
-  }
   std::vector<Meta> meta;
   auto mu = [&](const char* k, uint32_t v) { meta.push_back(Meta{k, 4, v, 0, ""}); };
   auto mf = [&](const char* k, float v) { meta.push_back(Meta{k, 6, 0, v, ""}); };
@@ -294,57 +358,94 @@ void write_gguf(const char* path, const s2synth_config& c, unsigned threads) {
   mb("fish_speech.scale_codebook_embeddings", true);
   mb("fish_speech.tie_word_embeddings", true);
   mb("fish_speech.fast_project_in", false);
+  emit_gguf(path, meta, ts, c.seed, c.init_std, threads);
+}
 
-  Writer w(path);
-  w.bytes("GGUF", 4);
-  w.put<uint32_t>(3);
-  w.put<uint64_t>(ts.size());
-  w.put<uint64_t>(meta.size());
-  for (const Meta& m : meta) {
-    w.str(m.key);
-    w.put<uint32_t>(m.type);
-    if (m.type == 4) w.put<uint32_t>(m.u);
-    if (m.type == 6) w.put<float>(m.f);
-    if (m.type == 7) w.put<uint8_t>(uint8_t(m.u));
-    if (m.type == 8) w.str(m.s);
+
+
+// Decode side of the codec GGUF (tensor names and ggml dims as the
+// reference's codec registry reads them, crates/fish_s2_infer/src/codec.rs:
+// quantizers :277-296, post_module layers :316-331 and norm :515, upsample
+// stages :431-444, decoder :1299-1317, 1393-1420 and the dims checked at
+// :1643-1681; decoder block conv_transpose kernels are 2 x stride, residual
+// units k7 then k1).  Weights are N(0, 1/sqrt(fan_in)) so activations stay
+// O(1) through the decoder; norms, layer scales and snake alphas are drawn
+// around their working values, and element 0 of every snake alpha is 0 so the
+// reference's near-zero alpha guard is exercised.
+void write_codec_gguf(const char* path, uint64_t seed, unsigned threads) {
+  std::vector<Tensor> ts;
+  auto add = [&](const std::string& n, std::vector<uint64_t> dims, double stdv, double mean = 0.0,
+                 bool zero_first = false) {
+    Tensor t{n, dims, 1, 0};
+    t.stdv = stdv;
+    t.mean = mean;
+    t.zero_first = zero_first;
+    ts.push_back(t);
+  };
+  const uint64_t H = 1024, P = 8;
+  auto quantizer = [&](const std::string& p, uint64_t size) {
+    add(p + ".in_proj.weight", {H, P}, 1.0 / 32.0);
+    add(p + ".in_proj.bias", {P}, 0.02);
+    add(p + ".out_proj.weight", {P, H}, 1.0 / std::sqrt(8.0));
+    add(p + ".out_proj.bias", {H}, 0.02);
+    add(p + ".codebook.weight", {P, size}, 1.0);
+  };
+  quantizer("quantizer.semantic_quantizer.quantizers.0", 4096);
+  for (int i = 0; i < 9; ++i) quantizer("quantizer.quantizer.quantizers." + std::to_string(i), 1024);
+  for (int l = 0; l < 8; ++l) {
+    const std::string p = "quantizer.post_module.layers." + std::to_string(l);
+    add(p + ".attention.wqkv.weight", {H, 3072}, 1.0 / 32.0);
+    add(p + ".attention.wo.weight", {H, H}, 1.0 / 32.0);
+    add(p + ".attention_norm.weight", {H}, 0.1, 1.0);
+    add(p + ".ffn_norm.weight", {H}, 0.1, 1.0);
+    add(p + ".feed_forward.w1.weight", {H, 3072}, 1.0 / 32.0);
+    add(p + ".feed_forward.w2.weight", {3072, H}, 1.0 / std::sqrt(3072.0));
+    add(p + ".feed_forward.w3.weight", {H, 3072}, 1.0 / 32.0);
+    add(p + ".attention_layer_scale.gamma", {H}, 0.05, 0.3);
+    add(p + ".ffn_layer_scale.gamma", {H}, 0.05, 0.3);
   }
-  for (const Tensor& t : ts) {
-    w.str(t.name);
-    w.put<uint32_t>(uint32_t(t.dims.size()));
-    for (uint64_t dd : t.dims) w.put<uint64_t>(dd);
-    w.put<uint32_t>(t.type);
-    w.put<uint64_t>(t.offset);
+  add("quantizer.post_module.norm.weight", {H}, 0.1, 1.0);
+  for (int st = 0; st < 2; ++st) {
+    const std::string p = "quantizer.upsample." + std::to_string(st);
+    add(p + ".0.conv.weight", {2, H, H}, 1.0 / 32.0);
+    add(p + ".0.conv.bias", {H}, 0.02);
+    add(p + ".1.gamma", {H}, 0.05, 0.3);
+    add(p + ".1.dwconv.conv.weight", {7, 1, H}, 1.0 / std::sqrt(7.0));
+    add(p + ".1.dwconv.conv.bias", {H}, 0.02);
+    add(p + ".1.norm.weight", {H}, 0.1, 1.0);
+    add(p + ".1.norm.bias", {H}, 0.1);
+    add(p + ".1.pwconv1.weight", {H, 4096}, 1.0 / 32.0);
+    add(p + ".1.pwconv1.bias", {4096}, 0.02);
+    add(p + ".1.pwconv2.weight", {4096, H}, 1.0 / 64.0);
+    add(p + ".1.pwconv2.bias", {H}, 0.02);
   }
-  w.pad(32);
-  const uint64_t data_start = w.pos();
-  const double stdv = c.init_std;
-  const unsigned nt = threads ? threads : std::max(1u, std::thread::hardware_concurrency());
-  std::vector<uint8_t> buf;
-  const bool progress = getenv("S2SYNTH_PROGRESS") != nullptr;
-  uint64_t reported = 0;
-  for (size_t ti = 0; ti < ts.size(); ++ti) {
-    const Tensor& t = ts[ti];
-    const uint64_t tkey = splitmix64(c.seed ^ splitmix64(0x5EED0000ull + ti));
-    const uint64_t rows = t.dims.size() == 2 ? t.dims[1] : 1;
-    const uint64_t rb = t.bytes / rows;
-    buf.resize(t.bytes);
-    std::vector<std::thread> pool;
-    const uint64_t per = (rows + nt - 1) / nt;
-    for (unsigned k = 0; k < nt; ++k) {
-      const uint64_t r0 = k * per, r1 = std::min(rows, r0 + per);
-      if (r0 >= r1) break;
-      pool.emplace_back([&, r0, r1] { fill_rows(t, tkey, stdv, r0, r1, buf.data() + r0 * rb); });
+  add("decoder.model.0.conv.weight", {7, H, 1536}, 1.0 / std::sqrt(7.0 * 1024.0));
+  add("decoder.model.0.conv.bias", {1536}, 0.02);
+  const uint64_t ch[5] = {1536, 768, 384, 192, 96};
+  const uint64_t rate[4] = {8, 8, 4, 2};
+  for (int b = 0; b < 4; ++b) {
+    const std::string p = "decoder.model." + std::to_string(b + 1) + ".block";
+    const uint64_t ci = ch[b], co = ch[b + 1];
+    add(p + ".0.alpha", {1, ci, 1}, 0.2, 1.0, true);
+    add(p + ".1.conv.weight", {2 * rate[b], co, ci}, 1.0 / std::sqrt(2.0 * double(ci)));
+    add(p + ".1.conv.bias", {co}, 0.02);
+    for (int r = 0; r < 3; ++r) {
+      const std::string q = p + "." + std::to_string(r + 2) + ".block";
+      add(q + ".0.alpha", {1, co, 1}, 0.2, 1.0, true);
+      add(q + ".1.conv.weight", {7, co, co}, 1.0 / std::sqrt(7.0 * double(co)));
+      add(q + ".1.conv.bias", {co}, 0.02);
+      add(q + ".2.alpha", {1, co, 1}, 0.2, 1.0, true);
+      add(q + ".3.conv.weight", {1, co, co}, 0.5 / std::sqrt(double(co)));
+      add(q + ".3.conv.bias", {co}, 0.02);
     }
-    for (auto& th : pool) th.join();
-    if (w.pos() != data_start + t.offset) fail("internal offset mismatch for %s", t.name.c_str());
-    w.bytes(buf.data(), buf.size());
-    w.pad(32);
-    if (progress && (w.pos() >> 30) != reported) {
-      reported = w.pos() >> 30;
-      fprintf(stderr, "[s2synth] %s: %.2f GB written\n", path, double(w.pos()) / 1e9);
-    }
   }
-  w.close();
+  add("decoder.model.5.alpha", {1, 96, 1}, 0.2, 1.0, true);
+  add("decoder.model.6.conv.weight", {7, 96, 1}, 0.08 / std::sqrt(7.0 * 96.0));
+  add("decoder.model.6.conv.bias", {1}, 0.02);
+  std::vector<Meta> meta;
+  meta.push_back(Meta{"general.architecture", 8, 0, 0, "fish-speech-codec"});
+  meta.push_back(Meta{"general.name", 8, 0, 0, "s2hip-synthetic-codec"});
+  emit_gguf(path, meta, ts, seed, 0.02, threads);
 }
 
 }  // namespace
@@ -355,6 +456,16 @@ int32_t s2synth_write_gguf(const char* path, const s2synth_config* cfg, uint32_t
                            size_t err_cap) {
   try {
     write_gguf(path, *cfg, threads);
+    return 1;
+  } catch (const std::exception& e) {
+    if (err && err_cap) snprintf(err, err_cap, "%s", e.what());
+    return 0;
+  }
+}
+
+int32_t s2synth_write_codec_gguf(const char* path, uint64_t seed, uint32_t threads, char* err, size_t err_cap) {
+  try {
+    write_codec_gguf(path, seed, threads);
     return 1;
   } catch (const std::exception& e) {
     if (err && err_cap) snprintf(err, err_cap, "%s", e.what());

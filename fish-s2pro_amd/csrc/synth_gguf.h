@@ -1,4 +1,4 @@
-/* synth_gguf.h -- seeded synthetic dual-AR GGUF writer (host-only helper). */
+/* synth_gguf.h -- seeded synthetic dual-AR and codec GGUF writers (host-only helper). */
 #ifndef S2SYNTH_GGUF_H
 #define S2SYNTH_GGUF_H
 
@@ -24,6 +24,9 @@ typedef struct {
 /* Returns 1 on success, 0 on failure with a message in err. */
 int32_t s2synth_write_gguf(const char* path, const s2synth_config* cfg, uint32_t threads, char* err,
                            size_t err_cap);
+/* Decode-side tensors of a synthetic RVQ codec GGUF (quantizers, post_module,
+   upsample, decoder), seeded; every tensor F16. */
+int32_t s2synth_write_codec_gguf(const char* path, uint64_t seed, uint32_t threads, char* err, size_t err_cap);
 uint16_t s2synth_f32_to_f16(float v);
 /* Quantise one 32-element block into Q8_0 (34 B) or Q4_0 (18 B). */
 int32_t s2synth_quantize_block(uint32_t type, const float* x, uint8_t* out);

@@ -134,6 +134,10 @@ def _load():
             ctypes.c_char_p, ctypes.c_size_t,
         ]
         lib.s2synth_write_gguf.restype = ctypes.c_int32
+        lib.s2synth_write_codec_gguf.argtypes = [
+            ctypes.c_char_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_char_p, ctypes.c_size_t,
+        ]
+        lib.s2synth_write_codec_gguf.restype = ctypes.c_int32
         lib.s2synth_f32_to_f16.argtypes = [ctypes.c_float]
         lib.s2synth_f32_to_f16.restype = ctypes.c_uint16
         lib.s2synth_quantize_block.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
@@ -162,6 +166,34 @@ def ensure_gguf(shape: ModelShape, directory: str, threads: int = 0) -> str:
     path = os.path.join(directory, shape.file_name())
     if not os.path.exists(path):
         write_gguf(shape, path, threads)
+    return path
+
+
+CODEC_SEED = 3
+
+
+def codec_file_name(seed: int = CODEC_SEED) -> str:
+    return f"s2synth-codec-f16-seed{seed}.gguf"
+
+
+def write_codec_gguf(path: str, seed: int = CODEC_SEED, threads: int = 0) -> str:
+    """Write the decode-side tensors of a seeded synthetic RVQ codec GGUF
+    (architecture ``fish-speech-codec``; quantizers, post_module, upsample and
+    decoder, all F16, about 370 MB) at ``path`` and return the path."""
+    err = ctypes.create_string_buffer(512)
+    tmp = path + ".tmp"
+    if not _load().s2synth_write_codec_gguf(tmp.encode(), seed, threads, err, len(err)):
+        raise RuntimeError(err.value.decode())
+    os.replace(tmp, path)
+    return path
+
+
+def ensure_codec_gguf(directory: str, seed: int = CODEC_SEED, threads: int = 0) -> str:
+    """Return a cached synthetic codec GGUF under ``directory``, writing it once."""
+    os.makedirs(directory, exist_ok=True)
+    path = os.path.join(directory, codec_file_name(seed))
+    if not os.path.exists(path):
+        write_codec_gguf(path, seed, threads)
     return path
 
 

@@ -94,6 +94,31 @@ def lib():
                                      ctypes.c_int32, ctypes.c_uint32, _u64p, vp, _u32p,
                                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                      ctypes.c_char_p, sz]
+    cp, u32 = ctypes.c_char_p, ctypes.c_uint32
+    L.orc_codec_open.argtypes = [cp, u32, cp, sz]
+    L.orc_codec_open.restype = vp
+    L.orc_codec_close.argtypes = [vp]
+    L.orc_codec_close.restype = None
+    L.orc_codec_rvq_lookup.argtypes = [vp, vp, u32, u32, vp, cp, sz]
+    L.orc_codec_post_module.argtypes = [vp, vp, u32, vp, cp, sz]
+    L.orc_codec_upsample.argtypes = [vp, vp, u32, vp, cp, sz]
+    L.orc_codec_decoder.argtypes = [vp, vp, u32, u32, u32, vp, cp, sz]
+    L.orc_codec_decode_waveform.argtypes = [vp, vp, u32, u32, vp, cp, sz]
+    L.orc_codec_snake.argtypes = [vp, sz, sz, vp, vp]
+    L.orc_codec_snake.restype = None
+    L.orc_codec_conv1d.argtypes = [vp, sz, sz, sz, sz, vp, sz, vp, vp, cp, sz]
+    L.orc_codec_conv_transpose.argtypes = [vp, sz, sz, sz, sz, vp, sz, vp, vp, cp, sz]
+    L.orc_codec_depthwise.argtypes = [vp, sz, sz, sz, vp, vp, vp]
+    L.orc_codec_depthwise.restype = None
+    L.orc_codec_layer_norm.argtypes = [vp, sz, sz, vp, vp, ctypes.c_float]
+    L.orc_codec_layer_norm.restype = None
+    L.orc_codec_erf.argtypes = [ctypes.c_float]
+    L.orc_codec_erf.restype = ctypes.c_float
+    L.orc_codec_gelu.argtypes = [ctypes.c_float]
+    L.orc_codec_gelu.restype = ctypes.c_float
+    for name in ("orc_codec_rvq_lookup", "orc_codec_post_module", "orc_codec_upsample", "orc_codec_decoder",
+                 "orc_codec_decode_waveform", "orc_codec_conv1d", "orc_codec_conv_transpose"):
+        getattr(L, name).restype = ctypes.c_int32
     for name in ("orc_dequant_row", "orc_rms_norm", "orc_rms_norm_heads", "orc_linear",
                  "orc_rope_normal", "orc_gqa_attention", "orc_sample_token", "orc_sample_token_margins",
                  "orc_transpose_to_time_major", "orc_get_spec", "orc_eval", "orc_fast_logits", "orc_embed",
@@ -333,3 +358,136 @@ class OracleModel:
             "prefill_seconds": tp.value,
             "decode_seconds": td.value,
         }
+
+
+# ---------------------------------------------------------------------------
+# RVQ codec decode (crates/fish_s2_infer/src/codec.rs:1690-1714)
+# ---------------------------------------------------------------------------
+CODEC_HIDDEN = 1024
+CODEC_SAMPLES_PER_LATENT = 512  # decoder rates 8 * 8 * 4 * 2
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def _check(ok, err):
+    if not ok:
+        raise RuntimeError(err.value.decode())
+
+
+def codec_snake(x, alpha):
+    x, alpha = _f32(x), _f32(alpha)
+    out = np.empty_like(x)
+    lib().orc_codec_snake(_p(x), x.shape[0], x.shape[1], _p(alpha), _p(out))
+    return out
+
+
+def codec_conv1d(x, weight, bias, dilation=1):
+    """x [frames][in]; weight in ggml order [out][in][k] (numpy shape (out, in, k))."""
+    x, w, b = _f32(x), _f32(weight), _f32(bias)
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    err = ctypes.create_string_buffer(512)
+    _check(lib().orc_codec_conv1d(_p(x), x.shape[0], x.shape[1], w.shape[0], dilation, _p(w), w.size, _p(b),
+                                  _p(out), err, len(err)), err)
+    return out
+
+
+def codec_conv_transpose(x, weight, bias, stride):
+    """x [frames][in]; weight in ggml order [in][out][k] (numpy shape (in, out, k))."""
+    x, w, b = _f32(x), _f32(weight), _f32(bias)
+    out = np.empty((x.shape[0] * stride, w.shape[1]), np.float32)
+    err = ctypes.create_string_buffer(512)
+    _check(lib().orc_codec_conv_transpose(_p(x), x.shape[0], x.shape[1], w.shape[1], stride, _p(w), w.size,
+                                          _p(b), _p(out), err, len(err)), err)
+    return out
+
+
+def codec_depthwise(x, weight, bias):
+    """x [frames][ch]; weight numpy shape (ch, k)."""
+    x, w, b = _f32(x), _f32(weight), _f32(bias)
+    out = np.empty_like(x)
+    lib().orc_codec_depthwise(_p(x), x.shape[0], x.shape[1], w.shape[1], _p(w), _p(b), _p(out))
+    return out
+
+
+def codec_layer_norm(x, weight, bias, eps):
+    x = _f32(x).copy()
+    w, b = _f32(weight), _f32(bias)
+    lib().orc_codec_layer_norm(_p(x), x.shape[0], x.shape[1], _p(w), _p(b), eps)
+    return x
+
+
+def codec_erf(v):
+    return float(lib().orc_codec_erf(v))
+
+
+def codec_gelu(v):
+    return float(lib().orc_codec_gelu(v))
+
+
+class OracleCodec:
+    """CPU decode_waveform and its stages over a codec GGUF."""
+
+    def __init__(self, gguf_path: str, threads: int = 0):
+        err = ctypes.create_string_buffer(1024)
+        self._h = lib().orc_codec_open(gguf_path.encode(), threads, err, len(err))
+        if not self._h:
+            raise RuntimeError(err.value.decode())
+
+    def close(self):
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.orc_codec_close(self._h)
+        self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def rvq_lookup(self, codes, num_codebooks, n_frames):
+        c = np.ascontiguousarray(codes, np.int32).ravel()
+        out = np.empty((n_frames, CODEC_HIDDEN), np.float32)
+        err = ctypes.create_string_buffer(512)
+        _check(lib().orc_codec_rvq_lookup(self._h, _p(c), num_codebooks, n_frames, _p(out), err, len(err)), err)
+        return out
+
+    def post_module(self, latents):
+        x = _f32(latents)
+        out = np.empty_like(x)
+        err = ctypes.create_string_buffer(512)
+        _check(lib().orc_codec_post_module(self._h, _p(x), x.shape[0], _p(out), err, len(err)), err)
+        return out
+
+    def upsample(self, hidden):
+        x = _f32(hidden)
+        out = np.empty((4 * x.shape[0], CODEC_HIDDEN), np.float32)
+        err = ctypes.create_string_buffer(512)
+        _check(lib().orc_codec_upsample(self._h, _p(x), x.shape[0], _p(out), err, len(err)), err)
+        return out
+
+    def decoder(self, hidden, stop_block=5):
+        """Samples (stop_block 5), or the residual stream after stop_block
+        (0..4) decoder blocks."""
+        x = _f32(hidden)
+        rates, ch = (8, 8, 4, 2), (1536, 768, 384, 192, 96)
+        if stop_block >= 5:
+            out = np.empty(x.shape[0] * CODEC_SAMPLES_PER_LATENT, np.float32)
+        else:
+            out = np.empty((x.shape[0] * int(np.prod(rates[:stop_block])), ch[stop_block]), np.float32)
+        err = ctypes.create_string_buffer(512)
+        _check(lib().orc_codec_decoder(self._h, _p(x), x.shape[0], x.shape[1], stop_block, _p(out), err,
+                                       len(err)), err)
+        return out
+
+    def decode_waveform(self, codes, num_codebooks, n_frames):
+        c = np.ascontiguousarray(codes, np.int32).ravel()
+        out = np.empty(n_frames * 4 * CODEC_SAMPLES_PER_LATENT, np.float32)
+        err = ctypes.create_string_buffer(512)
+        _check(lib().orc_codec_decode_waveform(self._h, _p(c), num_codebooks, n_frames, _p(out), err, len(err)),
+               err)
+        return out

@@ -1443,3 +1443,537 @@ int32_t orc_generate_codes(orc_model* m, const int32_t* prompt, size_t cols, uin
 }
 
 }  // extern "C"
+
+// ===========================================================================
+// RVQ codec decode (crates/fish_s2_infer/src/codec.rs): decode_waveform
+// (:1690-1714) = rvq_lookup_codes (:2536-2596) -> forward_codec_post_module
+// (:986-1018) -> forward_codec_upsample (:2302-2325) -> forward_codec_decoder
+// (:1941-2001).  Every F16 tensor is read as f32 values (F16TensorView,
+// tensor.rs:8-60).  Each output element is summed in the reference's order;
+// loops run several independent outputs side by side (vectorised across
+// output channels) and threads split output frames, which changes no sum.
+// ===========================================================================
+namespace {
+
+constexpr size_t CX_HIDDEN = 1024, CX_PROJ = 8, CX_SEM_CB = 4096, CX_RES_CB = 1024, CX_RES_Q = 9;
+constexpr size_t CX_LAYERS = 8, CX_QKV = 3072, CX_FFN = 3072, CX_HEADS = 16, CX_HD = 64, CX_WINDOW = 128;
+constexpr size_t CX_EXPANDED = 4096, CX_DW_K = 7, CX_ENTRY = 1536;
+constexpr float CX_RMS_EPS = 1e-5f, CX_LN_EPS = 1e-6f, CX_ROPE_BASE = 10000.0f;
+constexpr size_t CX_RATES[4] = {8, 8, 4, 2};
+constexpr size_t CX_CH[5] = {1536, 768, 384, 192, 96};
+
+float round_to_f16(float v) { return f16_to_f32(f32_to_f16(v)); }
+
+// snake_activation_frame_major (codec.rs:2162-2186)
+void cx_snake(const float* in, size_t frames, size_t ch, const float* alpha, float* out) {
+  for (size_t f = 0; f < frames; ++f) {
+    for (size_t c = 0; c < ch; ++c) {
+      const float a = std::fabs(alpha[c]) < 1e-8f ? 1e-8f : alpha[c];
+      const float x = in[f * ch + c];
+      const float s = sinf(a * x);
+      out[f * ch + c] = x + (s * s) / a;
+    }
+  }
+}
+
+// causal_conv_1d_frame_major with stride 1 (codec.rs:2212-2293): the input is
+// rounded to f16, left-padded by (k - 1) * dilation zero frames (the extra
+// right padding of extra_padding_for_conv1d, :2188-2201, is 0 at stride 1),
+// and out[t][o] = bias[o] + sum over tap, then input channel, of
+// x16[t + tap*d - (k-1)*d][i] * W[o][i][tap] (ggml index tap + k*i + k*in*o).
+// Padding frames contribute +-0 products, which leave a non-zero sum unchanged.
+void cx_conv1d(Pool& pool, const float* in, size_t frames, size_t in_ch, size_t out_ch, size_t dilation,
+               const float* w, size_t w_len, const float* bias, float* out) {
+  if (in_ch == 0 || out_ch == 0) fail("causal conv channel count is zero");
+  const size_t k = w_len / (in_ch * out_ch);
+  if (k == 0 || k * in_ch * out_ch != w_len)
+    fail("causal conv weight length mismatch: expected %zu, got %zu", k * in_ch * out_ch, w_len);
+  std::vector<float> x16(frames * in_ch);
+  for (size_t i = 0; i < x16.size(); ++i) x16[i] = round_to_f16(in[i]);
+  std::vector<float> wt(k * in_ch * out_ch);  // [tap][i][o]
+  for (size_t o = 0; o < out_ch; ++o)
+    for (size_t i = 0; i < in_ch; ++i)
+      for (size_t t = 0; t < k; ++t) wt[(t * in_ch + i) * out_ch + o] = w[t + k * i + k * in_ch * o];
+  const size_t span = (k - 1) * dilation;
+  pool.run(frames, 16, [&](size_t f0, size_t f1) {
+    std::vector<float> acc(out_ch);
+    for (size_t f = f0; f < f1; ++f) {
+      for (size_t o = 0; o < out_ch; ++o) acc[o] = bias[o];
+      for (size_t t = 0; t < k; ++t) {
+        const size_t p = f + t * dilation;  // padded frame
+        if (p < span) continue;
+        const float* xr = x16.data() + (p - span) * in_ch;
+        const float* wr = wt.data() + t * in_ch * out_ch;
+        for (size_t i = 0; i < in_ch; ++i) {
+          const float xv = xr[i];
+          const float* wi = wr + i * out_ch;
+          for (size_t o = 0; o < out_ch; ++o) acc[o] += xv * wi[o];
+        }
+      }
+      std::copy(acc.begin(), acc.end(), out + f * out_ch);
+    }
+  });
+}
+
+// causal_conv_transpose_1d with crop_right 0 (codec.rs:3505-3574): output
+// frames = frames * stride; out[r][o] accumulates, from 0, over input frames f
+// in ascending order with tap kk = r - f*stride in [0, k), then input channel,
+// x[f][i] * W[i][o][kk] (ggml index kk + k*o + k*out*i); bias is added last.
+// Taps that land past the last output frame are dropped.  No f16 rounding.
+void cx_conv_transpose(Pool& pool, const float* in, size_t frames, size_t in_ch, size_t out_ch, size_t stride,
+                       const float* w, size_t w_len, const float* bias, float* out) {
+  if (in_ch == 0 || out_ch == 0 || stride == 0) fail("conv_transpose dims are zero");
+  const size_t k = w_len / (in_ch * out_ch);
+  if (k == 0 || k * in_ch * out_ch != w_len)
+    fail("conv_transpose weight length mismatch: expected %zu, got %zu", k * in_ch * out_ch, w_len);
+  std::vector<float> wt(k * in_ch * out_ch);  // [tap][i][o]
+  for (size_t i = 0; i < in_ch; ++i)
+    for (size_t o = 0; o < out_ch; ++o)
+      for (size_t t = 0; t < k; ++t) wt[(t * in_ch + i) * out_ch + o] = w[t + k * o + k * out_ch * i];
+  const size_t out_frames = frames * stride;
+  pool.run(out_frames, 16, [&](size_t r0, size_t r1) {
+    std::vector<float> acc(out_ch);
+    for (size_t r = r0; r < r1; ++r) {
+      std::fill(acc.begin(), acc.end(), 0.0f);
+      const size_t f_lo = r + 1 > k ? (r + 1 - k + stride - 1) / stride : 0;
+      for (size_t f = f_lo; f * stride <= r && f < frames; ++f) {
+        const size_t kk = r - f * stride;
+        const float* xr = in + f * in_ch;
+        const float* wr = wt.data() + kk * in_ch * out_ch;
+        for (size_t i = 0; i < in_ch; ++i) {
+          const float xv = xr[i];
+          const float* wi = wr + i * out_ch;
+          for (size_t o = 0; o < out_ch; ++o) acc[o] += xv * wi[o];
+        }
+      }
+      for (size_t o = 0; o < out_ch; ++o) out[r * out_ch + o] = acc[o] + bias[o];
+    }
+  });
+}
+
+// depthwise_causal_conv1d (codec.rs:3576-3619): left padding k - 1,
+// out[t][c] = bias[c] + sum_kk x[t + kk - (k-1)][c] * W[c][kk] (index kk + k*c).
+void cx_depthwise(const float* in, size_t frames, size_t ch, size_t k, const float* w, const float* bias,
+                  float* out) {
+  for (size_t f = 0; f < frames; ++f) {
+    for (size_t c = 0; c < ch; ++c) {
+      float sum = bias[c];
+      for (size_t kk = 0; kk < k; ++kk) {
+        if (f + kk < k - 1) continue;
+        const size_t src = f + kk - (k - 1);
+        if (src < frames) sum += in[src * ch + c] * w[kk + k * c];
+      }
+      out[f * ch + c] = sum;
+    }
+  }
+}
+
+// layer_norm_affine_frame_major (codec.rs:3621-3654)
+void cx_layer_norm(float* x, size_t frames, size_t ch, const float* w, const float* b, float eps) {
+  for (size_t f = 0; f < frames; ++f) {
+    float* row = x + f * ch;
+    float s = 0.0f;
+    for (size_t c = 0; c < ch; ++c) s += row[c];
+    const float mean = s / float(ch);
+    float v = 0.0f;
+    for (size_t c = 0; c < ch; ++c) {
+      const float d = row[c] - mean;
+      v += d * d;
+    }
+    const float var = v / float(ch);
+    const float scale = 1.0f / std::sqrt(var + eps);
+    for (size_t c = 0; c < ch; ++c) row[c] = (row[c] - mean) * scale * w[c] + b[c];
+  }
+}
+
+// erf_approx (codec.rs:3890-3899): Abramowitz-Stegun 7.1.26 with f32 constants.
+float cx_erf(float value) {
+  const float sign = value < 0.0f ? -1.0f : 1.0f;
+  const float x = std::fabs(value);
+  const float t = 1.0f / (1.0f + 0.3275911f * x);
+  const float poly = (((((1.0614054f * t - 1.4531521f) * t) + 1.4214138f) * t - 0.28449672f) * t + 0.2548296f) * t;
+  return sign * (1.0f - poly * expf(-x * x));
+}
+
+// gelu_erf (codec.rs:3886-3888)
+float cx_gelu(float v) { return 0.5f * v * (1.0f + cx_erf(v * 0.70710677f)); }
+
+// silu (codec.rs:3882-3884)
+float cx_silu(float v) { return v / (1.0f + expf(-v)); }
+
+struct CxLayer {
+  std::vector<float> attn_norm, ffn_norm, als, fls;
+  const uint8_t *wqkv, *wo, *w1, *w2, *w3;  // raw F16 rows [out][in]
+};
+struct CxStage {
+  std::vector<float> ct_w, ct_b, gamma, dw_w, dw_b, ln_w, ln_b, pw1_b, pw2_b;
+  const uint8_t *pw1, *pw2;
+};
+struct CxRes {
+  std::vector<float> a0, w0, b0, a1, w1, b1;
+};
+struct CxBlock {
+  std::vector<float> alpha, ct_w, ct_b;
+  CxRes res[3];
+};
+
+}  // namespace
+
+struct orc_codec {
+  Gguf g;
+  Pool pool;
+  std::vector<float> cb[10], proj_w[10], proj_b[10];
+  CxLayer layers[CX_LAYERS];
+  std::vector<float> post_norm;
+  CxStage stages[2];
+  std::vector<float> entry_w, entry_b, tail_alpha, out_w, out_b;
+  CxBlock blocks[4];
+  explicit orc_codec(unsigned threads) : pool(threads) {}
+};
+
+namespace {
+
+// F16TensorView::from_gguf (tensor.rs:21-45) plus validate_f16_dims (codec.rs:3751-3759)
+std::vector<float> cx_tensor(const Gguf& g, const std::string& name, std::vector<uint64_t> dims) {
+  const TensorInfo& t = g.tensor(name);
+  if (t.type != T_F16) fail("expected F16 tensor %s, got type %u", name.c_str(), t.type);
+  if (t.dims != dims) fail("codec tensor %s has unexpected dimensions", name.c_str());
+  std::vector<float> v(t.elements());
+  const uint16_t* p = reinterpret_cast<const uint16_t*>(t.data);
+  for (size_t i = 0; i < v.size(); ++i) v[i] = f16_to_f32(p[i]);
+  return v;
+}
+const uint8_t* cx_raw(const Gguf& g, const std::string& name, std::vector<uint64_t> dims) {
+  const TensorInfo& t = g.tensor(name);
+  if (t.type != T_F16) fail("expected F16 tensor %s, got type %u", name.c_str(), t.type);
+  if (t.dims != dims) fail("codec tensor %s has unexpected dimensions", name.c_str());
+  return t.data;
+}
+
+void cx_load(orc_codec* c) {
+  const Gguf& g = c->g;
+  auto it = g.meta.find("general.architecture");
+  if (it == g.meta.end()) fail("missing general.architecture");
+  if (it->second.s != "fish-speech-codec") fail("expected fish-speech-codec codec GGUF, got %s", it->second.s.c_str());
+  for (size_t q = 0; q < 10; ++q) {
+    const std::string p = q == 0 ? "quantizer.semantic_quantizer.quantizers.0"
+                                 : "quantizer.quantizer.quantizers." + std::to_string(q - 1);
+    c->cb[q] = cx_tensor(g, p + ".codebook.weight", {CX_PROJ, q == 0 ? CX_SEM_CB : CX_RES_CB});
+    c->proj_w[q] = cx_tensor(g, p + ".out_proj.weight", {CX_PROJ, CX_HIDDEN});
+    c->proj_b[q] = cx_tensor(g, p + ".out_proj.bias", {CX_HIDDEN});
+  }
+  for (size_t l = 0; l < CX_LAYERS; ++l) {
+    const std::string p = "quantizer.post_module.layers." + std::to_string(l);
+    CxLayer& L = c->layers[l];
+    L.attn_norm = cx_tensor(g, p + ".attention_norm.weight", {CX_HIDDEN});
+    L.ffn_norm = cx_tensor(g, p + ".ffn_norm.weight", {CX_HIDDEN});
+    L.als = cx_tensor(g, p + ".attention_layer_scale.gamma", {CX_HIDDEN});
+    L.fls = cx_tensor(g, p + ".ffn_layer_scale.gamma", {CX_HIDDEN});
+    L.wqkv = cx_raw(g, p + ".attention.wqkv.weight", {CX_HIDDEN, CX_QKV});
+    L.wo = cx_raw(g, p + ".attention.wo.weight", {CX_HIDDEN, CX_HIDDEN});
+    L.w1 = cx_raw(g, p + ".feed_forward.w1.weight", {CX_HIDDEN, CX_FFN});
+    L.w2 = cx_raw(g, p + ".feed_forward.w2.weight", {CX_FFN, CX_HIDDEN});
+    L.w3 = cx_raw(g, p + ".feed_forward.w3.weight", {CX_HIDDEN, CX_FFN});
+  }
+  c->post_norm = cx_tensor(g, "quantizer.post_module.norm.weight", {CX_HIDDEN});
+  for (size_t s = 0; s < 2; ++s) {
+    const std::string p = "quantizer.upsample." + std::to_string(s);
+    CxStage& S = c->stages[s];
+    S.ct_w = cx_tensor(g, p + ".0.conv.weight", {2, CX_HIDDEN, CX_HIDDEN});
+    S.ct_b = cx_tensor(g, p + ".0.conv.bias", {CX_HIDDEN});
+    S.gamma = cx_tensor(g, p + ".1.gamma", {CX_HIDDEN});
+    S.dw_w = cx_tensor(g, p + ".1.dwconv.conv.weight", {CX_DW_K, 1, CX_HIDDEN});
+    S.dw_b = cx_tensor(g, p + ".1.dwconv.conv.bias", {CX_HIDDEN});
+    S.ln_w = cx_tensor(g, p + ".1.norm.weight", {CX_HIDDEN});
+    S.ln_b = cx_tensor(g, p + ".1.norm.bias", {CX_HIDDEN});
+    S.pw1 = cx_raw(g, p + ".1.pwconv1.weight", {CX_HIDDEN, CX_EXPANDED});
+    S.pw1_b = cx_tensor(g, p + ".1.pwconv1.bias", {CX_EXPANDED});
+    S.pw2 = cx_raw(g, p + ".1.pwconv2.weight", {CX_EXPANDED, CX_HIDDEN});
+    S.pw2_b = cx_tensor(g, p + ".1.pwconv2.bias", {CX_HIDDEN});
+  }
+  c->entry_w = cx_tensor(g, "decoder.model.0.conv.weight", {7, CX_HIDDEN, CX_ENTRY});
+  c->entry_b = cx_tensor(g, "decoder.model.0.conv.bias", {CX_ENTRY});
+  for (size_t b = 0; b < 4; ++b) {
+    const std::string p = "decoder.model." + std::to_string(b + 1) + ".block";
+    const uint64_t ci = CX_CH[b], co = CX_CH[b + 1];
+    CxBlock& B = c->blocks[b];
+    B.alpha = cx_tensor(g, p + ".0.alpha", {1, ci, 1});
+    B.ct_w = cx_tensor(g, p + ".1.conv.weight", {2 * CX_RATES[b], co, ci});
+    B.ct_b = cx_tensor(g, p + ".1.conv.bias", {co});
+    for (size_t r = 0; r < 3; ++r) {
+      const std::string q = p + "." + std::to_string(r + 2) + ".block";
+      CxRes& R = B.res[r];
+      R.a0 = cx_tensor(g, q + ".0.alpha", {1, co, 1});
+      R.w0 = cx_tensor(g, q + ".1.conv.weight", {7, co, co});
+      R.b0 = cx_tensor(g, q + ".1.conv.bias", {co});
+      R.a1 = cx_tensor(g, q + ".2.alpha", {1, co, 1});
+      R.w1 = cx_tensor(g, q + ".3.conv.weight", {1, co, co});
+      R.b1 = cx_tensor(g, q + ".3.conv.bias", {co});
+    }
+  }
+  c->tail_alpha = cx_tensor(g, "decoder.model.5.alpha", {1, 96, 1});
+  c->out_w = cx_tensor(g, "decoder.model.6.conv.weight", {7, 96, 1});
+  c->out_b = cx_tensor(g, "decoder.model.6.conv.bias", {1});
+}
+
+// rvq_lookup_codes (codec.rs:2536-2596) with project_code (:2428-2445) and
+// embedding_lookup_rows (tensor.rs:160-193): latents start at 0 and add each
+// codebook's projection (codebook row . out_proj row + bias) in codebook order.
+void cx_rvq_lookup(orc_codec* c, const int32_t* codes, uint32_t ncb, uint32_t n_frames, float* latents) {
+  if (ncb != 10) fail("codec codebook count mismatch: expected 10, got %u", ncb);
+  const size_t F = n_frames;
+  std::fill(latents, latents + F * CX_HIDDEN, 0.0f);
+  std::vector<float> proj(CX_HIDDEN);
+  for (size_t f = 0; f < F; ++f) {
+    for (size_t q = 0; q < ncb; ++q) {
+      const int32_t code = codes[q * F + f];
+      if (code < 0) fail("codec code must be non-negative, got %d", code);
+      const size_t size = q == 0 ? CX_SEM_CB : CX_RES_CB;
+      if (size_t(code) >= size) fail("embedding index %d out of range for vocab_dim %zu", code, size);
+      const float* z = c->cb[q].data() + size_t(code) * CX_PROJ;
+      for (size_t o = 0; o < CX_HIDDEN; ++o)
+        proj[o] = dot(z, c->proj_w[q].data() + o * CX_PROJ, CX_PROJ) + c->proj_b[q][o];
+      float* row = latents + f * CX_HIDDEN;
+      for (size_t o = 0; o < CX_HIDDEN; ++o) row[o] += proj[o];
+    }
+  }
+}
+
+// forward_codec_post_module (codec.rs:986-1018) over
+// forward_codec_transformer_layer_with_window (:3229-3336): window 128,
+// 16 heads of 64 (no GQA sharing), RoPE base 1e4 at the frame position,
+// attention scale 1/sqrt(64), layer scales on both residual branches.
+void cx_post_module(orc_codec* c, const float* latents, uint32_t n_frames, float* hidden) {
+  if (n_frames == 0) fail("codec transformer requires at least one frame");
+  const size_t T = n_frames, D = CX_HIDDEN;
+  std::vector<float> x(latents, latents + T * D), nrm(T * D), qkv(T * CX_QKV), att(T * D), proj(T * D);
+  std::vector<float> g(T * CX_FFN), u(T * CX_FFN), act(T * CX_FFN);
+  std::vector<float> keys, vals;
+  for (size_t l = 0; l < CX_LAYERS; ++l) {
+    const CxLayer& L = c->layers[l];
+    for (size_t t = 0; t < T; ++t) rms_norm(&x[t * D], L.attn_norm.data(), D, CX_RMS_EPS, &nrm[t * D]);
+    linear_multi(c->pool, nrm.data(), T, L.wqkv, T_F16, D, CX_QKV, qkv.data());
+    for (size_t t = 0; t < T; ++t) {
+      rope_normal(&qkv[t * CX_QKV], D, CX_HD, t, CX_ROPE_BASE);
+      rope_normal(&qkv[t * CX_QKV + D], D, CX_HD, t, CX_ROPE_BASE);
+    }
+    c->pool.run(T, 4, [&](size_t t0, size_t t1) {
+      std::vector<float> k, v;
+      for (size_t t = t0; t < t1; ++t) {
+        const size_t start = t + 1 > CX_WINDOW ? t + 1 - CX_WINDOW : 0, n = t + 1 - start;
+        k.resize(n * D);
+        v.resize(n * D);
+        for (size_t j = 0; j < n; ++j) {
+          std::copy_n(&qkv[(start + j) * CX_QKV + D], D, &k[j * D]);
+          std::copy_n(&qkv[(start + j) * CX_QKV + 2 * D], D, &v[j * D]);
+        }
+        gqa_attention(&qkv[t * CX_QKV], k.data(), v.data(), CX_HEADS, CX_HEADS, CX_HD, n, 1.0f / std::sqrt(64.0f),
+                      &att[t * D]);
+      }
+    });
+    linear_multi(c->pool, att.data(), T, L.wo, T_F16, D, D, proj.data());
+    for (size_t t = 0; t < T; ++t)
+      for (size_t i = 0; i < D; ++i) x[t * D + i] = x[t * D + i] + proj[t * D + i] * L.als[i];
+    for (size_t t = 0; t < T; ++t) rms_norm(&x[t * D], L.ffn_norm.data(), D, CX_RMS_EPS, &nrm[t * D]);
+    linear_multi(c->pool, nrm.data(), T, L.w1, T_F16, D, CX_FFN, g.data());
+    linear_multi(c->pool, nrm.data(), T, L.w3, T_F16, D, CX_FFN, u.data());
+    for (size_t i = 0; i < T * CX_FFN; ++i) act[i] = cx_silu(g[i]) * u[i];
+    linear_multi(c->pool, act.data(), T, L.w2, T_F16, CX_FFN, D, proj.data());
+    for (size_t t = 0; t < T; ++t)
+      for (size_t i = 0; i < D; ++i) x[t * D + i] = x[t * D + i] + proj[t * D + i] * L.fls[i];
+  }
+  for (size_t t = 0; t < T; ++t) rms_norm(&x[t * D], c->post_norm.data(), D, CX_RMS_EPS, hidden + t * D);
+}
+
+// forward_codec_upsample (codec.rs:2302-2325): two stages of
+// forward_codec_upsample_stage (:3338-3358) = conv_transpose (stride 2,
+// kernel 2) then forward_codec_convnext_block (:3438-3483).
+void cx_upsample(orc_codec* c, const float* hidden, uint32_t n_frames, float* out) {
+  size_t F = n_frames;
+  const size_t D = CX_HIDDEN;
+  std::vector<float> cur(hidden, hidden + F * D);
+  for (size_t s = 0; s < 2; ++s) {
+    const CxStage& S = c->stages[s];
+    std::vector<float> conv(2 * F * D);
+    cx_conv_transpose(c->pool, cur.data(), F, D, D, 2, S.ct_w.data(), S.ct_w.size(), S.ct_b.data(), conv.data());
+    F *= 2;
+    std::vector<float> x(F * D), h(F * CX_EXPANDED), y(F * D);
+    cx_depthwise(conv.data(), F, D, CX_DW_K, S.dw_w.data(), S.dw_b.data(), x.data());
+    cx_layer_norm(x.data(), F, D, S.ln_w.data(), S.ln_b.data(), CX_LN_EPS);
+    // linear_bias_frame_major (:3656-3679): linear, then + bias
+    linear_multi(c->pool, x.data(), F, S.pw1, T_F16, D, CX_EXPANDED, h.data());
+    for (size_t f = 0; f < F; ++f)
+      for (size_t i = 0; i < CX_EXPANDED; ++i) h[f * CX_EXPANDED + i] = cx_gelu(h[f * CX_EXPANDED + i] + S.pw1_b[i]);
+    linear_multi(c->pool, h.data(), F, S.pw2, T_F16, CX_EXPANDED, D, y.data());
+    cur.resize(F * D);
+    for (size_t f = 0; f < F; ++f)
+      for (size_t i = 0; i < D; ++i) {
+        const float v = (y[f * D + i] + S.pw2_b[i]) * S.gamma[i];
+        cur[f * D + i] = conv[f * D + i] + v;
+      }
+  }
+  std::copy(cur.begin(), cur.end(), out);
+}
+
+// forward_codec_decoder (codec.rs:1941-2001) with forward_codec_decoder_block
+// (:2015-2044) and forward_codec_residual_unit_impl (:2085-2160).
+// stop_block <= 4 returns the residual stream after that many blocks
+// (frames * prod(rates[0..stop_block]) x channels), a stage checkpoint;
+// 5 and above run the whole decoder.
+void cx_decoder(orc_codec* c, const float* hidden, uint32_t n_frames, uint32_t hidden_dim, float* out,
+                uint32_t stop_block = 5) {
+  if (hidden_dim != CX_HIDDEN) fail("decoder expects latent dim %zu, got %u", CX_HIDDEN, hidden_dim);
+  size_t F = n_frames;
+  std::vector<float> x(F * CX_ENTRY);
+  cx_conv1d(c->pool, hidden, F, CX_HIDDEN, CX_ENTRY, 1, c->entry_w.data(), c->entry_w.size(), c->entry_b.data(),
+            x.data());
+  size_t ch = CX_ENTRY;
+  for (size_t b = 0; b < 4 && b < stop_block; ++b) {
+    const CxBlock& B = c->blocks[b];
+    const size_t co = CX_CH[b + 1], s = CX_RATES[b];
+    std::vector<float> sn(F * ch);
+    cx_snake(x.data(), F, ch, B.alpha.data(), sn.data());
+    std::vector<float> y(F * s * co);
+    cx_conv_transpose(c->pool, sn.data(), F, ch, co, s, B.ct_w.data(), B.ct_w.size(), B.ct_b.data(), y.data());
+    F *= s;
+    ch = co;
+    x.swap(y);
+    std::vector<float> br(F * ch), br2(F * ch);
+    const size_t dil[3] = {1, 3, 9};
+    for (size_t r = 0; r < 3; ++r) {
+      const CxRes& R = B.res[r];
+      cx_snake(x.data(), F, ch, R.a0.data(), br.data());
+      cx_conv1d(c->pool, br.data(), F, ch, ch, dil[r], R.w0.data(), R.w0.size(), R.b0.data(), br2.data());
+      cx_snake(br2.data(), F, ch, R.a1.data(), br.data());
+      cx_conv1d(c->pool, br.data(), F, ch, ch, 1, R.w1.data(), R.w1.size(), R.b1.data(), br2.data());
+      for (size_t i = 0; i < F * ch; ++i) x[i] = x[i] + br2[i];
+    }
+  }
+  if (stop_block <= 4) {
+    std::copy(x.begin(), x.end(), out);
+    return;
+  }
+  std::vector<float> sn(F * ch);
+  cx_snake(x.data(), F, ch, c->tail_alpha.data(), sn.data());
+  cx_conv1d(c->pool, sn.data(), F, ch, 1, 1, c->out_w.data(), c->out_w.size(), c->out_b.data(), out);
+  for (size_t i = 0; i < F; ++i) out[i] = tanhf(out[i]);
+}
+
+}  // namespace
+
+extern "C" {
+
+orc_codec* orc_codec_open(const char* path, uint32_t threads, char* err, size_t cap) {
+  try {
+    std::unique_ptr<orc_codec> c(new orc_codec(threads ? threads : std::max(1u, std::thread::hardware_concurrency())));
+    c->g.open_file(path);
+    cx_load(c.get());
+    return c.release();
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return nullptr;
+  }
+}
+
+void orc_codec_close(orc_codec* c) { delete c; }
+
+int32_t orc_codec_rvq_lookup(orc_codec* c, const int32_t* codes, uint32_t ncb, uint32_t n_frames, float* latents,
+                             char* err, size_t cap) {
+  try {
+    cx_rvq_lookup(c, codes, ncb, n_frames, latents);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+int32_t orc_codec_post_module(orc_codec* c, const float* latents, uint32_t n_frames, float* hidden, char* err,
+                              size_t cap) {
+  try {
+    cx_post_module(c, latents, n_frames, hidden);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+int32_t orc_codec_upsample(orc_codec* c, const float* hidden, uint32_t n_frames, float* out, char* err, size_t cap) {
+  try {
+    cx_upsample(c, hidden, n_frames, out);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+int32_t orc_codec_decoder(orc_codec* c, const float* hidden, uint32_t n_frames, uint32_t hidden_dim,
+                          uint32_t stop_block, float* out, char* err, size_t cap) {
+  try {
+    cx_decoder(c, hidden, n_frames, hidden_dim, out, stop_block);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+int32_t orc_codec_decode_waveform(orc_codec* c, const int32_t* codes, uint32_t ncb, uint32_t n_frames,
+                                  float* samples, char* err, size_t cap) {
+  try {
+    std::vector<float> lat(size_t(n_frames) * CX_HIDDEN), post(size_t(n_frames) * CX_HIDDEN);
+    std::vector<float> up(size_t(n_frames) * 4 * CX_HIDDEN);
+    cx_rvq_lookup(c, codes, ncb, n_frames, lat.data());
+    cx_post_module(c, lat.data(), n_frames, post.data());
+    cx_upsample(c, post.data(), n_frames, up.data());
+    cx_decoder(c, up.data(), n_frames * 4, CX_HIDDEN, samples);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+void orc_codec_snake(const float* x, size_t frames, size_t ch, const float* alpha, float* out) {
+  cx_snake(x, frames, ch, alpha, out);
+}
+
+int32_t orc_codec_conv1d(const float* x, size_t frames, size_t in_ch, size_t out_ch, size_t dilation,
+                         const float* w, size_t w_len, const float* bias, float* out, char* err, size_t cap) {
+  try {
+    Pool pool(1);
+    cx_conv1d(pool, x, frames, in_ch, out_ch, dilation, w, w_len, bias, out);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+int32_t orc_codec_conv_transpose(const float* x, size_t frames, size_t in_ch, size_t out_ch, size_t stride,
+                                 const float* w, size_t w_len, const float* bias, float* out, char* err, size_t cap) {
+  try {
+    Pool pool(1);
+    cx_conv_transpose(pool, x, frames, in_ch, out_ch, stride, w, w_len, bias, out);
+    return 1;
+  } catch (const std::exception& e) {
+    copy_err(e, err, cap);
+    return 0;
+  }
+}
+
+void orc_codec_depthwise(const float* x, size_t frames, size_t ch, size_t k, const float* w, const float* bias,
+                         float* out) {
+  cx_depthwise(x, frames, ch, k, w, bias, out);
+}
+
+void orc_codec_layer_norm(float* x, size_t frames, size_t ch, const float* w, const float* b, float eps) {
+  cx_layer_norm(x, frames, ch, w, b, eps);
+}
+
+float orc_codec_erf(float v) { return cx_erf(v); }
+float orc_codec_gelu(float v) { return cx_gelu(v); }
+
+}  // extern "C"

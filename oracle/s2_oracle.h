@@ -112,6 +112,35 @@ int32_t orc_generate_codes(orc_model* m, const int32_t* prompt_flat, size_t prom
                            int32_t* codes_out, uint32_t* n_frames_out, double* prefill_seconds,
                            double* decode_seconds, char* err, size_t err_cap);
 
+
+/* RVQ codec decode (crates/fish_s2_infer/src/codec.rs:1690-1714) on the CPU.
+   Buffers are frame-major f32: latents/hidden [frames][1024]; the upsample
+   output [4 frames][1024]; decoder samples [frames * 512]; with stop_block
+   <= 4 the decoder writes the residual stream after that many blocks, with 5
+   and above the samples. */
+typedef struct orc_codec orc_codec;
+orc_codec* orc_codec_open(const char* path, uint32_t threads, char* err, size_t cap);
+void orc_codec_close(orc_codec* c);
+int32_t orc_codec_rvq_lookup(orc_codec* c, const int32_t* codes, uint32_t ncb, uint32_t n_frames, float* latents,
+                             char* err, size_t cap);
+int32_t orc_codec_post_module(orc_codec* c, const float* latents, uint32_t n_frames, float* hidden, char* err,
+                              size_t cap);
+int32_t orc_codec_upsample(orc_codec* c, const float* hidden, uint32_t n_frames, float* out, char* err, size_t cap);
+int32_t orc_codec_decoder(orc_codec* c, const float* hidden, uint32_t n_frames, uint32_t hidden_dim,
+                          uint32_t stop_block, float* out, char* err, size_t cap);
+int32_t orc_codec_decode_waveform(orc_codec* c, const int32_t* codes, uint32_t ncb, uint32_t n_frames,
+                                  float* samples, char* err, size_t cap);
+void orc_codec_snake(const float* x, size_t frames, size_t ch, const float* alpha, float* out);
+int32_t orc_codec_conv1d(const float* x, size_t frames, size_t in_ch, size_t out_ch, size_t dilation,
+                         const float* w, size_t w_len, const float* bias, float* out, char* err, size_t cap);
+int32_t orc_codec_conv_transpose(const float* x, size_t frames, size_t in_ch, size_t out_ch, size_t stride,
+                                 const float* w, size_t w_len, const float* bias, float* out, char* err, size_t cap);
+void orc_codec_depthwise(const float* x, size_t frames, size_t ch, size_t k, const float* w, const float* bias,
+                         float* out);
+void orc_codec_layer_norm(float* x, size_t frames, size_t ch, const float* w, const float* b, float eps);
+float orc_codec_erf(float v);
+float orc_codec_gelu(float v);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,3 +38,19 @@ def tiny_q8_gguf(model_dir):
 @pytest.fixture(scope="session")
 def tiny_q4_gguf(model_dir):
     return synth.ensure_gguf(synth.TINY.with_(linear_type=synth.GGML_Q4_0), model_dir)
+
+
+@pytest.fixture(scope="session")
+def codec_gguf(model_dir):
+    return synth.ensure_codec_gguf(model_dir)
+
+
+def random_codes(n_frames, seed):
+    """Codebook-major codes [10][n_frames]: row 0 semantic in [0, 4096), rows
+    1..9 residual in [0, 1024) (rvq_lookup_codes, codec.rs:2536-2596)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    sem = rng.integers(0, 4096, (1, n_frames))
+    res = rng.integers(0, 1024, (9, n_frames))
+    return np.concatenate([sem, res]).astype(np.int32)
