@@ -16,6 +16,13 @@ shortened; "steps" in the output is the number of frames actually timed.
 --warmup W runs the smallest number of untimed generations holding W frames
 (at least one).
 
+Workload "codec": the RVQ codec decode that follows code generation
+(decode_waveform, crates/fish_s2_infer/src/codec.rs:1690-1714) on a seeded
+synthetic codec: 512 code frames (the "full" workload's output length) ->
+4 x 512 latent frames -> 1,048,576 samples at 44.1 kHz.  One step = one
+whole decode with codes and samples resident in device memory; `value` is
+code frames/s.  The default run also reports this decode under "codec".
+
 Workload "full_b8": the voice-clone batch shape: 8 concurrent requests on
 the same f16 model, each a 1500-position prompt (250 text ids, 1000
 reference frames with uniform random codes, 250 text ids), MFMA prefill,
@@ -136,6 +143,76 @@ def cpu_baseline(path, shape, threads, prompt_len, frames):
     return r["n_frames"] / r["decode_seconds"], r
 
 
+CODEC_FRAMES = 512
+MFMA_F16_PEAK_TFLOPS = 2500.0
+CODEC_CONVS = (["entry"] + [f"b{b}_convT" for b in range(1, 5)] +
+               [f"b{b}_r{r}_conv{k}" for b in range(1, 5) for r in range(1, 4) for k in (0, 1)] +
+               [f"up{s}_{x}" for s in (1, 2) for x in ("convT", "pw1", "pw2")])
+
+
+def bench_codec(args, full):
+    """decode_waveform of CODEC_FRAMES code frames on the GPU (HIP events in
+    the library, device-resident codes and samples), the MFMA roofline of the
+    convolution with the largest share, and (full) the CPU oracle on a
+    bounded sample."""
+    from s2hip import Codec, synth
+
+    frames = (args.frames or CODEC_FRAMES) if full else CODEC_FRAMES
+    path = synth.ensure_codec_gguf(args.model_dir, threads=min(16, os.cpu_count() or 1))
+    timed = max(1, -(-(args.steps or frames) // frames)) if full else 3
+    warm = max(1, -(-args.warmup // frames)) if full else 1
+    with Codec(path, max_frames=frames, device=0) as c:
+        c.time("decode", frames, warm)
+        us, conv_flops = c.time("decode", frames, timed)
+        per = {}
+        for name in CODEC_CONVS:
+            per[name] = c.time(name, frames, 5)
+    top = max(per, key=lambda n: per[n][0])
+    kus, kfl = per[top]
+    ach = kfl / kus / 1e6
+    fps = frames / (us * 1e-6)
+    log(f"codec decode {frames} frames: {us / 1e3:.3f} ms, {fps:.0f} code frames/s; dominant {top} {kus:.1f} us")
+    out = {
+        "metric": "codec decode_waveform code frames/s (RVQ lookup + post-module + upsample + decoder), one GPU",
+        "value": round(fps, 1),
+        "unit": "code frames/s",
+        "n_gpus": 1,
+        "steps": timed * frames,
+        "warmup": warm * frames,
+        "ms_per_step": round(us / 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 MFMA (f16-rounded conv inputs as the reference; split f16 hi+lo for f32 inputs), f32 accumulate",
+        "data": "synthetic codec (seeded random-init, fan-in scaled), fixed pseudo-random codes",
+        "config": {"workload": f"codec: decode_waveform of {frames} code frames x 10 codebooks -> {4 * frames} latent "
+                               f"frames -> {frames * 2048} samples at 44.1 kHz", "frames": frames,
+                   "parallelism": "single GPU"},
+        "samples_per_s": round(frames * 2048 / (us * 1e-6)),
+        "realtime_factor": round(frames * 2048 / (us * 1e-6) / 44100.0, 1),
+        "conv_tflops": round(conv_flops / us / 1e6, 1),
+        "roofline": {"bound": "mfma", "kernel": f"conv_gemm {top}", "achieved": round(ach, 1),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": None, "flops_per_launch": round(kfl), "avg_us": round(kus, 2)},
+        "kernels": {n: round(v[0], 1) for n, v in sorted(per.items(), key=lambda kv: -kv[1][0])[:8]},
+    }
+    if full and args.cpu_baseline:
+        from oracle import oracle as O
+
+        threads = cpu_threads()
+        n = max(1, args.cpu_frames)
+        rng_codes = [[(f * 7919 + q * 104729 + 17) % (4096 if q == 0 else 1024) for f in range(n)] for q in range(10)]
+        t0 = time.time()
+        with O.OracleCodec(path, threads) as oc:
+            oc.decode_waveform(rng_codes, 10, n)
+        dt = time.time() - t0
+        out["cpu_baseline"] = {"value": round(n / dt, 4), "unit": "code frames/s", "cores": threads, "kind": "port",
+                               "cpu_model": cpu_model(),
+                               "sample": f"{n} code frames ({n * 2048} samples), the oracle's decode_waveform in the "
+                                         f"reference's summation order, output-frame parallel threads"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,7 +221,8 @@ def main():
     ap.add_argument("--frames", type=int, default=None, help="frames per generation (default: workload's)")
     ap.add_argument("--prompt", type=int, default=None, help="prompt tokens (default: workload's)")
     ap.add_argument("--warmup", type=int, default=1, help="untimed warm-up frames (whole generations, at least one)")
-    ap.add_argument("--workload", default="full", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="full", choices=sorted(list(WORKLOADS) + ["codec"]))
+    ap.add_argument("--codec", type=int, default=1, help="also time the 512-frame codec decode (default run)")
     ap.add_argument("--model-dir", default=os.environ.get("S2HIP_MODEL_DIR", "/tmp/s2hip_models"))
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--kv", choices=("f32", "f16"), default="f32",
@@ -157,6 +235,10 @@ def main():
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the dual-AR loop is a single-GPU "
               "batch-1 path in this build", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload == "codec":
+        print(json.dumps(bench_codec(args, full=True)), flush=True)
+        return
 
     from s2hip import Engine, synth
 
@@ -279,6 +361,11 @@ def main():
         "cpu_baseline": cpu,
         "graph_used": r["graph_used"],
     }
+    if args.codec and args.workload == "full":
+        try:
+            out["codec"] = bench_codec(args, full=False)
+        except Exception as e:  # the decode loop's line must still print
+            out["codec"] = {"error": str(e)}
     print(json.dumps(out), flush=True)
 
 

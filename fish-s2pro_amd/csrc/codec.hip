@@ -1,0 +1,559 @@
+// codec.hip -- HIP kernels of the RVQ codec decode (crates/fish_s2_infer/src/codec.rs:1690-1714).
+//
+// The decoder's convolutions (causal conv1d, transposed conv1d, pointwise
+// linears) all run on one implicit-GEMM MFMA kernel, conv_gemm_kernel:
+//   * block tile: 256 frames x TM = 32 * MC output channels, 4 waves each
+//     holding 64 frames x TM channels (2 x MC tiles of v_mfma_f32_32x32x16_f16,
+//     frames as the A operand, weights as B, so the 32 lanes of a row group
+//     store 32 consecutive channels of one frame);
+//   * K runs over input-channel stages of KC (16 or 32) channels; a stage
+//     holds the stage's A window -- the tile's 256 frames plus the halo the
+//     taps reach back, loaded once and read by every tap at its own row
+//     offset -- and the weights of all G taps for those channels;
+//   * two LDS buffers: the next stage's global loads are in registers while a
+//     stage computes, written to the other buffer after it, one barrier per
+//     stage;
+//   * tiles of one weight tile (m tile) are dealt to the same XCD, so that
+//     XCD's L2 serves its weights to all of its frame tiles.
+// Small per-frame kernels handle the rest: RVQ lookup, RoPE, the windowed
+// attention of the post-module transformer, depthwise conv + LayerNorm, the
+// output conv + tanh.
+
+#include "codec.h"
+#include "expf_glibc.h"
+
+namespace s2 {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t CG_TF = 256;    // frames per block tile
+constexpr uint32_t CG_MAXLD = 10;  // 16-byte staging loads per thread per stage
+
+// LDS rows are KC halfs (CH = KC / 8 chunks of 16 bytes), chunk c of row r
+// stored at c ^ swz(r).  Weight rows are read 32 at a time from a multiple
+// of 32; A window rows from any offset (the tap's shift), so their swizzle
+// only needs 8 consecutive rows on distinct banks.
+template <uint32_t CH>
+__device__ __forceinline__ uint32_t swz_a(uint32_t r) {
+  return CH == 2 ? ((r >> 2) & 1u) : (((r >> 1) ^ (r >> 3)) & 3u);
+}
+template <uint32_t CH>
+__device__ __forceinline__ uint32_t swz_w(uint32_t r) {
+  return CH == 2 ? (((r >> 2) ^ (r >> 3)) & 1u) : (((r >> 1) ^ (r >> 3)) & 3u);
+}
+
+// erf_approx and gelu_erf (codec.rs:3886-3899), the reference's operation order.
+__device__ __forceinline__ float erf_as(float value) {
+  const float sign = value < 0.0f ? -1.0f : 1.0f;
+  const float x = fabsf(value);
+  const float t = __fdiv_rn(1.0f, __fadd_rn(1.0f, __fmul_rn(0.3275911f, x)));
+  float p = __fsub_rn(__fmul_rn(1.0614054f, t), 1.4531521f);
+  p = __fadd_rn(__fmul_rn(p, t), 1.4214138f);
+  p = __fsub_rn(__fmul_rn(p, t), 0.28449672f);
+  p = __fadd_rn(__fmul_rn(p, t), 0.2548296f);
+  p = __fmul_rn(p, t);
+  return __fmul_rn(sign, __fsub_rn(1.0f, __fmul_rn(p, expf_glibc(__fmul_rn(-x, x)))));
+}
+__device__ __forceinline__ float gelu_as(float v) {
+  return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, erf_as(__fmul_rn(v, 0.70710677f))));
+}
+// snake_activation_frame_major (codec.rs:2162-2186)
+__device__ __forceinline__ float snake(float x, float alpha) {
+  const float a = fabsf(alpha) < 1e-8f ? 1e-8f : alpha;
+  const float s = sinf(__fmul_rn(a, x));
+  return __fadd_rn(x, __fdiv_rn(__fmul_rn(s, s), a));
+}
+
+template <int MC, int KC, int PL>
+__global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint32_t m_tiles, uint32_t f_tiles,
+                                                           uint32_t halo, int32_t wbase, int32_t toff0,
+                                                           int32_t tstep) {
+  constexpr uint32_t TM = 32 * MC, CH = KC / 8;
+  extern __shared__ __align__(16) _Float16 cg_lds[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  // workgroup b runs on XCD b % 8: tile t = XCD-major order, m-major tiles
+  const uint32_t nb = m_tiles * f_tiles, b = blockIdx.x, xcd = b & 7u, slot = b >> 3;
+  const uint32_t q8 = nb >> 3, r8 = nb & 7u;
+  const uint32_t t = xcd < r8 ? xcd * (q8 + 1u) + slot : r8 * (q8 + 1u) + (xcd - r8) * q8 + slot;
+  const uint32_t mt = t / f_tiles, ft = t - mt * f_tiles;
+  const uint32_t phase = blockIdx.y;
+  const uint32_t f0 = ft * CG_TF;
+  const uint32_t AR = CG_TF + halo;
+  const uint32_t a_chunks = PL * AR * CH, w_chunks = a.G * TM * CH, tot = a_chunks + w_chunks;
+  const uint32_t buf_halfs = (PL * AR + a.G * TM) * KC;
+  const uint32_t nst = a.C / KC;
+  const _Float16* wsrc = a.w + (size_t(phase) * m_tiles + mt) * (size_t(a.G) * TM * a.C);
+  const int32_t row0 = int32_t(f0) + wbase;
+
+  // Per staging slot i (chunk tid + 256 i of a stage): the element offset of
+  // its 16 bytes at stage 0 and its LDS offset, with the source in bits
+  // 30..31 (0: A hi plane, 1: A lo plane, 2: weights, 3: zero / no chunk).
+  // Stage st adds st * KC (A) or st * G * TM * KC (weights) to the offset.
+  uint32_t goff[CG_MAXLD], loff[CG_MAXLD];
+#pragma unroll
+  for (uint32_t i = 0; i < CG_MAXLD; ++i) {
+    const uint32_t qd = tid + 256u * i;
+    uint32_t kind = 3u, g = 0u, l = 0u;
+    if (qd < a_chunks) {
+      const uint32_t pl = PL == 2 ? qd / (AR * CH) : 0u, rem = qd - pl * (AR * CH);
+      const uint32_t row = rem / CH, c = rem - row * CH;
+      const int32_t src = row0 + int32_t(row);
+      l = (pl * AR + row) * KC + ((c ^ swz_a<CH>(row)) << 3);
+      if (src >= 0 && src < int32_t(a.F)) {
+        kind = pl;
+        g = uint32_t(src) * a.ldx + c * 8u;
+      }
+    } else if (qd < tot) {
+      const uint32_t wq = qd - a_chunks, row = wq / CH, c = wq - row * CH;
+      l = PL * AR * KC + row * KC + ((c ^ swz_w<CH>(row)) << 3);
+      kind = 2u;
+      g = wq * 8u;
+    } else {
+      l = 0xffffffffu >> 2;  // no chunk: nothing stored
+    }
+    goff[i] = g;
+    loff[i] = l | (kind << 30);
+  }
+  const uint32_t wstage = a.G * TM * KC;
+
+  uint4 stg[CG_MAXLD];
+  auto load = [&](uint32_t st) {
+#pragma unroll
+    for (uint32_t i = 0; i < CG_MAXLD; ++i) {
+      const uint32_t kind = loff[i] >> 30;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (kind == 2u) {
+        v = *reinterpret_cast<const uint4*>(wsrc + size_t(st) * wstage + goff[i]);
+      } else if (kind < 2u) {
+        const _Float16* base = kind ? a.xl : a.xh;
+        v = *reinterpret_cast<const uint4*>(base + size_t(goff[i]) + st * KC);
+      }
+      stg[i] = v;
+    }
+  };
+  auto store = [&](uint32_t bsel) {
+    _Float16* B = cg_lds + bsel * buf_halfs;
+#pragma unroll
+    for (uint32_t i = 0; i < CG_MAXLD; ++i) {
+      const uint32_t l = loff[i] & 0x3fffffffu;
+      if (l != (0xffffffffu >> 2)) *reinterpret_cast<uint4*>(B + l) = stg[i];
+    }
+  };
+
+  floatx16 acc[2][MC];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < MC; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  auto compute = [&](uint32_t bsel) {
+    const _Float16* A = cg_lds + bsel * buf_halfs;
+    const _Float16* W = A + PL * AR * KC;
+    for (uint32_t g = 0; g < a.G; ++g) {
+      const uint32_t toff = uint32_t(toff0 + int32_t(g) * tstep);
+#pragma unroll
+      for (uint32_t kk = 0; kk < uint32_t(KC / 16); ++kk) {
+        const uint32_t c = kk * 2u + (lane >> 5);
+        half8 bf[MC];
+#pragma unroll
+        for (int j = 0; j < MC; ++j) {
+          const uint32_t row = g * TM + uint32_t(j) * 32u + (lane & 31u);
+          bf[j] = *reinterpret_cast<const half8*>(W + row * KC + ((c ^ swz_w<CH>(row)) << 3));
+        }
+#pragma unroll
+        for (int p = 0; p < PL; ++p) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const uint32_t row = wave * 64u + uint32_t(i) * 32u + (lane & 31u) + toff;
+            const half8 af =
+                *reinterpret_cast<const half8*>(A + (uint32_t(p) * AR + row) * KC + ((c ^ swz_a<CH>(row)) << 3));
+#pragma unroll
+            for (int j = 0; j < MC; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+
+  load(0);
+  store(0);
+  __syncthreads();
+  if (nst > 1) load(1);
+  for (uint32_t st = 0; st < nst; ++st) {
+    compute(st & 1u);
+    if (st + 1 < nst) store((st + 1) & 1u);
+    __syncthreads();
+    if (st + 2 < nst) load(st + 2);
+  }
+
+  // epilogue: acc[i][j][v] = D[frame 8 (v/4) + 4 (lane/32) + v%4][channel lane%32].
+  // The residual values of a fragment are loaded together before its stores
+  // (res may be the output buffer itself, so loads cannot move past stores).
+#pragma unroll
+  for (int j = 0; j < MC; ++j) {
+    const uint32_t m = mt * TM + uint32_t(j) * 32u + (lane & 31u);
+    if (m >= a.M) continue;
+    const float bias = a.bias[m];
+    const float gam = a.gamma ? a.gamma[m] : 1.0f;
+    const float alp = a.alpha ? a.alpha[m] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t fb = f0 + wave * 64u + uint32_t(i) * 32u + 4u * (lane >> 5);
+      float rv[16];
+      if (a.res) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t f = fb + 8u * uint32_t(v >> 2) + uint32_t(v & 3);
+          rv[v] = f < a.F ? a.res[(size_t(f) * a.ostride + phase) * a.ldres + m] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t f = fb + 8u * uint32_t(v >> 2) + uint32_t(v & 3);
+        if (f >= a.F) continue;
+        const size_t row = size_t(f) * a.ostride + phase;
+        float val = __fadd_rn(acc[i][j][v], bias);
+        if (a.gelu) val = gelu_as(val);
+        if (a.gamma) val = __fmul_rn(val, gam);
+        if (a.res) val = __fadd_rn(rv[v], val);
+        if (a.y32) a.y32[row * a.ldy + m] = val;
+        if (a.alpha) val = snake(val, alp);
+        if (a.yh) {
+          const _Float16 h = _Float16(val);
+          a.yh[row * a.ldh + m] = h;
+          if (a.yl) a.yl[row * a.ldh + m] = _Float16(__fsub_rn(val, float(h)));
+        }
+      }
+    }
+  }
+}
+
+// rvq_lookup_codes (codec.rs:2536-2596): one block per frame, 4 outputs per
+// thread; every sum in the reference's order (bit-exact).
+__global__ __launch_bounds__(256) void codec_rvq_kernel(RvqArgs a) {
+  const uint32_t f = blockIdx.x;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t o = threadIdx.x + 256u * k;
+    float acc = 0.0f;
+    for (uint32_t q = 0; q < 10; ++q) {
+      int32_t code = a.codes[size_t(q) * a.F + f];
+      if (code < 0 || uint32_t(code) >= a.cb_size[q]) {
+        if (a.err) *a.err = 1u;
+        code = 0;
+      }
+      const float* z = a.cb[q] + size_t(code) * 8u;
+      const float* w = a.pw[q] + size_t(o) * 8u;
+      float d = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) d = __fadd_rn(d, __fmul_rn(z[j], w[j]));
+      acc = __fadd_rn(acc, __fadd_rn(d, a.pb[q][o]));
+    }
+    a.out[size_t(f) * 1024u + o] = acc;
+  }
+}
+
+__global__ __launch_bounds__(256) void codec_check_codes_kernel(const int32_t* codes, uint32_t F, uint32_t* err) {
+  const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+  if (i >= size_t(10) * F) return;
+  const int32_t c = codes[i];
+  const int32_t size = i < F ? 4096 : 1024;
+  if (c < 0 || c >= size) *err = 1u;
+}
+
+// apply_rope_normal (attention.rs:172-206) on q and k of one frame: pairs
+// (x0, x1) -> (x0 c - x1 s, x0 s + x1 c) with the table's (cos, sin).
+__global__ __launch_bounds__(256) void codec_rope_kernel(float* qkv, const float2* table) {
+  const uint32_t t = blockIdx.x;
+  float* row = qkv + size_t(t) * 3072u;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t p = threadIdx.x + 256u * k;  // pair 0..1023 over q (0..511) and k (512..1023)
+    const uint32_t i = p & 31u;
+    float* e = row + 2u * p;
+    const float2 cs = table[size_t(t) * 32u + i];
+    const float x0 = e[0], x1 = e[1];
+    e[0] = __fsub_rn(__fmul_rn(x0, cs.x), __fmul_rn(x1, cs.y));
+    e[1] = __fadd_rn(__fmul_rn(x0, cs.y), __fmul_rn(x1, cs.x));
+  }
+}
+
+// Windowed causal attention of the post-module transformer
+// (forward_codec_transformer_layer_with_window, codec.rs:3278-3300, over
+// gqa_decode_attention, attention.rs:208-247): block = 64 queries x one head;
+// the keys and values the block's queries see ([q0 - 127, q0 + 63]) sit in
+// LDS.  A wave takes 16 queries: lane j scores keys j and j + 64 of the
+// query's window, softmax over the wave, then lane d sums p_k v_k[d].
+constexpr uint32_t CA_Q = 64, CA_W = 128, CA_K = CA_Q + CA_W - 1;
+__global__ __launch_bounds__(256) void codec_attn_kernel(const float* qkv, uint32_t T, float* out) {
+  __shared__ float ks[CA_K][65];
+  __shared__ float vs[CA_K][64];
+  __shared__ float qs[CA_Q][64];
+  const uint32_t q0 = blockIdx.x * CA_Q, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t kstart = q0 >= CA_W - 1 ? q0 - (CA_W - 1) : 0u;
+  const uint32_t kend = min(T, q0 + CA_Q);
+  const uint32_t nk = kend - kstart;
+  for (uint32_t e = tid; e < nk * 64u; e += 256u) {
+    const uint32_t r = e >> 6, d = e & 63u;
+    const float* src = qkv + size_t(kstart + r) * 3072u + h * 64u + d;
+    ks[r][d] = src[1024];
+    vs[r][d] = src[2048];
+  }
+  for (uint32_t e = tid; e < CA_Q * 64u; e += 256u) {
+    const uint32_t r = e >> 6, d = e & 63u;
+    qs[r][d] = q0 + r < T ? qkv[size_t(q0 + r) * 3072u + h * 64u + d] : 0.0f;
+  }
+  __syncthreads();
+  for (uint32_t qq = 0; qq < 16; ++qq) {
+    const uint32_t ql = wave * 16u + qq, tq = q0 + ql;
+    if (tq >= T) break;
+    const uint32_t lo = tq >= CA_W - 1 ? tq - (CA_W - 1) : 0u, n = tq - lo + 1u;
+    float s0 = -INFINITY, s1 = -INFINITY;
+    if (lane < n) {
+      const float* kr = ks[lo + lane - kstart];
+      float d = 0.0f;
+#pragma unroll 16
+      for (int i = 0; i < 64; ++i) d = fmaf(qs[ql][i], kr[i], d);
+      s0 = d * 0.125f;
+    }
+    if (lane + 64u < n) {
+      const float* kr = ks[lo + lane + 64u - kstart];
+      float d = 0.0f;
+#pragma unroll 16
+      for (int i = 0; i < 64; ++i) d = fmaf(qs[ql][i], kr[i], d);
+      s1 = d * 0.125f;
+    }
+    float mx = fmaxf(s0, s1);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const float e0 = lane < n ? expf_glibc(s0 - mx) : 0.0f;
+    const float e1 = lane + 64u < n ? expf_glibc(s1 - mx) : 0.0f;
+    float sum = e0 + e1;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float p0 = e0 / sum, p1 = e1 / sum;
+    float o = 0.0f;
+    const uint32_t base = lo - kstart;
+    for (uint32_t k = 0; k < n; ++k) {
+      const float pk = __shfl(k < 64u ? p0 : p1, int(k & 63u), 64);
+      o = fmaf(pk, vs[base + k][lane], o);
+    }
+    out[size_t(tq) * 1024u + h * 64u + lane] = o;
+  }
+}
+
+__global__ __launch_bounds__(256) void codec_scaled_residual_kernel(float* x, const float* p, const float* scale,
+                                                                    size_t n, uint32_t D) {
+  const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+  if (i >= n) return;
+  x[i] = __fadd_rn(x[i], __fmul_rn(p[i], scale[i % D]));
+}
+
+__global__ __launch_bounds__(256) void codec_split16_kernel(const float* x, _Float16* hi, _Float16* lo, size_t n) {
+  const size_t i = size_t(blockIdx.x) * 256u + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  const _Float16 h = _Float16(v);
+  hi[i] = h;
+  lo[i] = _Float16(__fsub_rn(v, float(h)));
+}
+
+// forward_codec_convnext_block front (codec.rs:3444-3460): depthwise causal
+// conv k7 (depthwise_causal_conv1d :3576-3619, sums in the reference order)
+// then layer_norm_affine_frame_major (:3621-3654) over the frame's 1024
+// channels; output as hi / lo planes for the pointwise product.
+__global__ __launch_bounds__(256) void codec_dwconv_ln_kernel(const float* x, uint32_t F, const float* w,
+                                                              const float* b, const float* ln_w, const float* ln_b,
+                                                              float eps, _Float16* hi, _Float16* lo) {
+  __shared__ float red[4];
+  const uint32_t f = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  float d[4];
+  float s = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t c = tid + 256u * k;
+    float acc = b[c];
+#pragma unroll
+    for (uint32_t kk = 0; kk < 7; ++kk) {
+      if (f + kk < 6u) continue;
+      const uint32_t src = f + kk - 6u;
+      acc = __fadd_rn(acc, __fmul_rn(x[size_t(src) * 1024u + c], w[c * 7u + kk]));
+    }
+    d[k] = acc;
+    s += acc;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  const float mean = ((red[0] + red[1]) + (red[2] + red[3])) / 1024.0f;
+  __syncthreads();
+  float v = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const float c = d[k] - mean;
+    v += c * c;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const float var = ((red[0] + red[1]) + (red[2] + red[3])) / 1024.0f;
+  const float scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+#pragma unroll
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t c = tid + 256u * k;
+    const float y = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(d[k], mean), scale), ln_w[c]), ln_b[c]);
+    const _Float16 h = _Float16(y);
+    hi[size_t(f) * 1024u + c] = h;
+    lo[size_t(f) * 1024u + c] = _Float16(__fsub_rn(y, float(h)));
+  }
+}
+
+// Output conv of the decoder (96 -> 1, k 7, causal; causal_conv_1d_frame_major
+// :2212-2293, sum = bias, then tap, then channel, in order) over the f16
+// snake outputs, then tanh.  Block = 256 samples; the 262 input rows it reads
+// are staged in LDS (row stride 98 halfs: 49 dwords, odd, so lanes reading
+// consecutive rows hit distinct banks).
+constexpr uint32_t OC_ROW = 98;
+__global__ __launch_bounds__(256) void codec_out_conv_kernel(const _Float16* x, uint32_t T, const float* w, float b,
+                                                             float* out) {
+  __shared__ _Float16 xs[262 * OC_ROW];
+  __shared__ float wsm[7][96];
+  const uint32_t t0 = blockIdx.x * 256u, tid = threadIdx.x;
+  for (uint32_t e = tid; e < 96u * 7u; e += 256u) wsm[e % 7u][e / 7u] = w[e];  // w[c][tap]
+  for (uint32_t e = tid; e < 262u * 12u; e += 256u) {
+    const uint32_t r = e / 12u, c = e - r * 12u;
+    const int32_t src = int32_t(t0) + int32_t(r) - 6;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (src >= 0 && src < int32_t(T)) v = *reinterpret_cast<const uint4*>(x + size_t(src) * 96u + c * 8u);
+    uint32_t* d = reinterpret_cast<uint32_t*>(xs + r * OC_ROW + c * 8u);
+    d[0] = v.x;
+    d[1] = v.y;
+    d[2] = v.z;
+    d[3] = v.w;
+  }
+  __syncthreads();
+  const uint32_t t = t0 + tid;
+  if (t >= T) return;
+  float y = b;
+  for (uint32_t tap = 0; tap < 7; ++tap) {
+    const _Float16* row = xs + (tid + tap) * OC_ROW;
+    for (uint32_t c = 0; c < 96; c += 2) {
+      const uint32_t pr = *reinterpret_cast<const uint32_t*>(row + c);
+      const float x0 = float(__builtin_bit_cast(_Float16, uint16_t(pr & 0xffffu)));
+      const float x1 = float(__builtin_bit_cast(_Float16, uint16_t(pr >> 16)));
+      y = __fadd_rn(y, __fmul_rn(x0, wsm[tap][c]));
+      y = __fadd_rn(y, __fmul_rn(x1, wsm[tap][c + 1]));
+    }
+  }
+  out[t] = tanhf(y);
+}
+
+template <int MC, int KC, int PL>
+hipError_t conv_gemm_launch(const ConvGemmArgs& a, uint32_t phases, hipStream_t s) {
+  constexpr uint32_t TM = 32 * MC, CH = KC / 8;
+  const int32_t last = a.off0 + int32_t(a.G - 1) * a.ostep;
+  const int32_t wbase = a.off0 < last ? a.off0 : last;
+  const uint32_t halo = uint32_t((a.off0 < last ? last : a.off0) - wbase);
+  const uint32_t AR = CG_TF + halo;
+  if (size_t(PL) * AR * CH + size_t(a.G) * TM * CH > 256u * CG_MAXLD) return hipErrorInvalidValue;
+  const size_t lds = 2u * (size_t(PL) * AR + size_t(a.G) * TM) * KC * sizeof(_Float16);
+  if (lds > 160u * 1024u) return hipErrorInvalidValue;
+  const uint32_t m_tiles = (a.M + TM - 1) / TM, f_tiles = (a.F + CG_TF - 1) / CG_TF;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm_kernel<MC, KC, PL>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  conv_gemm_kernel<MC, KC, PL><<<dim3(m_tiles * f_tiles, phases), 256, lds, s>>>(
+      a, m_tiles, f_tiles, halo, wbase, a.off0 - wbase, a.ostep);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+ConvTile conv_tile(uint32_t M, uint32_t G, bool split) {
+  (void)split;
+  ConvTile t;
+  t.mc = (M % 128u != 0 && M % 96u == 0) ? 3u : 4u;
+  t.kc = G > 1 ? 16u : 32u;
+  return t;
+}
+
+size_t conv_packed_halfs(uint32_t phases, uint32_t M, uint32_t G, uint32_t C, ConvTile t) {
+  const uint32_t TM = 32 * t.mc;
+  return size_t(phases) * ((M + TM - 1) / TM) * TM * G * C;
+}
+
+hipError_t launch_conv_gemm(const ConvGemmArgs& a, uint32_t phases, ConvTile t, hipStream_t s) {
+  if (a.C == 0 || a.C % t.kc || a.F == 0 || a.M == 0 || a.G == 0 || phases == 0) return hipErrorInvalidValue;
+  if (a.ldx % 8u || (a.yh && a.ldh % 2u)) return hipErrorInvalidValue;
+  const bool split = a.xl != nullptr;
+  if (t.mc == 4 && t.kc == 16) return split ? conv_gemm_launch<4, 16, 2>(a, phases, s) : conv_gemm_launch<4, 16, 1>(a, phases, s);
+  if (t.mc == 4 && t.kc == 32) return split ? conv_gemm_launch<4, 32, 2>(a, phases, s) : conv_gemm_launch<4, 32, 1>(a, phases, s);
+  if (t.mc == 3 && t.kc == 16) return split ? conv_gemm_launch<3, 16, 2>(a, phases, s) : conv_gemm_launch<3, 16, 1>(a, phases, s);
+  if (t.mc == 3 && t.kc == 32) return split ? conv_gemm_launch<3, 32, 2>(a, phases, s) : conv_gemm_launch<3, 32, 1>(a, phases, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_codec_rvq(const RvqArgs& a, hipStream_t s) {
+  if (a.F == 0) return hipSuccess;
+  codec_rvq_kernel<<<a.F, 256, 0, s>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_check_codes(const int32_t* codes, uint32_t F, uint32_t* err, hipStream_t s) {
+  const size_t n = size_t(10) * F;
+  if (n == 0) return hipSuccess;
+  codec_check_codes_kernel<<<uint32_t((n + 255) / 256), 256, 0, s>>>(codes, F, err);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_rope(float* qkv, uint32_t T, const float2* table, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  codec_rope_kernel<<<T, 256, 0, s>>>(qkv, table);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_attention(const float* qkv, uint32_t T, float* out, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  codec_attn_kernel<<<dim3((T + CA_Q - 1) / CA_Q, 16), 256, 0, s>>>(qkv, T, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_scaled_residual(float* x, const float* p, const float* scale, uint32_t T, uint32_t D,
+                                        hipStream_t s) {
+  const size_t n = size_t(T) * D;
+  if (n == 0) return hipSuccess;
+  codec_scaled_residual_kernel<<<uint32_t((n + 255) / 256), 256, 0, s>>>(x, p, scale, n, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_split16(const float* x, _Float16* hi, _Float16* lo, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  codec_split16_kernel<<<uint32_t((n + 255) / 256), 256, 0, s>>>(x, hi, lo, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_dwconv_ln(const float* x, uint32_t F, const float* w, const float* b, const float* ln_w,
+                                  const float* ln_b, float eps, _Float16* hi, _Float16* lo, hipStream_t s) {
+  if (F == 0) return hipSuccess;
+  codec_dwconv_ln_kernel<<<F, 256, 0, s>>>(x, F, w, b, ln_w, ln_b, eps, hi, lo);
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_out_conv(const _Float16* x, uint32_t T, const float* w, float b, float* out, hipStream_t s) {
+  if (T == 0) return hipSuccess;
+  codec_out_conv_kernel<<<(T + 255) / 256, 256, 0, s>>>(x, T, w, b, out);
+  return hipGetLastError();
+}
+
+}  // namespace s2

@@ -67,6 +67,11 @@ FLAG_KV_F16 = 2
 FLAG_PROFILE = 4
 
 
+class WaveformInfo(ctypes.Structure):
+    _fields_ = [("sample_rate", ctypes.c_uint32), ("input_frames", ctypes.c_uint32),
+                ("latent_frames", ctypes.c_uint32), ("num_samples", ctypes.c_size_t)]
+
+
 class SlowProfile(ctypes.Structure):
     _fields_ = [(n, ctypes.c_double) for n in ("rms_norm_ms", "linear_ms", "gqa_attention_ms", "rope_ms",
                                                "kv_write_ms", "swiglu_ms", "output_head_ms")] + [
@@ -143,6 +148,23 @@ def load():
                  "s2hip_op_running_sums",
                  "s2hip_op_expf", "s2hip_op_embed", "s2hip_reset_slot", "s2hip_eval_slot",
                  "s2hip_transpose_to_time_major", "s2hip_time_kernel"):
+        getattr(L, name).restype = i32
+    L.s2hip_codec_open.argtypes = [cp, u32, i32, cp, sz]
+    L.s2hip_codec_open.restype = vp
+    L.s2hip_codec_close.argtypes = [vp]
+    L.s2hip_codec_close.restype = None
+    L.s2hip_codec_rvq_lookup.argtypes = [vp, vp, u32, u32, vp, cp, sz]
+    L.s2hip_codec_post_module.argtypes = [vp, vp, u32, vp, cp, sz]
+    L.s2hip_codec_upsample.argtypes = [vp, vp, u32, vp, cp, sz]
+    L.s2hip_codec_decode_latents.argtypes = [vp, vp, u32, vp, cp, sz]
+    L.s2hip_codec_decoder.argtypes = [vp, vp, u32, u32, u32, vp, sz, ctypes.POINTER(sz), cp, sz]
+    L.s2hip_codec_decode_waveform.argtypes = [vp, vp, u32, u32, vp, sz, ctypes.POINTER(WaveformInfo), cp, sz]
+    L.s2hip_codec_decode_waveform_device.argtypes = [vp, vp, u32, u32, vp, cp, sz]
+    L.s2hip_codec_time.argtypes = [vp, cp, u32, u32, ctypes.POINTER(ctypes.c_double),
+                                   ctypes.POINTER(ctypes.c_double), cp, sz]
+    for name in ("s2hip_codec_rvq_lookup", "s2hip_codec_post_module", "s2hip_codec_upsample",
+                 "s2hip_codec_decode_latents", "s2hip_codec_decoder", "s2hip_codec_decode_waveform",
+                 "s2hip_codec_decode_waveform_device", "s2hip_codec_time"):
         getattr(L, name).restype = i32
     _lib = L
     return L

@@ -278,6 +278,78 @@ void s2hip_expf_host(const float* x, size_t n, float* y);
 int32_t s2hip_time_kernel(s2hip_engine* engine, const char* kernel, uint32_t reps, double* avg_us,
                           double* bytes_per_launch, char* err, size_t err_cap);
 
+/* ---------------------------------------------------------------------------
+ * RVQ codec decode on the GPU: decode_waveform (crates/fish_s2_infer/src/codec.rs:1690-1714)
+ * = rvq_lookup_codes (:2536-2596) -> forward_codec_post_module (:986-1018) ->
+ * forward_codec_upsample (:2302-2325) -> forward_codec_decoder (:1941-2001),
+ * the pipeline's stage after generate_codes (pipeline.rs:166-199).  Weights come
+ * from the codec GGUF (architecture "fish-speech-codec"; the decode-side
+ * tensors the reference's registry names, codec.rs:58-265, all F16) and stay
+ * in HBM.  Buffers are frame-major f32 on the host: codes codebook-major
+ * [num_codebooks][n_frames]; latents / hidden [n_frames][1024]; the
+ * upsample output [4 n_frames][1024]; samples [n_frames * 2048] (44.1 kHz).
+ * Errors follow the reference's texts (codebook count, negative code,
+ * "embedding index N out of range for vocab_dim V", "codec transformer
+ * requires at least one frame", "decoder expects latent dim 1024, got N").
+ * Unlike the reference, a handle decodes at most max_frames code frames per
+ * call (buffers are sized once at open).
+ * ------------------------------------------------------------------------- */
+typedef struct s2hip_codec s2hip_codec;
+
+/* CodecWaveformResult (codec.rs:1681-1688) without the samples themselves. */
+typedef struct {
+  uint32_t sample_rate; /* 44100 */
+  uint32_t input_frames;
+  uint32_t latent_frames;
+  size_t num_samples;
+} s2hip_waveform_info;
+
+/* CodecF16Weights / CodecPostModuleF16Weights / CodecUpsampleF16Weights /
+ * CodecDecoderF16Weights ::from_gguf (codec.rs:2334-2360, 502-520, 1614-1640);
+ * max_frames: 1..4096 code frames per call. */
+s2hip_codec* s2hip_codec_open(const char* codec_gguf_path, uint32_t max_frames, int32_t device, char* err,
+                              size_t err_cap);
+void s2hip_codec_close(s2hip_codec* codec);
+/* rvq_lookup_codes (codec.rs:2536-2596): latents [n_frames][1024]. */
+int32_t s2hip_codec_rvq_lookup(s2hip_codec* codec, const int32_t* codes, uint32_t num_codebooks, uint32_t n_frames,
+                               float* latents, char* err, size_t err_cap);
+/* forward_codec_post_module (codec.rs:986-1018). */
+int32_t s2hip_codec_post_module(s2hip_codec* codec, const float* latents, uint32_t n_frames, float* hidden,
+                                char* err, size_t err_cap);
+/* forward_codec_upsample (codec.rs:2302-2325): out [4 n_frames][1024]. */
+int32_t s2hip_codec_upsample(s2hip_codec* codec, const float* hidden, uint32_t n_frames, float* out, char* err,
+                             size_t err_cap);
+/* rvq_decode_latents (codec.rs:1282-1297): post-module then upsample. */
+int32_t s2hip_codec_decode_latents(s2hip_codec* codec, const float* latents, uint32_t n_frames, float* out,
+                                   char* err, size_t err_cap);
+/* forward_codec_decoder (codec.rs:1941-2001) over n_frames latent frames:
+ * stop_block >= 5 writes the samples [n_frames * 512]; 0..4 writes the
+ * residual stream after that many decoder blocks (a stage checkpoint,
+ * [n_frames * prod(rates[:stop_block])][channels], rates 8, 8, 4, 2, channels
+ * 1536, 768, 384, 192, 96).  out_len receives the floats written. */
+int32_t s2hip_codec_decoder(s2hip_codec* codec, const float* hidden, uint32_t n_frames, uint32_t hidden_dim,
+                            uint32_t stop_block, float* out, size_t out_cap, size_t* out_len, char* err,
+                            size_t err_cap);
+/* decode_waveform (codec.rs:1690-1714): samples [n_frames * 2048] in [-1, 1]. */
+int32_t s2hip_codec_decode_waveform(s2hip_codec* codec, const int32_t* codes, uint32_t num_codebooks,
+                                    uint32_t n_frames, float* samples, size_t samples_cap, s2hip_waveform_info* info,
+                                    char* err, size_t err_cap);
+/* decode_waveform with codes and samples in device memory of the codec's
+ * device (the pipeline keeps generate_codes' output on the GPU); codes are
+ * range-checked on the device.  No counterpart in the reference. */
+int32_t s2hip_codec_decode_waveform_device(s2hip_codec* codec, const int32_t* codes_dev, uint32_t num_codebooks,
+                                           uint32_t n_frames, float* samples_dev, char* err, size_t err_cap);
+/* Measurement: average device time (HIP events on the codec stream) of
+ * `what` over `reps` launches, after one untimed decode of n_frames frames of
+ * fixed codes: "decode" (the whole decode_waveform on device buffers) or one
+ * convolution of that decode by name ("entry", "b1_convT" .. "b4_convT",
+ * "b<1-4>_r<1-3>_conv0" / "_conv1", "up1_convT", "up1_pw1", "up1_pw2",
+ * "up2_..."), relaunched with the same arguments.  flops receives 2 x the
+ * multiply-adds of one launch (for "decode": of all its convolutions).
+ * No counterpart in the reference (a measurement hook). */
+int32_t s2hip_codec_time(s2hip_codec* codec, const char* what, uint32_t n_frames, uint32_t reps, double* avg_us,
+                         double* flops, char* err, size_t err_cap);
+
 #ifdef __cplusplus
 }
 #endif
