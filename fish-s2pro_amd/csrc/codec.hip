@@ -21,6 +21,7 @@
 
 #include "codec.h"
 #include "expf_glibc.h"
+#include "sin_cw.h"
 
 namespace s2 {
 namespace {
@@ -59,12 +60,8 @@ __device__ __forceinline__ float erf_as(float value) {
 __device__ __forceinline__ float gelu_as(float v) {
   return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, erf_as(__fmul_rn(v, 0.70710677f))));
 }
-// snake_activation_frame_major (codec.rs:2162-2186)
-__device__ __forceinline__ float snake(float x, float alpha) {
-  const float a = fabsf(alpha) < 1e-8f ? 1e-8f : alpha;
-  const float s = sinf(__fmul_rn(a, x));
-  return __fadd_rn(x, __fdiv_rn(__fmul_rn(s, s), a));
-}
+// snake_activation_frame_major (codec.rs:2162-2186), sin^2 from sin_cw.h
+__device__ __forceinline__ float snake(float x, float alpha) { return snake_cw(x, alpha); }
 
 template <int MC, int KC, int PL>
 __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint32_t m_tiles, uint32_t f_tiles,
@@ -212,7 +209,8 @@ __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint3
           rv[v] = f < a.F ? a.res[(size_t(f) * a.ostride + phase) * a.ldres + m] : 0.0f;
         }
       }
-#pragma unroll
+      // not unrolled: 2 x MC x 16 inlined snake evaluations in one block spill
+#pragma nounroll
       for (int v = 0; v < 16; ++v) {
         const uint32_t f = fb + 8u * uint32_t(v >> 2) + uint32_t(v & 3);
         if (f >= a.F) continue;
@@ -285,65 +283,91 @@ __global__ __launch_bounds__(256) void codec_rope_kernel(float* qkv, const float
 
 // Windowed causal attention of the post-module transformer
 // (forward_codec_transformer_layer_with_window, codec.rs:3278-3300, over
-// gqa_decode_attention, attention.rs:208-247): block = 64 queries x one head;
-// the keys and values the block's queries see ([q0 - 127, q0 + 63]) sit in
-// LDS.  A wave takes 16 queries: lane j scores keys j and j + 64 of the
-// query's window, softmax over the wave, then lane d sums p_k v_k[d].
-constexpr uint32_t CA_Q = 64, CA_W = 128, CA_K = CA_Q + CA_W - 1;
+// gqa_decode_attention, attention.rs:208-247): block = 16 queries x one head,
+// the 143 keys / values those queries see ([q0 - 127, q0 + 15]) staged in LDS
+// (key rows padded to 68 floats: 16-byte aligned, and a 16-lane phase of
+// float4 reads covers all 64 banks).  A wave takes 4 queries: lane j scores
+// keys j and j + 64 of the query's window (four partial sums per dot
+// product), softmax over the wave, the probabilities go through wave-private
+// LDS, and lane d sums p_k v_k[d] (four partial sums).
+constexpr uint32_t CA_Q = 16, CA_W = 128, CA_K = CA_Q + CA_W - 1, CA_KS = 68;
 __global__ __launch_bounds__(256) void codec_attn_kernel(const float* qkv, uint32_t T, float* out) {
-  __shared__ float ks[CA_K][65];
-  __shared__ float vs[CA_K][64];
-  __shared__ float qs[CA_Q][64];
+  __shared__ __align__(16) float ks[CA_K * CA_KS];
+  __shared__ __align__(16) float vs[CA_K * 64];
+  __shared__ __align__(16) float qs[CA_Q * 64];
+  __shared__ __align__(16) float ps[4][128];
   const uint32_t q0 = blockIdx.x * CA_Q, h = blockIdx.y, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t kstart = q0 >= CA_W - 1 ? q0 - (CA_W - 1) : 0u;
   const uint32_t kend = min(T, q0 + CA_Q);
   const uint32_t nk = kend - kstart;
-  for (uint32_t e = tid; e < nk * 64u; e += 256u) {
-    const uint32_t r = e >> 6, d = e & 63u;
-    const float* src = qkv + size_t(kstart + r) * 3072u + h * 64u + d;
-    ks[r][d] = src[1024];
-    vs[r][d] = src[2048];
+  for (uint32_t e = tid; e < nk * 16u; e += 256u) {
+    const uint32_t r = e >> 4, d4 = (e & 15u) * 4u;
+    const float* src = qkv + size_t(kstart + r) * 3072u + h * 64u + d4;
+    *reinterpret_cast<float4*>(ks + r * CA_KS + d4) = *reinterpret_cast<const float4*>(src + 1024);
+    *reinterpret_cast<float4*>(vs + r * 64u + d4) = *reinterpret_cast<const float4*>(src + 2048);
   }
-  for (uint32_t e = tid; e < CA_Q * 64u; e += 256u) {
-    const uint32_t r = e >> 6, d = e & 63u;
-    qs[r][d] = q0 + r < T ? qkv[size_t(q0 + r) * 3072u + h * 64u + d] : 0.0f;
+  {
+    const uint32_t r = tid >> 4, d4 = (tid & 15u) * 4u;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (q0 + r < T) v = *reinterpret_cast<const float4*>(qkv + size_t(q0 + r) * 3072u + h * 64u + d4);
+    *reinterpret_cast<float4*>(qs + r * 64u + d4) = v;
   }
   __syncthreads();
-  for (uint32_t qq = 0; qq < 16; ++qq) {
-    const uint32_t ql = wave * 16u + qq, tq = q0 + ql;
+  float* pw = ps[wave];
+  for (uint32_t qq = 0; qq < 4; ++qq) {
+    const uint32_t ql = wave * 4u + qq, tq = q0 + ql;
     if (tq >= T) break;
     const uint32_t lo = tq >= CA_W - 1 ? tq - (CA_W - 1) : 0u, n = tq - lo + 1u;
-    float s0 = -INFINITY, s1 = -INFINITY;
-    if (lane < n) {
-      const float* kr = ks[lo + lane - kstart];
-      float d = 0.0f;
-#pragma unroll 16
-      for (int i = 0; i < 64; ++i) d = fmaf(qs[ql][i], kr[i], d);
-      s0 = d * 0.125f;
+    const float* qr = qs + ql * 64u;
+    float sc[2];
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const uint32_t j = lane + 64u * uint32_t(h2);
+      sc[h2] = -INFINITY;
+      if (j < n) {
+        const float* kr = ks + (lo + j - kstart) * CA_KS;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 64; i += 4) {
+          const float4 qv = *reinterpret_cast<const float4*>(qr + i);
+          const float4 kv = *reinterpret_cast<const float4*>(kr + i);
+          a0 = fmaf(qv.x, kv.x, a0);
+          a1 = fmaf(qv.y, kv.y, a1);
+          a2 = fmaf(qv.z, kv.z, a2);
+          a3 = fmaf(qv.w, kv.w, a3);
+        }
+        sc[h2] = ((a0 + a1) + (a2 + a3)) * 0.125f;
+      }
     }
-    if (lane + 64u < n) {
-      const float* kr = ks[lo + lane + 64u - kstart];
-      float d = 0.0f;
-#pragma unroll 16
-      for (int i = 0; i < 64; ++i) d = fmaf(qs[ql][i], kr[i], d);
-      s1 = d * 0.125f;
-    }
-    float mx = fmaxf(s0, s1);
+    float mx = fmaxf(sc[0], sc[1]);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    const float e0 = lane < n ? expf_glibc(s0 - mx) : 0.0f;
-    const float e1 = lane + 64u < n ? expf_glibc(s1 - mx) : 0.0f;
+    const float e0 = lane < n ? expf_glibc(sc[0] - mx) : 0.0f;
+    const float e1 = lane + 64u < n ? expf_glibc(sc[1] - mx) : 0.0f;
     float sum = e0 + e1;
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
-    const float p0 = e0 / sum, p1 = e1 / sum;
-    float o = 0.0f;
-    const uint32_t base = lo - kstart;
-    for (uint32_t k = 0; k < n; ++k) {
-      const float pk = __shfl(k < 64u ? p0 : p1, int(k & 63u), 64);
-      o = fmaf(pk, vs[base + k][lane], o);
+    const float inv = 1.0f / sum;
+    pw[lane] = e0 * inv;
+    pw[lane + 64u] = e1 * inv;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* vb = vs + (lo - kstart) * 64u + lane;
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;
+    uint32_t k = 0;
+    for (; k + 4u <= n; k += 4u) {
+      const float4 p4 = *reinterpret_cast<const float4*>(pw + k);
+      o0 = fmaf(p4.x, vb[(k + 0u) * 64u], o0);
+      o1 = fmaf(p4.y, vb[(k + 1u) * 64u], o1);
+      o2 = fmaf(p4.z, vb[(k + 2u) * 64u], o2);
+      o3 = fmaf(p4.w, vb[(k + 3u) * 64u], o3);
     }
-    out[size_t(tq) * 1024u + h * 64u + lane] = o;
+    for (; k < n; ++k) o0 = fmaf(pw[k], vb[k * 64u], o0);
+    out[size_t(tq) * 1024u + h * 64u + lane] = (o0 + o1) + (o2 + o3);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 

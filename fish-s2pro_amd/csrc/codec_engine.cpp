@@ -21,6 +21,7 @@
 
 #include "codec.h"
 #include "gguf.h"
+#include "sin_cw.h"
 #include "kernels.h"
 #include "s2hip.h"
 
@@ -778,6 +779,10 @@ int32_t s2hip_codec_decode_waveform(s2hip_codec* codec, const int32_t* codes, ui
 int32_t s2hip_codec_decode_waveform_device(s2hip_codec* codec, const int32_t* codes_dev, uint32_t num_codebooks,
                                            uint32_t n_frames, float* samples_dev, char* err, size_t err_cap) {
   CODEC_CALL(codec->eng->decode_waveform_device(codes_dev, num_codebooks, n_frames, samples_dev))
+}
+
+void s2hip_codec_snake_host(const float* x, size_t n, const float* alpha, float* y) {
+  for (size_t i = 0; i < n; ++i) y[i] = s2::snake_cw(x[i], alpha[i]);
 }
 
 int32_t s2hip_codec_time(s2hip_codec* codec, const char* what, uint32_t n_frames, uint32_t reps, double* avg_us,

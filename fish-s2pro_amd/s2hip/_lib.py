@@ -160,6 +160,8 @@ def load():
     L.s2hip_codec_decoder.argtypes = [vp, vp, u32, u32, u32, vp, sz, ctypes.POINTER(sz), cp, sz]
     L.s2hip_codec_decode_waveform.argtypes = [vp, vp, u32, u32, vp, sz, ctypes.POINTER(WaveformInfo), cp, sz]
     L.s2hip_codec_decode_waveform_device.argtypes = [vp, vp, u32, u32, vp, cp, sz]
+    L.s2hip_codec_snake_host.argtypes = [vp, sz, vp, vp]
+    L.s2hip_codec_snake_host.restype = None
     L.s2hip_codec_time.argtypes = [vp, cp, u32, u32, ctypes.POINTER(ctypes.c_double),
                                    ctypes.POINTER(ctypes.c_double), cp, sz]
     for name in ("s2hip_codec_rvq_lookup", "s2hip_codec_post_module", "s2hip_codec_upsample",

@@ -339,6 +339,11 @@ int32_t s2hip_codec_decode_waveform(s2hip_codec* codec, const int32_t* codes, ui
  * range-checked on the device.  No counterpart in the reference. */
 int32_t s2hip_codec_decode_waveform_device(s2hip_codec* codec, const int32_t* codes_dev, uint32_t num_codebooks,
                                            uint32_t n_frames, float* samples_dev, char* err, size_t err_cap);
+/* The snake activation of the codec's device kernels, x + sin(a x)^2 / a with
+ * the reference's guard (snake_activation_frame_major, codec.rs:2162-2186),
+ * evaluated on the host by the same routine: y[i] = snake(x[i], alpha[i]).
+ * A test hook (its sin is not the C library's sinf). */
+void s2hip_codec_snake_host(const float* x, size_t n, const float* alpha, float* y);
 /* Measurement: average device time (HIP events on the codec stream) of
  * `what` over `reps` launches, after one untimed decode of n_frames frames of
  * fixed codes: "decode" (the whole decode_waveform on device buffers) or one

@@ -177,3 +177,23 @@ def test_transpose_to_time_major_matches_reference_kat_and_oracle():
     with pytest.raises(S2HipError, match="does not fit i32"):
         transpose_to_time_major([1, 2 ** 31], 1, 2)
     assert transpose_to_time_major([], 3, 0).size == 0
+
+
+def test_codec_snake_routine_matches_glibc_snake():
+    """The device snake (sin^2 by Cody-Waite reduction + minimax polynomials,
+    csrc/sin_cw.h), built for the host, against the oracle's snake (glibc
+    sinf, snake_activation_frame_major codec.rs:2162-2186): mostly the same
+    bits, never more than 4 ulp of the larger of x and sin^2(a x) / a."""
+    L = _lib.load()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([np.linspace(-1024, 1024, 400_001), rng.standard_normal(200_000) * 30]).astype(np.float32)
+    a = np.where(rng.random(x.size) < 0.5, rng.uniform(0.5, 1.5, x.size), rng.uniform(-2, 2, x.size)).astype(np.float32)
+    a[::97] = 0.0  # the |a| < 1e-8 guard
+    y = np.empty_like(x)
+    L.s2hip_codec_snake_host(x.ctypes.data, x.size, a.ctypes.data, y.ctypes.data)
+    ref = O.codec_snake(x.reshape(1, -1), a).reshape(-1)
+    ae = np.where(np.abs(a) < 1e-8, 1e-8, a).astype(np.float64)
+    scale = np.maximum(np.abs(x), np.sin(ae * x) ** 2 / np.abs(ae)).astype(np.float32)
+    err = np.abs(y.astype(np.float64) - ref) / np.spacing(scale)
+    assert np.max(err) <= 4.0, np.max(err)
+    assert np.mean(y == ref) > 0.98
