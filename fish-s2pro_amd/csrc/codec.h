@@ -42,6 +42,12 @@ struct ConvGemmArgs {
   _Float16* yh;
   _Float16* yl;
   uint32_t ldh;
+  // K split (nullable): when a launch would leave CUs idle, splits of the
+  // input-channel stages write partial sums to part ([split][row][M] f32,
+  // part_cap floats) and a reduce kernel adds them in split order and
+  // applies the epilogue
+  float* part;
+  size_t part_cap;
 };
 
 // Tile geometry of a packed weight: TM = 32 * mc output channels per tile,

@@ -80,7 +80,8 @@ __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint3
   const uint32_t AR = CG_TF + halo;
   const uint32_t a_chunks = PL * AR * CH, w_chunks = a.G * TM * CH, tot = a_chunks + w_chunks;
   const uint32_t buf_halfs = (PL * AR + a.G * TM) * KC;
-  const uint32_t nst = a.C / KC;
+  const uint32_t nst_all = a.C / KC, splits = gridDim.z, sp = blockIdx.z;
+  const uint32_t st_begin = nst_all * sp / splits, nst = nst_all * (sp + 1) / splits - st_begin;
   const _Float16* wsrc = a.w + (size_t(phase) * m_tiles + mt) * (size_t(a.G) * TM * a.C);
   const int32_t row0 = int32_t(f0) + wbase;
 
@@ -122,10 +123,10 @@ __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint3
       const uint32_t kind = loff[i] >> 30;
       uint4 v = make_uint4(0u, 0u, 0u, 0u);
       if (kind == 2u) {
-        v = *reinterpret_cast<const uint4*>(wsrc + size_t(st) * wstage + goff[i]);
+        v = *reinterpret_cast<const uint4*>(wsrc + size_t(st_begin + st) * wstage + goff[i]);
       } else if (kind < 2u) {
         const _Float16* base = kind ? a.xl : a.xh;
-        v = *reinterpret_cast<const uint4*>(base + size_t(goff[i]) + st * KC);
+        v = *reinterpret_cast<const uint4*>(base + size_t(goff[i]) + (st_begin + st) * KC);
       }
       stg[i] = v;
     }
@@ -188,6 +189,24 @@ __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint3
     if (st + 2 < nst) load(st + 2);
   }
 
+  if (splits > 1) {  // partial sums; conv_split_reduce_kernel finishes
+    const size_t rows = size_t(a.F) * a.ostride;
+#pragma unroll
+    for (int j = 0; j < MC; ++j) {
+      const uint32_t m = mt * TM + uint32_t(j) * 32u + (lane & 31u);
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t fb = f0 + wave * 64u + uint32_t(i) * 32u + 4u * (lane >> 5);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t f = fb + 8u * uint32_t(v >> 2) + uint32_t(v & 3);
+          if (f < a.F) a.part[(size_t(sp) * rows + size_t(f) * a.ostride + phase) * a.M + m] = acc[i][j][v];
+        }
+      }
+    }
+    return;
+  }
   // epilogue: acc[i][j][v] = D[frame 8 (v/4) + 4 (lane/32) + v%4][channel lane%32].
   // The residual values of a fragment are loaded together before its stores
   // (res may be the output buffer itself, so loads cannot move past stores).
@@ -228,6 +247,29 @@ __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint3
         }
       }
     }
+  }
+}
+
+// Sum of the K splits (in split order) and the conv epilogue, one thread per
+// output element (row, m), rows = F * ostride.
+__global__ __launch_bounds__(256) void conv_split_reduce_kernel(ConvGemmArgs a, uint32_t splits) {
+  const size_t rows = size_t(a.F) * a.ostride;
+  const size_t idx = size_t(blockIdx.x) * 256u + threadIdx.x;
+  if (idx >= rows * a.M) return;
+  const size_t row = idx / a.M;
+  const uint32_t m = uint32_t(idx - row * a.M);
+  float acc = a.part[idx];
+  for (uint32_t z = 1; z < splits; ++z) acc = __fadd_rn(acc, a.part[size_t(z) * rows * a.M + idx]);
+  float val = __fadd_rn(acc, a.bias[m]);
+  if (a.gelu) val = gelu_as(val);
+  if (a.gamma) val = __fmul_rn(val, a.gamma[m]);
+  if (a.res) val = __fadd_rn(a.res[row * a.ldres + m], val);
+  if (a.y32) a.y32[row * a.ldy + m] = val;
+  if (a.alpha) val = snake(val, a.alpha[m]);
+  if (a.yh) {
+    const _Float16 h = _Float16(val);
+    a.yh[row * a.ldh + m] = h;
+    if (a.yl) a.yl[row * a.ldh + m] = _Float16(__fsub_rn(val, float(h)));
   }
 }
 
@@ -497,8 +539,21 @@ hipError_t conv_gemm_launch(const ConvGemmArgs& a, uint32_t phases, hipStream_t 
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  conv_gemm_kernel<MC, KC, PL><<<dim3(m_tiles * f_tiles, phases), 256, lds, s>>>(
+  // K split when the grid would leave CUs idle: each split keeps >= 4 stages
+  const uint32_t nst = a.C / KC, blocks = m_tiles * f_tiles * phases;
+  const size_t rows = size_t(a.F) * phases;
+  uint32_t splits = 1;
+  if (a.part) {
+    while (splits < 8 && blocks * splits < 256u && nst / (2 * splits) >= 4 &&
+           size_t(2 * splits) * rows * a.M <= a.part_cap)
+      splits *= 2;
+  }
+  conv_gemm_kernel<MC, KC, PL><<<dim3(m_tiles * f_tiles, phases, splits), 256, lds, s>>>(
       a, m_tiles, f_tiles, halo, wbase, a.off0 - wbase, a.ostep);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || splits == 1) return e;
+  const size_t n = rows * a.M;
+  conv_split_reduce_kernel<<<uint32_t((n + 255) / 256), 256, 0, s>>>(a, splits);
   return hipGetLastError();
 }
 

@@ -413,6 +413,8 @@ class CodecEngine {
     dh_ = dalloc<_Float16>(big);
     dl_ = dalloc<_Float16>(big);
     samples_ = dalloc<float>(F * SAMPLES_PER_FRAME);
+    cpart_cap_ = F * 32768;  // K-split partial sums of the short-grid products
+    cpart_ = dalloc<float>(cpart_cap_);
   }
 
   void check_frames(uint32_t n) {
@@ -510,6 +512,8 @@ class CodecEngine {
     a.M = w.M;
     a.ostride = w.phases;
     a.bias = w.bias;
+    a.part = cpart_;
+    a.part_cap = cpart_cap_;
     return a;
   }
   void run(const ConvGemmArgs& a, const ConvW& w, const char* name) {
@@ -690,6 +694,8 @@ class CodecEngine {
   float* x32_ = nullptr;
   _Float16 *a16_ = nullptr, *b16_ = nullptr, *dh_ = nullptr, *dl_ = nullptr;
   float* samples_ = nullptr;
+  float* cpart_ = nullptr;
+  size_t cpart_cap_ = 0;
 };
 
 void copy_err(const std::exception& e, char* err, size_t cap) {
