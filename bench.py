@@ -146,7 +146,8 @@ def cpu_baseline(path, shape, threads, prompt_len, frames):
 CODEC_FRAMES = 512
 MFMA_F16_PEAK_TFLOPS = 2500.0
 CODEC_CONVS = (["entry"] + [f"b{b}_convT" for b in range(1, 5)] +
-               [f"b{b}_r{r}_conv{k}" for b in range(1, 5) for r in range(1, 4) for k in (0, 1)] +
+               [f"b{b}_r{r}_conv{k}" for b in range(1, 4) for r in range(1, 4) for k in (0, 1)] +
+               [f"b4_r{r}_unit" for r in range(1, 4)] +  # 96 channels: k7 + snake + k1 in one launch
                [f"up{s}_{x}" for s in (1, 2) for x in ("convT", "pw1", "pw2")])
 
 

@@ -48,6 +48,13 @@ struct ConvGemmArgs {
   // applies the epilogue
   float* part;
   size_t part_cap;
+  // Fused residual unit (M <= 128, one m tile): the product above is the unit's
+  // k7 conv; Y = f16(snake(acc + bias_mid, alpha_mid)) goes to LDS and acc =
+  // Y . W1 (the unit's k1 conv, w1 packed like any k1 conv of M channels)
+  // before the epilogue, which then uses bias (the k1 conv's) onwards.
+  const _Float16* w1;
+  const float* bias_mid;
+  const float* alpha_mid;
 };
 
 // Tile geometry of a packed weight: TM = 32 * mc output channels per tile,
@@ -75,6 +82,9 @@ void pack_conv_weights(uint16_t* dst, uint32_t phases, uint32_t M, uint32_t G, u
             }
 }
 hipError_t launch_conv_gemm(const ConvGemmArgs& a, uint32_t phases, ConvTile t, hipStream_t s);
+// The residual unit's k7 conv + snake + k1 conv in one launch (a.w1 set; M a
+// multiple of 32, at most 128; tile t of the k7 conv).
+hipError_t launch_residual_unit(const ConvGemmArgs& a, ConvTile t, hipStream_t s);
 
 // rvq_lookup_codes: latents[f][o] = sum over codebooks q (in order) of
 // (codebook_q[code] . proj_w_q[o] + proj_b_q[o]); codes codebook-major

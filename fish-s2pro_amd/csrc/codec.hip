@@ -19,6 +19,8 @@
 // attention of the post-module transformer, depthwise conv + LayerNorm, the
 // output conv + tanh.
 
+#include <algorithm>
+
 #include "codec.h"
 #include "expf_glibc.h"
 #include "sin_cw.h"
@@ -63,7 +65,7 @@ __device__ __forceinline__ float gelu_as(float v) {
 // snake_activation_frame_major (codec.rs:2162-2186), sin^2 from sin_cw.h
 __device__ __forceinline__ float snake(float x, float alpha) { return snake_cw(x, alpha); }
 
-template <int MC, int KC, int PL>
+template <int MC, int KC, int PL, bool FU = false>
 __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint32_t m_tiles, uint32_t f_tiles,
                                                            uint32_t halo, int32_t wbase, int32_t toff0,
                                                            int32_t tstep) {
@@ -187,6 +189,56 @@ __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint3
     if (st + 1 < nst) store((st + 1) & 1u);
     __syncthreads();
     if (st + 2 < nst) load(st + 2);
+  }
+
+  if constexpr (FU) {
+    // The residual unit's k1 conv on the tile just computed (all M channels):
+    // Y = f16(snake(acc + bias_mid, alpha_mid)) in LDS ([256 frames][TM + 8]
+    // halfs: 16 consecutive rows fall on distinct 16-byte bank groups), the
+    // k1 weights W1 ([TM / 32 stages][TM rows][32], swizzled like W) next to
+    // it; every wave left the stage buffers at the loop's last barrier.
+    constexpr uint32_t YS = TM + 8;
+    _Float16* Y = cg_lds;
+    _Float16* W1 = cg_lds + CG_TF * YS;
+    for (uint32_t q = tid; q < TM * TM / 8u; q += 256u) {
+      const uint32_t st = q / (TM * 4u), rem = q - st * (TM * 4u), row = rem >> 2, c = rem & 3u;
+      *reinterpret_cast<uint4*>(W1 + st * (TM * 32u) + row * 32u + ((c ^ swz_w<4>(row)) << 3)) =
+          *reinterpret_cast<const uint4*>(a.w1 + size_t(q) * 8u);
+    }
+#pragma unroll
+    for (int j = 0; j < MC; ++j) {
+      const uint32_t m = uint32_t(j) * 32u + (lane & 31u);
+      const float bm = m < a.M ? a.bias_mid[m] : 0.0f;
+      const float am = m < a.M ? a.alpha_mid[m] : 1.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t fl = wave * 64u + uint32_t(i) * 32u + 4u * (lane >> 5);
+#pragma nounroll
+        for (int v = 0; v < 16; ++v) {
+          const float val = snake(__fadd_rn(acc[i][j][v], bm), am);
+          Y[(fl + 8u * uint32_t(v >> 2) + uint32_t(v & 3)) * YS + m] = _Float16(val);
+          acc[i][j][v] = 0.0f;
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t kk = 0; kk < TM / 16u; ++kk) {
+      const uint32_t c = kk * 2u + (lane >> 5);                  // chunk of the Y row
+      const uint32_t st = kk >> 1, cs = (kk & 1u) * 2u + (lane >> 5);  // W1 stage, chunk in it
+      half8 bf[MC];
+#pragma unroll
+      for (int j = 0; j < MC; ++j) {
+        const uint32_t row = uint32_t(j) * 32u + (lane & 31u);
+        bf[j] = *reinterpret_cast<const half8*>(W1 + st * (TM * 32u) + row * 32u + ((cs ^ swz_w<4>(row)) << 3));
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const half8 af = *reinterpret_cast<const half8*>(Y + (wave * 64u + uint32_t(i) * 32u + (lane & 31u)) * YS + c * 8u);
+#pragma unroll
+        for (int j = 0; j < MC; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[j], acc[i][j], 0, 0, 0);
+      }
+    }
   }
 
   if (splits > 1) {  // partial sums; conv_split_reduce_kernel finishes
@@ -521,7 +573,7 @@ __global__ __launch_bounds__(256) void codec_out_conv_kernel(const _Float16* x, 
   out[t] = tanhf(y);
 }
 
-template <int MC, int KC, int PL>
+template <int MC, int KC, int PL, bool FU = false>
 hipError_t conv_gemm_launch(const ConvGemmArgs& a, uint32_t phases, hipStream_t s) {
   constexpr uint32_t TM = 32 * MC, CH = KC / 8;
   const int32_t last = a.off0 + int32_t(a.G - 1) * a.ostep;
@@ -529,12 +581,13 @@ hipError_t conv_gemm_launch(const ConvGemmArgs& a, uint32_t phases, hipStream_t 
   const uint32_t halo = uint32_t((a.off0 < last ? last : a.off0) - wbase);
   const uint32_t AR = CG_TF + halo;
   if (size_t(PL) * AR * CH + size_t(a.G) * TM * CH > 256u * CG_MAXLD) return hipErrorInvalidValue;
-  const size_t lds = 2u * (size_t(PL) * AR + size_t(a.G) * TM) * KC * sizeof(_Float16);
+  size_t lds = 2u * (size_t(PL) * AR + size_t(a.G) * TM) * KC * sizeof(_Float16);
+  if (FU) lds = std::max(lds, (size_t(CG_TF) * (TM + 8) + size_t(TM) * TM) * sizeof(_Float16));
   if (lds > 160u * 1024u) return hipErrorInvalidValue;
   const uint32_t m_tiles = (a.M + TM - 1) / TM, f_tiles = (a.F + CG_TF - 1) / CG_TF;
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm_kernel<MC, KC, PL>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_gemm_kernel<MC, KC, PL, FU>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
@@ -543,12 +596,12 @@ hipError_t conv_gemm_launch(const ConvGemmArgs& a, uint32_t phases, hipStream_t 
   const uint32_t nst = a.C / KC, blocks = m_tiles * f_tiles * phases;
   const size_t rows = size_t(a.F) * phases;
   uint32_t splits = 1;
-  if (a.part) {
+  if (a.part && !FU) {
     while (splits < 8 && blocks * splits < 256u && nst / (2 * splits) >= 4 &&
            size_t(2 * splits) * rows * a.M <= a.part_cap)
       splits *= 2;
   }
-  conv_gemm_kernel<MC, KC, PL><<<dim3(m_tiles * f_tiles, phases, splits), 256, lds, s>>>(
+  conv_gemm_kernel<MC, KC, PL, FU><<<dim3(m_tiles * f_tiles, phases, splits), 256, lds, s>>>(
       a, m_tiles, f_tiles, halo, wbase, a.off0 - wbase, a.ostep);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
@@ -580,6 +633,15 @@ hipError_t launch_conv_gemm(const ConvGemmArgs& a, uint32_t phases, ConvTile t, 
   if (t.mc == 4 && t.kc == 32) return split ? conv_gemm_launch<4, 32, 2>(a, phases, s) : conv_gemm_launch<4, 32, 1>(a, phases, s);
   if (t.mc == 3 && t.kc == 16) return split ? conv_gemm_launch<3, 16, 2>(a, phases, s) : conv_gemm_launch<3, 16, 1>(a, phases, s);
   if (t.mc == 3 && t.kc == 32) return split ? conv_gemm_launch<3, 32, 2>(a, phases, s) : conv_gemm_launch<3, 32, 1>(a, phases, s);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_residual_unit(const ConvGemmArgs& a, ConvTile t, hipStream_t s) {
+  if (!a.w1 || !a.bias_mid || !a.alpha_mid || a.M % 32u || a.M > 32u * t.mc || t.kc != 16 || a.xl ||
+      a.C != a.M || a.ldx % 8u)
+    return hipErrorInvalidValue;
+  if (t.mc == 3) return conv_gemm_launch<3, 16, 1, true>(a, 1, s);
+  if (t.mc == 4) return conv_gemm_launch<4, 16, 1, true>(a, 1, s);
   return hipErrorInvalidValue;
 }
 

@@ -193,7 +193,9 @@ class CodecEngine {
     CHK(hipEventCreate(&e0));
     CHK(hipEventCreate(&e1));
     auto launch = [&] {
-      if (one)
+      if (one && one->phases == 0)
+        CHK(launch_residual_unit(one->a, one->tile, stream_));
+      else if (one)
         CHK(launch_conv_gemm(one->a, one->phases, one->tile, stream_));
       else
         waveform(n, nullptr, samples_);
@@ -529,6 +531,7 @@ class CodecEngine {
     uint32_t phases;
     ConvTile tile;
     double flops;  // 2 x multiply-adds of the convolution (the reference's arithmetic)
+    // phases 0: a fused residual unit (launch_residual_unit)
   };
   bool recording_ = false;
   std::vector<Rec> rec_;
@@ -575,6 +578,30 @@ class CodecEngine {
     return upx_;
   }
 
+  // outputs of a residual unit's k1 conv: the updated residual stream (kept
+  // when another unit of the block or a checkpoint reads it) and the snake of
+  // whatever comes next, as f16 or hi / lo planes
+  void set_unit_outputs(ConvGemmArgs& c, const Block& B, uint32_t b, uint32_t r, uint32_t co, bool stop_here) {
+    if (r < 2 || stop_here) {
+      c.y32 = x32_;
+      c.ldy = co;
+    }
+    c.ldh = co;
+    if (r < 2) {  // the next residual unit's conv0 input
+      c.alpha = B.res[r + 1].a0;
+      c.yh = a16_;
+    } else if (!stop_here) {
+      if (b < 3) {  // the next block's conv_transpose input
+        c.alpha = blocks_[b + 1].alpha;
+        c.yh = dh_;
+        c.yl = dl_;
+      } else {  // the output conv's input
+        c.alpha = tail_alpha_;
+        c.yh = a16_;
+      }
+    }
+  }
+
   static size_t decoder_out_elems(uint32_t frames, uint32_t stop_block) {
     if (stop_block >= 5) return size_t(frames) * 512;
     size_t f = frames;
@@ -599,6 +626,7 @@ class CodecEngine {
     run(e, entry_, "entry");
     if (stop_block == 0) return x32_;
     uint32_t F = frames;
+    const _Float16* out_in = a16_;  // the output conv's input (snake of the last residual stream)
     for (uint32_t b = 0; b < 4; ++b) {
       const Block& B = blocks_[b];
       const uint32_t co = CHS[b + 1];
@@ -616,6 +644,32 @@ class CodecEngine {
       const bool stop_here = stop_block == b + 1;
       for (uint32_t r = 0; r < 3; ++r) {
         const Res& R = B.res[r];
+        const bool fused = co % 32u == 0 && co <= 32u * R.c0.tile.mc && R.c1.tile.mc == R.c0.tile.mc;
+        if (fused) {  // k7 conv + snake + k1 conv in one launch (the block holds every channel)
+          // the k7 conv reads other tiles' rows (its halo), so the unit's f16
+          // output goes to the other buffer: units read a16, b16, a16 and
+          // write b16, a16, b16
+          _Float16* uin = (r & 1u) ? b16_ : a16_;
+          _Float16* uout = (r & 1u) ? a16_ : b16_;
+          ConvGemmArgs u = cargs(R.c0, uin, nullptr, F);
+          u.off0 = -6 * int32_t(dil[r]);
+          u.ostep = int32_t(dil[r]);
+          u.part = nullptr;
+          u.w1 = R.c1.w;
+          u.bias_mid = R.c0.bias;
+          u.alpha_mid = R.a1;
+          u.bias = R.c1.bias;
+          u.res = x32_;
+          u.ldres = co;
+          set_unit_outputs(u, B, b, r, co, stop_here);
+          if (u.yh == a16_) u.yh = uout;  // dh_ / dl_ outputs are separate buffers already
+          if (r == 2 && b == 3) out_in = uout;
+          CHK(launch_residual_unit(u, R.c0.tile, stream_));
+          if (recording_)
+            rec_.push_back(Rec{names_[b][1 + 2 * r].substr(0, 5) + "_unit", u, 0, R.c0.tile,
+                               2.0 * double(F) * co * (7.0 * co + co)});
+          continue;
+        }
         ConvGemmArgs c0 = cargs(R.c0, a16_, nullptr, F);
         c0.off0 = -6 * int32_t(dil[r]);
         c0.ostep = int32_t(dil[r]);
@@ -628,30 +682,13 @@ class CodecEngine {
         c1.ostep = 1;
         c1.res = x32_;
         c1.ldres = co;
-        if (r < 2 || stop_here) {
-          c1.y32 = x32_;
-          c1.ldy = co;
-        }
-        c1.ldh = co;
-        if (r < 2) {  // the next residual unit's conv0 input
-          c1.alpha = B.res[r + 1].a0;
-          c1.yh = a16_;
-        } else if (!stop_here) {
-          if (b < 3) {  // the next block's conv_transpose input
-            c1.alpha = blocks_[b + 1].alpha;
-            c1.yh = dh_;
-            c1.yl = dl_;
-          } else {  // the output conv's input
-            c1.alpha = tail_alpha_;
-            c1.yh = a16_;
-          }
-        }
+        set_unit_outputs(c1, B, b, r, co, stop_here);
         run(c1, R.c1, names_[b][2 + 2 * r].c_str());
       }
       if (stop_here) return x32_;
     }
     float* out = samples_out ? samples_out : samples_;
-    CHK(launch_codec_out_conv(a16_, F, out_w_, out_b_, out, stream_));
+    CHK(launch_codec_out_conv(out_in, F, out_w_, out_b_, out, stream_));
     return out;
   }
 
