@@ -15,6 +15,12 @@ and so does `s2hip.parity`, its restatement here:
   (fish_s2_slow_ar_dump.rs:9-74,110-226): every intermediate of a block of
   Slow-AR layers (forward_slow_ar_block_prefill_layers, slow_ar.rs:980-1039)
   over the tool's fixed hidden inputs, computed with the op-level kernels.
+* codec stages over a GeneratedCodesDump, computed by the GPU codec
+  (`s2hip.Codec`): `rvq_lookup_dump` RvqLookupDump
+  (fish_s2_rvq_lookup_dump.rs:16-27), `post_module_dump` PostModuleDump
+  (fish_s2_post_module_dump.rs:17-28), `decode_stage_dump` DecodeStageDump
+  (fish_s2_decode_stage_dump.rs:19-31, rvq_decode_latents' output) and
+  `waveform_dump` WaveformDump (fish_s2_waveform_dump.rs:19-31).
 
 The reference's tools build the prompt from text with tokenizer.json; here
 the caller passes the prompt as time-major token ids and `text` is carried
@@ -59,6 +65,20 @@ def tensor_stats(values) -> dict:
         "mean_abs": f32_json(mean_abs),
         "max_abs": f32_json(max_abs),
         "first8": [f32_json(x) for x in v[:8]],
+    }
+
+
+def f64_stats(prefix: str, values) -> dict:
+    """The codec dump tools' statistics (fish_s2_rvq_lookup_dump.rs:123-150):
+    l2 = sqrt of the sequential f64 sum of squares, mean_abs = sequential f64
+    sum of |x| / len, max_abs = fold(0, max) over |x|, first8 as f64."""
+    v = np.ascontiguousarray(values, np.float32).ravel().astype(np.float64)
+    n = v.size
+    return {
+        f"{prefix}_l2": float(np.sqrt(np.cumsum(v * v)[-1])) if n else 0.0,
+        f"{prefix}_mean_abs": float(np.cumsum(np.abs(v))[-1] / n) if n else 0.0,
+        f"{prefix}_max_abs": float(max(0.0, np.max(np.abs(v)))) if n else 0.0,
+        f"{prefix}_first8": [float(x) for x in v[:8]],
     }
 
 
@@ -373,6 +393,52 @@ def _load_prompt(path: str):
     return np.asarray(obj, np.int32)
 
 
+# -- codec stages ---------------------------------------------------------------
+
+def _codes(codes_dump: dict):
+    return (np.asarray(codes_dump["codes"], np.int32), int(codes_dump["num_codebooks"]),
+            int(codes_dump["n_frames"]))
+
+
+def rvq_lookup_dump(codec, codes_dump: dict) -> dict:
+    """RvqLookupDump of rvq_lookup_codes (codec.rs:2536-2596) on the codes."""
+    codes, ncb, n = _codes(codes_dump)
+    lat = codec.rvq_lookup(codes, ncb, n)
+    return {"backend": BACKEND, "text": codes_dump.get("text"), "num_codebooks": ncb, "n_frames": n,
+            "latent_dim": int(lat.shape[1]), "latent_len": int(lat.size), **f64_stats("latent", lat)}
+
+
+def post_module_dump(codec, codes_dump: dict) -> dict:
+    """PostModuleDump of forward_codec_post_module (codec.rs:986-1018) after the lookup."""
+    codes, ncb, n = _codes(codes_dump)
+    hid = codec.post_module(codec.rvq_lookup(codes, ncb, n))
+    return {"backend": BACKEND, "text": codes_dump.get("text"), "num_codebooks": ncb, "n_frames": n,
+            "hidden_dim": int(hid.shape[1]), "hidden_len": int(hid.size), **f64_stats("hidden", hid)}
+
+
+def decode_stage_dump(codec, codes_dump: dict) -> dict:
+    """DecodeStageDump of rvq_decode_latents (codec.rs:1282-1297) after the lookup."""
+    codes, ncb, n = _codes(codes_dump)
+    out = codec.decode_latents(codec.rvq_lookup(codes, ncb, n))
+    return {"backend": BACKEND, "text": codes_dump.get("text"), "num_codebooks": ncb, "input_frames": n,
+            "output_frames": int(out.shape[0]), "hidden_dim": int(out.shape[1]), "hidden_len": int(out.size),
+            **f64_stats("hidden", out)}
+
+
+def waveform_dump(codec, codes_dump: dict) -> dict:
+    """WaveformDump of decode_waveform (codec.rs:1690-1714)."""
+    codes, ncb, n = _codes(codes_dump)
+    w = codec.decode_waveform(codes, ncb, n)
+    return {"backend": BACKEND, "text": codes_dump.get("text"), "num_codebooks": ncb,
+            "input_frames": int(w.input_frames), "latent_frames": int(w.latent_frames),
+            "sample_rate": int(w.sample_rate), "num_samples": int(w.num_samples),
+            **f64_stats("samples", w.samples[: w.num_samples])}
+
+
+_CODEC_DUMPS = {"rvq-lookup": rvq_lookup_dump, "post-module": post_module_dump,
+                "decode-stage": decode_stage_dump, "waveform": waveform_dump}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(prog="python -m s2hip.dumps",
                                  description="Write parity dumps in the reference's JSON schemas.")
@@ -401,7 +467,23 @@ def main(argv=None):
     p.add_argument("--tokens", type=int, default=1)
     p.add_argument("--logits", action="store_true")
     p.add_argument("--top-k", type=int, default=8)
+    for kind in _CODEC_DUMPS:
+        p = sub.add_parser(kind)
+        p.add_argument("--codec", required=True, help="codec GGUF (fish-speech-codec)")
+        p.add_argument("--codes", required=True, help="GeneratedCodesDump JSON (the `codes` dump)")
+        p.add_argument("--output", required=True)
     a = ap.parse_args(argv)
+
+    if a.kind in _CODEC_DUMPS:
+        from .codec import Codec
+
+        with open(a.codes) as f:
+            codes_dump = json.load(f)
+        with Codec(a.codec, max(1, int(codes_dump["n_frames"]))) as c:
+            dump = _CODEC_DUMPS[a.kind](c, codes_dump)
+        write_json(a.output, dump)
+        print(f"wrote {a.output}")
+        return 0
 
     if a.kind == "slow-ar":
         g = GgufFile(a.transformer)

@@ -2,14 +2,21 @@
 
 Same checks, tolerances and failure texts as compare_generated_codes_dumps
 (:709-804), compare_fast_ar_frame_dumps (:1211-1289),
-compare_semantic_token_dumps (:1291-1348) and compare_slow_ar_dumps
-(:1365-1710), over the JSON files that `s2hip.dumps` and the reference's
-dump tools write.  Command line as `fish_s2_parity`'s subcommands:
+compare_semantic_token_dumps (:1291-1348), compare_slow_ar_dumps
+(:1365-1710) and the codec-stage comparators compare_rvq_lookup_dumps
+(:855-941), compare_post_module_dumps (:943-1029),
+compare_decode_stage_dumps (:1031-1122) and compare_waveform_dumps
+(:626-707), over the JSON files that `s2hip.dumps` and the reference's dump
+tools write.  Command line as `fish_s2_parity`'s subcommands:
 
     python -m s2hip.parity compare-generated-codes expected.json actual.json
     python -m s2hip.parity compare-semantic-tokens expected.json actual.json
     python -m s2hip.parity compare-fast-ar-frame expected.json actual.json
     python -m s2hip.parity compare-slow-ar expected.json actual.json
+    python -m s2hip.parity compare-rvq-lookup expected.json actual.json
+    python -m s2hip.parity compare-post-module expected.json actual.json
+    python -m s2hip.parity compare-decode-stage expected.json actual.json
+    python -m s2hip.parity compare-waveform expected.json actual.json
 """
 
 import json
@@ -222,11 +229,117 @@ def compare_slow_ar_dumps(expected: dict, actual: dict, tolerance: SlowArTensorT
     return Report(not f, f, deltas)
 
 
+# -- codec stages -----------------------------------------------------------------
+
+@dataclass(frozen=True)
+class StageTolerance:
+    max_l2_delta: float
+    max_mean_abs_delta: float
+    max_max_abs_delta: float
+    max_first8_mae: float
+    max_num_samples_delta: int = 0
+
+
+# RvqLookupTolerance / PostModuleTolerance / DecodeStageTolerance /
+# WaveformTolerance ::default (lib.rs:290-300, 334-344, 378-391, 584-595)
+RVQ_LOOKUP_TOLERANCE = StageTolerance(5e-4, 5e-6, 5e-5, 5e-5)
+POST_MODULE_TOLERANCE = StageTolerance(5e-4, 5e-6, 5e-5, 5e-5)
+DECODE_STAGE_TOLERANCE = StageTolerance(5e-3, 5e-5, 3e-3, 2e-3)
+WAVEFORM_TOLERANCE = StageTolerance(50.0, 0.05, 0.2, 0.15, 0)
+
+
+@dataclass
+class StageReport:
+    passed: bool
+    failures: List[str]
+    l2_delta: float
+    mean_abs_delta: float
+    max_abs_delta: float
+    first8_mae: float
+    prefix: str = ""
+
+    @property
+    def tensor_deltas(self):
+        return []
+
+
+def _stage_common(expected, actual, checks, failures):
+    if expected.get("text") != actual.get("text"):
+        failures.append(f"text mismatch: expected {_opt(expected.get('text'))}, actual {_opt(actual.get('text'))}")
+    for name in checks:
+        if int(expected[name]) != int(actual[name]):
+            failures.append(f"{name} mismatch: expected {int(expected[name])}, actual {int(actual[name])}")
+
+
+def _opt(text):
+    """Rust's {:?} of an Option<String>."""
+    return "None" if text is None else f"Some({json.dumps(text)})"
+
+
+def _stage_stats(expected, actual, prefix, tol, failures):
+    l2 = abs(expected[f"{prefix}_l2"] - actual[f"{prefix}_l2"])
+    mean = abs(expected[f"{prefix}_mean_abs"] - actual[f"{prefix}_mean_abs"])
+    mx = abs(expected[f"{prefix}_max_abs"] - actual[f"{prefix}_max_abs"])
+    f8 = _first8_mae(expected[f"{prefix}_first8"], actual[f"{prefix}_first8"])
+    if l2 > tol.max_l2_delta:
+        failures.append(f"{prefix}_l2 delta {l2:.8f} exceeds {tol.max_l2_delta:.8f}")
+    if mean > tol.max_mean_abs_delta:
+        failures.append(f"{prefix}_mean_abs delta {mean:.8f} exceeds {tol.max_mean_abs_delta:.8f}")
+    if mx > tol.max_max_abs_delta:
+        failures.append(f"{prefix}_max_abs delta {mx:.8f} exceeds {tol.max_max_abs_delta:.8f}")
+    if f8 > tol.max_first8_mae:
+        failures.append(f"{prefix}_first8 MAE {f8:.8f} exceeds {tol.max_first8_mae:.8f}")
+    return StageReport(not failures, failures, l2, mean, mx, f8, prefix)
+
+
+def _len_check(dump, side, len_key, frames_key, dim_key, failures):
+    want = int(dump[frames_key]) * int(dump[dim_key])
+    if int(dump[len_key]) != want:
+        failures.append(f"{side} {len_key} {int(dump[len_key])} does not match {frames_key}*{dim_key} {want}")
+
+
+def compare_rvq_lookup_dumps(expected: dict, actual: dict, tolerance: StageTolerance = RVQ_LOOKUP_TOLERANCE):
+    f = []
+    _stage_common(expected, actual, ("num_codebooks", "n_frames", "latent_dim", "latent_len"), f)
+    _len_check(expected, "expected", "latent_len", "n_frames", "latent_dim", f)
+    _len_check(actual, "actual", "latent_len", "n_frames", "latent_dim", f)
+    return _stage_stats(expected, actual, "latent", tolerance, f)
+
+
+def compare_post_module_dumps(expected: dict, actual: dict, tolerance: StageTolerance = POST_MODULE_TOLERANCE):
+    f = []
+    _stage_common(expected, actual, ("num_codebooks", "n_frames", "hidden_dim", "hidden_len"), f)
+    _len_check(expected, "expected", "hidden_len", "n_frames", "hidden_dim", f)
+    _len_check(actual, "actual", "hidden_len", "n_frames", "hidden_dim", f)
+    return _stage_stats(expected, actual, "hidden", tolerance, f)
+
+
+def compare_decode_stage_dumps(expected: dict, actual: dict, tolerance: StageTolerance = DECODE_STAGE_TOLERANCE):
+    f = []
+    _stage_common(expected, actual, ("num_codebooks", "input_frames", "output_frames", "hidden_dim", "hidden_len"), f)
+    _len_check(expected, "expected", "hidden_len", "output_frames", "hidden_dim", f)
+    _len_check(actual, "actual", "hidden_len", "output_frames", "hidden_dim", f)
+    return _stage_stats(expected, actual, "hidden", tolerance, f)
+
+
+def compare_waveform_dumps(expected: dict, actual: dict, tolerance: StageTolerance = WAVEFORM_TOLERANCE):
+    f = []
+    _stage_common(expected, actual, ("num_codebooks", "input_frames", "sample_rate"), f)
+    d = abs(int(expected["num_samples"]) - int(actual["num_samples"]))
+    if d > tolerance.max_num_samples_delta:
+        f.append(f"num_samples delta {d} exceeds {tolerance.max_num_samples_delta}")
+    return _stage_stats(expected, actual, "samples", tolerance, f)
+
+
 _COMMANDS = {
     "compare-generated-codes": (compare_generated_codes_dumps, "generated codebook parity failed"),
     "compare-semantic-tokens": (compare_semantic_token_dumps, "semantic token parity failed"),
     "compare-fast-ar-frame": (compare_fast_ar_frame_dumps, "Fast-AR frame parity failed"),
     "compare-slow-ar": (compare_slow_ar_dumps, "Slow-AR tensor parity failed"),
+    "compare-rvq-lookup": (compare_rvq_lookup_dumps, "RVQ lookup parity failed"),
+    "compare-post-module": (compare_post_module_dumps, "post-module parity failed"),
+    "compare-decode-stage": (compare_decode_stage_dumps, "decode-stage parity failed"),
+    "compare-waveform": (compare_waveform_dumps, "waveform parity failed"),
 }
 
 
@@ -240,6 +353,10 @@ def main(argv=None) -> int:
     with open(argv[1]) as fe, open(argv[2]) as fa:
         report = fn(json.load(fe), json.load(fa))
     print(f"passed={'true' if report.passed else 'false'}")
+    if isinstance(report, StageReport):
+        for key, v in (("l2_delta", report.l2_delta), ("mean_abs_delta", report.mean_abs_delta),
+                       ("max_abs_delta", report.max_abs_delta), ("first8_mae", report.first8_mae)):
+            print(f"{report.prefix}_{key}={v:.8f}")
     for d in report.tensor_deltas:
         print(f"tensor={d.name} l2_delta={d.l2_delta:.8f} mean_abs_delta={d.mean_abs_delta:.8f} "
               f"max_abs_delta={d.max_abs_delta:.8f} first8_mae={d.first8_mae:.8f}")

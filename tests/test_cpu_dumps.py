@@ -262,3 +262,88 @@ def test_gguf_reader_on_synthetic_model(tiny_gguf):
     with pytest.raises(ValueError):
         row_bytes(GGML_Q8_0, 40)
     g.close()
+
+
+# -- codec-stage dumps (fish_s2_parity lib.rs:268-403, 564-707, 855-1122) ---------------
+
+def _stage_dump(kind, prefix, **over):
+    d = {"backend": "rust", "text": "hi", "num_codebooks": 10}
+    if kind in ("rvq", "post"):
+        dim = "latent_dim" if kind == "rvq" else "hidden_dim"
+        d.update({"n_frames": 2, dim: 1024, f"{prefix}_len": 2048})
+    elif kind == "decode":
+        d.update({"input_frames": 2, "output_frames": 8, "hidden_dim": 1024, "hidden_len": 8192})
+    else:
+        d.update({"input_frames": 2, "latent_frames": 8, "sample_rate": 44100, "num_samples": 4096})
+    d.update({f"{prefix}_l2": 10.0, f"{prefix}_mean_abs": 0.25, f"{prefix}_max_abs": 1.5,
+              f"{prefix}_first8": [0.1 * i for i in range(8)]})
+    d.update(over)
+    return d
+
+
+STAGES = [("rvq", "latent", parity.compare_rvq_lookup_dumps, parity.RVQ_LOOKUP_TOLERANCE),
+          ("post", "hidden", parity.compare_post_module_dumps, parity.POST_MODULE_TOLERANCE),
+          ("decode", "hidden", parity.compare_decode_stage_dumps, parity.DECODE_STAGE_TOLERANCE),
+          ("wave", "samples", parity.compare_waveform_dumps, parity.WAVEFORM_TOLERANCE)]
+
+
+@pytest.mark.parametrize("kind,prefix,fn,tol", STAGES)
+def test_codec_stage_comparators(kind, prefix, fn, tol):
+    e = _stage_dump(kind, prefix)
+    r = fn(e, copy.deepcopy(e))
+    assert r.passed and r.failures == []
+    # each statistic just inside, then just past its tolerance (the reference's texts)
+    for key, limit, label in ((f"{prefix}_l2", tol.max_l2_delta, f"{prefix}_l2 delta"),
+                              (f"{prefix}_mean_abs", tol.max_mean_abs_delta, f"{prefix}_mean_abs delta"),
+                              (f"{prefix}_max_abs", tol.max_max_abs_delta, f"{prefix}_max_abs delta")):
+        assert fn(e, _stage_dump(kind, prefix, **{key: e[key] + 0.9 * limit})).passed
+        r = fn(e, _stage_dump(kind, prefix, **{key: e[key] + 1.5 * limit}))
+        assert not r.passed and r.failures == [f"{label} {1.5 * limit:.8f} exceeds {limit:.8f}"], r.failures
+    f8 = [x + 2 * tol.max_first8_mae for x in e[f"{prefix}_first8"]]
+    r = fn(e, _stage_dump(kind, prefix, **{f"{prefix}_first8": f8}))
+    assert r.failures == [f"{prefix}_first8 MAE {2 * tol.max_first8_mae:.8f} exceeds {tol.max_first8_mae:.8f}"]
+    r = fn(e, _stage_dump(kind, prefix, text="hello"))
+    assert r.failures == ['text mismatch: expected Some("hi"), actual Some("hello")']
+    r = fn(e, _stage_dump(kind, prefix, num_codebooks=9))
+    assert r.failures == ["num_codebooks mismatch: expected 10, actual 9"]
+
+
+def test_codec_stage_length_and_sample_checks():
+    e = _stage_dump("rvq", "latent")
+    r = parity.compare_rvq_lookup_dumps(e, _stage_dump("rvq", "latent", latent_len=2047))
+    assert r.failures == ["latent_len mismatch: expected 2048, actual 2047",
+                          "actual latent_len 2047 does not match n_frames*latent_dim 2048"]
+    e = _stage_dump("decode", "hidden")
+    r = parity.compare_decode_stage_dumps(e, _stage_dump("decode", "hidden", output_frames=9))
+    assert "output_frames mismatch: expected 8, actual 9" in r.failures
+    assert "actual hidden_len 8192 does not match output_frames*hidden_dim 9216" in r.failures
+    e = _stage_dump("wave", "samples")
+    r = parity.compare_waveform_dumps(e, _stage_dump("wave", "samples", num_samples=4095))
+    assert r.failures == ["num_samples delta 1 exceeds 0"]
+    # latent_frames is not compared (serde default field in the reference)
+    assert parity.compare_waveform_dumps(e, _stage_dump("wave", "samples", latent_frames=0)).passed
+
+
+def test_codec_stage_stats_definition():
+    v = np.array([3.0, -4.0, 0.5, 1e-3, -2.5, 7.0, 0.0, 1.0, 9.0], np.float32)
+    s = dumps.f64_stats("x", v)
+    x = v.astype(np.float64)
+    assert s["x_l2"] == pytest.approx(np.sqrt(np.sum(x * x)), rel=1e-15)
+    assert s["x_mean_abs"] == pytest.approx(np.mean(np.abs(x)), rel=1e-15)
+    assert s["x_max_abs"] == 9.0 and s["x_first8"] == [float(a) for a in x[:8]]
+    assert dumps.f64_stats("y", np.zeros(0, np.float32)) == {"y_l2": 0.0, "y_mean_abs": 0.0, "y_max_abs": 0.0,
+                                                             "y_first8": []}
+
+
+def test_codec_stage_cli(tmp_path, capsys):
+    e = _stage_dump("wave", "samples")
+    a = _stage_dump("wave", "samples", samples_max_abs=1.9)
+    pe, pa = tmp_path / "e.json", tmp_path / "a.json"
+    pe.write_text(json.dumps(e))
+    pa.write_text(json.dumps(a))
+    assert parity.main(["compare-waveform", str(pe), str(pe)]) == 0
+    assert "samples_l2_delta=0.00000000" in capsys.readouterr().out
+    assert parity.main(["compare-waveform", str(pe), str(pa)]) == 1
+    out = capsys.readouterr()
+    assert "failure=samples_max_abs delta 0.40000000 exceeds 0.20000000" in out.out
+    assert "waveform parity failed" in out.err

@@ -201,3 +201,40 @@ def test_full_size_decode_is_causal_extension_of_short_decode(codec_gguf, codec)
     assert d.max() < 1e-2 and d.mean() < 1e-3, (d.max(), d.mean())
     # the signal is not degenerate over the whole length
     assert np.std(full[-2048 * 16:]) > 0.05
+
+
+def test_codec_stage_dumps_pass_the_reference_comparators(codec, oracle):
+    """The GPU codec's stage dumps (s2hip.dumps, the reference dump tools'
+    schemas) against the same dumps of the oracle, under the reference
+    comparators' default tolerances (s2hip.parity; fish_s2_parity
+    compare-rvq-lookup / -post-module / -decode-stage / -waveform)."""
+    from s2hip import dumps, parity
+
+    n = 12
+    codes = random_codes(n, seed=21)
+    codes_dump = {"text": "hi", "num_codebooks": 10, "n_frames": n, "codes": codes.ravel().tolist()}
+    lat = oracle.rvq_lookup(codes, 10, n)
+    hid = oracle.post_module(lat)
+    up = oracle.upsample(hid)
+    wav = oracle.decode_waveform(codes, 10, n)
+    base = {"backend": "rust", "text": "hi", "num_codebooks": 10}
+    expect = {
+        "rvq": {**base, "n_frames": n, "latent_dim": 1024, "latent_len": lat.size, **dumps.f64_stats("latent", lat)},
+        "post": {**base, "n_frames": n, "hidden_dim": 1024, "hidden_len": hid.size, **dumps.f64_stats("hidden", hid)},
+        "decode": {**base, "input_frames": n, "output_frames": 4 * n, "hidden_dim": 1024, "hidden_len": up.size,
+                   **dumps.f64_stats("hidden", up)},
+        "wave": {**base, "input_frames": n, "latent_frames": 4 * n, "sample_rate": 44100, "num_samples": wav.size,
+                 **dumps.f64_stats("samples", wav)},
+    }
+    got = {"rvq": dumps.rvq_lookup_dump(codec, codes_dump), "post": dumps.post_module_dump(codec, codes_dump),
+           "decode": dumps.decode_stage_dump(codec, codes_dump), "wave": dumps.waveform_dump(codec, codes_dump)}
+    cmp = {"rvq": parity.compare_rvq_lookup_dumps, "post": parity.compare_post_module_dumps,
+           "decode": parity.compare_decode_stage_dumps, "wave": parity.compare_waveform_dumps}
+    for k in cmp:
+        assert got[k]["backend"] == "rust-hip"
+        r = cmp[k](expect[k], got[k])
+        print(f"[codec] {k} dump: l2 {r.l2_delta:.2e} mean_abs {r.mean_abs_delta:.2e} max_abs {r.max_abs_delta:.2e} "
+              f"first8 {r.first8_mae:.2e}", flush=True)
+        assert r.passed, (k, r.failures)
+    # the lookup is bit-exact, so its statistics are identical
+    assert got["rvq"] == {**expect["rvq"], "backend": "rust-hip"}
