@@ -127,6 +127,14 @@ class Codec:
                    out.ctypes.data, out.size, ctypes.byref(info))
         return CodecWaveformResult(info.sample_rate, info.input_frames, info.latent_frames, info.num_samples, out)
 
+    def decode_waveform_to_wav(self, codes, num_codebooks: int, n_frames: int) -> bytes:
+        """decode_waveform_to_wav (codec.rs:1716-1738): the decode, then
+        pcm_to_wav (wav.rs:7-39) on the host."""
+        from .wav import pcm_to_wav
+
+        w = self.decode_waveform(codes, num_codebooks, n_frames)
+        return pcm_to_wav(w.samples[: w.num_samples], w.sample_rate)
+
     def decode_waveform_device(self, codes_ptr: int, num_codebooks: int, n_frames: int, samples_ptr: int):
         """Device pointers (e.g. torch tensors' data_ptr() on the codec's device)."""
         self._call(self._L.s2hip_codec_decode_waveform_device, ctypes.c_void_p(codes_ptr), num_codebooks,

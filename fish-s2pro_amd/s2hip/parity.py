@@ -17,6 +17,8 @@ tools write.  Command line as `fish_s2_parity`'s subcommands:
     python -m s2hip.parity compare-post-module expected.json actual.json
     python -m s2hip.parity compare-decode-stage expected.json actual.json
     python -m s2hip.parity compare-waveform expected.json actual.json
+    python -m s2hip.parity metrics file.wav
+    python -m s2hip.parity compare golden.wav candidate.wav
 """
 
 import json
@@ -343,8 +345,37 @@ _COMMANDS = {
 }
 
 
+def _wav_main(argv) -> int:
+    from .wav import WavError, compare_metrics, metrics_from_wav_bytes
+
+    def load(p):
+        with open(p, "rb") as f:
+            return metrics_from_wav_bytes(f.read(), 50)
+    try:
+        if argv[0] == "metrics":
+            m = load(argv[1])
+            print(f"sample_rate={m.sample_rate}\nchannels={m.channels}\nbits_per_sample={m.bits_per_sample}\n"
+                  f"duration_seconds={m.duration_seconds:.6f}\nrms={m.rms:.8f}\npeak={m.peak:.8f}\n"
+                  f"envelope_frames={len(m.envelope_rms)}")
+            return 0
+        r = compare_metrics(load(argv[1]), load(argv[2]))
+    except (WavError, OSError) as e:
+        print(f"error: {e}", file=sys.stderr)
+        return 1
+    print(f"passed={'true' if r.passed else 'false'}\nduration_delta_seconds={r.duration_delta_seconds:.6f}\n"
+          f"rms_delta={r.rms_delta:.8f}\nenvelope_mae={r.envelope_mae:.8f}")
+    for x in r.failures:
+        print(f"failure={x}")
+    if not r.passed:
+        print("error: WAV parity failed", file=sys.stderr)
+        return 1
+    return 0
+
+
 def main(argv=None) -> int:
     argv = sys.argv[1:] if argv is None else argv
+    if (len(argv) == 2 and argv[0] == "metrics") or (len(argv) == 3 and argv[0] == "compare"):
+        return _wav_main(argv)
     if len(argv) != 3 or argv[0] not in _COMMANDS:
         print("usage:\n" + "\n".join(f"  python -m s2hip.parity {c} <expected.json> <actual.json>"
                                      for c in _COMMANDS), file=sys.stderr)

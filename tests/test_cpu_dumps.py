@@ -347,3 +347,59 @@ def test_codec_stage_cli(tmp_path, capsys):
     out = capsys.readouterr()
     assert "failure=samples_max_abs delta 0.40000000 exceeds 0.20000000" in out.out
     assert "waveform parity failed" in out.err
+
+
+# -- WAV output and WAV parity (wav.rs:7-39; fish_s2_parity lib.rs:1712-1944) --------------
+
+def test_pcm_to_wav_layout_and_reference_roundtrip():
+    from s2hip import wav
+    samples = np.array([-1.0, -0.25, 0.0, 0.25, 0.999], np.float32)  # wav.rs:201-210
+    b = wav.pcm_to_wav(samples, 44100)
+    assert len(b) == 44 + 10 and b[:4] == b"RIFF" and b[8:16] == b"WAVEfmt " and b[36:40] == b"data"
+    riff, fmt_size, fmt, ch, sr, br, ba, bits, dsz = (
+        *np.frombuffer(b[4:8], "<u4"), *np.frombuffer(b[16:20], "<u4"), *np.frombuffer(b[20:24], "<u2"),
+        *np.frombuffer(b[24:32], "<u4"), *np.frombuffer(b[32:36], "<u2"), *np.frombuffer(b[40:44], "<u4"))
+    assert (riff, fmt_size, fmt, ch, sr, br, ba, bits, dsz) == (54, 16, 1, 1, 44100, 88200, 2, 16, 10)
+    pcm = np.frombuffer(b[44:], "<i2")
+    # clamp, x 32767 in f32, truncation toward zero
+    assert pcm.tolist() == [-32767, -8191, 0, 8191, 32734]
+    decoded = pcm / 32768.0
+    assert np.all(np.abs(decoded - samples) <= 2.0 / 32768.0)
+    assert np.frombuffer(wav.pcm_to_wav(np.array([3.0, -7.0], np.float32), 8000)[44:], "<i2").tolist() == [32767, -32767]
+
+
+def test_wav_metrics_reference_cases():
+    from s2hip import wav
+
+    def pcm16(values, rate):
+        return wav.pcm_to_wav(np.zeros(0, np.float32), rate)[:40] + np.uint32(2 * len(values)).tobytes() + \
+            np.asarray(values, "<i2").tobytes()
+
+    m = wav.metrics_from_wav_bytes(pcm16([0, 16384, -16384, 0], 24000))  # lib.rs:1950-1958
+    assert (m.sample_rate, m.channels, m.bits_per_sample) == (24000, 1, 16)
+    assert abs(m.duration_seconds - 4 / 24000) < 1e-6 and 0.35 < m.rms < 0.36
+    a = wav.metrics_from_wav_bytes(pcm16([0] * 24000, 24000))  # lib.rs:1960-1967
+    b = wav.metrics_from_wav_bytes(pcm16([0] * 12000, 24000))
+    r = wav.compare_metrics(a, b)
+    assert not r.passed and r.failures == ["duration delta 0.5000s exceeds 0.1000s"]
+    assert wav.compare_metrics(a, a).passed
+    with pytest.raises(wav.WavError, match="not a RIFF/WAVE file"):
+        wav.metrics_from_wav_bytes(b"RIFX" + bytes(40))
+    with pytest.raises(wav.WavError, match="WAV contains no samples"):
+        wav.metrics_from_wav_bytes(pcm16([], 24000))
+    # envelope: 50 ms frames of RMS, compared after resampling both to a common length
+    x = np.concatenate([np.full(1200, 8000, np.int16), np.zeros(1200, np.int16)])
+    m = wav.metrics_from_wav_bytes(pcm16(x, 24000))
+    assert len(m.envelope_rms) == 2 and abs(m.envelope_rms[0] - 8000 / 32768) < 1e-12 and m.envelope_rms[1] == 0
+    assert wav.envelope_mae([1.0, 0.0], [1.0, 0.5, 0.0]) == pytest.approx(0.0)
+
+
+def test_wav_parity_cli(tmp_path, capsys):
+    from s2hip import wav
+    p = tmp_path / "a.wav"
+    p.write_bytes(wav.pcm_to_wav(np.sin(np.arange(4410, dtype=np.float32) / 7.0) * 0.5, 44100))
+    assert parity.main(["metrics", str(p)]) == 0
+    out = capsys.readouterr().out
+    assert "sample_rate=44100" in out and "duration_seconds=0.100000" in out and "envelope_frames=2" in out
+    assert parity.main(["compare", str(p), str(p)]) == 0
+    assert "passed=true" in capsys.readouterr().out

@@ -238,3 +238,22 @@ def test_codec_stage_dumps_pass_the_reference_comparators(codec, oracle):
         assert r.passed, (k, r.failures)
     # the lookup is bit-exact, so its statistics are identical
     assert got["rvq"] == {**expect["rvq"], "backend": "rust-hip"}
+
+
+def test_decode_waveform_to_wav_passes_the_reference_wav_parity(codec, oracle):
+    """decode_waveform_to_wav (codec.rs:1716-1738): the GPU decode packed by
+    pcm_to_wav against the oracle's samples packed the same way, under the
+    reference's WAV comparator (fish_s2_parity compare)."""
+    from s2hip import wav
+
+    n = 20
+    codes = random_codes(n, seed=22)
+    got = codec.decode_waveform_to_wav(codes, 10, n)
+    ref = wav.pcm_to_wav(oracle.decode_waveform(codes, 10, n), 44100)
+    assert len(got) == len(ref) == 44 + 2 * n * 2048 and got[:44] == ref[:44]
+    r = wav.compare_metrics(wav.metrics_from_wav_bytes(ref), wav.metrics_from_wav_bytes(got))
+    d = np.abs(np.frombuffer(got[44:], "<i2").astype(np.int32) - np.frombuffer(ref[44:], "<i2"))
+    print(f"[codec] wav: rms delta {r.rms_delta:.2e}, envelope MAE {r.envelope_mae:.2e}, "
+          f"PCM LSB diff max {d.max()} mean {d.mean():.3f}", flush=True)
+    assert r.passed, r.failures
+    assert d.max() <= 330  # the waveform bound (1e-2) in 16-bit steps
