@@ -644,7 +644,7 @@ class CodecEngine {
       const bool stop_here = stop_block == b + 1;
       for (uint32_t r = 0; r < 3; ++r) {
         const Res& R = B.res[r];
-        const bool fused = co % 32u == 0 && co <= 32u * R.c0.tile.mc && R.c1.tile.mc == R.c0.tile.mc;
+        const bool fused = co % 32u == 0 && co <= 32u * R.c0.tile.mc && R.c1.tile.mc == R.c0.tile.mc && R.c0.tile.mc <= 4;
         if (fused) {  // k7 conv + snake + k1 conv in one launch (the block holds every channel)
           // the k7 conv reads other tiles' rows (its halo), so the unit's f16
           // output goes to the other buffer: units read a16, b16, a16 and
