@@ -139,6 +139,8 @@ class Engine {
                     uint32_t T, float scale, float* out);
   void op_swiglu(const float* g, const float* u, size_t n, int fast, float* out);
   void op_running_sums(const float* terms, size_t n, float* prefix, float* total);
+  void op_running_cut(const float* terms, size_t n, float thr, bool absorb, size_t at, size_t* cut, float* sum,
+                      float* at_sum);
   void op_expf(const float* x, size_t n, float* y);
   void op_embed(const int32_t* flat, size_t n_tok, float* out);
   void op_sample(const float* logits, size_t n, const s2hip_sampler& smp, int64_t always, uint64_t* rng,
@@ -1693,6 +1695,30 @@ void Engine::op_running_sums(const float* terms, size_t n, float* prefix, float*
   HIPC(hipStreamSynchronize(stream_));
 }
 
+void Engine::op_running_cut(const float* terms, size_t n, float thr, bool absorb, size_t at, size_t* cut, float* sum,
+                            float* at_sum) {
+  select();
+  if (n > 8192) fail("running sums support at most 8192 terms on the device");
+  for (size_t i = 0; i < n; ++i)
+    if (!(terms[i] >= 0.0f)) fail("the cut search needs non-negative terms");
+  if (absorb)
+    for (size_t i = 1; i < n; ++i)
+      if (terms[i] > terms[i - 1]) fail("absorb needs non-increasing terms");
+  TmpBuf dt(n ? n * 4 : 4), dc(4), ds(8);
+  if (n) HIPC(hipMemcpyAsync(dt.p, terms, n * 4, hipMemcpyHostToDevice, stream_));
+  const uint32_t at32 = at < n ? uint32_t(at) : 0xffffffffu;
+  HIPC(launch_running_cut(dt.as<float>(), uint32_t(n), thr, absorb ? 1u : 0u, at32, dc.as<uint32_t>(), ds.as<float>(),
+                          stream_));
+  uint32_t c = 0;
+  float sums[2] = {0.0f, 0.0f};
+  HIPC(hipMemcpyAsync(&c, dc.p, 4, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipMemcpyAsync(sums, ds.p, 8, hipMemcpyDeviceToHost, stream_));
+  HIPC(hipStreamSynchronize(stream_));
+  *cut = c;
+  *sum = sums[0];
+  *at_sum = at < n ? sums[1] : 0.0f;
+}
+
 void Engine::op_embed(const int32_t* flat, size_t n_tok, float* out) {
   select();
   const s2hip_spec& s = spec;
@@ -2218,6 +2244,18 @@ int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n
     return 0;
   }
   return guarded(err, err_cap, [&] { engine->e->op_running_sums(terms, n, prefix_out, total_out); });
+}
+
+int32_t s2hip_op_running_cut(s2hip_engine* engine, const float* terms, size_t n, float threshold, int32_t absorb,
+                             size_t at, size_t* cut_out, float* sum_out, float* at_sum_out, char* err,
+                             size_t err_cap) {
+  if (!engine || (n && !terms) || !cut_out || !sum_out || !at_sum_out) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
+  return guarded(err, err_cap, [&] {
+    engine->e->op_running_cut(terms, n, threshold, absorb != 0, at, cut_out, sum_out, at_sum_out);
+  });
 }
 
 int32_t s2hip_op_expf(s2hip_engine* engine, const float* x, size_t n, float* y, char* err, size_t err_cap) {

@@ -239,6 +239,12 @@ hipError_t launch_swiglu(const float* g, const float* u, float* out, uint32_t n,
 hipError_t launch_expf(const float* x, float* y, size_t n, hipStream_t s);
 // Sequential f32 running sums of n <= 8192 terms (the samplers' summation routine).
 hipError_t launch_running_sum(const float* terms, uint32_t n, float* prefix, float* total, hipStream_t s);
+// The samplers' cut search over n <= 8192 terms: cut[0] = first index whose
+// running sum reaches thr (n if none; a NaN thr never does), sums[0] = the
+// running sum there (the total if none), sums[1] = the running sum at `at`
+// (at < n).  Terms non-negative; absorb: also non-increasing.
+hipError_t launch_running_cut(const float* terms, uint32_t n, float thr, uint32_t absorb, uint32_t at, uint32_t* cut,
+                              float* sums, hipStream_t s);
 // n_past += n for each of the n_seq sequences not done
 hipError_t launch_add_position(DevState* st, uint32_t n, uint32_t n_seq, hipStream_t s);
 // Plain device copy (bytes and both pointers 16-byte aligned).

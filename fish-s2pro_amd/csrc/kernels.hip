@@ -1985,9 +1985,9 @@ __device__ __forceinline__ void bitonic_sort_regs(uint32_t (&key)[E], uint32_t* 
   bitonic_stages<E, 2>(key, xbuf, par);
 }
 
-// One 32-element step of a sequential sum: add the batch into cs in order,
-// leave the running sums in the batch registers, write them to `prefix`.
-__device__ __forceinline__ void chain_batch(float4 (&v)[8], float& cs, float* prefix) {
+// One 32-element step of a sequential sum: add the batch into cs in order and
+// leave the running sums in the batch registers.
+__device__ __forceinline__ void chain_batch(float4 (&v)[8], float& cs) {
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     cs = __fadd_rn(cs, v[t].x);
@@ -1999,10 +1999,6 @@ __device__ __forceinline__ void chain_batch(float4 (&v)[8], float& cs, float* pr
     cs = __fadd_rn(cs, v[t].w);
     v[t].w = cs;
   }
-  if (prefix) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t) *reinterpret_cast<float4*>(prefix + 4 * t) = v[t];
-  }
 }
 
 __device__ __forceinline__ void chain_load(float4 (&v)[8], const float* p) {
@@ -2010,74 +2006,128 @@ __device__ __forceinline__ void chain_load(float4 (&v)[8], const float* p) {
   for (int t = 0; t < 8; ++t) v[t] = *reinterpret_cast<const float4*>(p + 4 * t);
 }
 
-// Sequential f32 sums in index order (one lane; one rounding per add).
+__device__ __forceinline__ void chain_store(const float4 (&v)[8], float* prefix) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) *reinterpret_cast<float4*>(prefix + 4 * t) = v[t];
+}
+
+// Running sum j of a batch (j uniform; unrolled selects, no indexed registers).
+__device__ __forceinline__ float chain_pick(const float4 (&v)[8], uint32_t j) {
+  float r = 0.0f;
+#pragma unroll
+  for (uint32_t t = 0; t < 8; ++t) {
+    r = j == 4 * t + 0 ? v[t].x : r;
+    r = j == 4 * t + 1 ? v[t].y : r;
+    r = j == 4 * t + 2 ? v[t].z : r;
+    r = j == 4 * t + 3 ? v[t].w : r;
+  }
+  return r;
+}
+
+// Count of running sums of a batch below thr: the offset of the first one
+// >= thr, as the sums of non-negative terms never decrease.
+__device__ __forceinline__ uint32_t chain_below(const float4 (&v)[8], float thr) {
+  uint32_t c = 0;
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+    c += (v[t].x < thr ? 1u : 0u) + (v[t].y < thr ? 1u : 0u) + (v[t].z < thr ? 1u : 0u) + (v[t].w < thr ? 1u : 0u);
+  return c;
+}
+
+struct ChainCut {
+  uint32_t cut;  // first i < n with run(i) >= thr; n if none
+  float sum;     // run(cut); the total run(n - 1) (0 for n = 0) if none
+  float at_sum;  // run(at) when at < n
+};
+
+// Sequential f32 running sums run(i) = fl(run(i - 1) + p[i]), run(-1) = 0,
+// in index order on one lane (the reference's sampling loops add term by
+// term): the first index whose running sum reaches thr (a NaN thr never
+// does), the running sum there, and the running sum at one more index `at`.
+// The terms must be non-negative when thr is a number (the running sums then
+// never decrease and the first crossing is found from a batch's sums).
 // Values are read from LDS 32 at a time into one of two register sets, the
-// next batch's reads in flight while the current one is added; `prefix`
-// (nullable) receives every running sum.  The chain stops after the first
-// batch whose last running sum reaches `stop` (use_stop), or as soon as the
-// next term is below half an ulp of the running sum (absorb: the terms are
-// non-negative and non-increasing, so that term and every later one leave
-// the sum unchanged).  *done_count receives the count of running sums made.
-__device__ __forceinline__ float seq_chain(const float* p, float* prefix, uint32_t n, bool use_stop, float stop,
-                                           bool absorb, uint32_t* done_count) {
+// next batch's reads issued before the current batch is added, with one
+// counter wait per batch (waits between the dependent adds cost more than
+// the reads).  The chain stops after the batch that settles both results,
+// or (absorb: terms also non-increasing) once the next term is below half an
+// ulp of the running sum, when it and every later term leave the sum
+// unchanged.  PREFIX: every running sum is also written to prefix.
+template <bool PREFIX>
+__device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float thr, bool absorb, uint32_t at,
+                                              float* prefix) {
   constexpr uint32_t B = 32;
+  ChainCut r{n, 0.0f, 0.0f};
   float cs = 0.0f;
   uint32_t i = 0;
-  float4 va[8], vb[8];
-  auto finish_batch = [&](uint32_t next) -> bool {  // true: stop here
-    if (use_stop && cs >= stop) return true;
-    if (absorb && next < n && cs > 0.0f) {
+  bool found = false;
+  // the batch [i - B, i) has been added and its sums are in v: record what it
+  // settles; true when the chain can stop (next: the term at i, if any)
+  auto settle = [&](const float4 (&v)[8], bool has_next, float next) -> bool {
+    const uint32_t base = i - B;
+    if (PREFIX) chain_store(v, prefix + base);
+    if (!found && cs >= thr) {
+      found = true;
+      const uint32_t k = chain_below(v, thr);
+      r.cut = base + k;
+      r.sum = chain_pick(v, k);
+    }
+    if (at - base < B) r.at_sum = chain_pick(v, at - base);
+    if (found && (at < i || at >= n)) return true;
+    if (absorb && has_next && cs > 0.0f) {
       const float half_ulp = __uint_as_float(__float_as_uint(cs) & 0x7f800000u) * 0x1p-24f;
-      if (p[next] < half_ulp) return true;
+      if (next < half_ulp) return true;
     }
     return false;
   };
-  if (n >= B) chain_load(va, p);
-  while (i + B <= n) {
-    if (i + 2 * B <= n) chain_load(vb, p + i + B);
-    chain_batch(va, cs, prefix ? prefix + i : nullptr);
-    i += B;
-    if (finish_batch(i)) {
-      *done_count = i;
-      return cs;
-    }
-    if (i + B > n) break;
-    if (i + 2 * B <= n) chain_load(va, p + i + B);
-    chain_batch(vb, cs, prefix ? prefix + i : nullptr);
-    i += B;
-    if (finish_batch(i)) {
-      *done_count = i;
-      return cs;
+  // stopped early: with no crossing the total is cs; an `at` not reached is
+  // past the absorbed point, where every running sum is cs
+  auto finish = [&]() -> ChainCut {
+    if (!found) r.sum = cs;
+    if (at >= i && at < n) r.at_sum = cs;
+    return r;
+  };
+  if (n >= B) {
+    const uint32_t last = n - B;  // reads past the last full batch repeat it (never added)
+    float4 va[8], vb[8];
+    chain_load(va, p);
+    while (true) {
+      chain_load(vb, p + min(i + B, last));
+      __builtin_amdgcn_s_waitcnt(0xC87F);  // lgkmcnt(8): va has arrived, vb may be in flight
+      __builtin_amdgcn_sched_barrier(0);
+      chain_batch(va, cs);
+      __builtin_amdgcn_sched_barrier(0);
+      i += B;
+      if (i + B > n) {
+        if (settle(va, i < n, i < n ? p[i] : 0.0f)) return finish();
+        break;
+      }
+      if (settle(va, true, vb[0].x)) return finish();
+      chain_load(va, p + min(i + B, last));
+      __builtin_amdgcn_s_waitcnt(0xC87F);
+      __builtin_amdgcn_sched_barrier(0);
+      chain_batch(vb, cs);
+      __builtin_amdgcn_sched_barrier(0);
+      i += B;
+      if (i + B > n) {
+        if (settle(vb, i < n, i < n ? p[i] : 0.0f)) return finish();
+        break;
+      }
+      if (settle(vb, true, va[0].x)) return finish();
     }
   }
   for (; i < n; ++i) {
     cs = __fadd_rn(cs, p[i]);
-    if (prefix) prefix[i] = cs;
-  }
-  *done_count = n;
-  return cs;
-}
-
-// First index i < n whose prefix[i] satisfies (prefix >= thr) when ge, else
-// (thr < prefix); n if none.  Whole block; result broadcast through *slot.
-__device__ __forceinline__ uint32_t block_first_index(const float* prefix, uint32_t n, float thr, bool ge,
-                                                      uint32_t* slot) {
-  __syncthreads();  // earlier readers of *slot are done
-  if (threadIdx.x == 0) *slot = 0xffffffffu;
-  __syncthreads();
-  uint32_t best = 0xffffffffu;
-  for (uint32_t i = threadIdx.x; i < n; i += SAMPLE_THREADS) {
-    const float c = prefix[i];
-    if (ge ? (c >= thr) : (thr < c)) {
-      best = i;
-      break;
+    if (PREFIX) prefix[i] = cs;
+    if (!found && cs >= thr) {
+      found = true;
+      r.cut = i;
+      r.sum = cs;
     }
+    if (i == at) r.at_sum = cs;
   }
-  for (int off = 32; off >= 1; off >>= 1) best = min(best, uint32_t(__shfl_xor(int(best), off, WAVE)));
-  if ((threadIdx.x & (WAVE - 1)) == 0 && best != 0xffffffffu) atomicMin(slot, best);
-  __syncthreads();
-  const uint32_t r = *slot;
-  return r == 0xffffffffu ? n : r;
+  if (!found) r.sum = cs;
+  return r;
 }
 
 // Candidate index of the m-th (0-based, ascending index) candidate whose key
@@ -2206,69 +2256,50 @@ __device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float
   __syncthreads();
   // softmax denominator: sequential sum over all valued items (the appended
   // item may break the non-increasing order, so it disables the early stop)
-  if (tid == 0) {
-    uint32_t cnt;
-    sh.bcast_f = seq_chain(sh.probs, nullptr, n_valued, false, 0.0f, !appended, &cnt);
-  }
+  constexpr uint32_t NO_POS = 0xffffffffu;
+  if (tid == 0) sh.bcast_f = seq_chain<false>(sh.probs, n_valued, __builtin_nanf(""), !appended, NO_POS, nullptr).sum;
   __syncthreads();
   const float sum = sh.bcast_f;
   if (sum > 0.0f)
     for (uint32_t i = tid; i < n_valued; i += NT) sh.probs[i] = __fdiv_rn(sh.probs[i], sum);
   __syncthreads();
-  // top-p: running sums of the probabilities (into sh.pref) until one reaches
-  // top_p; the cut is the first such index, found by the whole block
+  // top-p: the cut is the first index whose running sum of the probabilities
+  // reaches top_p; kept mass: the running sum at n_pv - 1, which is the cut,
+  // the always-include item's position when that extends the cut, or the
+  // last valued item when nothing is cut.  Then the draw's target.
   if (tid == 0) {
-    uint32_t cnt;
-    sh.bcast_f = seq_chain(sh.probs, sh.pref, n_valued, true, cfg.top_p, !appended, &cnt);
-    sh.bcast_u[3] = cnt;
-  }
-  __syncthreads();
-  const uint32_t pref_n = sh.bcast_u[3];
-  const float pref_last = sh.bcast_f;  // running sum after pref_n terms (the total when not cut)
-  const uint32_t cut = block_first_index(sh.pref, pref_n, cfg.top_p, true, &sh.bcast_u[2]);
-  uint32_t p_idx = cut < pref_n ? cut + 1 : n_items;  // zero-probability tail never reaches top_p either
-  if (p_idx == 0) p_idx = 1;
-  if (force_pos != 0xffffffffu && force_pos >= p_idx) p_idx = force_pos + 1;
-  const uint32_t n_pv = min(p_idx, n_valued);
-  // kept mass: the running sum at n_pv (past the computed prefix the terms
-  // were absorbed, or the always-include item extends the cut)
-  if (tid == 0) {
-    float sp = 0.0f;
-    if (n_pv > 0) {
-      if (n_pv <= pref_n) {
-        sp = sh.pref[n_pv - 1];
-      } else {
-        sp = pref_last;
-        // not cut: the chain stopped because every later term is absorbed;
-        // cut (the always-include item extends it): add the remaining terms
-        if (cut < pref_n)
-          for (uint32_t i = pref_n; i < n_pv; ++i) sp = __fadd_rn(sp, sh.probs[i]);
-      }
+    const uint32_t at = force_pos < n_valued ? force_pos : NO_POS;
+    const ChainCut c = seq_chain<false>(sh.probs, n_valued, cfg.top_p, !appended, at, nullptr);
+    uint32_t p_idx = c.cut < n_valued ? c.cut + 1 : n_items;  // zero-probability tail never reaches top_p either
+    if (p_idx == 0) p_idx = 1;
+    float sp = c.sum;
+    if (force_pos != NO_POS && force_pos >= p_idx) {
+      p_idx = force_pos + 1;
+      sp = c.at_sum;
     }
-    sh.bcast_f = sp;
-  }
-  __syncthreads();
-  const float sum_p = sh.bcast_f;
-  if (sum_p > 0.0f)
-    for (uint32_t i = tid; i < n_pv; i += NT) sh.probs[i] = __fdiv_rn(sh.probs[i], sum_p);
-  __syncthreads();
-  // draw: first index whose running sum exceeds the target; items past
-  // n_valued carry probability 0 and never raise the sum
-  if (tid == 0) {
+    if (min(p_idx, n_valued) == 0) sp = 0.0f;
+    sh.bcast_u[3] = p_idx;
+    sh.redf[0] = sp;
     const double draw = lcg_next_unit(rng);
     sh.bcast_f = fminf(fmaxf(float(draw), 0.0f), 1.0f - 1e-7f);
   }
   __syncthreads();
+  const uint32_t p_idx = sh.bcast_u[3];
+  const uint32_t n_pv = min(p_idx, n_valued);
+  const float sum_p = sh.redf[0];
   const float target = sh.bcast_f;
+  if (sum_p > 0.0f)
+    for (uint32_t i = tid; i < n_pv; i += NT) sh.probs[i] = __fdiv_rn(sh.probs[i], sum_p);
+  __syncthreads();
+  // draw: first index whose running sum exceeds the target (reaches the next
+  // float up); items past n_valued carry probability 0 and never raise the sum
   if (tid == 0) {
-    uint32_t cnt;
-    (void)seq_chain(sh.probs, sh.pref, n_pv, true, __uint_as_float(__float_as_uint(target) + 1u), !appended, &cnt);
-    sh.bcast_u[3] = cnt;
+    const float thr = __uint_as_float(__float_as_uint(target) + 1u);
+    sh.bcast_u[3] = seq_chain<false>(sh.probs, n_pv, thr, !appended, NO_POS, nullptr).cut;
   }
   __syncthreads();
-  const uint32_t draw_n = sh.bcast_u[3];
-  const uint32_t hit = block_first_index(sh.pref, draw_n, target, false, &sh.bcast_u[2]);
-  const uint32_t choice = hit < draw_n ? hit : p_idx - 1;
+  const uint32_t hit = sh.bcast_u[3];
+  const uint32_t choice = hit < n_pv ? hit : p_idx - 1;
   uint32_t tok;
   if (choice < n_top) {
     // id of sorted position `choice`: the (choice - first)-th smallest id
@@ -2484,12 +2515,25 @@ __global__ __launch_bounds__(WAVE) void running_sum_kernel(const float* terms, u
   __shared__ __align__(16) float ps[SAMPLE_MAX];
   for (uint32_t i = threadIdx.x; i < n; i += WAVE) t[i] = terms[i];
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t cnt;
-    *total = seq_chain(t, ps, n, false, 0.0f, false, &cnt);
-  }
+  if (threadIdx.x == 0) *total = seq_chain<true>(t, n, __builtin_nanf(""), false, 0xffffffffu, ps).sum;
   __syncthreads();
   for (uint32_t i = threadIdx.x; i < n; i += WAVE) prefix[i] = ps[i];
+}
+
+// The samplers' cut search through seq_chain for n <= SAMPLE_MAX terms: the
+// first index whose running sum reaches thr (n if none), the running sum
+// there (the total if none) and the running sum at index `at` (when at < n).
+__global__ __launch_bounds__(WAVE) void running_cut_kernel(const float* terms, uint32_t n, float thr, uint32_t absorb,
+                                                            uint32_t at, uint32_t* cut, float* sums) {
+  __shared__ __align__(16) float t[SAMPLE_MAX];
+  for (uint32_t i = threadIdx.x; i < n; i += WAVE) t[i] = terms[i];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const ChainCut c = seq_chain<false>(t, n, thr, absorb != 0, at, nullptr);
+    *cut = c.cut;
+    sums[0] = c.sum;
+    sums[1] = c.at_sum;
+  }
 }
 
 // expf_glibc over n inputs: the test hook of the device exp used by the
@@ -2778,6 +2822,13 @@ hipError_t launch_repack_q(const uint8_t* rows, size_t row_bytes, uint32_t wtype
 hipError_t launch_running_sum(const float* terms, uint32_t n, float* prefix, float* total, hipStream_t s) {
   if (n == 0 || n > SAMPLE_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(running_sum_kernel, dim3(1), dim3(WAVE), 0, s, terms, n, prefix, total);
+  return hipGetLastError();
+}
+
+hipError_t launch_running_cut(const float* terms, uint32_t n, float thr, uint32_t absorb, uint32_t at, uint32_t* cut,
+                              float* sums, hipStream_t s) {
+  if (n > SAMPLE_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(running_cut_kernel, dim3(1), dim3(WAVE), 0, s, terms, n, thr, absorb, at, cut, sums);
   return hipGetLastError();
 }
 

@@ -125,6 +125,8 @@ def load():
     L.s2hip_op_sample.argtypes = [vp, vp, sz, ctypes.POINTER(Sampler), ctypes.c_int64, u64p,
                                   ctypes.POINTER(u32), cp, sz]
     L.s2hip_op_running_sums.argtypes = [vp, vp, sz, vp, ctypes.POINTER(f32), cp, sz]
+    L.s2hip_op_running_cut.argtypes = [vp, vp, sz, f32, ctypes.c_int32, sz, ctypes.POINTER(sz), ctypes.POINTER(f32),
+                                       ctypes.POINTER(f32), cp, sz]
     L.s2hip_op_sample_noalloc.argtypes = [vp, vp, sz, ctypes.POINTER(Sampler), ctypes.c_int64, u64p,
                                           ctypes.POINTER(u32), cp, sz]
     L.s2hip_op_expf.argtypes = [vp, vp, sz, vp, cp, sz]
@@ -146,6 +148,7 @@ def load():
                  "s2hip_op_rms_norm", "s2hip_op_dequant_rows", "s2hip_op_qk_rope",
                  "s2hip_op_attention", "s2hip_op_swiglu", "s2hip_op_sample", "s2hip_op_sample_noalloc",
                  "s2hip_op_running_sums",
+                 "s2hip_op_running_cut",
                  "s2hip_op_expf", "s2hip_op_embed", "s2hip_reset_slot", "s2hip_eval_slot",
                  "s2hip_transpose_to_time_major", "s2hip_time_kernel"):
         getattr(L, name).restype = i32

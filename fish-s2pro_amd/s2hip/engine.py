@@ -283,6 +283,18 @@ class Engine:
         self._call(self._L.s2hip_op_running_sums, _p(t), t.size, _p(out), ctypes.byref(total))
         return out, total.value
 
+    def running_cut(self, terms, threshold, absorb=False, at=None):
+        """The samplers' cut search on the device: (first index whose running
+        sum reaches `threshold` or len(terms), the running sum there or the
+        total, the running sum at index `at` or 0.0)."""
+        t = _f32(terms)
+        cut = ctypes.c_size_t(0)
+        s, s_at = ctypes.c_float(0), ctypes.c_float(0)
+        at_v = t.size if at is None else int(at)
+        self._call(self._L.s2hip_op_running_cut, _p(t), t.size, float(threshold), 1 if absorb else 0, at_v,
+                   ctypes.byref(cut), ctypes.byref(s), ctypes.byref(s_at))
+        return cut.value, s.value, s_at.value
+
     def expf(self, x):
         """The device exp of the samplers and SwiGLU epilogues over an array."""
         a = _f32(x)

@@ -249,6 +249,18 @@ int32_t s2hip_op_sample_noalloc(s2hip_engine* engine, const float* logits, size_
 int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,
                               float* total_out, char* err, size_t err_cap);
 
+/* The samplers' cut search (sampling.rs:202-241: the top-p loop stops at the
+ * first item whose running sum reaches top_p; the draw takes the first item
+ * whose running sum exceeds the target): over n <= 8192 non-negative terms,
+ * cut_out = the first i with prefix(i) >= threshold (n if none; a NaN
+ * threshold never matches), sum_out = prefix(cut) (the total if none),
+ * at_sum_out = prefix(at) when at < n.  absorb != 0 lets the device stop once
+ * the terms no longer change the sum; it requires non-increasing terms.
+ * Results equal those of the full sequential loop.  A test hook. */
+int32_t s2hip_op_running_cut(s2hip_engine* engine, const float* terms, size_t n, float threshold, int32_t absorb,
+                             size_t at, size_t* cut_out, float* sum_out, float* at_sum_out, char* err,
+                             size_t err_cap);
+
 /* embed_slow_ar_time_major (crates/fish_s2_infer/src/slow_ar.rs:1041-1133):
  * out[t][dim] = emb[id] (+ the sum of the token's codebook rows, then the
  * 1/sqrt(num_codebooks + 1) scale, for semantic ids) for flat_tokens

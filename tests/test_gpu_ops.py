@@ -197,6 +197,60 @@ def test_running_sums_bit_exact(eng, name, terms):
     assert np.float32(total).view(np.uint32) == want[-1].view(np.uint32)
 
 
+
+def _cut_terms(n, rng):
+    lg = rng.standard_normal(n).astype(np.float32)
+    top = lg.max() if n else np.float32(0)
+    soft = np.exp((lg - top) / np.float32(0.7)).astype(np.float32)
+    steep = np.exp((lg - top) / np.float32(0.02)).astype(np.float32)
+    soft /= soft.sum() if n else np.float32(1)
+    steep /= steep.sum() if n else np.float32(1)
+    return [
+        ("uniform", np.full(n, np.float32(1.0) / np.float32(max(n, 1)), np.float32), True),
+        ("softmax", np.sort(soft)[::-1].astype(np.float32), True),
+        ("steep", np.sort(steep)[::-1].astype(np.float32), True),  # absorbed early
+        ("unsorted", rng.random(n).astype(np.float32), False),
+    ]
+
+
+@pytest.mark.parametrize("n", [0, 1, 31, 32, 33, 63, 64, 65, 100, 4096, 4100, 8192])
+def test_running_cut_matches_sequential_loop(eng, n):
+    # The top-p loop (sampling.rs:226-233) stops at the first item whose
+    # running sum reaches top_p, the draw (:235-240) at the first whose running
+    # sum exceeds the target; numpy's float32 add.accumulate is the loop.
+    # Thresholds hit running sums exactly (ties), fall just above one (the
+    # crossing is the next index), sit at batch edges and in the tail, and
+    # never match (NaN, above the total).
+    rng = np.random.default_rng(1000 + n)
+    for kind, terms, absorb in _cut_terms(n, rng):
+        pref = np.add.accumulate(terms, dtype=np.float32)
+        total = pref[-1] if n else np.float32(0)
+        thrs = [np.float32(np.nan), np.float32(0.0), np.float32(total) * np.float32(0.9),
+                np.nextafter(np.float32(total), np.float32(np.inf)), np.float32(total) + np.float32(1.0)]
+        for k in sorted({0, 30, 31, 32, 33, 64, n // 2, n - 2, n - 1}):
+            if 0 <= k < n:
+                thrs += [pref[k], np.nextafter(pref[k], np.float32(np.inf))]
+        for thr in thrs:
+            for at in (None, 0, 31, 32, n // 3, n - 1):
+                if at is not None and not 0 <= at < n:
+                    continue
+                hit = np.nonzero(pref >= thr)[0]
+                cut = int(hit[0]) if hit.size else n
+                want_s = pref[cut] if cut < n else np.float32(total)
+                want_at = pref[at] if at is not None else np.float32(0)
+                got_cut, got_s, got_at = eng.running_cut(terms, thr, absorb=absorb, at=at)
+                ctx = (kind, n, float(thr), at)
+                assert got_cut == cut, ctx
+                assert np.float32(got_s).view(np.uint32) == np.float32(want_s).view(np.uint32), ctx
+                assert np.float32(got_at).view(np.uint32) == np.float32(want_at).view(np.uint32), ctx
+
+
+def test_running_cut_rejects_bad_terms(eng):
+    with pytest.raises(Exception, match="non-negative"):
+        eng.running_cut(np.array([0.5, -0.1], np.float32), 0.3)
+    with pytest.raises(Exception, match="non-increasing"):
+        eng.running_cut(np.array([0.1, 0.5], np.float32), 0.3, absorb=True)
+
 SAMPLER_CASES = [
     (0.0, 1.0, 0), (0.0, 0.9, 0), (0.0, 1.0, 30), (0.7, 0.9, 0), (0.7, 0.7, 30), (1.0, 1.0, 0),
     (0.3, 0.5, 5), (0.7, 1.0, 4096), (1.5, 0.95, 1),
