@@ -2046,21 +2046,28 @@ struct ChainCut {
 // does), the running sum there, and the running sum at one more index `at`.
 // The terms must be non-negative when thr is a number (the running sums then
 // never decrease and the first crossing is found from a batch's sums).
-// Values are read from LDS 32 at a time into one of two register sets, the
-// next batch's reads issued before the current batch is added, with one
-// counter wait per batch (waits between the dependent adds cost more than
-// the reads).  The chain stops after the batch that settles both results,
-// or (absorb: terms also non-increasing) once the next term is below half an
-// ulp of the running sum, when it and every later term leave the sum
-// unchanged.  PREFIX: every running sum is also written to prefix.
+// Fast phase: groups of G batches of 32 terms read from LDS into one of two
+// register sets, the next batch's reads issued before the current batch is
+// added, one counter wait per batch and one test per group (waits and
+// branches between the dependent adds cost more than the reads).  A group
+// that reaches thr or holds `at` is added again from its start, batch by
+// batch (the same adds in the same order, so the same sums), to settle the
+// result; so are the last terms.  The chain stops once both results are
+// settled or (absorb: terms also non-increasing) once the next term is below
+// half an ulp of the running sum, when it and every later term leave the sum
+// unchanged.  PREFIX: every running sum is also written to prefix (batch by
+// batch throughout).
 template <bool PREFIX>
 __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float thr, bool absorb, uint32_t at,
                                               float* prefix) {
-  constexpr uint32_t B = 32;
+  constexpr uint32_t B = 32, G = 4, GT = G * B;
   ChainCut r{n, 0.0f, 0.0f};
   float cs = 0.0f;
   uint32_t i = 0;
-  bool found = false;
+  bool found = false, at_open = at < n;
+  auto absorbs = [&](float next) -> bool {  // next < half an ulp of cs
+    return absorb && cs > 0.0f && next < __uint_as_float(__float_as_uint(cs) & 0x7f800000u) * 0x1p-24f;
+  };
   // the batch [i - B, i) has been added and its sums are in v: record what it
   // settles; true when the chain can stop (next: the term at i, if any)
   auto settle = [&](const float4 (&v)[8], bool has_next, float next) -> bool {
@@ -2072,49 +2079,61 @@ __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float 
       r.cut = base + k;
       r.sum = chain_pick(v, k);
     }
-    if (at - base < B) r.at_sum = chain_pick(v, at - base);
-    if (found && (at < i || at >= n)) return true;
-    if (absorb && has_next && cs > 0.0f) {
-      const float half_ulp = __uint_as_float(__float_as_uint(cs) & 0x7f800000u) * 0x1p-24f;
-      if (next < half_ulp) return true;
+    if (at_open && at - base < B) {
+      r.at_sum = chain_pick(v, at - base);
+      at_open = false;
     }
-    return false;
+    if (found && !at_open) return true;
+    return has_next && absorbs(next);
   };
   // stopped early: with no crossing the total is cs; an `at` not reached is
   // past the absorbed point, where every running sum is cs
   auto finish = [&]() -> ChainCut {
     if (!found) r.sum = cs;
-    if (at >= i && at < n) r.at_sum = cs;
+    if (at_open) r.at_sum = cs;
     return r;
   };
-  if (n >= B) {
-    const uint32_t last = n - B;  // reads past the last full batch repeat it (never added)
-    float4 va[8], vb[8];
-    chain_load(va, p);
-    while (true) {
-      chain_load(vb, p + min(i + B, last));
-      __builtin_amdgcn_s_waitcnt(0xC87F);  // lgkmcnt(8): va has arrived, vb may be in flight
-      __builtin_amdgcn_sched_barrier(0);
-      chain_batch(va, cs);
-      __builtin_amdgcn_sched_barrier(0);
-      i += B;
-      if (i + B > n) {
-        if (settle(va, i < n, i < n ? p[i] : 0.0f)) return finish();
-        break;
-      }
-      if (settle(va, true, vb[0].x)) return finish();
-      chain_load(va, p + min(i + B, last));
-      __builtin_amdgcn_s_waitcnt(0xC87F);
-      __builtin_amdgcn_sched_barrier(0);
-      chain_batch(vb, cs);
-      __builtin_amdgcn_sched_barrier(0);
-      i += B;
-      if (i + B > n) {
-        if (settle(vb, i < n, i < n ? p[i] : 0.0f)) return finish();
-        break;
-      }
-      if (settle(vb, true, va[0].x)) return finish();
+  while (true) {
+    bool event = false;
+    if (!PREFIX && i + GT <= n) {
+      const uint32_t last = n - B;  // reads past the last full batch repeat it (never added)
+      float4 va[8], vb[8];
+      chain_load(va, p + i);
+      do {
+        const float cs0 = cs;
+#pragma unroll
+        for (uint32_t g = 0; g < G; g += 2) {
+          chain_load(vb, p + min(i + B, last));
+          __builtin_amdgcn_s_waitcnt(0xC87F);  // lgkmcnt(8): va has arrived, vb may be in flight
+          __builtin_amdgcn_sched_barrier(0);
+          chain_batch(va, cs);
+          __builtin_amdgcn_sched_barrier(0);
+          i += B;
+          chain_load(va, p + min(i + B, last));
+          __builtin_amdgcn_s_waitcnt(0xC87F);
+          __builtin_amdgcn_sched_barrier(0);
+          chain_batch(vb, cs);
+          __builtin_amdgcn_sched_barrier(0);
+          i += B;
+        }
+        if ((!found && cs >= thr) || (at_open && at < i)) {  // settle this group batch by batch
+          i -= GT;
+          cs = cs0;
+          event = true;
+          break;
+        }
+        if (i < n && absorbs(i + B <= n ? va[0].x : p[i])) return finish();
+      } while (i + GT <= n);
     }
+    const uint32_t end = event ? i + GT : n;
+    while (i + B <= end) {
+      float4 v[8];
+      chain_load(v, p + i);
+      chain_batch(v, cs);
+      i += B;
+      if (settle(v, i < n, i < n ? p[i] : 0.0f)) return finish();
+    }
+    if (!event) break;
   }
   for (; i < n; ++i) {
     cs = __fadd_rn(cs, p[i]);
