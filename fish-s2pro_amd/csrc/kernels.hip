@@ -1920,62 +1920,82 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, SampleShared& sh) 
   return t;
 }
 
+// Median of three unsigned words: with c = 0 the min of a and b, with
+// c = ~0 the max (one VALU op for a compare-exchange half).
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+  uint32_t d;
+  asm("v_med3_u32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
+// Word of the lane `x` lanes away (lane ^ x) within a wave, for 0 < x < WAVE:
+// DPP quad permutes for x < 4, bit-mask swizzles within 32 lanes below 32,
+// a permute through the LDS crossbar otherwise.
+template <uint32_t X>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v) {
+  if constexpr (X == 1) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false));  // [1,0,3,2]
+  else if constexpr (X == 2) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false));  // [2,3,0,1]
+  else if constexpr (X == 3) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x1B, 0xF, 0xF, false));  // [3,2,1,0]
+  else if constexpr (X < 32) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), int(0x1Fu | (X << 10))));
+  else return uint32_t(__shfl_xor(int(v), int(X), WAVE));
+}
+
 // Ascending bitonic sort of P = E * SAMPLE_THREADS 32-bit keys in registers:
-// element r * SAMPLE_THREADS + tid is register r of thread tid.  Partners
-// j >= SAMPLE_THREADS apart sit in the same thread, WAVE <= j < SAMPLE_THREADS
-// in another wave (exchanged through `xbuf`, 2 * P words, double-buffered:
-// one barrier per step), and j < WAVE in the same wave (shuffles).  The
-// stage sizes K and J are template constants, so register indices are static.
-template <int E, uint32_t K, uint32_t J>
+// element e = r * SAMPLE_THREADS + tid is register r of thread tid.  Stage K
+// (merging sorted runs of K / 2) starts with the partners e ^ (K - 1) (each
+// K-block folded onto itself), then e ^ J for J = K / 4 .. 1; of each pair
+// the element whose bit J (K / 2 on the first step) is set keeps the max.
+// With the fold no step needs a direction, so a compare-exchange half is one
+// med3 against a mask.  Partners in the same thread are registers; in the
+// same wave, lane permutes; otherwise they are exchanged through `xbuf`
+// (2 * P words, double-buffered: one barrier per step).  K and J are template
+// constants, so register indices are static.
+template <int E, uint32_t K, uint32_t J, bool FOLD>
 __device__ __forceinline__ void bitonic_step(uint32_t (&key)[E], uint32_t* xbuf, uint32_t& par) {
   constexpr uint32_t NT = SAMPLE_THREADS;
   constexpr uint32_t P = uint32_t(E) * NT;
+  constexpr uint32_t X = FOLD ? K - 1 : J;  // partner = e ^ X
+  constexpr uint32_t TX = X & (NT - 1), RX = X / NT;
   const uint32_t tid = threadIdx.x;
-  if constexpr (J >= NT) {
+  // all ones where bit J of e is set (that element keeps the max)
+  auto upper = [&](int r) -> uint32_t {
+    if constexpr (J >= NT) return ((uint32_t(r) * NT) & J) ? ~0u : 0u;
+    else return 0u - ((tid / J) & 1u);
+  };
+  if constexpr (TX == 0) {  // same thread (J >= NT, not a fold)
 #pragma unroll
     for (int r = 0; r < E; ++r) {
-      constexpr int RJ = int(J / NT);
-      const int rp = r ^ RJ;
+      const int rp = r ^ int(RX);
       if (rp > r) {
-        const bool up = ((uint32_t(r) * NT) & K) == 0;
         const uint32_t x = key[r], y = key[rp];
-        key[r] = up ? min(x, y) : max(x, y);
-        key[rp] = up ? max(x, y) : min(x, y);
+        key[r] = min(x, y);
+        key[rp] = max(x, y);
       }
     }
-  } else if constexpr (J >= WAVE) {
+  } else if constexpr (RX == 0 && TX < WAVE) {  // same wave
+#pragma unroll
+    for (int r = 0; r < E; ++r) key[r] = med3_u32(key[r], lane_xor<TX>(key[r]), upper(r));
+  } else {
     uint32_t* buf = xbuf + par * P;
 #pragma unroll
     for (int r = 0; r < E; ++r) buf[r * NT + tid] = key[r];
     __syncthreads();
-    const bool lower = (tid & J) == 0;
 #pragma unroll
-    for (int r = 0; r < E; ++r) {
-      const uint32_t o = buf[r * NT + (tid ^ J)];
-      const bool up = ((uint32_t(r) * NT + tid) & K) == 0;
-      key[r] = (lower == up) ? min(key[r], o) : max(key[r], o);
-    }
+    for (int r = 0; r < E; ++r) key[r] = med3_u32(key[r], buf[(uint32_t(r) ^ RX) * NT + (tid ^ TX)], upper(r));
     par ^= 1u;
-  } else {
-    const bool lower = (tid & J) == 0;
-#pragma unroll
-    for (int r = 0; r < E; ++r) {
-      const uint32_t o = uint32_t(__shfl_xor(int(key[r]), int(J), WAVE));
-      const bool up = ((uint32_t(r) * NT + tid) & K) == 0;
-      key[r] = (lower == up) ? min(key[r], o) : max(key[r], o);
-    }
   }
 }
 
 template <int E, uint32_t K, uint32_t J>
 __device__ __forceinline__ void bitonic_merge(uint32_t (&key)[E], uint32_t* xbuf, uint32_t& par) {
-  bitonic_step<E, K, J>(key, xbuf, par);
+  bitonic_step<E, K, J, false>(key, xbuf, par);
   if constexpr (J > 1) bitonic_merge<E, K, J / 2>(key, xbuf, par);
 }
 
 template <int E, uint32_t K>
 __device__ __forceinline__ void bitonic_stages(uint32_t (&key)[E], uint32_t* xbuf, uint32_t& par) {
-  bitonic_merge<E, K, K / 2>(key, xbuf, par);
+  bitonic_step<E, K, K / 2, true>(key, xbuf, par);
+  if constexpr (K >= 4) bitonic_merge<E, K, K / 4>(key, xbuf, par);
   if constexpr (K < uint32_t(E) * SAMPLE_THREADS) bitonic_stages<E, 2 * K>(key, xbuf, par);
 }
 
