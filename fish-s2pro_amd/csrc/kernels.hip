@@ -1892,6 +1892,7 @@ struct SampleShared {
   float probs[SAMPLE_MAX + 4]; // probs and pref double as the sort's exchange buffer
   float pref[SAMPLE_MAX + 4];  // running sums
   float redf[SAMPLE_THREADS / WAVE];
+  float rede[SAMPLE_THREADS / WAVE];
   uint32_t redu[SAMPLE_THREADS / WAVE];
   uint32_t redk[SAMPLE_THREADS / WAVE];
   float bcast_f;
@@ -2364,38 +2365,64 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
                                 uint32_t* err) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr uint32_t NW = SAMPLE_THREADS / WAVE;
-  // pass 1: max and finite count
-  float mx = -INFINITY;
-  uint32_t nfin = 0;
+  // One pass: the finite count, the largest value with the smallest id among
+  // its copies, and the second largest value (a second copy of the largest
+  // counts).  The greedy test of the reference -- one value within 1e-6 of
+  // the max -- holds exactly when the second largest is not within 1e-6 of
+  // it: x -> |x - M| never increases for x <= M, so no smaller value is
+  // within 1e-6 when the second largest is not.
+  float m1 = -INFINITY, m2 = -INFINITY;
+  uint32_t id1 = 0xffffffffu, nfin = 0;
   for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
     const uint32_t id = ids ? ids[i] : i;
     const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
     if (v > -INFINITY) {
-      mx = fmaxf(mx, v);
       ++nfin;
+      if (v > m1) {
+        m2 = m1;
+        m1 = v;
+        id1 = id;
+      } else {
+        if (v == m1) id1 = min(id1, id);
+        m2 = fmaxf(m2, v);
+      }
     }
   }
-  mx = wave_max(mx);
-  float nf = wave_sum(float(nfin));
+  auto merge = [](float& a1, uint32_t& ai, float& a2, float b1, uint32_t bi, float b2) {
+    const uint32_t wi = a1 > b1 ? ai : (b1 > a1 ? bi : min(ai, bi));
+    a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+    a1 = fmaxf(a1, b1);
+    ai = wi;
+  };
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o1 = __shfl_xor(m1, off, WAVE), o2 = __shfl_xor(m2, off, WAVE);
+    const uint32_t oi = uint32_t(__shfl_xor(int(id1), off, WAVE));
+    merge(m1, id1, m2, o1, oi, o2);
+  }
+  const float nf = wave_sum(float(nfin));
   if (lane == 0) {
-    sh.redf[wave] = mx;
+    sh.redf[wave] = m1;
+    sh.redk[wave] = id1;
+    sh.rede[wave] = m2;
     sh.redu[wave] = uint32_t(nf);
   }
   __syncthreads();
   if (tid == 0) {
-    float m = -INFINITY;
-    uint32_t c = 0;
-    for (uint32_t w = 0; w < NW; ++w) {
-      m = fmaxf(m, sh.redf[w]);
+    float a1 = sh.redf[0], a2 = sh.rede[0];
+    uint32_t ai = sh.redk[0], c = sh.redu[0];
+    for (uint32_t w = 1; w < NW; ++w) {
+      merge(a1, ai, a2, sh.redf[w], sh.redk[w], sh.rede[w]);
       c += sh.redu[w];
     }
-    sh.bcast_f = m;
+    sh.bcast_f = a1;
     sh.bcast_u[0] = c;
+    sh.bcast_u[1] = (c > 0 && !(cfg.temperature > 0.0f) && !(fabsf(a2 - a1) < 1e-6f)) ? 1u : 0u;
+    sh.bcast_u[2] = ai;
   }
   __syncthreads();
-  const float M = sh.bcast_f;
-  const uint32_t n_fin = sh.bcast_u[0];
-  __syncthreads();
+  const uint32_t n_fin = sh.bcast_u[0], greedy = sh.bcast_u[1], arg = sh.bcast_u[2];
+  __syncthreads();  // every thread has read the broadcast words before they are reused
 
   if (n_fin == 0) {  // every candidate masked: the reference returns the first id of a -inf list
     uint32_t tok = 0;
@@ -2407,40 +2434,10 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
   }
 
   // greedy fast path: T <= 0 and a unique value within 1e-6 of the max
-  if (!(cfg.temperature > 0.0f)) {
-    uint32_t cnt = 0, arg = 0xffffffffu;
-    for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
-      const uint32_t id = ids ? ids[i] : i;
-      const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
-      if (v > -INFINITY && fabsf(v - M) < 1e-6f) {
-        ++cnt;
-        arg = min(arg, id);
-      }
-    }
-    cnt = uint32_t(wave_sum(float(cnt)));
-    for (int off = 32; off >= 1; off >>= 1) arg = min(arg, uint32_t(__shfl_xor(int(arg), off, 64)));
-    if (lane == 0) {
-      sh.redu[wave] = cnt;
-      sh.redk[wave] = arg;
-    }
+  if (greedy) {
+    if (tid == 0) (void)lcg_next_unit(rng);
     __syncthreads();
-    if (tid == 0) {
-      uint32_t c = 0, a = 0xffffffffu;
-      for (uint32_t w = 0; w < NW; ++w) {
-        c += sh.redu[w];
-        a = min(a, sh.redk[w]);
-      }
-      sh.bcast_u[1] = c;
-      sh.bcast_u[2] = a;
-    }
-    __syncthreads();
-    if (sh.bcast_u[1] == 1) {
-      const uint32_t tok = sh.bcast_u[2];
-      if (tid == 0) (void)lcg_next_unit(rng);
-      __syncthreads();
-      return tok;
-    }
-    __syncthreads();
+    return arg;
   }
 
   // general path: sort finite candidates by (value desc, id asc)
