@@ -2204,8 +2204,15 @@ __device__ __forceinline__ uint32_t block_nth_match(SampleShared& sh, uint32_t n
 // (the masked tail of the item list).  Whole block; binary search with a
 // block-wide count per step.
 template <int E>
-__device__ uint32_t block_masked_id(SampleShared& sh, const uint32_t (&cid)[E], const uint32_t (&ckey_r)[E],
-                                    uint32_t j, uint32_t vocab) {
+__device__ uint32_t block_masked_id(SampleShared& sh, const uint32_t* ids, uint32_t n, uint32_t j, uint32_t vocab) {
+  // this thread's candidates: id and key (keys from the candidate-order copy)
+  uint32_t cid[E], ckey_r[E];
+#pragma unroll
+  for (int r = 0; r < E; ++r) {
+    const uint32_t i = uint32_t(r) * SAMPLE_THREADS + threadIdx.x;
+    cid[r] = i < n ? (ids ? ids[i] : i) : 0xffffffffu;
+    ckey_r[r] = sh.ckey[i];
+  }
   uint32_t lo = 0, hi = vocab ? vocab - 1 : 0;
   while (lo < hi) {
     const uint32_t mid = lo + (hi - lo) / 2;
@@ -2230,21 +2237,20 @@ __device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float
                                                    int64_t force, uint64_t* rng, uint32_t n_fin) {
   constexpr uint32_t NT = SAMPLE_THREADS;
   const uint32_t tid = threadIdx.x;
-  uint32_t key[E], cid[E], ckr[E];
+  // keys in candidate order stay in sh.ckey (ids are re-read where needed),
+  // so no per-candidate registers live across the sums
+  uint32_t key[E];
   uint32_t fi_local = 0xffffffffu;
 #pragma unroll
   for (int r = 0; r < E; ++r) {
     const uint32_t i = uint32_t(r) * NT + tid;
     key[r] = NO_KEY;
-    cid[r] = 0xffffffffu;
     if (i < n) {
       const uint32_t id = ids ? ids[i] : i;
-      cid[r] = id;
       const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
       if (v > -INFINITY) key[r] = value_key(v);
       if (force >= 0 && int64_t(id) == force) fi_local = i;
     }
-    ckr[r] = key[r];
     sh.ckey[i] = key[r];
   }
   if (tid == 0) sh.bcast_u[1] = 0xffffffffu;
@@ -2270,7 +2276,8 @@ __device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float
 #pragma unroll
     for (int r = 0; r < E; ++r) {
       const uint32_t i = uint32_t(r) * NT + tid;
-      c += (ckr[r] < kf || (ckr[r] == kf && i < fi)) ? 1u : 0u;
+      const uint32_t kr = sh.ckey[i];
+      c += (kr < kf || (kr == kf && i < fi)) ? 1u : 0u;
     }
     const uint32_t rank = block_sum_u32(c, sh);
     if (rank < n_top) {
@@ -2355,7 +2362,7 @@ __device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float
   } else if (appended) {
     tok = uint32_t(force);
   } else {
-    tok = block_masked_id<E>(sh, cid, ckr, choice - n_fin, vocab);
+    tok = block_masked_id<E>(sh, ids, n, choice - n_fin, vocab);
   }
   return tok;
 }
