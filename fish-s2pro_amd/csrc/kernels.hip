@@ -2424,7 +2424,9 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
     }
     sh.bcast_f = a1;
     sh.bcast_u[0] = c;
-    sh.bcast_u[1] = (c > 0 && !(cfg.temperature > 0.0f) && !(fabsf(a2 - a1) < 1e-6f)) ? 1u : 0u;
+    // the max itself passes the test unless it is +inf (inf - inf is NaN),
+    // when the reference counts no value and leaves the greedy path
+    sh.bcast_u[1] = (c > 0 && !(cfg.temperature > 0.0f) && fabsf(a1 - a1) < 1e-6f && !(fabsf(a2 - a1) < 1e-6f)) ? 1u : 0u;
     sh.bcast_u[2] = ai;
   }
   __syncthreads();

@@ -276,6 +276,36 @@ def test_sampler_bit_exact(eng, T, top_p, top_k, n):
         assert (tg, st_g) == (to, st_o), (trial, tg, to)
 
 
+
+@pytest.mark.parametrize("n", [4096, 4097, 37])
+def test_sampler_greedy_uniqueness_threshold(eng, n):
+    # The greedy path needs exactly one value within 1e-6 of the max
+    # (sampling.rs:120-140); the device decides it from the largest and the
+    # second largest value.  Second values one ulp below the max, at about
+    # 1e-6 below it on either side of the threshold, masked (-inf) entries
+    # and a +inf max (inf - inf is NaN: no value passes, so the reference
+    # leaves the greedy path) must give the oracle's token and RNG state.
+    rng = np.random.default_rng(900 + n)
+    st_o = st_g = 777 + n
+    one = np.float32(1.0)
+    seconds = [np.nextafter(one, np.float32(0)), one - np.float32(1e-6), one - np.float32(9e-7),
+               one - np.float32(1.1e-6), one - np.float32(2e-6), np.float32(0.5)]
+    for trial in range(2 * len(seconds) + 4):
+        logits = (rng.standard_normal(n) * 0.1).astype(np.float32)
+        i, j = rng.choice(n, 2, replace=False)
+        logits[i] = one
+        if trial < 2 * len(seconds):
+            logits[j] = seconds[trial % len(seconds)]
+            if trial >= len(seconds):  # a masked (-inf) entry above them: ignored
+                logits[rng.integers(0, n)] = -np.inf
+        elif trial % 2 == 0:
+            logits[j] = np.float32(np.inf)
+        else:
+            logits[i] = logits[j] = np.float32(np.inf)
+        to, st_o = O.sample_token(logits, 0.0, 1.0, 0, None, st_o)
+        tg, st_g = eng.sample(logits, 0.0, 1.0, 0, None, st_g)
+        assert (tg, st_g) == (to, st_o), (trial, tg, to)
+
 def test_sampler_exact_on_the_draws_nearest_a_boundary(eng):
     # Draws whose target lies closest to a cumulative-probability boundary (or
     # whose top-p sums lie closest to top_p) are the ones a probability that is
