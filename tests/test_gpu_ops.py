@@ -306,6 +306,22 @@ def test_sampler_greedy_uniqueness_threshold(eng, n):
         tg, st_g = eng.sample(logits, 0.0, 1.0, 0, None, st_g)
         assert (tg, st_g) == (to, st_o), (trial, tg, to)
 
+
+@pytest.mark.parametrize("T,top_p,top_k", [(0.7, 0.9, 0), (0.7, 0.7, 30), (1.0, 1.0, 0)])
+def test_sampler_infinite_logits(eng, T, top_p, top_k):
+    # +inf logits make the softmax numerators NaN ((inf - inf) / T); the
+    # reference's sums, cut and draw then compare against NaN, and the
+    # device must end on the same item and RNG state.
+    rng = np.random.default_rng(31)
+    st_o = st_g = 4242
+    for trial in range(6):
+        n = (4096, 37, 4097)[trial % 3]
+        logits = rng.standard_normal(n).astype(np.float32)
+        logits[rng.choice(n, 1 + trial % 2, replace=False)] = np.inf
+        to, st_o = O.sample_token(logits, T, top_p, top_k, None, st_o)
+        tg, st_g = eng.sample(logits, T, top_p, top_k, None, st_g)
+        assert (tg, st_g) == (to, st_o), (trial, tg, to)
+
 def test_sampler_exact_on_the_draws_nearest_a_boundary(eng):
     # Draws whose target lies closest to a cumulative-probability boundary (or
     # whose top-p sums lie closest to top_p) are the ones a probability that is
