@@ -2000,9 +2000,26 @@ __device__ __forceinline__ void bitonic_stages(uint32_t (&key)[E], uint32_t* xbu
   if constexpr (K < uint32_t(E) * SAMPLE_THREADS) bitonic_stages<E, 2 * K>(key, xbuf, par);
 }
 
+// upper_sorted (block-uniform): registers E/2 .. E-1 already hold ascending
+// keys (one real key, then padding), as for n = E/2 * SAMPLE_THREADS + 1
+// candidates: only the lower half is sorted, then the last stage merges the
+// halves.  The lower half's exchanges use xbuf words [0, P), the first full
+// exchange words [P, 2P), so no step writes what the previous one may still
+// be reading.
 template <int E>
-__device__ __forceinline__ void bitonic_sort_regs(uint32_t (&key)[E], uint32_t* xbuf) {
+__device__ __forceinline__ void bitonic_sort_regs(uint32_t (&key)[E], uint32_t* xbuf, bool upper_sorted = false) {
   uint32_t par = 0;
+  if constexpr (E >= 2) {
+    if (upper_sorted) {
+      constexpr uint32_t P = uint32_t(E) * SAMPLE_THREADS;
+      uint32_t (&lo)[E / 2] = *reinterpret_cast<uint32_t(*)[E / 2]>(&key[0]);
+      bitonic_stages<E / 2, 2>(lo, xbuf, par);
+      par = 1;
+      bitonic_step<E, P, P / 2, true>(key, xbuf, par);
+      bitonic_merge<E, P, P / 4>(key, xbuf, par);
+      return;
+    }
+  }
   bitonic_stages<E, 2>(key, xbuf, par);
 }
 
@@ -2256,7 +2273,7 @@ __device__ __forceinline__ uint32_t sample_general(SampleShared& sh, const float
   if (tid == 0) sh.bcast_u[1] = 0xffffffffu;
   __syncthreads();
   if (fi_local != 0xffffffffu) sh.bcast_u[1] = fi_local;  // ids are unique
-  bitonic_sort_regs<E>(key, reinterpret_cast<uint32_t*>(sh.probs));
+  bitonic_sort_regs<E>(key, reinterpret_cast<uint32_t*>(sh.probs), n <= uint32_t(E / 2) * NT + 1u);
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < E; ++r) sh.skey[uint32_t(r) * NT + tid] = key[r];
