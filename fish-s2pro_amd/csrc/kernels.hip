@@ -2139,6 +2139,7 @@ __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float 
       chain_load(va, p + i);
       do {
         const float cs0 = cs;
+        float tl = 0.0f;  // the group's last term
 #pragma unroll
         for (uint32_t g = 0; g < G; g += 2) {
           chain_load(vb, p + min(i + B, last));
@@ -2150,6 +2151,7 @@ __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float 
           chain_load(va, p + min(i + B, last));
           __builtin_amdgcn_s_waitcnt(0xC87F);
           __builtin_amdgcn_sched_barrier(0);
+          tl = vb[7].w;
           chain_batch(vb, cs);
           __builtin_amdgcn_sched_barrier(0);
           i += B;
@@ -2160,7 +2162,9 @@ __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float 
           event = true;
           break;
         }
-        if (i < n && absorbs(i + B <= n ? va[0].x : p[i])) return finish();
+        // every later term is at most the group's last one (the terms never
+        // increase), which is in registers: no wait for the next batch's reads
+        if (absorbs(tl)) return finish();
       } while (i + GT <= n);
     }
     const uint32_t end = event ? i + GT : n;
