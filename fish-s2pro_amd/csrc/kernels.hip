@@ -2091,10 +2091,11 @@ struct ChainCut {
 // that reaches thr or holds `at` is added again from its start, batch by
 // batch (the same adds in the same order, so the same sums), to settle the
 // result; so are the last terms.  The chain stops once both results are
-// settled or (absorb: terms also non-increasing) once the next term is below
-// half an ulp of the running sum, when it and every later term leave the sum
-// unchanged.  PREFIX: every running sum is also written to prefix (batch by
-// batch throughout).
+// settled or (absorb: terms also non-increasing) once a term that bounds
+// every later one (the next term, or at a group's end the last term added)
+// is below half an ulp of the running sum: no later term changes the sum.
+// PREFIX: every running sum is also written to prefix (batch by batch
+// throughout).
 template <bool PREFIX>
 __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float thr, bool absorb, uint32_t at,
                                               float* prefix) {
