@@ -1124,6 +1124,22 @@ void fast_logits_recompute(orc_model* m, const float* hidden, const uint32_t* pr
   fast_head(m, seq.data() + (n - 1) * s.dim, logits);
 }
 
+// forward_codebook_prefix by the incremental form that fast_codebooks uses:
+// position 0 (the Slow hidden) and the prefix codes' fast_emb rows appended
+// one at a time over the cached K/V, then the head on the last position.
+void fast_logits_incremental(orc_model* m, const float* hidden, const uint32_t* prefix, size_t plen,
+                             float* logits) {
+  const orc_spec& s = m->spec;
+  if (plen >= s.num_codebooks) fail("fast prefix too long: %zu codes", plen);
+  std::vector<float> h(s.dim), row(s.dim);
+  fast_append(m, hidden, 0, h.data());
+  for (size_t i = 0; i < plen; ++i) {
+    emb_row(m->fast_emb, s.dim, prefix[i], row.data());
+    fast_append(m, row.data(), uint32_t(i + 1), h.data());
+  }
+  fast_head(m, h.data(), logits);
+}
+
 // generate_codebooks_for_semantic (fast_ar.rs:440-470)
 void fast_codebooks(orc_model* m, const float* hidden, uint32_t sem, float T, float top_p, int32_t top_k,
                     uint64_t* rng, uint32_t* codes) {
@@ -1379,7 +1395,10 @@ int32_t orc_embed(orc_model* m, const int32_t* flat, size_t n_tok, float* out, c
 int32_t orc_fast_logits(orc_model* m, const float* hidden, const uint32_t* prefix, size_t plen, float* logits,
                         char* err, size_t cap) {
   try {
-    fast_logits_recompute(m, hidden, prefix, plen, logits);
+    if (m->flags & ORC_FAITHFUL_FAST_RECOMPUTE)
+      fast_logits_recompute(m, hidden, prefix, plen, logits);
+    else
+      fast_logits_incremental(m, hidden, prefix, plen, logits);
     return 1;
   } catch (const std::exception& e) {
     copy_err(e, err, cap);

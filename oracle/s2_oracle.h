@@ -100,6 +100,8 @@ int32_t orc_eval(orc_model* m, const int32_t* flat_tokens, size_t n_tokens, floa
 /* embed_slow_ar_time_major alone: out [n_tokens][dim] */
 int32_t orc_embed(orc_model* m, const int32_t* flat_tokens, size_t n_tokens, float* out, char* err,
                   size_t err_cap);
+/* logits of the Fast-AR's last position after [slow_hidden, fast_emb[prefix]...]:
+ * the recompute form with ORC_FAITHFUL_FAST_RECOMPUTE, else the incremental one */
 int32_t orc_fast_logits(orc_model* m, const float* slow_hidden, const uint32_t* prefix,
                         size_t prefix_len, float* logits_out, char* err, size_t err_cap);
 int32_t orc_fast_codebooks(orc_model* m, const float* slow_hidden, uint32_t semantic_code,

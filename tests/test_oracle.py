@@ -312,6 +312,13 @@ def test_tiny_fast_incremental_equals_recompute(tiny_gguf):
         ci, si = inc.fast_codebooks(h, 17, T, top_p, 0, seed)
         cr, sr = rec.fast_codebooks(h, 17, T, top_p, 0, seed)
         assert np.array_equal(ci, cr) and si == sr
+    # the logits themselves, bit for bit, at every prefix length
+    rng = np.random.default_rng(8)
+    for plen in range(synth.TINY.num_codebooks):
+        prefix = rng.integers(0, synth.TINY.codebook_size, plen).tolist()
+        li = np.asarray(inc.fast_logits(h, prefix), np.float32)
+        lr = np.asarray(rec.fast_logits(h, prefix), np.float32)
+        assert np.array_equal(li.view(np.uint32), lr.view(np.uint32)), plen
 
 
 def test_tiny_faithful_modes_give_identical_codes(tiny_gguf):
@@ -522,3 +529,135 @@ def test_sampler_margins_kat():
     # top_p 0.6 over [0.5, 0.5]: the cut falls after item 1 with sums 0.5 / 1.0
     _, _, (_, cut, _) = O.sample_token_margins([1.0, 1.0], 1.0, 0.6, 0, None, 7)
     assert abs(cut - 0.1) < 1e-6
+
+
+# ------------------------------------------------- FFN sublayer KATs ------
+# forward_feed_forward (Slow: slow_ar.rs:659-710, swiglu_split :1215-1232;
+# Fast: fast_ar.rs:325-353, swiglu_split :472-485), derived by hand on d = 4,
+# ffn = 2 toys whose attention sublayer is zero (wqkv = 0, so v = 0 and the
+# attention adds nothing): the residual entering the FFN is the input x =
+# [2, 2, 2, 2] (rms 2).  ffn_norm gains g = [0.5, 1, 2, 1.5], eps 0, so the
+# normalised input is n = x / 2 * g = g exactly.
+#   w1 rows [0, 0, -1.5, 0], [0, -2.5, 0, 0]  -> gate = [-3, -2.5]
+#   w3 rows [2, 0, 0, 0],    [0, 2, 0, 0]     -> up   = [1, 2]
+#   a_i = SwiGLU(gate_i, up_i)
+#   w2 rows [1, 0], [0, 1], [1, 1], [0, 0]    -> proj = [a0, a1, a0 + a1, 0]
+#   out = x + proj, then the final RMSNorm (gain 1, eps 0).
+# Each planted mistake moves the output by far more than the 1e-6 tolerance:
+# w1 <-> w3 (gate [1, 2], up [-3, -2.5]), ffn_norm dropped (n = x) or its
+# gain dropped (n = [1, 1, 1, 1]), the FFN residual dropped (out[3] = 0).
+# The Slow and Fast SwiGLU forms, g * sigmoid(g) * u and g / (1 + e^-g) * u,
+# differ only in rounding; at gate -2.5, up 2 they differ by one f32 ulp, and
+# the bit-level checks below see it in the output.
+FFN_GAIN = [0.5, 1.0, 2.0, 1.5]
+FFN_W1 = [[0, 0, -1.5, 0], [0, -2.5, 0, 0]]
+FFN_W3 = [[2, 0, 0, 0], [0, 2, 0, 0]]
+FFN_W2 = [[1, 0], [0, 1], [1, 1], [0, 0]]
+FFN_X = [2.0, 2.0, 2.0, 2.0]
+
+
+def _libm_expf():
+    import ctypes
+    import ctypes.util
+
+    libm = ctypes.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+    fn = libm.expf
+    fn.restype, fn.argtypes = ctypes.c_float, [ctypes.c_float]
+    return lambda v: np.float32(fn(np.float32(v)))
+
+
+def _ffn_closed_form():
+    """float64: the toy's normalised output vector from the formulas above."""
+    sig = lambda v: 1.0 / (1.0 + math.exp(-v))
+    a0, a1 = -3.0 * sig(-3.0) * 1.0, -2.5 * sig(-2.5) * 2.0
+    out = np.array([2 + a0, 2 + a1, 2 + a0 + a1, 2.0])
+    return out / math.sqrt(float(np.mean(out * out)))
+
+
+def _ffn_f32(fast_form):
+    """The same toy in f32 with the reference's operation order: sequential
+    sums (`Iterator::sum`, no fused multiply-add), RMSNorm as
+    (x * (ms + eps).sqrt().recip()) * w (backend.rs:95-101), glibc expf (what
+    Rust's f32::exp calls on Linux)."""
+    f = np.float32
+    expf = _libm_expf()
+
+    def dot(x, w):
+        s = f(0)
+        for a, b in zip(x, w):
+            s = f(s + f(f(a) * f(b)))
+        return s
+
+    def rms(x, w):
+        ss = f(0)
+        for v in x:
+            ss = f(ss + f(v * v))
+        sc = f(f(1) / f(np.sqrt(f(f(ss / f(len(x))) + f(0)))))
+        return [f(f(v * sc) * f(g)) for v, g in zip(x, w)]
+
+    def swiglu(g, u):
+        if fast_form:  # fast_ar.rs:484
+            return f(f(g / f(f(1) + expf(-g))) * u)
+        return f(f(g * f(f(1) / f(f(1) + expf(-g)))) * u)  # slow_ar.rs:1229,1234
+
+    x = [f(v) for v in FFN_X]
+    n = rms(x, FFN_GAIN)
+    act = [swiglu(dot(n, r1), dot(n, r3)) for r1, r3 in zip(FFN_W1, FFN_W3)]
+    out = [f(a + dot(act, r)) for a, r in zip(x, FFN_W2)]
+    return np.array(rms(out, [1.0] * 4), np.float32)
+
+
+def _ffn_layer(**extra):
+    return {"ffn_norm.weight": FFN_GAIN, "feed_forward.w1.weight": FFN_W1,
+            "feed_forward.w3.weight": FFN_W3, "feed_forward.w2.weight": FFN_W2, **extra}
+
+
+def test_swiglu_rounding_orders_bit_exact():
+    # gate -2.5, up 2: the Slow form rounds g * sigmoid(g) first, the Fast form
+    # g / (1 + e^-g); the two f32 results differ by one ulp here, and -3 / 1 too
+    f = np.float32
+    expf = _libm_expf()
+    g = np.array([-2.5, -3.0], np.float32)
+    u = np.array([2.0, 1.0], np.float32)
+    slow = np.array([f(f(a * f(f(1) / f(f(1) + expf(-a)))) * b) for a, b in zip(g, u)], np.float32)
+    fast = np.array([f(f(a / f(f(1) + expf(-a))) * b) for a, b in zip(g, u)], np.float32)
+    assert (slow.view(np.uint32) != fast.view(np.uint32)).all()
+    assert np.array_equal(np.asarray(O.swiglu(g, u), np.float32).view(np.uint32), slow.view(np.uint32))
+    assert np.array_equal(np.asarray(O.swiglu(g, u, fast=True), np.float32).view(np.uint32), fast.view(np.uint32))
+
+
+@pytest.fixture(scope="module")
+def ffn_toy_gguf(tmp_path_factory):
+    # token 0 embeds to x; rows 1..4 of the tied head are unit vectors, so
+    # logits[1..4] read the hidden state back; no QK-norm (q = k = 0)
+    emb = np.zeros((8, 4), np.float32)
+    emb[0] = FFN_X
+    emb[1:5] = np.eye(4)
+    p = str(tmp_path_factory.mktemp("ffntoy") / "ffn_toy.gguf")
+    gguf_util.toy_model(p, 4, 8, slow=_ffn_layer(), emb=emb, qk_norm=False, semantic=(3, 6),
+                        codebook_size=4, fast=_ffn_layer(), fast_output=np.eye(4), fast_ffn=2)
+    return p
+
+
+def test_slow_ffn_sublayer_kat(ffn_toy_gguf):
+    m = O.OracleModel(ffn_toy_gguf, 4, im_end_id=7)
+    hidden, logits = m.eval([0, 0])
+    want = _ffn_closed_form()
+    np.testing.assert_allclose(hidden, want, rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(logits, [2 * want.sum(), *want, 0, 0, 0], rtol=1e-6, atol=1e-6)
+    # the Slow rounding order, bit for bit; the Fast form gives other bits
+    bits = _ffn_f32(fast_form=False).view(np.uint32)
+    assert np.array_equal(hidden.view(np.uint32), bits)
+    assert not np.array_equal(_ffn_f32(fast_form=True).view(np.uint32), bits)
+
+
+@pytest.mark.parametrize("flags", [0, O.FAITHFUL_FAST_RECOMPUTE])
+def test_fast_ffn_sublayer_kat(ffn_toy_gguf, flags):
+    # fast_logits with no prefix: the one position is the Slow hidden x;
+    # logits = fast_output . rmsnorm(out) with unit-vector rows
+    m = O.OracleModel(ffn_toy_gguf, 4, im_end_id=7, flags=flags)
+    logits = np.asarray(m.fast_logits(np.asarray(FFN_X, np.float32), []), np.float32)
+    np.testing.assert_allclose(logits, _ffn_closed_form(), rtol=1e-6, atol=1e-6)
+    bits = _ffn_f32(fast_form=True).view(np.uint32)
+    assert np.array_equal(logits.view(np.uint32), bits)
+    assert not np.array_equal(_ffn_f32(fast_form=False).view(np.uint32), bits)
