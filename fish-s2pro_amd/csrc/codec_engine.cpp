@@ -479,7 +479,7 @@ class CodecEngine {
     CHK(launch_gemm_mfma(W_F16, epi, g, stream_));
   }
   void split(const float* x, uint32_t ld, const float* norm, uint32_t n, uint32_t k) {
-    CHK(launch_split_rows(x, ld, norm, 1e-5f, n, gemm_rows_pad(n), k, pxh_, pxl_, prs_, stream_));
+    CHK(launch_split_rows(x, ld, norm, 1e-5f, n, gemm_rows_pad(n), k, pxh_, pxl_, prs_, nullptr, stream_));
   }
 
   // forward_codec_post_module (codec.rs:986-1018): lat_ -> hid_

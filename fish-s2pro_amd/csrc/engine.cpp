@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -39,6 +40,11 @@ void hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) throw HipFailure(std::string(what) + ": " + hipGetErrorString(e));
 }
 #define HIPC(expr) hip_check((expr), #expr)
+
+// device allocations the dual-AR engines of this process have made
+// (s2hip_device_allocations)
+std::atomic<uint64_t> g_device_allocs{0};
+void count_device_alloc() { g_device_allocs.fetch_add(1, std::memory_order_relaxed); }
 
 [[noreturn]] void fail(const std::string& m) { throw std::runtime_error(m); }
 
@@ -154,6 +160,7 @@ class Engine {
   T* dalloc(size_t count, size_t pad = 0) {
     void* p = nullptr;
     HIPC(hipMalloc(&p, count * sizeof(T) + pad));
+    count_device_alloc();
     allocs_.push_back(p);
     return static_cast<T*>(p);
   }
@@ -230,6 +237,15 @@ class Engine {
   DevLin head_cand_;  // the candidate rows of the head (tiled copy only)
   bool tiled_ = false;
   uint32_t bmm_min_cols_ = 2;  // columns from which F16 linears use the batched product
+  // Set while a call is re-run after ERR_F16_RANGE: every multi-column linear
+  // then takes the per-column paths (two-column GEMV, or the skinny product
+  // over rows split with a whole-row scale), which have no per-wave range.
+  bool bmm_off_ = false;
+  bool any_f16_range(uint32_t nseq) const {
+    for (uint32_t b = 0; b < nseq; ++b)
+      if (st_host_[b].err & ERR_F16_RANGE) return true;
+    return false;
+  }
   // L2 warming of the output projection by decode attention
   uint32_t warm_blocks_ = 256;            // warming blocks per kernel (0: off)
   uint32_t warm_depth_ = 4;               // 16-byte loads per thread in flight
@@ -281,6 +297,7 @@ class Engine {
   size_t graph_codes_stride_ = 0;
   uint32_t graph_nseq_ = 0;
   uint64_t graph_kv_gen_ = 0;
+  bool graph_bmm_off_ = false;
 };
 
 Engine::Engine(const s2hip_config& cfg) {
@@ -654,7 +671,7 @@ void Engine::bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, cons
 // up to 4096 (S2-Pro wqkv 9.2 vs 12.9 us, wo 7.7 vs 8.3 us); w1/w3 and w2
 // stay on the product (22.6 vs 25.8 us, 15.9 vs 17.9 us).
 bool Engine::uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const {
-  if (!L.wt || !bmm_min_cols_ || ncol < bmm_min_cols_ || (L3 && !L3->wt)) return false;
+  if (bmm_off_ || !L.wt || !bmm_min_cols_ || ncol < bmm_min_cols_ || (L3 && !L3->wt)) return false;
   return !(ncol == 2 && !L3 && L.in <= 4096 && gemv_rows_per_block(L.in, L.out, false, false, ncol) != 0);
 }
 
@@ -942,7 +959,7 @@ void Engine::enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_st
 // leaves the last token's residual row in decode column 0 for the output head.
 void Engine::mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm, float eps,
                 uint32_t n, uint32_t npad, float* y, uint32_t ldy) {
-  HIPC(launch_split_rows(x, ldx, norm, eps, n, npad, L.in, pxh_, pxl_, prs_, stream_));
+  HIPC(launch_split_rows(x, ldx, norm, eps, n, npad, L.in, pxh_, pxl_, prs_, nullptr, stream_));
   GemmArgs g{};
   g.w = L.w;
   g.w3 = L3 ? L3->w : nullptr;
@@ -965,7 +982,7 @@ void Engine::mm(const DevLin& L, const DevLin* L3, int epi, const float* x, uint
 void Engine::mm_skinny(const DevLin& L, const DevLin* L3, int epi, const float* x, uint32_t ldx, const float* norm,
                        float eps, uint32_t n, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
                        uint32_t out_rows, const uint32_t* done) {
-  HIPC(launch_split_rows(x, ldx, norm, eps, n, 16, L.in, pxh_, pxl_, prs_, stream_));
+  HIPC(launch_split_rows(x, ldx, norm, eps, n, 16, L.in, pxh_, pxl_, prs_, &st_->err, stream_));
   SkinnyArgs g{};
   g.w = L.w;
   g.w3 = L3 ? L3->w : nullptr;
@@ -1197,6 +1214,7 @@ void Engine::check_state_err(uint32_t nseq) {
     if (st_host_[b].err & ERR_KV_OVERFLOW) fail("KV cache overflow" + who);
     if (st_host_[b].err & ERR_SAMPLER) fail("sampler failure" + who);
     if (st_host_[b].err & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
+    if (st_host_[b].err & ERR_NONFINITE) fail("activation not finite");
   }
 }
 
@@ -1252,6 +1270,7 @@ void Engine::eval(const int32_t* flat, size_t n_tok, float* hidden_out, float* l
   if (e & ERR_TOKEN_RANGE) fail("token id out of range");
   if (e & ERR_KV_OVERFLOW) fail("KV cache overflow");
   if (e & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
+  if (e & ERR_NONFINITE) fail("activation not finite");
   n_past_host[slot] += uint32_t(n_tok);
 }
 
@@ -1295,6 +1314,17 @@ void Engine::fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampl
   enqueue_fast_frame(SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, 1, nullptr);
   HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
+  if (!bmm_off_ && any_f16_range(1)) {  // again on the per-column paths (as in generate)
+    bmm_off_ = true;
+    try {
+      fast_codebooks(hidden, sem, smp, rng, codes);
+    } catch (...) {
+      bmm_off_ = false;
+      throw;
+    }
+    bmm_off_ = false;
+    return;
+  }
   check_state_err();
   for (uint32_t cb = 0; cb < s.num_codebooks; ++cb) codes[cb] = st_host_->codes_frame[cb];
   *rng = st_host_->rng;
@@ -1404,7 +1434,8 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   }
   if (use_graph && launched < max_frames) {
     const bool stale = !graph_exec_ || graph_codes_ != codes_dev_ || graph_codes_stride_ != ncodes ||
-                       graph_nseq_ != nseq || graph_kv_gen_ != kv_gen_ || graph_cfg_.temperature != cfg.temperature ||
+                       graph_nseq_ != nseq || graph_kv_gen_ != kv_gen_ || graph_bmm_off_ != bmm_off_ ||
+                       graph_cfg_.temperature != cfg.temperature ||
                        graph_cfg_.top_p != cfg.top_p || graph_cfg_.top_k != cfg.top_k;
     if (stale) {
       if (graph_exec_) {
@@ -1431,6 +1462,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
       graph_codes_stride_ = ncodes;
       graph_nseq_ = nseq;
       graph_kv_gen_ = kv_gen_;
+      graph_bmm_off_ = bmm_off_;
     }
   }
   // Frames in batches; the done flag of batch i is read while batch i+1 runs.
@@ -1468,6 +1500,22 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   HIPC(hipEventElapsedTime(&ms_prefill, ev[0], ev[1]));
   HIPC(hipEventElapsedTime(&ms_decode, ev[1], ev[2]));
   for (auto& e : ev) (void)hipEventDestroy(e);
+  if (!bmm_off_ && any_f16_range(nseq)) {
+    // An activation beyond the batched product's per-wave range (one more
+    // than 2^15 times the largest of the first 256 of its wave's k range):
+    // the whole call runs again from its inputs (rngs and codes are only
+    // written below) with the per-column paths.
+    bmm_off_ = true;
+    try {
+      generate(nseq, prompts, cols, p, rngs, codes, n_frames, stats);
+    } catch (...) {
+      bmm_off_ = false;
+      throw;
+    }
+    bmm_off_ = false;
+    if (stats) stats->per_column_rerun = 1;
+    return;
+  }
   check_state_err(nseq);
   std::vector<int32_t> full(ncodes * nseq);
   if (ncodes) HIPC(hipMemcpy(full.data(), codes_dev_, ncodes * nseq * 4, hipMemcpyDeviceToHost));
@@ -1488,6 +1536,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
     stats->decode_ms = ms_decode;
     stats->n_frames = total;
     stats->graph_used = use_graph ? 1u : 0u;
+    stats->per_column_rerun = 0;
   }
 }
 
@@ -1497,7 +1546,10 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
 namespace {
 struct TmpBuf {
   void* p = nullptr;
-  TmpBuf(size_t bytes) { hip_check(hipMalloc(&p, bytes + WEIGHT_PAD), "hipMalloc"); }
+  TmpBuf(size_t bytes) {
+    hip_check(hipMalloc(&p, bytes + WEIGHT_PAD), "hipMalloc");
+    count_device_alloc();
+  }
   ~TmpBuf() { (void)hipFree(p); }
   template <class T>
   T* as() { return static_cast<T*>(p); }
@@ -1532,8 +1584,11 @@ void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, cons
     HIPC(hipMemcpyAsync(y, dy.p, out * ncol * 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipMemcpyAsync(&herr, derr.p, 4, hipMemcpyDeviceToHost, stream_));
     HIPC(hipStreamSynchronize(stream_));
-    if (herr & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
-    return;
+    if (!(herr & ERR_F16_RANGE)) return;
+    for (size_t i = 0; i < in * ncol; ++i)
+      if (!std::isfinite(x[i])) fail("activation not finite or beyond the range of the batched product");
+    // finite but beyond the per-wave range: the per-column paths below
+    // (whole-row scale) give the product
   }
   // quantized rows: the repacked planes that one-column decode GEMVs read
   std::unique_ptr<TmpBuf> dq, dsc;
@@ -2068,7 +2123,10 @@ int32_t s2hip_get_spec(const s2hip_engine* engine, s2hip_spec* out) {
 }
 
 int32_t s2hip_reset(s2hip_engine* engine, char* err, size_t err_cap) {
-  if (!engine) return 0;
+  if (!engine) {
+    set_err(err, err_cap, "NULL argument");
+    return 0;
+  }
   return guarded(err, err_cap, [&] { engine->e->reset(); });
 }
 
@@ -2235,6 +2293,10 @@ int32_t s2hip_op_sample_noalloc(s2hip_engine* engine, const float* logits, size_
     return 0;
   }
   return guarded(err, err_cap, [&] { engine->e->op_sample_noalloc(logits, n, *smp, always, rng, tok); });
+}
+
+void s2hip_device_allocations(uint64_t* count_out) {
+  if (count_out) *count_out = s2::g_device_allocs.load(std::memory_order_relaxed);
 }
 
 int32_t s2hip_op_running_sums(s2hip_engine* engine, const float* terms, size_t n, float* prefix_out,

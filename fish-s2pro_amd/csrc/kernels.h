@@ -33,7 +33,7 @@ struct DevState {
   uint32_t codes_frame[16];  // codebook ids of the frame being built
 };
 
-enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u, ERR_F16_RANGE = 8u };
+enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u, ERR_F16_RANGE = 8u, ERR_NONFINITE = 16u };
 constexpr uint32_t NO_ROW = 0xffffffffu;
 
 // Weight rows of the GEMV launched next, read into L2 by extra blocks of a
@@ -256,8 +256,9 @@ hipError_t launch_copy(const void* src, void* dst, size_t bytes, hipStream_t s);
 // Npad >= N, a multiple of 16 (gemm_rows_pad(N) for launch_gemm_mfma, 16 for
 // launch_skinny_mfma); K must be a multiple of 32.
 uint32_t gemm_rows_pad(uint32_t n);
+// err (nullable): ERR_NONFINITE is or-ed in when a row holds a non-finite value.
 hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, float eps, uint32_t N, uint32_t Npad,
-                             uint32_t K, _Float16* xh, _Float16* xl, float* rs, hipStream_t s);
+                             uint32_t K, _Float16* xh, _Float16* xl, float* rs, uint32_t* err, hipStream_t s);
 
 // MFMA product y[n][m] (op)= rs[n] * sum_k W[m][k] * x[n][k] for n < N, m < M,
 // x given as the split planes; epilogues as for launch_gemv (SwiGLU uses w3).

@@ -2135,7 +2135,9 @@ __device__ __forceinline__ ChainCut seq_chain(const float* p, uint32_t n, float 
   while (true) {
     bool event = false;
     if (!PREFIX && i + GT <= n) {
-      const uint32_t last = n - B;  // reads past the last full batch repeat it (never added)
+      // reads past the last full batch re-read an earlier, 16-byte aligned
+      // address (never added)
+      const uint32_t last = (n - B) & ~3u;
       float4 va[8], vb[8];
       chain_load(va, p + i);
       do {

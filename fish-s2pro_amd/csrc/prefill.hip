@@ -85,7 +85,7 @@ __device__ __forceinline__ float split_scale(float mx) {
 
 __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_t ldx, const float* norm, float eps,
                                                          uint32_t N, uint32_t K, _Float16* xh, _Float16* xl,
-                                                         float* rs) {
+                                                         float* rs, uint32_t* err) {
   __shared__ float red[4];
   const uint32_t n = blockIdx.x, tid = threadIdx.x;
   _Float16* hr = xh + size_t(n) * K;
@@ -117,6 +117,7 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_
       scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(K)), eps)));
     }
     float mx = 0.0f;
+    bool nf = false;
 #pragma unroll
     for (int i = 0; i < SR_REG; ++i) {
       if (norm) {
@@ -126,7 +127,11 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_
         v[i].w = __fmul_rn(__fmul_rn(v[i].w, scale), g[i].w);
       }
       mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+      // fmaxf drops NaN: non-finite values are flagged on their own
+      nf = nf || !(fabsf(v[i].x) <= 3.4028235e38f) || !(fabsf(v[i].y) <= 3.4028235e38f) ||
+           !(fabsf(v[i].z) <= 3.4028235e38f) || !(fabsf(v[i].w) <= 3.4028235e38f);
     }
+    if (__any(nf) && (tid & 63u) == 0 && err) atomicOr(err, ERR_NONFINITE);
     const float r = split_scale(block_reduce_max4(mx, red));
     const float inv = 1.0f / r;
 #pragma unroll
@@ -154,11 +159,14 @@ __global__ __launch_bounds__(256) void split_rows_kernel(const float* x, uint32_
     scale = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(tot, float(K)), eps)));
   }
   float mx = 0.0f;
+  bool nf = false;
   for (uint32_t i = tid; i < K; i += 256) {
     float v = xr[i];
     if (norm) v = __fmul_rn(__fmul_rn(v, scale), norm[i]);
     mx = fmaxf(mx, fabsf(v));
+    nf = nf || !(fabsf(v) <= 3.4028235e38f);
   }
+  if (__any(nf) && (tid & 63u) == 0 && err) atomicOr(err, ERR_NONFINITE);
   const float r = split_scale(block_reduce_max4(mx, red));
   const float inv = 1.0f / r;
   for (uint32_t i = tid; i < K; i += 256) {
@@ -847,6 +855,9 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_kernel(PrefillAttnArgs a,
       } else {
         kr[j] = *reinterpret_cast<const float4*>(kc + size_t(t) * HD + d);
       }
+      // keys past the last query: zero, so that whatever an earlier call left
+      // in the cache there (masked anyway) cannot flag a range error
+      if (t0 + key >= t_end) kr[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
     for (int j = 0; j < VG; ++j) {
@@ -1038,9 +1049,9 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(PrefillAttnArgs
 }  // namespace
 
 hipError_t launch_split_rows(const float* x, uint32_t ldx, const float* norm, float eps, uint32_t N, uint32_t Npad,
-                             uint32_t K, _Float16* xh, _Float16* xl, float* rs, hipStream_t s) {
+                             uint32_t K, _Float16* xh, _Float16* xl, float* rs, uint32_t* err, hipStream_t s) {
   if (Npad < N || Npad % 16 || K % KS) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(split_rows_kernel, dim3(Npad), dim3(256), 0, s, x, ldx, norm, eps, N, K, xh, xl, rs);
+  hipLaunchKernelGGL(split_rows_kernel, dim3(Npad), dim3(256), 0, s, x, ldx, norm, eps, N, K, xh, xl, rs, err);
   return hipGetLastError();
 }
 

@@ -59,6 +59,7 @@ class GenStats(ctypes.Structure):
         ("decode_ms", ctypes.c_double),
         ("n_frames", ctypes.c_uint32),
         ("graph_used", ctypes.c_uint32),
+        ("per_column_rerun", ctypes.c_uint32),
     ]
 
 
@@ -129,6 +130,8 @@ def load():
                                        ctypes.POINTER(f32), cp, sz]
     L.s2hip_op_sample_noalloc.argtypes = [vp, vp, sz, ctypes.POINTER(Sampler), ctypes.c_int64, u64p,
                                           ctypes.POINTER(u32), cp, sz]
+    L.s2hip_device_allocations.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    L.s2hip_device_allocations.restype = None
     L.s2hip_op_expf.argtypes = [vp, vp, sz, vp, cp, sz]
     L.s2hip_op_embed.argtypes = [vp, vp, sz, vp, cp, sz]
     L.s2hip_last_slow_profile.argtypes = [vp, ctypes.POINTER(SlowProfile)]

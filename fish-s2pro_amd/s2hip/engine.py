@@ -180,6 +180,7 @@ class Engine:
             "prefill_ms": stats.prefill_ms,
             "decode_ms": stats.decode_ms,
             "graph_used": bool(stats.graph_used),
+            "per_column_rerun": bool(stats.per_column_rerun),
         }
 
     def generate_codes_batch(self, prompts, max_new_tokens, temperature=0.0, top_p=1.0, top_k=0,
@@ -225,6 +226,7 @@ class Engine:
             "decode_ms": stats.decode_ms,
             "total_frames": stats.n_frames,
             "graph_used": bool(stats.graph_used),
+            "per_column_rerun": bool(stats.per_column_rerun),
         }
 
     # -- op level -------------------------------------------------------------

@@ -91,6 +91,11 @@ typedef struct {
   double decode_ms;  /* all frames: Fast-AR codebooks + Slow-AR step + sampling */
   uint32_t n_frames;
   uint32_t graph_used;
+  /* 1 when an activation beyond the range of the batched product (one more
+   * than 2^15 times the largest of the first 256 in its wave's share of the
+   * row) made the call run again from its inputs with every multi-column
+   * linear on the per-column paths, whose split scale covers the whole row */
+  uint32_t per_column_rerun;
 } s2hip_gen_stats;
 
 /* SlowArDecodeProfile (crates/fish_s2_infer/src/slow_ar.rs:248-319, filled by
@@ -240,6 +245,11 @@ int32_t s2hip_op_sample(s2hip_engine* engine, const float* logits, size_t n, con
 int32_t s2hip_op_sample_noalloc(s2hip_engine* engine, const float* logits, size_t n, const s2hip_sampler* sampler,
                                 int64_t always_include, uint64_t* rng_state, uint32_t* token_out, char* err,
                                 size_t err_cap);
+
+/* Test hook, no counterpart in the reference: the number of device
+ * allocations (hipMalloc) the dual-AR engines of this process have made so
+ * far, so that a test can check that an entry point allocates nothing. */
+void s2hip_device_allocations(uint64_t* count_out);
 
 /* The samplers' sequential f32 running sums (softmax normaliser, top-p
  * cumulative sum and draw of sample_token, sampling.rs:202-241, whose Rust

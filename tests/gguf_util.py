@@ -196,6 +196,67 @@ def toy_model(path, d, vocab, slow=None, fast=None, emb=None, cb_emb=None, fast_
     write(path, meta, tensors)
 
 
+def scale_rows(path, name, rows, factor):
+    """Multiplies rows `rows` of the F16 matrix `name` ([ne1][ne0]) by
+    `factor`, in place in the GGUF file."""
+    raw = bytearray(open(path, "rb").read())
+    off, dims, typ = _locate(raw, name)
+    assert typ == 1 and len(dims) == 2, (name, typ, dims)
+    ne0 = dims[0]
+    mat = np.frombuffer(raw, np.float16, ne0 * dims[1], off).reshape(dims[1], ne0).copy()
+    mat[rows] = (mat[rows].astype(np.float32) * factor).astype(np.float16)
+    raw[off:off + mat.nbytes] = mat.tobytes()
+    with open(path, "wb") as f:
+        f.write(raw)
+
+
+def _locate(raw, want):
+    """(absolute data offset, dims ne0 first, ggml type) of tensor `want`."""
+    pos = 4
+
+    def get(fmt):
+        nonlocal pos
+        v = struct.unpack_from(fmt, raw, pos)
+        pos += struct.calcsize(fmt)
+        return v[0]
+
+    def gstr():
+        n = get("<Q")
+        nonlocal pos
+        s = bytes(raw[pos:pos + n]).decode()
+        pos += n
+        return s
+
+    sizes = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+    def skip(t):
+        nonlocal pos
+        if t == 8:
+            gstr()
+        elif t == 9:
+            et, n = get("<I"), get("<Q")
+            for _ in range(n):
+                skip(et)
+        else:
+            pos += sizes[t]
+
+    _ver, n_t, n_kv = get("<I"), get("<Q"), get("<Q")
+    for _ in range(n_kv):
+        gstr()
+        skip(get("<I"))
+    found = None
+    for _ in range(n_t):
+        name = gstr()
+        nd = get("<I")
+        dims = [get("<Q") for _ in range(nd)]
+        typ, off = get("<I"), get("<Q")
+        if name == want:
+            found = (off, dims, typ)
+    start = (pos + 31) // 32 * 32
+    assert found is not None, want
+    return start + found[0], found[1], found[2]
+
+
 def read_tensors(path):
     """name -> numpy array ([ne1][ne0] for matrices) for F32 / F16 tensors."""
     raw = open(path, "rb").read()

@@ -90,6 +90,13 @@ def test_create_rejects_bad_config_without_gpu():
     err = ctypes.create_string_buffer(256)
     assert not L.s2hip_create(None, err, len(err))
     assert b"NULL" in err.value
+    # a NULL engine fails with a message, not a silent 0
+    err2 = ctypes.create_string_buffer(256)
+    assert L.s2hip_reset(None, err2, len(err2)) == 0 and b"NULL" in err2.value
+    # the allocation counter answers without a device
+    c = ctypes.c_uint64(123)
+    L.s2hip_device_allocations(ctypes.byref(c))
+    assert c.value == 0
 
 
 # Algorithmic HBM bytes per launch of each profiled w13 kernel: w1 and w3

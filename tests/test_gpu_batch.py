@@ -144,6 +144,40 @@ def test_batch_kv_f16_greedy_codes_match_oracle(tiny_gguf):
         assert np.array_equal(rb["requests"][b]["codes"], ro["codes"]), b
 
 
+def test_batch_with_an_outlier_channel_matches_oracle(model_dir, tmp_path):
+    """SwiGLU output channel 300 of every layer is ~1e4-1e5 times the others
+    (rows 300 of w1 and w3 scaled by 300): it lies past the first 256
+    elements of its wave's k range in the batched w2 product, beyond the
+    per-wave scale's headroom.  The call then runs again on the per-column
+    paths (whole-row scale) and every request's greedy codes match the
+    oracle."""
+    import shutil
+
+    import gguf_util
+
+    src = synth.ensure_gguf(synth.TINY, model_dir)
+    path = str(tmp_path / "tiny_outlier.gguf")
+    shutil.copyfile(src, path)
+    for pre, n in (("layers", synth.TINY.slow_layers), ("fast_layers", synth.TINY.fast_layers)):
+        for l in range(n):
+            for w in ("w1", "w3"):
+                gguf_util.scale_rows(path, f"{pre}.{l}.feed_forward.{w}.weight", [300], 300.0)
+    prompts = _prompts(3, seed=150)
+    e, o = _engine(path), _oracle(path)
+    rb = e.generate_codes_batch(prompts, 12, min_tokens_before_end=100, rng_states=[0, 1, 2])
+    assert rb["per_column_rerun"]
+    for b, pr in enumerate(prompts):
+        ro = o.generate_codes(pr, 12, 0.0, 1.0, 0, 100, b)
+        got = rb["requests"][b]
+        assert got["n_frames"] == ro["n_frames"] == 12
+        assert np.array_equal(got["codes"], ro["codes"]), b
+    # the engine keeps working on the batched product afterwards
+    rb2 = e.generate_codes_batch(prompts[:2], 4, min_tokens_before_end=100, rng_states=[0, 1])
+    for b in range(2):
+        ro = o.generate_codes(prompts[b], 4, 0.0, 1.0, 0, 100, b)
+        assert np.array_equal(rb2["requests"][b]["codes"], ro["codes"]), b
+
+
 def test_batch_with_large_norm_gains_matches_oracle(model_dir):
     """Every Slow and Fast linear of a 3-request batch runs the batched MFMA
     product; with RMSNorm gains of 100 the raw residual times the gain reaches

@@ -90,6 +90,16 @@ def test_batched_linear_activation_range(eng, ncol):
     got = eng.linear(raw, 1, in_dim, out_dim, x)
     for c in range(ncol):
         assert _rel(got[c], O.linear(x[c], raw, 1, in_dim, out_dim)) < 1e-4, c
+    # one channel 1e6 / 1e5 times the rest, past the first 256 elements of its
+    # wave's k range (beyond the per-wave scale's 2^15 headroom): the product
+    # is taken on the per-column path and still matches
+    for spike in (1e6, -1e5):
+        xs = rng.standard_normal((ncol, in_dim)).astype(np.float32)
+        xs[0, 300] = spike
+        xs[-1, 2000] = spike
+        got = eng.linear(raw, 1, in_dim, out_dim, xs)
+        for c in range(ncol):
+            assert _rel(got[c], O.linear(xs[c], raw, 1, in_dim, out_dim)) < 1e-4, (spike, c)
     for bad in (np.nan, np.inf):
         x[0, 5] = bad
         with pytest.raises(S2HipError, match="batched product"):

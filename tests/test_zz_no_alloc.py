@@ -2,7 +2,8 @@
 the existing one (s2hip_op_sample), through the C ABI: identical tokens and
 RNG states on consecutive calls (the second with fewer logits, so stale
 values left in the shared device array would show), at the 8191-logit limit,
-and a clear error beyond it."""
+and a clear error beyond it; the library's device-allocation count does not
+move across the allocation-free calls and grows across s2hip_op_sample's."""
 
 import ctypes
 
@@ -25,6 +26,12 @@ def _sample(L, h, fn, logits, T, top_p, top_k, always, rng):
     return ok, tok.value, st.value, err.value.decode()
 
 
+def _allocs(L):
+    c = ctypes.c_uint64(0)
+    L.s2hip_device_allocations(ctypes.byref(c))
+    return c.value
+
+
 def test_noalloc_sampler_matches_existing_entry_point(tiny_gguf):
     from s2hip import Engine
 
@@ -36,8 +43,11 @@ def test_noalloc_sampler_matches_existing_entry_point(tiny_gguf):
                 logits = (rng.standard_normal(n) * 2).astype(np.float32)
                 always = int(rng.integers(0, n)) if n > 100 else None
                 st = int(rng.integers(1, 1 << 62))
+                n0 = _allocs(L)
                 a = _sample(L, h, L.s2hip_op_sample, logits, T, top_p, top_k, always, st)
+                n1 = _allocs(L)
                 b = _sample(L, h, L.s2hip_op_sample_noalloc, logits, T, top_p, top_k, always, st)
+                assert n1 > n0 and _allocs(L) == n1, (n0, n1, _allocs(L))
                 assert a[0] == 1 and b[0] == 1, (a, b)
                 assert a[1:3] == b[1:3], (T, n, a, b)
         ok, _, st, msg = _sample(L, h, L.s2hip_op_sample_noalloc, np.zeros(8192, np.float32), 0.7, 0.9, 0, None, 5)
