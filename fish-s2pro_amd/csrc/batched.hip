@@ -37,6 +37,7 @@
 
 #include "expf_glibc.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace s2 {
 namespace {
@@ -178,15 +179,16 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
     }
     float m = fmaxf(fmaxf(fabsf(va.x), fabsf(va.y)), fmaxf(fabsf(va.z), fabsf(va.w)));
     m = fmaxf(m, fmaxf(fmaxf(fabsf(vb.x), fabsf(vb.y)), fmaxf(fabsf(vb.z), fabsf(vb.w))));
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    rm[j] = m;  // max of staged row 2 j + (lane >> 5)
+    rm[j] = row_reduce(m, [](float a, float b) { return fmaxf(a, b); });
   }
+  // staged row 2 j is lanes 0-31, row 2 j + 1 lanes 32-63: the max of each
+  // half from its two 16-lane rows, read into scalars
   float cmax = 0.0f;
 #pragma unroll
   for (int j = 0; j < LDX; ++j) {
-    const float v = __shfl(rm[j], int((n & 1u) << 5), 64);
-    cmax = (uint32_t(j) == (n >> 1)) ? v : cmax;
+    const float lo = fmaxf(lane_read_f32(rm[j], 0), lane_read_f32(rm[j], 16));
+    const float hi = fmaxf(lane_read_f32(rm[j], 32), lane_read_f32(rm[j], 48));
+    cmax = (uint32_t(j) == (n >> 1)) ? ((n & 1u) ? hi : lo) : cmax;
   }
   // cmax in [2^e, 2^(e+1)): scale by 2^-e (e clamped to +-100; 0 for zero,
   // subnormal or non-finite maxima -- a non-finite value still ends as a

@@ -23,6 +23,7 @@
 
 #include "codec.h"
 #include "expf_glibc.h"
+#include "wave.h"
 #include "sin_cw.h"
 
 namespace s2 {
@@ -433,14 +434,10 @@ __global__ __launch_bounds__(256) void codec_attn_kernel(const float* qkv, uint3
         sc[h2] = ((a0 + a1) + (a2 + a3)) * 0.125f;
       }
     }
-    float mx = fmaxf(sc[0], sc[1]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const float mx = wave_max(fmaxf(sc[0], sc[1]));
     const float e0 = lane < n ? expf_glibc(sc[0] - mx) : 0.0f;
     const float e1 = lane + 64u < n ? expf_glibc(sc[1] - mx) : 0.0f;
-    float sum = e0 + e1;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    const float sum = wave_sum(e0 + e1);
     const float inv = 1.0f / sum;
     pw[lane] = e0 * inv;
     pw[lane + 64u] = e1 * inv;
@@ -505,8 +502,7 @@ __global__ __launch_bounds__(256) void codec_dwconv_ln_kernel(const float* x, ui
     d[k] = acc;
     s += acc;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  s = wave_sum(s);
   if (lane == 0) red[wave] = s;
   __syncthreads();
   const float mean = ((red[0] + red[1]) + (red[2] + red[3])) / 1024.0f;
@@ -517,8 +513,7 @@ __global__ __launch_bounds__(256) void codec_dwconv_ln_kernel(const float* x, ui
     const float c = d[k] - mean;
     v += c * c;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  v = wave_sum(v);
   if (lane == 0) red[wave] = v;
   __syncthreads();
   const float var = ((red[0] + red[1]) + (red[2] + red[3])) / 1024.0f;

@@ -13,6 +13,7 @@
 
 #include "expf_glibc.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace s2 {
 namespace {
@@ -24,18 +25,6 @@ constexpr int SAMPLE_THREADS = 1024;
 constexpr uint32_t SAMPLE_MAX = 8192;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = WAVE / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
-  return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = WAVE / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
-  return v;
-}
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
@@ -1154,8 +1143,8 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
           *reinterpret_cast<float4*>(xs + c * XS + b * 32u + ((ch ^ qswz(b)) << 2)) = u;
           part += (u.x + u.y) + (u.z + u.w);
         }
-        part += __shfl_xor(part, 1, WAVE);
-        part += __shfl_xor(part, 2, WAVE);
+        part += dpp_f32<DPP_QUAD_XOR1>(part);
+        part += dpp_f32<DPP_QUAD_XOR2>(part);
         if ((lane & 3) == 0) xs[c * XS + NB * 32u + b] = part;
       }
     }
@@ -1910,8 +1899,7 @@ __device__ __forceinline__ double lcg_next_unit(uint64_t* s) {
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, SampleShared& sh) {
   constexpr uint32_t NW = SAMPLE_THREADS / WAVE;
   const uint32_t lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += uint32_t(__shfl_xor(int(v), off, WAVE));
+  v = wave_sum_u32(v);
   __syncthreads();
   if (lane == 0) sh.redk[wave] = v;
   __syncthreads();
@@ -2425,11 +2413,28 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
     a1 = fmaxf(a1, b1);
     ai = wi;
   };
+  // rows of 16 lanes by DPP exchanges (the mirrors pair already-merged quads
+  // and half-rows), then the four rows' values read into scalars
+  merge(m1, id1, m2, dpp_f32<DPP_QUAD_XOR1>(m1), dpp_u32<DPP_QUAD_XOR1>(id1), dpp_f32<DPP_QUAD_XOR1>(m2));
+  merge(m1, id1, m2, dpp_f32<DPP_QUAD_XOR2>(m1), dpp_u32<DPP_QUAD_XOR2>(id1), dpp_f32<DPP_QUAD_XOR2>(m2));
+  merge(m1, id1, m2, dpp_f32<DPP_ROW_HALF_MIRROR>(m1), dpp_u32<DPP_ROW_HALF_MIRROR>(id1),
+        dpp_f32<DPP_ROW_HALF_MIRROR>(m2));
+  merge(m1, id1, m2, dpp_f32<DPP_ROW_MIRROR>(m1), dpp_u32<DPP_ROW_MIRROR>(id1), dpp_f32<DPP_ROW_MIRROR>(m2));
+  {
+    float r1[4], r2[4];
+    uint32_t ri[4];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o1 = __shfl_xor(m1, off, WAVE), o2 = __shfl_xor(m2, off, WAVE);
-    const uint32_t oi = uint32_t(__shfl_xor(int(id1), off, WAVE));
-    merge(m1, id1, m2, o1, oi, o2);
+    for (int r = 0; r < 4; ++r) {
+      r1[r] = lane_read_f32(m1, 16 * r);
+      r2[r] = lane_read_f32(m2, 16 * r);
+      ri[r] = lane_read_u32(id1, 16 * r);
+    }
+    merge(r1[0], ri[0], r2[0], r1[1], ri[1], r2[1]);
+    merge(r1[2], ri[2], r2[2], r1[3], ri[3], r2[3]);
+    merge(r1[0], ri[0], r2[0], r1[2], ri[2], r2[2]);
+    m1 = r1[0];
+    id1 = ri[0];
+    m2 = r2[0];
   }
   const float nf = wave_sum(float(nfin));
   if (lane == 0) {

@@ -20,6 +20,7 @@
 
 #include "expf_glibc.h"
 #include "kernels.h"
+#include "wave.h"
 
 namespace s2 {
 namespace {
@@ -28,19 +29,11 @@ constexpr int WAVE = 64;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int off = WAVE / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, WAVE);
-  return v;
-}
+__device__ __forceinline__ float wave_sum_f(float v) { return wave_sum(v); }
 __device__ __forceinline__ float half_bits_to_float_p(uint16_t b) {
   return static_cast<float>(__builtin_bit_cast(_Float16, b));
 }
-__device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-  for (int off = WAVE / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, WAVE));
-  return v;
-}
+__device__ __forceinline__ float wave_max_f(float v) { return wave_max(v); }
 
 // ---------------------------------------------------------------------------
 // Activation split: one block per row n < Npad.
