@@ -15,6 +15,12 @@ and prompt (checked by sha256), then:
 * cfg5 (8 voice-clone requests of 1500 positions, batch 8, KV 2560):
   requests 0 and 1 of the batch bit-exact over 16 greedy frames, with every
   request's frame count.
+
+At the configs' full lengths (the oracle's fixtures cover the first frames):
+cfg2 (512 frames, KV 768) and cfg4 (1024 frames, KV 1280) run to the end of
+their caches with graph replay equal to direct launches, codes in range, the
+SeededRng stepped once per draw and the first 64 frames equal to the oracle's;
+cfg5 (1024 frames) equals its 8 requests' single calls up to logit ties.
 """
 
 import hashlib
@@ -24,7 +30,7 @@ import os
 import numpy as np
 import pytest
 
-from loop_util import at_boundary
+from loop_util import TIE_EPS, at_boundary
 from s2hip import synth
 
 pytestmark = pytest.mark.gpu
@@ -94,6 +100,23 @@ def _margins(req, t, cb):
         if d[0] == t and d[1] == cb:
             return d[3], d[4], d[5]
     raise KeyError((t, cb))
+
+
+def _replayed_gap(e, shape, prompt, codes, t, cb, a, b):
+    """Relative gap between the logits of codes a and b at draw (t, cb) of a
+    greedy trajectory, replayed on the engine one step at a time: the prompt,
+    then frames 0 .. t-1 through the Slow-AR (eval), then the semantic logits
+    (cb 0) or the Fast-AR logits over the frame's first cb codes."""
+    e.reset()
+    hidden, logits = e.eval(prompt, want_logits=(t == 0))
+    for f in range(t):
+        step = np.concatenate([[shape.semantic_begin + codes[0, f]], codes[:, f]]).astype(np.int32)
+        hidden, logits = e.eval(step, want_logits=(f == t - 1))
+    if cb == 0:
+        lg = logits[shape.semantic_begin:shape.semantic_end + 1]
+    else:
+        lg = e.fast_logits(hidden, codes[:cb, t])
+    return abs(float(lg[a]) - float(lg[b])) / max(1.0, abs(float(lg[a])))
 
 
 def _engine(path, fx):
@@ -168,3 +191,82 @@ def test_full_size_voice_clone_batch_of_8_bit_exact():
         assert diff is None, (f"request {req['index']}: first differing draw at frame {diff[0]} codebook "
                               f"{diff[1]}; oracle margins {_margins(req, *diff)}")
         assert got["rng_state"] == req["rng_state"]
+
+
+# --------------------------------------------- the configs' full lengths ----
+# generate.rs:117-221 at each workload's own length and KV size (the
+# fixtures above hold the oracle's first 64 frames; the oracle cannot afford
+# the rest in the build container).  Properties checked at full length:
+# every frame produced (no early im_end: min_tokens_before_end is above the
+# frame count), codes in range, graph replay == direct launches, the first
+# 64 frames equal to the oracle's, and the KV cache filled to its end.
+@pytest.mark.parametrize("name,frames,max_seq", [("cfg2", 512, 768), ("cfg4", 1024, 1280)])
+def test_full_length_generation_properties(name, frames, max_seq):
+    from s2hip import Engine
+
+    fx = _fixture(name)
+    shape, path = _model(fx)
+    req = fx["requests"][0]
+    prompt = _prompt(shape, fx, 0)
+    _check_prompt(prompt, req)
+    runs = []
+    for graph in (True, False):
+        with Engine(path, max_seq, fx["im_end_id"], use_graph=graph) as e:
+            runs.append(e.generate_codes(prompt, frames, 0.0, 1.0, 0, 1 << 30, req["rng_seed"]))
+            assert e.n_past == 256 + frames  # prompt + one Slow-AR step per frame
+    g, d = runs
+    assert g["n_frames"] == d["n_frames"] == frames
+    assert g["codes"].shape == (shape.num_codebooks, frames)
+    assert (g["codes"] >= 0).all() and (g["codes"] < shape.codebook_size).all()
+    assert np.array_equal(g["codes"], d["codes"]) and g["rng_state"] == d["rng_state"]
+    want = np.array(req["codes"], np.int32)
+    assert np.array_equal(g["codes"][:, :want.shape[1]], want)
+    # the greedy sampler steps the SeededRng once per draw, 10 draws per frame
+    s = req["rng_seed"]
+    for _ in range(10 * frames + 1):  # + the first semantic sample after prefill
+        s = (s * 6364136223846793005 + 1) & ((1 << 64) - 1)
+    assert g["rng_state"] == s
+    # one more frame does not fit the cache: KV overflow, as SlowArState::eval
+    with Engine(path, max_seq, fx["im_end_id"]) as e:
+        with pytest.raises(Exception, match="KV cache overflow"):
+            e.generate_codes(prompt, frames + 1, 0.0, 1.0, 0, 1 << 30, req["rng_seed"])
+
+
+def test_full_size_voice_clone_batch_equals_single_requests():
+    """cfg5 at its full length: 8 requests of 1500 positions, 1024 frames each,
+    batch 8, KV 2560.  Every request's frame count equals its own batch-1
+    generate_codes call, and so do its codes and RNG state, except that the
+    batch product and the one-column GEMVs round differently: where two codes'
+    logits tie (within TIE_EPS relative, measured by replaying the single
+    call's trajectory up to that draw) the two trajectories may part.  On the
+    MI355X, 4 of the 8 requests part, at gaps of 0 to 5e-6."""
+    from s2hip import Engine
+
+    fx = _fixture("cfg5")
+    shape, path = _model(fx)
+    n, frames, max_seq = fx["n_requests"], 1024, 2560
+    prompts = [_prompt(shape, fx, b) for b in range(n)]
+    for req in fx["requests"]:
+        _check_prompt(prompts[req["index"]], req)
+    with Engine(path, max_seq, fx["im_end_id"]) as e:
+        rb = e.generate_codes_batch(prompts, frames, 0.0, 1.0, 0, 1 << 30, [1 + b for b in range(n)])
+        assert [q["n_frames"] for q in rb["requests"]] == [frames] * n
+        for req in fx["requests"]:  # the oracle's first 16 frames
+            want = np.array(req["codes"], np.int32)
+            assert np.array_equal(rb["requests"][req["index"]]["codes"][:, :want.shape[1]], want)
+        parted = []
+        for b in range(n):
+            e.reset()
+            r1 = e.generate_codes(prompts[b], frames, 0.0, 1.0, 0, 1 << 30, 1 + b)
+            got = rb["requests"][b]
+            assert r1["n_frames"] == frames
+            diff = _first_difference(got["codes"], r1["codes"])
+            if diff is None:
+                assert got["rng_state"] == r1["rng_state"]
+                continue
+            # where the two trajectories part, the two codes' logits must tie
+            t, cb = diff
+            gap = _replayed_gap(e, shape, prompts[b], r1["codes"], t, cb, got["codes"][cb, t], r1["codes"][cb, t])
+            parted.append((b, t, cb, gap))
+            assert gap < TIE_EPS, f"request {b}: batch and single call part at frame {t} codebook {cb}, gap {gap}"
+        print("requests parting at a logit tie (request, frame, codebook, relative gap):", parted)
