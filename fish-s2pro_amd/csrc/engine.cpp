@@ -702,7 +702,9 @@ L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool n
                         uint32_t pct_end) const {
   L2Warm w{};
   if (!warm_blocks_ || ncol > 2 || !L.w || pct_end <= pct_begin || uses_bmm(L, L3, ncol)) return w;
-  if (L.qp && ncol <= 2) return w;  // the repacked planes are read, not these rows
+  // Q8_0 / Q4_0 GEMVs read the repacked planes, except one matrix with
+  // 2560-wide rows and an RMSNorm (wqkv, the heads): that stays on the GGUF rows
+  if (L.qp && ncol <= 2 && !(norm && !L3 && L.in == 2560)) return w;
   const uint32_t rpb = gemv_rows_per_block(L.in, L.out, norm, L3 != nullptr, ncol);
   const size_t span = size_t(rpb) * L.row_bytes;
   if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||
@@ -894,8 +896,10 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint
     sa.next_input = (cb + 1 < s.num_codebooks) ? fh_ : nullptr;
     sa.dim = s.dim;
     sa.n_seq = nseq;
-    // the next sub-step's first linear (one column per slot)
-    if (sa.next_input) sa.warm = warm_for(fast_[0].wqkv, nullptr, nseq, true, 0, warm_step_);
+    // the next sub-step's first linear (one column per slot); the general
+    // path (tens of microseconds on one CU, HBM idle) reads all of its rows
+    if (sa.next_input)
+      sa.warm = warm_for(fast_[0].wqkv, nullptr, nseq, true, 0, cfg.temperature > 0.0f ? 100u : warm_step_);
     HIPC(launch_sample_fast(sa, stream_));
     p0 += cps;
     cps = 1;

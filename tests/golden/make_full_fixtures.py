@@ -46,16 +46,16 @@ CONFIGS = {
     "cfg2": dict(shape="full", prompt=("synthetic", 256), max_seq=768, frames=64,
                  sampler=(0.0, 1.0, 0), rng=1,
                  what="full S2-Pro shape, f16, seed 1, 256-token prompt, greedy, KV 768"),
-    "cfg3": dict(shape="full_q8", prompt=("synthetic", 256), max_seq=768, frames=32,
+    "cfg3": dict(shape="full_q8", prompt=("synthetic", 256), max_seq=768, frames=64,
                  sampler=(0.7, 0.9, 0), rng=1,
                  what="full shape, Q8_0 linears, 256-token prompt, T 0.7 top-p 0.9 top-k 0, SeededRng seed 1"),
     "cfg4": dict(shape="full_q4", prompt=("synthetic", 256), max_seq=1280, frames=64,
                  sampler=(0.0, 1.0, 0), rng=1,
                  what="full shape, Q4_0 linears, 256-token prompt, greedy, KV 1280"),
     "cfg5": dict(shape="full", prompt=("voice_clone", 500, 1000), max_seq=2560, frames=16,
-                 sampler=(0.0, 1.0, 0), rng=1, requests=8, oracle_requests=(0, 1),
+                 sampler=(0.0, 1.0, 0), rng=1, requests=8, oracle_requests=(0, 1, 2, 3),
                  what="full shape, f16, 8 requests of 500 text ids + 1000 reference frames "
-                      "(1500 positions), greedy, batch 8, KV 2560; requests 0 and 1 run on the oracle"),
+                      "(1500 positions), greedy, batch 8, KV 2560; requests 0 to 3 run on the oracle"),
 }
 
 
