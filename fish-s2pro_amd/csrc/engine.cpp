@@ -173,17 +173,20 @@ class Engine {
 
   void gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
             const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row, uint32_t out_rows,
-            const uint32_t* done);
+            const uint32_t* done, const GreedyFold* fold = nullptr);
   // linear over ncol columns: GEMV kernels for 1-2, skinny MFMA for more
   // (bmm_waves: waves per tile when the batched product serves it, 0 = its default)
   void lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
            const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
-           uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves = 0);
+           uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves = 0, const GreedyFold* fold = nullptr);
   // ncol = nseq * cps columns of slots seq0 .. seq0 + nseq - 1 in h_
   void enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done);
   void enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done);
-  void enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done);
+  // fold (nullable): the first linear takes its input from the greedy sample
+  void enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done,
+                           const GreedyFold* fold = nullptr);
   void enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint32_t* done);
+  bool fold_greedy(const SamplerCfg& cfg, uint32_t nseq) const;
   void enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_stride);
   void enqueue_prefill(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
   void enqueue_prefill_gemv(const int32_t* prompt_dev, size_t n_tok, uint32_t seq);
@@ -241,11 +244,16 @@ class Engine {
   // then takes the per-column paths (two-column GEMV, or the skinny product
   // over rows split with a whole-row scale), which have no per-wave range.
   bool bmm_off_ = false;
-  bool any_f16_range(uint32_t nseq) const {
+  bool any_f16_range(uint32_t nseq) const { return any_err(nseq, ERR_F16_RANGE); }
+  bool any_err(uint32_t nseq, uint32_t bits) const {
     for (uint32_t b = 0; b < nseq; ++b)
-      if (st_host_[b].err & ERR_F16_RANGE) return true;
+      if (st_host_[b].err & bits) return true;
     return false;
   }
+  // the Fast-AR greedy samples run as sampler kernels (after a tie at a
+  // folded sample's max)
+  bool fold_off_ = false;
+  bool fold_env_off_ = false;  // S2HIP_NO_GREEDY_FOLD: always the sampler kernel
   // L2 warming of the output projection by decode attention
   uint32_t warm_blocks_ = 256;            // warming blocks per kernel (0: off)
   uint32_t warm_depth_ = 4;               // 16-byte loads per thread in flight
@@ -298,6 +306,7 @@ class Engine {
   uint32_t graph_nseq_ = 0;
   uint64_t graph_kv_gen_ = 0;
   bool graph_bmm_off_ = false;
+  bool graph_fold_off_ = false;
 };
 
 Engine::Engine(const s2hip_config& cfg) {
@@ -444,6 +453,7 @@ Engine::Engine(const s2hip_config& cfg) {
   // store-wait + counter + reload chain measures slower than the kernel
   // boundary it replaces: 18.7 vs 13.2 us at T = 384 on the S2-Pro shape)
   attn_mode_ = getenv("S2HIP_ATTN_FUSED") ? ATTN_FUSED : ATTN_SPLIT;
+  fold_env_off_ = getenv("S2HIP_NO_GREEDY_FOLD") != nullptr;
   prefill_gemv_ = getenv("S2HIP_PREFILL_GEMV") != nullptr;
   attn_chunks_ = attention_chunks(s.max_seq_len, attn_mode_);
   // S2HIP_BMM_MIN_COLS=n: F16 linears over >= n columns use the batched MFMA
@@ -614,7 +624,8 @@ void Engine::build_rope(float2* dst, uint32_t positions, uint32_t hd, float base
 
 void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
                   const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row, uint32_t out_rows,
-                  const uint32_t* done) {
+                  const uint32_t* done, const GreedyFold* fold) {
+  if (fold && ncol != 1) fail("the greedy fold feeds one column");
   uint32_t c = 0;
   while (c < ncol) {
     uint32_t w = 8;
@@ -638,6 +649,7 @@ void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, con
     a.qs = L.qs;
     a.qp3 = L3 ? L3->qp : nullptr;
     a.qs3 = L3 ? L3->qs : nullptr;
+    if (fold) a.fold = *fold;
     HIPC(launch_gemv(L.type, epi, int(w), a, stream_));
     c += w;
   }
@@ -677,7 +689,11 @@ bool Engine::uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const {
 
 void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
                  const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
-                 uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves) {
+                 uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves, const GreedyFold* fold) {
+  if (fold) {  // one column (checked by gemv), never on the batched product
+    gemv(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, row_base, extra_row, out_rows, done, fold);
+    return;
+  }
   if (uses_bmm(L, L3, ncol)) {
     bmm(L, L3, epi, ncol, x, ldx, norm, eps, y, ldy, done, &st_->err, bmm_waves);
     return;
@@ -824,14 +840,16 @@ void Engine::enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, co
 
 // Fast-AR layers (forward_prefill, fast_ar.rs:245-358) over nseq slots with cps consecutive
 // positions each from p0 (every slot is at the same Fast-AR position).
-void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done) {
+void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done,
+                                 const GreedyFold* fold) {
   const s2hip_spec& s = spec;
   const uint32_t fq = s.fast_heads * s.fast_head_dim, fkv = s.fast_kv_heads * s.fast_head_dim;
   const uint32_t w = fq + 2 * fkv;
   const uint32_t ncol = nseq * cps;
   for (uint32_t l = 0; l < s.fast_layers; ++l) {
     const FastLayer& L = fast_[l];
-    lin(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out, done);
+    lin(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out, done,
+        0, l == 0 ? fold : nullptr);
     AttnArgs aa{};
     aa.qkv = fqkv_;
     aa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
@@ -874,17 +892,43 @@ void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const
 // generate_codebooks_for_semantic (fast_ar.rs:440-470), incremental, for the
 // slots 0 .. nseq - 1: sub-step 1 runs positions 0 (slow hidden) and 1
 // (fast_emb[code0]) together, each later sub-step appends one position.  The
-// sampler writes each slot's next input row.
+// sampler writes each slot's next input row.  A greedy sample of one slot
+// before a further sub-step is folded into that sub-step's first linear
+// (GreedyFold): one kernel less per codebook; a tie at the max sets
+// ERR_GREEDY_TIE and the caller runs again with the sampler kernel.
+bool Engine::fold_greedy(const SamplerCfg& cfg, uint32_t nseq) const {
+  const s2hip_spec& s = spec;
+  const DevLin& L = fast_[0].wqkv;
+  if (fold_off_ || fold_env_off_ || nseq != 1 || cfg.temperature > 0.0f || s.codebook_size % 4 || s.fast_layers == 0) return false;
+  // the one-column wqkv kernel (the GGUF-row kernel for every weight type)
+  if (L.type == W_F16) return s.dim == 512 || s.dim == 1536 || s.dim == 2560;
+  return (L.type == W_Q8_0 || L.type == W_Q4_0) && s.dim == 2560;
+}
+
 void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint32_t* done) {
   const s2hip_spec& s = spec;
   HIPC(launch_fast_begin(st_, hn_, fast_emb_, fh_, s.dim, s.codebook_size, s.semantic_begin, s.semantic_end, nseq,
                          stream_));
+  const bool fold = fold_greedy(cfg, nseq);
+  GreedyFold gf{};
   uint32_t cps = 2, p0 = 0;
   for (uint32_t cb = 1; cb < s.num_codebooks; ++cb) {
-    enqueue_fast_layers(nseq, cps, p0, done);
+    enqueue_fast_layers(nseq, cps, p0, done, gf.logits ? &gf : nullptr);
     // the last position of each slot: rows cps - 1, 2 cps - 1, ...
     lin(fast_out_, nullptr, EPI_STORE, nseq, fh_ + size_t(cps - 1) * s.dim, cps * s.dim, fast_norm_, s.fast_eps,
         flogits_, s.codebook_size, 0, NO_ROW, s.codebook_size, done);
+    p0 += cps;
+    cps = 1;
+    if (fold && cb + 1 < s.num_codebooks) {
+      gf.logits = flogits_;
+      gf.n = s.codebook_size;
+      gf.emb = fast_emb_;
+      gf.st = st_;
+      gf.cb_index = cb;
+      gf.x_out = fh_;
+      continue;
+    }
+    gf = GreedyFold{};
     SampleArgs sa{};
     sa.logits = flogits_;
     sa.n = s.codebook_size;
@@ -901,8 +945,6 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint
     if (sa.next_input)
       sa.warm = warm_for(fast_[0].wqkv, nullptr, nseq, true, 0, cfg.temperature > 0.0f ? 100u : warm_step_);
     HIPC(launch_sample_fast(sa, stream_));
-    p0 += cps;
-    cps = 1;
   }
 }
 
@@ -1219,6 +1261,7 @@ void Engine::check_state_err(uint32_t nseq) {
     if (st_host_[b].err & ERR_SAMPLER) fail("sampler failure" + who);
     if (st_host_[b].err & ERR_F16_RANGE) fail("activation not finite or beyond the range of the batched product");
     if (st_host_[b].err & ERR_NONFINITE) fail("activation not finite");
+    if (st_host_[b].err & ERR_GREEDY_TIE) fail("tie at a folded greedy sample" + who);
   }
 }
 
@@ -1318,15 +1361,20 @@ void Engine::fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampl
   enqueue_fast_frame(SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, 1, nullptr);
   HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
-  if (!bmm_off_ && any_f16_range(1)) {  // again on the per-column paths (as in generate)
-    bmm_off_ = true;
+  const bool range = !bmm_off_ && any_f16_range(1), tie = !fold_off_ && any_err(1, ERR_GREEDY_TIE);
+  if (range || tie) {  // again on the per-column paths / with the sampler kernels (as in generate)
+    const bool bmm0 = bmm_off_, fold0 = fold_off_;
+    bmm_off_ = bmm_off_ || range;
+    fold_off_ = fold_off_ || tie;
     try {
       fast_codebooks(hidden, sem, smp, rng, codes);
     } catch (...) {
-      bmm_off_ = false;
+      bmm_off_ = bmm0;
+      fold_off_ = fold0;
       throw;
     }
-    bmm_off_ = false;
+    bmm_off_ = bmm0;
+    fold_off_ = fold0;
     return;
   }
   check_state_err();
@@ -1439,6 +1487,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   if (use_graph && launched < max_frames) {
     const bool stale = !graph_exec_ || graph_codes_ != codes_dev_ || graph_codes_stride_ != ncodes ||
                        graph_nseq_ != nseq || graph_kv_gen_ != kv_gen_ || graph_bmm_off_ != bmm_off_ ||
+                       graph_fold_off_ != fold_off_ ||
                        graph_cfg_.temperature != cfg.temperature ||
                        graph_cfg_.top_p != cfg.top_p || graph_cfg_.top_k != cfg.top_k;
     if (stale) {
@@ -1467,6 +1516,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
       graph_nseq_ = nseq;
       graph_kv_gen_ = kv_gen_;
       graph_bmm_off_ = bmm_off_;
+      graph_fold_off_ = fold_off_;
     }
   }
   // Frames in batches; the done flag of batch i is read while batch i+1 runs.
@@ -1504,20 +1554,29 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   HIPC(hipEventElapsedTime(&ms_prefill, ev[0], ev[1]));
   HIPC(hipEventElapsedTime(&ms_decode, ev[1], ev[2]));
   for (auto& e : ev) (void)hipEventDestroy(e);
-  if (!bmm_off_ && any_f16_range(nseq)) {
+  const bool range = !bmm_off_ && any_f16_range(nseq), tie = !fold_off_ && any_err(nseq, ERR_GREEDY_TIE);
+  if (range || tie) {
     // An activation beyond the batched product's per-wave range (one more
-    // than 2^15 times the largest of the first 256 of its wave's k range):
-    // the whole call runs again from its inputs (rngs and codes are only
-    // written below) with the per-column paths.
-    bmm_off_ = true;
+    // than 2^15 times the largest of the first 256 of its wave's k range),
+    // or a tie at the max of a folded greedy sample: the whole call runs
+    // again from its inputs (rngs and codes are only written below) with
+    // the per-column paths / the sampler kernels.
+    const bool bmm0 = bmm_off_, fold0 = fold_off_;
+    bmm_off_ = bmm_off_ || range;
+    fold_off_ = fold_off_ || tie;
     try {
       generate(nseq, prompts, cols, p, rngs, codes, n_frames, stats);
     } catch (...) {
-      bmm_off_ = false;
+      bmm_off_ = bmm0;
+      fold_off_ = fold0;
       throw;
     }
-    bmm_off_ = false;
-    if (stats) stats->per_column_rerun = 1;
+    bmm_off_ = bmm0;
+    fold_off_ = fold0;
+    if (stats) {
+      stats->per_column_rerun = stats->per_column_rerun || range;
+      stats->greedy_rerun = stats->greedy_rerun || tie;
+    }
     return;
   }
   check_state_err(nseq);
@@ -1541,6 +1600,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
     stats->n_frames = total;
     stats->graph_used = use_graph ? 1u : 0u;
     stats->per_column_rerun = 0;
+    stats->greedy_rerun = 0;
   }
 }
 

@@ -33,7 +33,14 @@ struct DevState {
   uint32_t codes_frame[16];  // codebook ids of the frame being built
 };
 
-enum : uint32_t { ERR_TOKEN_RANGE = 1u, ERR_KV_OVERFLOW = 2u, ERR_SAMPLER = 4u, ERR_F16_RANGE = 8u, ERR_NONFINITE = 16u };
+enum : uint32_t {
+  ERR_TOKEN_RANGE = 1u,
+  ERR_KV_OVERFLOW = 2u,
+  ERR_SAMPLER = 4u,
+  ERR_F16_RANGE = 8u,
+  ERR_NONFINITE = 16u,
+  ERR_GREEDY_TIE = 32u,  // a folded greedy sample met a tie (the call re-runs with the sampler kernel)
+};
 constexpr uint32_t NO_ROW = 0xffffffffu;
 
 // Weight rows of the GEMV launched next, read into L2 by extra blocks of a
@@ -53,6 +60,21 @@ struct L2Warm {
   uint32_t blocks;       // warming blocks, multiple of 8
   uint32_t depth;        // 16-byte loads per thread in flight: 4, 8 or 16
 };
+// The Fast-AR greedy sample folded into the next sub-step's first linear
+// (one column, RMSNorm): every block reduces the codebook logits to their
+// argmax and reads x = emb[argmax] (f16 rows of `in` elements) instead of x;
+// block 0 also writes x to x_out, the code to st->codes_frame[cb_index] and
+// steps st->rng once, as the sampler kernel would.  A maximum that is not
+// unique within 1e-6 (or not finite) sets ERR_GREEDY_TIE.
+struct GreedyFold {
+  const float* logits;   // nullptr: no fold
+  uint32_t n;            // codebook size (a multiple of 4)
+  const uint16_t* emb;   // [n][in] f16
+  DevState* st;
+  uint32_t cb_index;
+  float* x_out;          // [in]
+};
+
 struct GemvArgs {
   const uint8_t* w;      // weight rows
   const uint8_t* w3;     // second matrix for SwiGLU epilogues (same shape)
@@ -75,6 +97,7 @@ struct GemvArgs {
   const uint8_t* qp3;
   const uint16_t* qs;
   const uint16_t* qs3;
+  GreedyFold fold;       // fold.logits != nullptr: x comes from the greedy sample
 };
 
 // Q8_0 / Q4_0 rows repacked for the decode GEMV: block b of row r (32

@@ -52,6 +52,65 @@ __device__ const float kUnitGain[256] = {
 };
 
 // ---------------------------------------------------------------------------
+// Greedy keys: the largest value m1 with the smallest id among its copies and
+// the second largest m2 (a second copy of the largest counts), so that the
+// reference's greedy test -- one value within 1e-6 of the max -- holds
+// exactly when m2 is not within 1e-6 of m1 (x -> |x - M| never increases for
+// x <= M).  Values that are not > -inf (masked, -inf, NaN) take no part.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void greedy_add(float& m1, uint32_t& id1, float& m2, float v, uint32_t id) {
+  if (v > m1) {
+    m2 = m1;
+    m1 = v;
+    id1 = id;
+  } else {
+    if (v == m1) id1 = min(id1, id);
+    m2 = fmaxf(m2, v);
+  }
+}
+
+__device__ __forceinline__ void greedy_merge(float& a1, uint32_t& ai, float& a2, float b1, uint32_t bi, float b2) {
+  const uint32_t wi = a1 > b1 ? ai : (b1 > a1 ? bi : min(ai, bi));
+  a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+  a1 = fmaxf(a1, b1);
+  ai = wi;
+}
+
+// The wave's keys in every lane: rows of 16 lanes by DPP exchanges (the
+// mirrors pair already-merged quads and half-rows), then the four rows' keys
+// read into scalars.  All 64 lanes active.
+__device__ __forceinline__ void greedy_wave(float& m1, uint32_t& id1, float& m2) {
+  greedy_merge(m1, id1, m2, dpp_f32<DPP_QUAD_XOR1>(m1), dpp_u32<DPP_QUAD_XOR1>(id1), dpp_f32<DPP_QUAD_XOR1>(m2));
+  greedy_merge(m1, id1, m2, dpp_f32<DPP_QUAD_XOR2>(m1), dpp_u32<DPP_QUAD_XOR2>(id1), dpp_f32<DPP_QUAD_XOR2>(m2));
+  greedy_merge(m1, id1, m2, dpp_f32<DPP_ROW_HALF_MIRROR>(m1), dpp_u32<DPP_ROW_HALF_MIRROR>(id1),
+               dpp_f32<DPP_ROW_HALF_MIRROR>(m2));
+  greedy_merge(m1, id1, m2, dpp_f32<DPP_ROW_MIRROR>(m1), dpp_u32<DPP_ROW_MIRROR>(id1), dpp_f32<DPP_ROW_MIRROR>(m2));
+  float r1[4], r2[4];
+  uint32_t ri[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    r1[r] = lane_read_f32(m1, 16 * r);
+    r2[r] = lane_read_f32(m2, 16 * r);
+    ri[r] = lane_read_u32(id1, 16 * r);
+  }
+  greedy_merge(r1[0], ri[0], r2[0], r1[1], ri[1], r2[1]);
+  greedy_merge(r1[2], ri[2], r2[2], r1[3], ri[3], r2[3]);
+  greedy_merge(r1[0], ri[0], r2[0], r1[2], ri[2], r2[2]);
+  m1 = r1[0];
+  id1 = ri[0];
+  m2 = r2[0];
+}
+
+// SeededRng state step (the draw is the top 53 bits of the new state)
+__device__ __forceinline__ uint64_t lcg_step(uint64_t s) { return s * 6364136223846793005ull + 1ull; }
+
+// The greedy test on a merged key: `count` values took part.  +inf as the
+// max fails it (inf - inf is NaN), as the reference counts no value then.
+__device__ __forceinline__ bool greedy_unique(uint32_t count, float m1, float m2) {
+  return count > 0 && fabsf(m1 - m1) < 1e-6f && !(fabsf(m2 - m1) < 1e-6f);
+}
+
+// ---------------------------------------------------------------------------
 // Raw weight payload for 8 consecutive elements, loaded first and decoded
 // later so a wave can keep many independent 16-byte loads in flight.
 // ---------------------------------------------------------------------------
@@ -762,32 +821,61 @@ __device__ __forceinline__ void l2_warm(const L2Warm& w, uint32_t L, uint32_t r,
 //   waits before the two barriers cover them and not the weights (vector
 //   memory counters retire in order), and the LDS staging overlaps the HBM
 //   latency of the weight rows.  One row (two for SwiGLU: w1 and w3) per wave.
+//
+// FOLD (one column, RMSNorm, store): x is emb[argmax of fold.logits], the
+//   greedy sample of the previous sub-step (GreedyFold).  The logit loads go
+//   first, then the first half of the weight loads; the block reduces the
+//   greedy keys while those are in flight, loads the embedding row, and only
+//   then issues the rest of the weights, so the wait for the row drains only
+//   the loads issued before it.
 // ---------------------------------------------------------------------------
-template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, bool NORM>
+template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, bool NORM, bool FOLD = false>
 __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows, const uint8_t* w3_rows, const float* x_in,
                                                               const float* gain, const uint32_t* done_ptr,
                                                               uint32_t row_bytes, uint32_t out, uint32_t row_base,
                                                               uint32_t extra_row, GemvArgs a) {
   constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  static_assert(!FOLD || (NCOL == 1 && NORM && EPI == EPI_STORE), "the greedy fold feeds one normalised column");
   constexpr uint32_t IN = uint32_t(KIT) * WAVE * 8;
   constexpr int KW = (KIT + WPB - 1) / WPB;
+  constexpr uint32_t NT = 64u * WPB;
+  // FOLD: weight steps loaded before the embedding row (the rest after it)
+  constexpr int KA = FOLD ? (KIT + 1) / 2 : KIT;
   __shared__ float4 xs[NCOL][IN / 4];
   __shared__ float red[NCOL][WPB];
+  __shared__ float fold_m1[FOLD ? WPB : 1], fold_m2[FOLD ? WPB : 1];
+  __shared__ uint32_t fold_id[FOLD ? WPB : 1], fold_cnt[FOLD ? WPB : 1];
   const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x >> 6;
   const uint32_t row = blockIdx.x * WPB + wave;
 
   // 1. this wave's steps of x and of the gain (steps past KIT re-read the last
-  //    step; they are not used)
+  //    step; they are not used); FOLD: the logits instead of x
   float4 xv[NCOL][KW][2], gv[KW][2];
+  float4 lg[2];
+  uint32_t st_done = 0;
+  uint64_t st_rng = 0;
+  if constexpr (FOLD) {
+    const float4* l4 = reinterpret_cast<const float4*>(a.fold.logits);
+    const uint32_t n4 = a.fold.n / 4u;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t i = threadIdx.x + uint32_t(r) * NT;
+      lg[r] = i < n4 ? l4[i] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+    st_done = a.fold.st->done;  // uniform: scalar loads, no vector wait later
+    st_rng = a.fold.st->rng;
+  }
 #pragma unroll
   for (int j = 0; j < KW; ++j) {
     const int k = min(wave + j * WPB, KIT - 1);
     const uint32_t e = k * 512 + lane * 8;
+    if constexpr (!FOLD) {
 #pragma unroll
-    for (int c = 0; c < NCOL; ++c) {
-      const float* xc = x_in + size_t(c) * a.ldx + e;
-      xv[c][j][0] = *reinterpret_cast<const float4*>(xc);
-      xv[c][j][1] = *reinterpret_cast<const float4*>(xc + 4);
+      for (int c = 0; c < NCOL; ++c) {
+        const float* xc = x_in + size_t(c) * a.ldx + e;
+        xv[c][j][0] = *reinterpret_cast<const float4*>(xc);
+        xv[c][j][1] = *reinterpret_cast<const float4*>(xc + 4);
+      }
     }
     if constexpr (NORM) {
       gv[j][0] = *reinterpret_cast<const float4*>(gain + e);
@@ -802,9 +890,76 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
   Raw8<WT> wb[KIT];
   Raw8<WT> wb3[DUAL ? KIT : 1];
 #pragma unroll
-  for (int k = 0; k < KIT; ++k) {
+  for (int k = 0; k < KA; ++k) {
     wb[k] = load_raw<WT>(rp, k * 512 + lane * 8);
     if constexpr (DUAL) wb3[k] = load_raw<WT>(rp3, k * 512 + lane * 8);
+  }
+  uint32_t fold_tok = 0, fold_tie = 0;
+  if constexpr (FOLD) {
+    // greedy keys of the logits (ids 4 i .. 4 i + 3 for float4 i)
+    float m1 = -INFINITY, m2 = -INFINITY;
+    uint32_t id1 = 0xffffffffu, cnt = 0;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t id0 = 4u * (threadIdx.x + uint32_t(r) * NT);
+      const float v4[4] = {lg[r].x, lg[r].y, lg[r].z, lg[r].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (v4[c] > -INFINITY) {
+          ++cnt;
+          greedy_add(m1, id1, m2, v4[c], id0 + uint32_t(c));
+        }
+      }
+    }
+    const float4* l4 = reinterpret_cast<const float4*>(a.fold.logits);
+    for (uint32_t i = threadIdx.x + 2u * NT; i < a.fold.n / 4u; i += NT) {
+      const float4 q = l4[i];
+      const float v4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (v4[c] > -INFINITY) {
+          ++cnt;
+          greedy_add(m1, id1, m2, v4[c], 4u * i + uint32_t(c));
+        }
+      }
+    }
+    greedy_wave(m1, id1, m2);
+    cnt = wave_sum_u32(cnt);
+    if (lane == 0) {
+      fold_m1[wave] = m1;
+      fold_m2[wave] = m2;
+      fold_id[wave] = id1;
+      fold_cnt[wave] = cnt;
+    }
+    __syncthreads();
+    float a1 = fold_m1[0], a2 = fold_m2[0];
+    uint32_t ai = fold_id[0], c = fold_cnt[0];
+#pragma unroll
+    for (int w = 1; w < WPB; ++w) {
+      greedy_merge(a1, ai, a2, fold_m1[w], fold_id[w], fold_m2[w]);
+      c += fold_cnt[w];
+    }
+    // no finite logit: the reference returns id 0 (a draw is still taken)
+    fold_tok = c > 0 ? ai : 0u;
+    fold_tie = (c > 0 && !greedy_unique(c, a1, a2)) ? 1u : 0u;
+    // the embedding row (f16) of the sample
+    const uint16_t* er = a.fold.emb + size_t(fold_tok) * IN;
+#pragma unroll
+    for (int j = 0; j < KW; ++j) {
+      const int k = min(wave + j * WPB, KIT - 1);
+      const uint4 raw = *reinterpret_cast<const uint4*>(er + k * 512 + lane * 8);
+      const uint32_t h[4] = {raw.x, raw.y, raw.z, raw.w};
+      float f[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f[2 * i] = half_bits_to_float(uint16_t(h[i] & 0xffffu));
+        f[2 * i + 1] = half_bits_to_float(uint16_t(h[i] >> 16));
+      }
+      xv[0][j][0] = make_float4(f[0], f[1], f[2], f[3]);
+      xv[0][j][1] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+#pragma unroll
+    for (int k = KA; k < KIT; ++k) wb[k] = load_raw<WT>(rp, k * 512 + lane * 8);
   }
   const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
   // the argument-block fields used later are read now, while the loads above
@@ -861,6 +1016,27 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
     }
   }
   __syncthreads();
+  if constexpr (FOLD) {
+    // the sampler's side effects, once: the next input row (as f32), the
+    // code, one SeededRng step
+    if (blockIdx.x == 0 && !st_done) {
+#pragma unroll
+      for (int j = 0; j < KW; ++j) {
+        const int k = wave + j * WPB;
+        if (k < KIT) {
+          float* xo = a.fold.x_out + k * 512 + lane * 8;
+          *reinterpret_cast<float4*>(xo) = xv[0][j][0];
+          *reinterpret_cast<float4*>(xo + 4) = xv[0][j][1];
+        }
+      }
+      if (threadIdx.x == 0) {
+        DevState* st = a.fold.st;
+        st->rng = lcg_step(st_rng);
+        st->codes_frame[a.fold.cb_index] = fold_tok;
+        if (fold_tie) atomicOr(&st->err, ERR_GREEDY_TIE);
+      }
+    }
+  }
   if (done) return;
   // 5. dot products against the LDS copy
   float acc[NCOL], acc3[NCOL];
@@ -906,13 +1082,31 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
   }
 }
 
-template <uint32_t WT, int NCOL, int EPI, int KIT, bool NORM = true, int WPB = 8>
+template <uint32_t WT, int NCOL, int EPI, int KIT, bool NORM = true, int WPB = 8, bool FOLD = false>
 hipError_t gemv_n_launch(const GemvArgs& a, hipStream_t s) {
   const dim3 grid((a.out + WPB - 1) / WPB);
   if (a.row_bytes > UINT32_MAX) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB, NORM>), grid, dim3(64 * WPB), 0, s, a.w, a.w3, a.x,
+  hipLaunchKernelGGL((gemv_n_kernel<WT, NCOL, EPI, KIT, WPB, NORM, FOLD>), grid, dim3(64 * WPB), 0, s, a.w, a.w3, a.x,
                      a.norm, a.done, uint32_t(a.row_bytes), a.out, a.row_base, a.extra_row, a);
   return hipGetLastError();
+}
+
+// The greedy fold's shapes: one column into an RMSNorm + store linear with
+// 512 / 1536 / 2560-wide rows (the Fast-AR wqkv of the S2-Pro family).
+template <uint32_t WT>
+hipError_t gemv_fold_launch(const GemvArgs& a, hipStream_t s) {
+  if (!a.norm || !a.fold.emb || !a.fold.st || !a.fold.x_out || a.fold.n == 0 || a.fold.n % 4 ||
+      reinterpret_cast<uintptr_t>(a.fold.logits) % 16 || reinterpret_cast<uintptr_t>(a.fold.emb) % 16 ||
+      reinterpret_cast<uintptr_t>(a.fold.x_out) % 16 || a.fold.cb_index >= 16)
+    return hipErrorInvalidValue;
+  switch (a.in) {
+    case 512: return gemv_n_launch<WT, 1, EPI_STORE, 1, true, 8, true>(a, s);
+    case 1536: return gemv_n_launch<WT, 1, EPI_STORE, 3, true, 8, true>(a, s);
+    case 2560:
+      if (a.out <= 4096) return gemv_n_launch<WT, 1, EPI_STORE, 5, true, 16, true>(a, s);
+      return gemv_n_launch<WT, 1, EPI_STORE, 5, true, 12, true>(a, s);
+    default: return hipErrorNotSupported;
+  }
 }
 
 // Row shapes of the S2-Pro family: 512 / 1536 (tiny), 2560, 4096, 9728.
@@ -1890,7 +2084,7 @@ struct SampleShared {
 };
 
 __device__ __forceinline__ double lcg_next_unit(uint64_t* s) {
-  *s = *s * 6364136223846793005ull + 1ull;
+  *s = lcg_step(*s);
   const uint64_t mant = (*s >> 11) & ((1ull << 53) - 1ull);
   return double(mant) / double(1ull << 53);
 }
@@ -2384,12 +2578,7 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
                                 uint32_t* err) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr uint32_t NW = SAMPLE_THREADS / WAVE;
-  // One pass: the finite count, the largest value with the smallest id among
-  // its copies, and the second largest value (a second copy of the largest
-  // counts).  The greedy test of the reference -- one value within 1e-6 of
-  // the max -- holds exactly when the second largest is not within 1e-6 of
-  // it: x -> |x - M| never increases for x <= M, so no smaller value is
-  // within 1e-6 when the second largest is not.
+  // One pass: the finite count and the greedy keys (greedy_add)
   float m1 = -INFINITY, m2 = -INFINITY;
   uint32_t id1 = 0xffffffffu, nfin = 0;
   for (uint32_t i = tid; i < n; i += SAMPLE_THREADS) {
@@ -2397,45 +2586,10 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
     const float v = (int64_t(id) == masked) ? -INFINITY : logits[i];
     if (v > -INFINITY) {
       ++nfin;
-      if (v > m1) {
-        m2 = m1;
-        m1 = v;
-        id1 = id;
-      } else {
-        if (v == m1) id1 = min(id1, id);
-        m2 = fmaxf(m2, v);
-      }
+      greedy_add(m1, id1, m2, v, id);
     }
   }
-  auto merge = [](float& a1, uint32_t& ai, float& a2, float b1, uint32_t bi, float b2) {
-    const uint32_t wi = a1 > b1 ? ai : (b1 > a1 ? bi : min(ai, bi));
-    a2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
-    a1 = fmaxf(a1, b1);
-    ai = wi;
-  };
-  // rows of 16 lanes by DPP exchanges (the mirrors pair already-merged quads
-  // and half-rows), then the four rows' values read into scalars
-  merge(m1, id1, m2, dpp_f32<DPP_QUAD_XOR1>(m1), dpp_u32<DPP_QUAD_XOR1>(id1), dpp_f32<DPP_QUAD_XOR1>(m2));
-  merge(m1, id1, m2, dpp_f32<DPP_QUAD_XOR2>(m1), dpp_u32<DPP_QUAD_XOR2>(id1), dpp_f32<DPP_QUAD_XOR2>(m2));
-  merge(m1, id1, m2, dpp_f32<DPP_ROW_HALF_MIRROR>(m1), dpp_u32<DPP_ROW_HALF_MIRROR>(id1),
-        dpp_f32<DPP_ROW_HALF_MIRROR>(m2));
-  merge(m1, id1, m2, dpp_f32<DPP_ROW_MIRROR>(m1), dpp_u32<DPP_ROW_MIRROR>(id1), dpp_f32<DPP_ROW_MIRROR>(m2));
-  {
-    float r1[4], r2[4];
-    uint32_t ri[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      r1[r] = lane_read_f32(m1, 16 * r);
-      r2[r] = lane_read_f32(m2, 16 * r);
-      ri[r] = lane_read_u32(id1, 16 * r);
-    }
-    merge(r1[0], ri[0], r2[0], r1[1], ri[1], r2[1]);
-    merge(r1[2], ri[2], r2[2], r1[3], ri[3], r2[3]);
-    merge(r1[0], ri[0], r2[0], r1[2], ri[2], r2[2]);
-    m1 = r1[0];
-    id1 = ri[0];
-    m2 = r2[0];
-  }
+  greedy_wave(m1, id1, m2);
   const float nf = wave_sum(float(nfin));
   if (lane == 0) {
     sh.redf[wave] = m1;
@@ -2448,14 +2602,12 @@ __device__ __forceinline__ uint32_t sample_core(SampleShared& sh, const float* l
     float a1 = sh.redf[0], a2 = sh.rede[0];
     uint32_t ai = sh.redk[0], c = sh.redu[0];
     for (uint32_t w = 1; w < NW; ++w) {
-      merge(a1, ai, a2, sh.redf[w], sh.redk[w], sh.rede[w]);
+      greedy_merge(a1, ai, a2, sh.redf[w], sh.redk[w], sh.rede[w]);
       c += sh.redu[w];
     }
     sh.bcast_f = a1;
     sh.bcast_u[0] = c;
-    // the max itself passes the test unless it is +inf (inf - inf is NaN),
-    // when the reference counts no value and leaves the greedy path
-    sh.bcast_u[1] = (c > 0 && !(cfg.temperature > 0.0f) && fabsf(a1 - a1) < 1e-6f && !(fabsf(a2 - a1) < 1e-6f)) ? 1u : 0u;
+    sh.bcast_u[1] = (!(cfg.temperature > 0.0f) && greedy_unique(c, a1, a2)) ? 1u : 0u;
     sh.bcast_u[2] = ai;
   }
   __syncthreads();
@@ -2686,6 +2838,14 @@ uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, ui
 hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hipStream_t s) {
   if (wtype != W_F16 && wtype != W_Q8_0 && wtype != W_Q4_0) return hipErrorInvalidValue;
   if (a.in % (wtype == W_F16 ? 8 : 32)) return hipErrorInvalidValue;
+  if (a.fold.logits) {
+    if (ncol != 1 || epi != EPI_STORE) return hipErrorInvalidValue;
+    switch (wtype) {
+      case W_F16: return gemv_fold_launch<W_F16>(a, s);
+      case W_Q8_0: return gemv_fold_launch<W_Q8_0>(a, s);
+      default: return gemv_fold_launch<W_Q4_0>(a, s);
+    }
+  }
   if (wtype != W_F16 && (ncol == 1 || ncol == 2) && a.qp && a.qs && a.row_base == 0 && a.extra_row == NO_ROW &&
       a.ldx % 4 == 0 && !((epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST) && (!a.qp3 || !a.qs3))) {
     const hipError_t e = ncol == 1

@@ -60,6 +60,7 @@ class GenStats(ctypes.Structure):
         ("n_frames", ctypes.c_uint32),
         ("graph_used", ctypes.c_uint32),
         ("per_column_rerun", ctypes.c_uint32),
+        ("greedy_rerun", ctypes.c_uint32),
     ]
 
 

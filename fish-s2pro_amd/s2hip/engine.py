@@ -181,6 +181,7 @@ class Engine:
             "decode_ms": stats.decode_ms,
             "graph_used": bool(stats.graph_used),
             "per_column_rerun": bool(stats.per_column_rerun),
+            "greedy_rerun": bool(stats.greedy_rerun),
         }
 
     def generate_codes_batch(self, prompts, max_new_tokens, temperature=0.0, top_p=1.0, top_k=0,
@@ -227,6 +228,7 @@ class Engine:
             "total_frames": stats.n_frames,
             "graph_used": bool(stats.graph_used),
             "per_column_rerun": bool(stats.per_column_rerun),
+            "greedy_rerun": bool(stats.greedy_rerun),
         }
 
     # -- op level -------------------------------------------------------------

@@ -96,6 +96,10 @@ typedef struct {
    * row) made the call run again from its inputs with every multi-column
    * linear on the per-column paths, whose split scale covers the whole row */
   uint32_t per_column_rerun;
+  /* 1: a one-request greedy call met a tie at the max of a Fast-AR sample
+   * folded into the next sub-step's first linear, and ran again from its
+   * inputs with the sampler kernel, which resolves ties as the reference */
+  uint32_t greedy_rerun;
 } s2hip_gen_stats;
 
 /* SlowArDecodeProfile (crates/fish_s2_infer/src/slow_ar.rs:248-319, filled by

@@ -210,6 +210,17 @@ def scale_rows(path, name, rows, factor):
         f.write(raw)
 
 
+def copy_row(path, name, src, dst):
+    """Row dst of the F16 matrix `name` := row src, in place in the GGUF file."""
+    raw = bytearray(open(path, "rb").read())
+    off, dims, typ = _locate(raw, name)
+    assert typ == 1 and len(dims) == 2, (name, typ, dims)
+    rb = dims[0] * 2
+    raw[off + dst * rb:off + (dst + 1) * rb] = raw[off + src * rb:off + (src + 1) * rb]
+    with open(path, "wb") as f:
+        f.write(raw)
+
+
 def _locate(raw, want):
     """(absolute data offset, dims ne0 first, ggml type) of tensor `want`."""
     pos = 4

@@ -8,12 +8,12 @@ and prompt (checked by sha256), then:
 * cfg2 (S2-Pro shape, f16, 256-token prompt, KV 768) and cfg4 (Q4_0, KV 1280):
   the prompt's post-final-norm hidden within 1e-4 relative, and 64 greedy
   frames bit-exact with the final RNG state (generate.rs:117-221);
-* cfg3 (Q8_0, T 0.7, top-p 0.9, SeededRng 1): 32 sampled frames equal, or the
+* cfg3 (Q8_0, T 0.7, top-p 0.9, SeededRng 1): 64 sampled frames equal, or the
   first differing draw sits at a boundary of the oracle's own probabilities
   (tests/loop_util.py: a draw target or top-p sum within 1e-4, or a logit
   tie within 1e-4 relative) -- after it the trajectories may part;
 * cfg5 (8 voice-clone requests of 1500 positions, batch 8, KV 2560):
-  requests 0 and 1 of the batch bit-exact over 16 greedy frames, with every
+  requests 0 to 3 of the batch bit-exact over 16 greedy frames, with every
   request's frame count.
 
 At the configs' full lengths (the oracle's fixtures cover the first frames):

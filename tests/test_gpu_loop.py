@@ -106,6 +106,42 @@ def test_sampled_codes_match_oracle(tiny_gguf):
     assert_draws_match(mism, total, 200)
 
 
+@pytest.mark.parametrize("graph", [True, False])
+def test_greedy_tie_reruns_with_the_sampler_kernel(tiny_gguf, tmp_path, graph):
+    """One-request greedy calls fold each Fast-AR sample into the next
+    sub-step's wqkv.  Here Fast-AR output rows 5 and 9 are equal and every
+    other row is zero, so every Fast-AR sample ties (two equal maxima, or 1022
+    zeros): the fold flags the tie and the call runs again with the sampler
+    kernel, whose draws among the tied values match the oracle's codes and
+    SeededRng state.  A model without ties keeps the fold (no re-run)."""
+    import shutil
+
+    import gguf_util
+
+    path = str(tmp_path / "tiny_fast_tie.gguf")
+    shutil.copyfile(tiny_gguf, path)
+    rows = [r for r in range(synth.TINY.codebook_size) if r != 5]
+    gguf_util.scale_rows(path, "fast_output.weight", rows, 0.0)
+    gguf_util.copy_row(path, "fast_output.weight", 5, 9)
+    prompt = make_prompt(synth.TINY, 16, seed=21)
+    e, o = _engine(path, graph=graph), _oracle(path)
+    r = e.generate_codes(prompt, 8, 0.0, 1.0, 0, 100, 3)
+    ro = o.generate_codes(prompt, 8, 0.0, 1.0, 0, 100, 3)
+    assert r["greedy_rerun"] and r["n_frames"] == ro["n_frames"] == 8
+    assert np.array_equal(r["codes"], ro["codes"]) and r["rng_state"] == ro["rng_state"]
+    assert set(np.unique(r["codes"][1:])) <= set(range(synth.TINY.codebook_size))
+    # the op entry point re-runs the same way
+    h, _ = o.eval(make_prompt(synth.TINY, 8, seed=22))
+    for sem in (0, 17):
+        cg, sg = e.fast_codebooks(h, sem, 0.0, 1.0, 0, 5)
+        co, so = o.fast_codebooks(h, sem, 0.0, 1.0, 0, 5)
+        assert np.array_equal(cg, co) and sg == so
+    r2 = _engine(tiny_gguf, graph=graph).generate_codes(prompt, 8, 0.0, 1.0, 0, 100, 3)
+    ro2 = _oracle(tiny_gguf).generate_codes(prompt, 8, 0.0, 1.0, 0, 100, 3)
+    assert not r2["greedy_rerun"]
+    assert np.array_equal(r2["codes"], ro2["codes"]) and r2["rng_state"] == ro2["rng_state"]
+
+
 def test_repeated_generate_is_deterministic(tiny_gguf):
     prompt = make_prompt(synth.TINY, 16, seed=12)
     e = _engine(tiny_gguf)
