@@ -183,8 +183,10 @@ class Engine {
   void enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done);
   void enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done);
   // fold (nullable): the first linear takes its input from the greedy sample
+  // code (nullable): the single column is the embedding of *code (the first
+  // linear's output comes from fast_table_)
   void enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done,
-                           const GreedyFold* fold = nullptr);
+                           const GreedyFold* fold = nullptr, const uint32_t* code = nullptr);
   void enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint32_t* done);
   bool fold_greedy(const SamplerCfg& cfg, uint32_t nseq) const;
   void enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_stride);
@@ -254,6 +256,13 @@ class Engine {
   // folded sample's max)
   bool fold_off_ = false;
   bool fold_env_off_ = false;  // S2HIP_NO_GREEDY_FOLD: always the sampler kernel
+  // The Fast-AR's first wqkv for every code: row c = wqkv(RMSNorm(fast_emb[c]))
+  // as the one-column GEMV computes it.  A sub-step whose input is one code's
+  // embedding (one request, after the first) then reads its q / k / v from
+  // the table instead of running the linear.  S2HIP_NO_FAST_TABLE: off.
+  float* fast_table_ = nullptr;
+  bool fast_table_off_ = false;
+  void ensure_fast_table();
   // L2 warming of the output projection by decode attention
   uint32_t warm_blocks_ = 256;            // warming blocks per kernel (0: off)
   uint32_t warm_depth_ = 4;               // 16-byte loads per thread in flight
@@ -454,6 +463,7 @@ Engine::Engine(const s2hip_config& cfg) {
   // boundary it replaces: 18.7 vs 13.2 us at T = 384 on the S2-Pro shape)
   attn_mode_ = getenv("S2HIP_ATTN_FUSED") ? ATTN_FUSED : ATTN_SPLIT;
   fold_env_off_ = getenv("S2HIP_NO_GREEDY_FOLD") != nullptr;
+  fast_table_off_ = getenv("S2HIP_NO_FAST_TABLE") != nullptr;
   prefill_gemv_ = getenv("S2HIP_PREFILL_GEMV") != nullptr;
   attn_chunks_ = attention_chunks(s.max_seq_len, attn_mode_);
   // S2HIP_BMM_MIN_COLS=n: F16 linears over >= n columns use the batched MFMA
@@ -841,17 +851,27 @@ void Engine::enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, co
 // Fast-AR layers (forward_prefill, fast_ar.rs:245-358) over nseq slots with cps consecutive
 // positions each from p0 (every slot is at the same Fast-AR position).
 void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const uint32_t* done,
-                                 const GreedyFold* fold) {
+                                 const GreedyFold* fold, const uint32_t* code) {
   const s2hip_spec& s = spec;
   const uint32_t fq = s.fast_heads * s.fast_head_dim, fkv = s.fast_kv_heads * s.fast_head_dim;
   const uint32_t w = fq + 2 * fkv;
   const uint32_t ncol = nseq * cps;
   for (uint32_t l = 0; l < s.fast_layers; ++l) {
     const FastLayer& L = fast_[l];
-    lin(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out, done,
-        0, l == 0 ? fold : nullptr);
+    // layer 0 of a table sub-step: q / k / v from the table (the attention
+    // takes the code, sampling it itself under a fold)
+    const bool table = l == 0 && fast_table_ && ncol == 1 && (code || fold);
+    if (!table)
+      lin(L.wqkv, nullptr, EPI_STORE, ncol, fh_, s.dim, L.attn_norm, s.fast_eps, fqkv_, w, 0, NO_ROW, L.wqkv.out,
+          done, 0, l == 0 ? fold : nullptr);
     AttnArgs aa{};
     aa.qkv = fqkv_;
+    if (table) {
+      aa.qkv_rows = fast_table_;
+      if (fold) aa.fold = *fold;
+      else aa.code_ptr = code;
+      aa.fold.n = s.codebook_size;
+    }
     aa.q_norm = nullptr;  // the Fast-AR applies no QK-norm (fast_ar.rs:310-334)
     aa.k_norm = nullptr;
     aa.eps = s.fast_eps;
@@ -869,7 +889,7 @@ void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const
     aa.max_seq = fctx_;
     aa.ncol = ncol;
     aa.max_chunks = attention_chunks(fctx_, attn_mode_);
-    aa.mode = attn_mode_;
+    aa.mode = table ? ATTN_SPLIT : attn_mode_;  // (a table sub-step: the partial kernel's table form)
     aa.scale = 1.0f / std::sqrt(float(s.fast_head_dim));  // fast_ar.rs:60-62
     aa.done = done ? &st_->done : nullptr;
     aa.err = &st_->err;
@@ -910,10 +930,12 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint
   HIPC(launch_fast_begin(st_, hn_, fast_emb_, fh_, s.dim, s.codebook_size, s.semantic_begin, s.semantic_end, nseq,
                          stream_));
   const bool fold = fold_greedy(cfg, nseq);
+  const bool table = fast_table_ && nseq == 1;
   GreedyFold gf{};
+  const uint32_t* code = nullptr;  // the code whose embedding the next sub-step takes (table sub-steps)
   uint32_t cps = 2, p0 = 0;
   for (uint32_t cb = 1; cb < s.num_codebooks; ++cb) {
-    enqueue_fast_layers(nseq, cps, p0, done, gf.logits ? &gf : nullptr);
+    enqueue_fast_layers(nseq, cps, p0, done, gf.logits ? &gf : nullptr, code);
     // the last position of each slot: rows cps - 1, 2 cps - 1, ...
     lin(fast_out_, nullptr, EPI_STORE, nseq, fh_ + size_t(cps - 1) * s.dim, cps * s.dim, fast_norm_, s.fast_eps,
         flogits_, s.codebook_size, 0, NO_ROW, s.codebook_size, done);
@@ -926,9 +948,11 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint
       gf.st = st_;
       gf.cb_index = cb;
       gf.x_out = fh_;
+      gf.dim = s.dim;
       continue;
     }
     gf = GreedyFold{};
+    code = (table && cb + 1 < s.num_codebooks) ? &st_->codes_frame[cb] : nullptr;
     SampleArgs sa{};
     sa.logits = flogits_;
     sa.n = s.codebook_size;
@@ -942,7 +966,7 @@ void Engine::enqueue_fast_frame(const SamplerCfg& cfg, uint32_t nseq, const uint
     sa.n_seq = nseq;
     // the next sub-step's first linear (one column per slot); the general
     // path (tens of microseconds on one CU, HBM idle) reads all of its rows
-    if (sa.next_input)
+    if (sa.next_input && !table)
       sa.warm = warm_for(fast_[0].wqkv, nullptr, nseq, true, 0, cfg.temperature > 0.0f ? 100u : warm_step_);
     HIPC(launch_sample_fast(sa, stream_));
   }
@@ -1358,6 +1382,7 @@ void Engine::fast_codebooks(const float* hidden, uint32_t sem, const s2hip_sampl
   *st_host_ = init;
   HIPC(hipMemcpyAsync(st_, st_host_, sizeof(DevState), hipMemcpyHostToDevice, stream_));
   HIPC(hipMemcpyAsync(hn_, hidden, s.dim * 4, hipMemcpyHostToDevice, stream_));
+  ensure_fast_table();
   enqueue_fast_frame(SamplerCfg{smp.temperature, smp.top_p, smp.top_k}, 1, nullptr);
   HIPC(hipMemcpyAsync(st_host_, st_, sizeof(DevState), hipMemcpyDeviceToHost, stream_));
   HIPC(hipStreamSynchronize(stream_));
@@ -1419,6 +1444,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   const size_t ncodes = size_t(s.num_codebooks) * p.max_new_tokens;
   ensure_slots(nseq);
   ensure_tiled();
+  ensure_fast_table();
   ensure_codes(ncodes * nseq);
   ensure_prompt(total_cols * cdim);
   HIPC(hipStreamSynchronize(stream_));
@@ -1619,6 +1645,24 @@ struct TmpBuf {
   T* as() { return static_cast<T*>(p); }
 };
 }  // namespace
+
+void Engine::ensure_fast_table() {
+  const s2hip_spec& s = spec;
+  if (fast_table_ || fast_table_off_ || s.fast_layers == 0) return;
+  ensure_tiled();  // the repacked rows decide which one-column kernel the linear takes
+  const DevLin& L = fast_[0].wqkv;
+  const uint32_t w = (s.fast_heads + 2 * s.fast_kv_heads) * s.fast_head_dim;
+  float* tab = dalloc<float>(size_t(s.codebook_size) * w);
+  TmpBuf x(size_t(s.codebook_size) * s.dim * 4);
+  HIPC(launch_dequant_rows(W_F16, reinterpret_cast<const uint8_t*>(fast_emb_), size_t(s.dim) * 2, s.codebook_size,
+                           s.dim, x.as<float>(), stream_));
+  // the same one-column call a sub-step makes (enqueue_fast_layers, layer 0)
+  for (uint32_t c = 0; c < s.codebook_size; ++c)
+    lin(L, nullptr, EPI_STORE, 1, x.as<float>() + size_t(c) * s.dim, s.dim, fast_[0].attn_norm, s.fast_eps,
+        tab + size_t(c) * w, w, 0, NO_ROW, L.out, nullptr);
+  HIPC(hipStreamSynchronize(stream_));
+  fast_table_ = tab;
+}
 
 void Engine::op_linear(const void* w, uint32_t type, size_t in, size_t out, const float* x, size_t ncol, float* y) {
   select();

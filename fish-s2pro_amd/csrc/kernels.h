@@ -72,7 +72,8 @@ struct GreedyFold {
   const uint16_t* emb;   // [n][in] f16
   DevState* st;
   uint32_t cb_index;
-  float* x_out;          // [in]
+  float* x_out;          // [dim]
+  uint32_t dim;          // row length of emb / x_out (the linear's input length)
 };
 
 struct GemvArgs {
@@ -183,6 +184,13 @@ struct AttnArgs {
   L2Warm warm;             // rows of the next GEMV (wo) warmed by extra blocks of the partial kernel
   L2Warm warm2;            // ... and of the merge kernel
   uint32_t kv_f16;         // 1: k_cache / v_cache hold f16 (seq_stride_kv and offsets in elements)
+  // one column: q / k / v from row `code` of qkv_rows ([fold.n][(H + 2 Hkv)
+  // hd]) instead of qkv, code = *code_ptr or, with fold.logits, the greedy
+  // sample of the logits (then block 0 also has the sampler's side effects,
+  // as GemvArgs::fold).  nullptr: qkv.
+  const float* qkv_rows;
+  const uint32_t* code_ptr;
+  GreedyFold fold;
 };
 enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
 constexpr uint32_t ATTN_MAX_CHUNKS = 1024;  // max_seq <= 32768

@@ -110,6 +110,49 @@ __device__ __forceinline__ bool greedy_unique(uint32_t count, float m1, float m2
   return count > 0 && fabsf(m1 - m1) < 1e-6f && !(fabsf(m2 - m1) < 1e-6f);
 }
 
+// The greedy sample of logits[0, n) (n % 4 == 0) by a block of NW waves
+// (LDS scratch of NW entries each): every thread gets the token (id 0 when
+// no value is finite) and whether the greedy test failed (a tie within 1e-6
+// at the max, or a non-finite max) while some value was finite.
+template <int NW>
+__device__ __forceinline__ void block_greedy(const float* logits, uint32_t n, float* s1, float* s2, uint32_t* sid,
+                                             uint32_t* scnt, uint32_t& tok, uint32_t& tie) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  float m1 = -INFINITY, m2 = -INFINITY;
+  uint32_t id1 = 0xffffffffu, cnt = 0;
+  const float4* l4 = reinterpret_cast<const float4*>(logits);
+  for (uint32_t i = tid; i < n / 4u; i += NW * 64u) {
+    const float4 q = l4[i];
+    const float v4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (v4[c] > -INFINITY) {
+        ++cnt;
+        greedy_add(m1, id1, m2, v4[c], 4u * i + uint32_t(c));
+      }
+    }
+  }
+  greedy_wave(m1, id1, m2);
+  cnt = wave_sum_u32(cnt);
+  if (lane == 0) {
+    s1[wave] = m1;
+    s2[wave] = m2;
+    sid[wave] = id1;
+    scnt[wave] = cnt;
+  }
+  __syncthreads();
+  float a1 = s1[0], a2 = s2[0];
+  uint32_t ai = sid[0], c = scnt[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    greedy_merge(a1, ai, a2, s1[w], sid[w], s2[w]);
+    c += scnt[w];
+  }
+  tok = c > 0 ? min(ai, n - 1u) : 0u;
+  tie = (c > 0 && !greedy_unique(c, a1, a2)) ? 1u : 0u;
+}
+
+
 // ---------------------------------------------------------------------------
 // Raw weight payload for 8 consecutive elements, loaded first and decoded
 // later so a wave can keep many independent 16-byte loads in flight.
@@ -1602,7 +1645,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 //       per (col, g) elects the last block of the pair, which merges them with
 //       agent-scope loads and resets the counter for the next launch.
 // ---------------------------------------------------------------------------
-template <int HD, int CH, bool LAST, bool KH>
+template <int HD, int CH, bool LAST, bool KH, bool GATHER = false>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, void* k_cache, void* v_cache,
                                                              const uint32_t* pos_ptr, const uint32_t* done_ptr,
                                                              uint32_t ncol, uint32_t max_seq, uint32_t kv_stride,
@@ -1617,6 +1660,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
   __shared__ float ps[GEMV_WAVES][CH];
   __shared__ float knew[4][HD], vnew[4][HD];
   __shared__ uint32_t is_last;
+  __shared__ float gm1[GATHER ? GEMV_WAVES : 1], gm2[GATHER ? GEMV_WAVES : 1];
+  __shared__ uint32_t gid[GATHER ? GEMV_WAVES : 1], gcnt[GATHER ? GEMV_WAVES : 1];
   if (__builtin_expect(blockIdx.z >= ncol, 0)) {  // warming planes after the attention blocks (laid out last)
     const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
     l2_warm(a.warm, L, L - gridDim.x * gridDim.y * ncol, threadIdx.x, 256u);
@@ -1657,6 +1702,30 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
       vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
     }
   }
+  // one column from a table row: its code (the greedy sample of the logits,
+  // reduced by every block, or a sampled code), and block 0 carries the
+  // sampler's side effects (input row, code, SeededRng step, tie flag)
+  if constexpr (GATHER) {
+    uint32_t code;
+    if (a.fold.logits) {
+      const uint32_t st_done = opt_word(&a.fold.st->done);
+      uint32_t tie;
+      block_greedy<GEMV_WAVES>(a.fold.logits, a.fold.n, gm1, gm2, gid, gcnt, code, tie);
+      if (chunk == 0 && g == 0 && !st_done) {
+        for (uint32_t i = tid; i < a.fold.dim; i += 256)
+          a.fold.x_out[i] = half_bits_to_float(a.fold.emb[size_t(code) * a.fold.dim + i]);
+        if (tid == 0) {
+          DevState* st = a.fold.st;
+          st->rng = lcg_step(st->rng);
+          st->codes_frame[a.fold.cb_index] = code;
+          if (tie) atomicOr(&st->err, ERR_GREEDY_TIE);
+        }
+      }
+    } else {
+      code = min(opt_word(a.code_ptr), a.fold.n - 1u);  // table rows: fold.n
+    }
+    row = a.qkv_rows + size_t(code) * width;
+  }
   // q row of head g * rep + wave and the k / v rows of this sequence's
   // columns (wave w <-> column w <= lc): every lane loads from a clamped,
   // valid address and lanes outside the ranges drop the value, so no branch
@@ -1665,7 +1734,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
   const bool qlane = wave < rep && lane < HD / 2;
   const bool kwave = wave < cps && wave <= lc;
   const float2 qraw = *reinterpret_cast<const float2*>(row + size_t(g * rep + min(wave, rep - 1)) * HD + e2);
-  const float* r2 = qkv + size_t(seq * cps + min(wave, lc)) * width;
+  const float* r2 = GATHER ? row : qkv + size_t(seq * cps + min(wave, lc)) * width;
   const float2 kraw = *reinterpret_cast<const float2*>(r2 + size_t(H + g) * HD + e2);
   const float2 vraw = *reinterpret_cast<const float2*>(r2 + size_t(H + Hkv + g) * HD + e2);
   const float2 qn = *reinterpret_cast<const float2*>((a.q_norm ? a.q_norm : kUnitGain) + e2);
@@ -2920,6 +2989,13 @@ void launch_combine(const AttnArgs& a, dim3 grid, hipStream_t s) {
 
 template <int HD, bool LAST>
 void launch_partial(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (!LAST && a.qkv_rows) {  // q / k / v from a table row (f32 cache: the Fast-AR's)
+    if (a.kv_f16) return;     // rejected by launch_attention
+    hipLaunchKernelGGL((attn_partial_kernel<HD, 32, false, false, true>), grid, dim3(256), 0, s, a.qkv,
+                       static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache), a.pos_ptr, a.done, a.ncol,
+                       a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
+    return;
+  }
   hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<HD, 32, LAST, true> : attn_partial_kernel<HD, 32, LAST, false>),
                      grid, dim3(256), 0, s, a.qkv, static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache),
                      a.pos_ptr, a.done, a.ncol, a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
@@ -2934,6 +3010,14 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   if (a.H % a.Hkv || a.H / a.Hkv > 4 || a.H > 255 || a.seq_stride_words > 255 || a.seq_stride_kv > UINT32_MAX)
     return hipErrorInvalidValue;
   if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
+  if (a.qkv_rows) {
+    const GreedyFold& f = a.fold;
+    if (a.ncol != 1 || a.cols_per_seq != 1 || a.mode != ATTN_SPLIT || a.kv_f16) return hipErrorInvalidValue;
+    if (f.n == 0 || (f.logits ? (!f.emb || !f.st || !f.x_out || f.n % 4 || f.dim == 0 || f.cb_index >= 16 ||
+                                 reinterpret_cast<uintptr_t>(f.logits) % 16)
+                              : !a.code_ptr))
+      return hipErrorInvalidValue;
+  }
   hipError_t werr = hipSuccess;
   const uint32_t planes = l2_warm_planes(a.warm, a.max_chunks * a.Hkv, &werr);  // z-planes of warming blocks
   const uint32_t planes2 = a.max_chunks > 1 ? l2_warm_planes(a.warm2, a.H, &werr) : 0u;

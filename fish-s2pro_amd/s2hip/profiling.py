@@ -21,6 +21,13 @@ flops (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512) per dispatch.
 in a kernel-trace CSV (e.g. bench.py's timing loop, which runs after the
 decode generations).
 
+`budget` splits the decode frames of a kernel-trace CSV (one stream, so
+kernels do not overlap) into kernel time and launch gaps: the window runs
+from the --begin kernel's first dispatch after the last --after dispatch
+(the last prefill) up to its (--frames + 1)-th dispatch, i.e. --frames whole
+frames that each start with --begin; it prints each kernel's dispatches and
+microseconds per frame and the idle time between kernels per frame.
+
 `counters` averages one HBM byte counter (FETCH_SIZE or WRITE_SIZE, reported
 in KiB per dispatch) over every dispatch of the kernel matching --kernel, and
 calibrates it against a plain copy kernel of known size: the copy reads and
@@ -165,6 +172,36 @@ def tail(path, kernel_re, count):
             f"last {len(last)}: mean {statistics.fmean(last):.3f} us, min {min(last):.3f}, max {max(last):.3f}")
 
 
+def budget(path, after_re, begin_re, frames, top):
+    rows = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((int(_col(r, "Start_Timestamp")), int(_col(r, "End_Timestamp")),
+                         short_name(_col(r, "Kernel_Name"))))
+    rows.sort()
+    after, begin = re.compile(after_re), re.compile(begin_re)
+    last_after = max((i for i, r in enumerate(rows) if after.search(r[2])), default=-1)
+    starts = [i for i in range(last_after + 1, len(rows)) if begin.search(rows[i][2])]
+    if len(starts) < frames + 1:
+        raise SystemExit(f"{len(starts)} {begin_re!r} dispatches after the last {after_re!r}; need {frames + 1}")
+    win = rows[starts[0]:starts[frames]]
+    span = (rows[starts[frames]][0] - win[0][0]) / 1e3
+    busy = 0.0
+    per = {}
+    for s0, e0, name in win:
+        d = (e0 - s0) / 1e3
+        busy += d
+        c, t = per.get(name, (0, 0.0))
+        per[name] = (c + 1, t + d)
+    lines = [f"window: {len(win)} dispatches, {frames} frames, {span / frames:.1f} us per frame; kernels "
+             f"{busy / frames:.1f} us per frame, gaps {(span - busy) / frames:.1f} us per frame "
+             f"({100 * (span - busy) / span:.1f} %)",
+             f"{'kernel':72s} {'per frame':>9s} {'avg_us':>8s} {'us/frame':>9s} {'%':>6s}"]
+    for name, (c, t) in sorted(per.items(), key=lambda kv: -kv[1][1])[:top]:
+        lines.append(f"{name[:72]:72s} {c / frames:9.2f} {t / c:8.2f} {t / frames:9.1f} {100 * t / span:6.2f}")
+    return "\n".join(lines)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -186,6 +223,12 @@ def main(argv=None):
     tl.add_argument("csv")
     tl.add_argument("--kernel", required=True)
     tl.add_argument("--count", type=int, required=True)
+    bu = sub.add_parser("budget")
+    bu.add_argument("csv")
+    bu.add_argument("--after", required=True)
+    bu.add_argument("--begin", required=True)
+    bu.add_argument("--frames", type=int, required=True)
+    bu.add_argument("--top", type=int, default=40)
     m = sub.add_parser("mfma")
     m.add_argument("csv")
     m.add_argument("--kernel", action="append", required=True)
@@ -196,6 +239,8 @@ def main(argv=None):
         print(traffic(args.fetch_csv, args.write_csv, args.copy_kernel, args.copy_bytes, args.row))
     elif args.cmd == "tail":
         print(tail(args.csv, args.kernel, args.count))
+    elif args.cmd == "budget":
+        print(budget(args.csv, args.after, args.begin, args.frames, args.top))
     elif args.cmd == "mfma":
         print(mfma(args.csv, args.kernel))
     else:

@@ -142,6 +142,33 @@ def test_greedy_tie_reruns_with_the_sampler_kernel(tiny_gguf, tmp_path, graph):
     assert np.array_equal(r2["codes"], ro2["codes"]) and r2["rng_state"] == ro2["rng_state"]
 
 
+@pytest.mark.parametrize("sampled", [False, True])
+def test_fast_wqkv_table_equals_the_linear(tiny_gguf, monkeypatch, sampled):
+    """A one-request sub-step whose input is one code's embedding takes the
+    Fast-AR's first wqkv output from a per-code table built with the same
+    one-column linear: codes, SeededRng state and the Fast-AR logits equal the
+    engine without the table (S2HIP_NO_FAST_TABLE) bit for bit, greedy (the
+    sample folded into the table read) and sampled."""
+    prompt = make_prompt(synth.TINY, 24, seed=23)
+    kw = dict(temperature=0.7 if sampled else 0.0, top_p=0.9 if sampled else 1.0, top_k=0,
+              min_tokens_before_end=100, rng_state=5)
+    runs = []
+    for off in (False, True):
+        if off:
+            monkeypatch.setenv("S2HIP_NO_FAST_TABLE", "1")
+        else:
+            monkeypatch.delenv("S2HIP_NO_FAST_TABLE", raising=False)
+        e = _engine(tiny_gguf)
+        r = e.generate_codes(prompt, 12, **kw)
+        h, _ = _oracle(tiny_gguf).eval(make_prompt(synth.TINY, 8, seed=24))
+        fc = e.fast_codebooks(h, 33, kw["temperature"], kw["top_p"], 0, 9)
+        runs.append((r, fc))
+    (a, fa), (b, fb) = runs
+    assert a["n_frames"] == b["n_frames"] == 12 and not a["greedy_rerun"]
+    assert np.array_equal(a["codes"], b["codes"]) and a["rng_state"] == b["rng_state"]
+    assert np.array_equal(fa[0], fb[0]) and fa[1] == fb[1]
+
+
 def test_repeated_generate_is_deterministic(tiny_gguf):
     prompt = make_prompt(synth.TINY, 16, seed=12)
     e = _engine(tiny_gguf)
