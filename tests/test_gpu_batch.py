@@ -181,7 +181,8 @@ def test_batch_with_an_outlier_channel_matches_oracle(model_dir, tmp_path):
 def test_batch_with_large_norm_gains_matches_oracle(model_dir):
     """Every Slow and Fast linear of a 3-request batch runs the batched MFMA
     product; with RMSNorm gains of 100 the raw residual times the gain reaches
-    ~1e6-1e7, inside the three-part split's range, and codes stay bit-exact."""
+    ~1e6-1e7, which the per-wave power-of-two scale brings into the f16 hi / lo
+    split's range, and codes stay bit-exact."""
     path = synth.ensure_gguf(synth.TINY.with_(norm_gain=100.0), model_dir)
     prompts = _prompts(3, seed=140)
     e, o = _engine(path), _oracle(path)

@@ -313,8 +313,9 @@ def tiny_gain_gguf(model_dir):
 
 def test_large_norm_gains_keep_greedy_codes_bit_exact(tiny_gain_gguf):
     """The first Fast-AR pass runs the batched MFMA product on the raw
-    pre-norm residual times the gain (~1e6 here): its three-part f16 split
-    must carry that without a range failure, and codes stay bit-exact."""
+    pre-norm residual times the gain (~1e6 here): its per-wave power-of-two
+    scale and f16 hi / lo split carry that without a range failure, and codes
+    stay bit-exact."""
     prompt = make_prompt(synth.TINY, 24, seed=31)
     e, o = _engine(tiny_gain_gguf), _oracle(tiny_gain_gguf)
     hg, _ = e.eval(prompt)

@@ -64,10 +64,12 @@ def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
 
 @pytest.mark.parametrize("ncol", [2, 8])
 def test_batched_linear_activation_range(eng, ncol):
-    """Batched F16 columns go through the MFMA product with activations split
-    into three f16 parts: columns whose values span 1e-6 .. 1e6 (and single
-    entries up to 1e8) match the oracle to 1e-4, and a non-finite value makes
-    the call fail instead of returning a wrong result."""
+    """Batched F16 columns go through the MFMA product with activations scaled
+    per wave by a power of two and split into f16 hi and lo parts: columns
+    whose values span 1e-6 .. 1e6 (and single entries up to 1e8) match the
+    oracle to 1e-4, a spike beyond the per-wave headroom is taken on the
+    per-column path, and a non-finite value makes the call fail instead of
+    returning a wrong result."""
     from s2hip import S2HipError
 
     rng = np.random.default_rng(31 + ncol)
