@@ -109,7 +109,8 @@ def test_sampled_codes_match_oracle(tiny_gguf):
 @pytest.mark.parametrize("graph", [True, False])
 def test_greedy_tie_reruns_with_the_sampler_kernel(tiny_gguf, tmp_path, graph):
     """One-request greedy calls fold each Fast-AR sample into the next
-    sub-step's wqkv.  Here Fast-AR output rows 5 and 9 are equal and every
+    sub-step (its layer-0 attention reading the wqkv table, or its wqkv
+    without the table).  Here Fast-AR output rows 5 and 9 are equal and every
     other row is zero, so every Fast-AR sample ties (two equal maxima, or 1022
     zeros): the fold flags the tie and the call runs again with the sampler
     kernel, whose draws among the tied values match the oracle's codes and
