@@ -41,6 +41,24 @@ __device__ __forceinline__ uint32_t opt_word(const uint32_t* p) {
   return *(gword*)(p ? p : &kZeroWord);
 }
 
+// Values read through the global address space (see opt_word)
+__device__ __forceinline__ float gload_f32(const float* p) {
+  typedef const __attribute__((address_space(1))) float gfloat;
+  return *(gfloat*)p;
+}
+__device__ __forceinline__ float2 gload_f2(const float2* p) {
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef const __attribute__((address_space(1))) f2v gf2v;
+  const f2v v = *(gf2v*)p;
+  return make_float2(v.x, v.y);
+}
+__device__ __forceinline__ float4 gload_f4(const float4* p) {
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  typedef const __attribute__((address_space(1))) f4v gf4v;
+  const f4v v = *(gf4v*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // Unit gains: the stand-in for an absent QK-norm gain, so that the gain loads
 // need no branch.
 __device__ const float kUnitGain[256] = {
@@ -110,19 +128,31 @@ __device__ __forceinline__ bool greedy_unique(uint32_t count, float m1, float m2
   return count > 0 && fabsf(m1 - m1) < 1e-6f && !(fabsf(m2 - m1) < 1e-6f);
 }
 
-// The greedy sample of logits[0, n) (n % 4 == 0) by a block of NW waves
-// (LDS scratch of NW entries each): every thread gets the token (id 0 when
-// no value is finite) and whether the greedy test failed (a tie within 1e-6
-// at the max, or a non-finite max) while some value was finite.
-template <int NW>
-__device__ __forceinline__ void block_greedy(const float* logits, uint32_t n, float* s1, float* s2, uint32_t* sid,
-                                             uint32_t* scnt, uint32_t& tok, uint32_t& tie) {
+// The greedy sample of logits[0, n) (n % 4 == 0, n > 0) by a block of NW
+// waves, in two parts so that a kernel can issue the loads early:
+// greedy_loads issues U float4 per thread (addresses clamped into the
+// logits; values past n are dropped by the second part), block_greedy_keys
+// adds any remainder and reduces over the block (LDS scratch of NW entries
+// each).  Every thread gets the token (id 0 when no value is finite) and
+// whether the greedy test failed (a tie within 1e-6 at the max, or a
+// non-finite max) while some value was finite.
+template <int NW, int U>
+__device__ __forceinline__ void greedy_loads(const float* logits, uint32_t n, float4 (&lg)[U]) {
+  const float4* l4 = reinterpret_cast<const float4*>(logits);
+  const uint32_t n4 = n / 4u;
+#pragma unroll
+  for (int r = 0; r < U; ++r) lg[r] = gload_f4(l4 + min(threadIdx.x + uint32_t(r) * NW * 64u, n4 - 1u));
+}
+
+template <int NW, int U>
+__device__ __forceinline__ void block_greedy_keys(const float4 (&lg)[U], const float* logits, uint32_t n, float* s1,
+                                                  float* s2, uint32_t* sid, uint32_t* scnt, uint32_t& tok,
+                                                  uint32_t& tie) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t n4 = n / 4u;
   float m1 = -INFINITY, m2 = -INFINITY;
   uint32_t id1 = 0xffffffffu, cnt = 0;
-  const float4* l4 = reinterpret_cast<const float4*>(logits);
-  for (uint32_t i = tid; i < n / 4u; i += NW * 64u) {
-    const float4 q = l4[i];
+  auto add4 = [&](const float4 q, uint32_t i) {
     const float v4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -131,7 +161,14 @@ __device__ __forceinline__ void block_greedy(const float* logits, uint32_t n, fl
         greedy_add(m1, id1, m2, v4[c], 4u * i + uint32_t(c));
       }
     }
+  };
+#pragma unroll
+  for (int r = 0; r < U; ++r) {
+    const uint32_t i = tid + uint32_t(r) * NW * 64u;
+    if (i < n4) add4(lg[r], i);
   }
+  const float4* l4 = reinterpret_cast<const float4*>(logits);
+  for (uint32_t i = tid + uint32_t(U) * NW * 64u; i < n4; i += NW * 64u) add4(gload_f4(l4 + i), i);
   greedy_wave(m1, id1, m2);
   cnt = wave_sum_u32(cnt);
   if (lane == 0) {
@@ -1011,6 +1048,16 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
   float* ybase = a.y;
   uint32_t ldy = a.ldy;
   asm volatile("" : "+s"(eps), "+s"(ybase), "+s"(ldy));
+  // RESID: the residual values are loaded now, behind the weight loads, so
+  // the epilogue does not add a memory round trip to the wave's tail
+  // (every lane reads its wave's row: one request, no branch, and a global
+  // load whose wait drains only the loads issued before it)
+  float yres[NCOL];
+#pragma unroll
+  for (int c = 0; c < NCOL; ++c) {
+    yres[c] = 0.0f;
+    if constexpr (EPI == EPI_RESID) yres[c] = gload_f32(ybase + size_t(c) * ldy + (row < out ? row : out - 1));
+  }
   // 3. block sum of squares -> scale
 #pragma unroll
   for (int c = 0; c < NCOL && NORM; ++c) {
@@ -1114,7 +1161,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
       if constexpr (EPI == EPI_STORE) {
         *dst = gsum;
       } else if constexpr (EPI == EPI_RESID) {
-        *dst = __fadd_rn(*dst, gsum);
+        *dst = __fadd_rn(yres[c], gsum);
       } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
         const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc_wave(-gsum)));
         *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
@@ -1329,6 +1376,14 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
   float* ybase = a.y;
   uint32_t ldy = a.ldy;
   asm volatile("" : "+s"(eps), "+s"(ybase), "+s"(ldy));
+  // RESID: the residual values go out behind the weight loads (as in
+  // gemv_n_kernel)
+  float yres[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    yres[c] = 0.0f;
+    if constexpr (EPI == EPI_RESID) yres[c] = gload_f32(ybase + size_t(c) * ldy + (row < out ? row : out - 1));
+  }
   // 3. block sum of squares -> scale (per column)
   if constexpr (NORM) {
 #pragma unroll
@@ -1419,7 +1474,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
       if constexpr (EPI == EPI_STORE) {
         *dst = gsum;
       } else if constexpr (EPI == EPI_RESID) {
-        *dst = __fadd_rn(*dst, gsum);
+        *dst = __fadd_rn(yres[c], gsum);
       } else if constexpr (EPI == EPI_SWIGLU_SLOW) {
         const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc_wave(-gsum)));
         *dst = __fmul_rn(__fmul_rn(gsum, sig), u);
@@ -1688,6 +1743,19 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
   //    block)
   const uint32_t done = opt_word(done_ptr ? done_ptr + size_t(seq) * sw : nullptr);
   const uint32_t pbase = opt_word(pos_ptr ? pos_ptr + size_t(seq) * sw : nullptr);
+  // GATHER: what picks the table row goes out before the tile, so that the
+  // wait for it leaves the tile in flight: the logits of the greedy fold (or
+  // the sampled code word) and the state words of the sampler's side effects
+  //   (no branch: absent inputs read stand-ins, so all of these go out
+  //   together; the sampled-code form reads a unit gain row as its logits)
+  float4 glg[GATHER ? 4 : 1];
+  uint32_t code_word = 0, st_done = 1;
+  if constexpr (GATHER) {
+    const bool fl = a.fold.logits != nullptr;
+    greedy_loads<GEMV_WAVES, 4>(fl ? a.fold.logits : kUnitGain, fl ? a.fold.n : 4u, glg);
+    code_word = opt_word(a.code_ptr);
+    st_done = opt_word(fl ? &a.fold.st->done : nullptr);
+  }
   float4 kr[PER], vr[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -1702,18 +1770,54 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
       vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
     }
   }
+  // rotation rows of the query position and of column `wave`'s position:
+  // they need only the position word, so they go out with the loads above
+  // (addresses clamped into the table, which has max_seq rows; values for
+  // lanes and positions outside the ranges are dropped below)
+  const uint32_t pos = pbase + a.pos_offset + lc;
+  const uint32_t base = pos - lc;   // first position of this sequence's columns
+  const uint32_t tk = base + wave;  // position of column `wave`
+  const uint32_t hl = lane & (HD / 2 - 1);
+  float2 rp_raw, rk_raw;
+  auto rope_loads = [&] {
+    rp_raw = gload_f2(a.rope + size_t(min(pos, max_seq - 1)) * (HD / 2) + hl);
+    rk_raw = gload_f2(a.rope + size_t(min(tk, max_seq - 1)) * (HD / 2) + hl);
+  };
+  if constexpr (GATHER) rope_loads();
   // one column from a table row: its code (the greedy sample of the logits,
   // reduced by every block, or a sampled code), and block 0 carries the
   // sampler's side effects (input row, code, SeededRng step, tie flag)
   if constexpr (GATHER) {
     uint32_t code;
     if (a.fold.logits) {
-      const uint32_t st_done = opt_word(&a.fold.st->done);
       uint32_t tie;
-      block_greedy<GEMV_WAVES>(a.fold.logits, a.fold.n, gm1, gm2, gid, gcnt, code, tie);
+      block_greedy_keys<GEMV_WAVES, 4>(glg, a.fold.logits, a.fold.n, gm1, gm2, gid, gcnt, code, tie);
       if (chunk == 0 && g == 0 && !st_done) {
-        for (uint32_t i = tid; i < a.fold.dim; i += 256)
-          a.fold.x_out[i] = half_bits_to_float(a.fold.emb[size_t(code) * a.fold.dim + i]);
+        // the next input row (f16 -> f32), 8 elements per thread with every
+        // load of a pass issued before its stores (fold.dim % 8 == 0)
+        const uint4* er = reinterpret_cast<const uint4*>(a.fold.emb + size_t(code) * a.fold.dim);
+        const uint32_t n8 = a.fold.dim / 8u;
+        for (uint32_t b0 = 0; b0 < n8; b0 += 2u * 256u) {
+          uint4 raw[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) raw[u] = er[min(b0 + tid + uint32_t(u) * 256u, n8 - 1u)];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const uint32_t b = b0 + tid + uint32_t(u) * 256u;
+            if (b < n8) {
+              const uint32_t h[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+              float f[8];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                f[2 * k] = half_bits_to_float(uint16_t(h[k] & 0xffffu));
+                f[2 * k + 1] = half_bits_to_float(uint16_t(h[k] >> 16));
+              }
+              float4* xo = reinterpret_cast<float4*>(a.fold.x_out + size_t(b) * 8u);
+              xo[0] = make_float4(f[0], f[1], f[2], f[3]);
+              xo[1] = make_float4(f[4], f[5], f[6], f[7]);
+            }
+          }
+        }
         if (tid == 0) {
           DevState* st = a.fold.st;
           st->rng = lcg_step(st->rng);
@@ -1722,7 +1826,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
         }
       }
     } else {
-      code = min(opt_word(a.code_ptr), a.fold.n - 1u);  // table rows: fold.n
+      code = min(code_word, a.fold.n - 1u);  // table rows: fold.n
     }
     row = a.qkv_rows + size_t(code) * width;
   }
@@ -1737,13 +1841,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
   const float* r2 = GATHER ? row : qkv + size_t(seq * cps + min(wave, lc)) * width;
   const float2 kraw = *reinterpret_cast<const float2*>(r2 + size_t(H + g) * HD + e2);
   const float2 vraw = *reinterpret_cast<const float2*>(r2 + size_t(H + Hkv + g) * HD + e2);
-  const float2 qn = *reinterpret_cast<const float2*>((a.q_norm ? a.q_norm : kUnitGain) + e2);
-  const float2 kn = *reinterpret_cast<const float2*>((a.k_norm ? a.k_norm : kUnitGain) + e2);
+  // (global-space loads: a generic pointer would make flat loads, whose
+  // waits drain every load in flight, the K/V tile included)
+  const float2 qn = gload_f2(reinterpret_cast<const float2*>((a.q_norm ? a.q_norm : kUnitGain) + e2));
+  const float2 kn = gload_f2(reinterpret_cast<const float2*>((a.k_norm ? a.k_norm : kUnitGain) + e2));
+  if constexpr (!GATHER) rope_loads();
   const float2 zero2 = make_float2(0.f, 0.f);
   const float2 qv = qlane ? qraw : zero2;
   const float2 kx = (kwave && lane < HD / 2) ? kraw : zero2;
   const float2 vx = (kwave && lane < HD / 2) ? vraw : zero2;
-  const uint32_t pos = pbase + a.pos_offset + lc;
   const uint32_t T = pos + 1;
   const uint32_t nch = (T + CH - 1) / CH;
   if (done || pos >= max_seq || chunk >= nch) {
@@ -1752,7 +1858,13 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
     // The exit path also reads the loaded values, so the compiler keeps the
     // loads ahead of this branch (where they overlap the state read) instead
     // of sinking them behind it.  The test is never true for finite data.
-    float keep = qv.x + qv.y + kx.x + kx.y + vx.x + vx.y + qn.x + qn.y + kn.x + kn.y;
+    float keep = qv.x + qv.y + kx.x + kx.y + vx.x + vx.y + qn.x + qn.y + kn.x + kn.y + rp_raw.x + rp_raw.y +
+                 rk_raw.x + rk_raw.y;
+    if constexpr (GATHER) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) keep += (glg[r].x + glg[r].y) + (glg[r].z + glg[r].w);
+      keep += float(code_word) + float(st_done);
+    }
 #pragma unroll
     for (int j = 0; j < PER; ++j)
       keep += (kr[j].x + kr[j].y) + (kr[j].z + kr[j].w) + (vr[j].x + vr[j].y) + (vr[j].z + vr[j].w);
@@ -1760,15 +1872,12 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
     return;
   }
   const uint32_t t1 = min(T, t0 + CH), nt = t1 - t0;
-  const uint32_t base = pos - lc;              // first position of this sequence's columns
   const uint32_t lo = max(t0, min(base, t1));  // [lo, t1): positions of this launch
 
-  // 1. rotation rows (the only position-dependent loads), then q and the
-  //    new k: QK-norm (optional) + rotation
-  const uint32_t tk = base + wave;  // position of column `wave`
+  // 1. q and the new k: QK-norm (optional) + rotation
   const bool khere = kwave && tk >= t0 && tk < t1;
-  const float2 rp = qlane ? a.rope[size_t(pos) * (HD / 2) + lane] : make_float2(1.f, 0.f);
-  const float2 rk = (khere && lane < HD / 2) ? a.rope[size_t(tk) * (HD / 2) + lane] : make_float2(1.f, 0.f);
+  const float2 rp = qlane ? rp_raw : make_float2(1.f, 0.f);
+  const float2 rk = (khere && lane < HD / 2) ? rk_raw : make_float2(1.f, 0.f);
   if (khere) {
     float x0 = kx.x, x1 = kx.y;
     if (a.k_norm) {
@@ -3013,8 +3122,9 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   if (a.qkv_rows) {
     const GreedyFold& f = a.fold;
     if (a.ncol != 1 || a.cols_per_seq != 1 || a.mode != ATTN_SPLIT || a.kv_f16) return hipErrorInvalidValue;
-    if (f.n == 0 || (f.logits ? (!f.emb || !f.st || !f.x_out || f.n % 4 || f.dim == 0 || f.cb_index >= 16 ||
-                                 reinterpret_cast<uintptr_t>(f.logits) % 16)
+    if (f.n == 0 || (f.logits ? (!f.emb || !f.st || !f.x_out || f.n % 4 || f.dim == 0 || f.dim % 8 ||
+                                 f.cb_index >= 16 || reinterpret_cast<uintptr_t>(f.logits) % 16 ||
+                                 reinterpret_cast<uintptr_t>(f.emb) % 16 || reinterpret_cast<uintptr_t>(f.x_out) % 16)
                               : !a.code_ptr))
       return hipErrorInvalidValue;
   }
