@@ -41,6 +41,17 @@ __device__ __forceinline__ uint32_t opt_word(const uint32_t* p) {
   return *(gword*)(p ? p : &kZeroWord);
 }
 
+// Two optional words at p0 + off and p1 + off (null: zero), both loads
+// issued before either is made wave-uniform, so one wait covers both.
+__device__ __forceinline__ void opt_words2(const uint32_t* p0, const uint32_t* p1, size_t off, uint32_t& w0,
+                                           uint32_t& w1) {
+  typedef const __attribute__((address_space(1))) uint32_t gword;
+  const uint32_t v0 = *(gword*)(p0 ? p0 + off : &kZeroWord);
+  const uint32_t v1 = *(gword*)(p1 ? p1 + off : &kZeroWord);
+  w0 = uint32_t(__builtin_amdgcn_readfirstlane(int(v0)));
+  w1 = uint32_t(__builtin_amdgcn_readfirstlane(int(v1)));
+}
+
 // Values read through the global address space (see opt_word)
 __device__ __forceinline__ float gload_f32(const float* p) {
   typedef const __attribute__((address_space(1))) float gfloat;
@@ -962,6 +973,9 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
       gv[j][1] = *reinterpret_cast<const float4*>(gain + e + 4);
     }
   }
+  // (pinned: left to the scheduler, the gain loads sink below the weight
+  // loads, and the staging wait for them then drains every weight load)
+  __builtin_amdgcn_sched_barrier(0);
   // 2. weight loads of the wave's row
   uint32_t lr = row < out ? row : out - 1;  // clamp; result discarded
   const uint32_t wr = (extra_row != NO_ROW && lr == out - 1) ? extra_row : row_base + lr;
@@ -1349,6 +1363,7 @@ __global__ __launch_bounds__(64 * WPB) void gemv_q_kernel(const uint8_t* qp, con
       gv[j][1] = *reinterpret_cast<const float4*>(gain + e + 4);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // x / gain loads before the weights (as in gemv_n_kernel)
   // 2. block values and scales of the wave's row (clamped; unused past the
   //    end).  SwiGLU rows index w1's and w3's blocks as one list of 2 NB
   //    (i < NB: w1 block i, else w3 block i - NB), which fills the lanes
@@ -2048,20 +2063,22 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, flo
   const float* pbase = part + ((size_t(col) * Hkv + g) * max_chunks * rep + w) * (HD + 2);
   const size_t stride = size_t(rep) * (HD + 2);
   const uint32_t seq = col / cps, lc = col % cps;
-  const uint32_t done = opt_word(done_ptr ? done_ptr + size_t(seq) * sw : nullptr);
-  const uint32_t pb = opt_word(pos_ptr ? pos_ptr + size_t(seq) * sw : nullptr);
   if constexpr (MAXC > 0) {
     static_assert(MAXC <= HD, "one thread per chunk slot");
-    __shared__ float2 ml[MAXC];
-    // no branch before these loads: every slot is read, the result is
-    // discarded at the store when the launch has nothing to merge
-    float2 mlv = make_float2(0.f, 0.f);
-    if (d < uint32_t(MAXC))
-      mlv = *reinterpret_cast<const float2*>(pbase + size_t(min(d, max_chunks - 1)) * stride);
+    __shared__ float2 ml[HD];  // one slot per thread: an unconditional store keeps its load up front
+    // no branch before these loads: every slot is read (threads past MAXC
+    // re-read the last one), the result is discarded at the store when the
+    // launch has nothing to merge; the state words go out last, so the
+    // wait for them (they are made wave-uniform right after their loads)
+    // leaves the partials in flight no longer than they take anyway
+    const float2 mlv =
+        gload_f2(reinterpret_cast<const float2*>(pbase + size_t(min(min(d, uint32_t(MAXC) - 1u), max_chunks - 1)) * stride));
     float oc[MAXC];
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) oc[c] = pbase[size_t(min(uint32_t(c), max_chunks - 1)) * stride + 2 + d];
-    if (d < uint32_t(MAXC)) ml[d] = mlv;
+    for (int c = 0; c < MAXC; ++c) oc[c] = gload_f32(pbase + size_t(min(uint32_t(c), max_chunks - 1)) * stride + 2 + d);
+    uint32_t done, pb;
+    opt_words2(done_ptr, pos_ptr, size_t(seq) * sw, done, pb);
+    ml[d] = mlv;
     __syncthreads();
     const uint32_t pos = pb + pos_offset + lc;
     const bool live = !done && pos < a.max_seq;
@@ -2086,6 +2103,8 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, flo
     constexpr int NWV = HD / 64;
     __shared__ float fs[ATTN_MAX_CHUNKS];
     __shared__ float rm[NWV], rl[NWV];
+    const uint32_t done = opt_word(done_ptr ? done_ptr + size_t(seq) * sw : nullptr);
+    const uint32_t pb = opt_word(pos_ptr ? pos_ptr + size_t(seq) * sw : nullptr);
     const uint32_t pos = pb + pos_offset + lc;
     if (done || pos >= a.max_seq) return;
     const uint32_t nch = (pos + CH) / CH;
