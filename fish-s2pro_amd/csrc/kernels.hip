@@ -1213,6 +1213,109 @@ hipError_t gemv_fold_launch(const GemvArgs& a, hipStream_t s) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV, one column, each row's steps split over the block's waves.
+//   The block owns R consecutive rows; wave w takes the 512-element steps
+//   k = w, w + WPB, ... (k < KIT) of all R rows: it loads only those steps of
+//   x into registers and issues its weight loads (R per step) before anything
+//   waits.  x never goes through LDS: each x element is read once per block,
+//   by the one wave that uses it, and reused across the R rows from
+//   registers.  Each row's partial sums are reduced in the wave (DPP) and
+//   then over the waves in a fixed order through LDS, so the result does not
+//   depend on timing.  Lane r < R of wave 0 finishes row r; its residual
+//   (RESID) is loaded with the weights.  This form keeps whole blocks per CU
+//   where one row per wave would not (w2: 2560 rows of 9728 -> 512 blocks).
+// ---------------------------------------------------------------------------
+template <uint32_t WT, int EPI, int KIT, int WPB, int R>
+__global__ __launch_bounds__(64 * WPB) void gemv_ks_kernel(const uint8_t* w_rows, const float* x_in,
+                                                               const uint32_t* done_ptr, uint32_t row_bytes,
+                                                               uint32_t out, uint32_t row_base, uint32_t extra_row,
+                                                               GemvArgs a) {
+  static_assert(EPI == EPI_STORE || EPI == EPI_RESID, "one matrix, no activation");
+  static_assert(R <= WAVE, "one epilogue lane per row");
+  constexpr int KW = (KIT + WPB - 1) / WPB;
+  __shared__ float part[R][WPB];
+  const int lane = threadIdx.x & (WAVE - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const uint32_t row0 = blockIdx.x * R;
+  // 1. this wave's steps of x (a step past KIT re-reads the last one)
+  //    No branch in the load phase: a branch around loads leaves the wait
+  //    counts at the join conservative, and the first use then waits for
+  //    nearly every load in flight.
+  float4 xv[KW][2];
+#pragma unroll
+  for (int j = 0; j < KW; ++j) {
+    const uint32_t e = uint32_t(min(wave + j * WPB, KIT - 1)) * 512u + lane * 8u;
+    xv[j][0] = *reinterpret_cast<const float4*>(x_in + e);
+    xv[j][1] = *reinterpret_cast<const float4*>(x_in + e + 4);
+  }
+  // 2. weight loads: step-major, so the dot loop consumes them in issue order;
+  //    a step past KIT reads x's first lines instead (cached, no HBM bytes;
+  //    the values are not used)
+  const uint8_t* rp[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t lr = min(row0 + uint32_t(r), out - 1u);  // clamp; result discarded
+    const uint32_t wr = (extra_row != NO_ROW && lr == out - 1u) ? extra_row : row_base + lr;
+    rp[r] = w_rows + size_t(wr) * row_bytes;
+  }
+  Raw8<WT> wb[KW][R];
+#pragma unroll
+  for (int j = 0; j < KW; ++j) {
+    const bool live = wave + j * WPB < KIT;
+    const uint32_t e = live ? uint32_t(wave + j * WPB) * 512u + lane * 8u : lane * 8u;
+#pragma unroll
+    for (int r = 0; r < R; ++r) wb[j][r] = load_raw<WT>(live ? rp[r] : reinterpret_cast<const uint8_t*>(x_in), e);
+  }
+  const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
+  float* ybase = a.y;
+  asm volatile("" : "+s"(ybase));
+  // lane r's row (clamped): its residual, behind the weight loads
+  const uint32_t my_row = min(row0 + min(uint32_t(lane), uint32_t(R) - 1u), out - 1u);
+  const float yres = EPI == EPI_RESID ? gload_f32(ybase + my_row) : 0.0f;
+  // 3. dot products of the wave's steps
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < KW; ++j) {
+    if (wave + j * WPB < KIT) {
+      const float xv8[8] = {xv[j][0].x, xv[j][0].y, xv[j][0].z, xv[j][0].w,
+                            xv[j][1].x, xv[j][1].y, xv[j][1].z, xv[j][1].w};
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float w[8];
+        decode8<WT>(wb[j][r], w);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[r] = fmaf(w[i], xv8[i], acc[r]);
+      }
+    }
+  }
+  // 4. per-row sums: the wave's, then the waves' in order
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float g = wave_sum(acc[r]);
+    if (lane == 0) part[r][wave] = g;
+  }
+  __syncthreads();
+  if (done || wave != 0 || lane >= R) return;
+  const uint32_t row = row0 + uint32_t(lane);
+  if (row >= out) return;
+  float gsum = part[lane][0];
+#pragma unroll
+  for (int i = 1; i < WPB; ++i) gsum += part[lane][i];
+  ybase[row] = EPI == EPI_RESID ? __fadd_rn(yres, gsum) : gsum;
+}
+
+template <uint32_t WT, int EPI, int KIT, int WPB, int R>
+hipError_t gemv_ks_launch(const GemvArgs& a, hipStream_t s) {
+  if (a.row_bytes > UINT32_MAX) return hipErrorInvalidValue;
+  const dim3 grid((a.out + R - 1) / R);
+  hipLaunchKernelGGL((gemv_ks_kernel<WT, EPI, KIT, WPB, R>), grid, dim3(64 * WPB), 0, s, a.w, a.x, a.done,
+                     uint32_t(a.row_bytes), a.out, a.row_base, a.extra_row, a);
+  return hipGetLastError();
+}
+
 // Row shapes of the S2-Pro family: 512 / 1536 (tiny), 2560, 4096, 9728.
 // Returns hipErrorNotSupported for other row lengths.
 template <uint32_t WT, int NCOL, int EPI>
@@ -1245,10 +1348,18 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
     // 640 blocks for the 256 CUs (8 left a quarter of the CUs with two
     // blocks): w2 12.1 -> 10.9 us, wo 6.3 -> 5.9 us
     // wo at one column: 10 waves, one 256-block round with x staged 256
-    // times instead of 1280 (5.3 -> 5.0 us); w2 keeps 4 (5 and 10 waves: 10.5
-    // and 10.9 us against 10.3)
+    // times instead of 1280 (5.3 -> 5.0 us); w2 in this form kept 4 (5 and
+    // 10 waves: 10.5 and 10.9 us against 10.3)
+    // (wo in the split-step form -- 8/4/8 waves x 10/5/5 rows -- ran the
+    // default decode at 295.2-296.2 / 286.4-286.5 / 286.6-287.2 frames/s
+    // against 299.5-300.3 with this one)
     case 4096: return gemv_n_launch<WT, NCOL, EPI, 8, false, (NCOL == 1 ? 10 : 2)>(a, s);
-    case 9728: return gemv_n_launch<WT, NCOL, EPI, 19, false, 4>(a, s);
+    // w2 at one column (F16): the split-step form, 10 waves x 5 rows, 512
+    // blocks (default decode 300.3-300.6 frames/s against 298.2-298.4)
+    case 9728:
+      if constexpr (NCOL == 1 && WT == W_F16 && (EPI == EPI_STORE || EPI == EPI_RESID))
+        return gemv_ks_launch<WT, EPI, 19, 10, 5>(a, s);
+      return gemv_n_launch<WT, NCOL, EPI, 19, false, 4>(a, s);
     default: return hipErrorNotSupported;
   }
 }

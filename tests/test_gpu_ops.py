@@ -50,7 +50,7 @@ def test_dequant_bit_exact(eng, gtype):
 @pytest.mark.parametrize("in_dim,out_dim,ncol", [(512, 768, 1), (2560, 6144, 1), (9728, 2560, 1), (4096, 2560, 1),
                                                  (4096, 2560, 2), (2560, 9728, 4), (1536, 100, 3),
                                                  (9728, 2560, 8), (4096, 2560, 16), (512, 1029, 11),
-                                                 (1056, 64, 5)])
+                                                 (1056, 64, 5), (9728, 103, 1), (9728, 2561, 1)])
 def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
     rng = np.random.default_rng(in_dim + out_dim + ncol)
     wf = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
