@@ -2065,18 +2065,27 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
     }
   }
   __syncthreads();
-  // 4. scores (lane = position) and chunk softmax
+  // 4. scores and chunk softmax: position lane % CH, the two halves of the
+  //    wave take the two halves of the head dimension (two accumulators
+  //    each), joined by one cross-half exchange
   float m = -INFINITY, l = 0.0f;
+  static_assert(CH == 32, "two half-waves of 32 positions");
   if (wave < rep) {
-    float s = -INFINITY;
-    if (lane < nt) {
-      float dsum = 0.0f;
+    const uint32_t tp = lane & (CH - 1), hh = lane / CH;
+    const float* qh = &qs[wave][hh * (HD / 2)];
+    const float* kh = &kt[tp * KS + hh * (HD / 2)];
+    float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll 16
-      for (int d = 0; d < HD; ++d) dsum = fmaf(qs[wave][d], kt[lane * KS + d], dsum);
-      s = dsum * a.scale;
+    for (int d = 0; d < HD / 2; d += 2) {
+      d0 = fmaf(qh[d], kh[d], d0);
+      d1 = fmaf(qh[d + 1], kh[d + 1], d1);
     }
+    float dsum = d0 + d1;
+    dsum += __shfl_xor(dsum, 32);
+    const bool live = hh == 0 && tp < nt;
+    const float s = live ? dsum * a.scale : -INFINITY;
     m = wave_max(s);
-    const float p = (lane < nt) ? expf(s - m) : 0.0f;
+    const float p = live ? expf(s - m) : 0.0f;
     l = wave_sum(p);
     if (lane < CH) ps[wave][lane] = p;
   }
@@ -2198,11 +2207,15 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, flo
 #pragma unroll
     for (int c = 0; c < MAXC; ++c)
       if (uint32_t(c) < nch) M = fmaxf(M, ml[c].x);
+    // each chunk's weight once per block (thread c), not once per thread
+    __shared__ float fw[MAXC];
+    if (d < uint32_t(MAXC)) fw[d] = d < nch ? expf(ml[d].x - M) : 0.0f;
+    __syncthreads();
     float L = 0.0f, acc = 0.0f;
 #pragma unroll
     for (int c = 0; c < MAXC; ++c) {
       if (uint32_t(c) < nch) {
-        const float f = expf(ml[c].x - M);
+        const float f = fw[c];
         L = fmaf(ml[c].y, f, L);
         acc = fmaf(oc[c], f, acc);
       }
