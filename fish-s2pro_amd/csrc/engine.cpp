@@ -689,12 +689,13 @@ void Engine::bmm(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, cons
 }
 
 // Whether lin() runs L over ncol columns on the batched MFMA product.  At
-// two columns the two-column GEMV is faster for single matrices with rows of
-// up to 4096 (S2-Pro wqkv 9.2 vs 12.9 us, wo 7.7 vs 8.3 us); w1/w3 and w2
-// stay on the product (22.6 vs 25.8 us, 15.9 vs 17.9 us).
+// two columns every S2-Pro linear is faster on the two-column GEMV (wqkv 8.3
+// vs 12.6 us, wo 7.6 vs 8.5, w1/w3 18.5 vs 23.4, w2 12.3 vs 16.6; the first
+// Fast-AR sub-step of a frame runs two columns: default decode 308.5-308.7
+// frames/s against 304.1-304.3 with w1/w3 and w2 on the product).
 bool Engine::uses_bmm(const DevLin& L, const DevLin* L3, uint32_t ncol) const {
   if (bmm_off_ || !L.wt || !bmm_min_cols_ || ncol < bmm_min_cols_ || (L3 && !L3->wt)) return false;
-  return !(ncol == 2 && !L3 && L.in <= 4096 && gemv_rows_per_block(L.in, L.out, false, false, ncol) != 0);
+  return !(ncol == 2 && gemv_rows_per_block(L.type, L.in, L.out, false, L3 != nullptr, ncol) != 0);
 }
 
 void Engine::lin(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, const float* x, uint32_t ldx,
@@ -731,7 +732,7 @@ L2Warm Engine::warm_for(const DevLin& L, const DevLin* L3, uint32_t ncol, bool n
   // Q8_0 / Q4_0 GEMVs read the repacked planes, except one matrix with
   // 2560-wide rows and an RMSNorm (wqkv, the heads): that stays on the GGUF rows
   if (L.qp && ncol <= 2 && !(norm && !L3 && L.in == 2560)) return w;
-  const uint32_t rpb = gemv_rows_per_block(L.in, L.out, norm, L3 != nullptr, ncol);
+  const uint32_t rpb = gemv_rows_per_block(L.type, L.in, L.out, norm, L3 != nullptr, ncol);
   const size_t span = size_t(rpb) * L.row_bytes;
   if (!rpb || span % 16 || span > UINT32_MAX || reinterpret_cast<uintptr_t>(L.w) % 16 ||
       (L3 && reinterpret_cast<uintptr_t>(L3->w) % 16))
@@ -901,8 +902,8 @@ void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const
     lin(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
     // one wave per tile from 8 columns: the Fast-AR weights are re-read every
     // sub-step and this product runs warm (batch 8: 22.3 us against 24.2 us
-    // with the two waves that suit the Slow-AR layers; at 2 columns two
-    // waves stay faster)
+    // with the two waves that suit the Slow-AR layers; 3-7 columns keep two
+    // waves; 2 columns take the GEMV)
     lin(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
         L.w1.out, done, ncol >= 8 && (L.w1.out + 15) / 16 >= 512 ? 1u : 0u);
     lin(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.w2.out, done);

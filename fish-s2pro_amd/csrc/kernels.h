@@ -145,10 +145,10 @@ hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s);
 // Warming planes a kernel of `plane` blocks per plane appends for w (0 when
 // w.base is null); hipErrorInvalidValue in *err for a malformed descriptor.
 uint32_t l2_warm_planes(const L2Warm& w, uint32_t plane, hipError_t* err);
-// Rows per block of the decode GEMV launch_gemv picks for 1-2 columns and
-// this row length (norm: RMS-normalised input; dual: SwiGLU pair), or 0 when
-// another kernel serves the shape.
-uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, uint32_t ncol);
+// Rows per block of the decode GEMV launch_gemv picks for 1-2 columns, this
+// weight type and row length (norm: RMS-normalised input; dual: SwiGLU
+// pair), or 0 when another kernel serves the shape.
+uint32_t gemv_rows_per_block(uint32_t wtype, uint32_t in, uint32_t out, bool norm, bool dual, uint32_t ncol);
 
 // Fused decode attention for ncol / cols_per_seq sequences, each with
 // cols_per_seq consecutive query positions starting at its *pos_ptr +

@@ -1226,28 +1226,32 @@ hipError_t gemv_fold_launch(const GemvArgs& a, hipStream_t s) {
 //   (RESID) is loaded with the weights.  This form keeps whole blocks per CU
 //   where one row per wave would not (w2: 2560 rows of 9728 -> 512 blocks).
 // ---------------------------------------------------------------------------
-template <uint32_t WT, int EPI, int KIT, int WPB, int R>
+template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, int R>
 __global__ __launch_bounds__(64 * WPB) void gemv_ks_kernel(const uint8_t* w_rows, const float* x_in,
                                                                const uint32_t* done_ptr, uint32_t row_bytes,
                                                                uint32_t out, uint32_t row_base, uint32_t extra_row,
                                                                GemvArgs a) {
   static_assert(EPI == EPI_STORE || EPI == EPI_RESID, "one matrix, no activation");
-  static_assert(R <= WAVE, "one epilogue lane per row");
+  static_assert(NCOL * R <= WAVE, "one epilogue lane per (column, row)");
   constexpr int KW = (KIT + WPB - 1) / WPB;
-  __shared__ float part[R][WPB];
+  __shared__ float part[NCOL][R][WPB];
   const int lane = threadIdx.x & (WAVE - 1);
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const uint32_t row0 = blockIdx.x * R;
+  const uint32_t ldx = a.ldx;
   // 1. this wave's steps of x (a step past KIT re-reads the last one)
   //    No branch in the load phase: a branch around loads leaves the wait
   //    counts at the join conservative, and the first use then waits for
   //    nearly every load in flight.
-  float4 xv[KW][2];
+  float4 xv[NCOL][KW][2];
 #pragma unroll
   for (int j = 0; j < KW; ++j) {
     const uint32_t e = uint32_t(min(wave + j * WPB, KIT - 1)) * 512u + lane * 8u;
-    xv[j][0] = *reinterpret_cast<const float4*>(x_in + e);
-    xv[j][1] = *reinterpret_cast<const float4*>(x_in + e + 4);
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      xv[c][j][0] = *reinterpret_cast<const float4*>(x_in + size_t(c) * ldx + e);
+      xv[c][j][1] = *reinterpret_cast<const float4*>(x_in + size_t(c) * ldx + e + 4);
+    }
   }
   // 2. weight loads: step-major, so the dot loop consumes them in issue order;
   //    a step past KIT reads x's first lines instead (cached, no HBM bytes;
@@ -1269,49 +1273,60 @@ __global__ __launch_bounds__(64 * WPB) void gemv_ks_kernel(const uint8_t* w_rows
   }
   const uint32_t done = done_ptr ? __builtin_nontemporal_load(done_ptr) : 0u;
   float* ybase = a.y;
-  asm volatile("" : "+s"(ybase));
-  // lane r's row (clamped): its residual, behind the weight loads
-  const uint32_t my_row = min(row0 + min(uint32_t(lane), uint32_t(R) - 1u), out - 1u);
-  const float yres = EPI == EPI_RESID ? gload_f32(ybase + my_row) : 0.0f;
+  uint32_t ldy = a.ldy;
+  asm volatile("" : "+s"(ybase), "+s"(ldy));
+  // lane c R + r finishes (column c, row r): its residual (clamped address),
+  // behind the weight loads
+  const uint32_t ec = min(uint32_t(lane) / uint32_t(R), uint32_t(NCOL) - 1u), er = uint32_t(lane) % uint32_t(R);
+  const uint32_t my_row = min(row0 + er, out - 1u);
+  const float yres = EPI == EPI_RESID ? gload_f32(ybase + size_t(ec) * ldy + my_row) : 0.0f;
   // 3. dot products of the wave's steps
-  float acc[R];
+  float acc[NCOL][R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int c = 0; c < NCOL; ++c)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[c][r] = 0.0f;
 #pragma unroll
   for (int j = 0; j < KW; ++j) {
     if (wave + j * WPB < KIT) {
-      const float xv8[8] = {xv[j][0].x, xv[j][0].y, xv[j][0].z, xv[j][0].w,
-                            xv[j][1].x, xv[j][1].y, xv[j][1].z, xv[j][1].w};
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float w[8];
         decode8<WT>(wb[j][r], w);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[r] = fmaf(w[i], xv8[i], acc[r]);
+        for (int c = 0; c < NCOL; ++c) {
+          const float xv8[8] = {xv[c][j][0].x, xv[c][j][0].y, xv[c][j][0].z, xv[c][j][0].w,
+                                xv[c][j][1].x, xv[c][j][1].y, xv[c][j][1].z, xv[c][j][1].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[c][r] = fmaf(w[i], xv8[i], acc[c][r]);
+        }
       }
     }
   }
   // 4. per-row sums: the wave's, then the waves' in order
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const float g = wave_sum(acc[r]);
-    if (lane == 0) part[r][wave] = g;
+  for (int c = 0; c < NCOL; ++c) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float g = wave_sum(acc[c][r]);
+      if (lane == 0) part[c][r][wave] = g;
+    }
   }
   __syncthreads();
-  if (done || wave != 0 || lane >= R) return;
-  const uint32_t row = row0 + uint32_t(lane);
+  if (done || wave != 0 || lane >= NCOL * R) return;
+  const uint32_t row = row0 + er;
   if (row >= out) return;
-  float gsum = part[lane][0];
+  float gsum = part[ec][er][0];
 #pragma unroll
-  for (int i = 1; i < WPB; ++i) gsum += part[lane][i];
-  ybase[row] = EPI == EPI_RESID ? __fadd_rn(yres, gsum) : gsum;
+  for (int i = 1; i < WPB; ++i) gsum += part[ec][er][i];
+  ybase[size_t(ec) * ldy + row] = EPI == EPI_RESID ? __fadd_rn(yres, gsum) : gsum;
 }
 
-template <uint32_t WT, int EPI, int KIT, int WPB, int R>
+template <uint32_t WT, int NCOL, int EPI, int KIT, int WPB, int R>
 hipError_t gemv_ks_launch(const GemvArgs& a, hipStream_t s) {
   if (a.row_bytes > UINT32_MAX) return hipErrorInvalidValue;
   const dim3 grid((a.out + R - 1) / R);
-  hipLaunchKernelGGL((gemv_ks_kernel<WT, EPI, KIT, WPB, R>), grid, dim3(64 * WPB), 0, s, a.w, a.x, a.done,
+  hipLaunchKernelGGL((gemv_ks_kernel<WT, NCOL, EPI, KIT, WPB, R>), grid, dim3(64 * WPB), 0, s, a.w, a.x, a.done,
                      uint32_t(a.row_bytes), a.out, a.row_base, a.extra_row, a);
   return hipGetLastError();
 }
@@ -1357,8 +1372,8 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
     // w2 at one column (F16): the split-step form, 10 waves x 5 rows, 512
     // blocks (default decode 300.3-300.6 frames/s against 298.2-298.4)
     case 9728:
-      if constexpr (NCOL == 1 && WT == W_F16 && (EPI == EPI_STORE || EPI == EPI_RESID))
-        return gemv_ks_launch<WT, EPI, 19, 10, 5>(a, s);
+      if constexpr (NCOL <= 2 && WT == W_F16 && (EPI == EPI_STORE || EPI == EPI_RESID))
+        return gemv_ks_launch<WT, NCOL, EPI, 19, 10, 5>(a, s);
       return gemv_n_launch<WT, NCOL, EPI, 19, false, 4>(a, s);
     default: return hipErrorNotSupported;
   }
@@ -3142,7 +3157,7 @@ uint32_t l2_warm_planes(const L2Warm& w, uint32_t plane, hipError_t* err) {
 }
 
 // The block shapes gemv_k_pick launches (rows per wave x waves per block).
-uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, uint32_t ncol) {
+uint32_t gemv_rows_per_block(uint32_t wtype, uint32_t in, uint32_t out, bool norm, bool dual, uint32_t ncol) {
   const uint32_t rs = dual ? 1u : 2u;
   switch (in) {
     case 512:
@@ -3151,7 +3166,7 @@ uint32_t gemv_rows_per_block(uint32_t in, uint32_t out, bool norm, bool dual, ui
       if (!norm) return rs * 4u;
       return (ncol == 1 && !dual) ? (out <= 4096 ? 16u : 12u) : 8u;
     case 4096: return norm ? 8u : (ncol == 1 ? 10u : 2u);
-    case 9728: return norm ? 8u : 4u;
+    case 9728: return norm ? 8u : (ncol == 1 && !dual && wtype == W_F16 ? 5u : 4u);  // (split-step w2: 5)
     default: return 0u;
   }
 }
