@@ -1350,6 +1350,8 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
           if (a.out <= 4096) return gemv_n_launch<WT, 1, EPI, 5, true, 16>(a, s);
           return gemv_n_launch<WT, 1, EPI, 5, true, 12>(a, s);
         }
+        // (two columns keep 8: wqkv 8.4 us against 9.4 / 8.7 / 10.1 with 4 /
+        // 12 / 16 waves, w1/w3 19.9 against 21.4 / 26.2 / 27.1)
         return gemv_n_launch<WT, NCOL, EPI, 5>(a, s);
       default: break;
     }
@@ -1368,7 +1370,9 @@ hipError_t gemv_k_pick(const GemvArgs& a, hipStream_t s) {
     // (wo in the split-step form -- 8/4/8 waves x 10/5/5 rows -- ran the
     // default decode at 295.2-296.2 / 286.4-286.5 / 286.6-287.2 frames/s
     // against 299.5-300.3 with this one)
-    case 4096: return gemv_n_launch<WT, NCOL, EPI, 8, false, (NCOL == 1 ? 10 : 2)>(a, s);
+    // (two columns: 10 waves as well, 5.9 us against 7.6 / 6.5 / 7.4 with 2
+    // / 4 / 8)
+    case 4096: return gemv_n_launch<WT, NCOL, EPI, 8, false, 10>(a, s);
     // w2 at one column (F16): the split-step form, 10 waves x 5 rows, 512
     // blocks (default decode 300.3-300.6 frames/s against 298.2-298.4)
     case 9728:
@@ -3165,7 +3169,7 @@ uint32_t gemv_rows_per_block(uint32_t wtype, uint32_t in, uint32_t out, bool nor
     case 2560:
       if (!norm) return rs * 4u;
       return (ncol == 1 && !dual) ? (out <= 4096 ? 16u : 12u) : 8u;
-    case 4096: return norm ? 8u : (ncol == 1 ? 10u : 2u);
+    case 4096: return norm ? 8u : 10u;
     case 9728: return norm ? 8u : (ncol == 1 && !dual && wtype == W_F16 ? 5u : 4u);  // (split-step w2: 5)
     default: return 0u;
   }
