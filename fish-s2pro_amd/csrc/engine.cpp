@@ -897,16 +897,27 @@ void Engine::enqueue_fast_layers(uint32_t nseq, uint32_t cps, uint32_t p0, const
     aa.cols_per_seq = cps;
     aa.seq_stride_words = sizeof(DevState) / 4;
     aa.seq_stride_kv = fslot_kv_;
-    aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, warm_fast_);
+    // The last layer's outputs feed only the head, which reads each slot's
+    // last position: with several positions per slot (the first pass), wo,
+    // w1/w3 and w2 run on those columns alone (strided views of fatt_ and
+    // fh_; the earlier positions' rows are rewritten before the next pass
+    // reads fh_, and their K/V were appended by the attention above).
+    const bool last_only = l + 1 == s.fast_layers && cps > 1;
+    const uint32_t fcols = last_only ? nseq : ncol;
+    const float* att_in = fatt_ + (last_only ? size_t(cps - 1) * fq : 0);
+    const uint32_t att_ld = last_only ? cps * fq : fq;
+    float* res = fh_ + (last_only ? size_t(cps - 1) * s.dim : 0);
+    const uint32_t res_ld = last_only ? cps * s.dim : s.dim;
+    aa.warm = warm_for(L.wo, nullptr, fcols, false, 0, warm_fast_);
     HIPC(launch_attention(aa, stream_));
-    lin(L.wo, nullptr, EPI_RESID, ncol, fatt_, fq, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.wo.out, done);
+    lin(L.wo, nullptr, EPI_RESID, fcols, att_in, att_ld, nullptr, 0.0f, res, res_ld, 0, NO_ROW, L.wo.out, done);
     // one wave per tile from 8 columns: the Fast-AR weights are re-read every
     // sub-step and this product runs warm (batch 8: 22.3 us against 24.2 us
     // with the two waves that suit the Slow-AR layers; 3-7 columns keep two
     // waves; 2 columns take the GEMV)
-    lin(L.w1, &L.w3, EPI_SWIGLU_FAST, ncol, fh_, s.dim, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
-        L.w1.out, done, ncol >= 8 && (L.w1.out + 15) / 16 >= 512 ? 1u : 0u);
-    lin(L.w2, nullptr, EPI_RESID, ncol, fact_, s.fast_ffn, nullptr, 0.0f, fh_, s.dim, 0, NO_ROW, L.w2.out, done);
+    lin(L.w1, &L.w3, EPI_SWIGLU_FAST, fcols, res, res_ld, L.ffn_norm, s.fast_eps, fact_, s.fast_ffn, 0, NO_ROW,
+        L.w1.out, done, fcols >= 8 && (L.w1.out + 15) / 16 >= 512 ? 1u : 0u);
+    lin(L.w2, nullptr, EPI_RESID, fcols, fact_, s.fast_ffn, nullptr, 0.0f, res, res_ld, 0, NO_ROW, L.w2.out, done);
   }
 }
 
