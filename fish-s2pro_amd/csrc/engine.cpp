@@ -266,7 +266,10 @@ class Engine {
   // L2 warming of the output projection by decode attention
   uint32_t warm_blocks_ = 256;            // warming blocks per kernel (0: off)
   uint32_t warm_depth_ = 4;               // 16-byte loads per thread in flight
-  uint32_t warm_split_ = 100;             // % of the Slow-AR rows warmed by the partial kernel (rest: merge)
+  // % of the Slow-AR wo rows warmed by the attention partials: none by default
+  // (default decode 309.0-309.4 frames/s against 307.4-307.9 with all of them
+  // and 305.6-306.1 with 30-60 %; the Fast-AR warming pays, 1 % on the line)
+  uint32_t warm_slow_ = 0;
   uint32_t warm_fast_ = 100;              // % of the Fast-AR rows warmed (one attention kernel)
   uint32_t warm_step_ = 0;                // % of the first linear's rows warmed by embedding / sampler (no measured gain: off)
   size_t warm_bytes_ = size_t(24) << 20;  // at most this many weight bytes warmed (8 L2s of 4 MiB)
@@ -474,11 +477,11 @@ Engine::Engine(const s2hip_config& cfg) {
   // to read the next linear's rows into L2 (blocks rounded down to a
   // multiple of 8; 0: off)
   if (const char* v = getenv("S2HIP_L2_WARM")) {
-    unsigned b = 0, d = warm_depth_, sp = warm_split_, fp = warm_fast_, ep = warm_step_;
+    unsigned b = 0, d = warm_depth_, sp = warm_slow_, fp = warm_fast_, ep = warm_step_;
     const int n = sscanf(v, "%u,%u,%u,%u,%u", &b, &d, &sp, &fp, &ep);
     if (n >= 1) warm_blocks_ = b & ~7u;
     if (n >= 2) warm_depth_ = d;
-    if (n >= 3) warm_split_ = std::min(sp, 100u);
+    if (n >= 3) warm_slow_ = std::min(sp, 100u);
     if (n >= 4) warm_fast_ = std::min(fp, 100u);
     if (n >= 5) warm_step_ = std::min(ep, 100u);
   }
@@ -823,9 +826,10 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     aa.cols_per_seq = cps;
     aa.seq_stride_words = sizeof(DevState) / 4;
     aa.seq_stride_kv = slot_kv_;
-    const bool merge = attn_chunks_ > 1 && attn_mode_ == ATTN_SPLIT;  // a merge kernel follows the partials
-    aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, merge ? warm_split_ : 100);
-    if (merge) aa.warm2 = warm_for(L.wo, nullptr, ncol, false, warm_split_, 100);
+    // (the merge kernel carries no warming: its 128-thread blocks warm too
+    // slowly, and it waits for them -- 292.3-292.7 against 307.4-308.1
+    // frames/s with half the rows given to it)
+    aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, warm_slow_);
     HIPC(launch_attention(aa, stream_));
     prof_mark(PROF_ATTN);
     lin(L.wo, nullptr, EPI_RESID, ncol, att_, q, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.wo.out, done);

@@ -182,7 +182,6 @@ struct AttnArgs {
   uint32_t seq_stride_words;
   size_t seq_stride_kv;
   L2Warm warm;             // rows of the next GEMV (wo) warmed by extra blocks of the partial kernel
-  L2Warm warm2;            // ... and of the merge kernel
   uint32_t kv_f16;         // 1: k_cache / v_cache hold f16 (seq_stride_kv and offsets in elements)
   // one column: q / k / v from row `code` of qkv_rows ([fold.n][(H + 2 Hkv)
   // hd]) instead of qkv, code = *code_ptr or, with fold.logits, the greedy

@@ -2191,11 +2191,6 @@ template <int HD, int CH, int MAXC>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const float* part, float* out, const uint32_t* pos_ptr,
                                                             const uint32_t* done_ptr, uint32_t ncol, uint32_t max_chunks,
                                                             uint32_t shape, uint32_t pos_offset, AttnArgs a) {
-  if (__builtin_expect(blockIdx.y >= ncol, 0)) {  // warming planes after the merge blocks (laid out last)
-    const uint32_t L = blockIdx.x + gridDim.x * blockIdx.y;
-    l2_warm(a.warm2, L, L - gridDim.x * ncol, threadIdx.x, HD);
-    return;
-  }
   const uint32_t H = shape & 0xffu, Hkv = (shape >> 8) & 0xffu, cps = (shape >> 16) & 0xffu, sw = shape >> 24;
   const uint32_t h = blockIdx.x, col = blockIdx.y, d = threadIdx.x;
   const uint32_t rep = H / Hkv, g = h / rep, w = h % rep;
@@ -3292,7 +3287,6 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   }
   hipError_t werr = hipSuccess;
   const uint32_t planes = l2_warm_planes(a.warm, a.max_chunks * a.Hkv, &werr);  // z-planes of warming blocks
-  const uint32_t planes2 = a.max_chunks > 1 ? l2_warm_planes(a.warm2, a.H, &werr) : 0u;
   if (werr != hipSuccess) return werr;
   const dim3 grid(a.max_chunks, a.Hkv, a.ncol + planes);
   if (a.hd != 64 && a.hd != 128) return hipErrorInvalidValue;
@@ -3310,7 +3304,7 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
     launch_partial<128, false>(a, grid, s);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.max_chunks == 1) return e;
-  const dim3 cgrid(a.H, a.ncol + planes2);
+  const dim3 cgrid(a.H, a.ncol);
   if (a.hd == 64)
     launch_combine<64>(a, cgrid, s);
   else

@@ -259,9 +259,9 @@ def test_attention_modes_match_oracle(tiny_gguf, monkeypatch, fused):
 @pytest.mark.parametrize("which", ["f16", "q8"])
 def test_l2_warming_leaves_codes_unchanged(request, monkeypatch, which, warm):
     """The blocks that read the next linear's rows into L2 (carried by the
-    attention partial / merge kernels, the step embedding and the Fast-AR
-    sampler) only read: codes and RNG state equal those of a run without them,
-    and greedy codes stay bit-exact against the oracle."""
+    attention partial kernels, the step embedding and the Fast-AR sampler)
+    only read: codes and RNG state equal those of a run without them, and
+    greedy codes stay bit-exact against the oracle."""
     path = request.getfixturevalue("tiny_gguf" if which == "f16" else "tiny_q8_gguf")
     prompt = make_prompt(synth.TINY, 70, seed=17)
     kw = dict(temperature=0.7, top_p=0.9, top_k=0, min_tokens_before_end=100, rng_state=9)
