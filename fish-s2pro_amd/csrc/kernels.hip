@@ -1845,7 +1845,7 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 //       per (col, g) elects the last block of the pair, which merges them with
 //       agent-scope loads and resets the counter for the next launch.
 // ---------------------------------------------------------------------------
-template <int HD, int CH, bool LAST, bool KH, bool GATHER = false>
+template <int HD, int CH, bool LAST, bool KH, bool GATHER = false, bool WARM = true>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, void* k_cache, void* v_cache,
                                                              const uint32_t* pos_ptr, const uint32_t* done_ptr,
                                                              uint32_t ncol, uint32_t max_seq, uint32_t kv_stride,
@@ -1862,10 +1862,16 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
   __shared__ uint32_t is_last;
   __shared__ float gm1[GATHER ? GEMV_WAVES : 1], gm2[GATHER ? GEMV_WAVES : 1];
   __shared__ uint32_t gid[GATHER ? GEMV_WAVES : 1], gcnt[GATHER ? GEMV_WAVES : 1];
-  if (__builtin_expect(blockIdx.z >= ncol, 0)) {  // warming planes after the attention blocks (laid out last)
-    const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    l2_warm(a.warm, L, L - gridDim.x * gridDim.y * ncol, threadIdx.x, 256u);
-    return;
+  // warming planes after the attention blocks (laid out last); launches
+  // without warming use the form compiled without this path (its keep-alive
+  // asm statement makes the compiler treat memory as written, which turns
+  // the state-word reads below into vector loads)
+  if constexpr (WARM) {
+    if (__builtin_expect(blockIdx.z >= ncol, 0)) {
+      const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+      l2_warm(a.warm, L, L - gridDim.x * gridDim.y * ncol, threadIdx.x, 256u);
+      return;
+    }
   }
   const uint32_t H = shape & 0xffu, Hkv = (shape >> 8) & 0xffu, cps_ = (shape >> 16) & 0xffu, sw = shape >> 24;
   const uint32_t chunk = blockIdx.x, g = blockIdx.y, col = blockIdx.z;
@@ -3262,7 +3268,10 @@ void launch_partial(const AttnArgs& a, dim3 grid, hipStream_t s) {
                        a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
     return;
   }
-  hipLaunchKernelGGL((a.kv_f16 ? attn_partial_kernel<HD, 32, LAST, true> : attn_partial_kernel<HD, 32, LAST, false>),
+  const bool warm = a.warm.base != nullptr;
+  hipLaunchKernelGGL((a.kv_f16 ? (warm ? attn_partial_kernel<HD, 32, LAST, true> : attn_partial_kernel<HD, 32, LAST, true, false, false>)
+                               : (warm ? attn_partial_kernel<HD, 32, LAST, false>
+                                       : attn_partial_kernel<HD, 32, LAST, false, false, false>)),
                      grid, dim3(256), 0, s, a.qkv, static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache),
                      a.pos_ptr, a.done, a.ncol, a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
 }
