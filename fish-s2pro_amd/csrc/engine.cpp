@@ -180,7 +180,9 @@ class Engine {
            const float* norm, float eps, float* y, uint32_t ldy, uint32_t row_base, uint32_t extra_row,
            uint32_t out_rows, const uint32_t* done, uint32_t bmm_waves = 0, const GreedyFold* fold = nullptr);
   // ncol = nseq * cps columns of slots seq0 .. seq0 + nseq - 1 in h_
-  void enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done);
+  // advance: add cps to each unfinished slot's n_past afterwards (the frame
+  // loop leaves it to its sampler instead)
+  void enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done, bool advance = true);
   void enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done);
   // fold (nullable): the first linear takes its input from the greedy sample
   // code (nullable): the single column is the embedding of *code (the first
@@ -265,6 +267,7 @@ class Engine {
   void ensure_fast_table();
   // L2 warming of the output projection by decode attention
   uint32_t warm_blocks_ = 256;            // warming blocks per kernel (0: off)
+  float* gemv_xn_ = nullptr;              // normalised-x output of the next gemv() launch (consumed there)
   uint32_t warm_depth_ = 4;               // 16-byte loads per thread in flight
   // % of the Slow-AR wo rows warmed by the attention partials: none by default
   // (default decode 309.0-309.4 frames/s against 307.4-307.9 with all of them
@@ -663,6 +666,7 @@ void Engine::gemv(const DevLin& L, const DevLin* L3, int epi, uint32_t ncol, con
     a.qp3 = L3 ? L3->qp : nullptr;
     a.qs3 = L3 ? L3->qs : nullptr;
     if (fold) a.fold = *fold;
+    if (gemv_xn_) a.xn_out = gemv_xn_ + size_t(c) * ldx;
     HIPC(launch_gemv(L.type, epi, int(w), a, stream_));
     c += w;
   }
@@ -789,7 +793,7 @@ void Engine::prof_book(uint32_t nseq) {
 // slots from seq0 with cps consecutive positions each, then n_past += cps per
 // slot.  done (nullable) stops the linears; attention and the position
 // update skip each finished slot by its own done word.
-void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done) {
+void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, const uint32_t* done, bool advance) {
   const s2hip_spec& s = spec;
   const uint32_t q = s.heads * s.head_dim, kv = s.kv_heads * s.head_dim, qkv_w = q + 2 * kv;
   const uint32_t ncol = nseq * cps;
@@ -837,7 +841,7 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     lin(L.w2, nullptr, EPI_RESID, ncol, act_, s.ffn, nullptr, 0.0f, h_, s.dim, 0, NO_ROW, L.w2.out, done);
     prof_mark(PROF_LINEAR);
   }
-  HIPC(launch_add_position(st, cps, nseq, stream_));
+  if (advance) HIPC(launch_add_position(st, cps, nseq, stream_));
 }
 
 // SlowArOutputHeadF16Weights::forward_logits (slow_ar.rs:943-955): post-norm
@@ -846,9 +850,18 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
 // masked to -inf before sampling.  hn [ncol][dim], logits [ncol][n_cand].
 void Engine::enqueue_head(uint32_t ncol, float* hn, float* logits, bool full, const uint32_t* done) {
   const s2hip_spec& s = spec;
-  HIPC(launch_rms_norm(h_, norm_, hn, s.dim, ncol, s.eps, done, stream_));
-  lin(head_cand_, nullptr, EPI_STORE, ncol, hn, s.dim, nullptr, 0.0f, logits, n_cand_, s.semantic_begin, head_extra_,
-      n_cand_, done);
+  if (ncol == 1 && (s.dim == 512 || s.dim == 1536 || s.dim == 2560)) {
+    // one column: the RMSNorm is the head GEMV's own (its block 0 writes the
+    // normalised row to hn, which the Fast-AR and the full head read)
+    gemv_xn_ = hn;
+    lin(head_cand_, nullptr, EPI_STORE, 1, h_, s.dim, norm_, s.eps, logits, n_cand_, s.semantic_begin, head_extra_,
+        n_cand_, done);
+    gemv_xn_ = nullptr;
+  } else {
+    HIPC(launch_rms_norm(h_, norm_, hn, s.dim, ncol, s.eps, done, stream_));
+    lin(head_cand_, nullptr, EPI_STORE, ncol, hn, s.dim, nullptr, 0.0f, logits, n_cand_, s.semantic_begin,
+        head_extra_, n_cand_, done);
+  }
   if (full)
     gemv(head_full_, nullptr, EPI_STORE, 1, hn, s.dim, nullptr, 0.0f, logits_full_, s.vocab, 0, NO_ROW, s.vocab, done);
 }
@@ -1016,7 +1029,7 @@ void Engine::enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_st
   ea.err = &st_->err;
   ea.warm = warm_for(slow_[0].wqkv, nullptr, nseq, true, 0, warm_step_);
   HIPC(launch_embed(ea, stream_));
-  enqueue_slow_layers(nseq, 1, 0, done);
+  enqueue_slow_layers(nseq, 1, 0, done, false);  // the sampler advances n_past
   prof_mark(PROF_NONE);
   enqueue_head(nseq, hn_, logits_c_, false, done);
   prof_mark(PROF_HEAD);
@@ -1029,6 +1042,7 @@ void Engine::enqueue_frame(const SamplerCfg& cfg, uint32_t nseq, size_t codes_st
   sa.st = st_;
   sa.im_end = im_end_;
   sa.after_step = 1;
+  sa.advance = 1;
   sa.codes_out = codes_dev_;
   sa.num_codebooks = s.num_codebooks;
   sa.n_seq = nseq;

@@ -99,6 +99,9 @@ struct GemvArgs {
   const uint16_t* qs;
   const uint16_t* qs3;
   GreedyFold fold;       // fold.logits != nullptr: x comes from the greedy sample
+  // nullable, with norm: block 0 also writes the normalised x (x * scale *
+  // gain, [ncol][ldx]) there (the RMSNorm GEMV form serves such launches)
+  float* xn_out;
 };
 
 // Q8_0 / Q4_0 rows repacked for the decode GEMV: block b of row r (32
@@ -239,6 +242,7 @@ struct SampleArgs {
   // slow mode
   uint32_t im_end;
   uint32_t after_step;       // 1: a Slow step just ran (advance frame counters)
+  uint32_t advance;          // added to n_past of each unfinished sequence first (the step's position)
   int32_t* codes_out;        // [num_codebooks][max_new] codebook-major (nullable)
   uint32_t num_codebooks;
   // fast mode

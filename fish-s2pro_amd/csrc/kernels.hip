@@ -1090,7 +1090,8 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
     if (lane == 0) red[c][wave] = ss;
   }
   if constexpr (NORM) __syncthreads();
-  // 4. (normalised) x into LDS
+  // 4. (normalised) x into LDS (and, xn_out, from block 0 to memory)
+  const bool xn0 = NORM && !FOLD && a.xn_out != nullptr && blockIdx.x == 0;
 #pragma unroll
   for (int c = 0; c < NCOL; ++c) {
     float scale = 1.0f;
@@ -1115,6 +1116,9 @@ __global__ __launch_bounds__(64 * WPB) void gemv_n_kernel(const uint8_t* w_rows,
             u.w = __fmul_rn(__fmul_rn(u.w, scale), g.w);
           }
           xs[c][(k * 512 + lane * 8) / 4 + h] = u;
+          if constexpr (NORM && !FOLD) {
+            if (xn0) *reinterpret_cast<float4*>(a.xn_out + size_t(c) * a.ldx + k * 512 + lane * 8 + 4 * h) = u;
+          }
         }
       }
     }
@@ -2994,6 +2998,7 @@ __global__ __launch_bounds__(SAMPLE_THREADS) void sample_slow_kernel(SampleArgs 
   if (st->done) return;
   __shared__ uint32_t gen;
   if (threadIdx.x == 0) {
+    st->n_past += a.advance;  // the Slow step's position (an unfinished sequence only)
     if (a.after_step) {
       if (a.codes_out) {
         for (uint32_t cb = 0; cb < a.num_codebooks; ++cb)
@@ -3187,7 +3192,13 @@ hipError_t launch_gemv(uint32_t wtype, int epi, int ncol, const GemvArgs& a, hip
       default: return gemv_fold_launch<W_Q4_0>(a, s);
     }
   }
-  if (wtype != W_F16 && (ncol == 1 || ncol == 2) && a.qp && a.qs && a.row_base == 0 && a.extra_row == NO_ROW &&
+  // the normalised-x output: only the RMSNorm GEMV form (gemv_n_kernel) over
+  // 1-2 columns of the rows it serves writes it
+  if (a.xn_out && (!a.norm || a.w3 || ncol > 2 || a.fold.logits || a.ldx % 4 ||
+                   (a.in != 512 && a.in != 1536 && a.in != 2560) ||
+                   reinterpret_cast<uintptr_t>(a.xn_out) % 16))
+    return hipErrorInvalidValue;
+  if (wtype != W_F16 && !a.xn_out && (ncol == 1 || ncol == 2) && a.qp && a.qs && a.row_base == 0 && a.extra_row == NO_ROW &&
       a.ldx % 4 == 0 && !((epi == EPI_SWIGLU_SLOW || epi == EPI_SWIGLU_FAST) && (!a.qp3 || !a.qs3))) {
     const hipError_t e = ncol == 1
         ? (wtype == W_Q8_0 ? gemv_q_epi<W_Q8_0, 1>(epi, a, s) : gemv_q_epi<W_Q4_0, 1>(epi, a, s))
