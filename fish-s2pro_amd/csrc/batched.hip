@@ -340,6 +340,260 @@ __global__ __launch_bounds__(WAVES * 64) void bmm_kernel(BmmArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Product for up to 8 columns: hi and lo parts share one MFMA.  The B
+// operand's 16 columns carry the hi parts of the 8 activation columns (0-7)
+// and their lo parts (8-15), so one MFMA per weight step and matrix does the
+// work of two, and no MFMA column is idle.  Each activation is split once,
+// by the lane that stages it: the staging lanes scale and split their 16
+// values of a chunk and write the f16 hi / lo fragments (plus, for RMSNorm
+// inputs, each 4-value sum of squares) into the wave's LDS buffer; the MFMA
+// lanes then read one 16-byte fragment per step and do no conversions.  The
+// values, the scale, the MFMA columns' sums and every later addition are
+// those of bmm_kernel, in the same order, so both give the same bits.
+//   LDS per wave and buffer: XC steps x [16 fragment rows of PK_ROW halfs]
+//   (row n < 8: hi of column n, row n + 8: its lo), and per step the sums of
+//   squares [column][k group][half].
+// ---------------------------------------------------------------------------
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+constexpr int PK_ROW = 40;                 // halfs per fragment row: 32 + 8 (conflict-free 16-byte reads)
+constexpr int PK_STEP = 16 * PK_ROW + 32;  // halfs per step: +64 B puts the 4 steps' staging writes on other banks
+constexpr int PK_QSTEP = 72;               // sum-of-squares floats per step: 8 columns x 4 groups x 2, +8
+
+template <int EPI, bool NORM, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void bmm_pk_kernel(BmmArgs a) {
+  constexpr bool DUAL = (EPI == EPI_SWIGLU_SLOW || EPI == EPI_SWIGLU_FAST);
+  constexpr int NW = DUAL ? 2 : 1;
+  constexpr int CHH = XC * PK_STEP;             // halfs per chunk buffer
+  constexpr int CHQ = NORM ? XC * PK_QSTEP : 1;  // floats per chunk buffer
+  constexpr int LDX = 4;                        // staging loads per chunk (8 rows, 2 per load)
+  // each wave's partial sums go to its own staging buffers after its loop
+  static_assert(NW * 64 * 16 <= 2 * CHH * 2, "partials must fit the staging buffers");
+  __shared__ __align__(16) _Float16 fs[WAVES][2][CHH];
+  __shared__ __align__(16) float qs[WAVES][2][CHQ];
+  __shared__ float ssq[WAVES][64];
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t tm = blockIdx.x, m0 = tm * 16;
+  const uint32_t kt = a.K / 32, KS = kt / WAVES;
+  const uint32_t n = lane & 15u, grp = lane >> 4, col = n & 7u;
+  const size_t tile0 = (size_t(tm) * kt + size_t(wave) * KS) * 512 + size_t(lane) * 8;
+  const _Float16* wp0 = a.wt + tile0;
+  const _Float16* wp1 = DUAL ? a.wt3 + tile0 : wp0;
+  const uint32_t last = KS - 1;
+  const uint32_t nsc = (KS + WIN - 1) / WIN;  // pairs of chunks
+  const uint32_t kbase = wave * KS * 32;
+  // staging: load j of a chunk covers rows 2 j + lane / 32, 4-float group lane % 32
+  const uint32_t srow = lane >> 5, sq = lane & 31u;
+  _Float16* fsw = &fs[wave][0][0];
+  float* qsw = &qs[wave][0][0];
+
+  auto stage_load = [&](floatx4 (&r)[LDX], floatx4& gr, uint32_t chunk) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < LDX; ++j) {
+      const uint32_t row = 2 * j + srow;
+      const uint32_t rr = row < a.N ? row : 0u;
+      const uint32_t k = min(kbase + chunk * (XC * 32) + 4 * sq, a.K - 4);
+      r[j] = *reinterpret_cast<const floatx4*>(a.x + size_t(rr) * a.ldx + k);
+    }
+    if constexpr (NORM) {
+      const uint32_t k = min(kbase + chunk * (XC * 32) + 4 * sq, a.K - 4);
+      gr = *reinterpret_cast<const floatx4*>(a.norm + k);
+    }
+  };
+
+  half8 wb[WIN][NW];
+  floatx4 sxa[LDX], sxb[LDX], sga, sgb;  // staged chunks in flight (even, odd)
+  stage_load(sxa, sga, 0);
+  stage_load(sxb, sgb, 1);
+#pragma unroll
+  for (int i = 0; i < WIN; ++i) {
+    const uint32_t t = min(uint32_t(i), last);
+    wb[i][0] = bmm_wload(reinterpret_cast<const half8*>(wp0 + 512 * t));
+    if constexpr (DUAL) wb[i][1] = bmm_wload(reinterpret_cast<const half8*>(wp1 + 512 * t));
+  }
+  // Per-(wave, column) power-of-two scale from the largest |x g| of the first
+  // two chunks of this wave's range, as in bmm_kernel.  Staging lanes need it
+  // for their rows 2 j + lane / 32, MFMA lanes for column n % 8.
+  float cinv_s[LDX];
+  float cmax_c = 0.0f;
+  auto pow2_exp = [](float cm) __attribute__((always_inline)) {
+    const int e = int((__float_as_uint(cm) >> 23) & 0xffu) - 127;
+    return (cm >= 1.0e-30f && cm <= 1.0e30f) ? e : 0;
+  };
+#pragma unroll
+  for (int j = 0; j < LDX; ++j) {
+    floatx4 va = sxa[j], vb = sxb[j];
+    if constexpr (NORM) {
+      va = va * sga;
+      vb = vb * sgb;
+    }
+    float m = fmaxf(fmaxf(fabsf(va.x), fabsf(va.y)), fmaxf(fabsf(va.z), fabsf(va.w)));
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(vb.x), fabsf(vb.y)), fmaxf(fabsf(vb.z), fabsf(vb.w))));
+    const float rm = row_reduce(m, [](float a, float b) { return fmaxf(a, b); });
+    const float lo = fmaxf(lane_read_f32(rm, 0), lane_read_f32(rm, 16));
+    const float hi = fmaxf(lane_read_f32(rm, 32), lane_read_f32(rm, 48));
+    cmax_c = (uint32_t(j) == (col >> 1)) ? ((col & 1u) ? hi : lo) : cmax_c;
+    cinv_s[j] = __uint_as_float(uint32_t(127 - pow2_exp(srow ? hi : lo)) << 23);
+  }
+  const float cscale = __uint_as_float(uint32_t(127 + pow2_exp(cmax_c)) << 23);
+
+  // split chunk `chunk` (registers r, gains gr) into LDS buffer buf: hi of
+  // row j at fragment row j, lo at row j + 8; values of steps past this
+  // wave's range are zero (their weight fragments re-read in-bounds data)
+  auto stage_split = [&](const floatx4 (&r)[LDX], const floatx4& gr, uint32_t chunk, int buf)
+                         __attribute__((always_inline)) {
+    const uint32_t st = sq >> 3, off = 4 * (sq & 7u);
+    const bool live = chunk * XC + st < KS;
+    _Float16* dst = fsw + buf * CHH + st * PK_STEP + off;
+    const floatx4 z4 = floatx4{};
+#pragma unroll
+    for (int j = 0; j < LDX; ++j) {
+      const uint32_t row = 2 * j + srow;
+      floatx4 v = live ? r[j] : z4;
+      if constexpr (NORM) {
+        qsw[buf * CHQ + st * PK_QSTEP + row * 8 + (sq & 7u)] = (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+        v = v * gr;
+      }
+      v = v * cinv_s[j];
+      half4 h, l;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        h[e] = _Float16(v[e]);
+        l[e] = _Float16((v[e] - float(h[e])) * 2048.0f);
+      }
+      *reinterpret_cast<half4*>(dst + row * PK_ROW) = h;
+      *reinterpret_cast<half4*>(dst + (row + 8) * PK_ROW) = l;
+    }
+  };
+  stage_split(sxa, sga, 0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  floatx4 acc[NW];
+#pragma unroll
+  for (int m = 0; m < NW; ++m) acc[m] = floatx4{};
+  float ss = 0.0f;
+  // the steps of chunk c from LDS buffer h (weight slots h XC .. h XC + 3);
+  // each step's fragment is read one step ahead of its use
+  auto chunk_steps = [&](uint32_t c, auto hc) __attribute__((always_inline)) {
+    constexpr int h = decltype(hc)::value;
+    const _Float16* fb = fsw + h * CHH + n * PK_ROW + 8 * grp;
+    const float* qb = qsw + h * CHQ + col * 8 + 2 * grp;
+    half8 cf = *reinterpret_cast<const half8*>(fb);
+    float2 cq = make_float2(0.f, 0.f);
+    if constexpr (NORM) cq = *reinterpret_cast<const float2*>(qb);
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+      const uint32_t s = c * XC + i;
+      const int wi = h * XC + i;
+      half8 nf = cf;
+      float2 nq = cq;
+      if (i + 1 < XC) {
+        nf = *reinterpret_cast<const half8*>(fb + (i + 1) * PK_STEP);
+        if constexpr (NORM) nq = *reinterpret_cast<const float2*>(qb + (i + 1) * PK_QSTEP);
+      }
+      if constexpr (NORM) {
+        ss += cq.x;
+        ss += cq.y;
+      }
+#pragma unroll
+      for (int m = 0; m < NW; ++m) acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wb[wi][m], cf, acc[m], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t tw = min(s + WIN, last);
+      wb[wi][0] = bmm_wload(reinterpret_cast<const half8*>(wp0 + 512 * tw));
+      if constexpr (DUAL) wb[wi][1] = bmm_wload(reinterpret_cast<const half8*>(wp1 + 512 * tw));
+      __builtin_amdgcn_sched_barrier(0);
+      cf = nf;
+      cq = nq;
+    }
+  };
+  for (uint32_t sc = 0; sc < nsc; ++sc) {
+    // chunk 2 sc from buffer 0: first the odd chunk (loaded one chunk ago)
+    // into buffer 1, then the loads of chunk 2 sc + 2
+    stage_split(sxb, sgb, 2 * sc + 1, 1);
+    stage_load(sxa, sga, 2 * sc + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_steps(2 * sc, std::integral_constant<int, 0>{});
+    // chunk 2 sc + 1 from buffer 1
+    stage_split(sxa, sga, 2 * sc + 2, 0);
+    stage_load(sxb, sgb, 2 * sc + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    chunk_steps(2 * sc + 1, std::integral_constant<int, 1>{});
+  }
+  // partials of wave w: slot m, lane l of its own staging region (lanes
+  // n < 8: hi sums of column n, lanes n >= 8: lo sums of column n - 8)
+  auto red = [&](uint32_t w, int slot) __attribute__((always_inline)) -> floatx4* {
+    return reinterpret_cast<floatx4*>(&fs[w][0][0]) + slot * 64 + lane;
+  };
+#pragma unroll
+  for (int m = 0; m < NW; ++m) *red(wave, m) = acc[m] * cscale;
+  if constexpr (NORM) ssq[wave][lane] = ss;
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int m = 0; m < NW; ++m) {
+    floatx4 t = *red(0, m);
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += *red(w, m);
+    floatx4 tl;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tl[v] = __shfl_xor(t[v], 8, 64);
+    acc[m] = t + tl * (1.0f / 2048.0f);
+  }
+  float r = 1.0f;
+  if constexpr (NORM) {
+    float t = ssq[0][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) t += ssq[w][lane];
+    // the four k groups of column n: lanes n, n + 16, n + 32, n + 48
+    t = t + __shfl_xor(t, 16, 64);
+    t = t + __shfl_xor(t, 32, 64);
+    r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(t, float(a.K)), a.eps)));
+  }
+  // a non-finite activation (or one beyond the split's range) leaves
+  // non-finite sums
+  bool bad = false;
+#pragma unroll
+  for (int m = 0; m < NW; ++m)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) bad = bad || !(fabsf(acc[m][v]) <= 3.0e38f);
+  bad = bad && n < a.N;
+  if (__any(bad) && lane == 0 && a.err) atomicOr(a.err, ERR_F16_RANGE);
+  const uint32_t done = a.done ? *a.done : 0u;
+  if (done || n >= a.N) return;
+  float* yrow = a.y + size_t(n) * a.ldy;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const uint32_t m = m0 + 4 * grp + v;
+    if (m >= a.M) continue;
+    const float g = acc[0][v] * r;
+    if constexpr (EPI == EPI_STORE) {
+      yrow[m] = g;
+    } else if constexpr (EPI == EPI_RESID) {
+      yrow[m] = __fadd_rn(yrow[m], g);
+    } else {
+      const float u = acc[NW - 1][v] * r;
+      if constexpr (EPI == EPI_SWIGLU_SLOW) {
+        const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf_glibc(-g)));
+        yrow[m] = __fmul_rn(__fmul_rn(g, sig), u);
+      } else {
+        yrow[m] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_glibc(-g))), u);
+      }
+    }
+  }
+}
+
+template <int EPI, bool NORM>
+hipError_t launch_bmm_pk(const BmmArgs& a, uint32_t waves, hipStream_t s) {
+  const dim3 grid((a.M + 15) / 16);
+  switch (waves) {
+    case 1: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 1>), grid, dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 2>), grid, dim3(128), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 4>), grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 template <int EPI, bool NORM, int NB>
 hipError_t launch_bmm_waves(const BmmArgs& a, uint32_t waves, hipStream_t s) {
   const dim3 grid((a.M + 15) / 16);
@@ -355,7 +609,7 @@ hipError_t launch_bmm_waves(const BmmArgs& a, uint32_t waves, hipStream_t s) {
 template <int EPI>
 hipError_t launch_bmm_epi(const BmmArgs& a, uint32_t waves, hipStream_t s) {
   const bool norm = a.norm != nullptr;
-  if (a.N <= 8) return norm ? launch_bmm_waves<EPI, true, 8>(a, waves, s) : launch_bmm_waves<EPI, false, 8>(a, waves, s);
+  if (a.N <= 8) return norm ? launch_bmm_pk<EPI, true>(a, waves, s) : launch_bmm_pk<EPI, false>(a, waves, s);
   return norm ? launch_bmm_waves<EPI, true, 16>(a, waves, s) : launch_bmm_waves<EPI, false, 16>(a, waves, s);
 }
 
