@@ -589,6 +589,7 @@ hipError_t launch_bmm_pk(const BmmArgs& a, uint32_t waves, hipStream_t s) {
     case 1: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 1>), grid, dim3(64), 0, s, a); break;
     case 2: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 2>), grid, dim3(128), 0, s, a); break;
     case 4: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 4>), grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((bmm_pk_kernel<EPI, NORM, 8>), grid, dim3(512), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -54,6 +54,7 @@ constexpr uint32_t BMM_MAX_K = 10240;    // input width limit of the batched pro
 constexpr uint32_t ACT_COLS = 2 * MAX_SEQS;  // activation columns (Fast-AR pass 0 has two per request)
 constexpr uint32_t PREFILL_CHUNK = 512;  // prompt tokens per MFMA prefill pass
 constexpr uint32_t FRAME_BATCH = 4;
+constexpr uint32_t ATTN_CHECK_MIN_SEQS = 2;  // batched requests: tail attention chunks check first
 constexpr size_t WEIGHT_PAD = 256;  // trailing bytes so block loads never leave a buffer
 
 // Device scratch of the allocation-free sampler entry point
@@ -322,6 +323,10 @@ class Engine {
   uint64_t graph_kv_gen_ = 0;
   bool graph_bmm_off_ = false;
   bool graph_fold_off_ = false;
+  uint32_t graph_check_from_ = 0;
+  // Slow-AR decode attention: chunks from here on check the position before
+  // their K/V tile (0: every chunk loads it first); set per generate call
+  uint32_t attn_check_from_ = 0;
 };
 
 Engine::Engine(const s2hip_config& cfg) {
@@ -833,6 +838,7 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     // (the merge kernel carries no warming: its 128-thread blocks warm too
     // slowly, and it waits for them -- 292.3-292.7 against 307.4-308.1
     // frames/s with half the rows given to it)
+    aa.check_from = attn_check_from_;
     aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, warm_slow_);
     HIPC(launch_attention(aa, stream_));
     prof_mark(PROF_ATTN);
@@ -1529,6 +1535,16 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   // ERR_KV_OVERFLOW on the device and the call fails, as SlowArState::eval does
   // (slow_ar.rs:469-474).
   const uint32_t max_frames = p.max_new_tokens;
+  // Batched requests: the Slow-AR attention grid spans max_seq_len, and the
+  // chunks past every request's prompt read the position before their K/V
+  // tile, so chunks past a request's end read nothing (one request keeps
+  // every tile load ahead of the position: its attention is bound by
+  // latency, not by bytes)
+  {
+    size_t min_cols = cols[0];
+    for (uint32_t b = 1; b < nseq; ++b) min_cols = std::min(min_cols, cols[b]);
+    attn_check_from_ = nseq >= ATTN_CHECK_MIN_SEQS ? uint32_t(min_cols / ATTN_CHUNK + 1) : 0u;
+  }
   const bool profile = (flags_ & S2HIP_FLAG_PROFILE) != 0;
   bool use_graph = !(flags_ & S2HIP_FLAG_NO_GRAPH) && !profile;
   slow_prof = s2hip_slow_profile{};
@@ -1543,7 +1559,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
   if (use_graph && launched < max_frames) {
     const bool stale = !graph_exec_ || graph_codes_ != codes_dev_ || graph_codes_stride_ != ncodes ||
                        graph_nseq_ != nseq || graph_kv_gen_ != kv_gen_ || graph_bmm_off_ != bmm_off_ ||
-                       graph_fold_off_ != fold_off_ ||
+                       graph_fold_off_ != fold_off_ || graph_check_from_ != attn_check_from_ ||
                        graph_cfg_.temperature != cfg.temperature ||
                        graph_cfg_.top_p != cfg.top_p || graph_cfg_.top_k != cfg.top_k;
     if (stale) {
@@ -1573,6 +1589,7 @@ void Engine::generate(uint32_t nseq, const int32_t* const* prompts, const size_t
       graph_kv_gen_ = kv_gen_;
       graph_bmm_off_ = bmm_off_;
       graph_fold_off_ = fold_off_;
+      graph_check_from_ = attn_check_from_;
     }
   }
   // Frames in batches; the done flag of batch i is read while batch i+1 runs.

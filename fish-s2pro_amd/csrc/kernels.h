@@ -186,6 +186,11 @@ struct AttnArgs {
   size_t seq_stride_kv;
   L2Warm warm;             // rows of the next GEMV (wo) warmed by extra blocks of the partial kernel
   uint32_t kv_f16;         // 1: k_cache / v_cache hold f16 (seq_stride_kv and offsets in elements)
+  // nonzero: chunks >= check_from read their sequence's position before
+  // their K/V tile and end without loading it when they lie past the
+  // sequence; chunks below it load the tile first (set it to a lower bound of
+  // every sequence's chunk count, so that only chunks that may be dead wait)
+  uint32_t check_from;
   // one column: q / k / v from row `code` of qkv_rows ([fold.n][(H + 2 Hkv)
   // hd]) instead of qkv, code = *code_ptr or, with fold.logits, the greedy
   // sample of the logits (then block 0 also has the sampler's side effects,
@@ -195,6 +200,7 @@ struct AttnArgs {
   GreedyFold fold;
 };
 enum : uint32_t { ATTN_SPLIT = 0u, ATTN_FUSED = 1u };
+constexpr uint32_t ATTN_CHUNK = 32;         // cache positions per decode attention block
 constexpr uint32_t ATTN_MAX_CHUNKS = 1024;  // max_seq <= 32768
 uint32_t attention_chunks(uint32_t max_seq, uint32_t mode);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);

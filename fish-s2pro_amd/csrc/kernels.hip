@@ -1852,8 +1852,11 @@ __global__ __launch_bounds__(64) void qkv_post_kernel(QkvPostArgs a) {
 template <int HD, int CH, bool LAST, bool KH, bool GATHER = false, bool WARM = true>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, void* k_cache, void* v_cache,
                                                              const uint32_t* pos_ptr, const uint32_t* done_ptr,
-                                                             uint32_t ncol, uint32_t max_seq, uint32_t kv_stride,
+                                                             uint32_t ncol_cf, uint32_t max_seq, uint32_t kv_stride,
                                                              uint32_t shape, AttnArgs a) {
+  // ncol | check_from << 8: both among the preloaded arguments, so blocks
+  // below check_from issue their tile loads without waiting on a scalar load
+  const uint32_t ncol = ncol_cf & 0xffu, check_from = ncol_cf >> 8;
   using KT = std::conditional_t<KH, uint16_t, float>;  // cache element: f16 bits or f32
   constexpr int KS = HD + 1;
   constexpr int PER = CH * HD / 4 / 256;  // float4 per thread per tile
@@ -1911,6 +1914,14 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
     code_word = opt_word(a.code_ptr);
     st_done = opt_word(fl ? &a.fold.st->done : nullptr);
   }
+  // chunks from check_from on may lie past the sequence (the bound is known
+  // where the launch is recorded): they wait for the position and a dead one
+  // ends here, before its tile is read
+  if constexpr (!GATHER) {
+    if (check_from != 0u && chunk >= check_from) {
+      if (done || t0 >= pbase + a.pos_offset + lc + 1u) return;
+    }
+  }
   float4 kr[PER], vr[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -1925,6 +1936,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const float* qkv, voi
       vr[j] = *reinterpret_cast<const float4*>(vc + size_t(tt) * HD + d);
     }
   }
+  // the whole tile is issued before anything that needs the position word
+  // (left to itself, the scheduler moves the position arithmetic, and so the
+  // wait for the state words, in between the tile loads)
+  if constexpr (!GATHER) __builtin_amdgcn_sched_barrier(0);
   // rotation rows of the query position and of column `wave`'s position:
   // they need only the position word, so they go out with the loads above
   // (addresses clamped into the table, which has max_seq rows; values for
@@ -3242,7 +3257,7 @@ hipError_t launch_qkv_post(const QkvPostArgs& a, hipStream_t s) {
 
 uint32_t attention_chunks(uint32_t max_seq, uint32_t mode) {
   (void)mode;
-  return (max_seq + 31u) / 32u;
+  return (max_seq + ATTN_CHUNK - 1u) / ATTN_CHUNK;
 }
 
 // H | Hkv << 8 | cols_per_seq << 16 | seq_stride_words << 24: the shape word
@@ -3275,8 +3290,8 @@ void launch_partial(const AttnArgs& a, dim3 grid, hipStream_t s) {
   if (!LAST && a.qkv_rows) {  // q / k / v from a table row (f32 cache: the Fast-AR's)
     if (a.kv_f16) return;     // rejected by launch_attention
     hipLaunchKernelGGL((attn_partial_kernel<HD, 32, false, false, true>), grid, dim3(256), 0, s, a.qkv,
-                       static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache), a.pos_ptr, a.done, a.ncol,
-                       a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
+                       static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache), a.pos_ptr, a.done,
+                       a.ncol | a.check_from << 8, a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
     return;
   }
   const bool warm = a.warm.base != nullptr;
@@ -3284,7 +3299,8 @@ void launch_partial(const AttnArgs& a, dim3 grid, hipStream_t s) {
                                : (warm ? attn_partial_kernel<HD, 32, LAST, false>
                                        : attn_partial_kernel<HD, 32, LAST, false, false, false>)),
                      grid, dim3(256), 0, s, a.qkv, static_cast<void*>(a.k_cache), static_cast<void*>(a.v_cache),
-                     a.pos_ptr, a.done, a.ncol, a.max_seq, uint32_t(a.seq_stride_kv), attn_shape_word(a), a);
+                     a.pos_ptr, a.done, a.ncol | a.check_from << 8, a.max_seq, uint32_t(a.seq_stride_kv),
+                     attn_shape_word(a), a);
 }
 
 hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
@@ -3295,7 +3311,7 @@ hipError_t launch_attention(const AttnArgs& args, hipStream_t s) {
   if (a.ncol > a.cols_per_seq && a.seq_stride_words == 0 && (a.pos_ptr || a.done)) return hipErrorInvalidValue;
   if (a.H % a.Hkv || a.H / a.Hkv > 4 || a.H > 255 || a.seq_stride_words > 255 || a.seq_stride_kv > UINT32_MAX)
     return hipErrorInvalidValue;
-  if (a.max_chunks != attention_chunks(a.max_seq, a.mode)) return hipErrorInvalidValue;
+  if (a.max_chunks != attention_chunks(a.max_seq, a.mode) || a.check_from > a.max_chunks) return hipErrorInvalidValue;
   if (a.qkv_rows) {
     const GreedyFold& f = a.fold;
     if (a.ncol != 1 || a.cols_per_seq != 1 || a.mode != ATTN_SPLIT || a.kv_f16) return hipErrorInvalidValue;
