@@ -34,6 +34,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t CG_TF = 256;    // frames per block tile
 constexpr uint32_t CG_MAXLD = 10;  // 16-byte staging loads per thread per stage
+constexpr size_t CG_FMAJOR_WEIGHT_BYTES = size_t(3) << 19;  // 1.5 MiB of a 4 MiB XCD L2
 
 // LDS rows are KC halfs (CH = KC / 8 chunks of 16 bytes), chunk c of row r
 // stored at c ^ swz(r).  Weight rows are read 32 at a time from a multiple
@@ -69,16 +70,44 @@ __device__ __forceinline__ float snake(float x, float alpha) { return snake_cw(x
 template <int MC, int KC, int PL, bool FU = false>
 __global__ __launch_bounds__(256, 2) void conv_gemm_kernel(ConvGemmArgs a, uint32_t m_tiles, uint32_t f_tiles,
                                                            uint32_t halo, int32_t wbase, int32_t toff0,
-                                                           int32_t tstep) {
+                                                           int32_t tstep, uint32_t fmajor) {
   constexpr uint32_t TM = 32 * MC, CH = KC / 8;
   extern __shared__ __align__(16) _Float16 cg_lds[];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  // workgroup b runs on XCD b % 8: tile t = XCD-major order, m-major tiles
-  const uint32_t nb = m_tiles * f_tiles, b = blockIdx.x, xcd = b & 7u, slot = b >> 3;
-  const uint32_t q8 = nb >> 3, r8 = nb & 7u;
+  // Workgroup b runs on XCD b % 8; tiles are dealt to XCDs in contiguous
+  // ranges (XCD-major), in one of two orders.
+  //   fmajor: over all phases, t = (ft * phases + phase) * m_tiles + mt, so
+  //     the blocks that read one frame tile's input window (every phase and
+  //     weight tile) run one after another on one XCD: the window comes from
+  //     HBM once and from that XCD's L2 after, while the weights of every
+  //     (phase, m tile), small enough, stay in each L2.
+  //   otherwise: phase by phase (phase = b / (m_tiles f_tiles)), and within
+  //     a phase t = mt * f_tiles + ft: an XCD works through one weight tile at
+  //     a time, which its L2 serves to all of that XCD's frame tiles.
+  const uint32_t nb1 = m_tiles * f_tiles;
+  uint32_t b = blockIdx.x, nb = gridDim.x, phase = 0, phases = nb / nb1;
+  if (!fmajor) {
+    phase = b / nb1;
+    b -= phase * nb1;
+    nb = nb1;
+  }
+  const uint32_t xcd = b & 7u, slot = b >> 3, q8 = nb >> 3, r8 = nb & 7u;
   const uint32_t t = xcd < r8 ? xcd * (q8 + 1u) + slot : r8 * (q8 + 1u) + (xcd - r8) * q8 + slot;
-  const uint32_t mt = t / f_tiles, ft = t - mt * f_tiles;
-  const uint32_t phase = blockIdx.y;
+  uint32_t mt, ft;
+  if (fmajor) {
+    mt = t % m_tiles;
+    const uint32_t tr = t / m_tiles;
+    phase = tr % phases;
+    ft = tr / phases;
+  } else {
+    mt = t / f_tiles;
+    ft = t - mt * f_tiles;
+  }
+  // (the divisions above are expanded on the vector unit: move the results
+  // to scalar registers, where they cost no vector registers in the loop)
+  mt = uint32_t(__builtin_amdgcn_readfirstlane(int(mt)));
+  ft = uint32_t(__builtin_amdgcn_readfirstlane(int(ft)));
+  phase = uint32_t(__builtin_amdgcn_readfirstlane(int(phase)));
   const uint32_t f0 = ft * CG_TF;
   const uint32_t AR = CG_TF + halo;
   const uint32_t a_chunks = PL * AR * CH, w_chunks = a.G * TM * CH, tot = a_chunks + w_chunks;
@@ -596,8 +625,12 @@ hipError_t conv_gemm_launch(const ConvGemmArgs& a, uint32_t phases, hipStream_t 
            size_t(2 * splits) * rows * a.M <= a.part_cap)
       splits *= 2;
   }
-  conv_gemm_kernel<MC, KC, PL, FU><<<dim3(m_tiles * f_tiles, phases, splits), 256, lds, s>>>(
-      a, m_tiles, f_tiles, halo, wbase, a.off0 - wbase, a.ostep);
+  // frame-tile-major block order when the weights of every (phase, m tile)
+  // fit in an XCD's L2 next to the streamed input windows
+  const size_t wbytes = size_t(phases) * m_tiles * a.G * TM * a.C * sizeof(_Float16);
+  const uint32_t fmajor = wbytes <= CG_FMAJOR_WEIGHT_BYTES ? 1u : 0u;
+  conv_gemm_kernel<MC, KC, PL, FU><<<dim3(m_tiles * f_tiles * phases, 1, splits), 256, lds, s>>>(
+      a, m_tiles, f_tiles, halo, wbase, a.off0 - wbase, a.ostep, fmajor);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || splits == 1) return e;
   const size_t n = rows * a.M;
