@@ -197,7 +197,7 @@ def bench_codec(args, full):
         "conv_tflops": round(conv_flops / us / 1e6, 1),
         "roofline": {"bound": "mfma", "kernel": f"conv_gemm {top}", "achieved": round(ach, 1),
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4),
-                     "traffic": None, "flops_per_launch": round(kfl), "avg_us": round(kus, 2)},
+                     "traffic": counter_traffic(top, "codec"), "flops_per_launch": round(kfl), "avg_us": round(kus, 2)},
         "kernels": {n: round(v[0], 1) for n, v in sorted(per.items(), key=lambda kv: -kv[1][0])[:8]},
     }
     if full and args.cpu_baseline:
