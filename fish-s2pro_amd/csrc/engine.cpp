@@ -324,8 +324,10 @@ class Engine {
   bool graph_bmm_off_ = false;
   bool graph_fold_off_ = false;
   uint32_t graph_check_from_ = 0;
-  // Slow-AR decode attention: chunks from here on check the position before
-  // their K/V tile (0: every chunk loads it first); set per generate call
+  // Slow-AR decode attention of batched requests: chunks from here on check
+  // the position before their K/V tile (0: every chunk loads it first).  Set
+  // by each generate call from its prompts; it decides only which blocks wait
+  // for the position, never a result.
   uint32_t attn_check_from_ = 0;
 };
 
@@ -838,7 +840,7 @@ void Engine::enqueue_slow_layers(uint32_t nseq, uint32_t cps, uint32_t seq0, con
     // (the merge kernel carries no warming: its 128-thread blocks warm too
     // slowly, and it waits for them -- 292.3-292.7 against 307.4-308.1
     // frames/s with half the rows given to it)
-    aa.check_from = attn_check_from_;
+    aa.check_from = nseq >= ATTN_CHECK_MIN_SEQS ? attn_check_from_ : 0u;
     aa.warm = warm_for(L.wo, nullptr, ncol, false, 0, warm_slow_);
     HIPC(launch_attention(aa, stream_));
     prof_mark(PROF_ATTN);
