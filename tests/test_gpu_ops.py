@@ -62,6 +62,26 @@ def test_linear_matches_oracle(eng, gtype, tol, in_dim, out_dim, ncol):
         assert _rel(got[c], want) < min(tol, 1e-4), c
 
 
+@pytest.mark.parametrize("in_dim,out_dim", [(2560, 6144), (4096, 2560), (9728, 2560), (512, 1029)])
+def test_batched_product_column_bits_independent_of_batch_width(eng, in_dim, out_dim):
+    """Up to 8 columns take the packed batched product (the 8 columns' hi and
+    lo parts in one MFMA's 16 columns, split where they are staged), 9-16
+    columns the 16-column product (hi and lo in two MFMAs, split in the MFMA
+    lanes).  Both take the same per-column scale, split and sums in the same
+    order, so each column's result has the same bits whichever product serves
+    it (a swapped hi / lo half, a wrong scale lane or a misplaced fragment
+    row would break this)."""
+    rng = np.random.default_rng(in_dim * 7 + out_dim)
+    wf = (rng.standard_normal((out_dim, in_dim)) * 0.02).astype(np.float32)
+    raw = _rows(1, wf)
+    x = rng.standard_normal((9, in_dim)).astype(np.float32)
+    x *= (10.0 ** rng.uniform(-3, 3, (9, in_dim))).astype(np.float32)
+    y9 = eng.linear(raw, 1, in_dim, out_dim, x)
+    for n in (8, 5, 3):
+        yn = eng.linear(raw, 1, in_dim, out_dim, x[:n])
+        assert np.array_equal(yn.view(np.uint32), y9[:n].view(np.uint32)), n
+
+
 @pytest.mark.parametrize("ncol", [2, 8])
 def test_batched_linear_activation_range(eng, ncol):
     """Batched F16 columns go through the MFMA product with activations scaled
