@@ -16,12 +16,14 @@
 // column in the fastest lane bits) nor hold up the weight loads' wait
 // counter.  Each wave scales each column by a power of two that brings the
 // largest |x| of its first two staged chunks (256 elements of its k range)
-// to [1, 2).  Each lane then splits its 8 scaled elements per step into f16
-// hi = f16(x) and lo = f16((x - hi) 2^11) (x = hi + 2^-11 lo to ~2^-22 |x|
-// for |x| >= 2^-14 of that maximum, absolute ~2^-35 of it below); hi and lo
-// go through the MFMA with the same weight fragment into two accumulators,
-// and each wave's sums are scaled back exactly before the waves' sums are
-// added.  So columns of any magnitude keep the same relative accuracy (1e-6
+// to [1, 2).  Each scaled value is split into f16 hi = f16(x) and lo =
+// f16((x - hi) 2^11) (x = hi + 2^-11 lo to ~2^-22 |x| for |x| >= 2^-14 of
+// that maximum, absolute ~2^-35 of it below); hi and lo go through the MFMA
+// with the same weight fragment, and each wave's sums are scaled back
+// exactly before the waves' sums are added.  9-16 columns (bmm_kernel): the
+// MFMA lanes split 8 values per step and run hi and lo through two MFMAs.
+// Up to 8 columns (bmm_pk_kernel): the staging lanes split each value once
+// and hi / lo share one MFMA's 16 columns.  So columns of any magnitude keep the same relative accuracy (1e-6
 // or a raw pre-norm residual of 1e7 times its gain), and an element may be
 // up to 2^15 times the maximum of the first chunks.  RMSNorm inputs: the sum
 // of squares of each column is accumulated from the same values and the RMS
@@ -95,7 +97,8 @@ __device__ __forceinline__ void split8(const floatx4& a, const floatx4& b, half8
 // load at the join): steps run in pairs of chunks (WIN steps), loads past
 // the end re-read in-bounds data, and a step past the end, or a column >= N,
 // gets a zero activation by a select.  Lane l: column n = l % 16, k group
-// l / 16.  NB = activation rows staged (8 when N <= 8, else 16).
+// l / 16.  NB = activation rows staged: 16 (this kernel serves 9-16
+// columns; up to 8 take bmm_pk_kernel below).
 // ---------------------------------------------------------------------------
 // Weight fragments are read once per launch: non-temporal loads stream them
 // past L2 without evicting the staged activations (8 columns: w13 24.4 ->
