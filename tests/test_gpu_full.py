@@ -232,6 +232,43 @@ def test_full_length_generation_properties(name, frames, max_seq):
             e.generate_codes(prompt, frames + 1, 0.0, 1.0, 0, 1 << 30, req["rng_seed"])
 
 
+def test_full_length_q8_sampled_properties():
+    """cfg3 (Q8_0 rows, T 0.7, top-p 0.9) at its full length: 512 sampled
+    frames to KV 768.  Every frame produced, codes in range, graph replay ==
+    direct launches (codes and RNG state), the first 64 frames equal to the
+    oracle's or first differing only at a sampling boundary (as the 64-frame
+    test), the SeededRng stepped once per draw (10 per frame plus the first
+    semantic sample; the fixture's own state after 64 frames follows the same
+    count), and the KV cache filled to its end."""
+    from s2hip import Engine
+
+    fx = _fixture("cfg3")
+    frames, max_seq = 512, 768
+    shape, path = _model(fx)
+    req = fx["requests"][0]
+    prompt = _prompt(shape, fx, 0)
+    _check_prompt(prompt, req)
+    runs = []
+    for graph in (True, False):
+        with Engine(path, max_seq, fx["im_end_id"], use_graph=graph) as e:
+            runs.append(e.generate_codes(prompt, frames, fx["temperature"], fx["top_p"], fx["top_k"], 1 << 30,
+                                         req["rng_seed"]))
+            assert e.n_past == 256 + frames
+    g, d = runs
+    assert g["n_frames"] == d["n_frames"] == frames
+    assert g["codes"].shape == (shape.num_codebooks, frames)
+    assert (g["codes"] >= 0).all() and (g["codes"] < shape.codebook_size).all()
+    assert np.array_equal(g["codes"], d["codes"]) and g["rng_state"] == d["rng_state"]
+    want = np.array(req["codes"], np.int32)
+    diff = _first_difference(g["codes"][:, :want.shape[1]], want)
+    if diff is not None:
+        assert at_boundary(1.0, _margins(req, *diff)), (diff, _margins(req, *diff))
+    s = req["rng_seed"]
+    for _ in range(10 * frames + 1):
+        s = (s * 6364136223846793005 + 1) & ((1 << 64) - 1)
+    assert g["rng_state"] == s
+
+
 def test_full_size_voice_clone_batch_equals_single_requests():
     """cfg5 at its full length: 8 requests of 1500 positions, 1024 frames each,
     batch 8, KV 2560.  Every request's frame count equals its own batch-1
